@@ -1,0 +1,204 @@
+/*
+ * myl_hip.h -- C ABI of libmyl_hip.so, the MI355X (gfx950) backend of the
+ * INTEGER_LLM integer forward path.
+ *
+ * Plain C types only (pointers, sizes, fixed-width integers): this is the
+ * surface a Rust `RocmBackend` (INTEGER_LLM/kernels/src/backends/rocm.rs)
+ * binds through `extern "C"`, replacing the delegating stub.  Every compute
+ * entry point is bit-identical to the reference Rust kernel it names.
+ *
+ * Three layers:
+ *   1. Backend-trait mirror (host slices in, host slices out), one function per
+ *      method of `trait Backend` (INTEGER_LLM/kernels/src/backend.rs:23-127) and
+ *      per free function that runtime/src/model.rs calls directly
+ *      (model.rs:16-22).  Slices are copied to and from the device per call,
+ *      like the reference passes weights per call (linear.rs:43-50).
+ *   2. Device-pointer forms (`*_dev`): the same arithmetic on device buffers,
+ *      asynchronous on the context's stream, with a batch dimension M.
+ *   3. A device-resident model (`myl_model_*`): forward_token / run_layers /
+ *      head_logits of runtime/src/model.rs:229-399 with weights uploaded once
+ *      and the KV cache of runtime/src/kv_cache.rs held in HBM.
+ *
+ * Status codes: 0 = ok; MYL_E_INVALID where the reference panics (assert!,
+ * empty slices, length mismatches); MYL_E_HIP for runtime failures;
+ * MYL_E_NOMEM; MYL_E_UNSUPPORTED.  myl_last_error() returns the message of the
+ * last failure on a context.
+ *
+ * Threading: one context per device; calls on one context must be serialised
+ * by the caller (the trait's `&self` methods map onto a Mutex in the shim).
+ */
+#ifndef MYL_HIP_H
+#define MYL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "myl_theta_v.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MYL_OK 0
+#define MYL_E_INVALID (-1)
+#define MYL_E_HIP (-2)
+#define MYL_E_NOMEM (-3)
+#define MYL_E_UNSUPPORTED (-4)
+
+typedef struct myl_ctx myl_ctx;
+typedef struct myl_model myl_model;
+
+/* ---- backend identity: rocm.rs:71-82 (name / hardware_family / feature_tag) */
+const char* myl_backend_name(void);     /* "rocm"    */
+const char* myl_hardware_family(void);  /* "amd-gpu" */
+const char* myl_feature_tag(void);      /* "rocm"    */
+
+/* ---- context: RocmBackend::init(device_id) -> Result<Self, String> (rocm.rs:54-59) */
+int myl_init(int device_id, myl_ctx** out);
+void myl_destroy(myl_ctx* ctx);
+const char* myl_last_error(const myl_ctx* ctx);
+/* The real gcnArchName (e.g. "gfx950:sramecc+:xnack-") in place of the stub's
+ * hard-coded "gfx90a" (rocm.rs:58); cu_count / hbm_bytes may be NULL. */
+int myl_device_info(const myl_ctx* ctx, char* gcn_arch, size_t cap, int* cu_count, uint64_t* hbm_bytes);
+int myl_synchronize(myl_ctx* ctx);
+void* myl_stream(myl_ctx* ctx); /* the hipStream_t all *_dev calls use */
+/* Use the caller's stream (hipStream_t) for all later calls; NULL restores the
+ * context's own stream.  The caller keeps ownership. */
+int myl_set_stream(myl_ctx* ctx, void* stream);
+
+/* ---- device memory for callers without their own allocator ------------- */
+int myl_malloc(myl_ctx* ctx, size_t bytes, void** dptr);
+int myl_free(myl_ctx* ctx, void* dptr);
+int myl_memcpy_htod(myl_ctx* ctx, void* dst, const void* src, size_t bytes);
+int myl_memcpy_dtoh(myl_ctx* ctx, void* dst, const void* src, size_t bytes);
+
+/* ======================================================================
+ * 1. Backend-trait mirror (host slices)
+ * ==================================================================== */
+
+/* Backend::linear_w8a16 (backend.rs:39-49) == linear.rs:43-70.
+ * W is flat row-major [out_features x in_features]. */
+int myl_linear_w8a16(myl_ctx* ctx, const int16_t* x, const int8_t* W, int16_t* out, size_t in_features,
+                     size_t out_features, const uint8_t* w_shifts, uint8_t act_frac, uint8_t out_frac);
+
+/* linear.rs:87-119 (o_proj / down_proj, per-channel output scale; model.rs:582,618). */
+int myl_linear_w8a16_pc(myl_ctx* ctx, const int16_t* x, const int8_t* W, int16_t* out, size_t in_features,
+                        size_t out_features, const uint8_t* w_shifts, uint8_t act_frac, const uint8_t* out_frac);
+
+/* linear.rs:132-145 (in place on out). */
+int myl_add_bias_i16(myl_ctx* ctx, int16_t* out, const int16_t* bias, const uint8_t* bias_shifts, size_t n,
+                     uint8_t out_frac);
+
+/* Backend::rmsnorm (backend.rs:54-66) == rmsnorm.rs:61-161. */
+int myl_rmsnorm(myl_ctx* ctx, const int16_t* x, const uint8_t* x_shifts, const int8_t* gamma,
+                const uint8_t* gamma_shifts, size_t n, const int16_t* rsqrt_lut, size_t lut_len,
+                uint8_t lut_input_shift, uint8_t lut_output_frac, int64_t inv_n_q20, int16_t* out, uint8_t out_frac);
+
+/* Backend::softmax (backend.rs:69-75) == softmax.rs:24-64. */
+int myl_softmax(myl_ctx* ctx, const int32_t* logits, int32_t* out, size_t n, const int16_t* exp_lut,
+                size_t lut_len, uint8_t lut_shift, uint8_t frac_bits);
+
+/* Backend::attention (backend.rs:79-91) == attention.rs:42-90.  The Vec<Vec<i16>>
+ * arguments are flattened: q/out [q_len x head_dim], k/v [kv_len x head_dim];
+ * mask is [q_len x kv_len] bytes (nonzero = attend) or NULL for all-true. */
+int myl_attention(myl_ctx* ctx, const int16_t* q, const int16_t* k, const int16_t* v, int16_t* out,
+                  size_t q_len, size_t kv_len, size_t head_dim, const uint8_t* mask, int64_t score_mult,
+                  uint8_t score_shift, const int16_t* exp_lut, size_t lut_len, uint8_t lut_shift, uint8_t prob_frac);
+
+/* Backend::rope (backend.rs:94-101) == rope.rs:36-59, in place on q and k
+ * ([n x head_dim] each); LUT row = positions[i] % (lut_len / (head_dim/2)). */
+int myl_rope(myl_ctx* ctx, int16_t* q, int16_t* k, size_t n, size_t head_dim, const int16_t* cos_lut,
+             const int16_t* sin_lut, size_t lut_len, const uint64_t* positions, uint8_t frac_bits);
+
+/* Backend::mlp (backend.rs:107-126) == mlp.rs:28-74; intermediate size is
+ * inferred from the slice lengths as in rocm.rs:183-186 (given explicitly here). */
+int myl_mlp(myl_ctx* ctx, const int16_t* x, const int8_t* W_gate, const int8_t* W_up, const int8_t* W_down,
+            int16_t* out, size_t hidden, size_t inter, const uint8_t* gate_w_shifts, const uint8_t* up_w_shifts,
+            const uint8_t* down_w_shifts, const int16_t* silu_lut, size_t silu_len, uint8_t in_frac,
+            uint8_t gate_out_frac, uint8_t up_out_frac, uint8_t down_in_frac, uint8_t silu_in_frac,
+            int16_t silu_lut_offset, uint8_t silu_out_frac, const uint8_t* out_frac);
+
+/* sampling.rs:8-18 (first maximum wins); *out_index receives the token id. */
+int myl_argmax_int(myl_ctx* ctx, const int32_t* values, size_t n, int64_t* out_index);
+
+/* ======================================================================
+ * 2. Device-pointer forms (asynchronous on myl_stream(ctx))
+ * ==================================================================== */
+
+/* M independent linear_w8a16 / linear_w8a16_pc calls: x [M x K] (row stride
+ * ldx), W [N x K], out [M x N] (row stride ldo).  out_frac_pc = NULL selects
+ * the scalar out_frac (linear.rs:43-70), else per channel (linear.rs:87-119). */
+int myl_linear_w8a16_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, const int8_t* W, size_t N,
+                         size_t K, const uint8_t* w_shifts, uint8_t act_frac, uint8_t out_frac,
+                         const uint8_t* out_frac_pc, int16_t* out, size_t ldo);
+
+/* Multiplier + shift requantization (no reference counterpart: a superset of
+ * linear.rs's power-of-two rescale): out = clamp_i16(RNE(dot * mult[r], shift[r]))
+ * in 128-bit arithmetic.  mult = 2^k, shift = k + w_shift + act_frac - out_frac
+ * reproduces myl_linear_w8a16_dev exactly whenever that shift is >= 0. */
+int myl_linear_w8a16_mult_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, const int8_t* W, size_t N,
+                              size_t K, const int32_t* mult, const uint8_t* shift, int16_t* out, size_t ldo);
+
+/* LM head (model.rs:284-308): logits[m][r] = clamp_i32(rescale_i64(W[r].x[m],
+ * row_shifts[r] + norm_frac, logit_frac)); w_bits = 16 for the int16 head
+ * (path A), 8 for the tied int8 embedding (path B). */
+int myl_logits_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, const void* W, int w_bits, size_t N,
+                   size_t K, const uint8_t* row_shifts, uint8_t norm_frac, uint8_t logit_frac, int32_t* out,
+                   size_t ldo);
+
+/* Exact i64 dot products (dot.rs:141-147) of M activation rows with N weight rows. */
+int myl_dot_i8_i16_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, const int8_t* W, size_t N, size_t K,
+                       int64_t* out, size_t ldo);
+
+/* M rows of rmsnorm_i16 (rmsnorm.rs:61-161), shared x_shifts / gamma. */
+int myl_rmsnorm_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, const uint8_t* x_shifts,
+                    const int8_t* gamma, const uint8_t* gamma_shifts, size_t n, const int16_t* rsqrt_lut,
+                    size_t lut_len, uint8_t lut_input_shift, uint8_t lut_output_frac, int64_t inv_n_q20,
+                    uint8_t out_frac, int16_t* out, size_t ldo);
+
+/* M rows of softmax_int (softmax.rs:24-64). */
+int myl_softmax_dev(myl_ctx* ctx, const int32_t* logits, size_t M, size_t n, size_t ldz, const int16_t* exp_lut,
+                    size_t lut_len, uint8_t lut_shift, uint8_t frac_bits, int32_t* out, size_t ldo);
+
+/* M rows of argmax_int (sampling.rs:8-18). */
+int myl_argmax_dev(myl_ctx* ctx, const int32_t* values, size_t M, size_t n, size_t ldv, int64_t* out_index);
+
+/* ======================================================================
+ * 3. Device-resident model (runtime/src/model.rs, kv_cache.rs)
+ * ==================================================================== */
+
+/* Builds the seeded synthetic model of include/myl_synth.h directly in HBM
+ * (weights are generated on the device; the LUTs are uploaded). */
+int myl_model_create_synthetic(myl_ctx* ctx, const myl_synth_spec* spec, const myl_luts* luts, myl_model** out);
+void myl_model_destroy(myl_model* m);
+/* Empties the KV cache (KVCache::new, kv_cache.rs:14-16). */
+int myl_model_reset(myl_model* m);
+/* IntegerModel::forward_token (model.rs:229-311) for one token at position pos.
+ * logits (host, vocab entries) may be NULL; argmax (host) may be NULL.
+ * Positions must be written contiguously from 0 (the generate loop,
+ * generate.rs:28-50). */
+int myl_model_forward_token(myl_model* m, uint32_t token, uint32_t pos, int32_t* logits, int64_t* argmax);
+/* Greedy decode: n_steps tokens after `token` at `pos` (generate.rs:38-50),
+ * each step's argmax feeding the next without a host round trip.  tokens_out
+ * (host, n_steps) receives the chosen ids; logits_out (host, n_steps x vocab)
+ * may be NULL. */
+int myl_model_decode_greedy(myl_model* m, uint32_t token, uint32_t pos, uint32_t n_steps, int64_t* tokens_out,
+                            int32_t* logits_out);
+/* IntegerModel::embed_token (model.rs:323-331): hidden (host, hidden entries). */
+int myl_model_embed_token(myl_model* m, uint32_t token, int16_t* hidden);
+/* IntegerModel::run_layers (model.rs:339-356), hidden in/out on the host. */
+int myl_model_run_layers(myl_model* m, int16_t* hidden, uint32_t pos, uint32_t layer_start, uint32_t layer_end);
+/* IntegerModel::head_logits (model.rs:360-399). */
+int myl_model_head_logits(myl_model* m, const int16_t* hidden, int32_t* logits);
+/* KVCache::read (kv_cache.rs:43-52) for positions [0, n_pos): k/v [n_pos x head_dim]. */
+int myl_model_read_kv(myl_model* m, uint32_t layer, uint32_t kv_head, uint32_t n_pos, int16_t* k_out,
+                      int16_t* v_out);
+/* Device copy of a named weight tensor (the synthetic generator's output),
+ * for verification; same names as the oracle's tensor table. */
+int myl_model_read_tensor(myl_model* m, const char* name, uint32_t layer, void* host_out, size_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MYL_HIP_H */

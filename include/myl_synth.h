@@ -145,6 +145,29 @@ MYL_HD uint8_t myl_synth_res_frac(uint64_t tseed, uint64_t ch) {
     return (uint8_t)myl_draw_range(myl_splitmix_at(tseed, ch), 7, 10);
 }
 
+/* Small per-row / per-element tensors: value i of (layer, role) is uniform in
+ * the role's range.  One table, so the device generator and the oracle agree. */
+MYL_HD void myl_synth_small_range(uint32_t role, int32_t* lo, int32_t* hi) {
+    switch (role) {
+    case MYL_R_EMB_SHIFT:         *lo = 7;     *hi = 9;    break; /* int8 row scale 2^-7..2^-9 */
+    case MYL_R_LM16_SHIFT:        *lo = 17;    *hi = 19;   break;
+    case MYL_R_FINAL_GAMMA_SHIFT:
+    case MYL_R_IN_GAMMA_SHIFT:
+    case MYL_R_POST_GAMMA_SHIFT:  *lo = 6;     *hi = 7;    break;
+    case MYL_R_BQ: case MYL_R_BK: case MYL_R_BV:
+                                  *lo = -3000; *hi = 3000; break; /* int16 biases */
+    case MYL_R_BQ_SHIFT: case MYL_R_BK_SHIFT: case MYL_R_BV_SHIFT:
+                                  *lo = 10;    *hi = 13;   break;
+    default:                      *lo = 0;     *hi = 0;    break;
+    }
+}
+
+MYL_HD int32_t myl_synth_small(uint64_t model_seed, uint32_t layer, uint32_t role, uint64_t i) {
+    int32_t lo, hi;
+    myl_synth_small_range(role, &lo, &hi);
+    return myl_draw_range(myl_splitmix_at(myl_tensor_seed(model_seed, layer, role), i), lo, hi);
+}
+
 /* Model-wide scalars. */
 MYL_HD uint8_t myl_synth_final_norm_frac(uint64_t model_seed) {
     return (uint8_t)myl_draw_range(myl_splitmix_at(myl_tensor_seed(model_seed, 0, MYL_R_MODEL_FRACS), 0), 9, 10);

@@ -1,0 +1,24 @@
+// abi_internal.h -- the context object behind the opaque myl_ctx handle.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "../../include/myl_hip.h"
+#include "internal.h"
+
+struct myl_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;      // stream of every launch (own_stream or the caller's)
+    hipStream_t own_stream = nullptr;
+    hipDeviceProp_t prop{};
+    std::string err;
+    void* scratch_ptr = nullptr;
+    size_t scratch_bytes = 0;
+
+    int fail(int code, const std::string& msg);
+    int hip(hipError_t e, const char* what);
+    // Grow-only device scratch for host-slice staging (valid until the next call).
+    void* scratch(size_t bytes);
+};

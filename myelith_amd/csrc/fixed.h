@@ -1,0 +1,133 @@
+// fixed.h -- integer fixed-point primitives of the theta_v numeric contract,
+// for device (and host) code of the HIP library.
+//
+// Semantics are those of the reference Rust kernels compiled in release mode
+// (INTEGER_LLM/kernels/src/fixed_point.rs): + - * wrap, `as` truncates and
+// shift amounts are masked to the operand width.  Nothing here uses floating
+// point: integer division is done by shift-and-subtract or by a reciprocal
+// computed that way, so no v_rcp_f32 sequence enters an integer kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define MYL_FN __host__ __device__ static inline
+
+typedef __int128 myl_i128;
+typedef unsigned __int128 myl_u128;
+
+MYL_FN int32_t shl32(int32_t v, uint32_t s) { return (int32_t)((uint32_t)v << (s & 31u)); }
+MYL_FN int32_t shr32(int32_t v, uint32_t s) { return v >> (s & 31u); }
+MYL_FN int64_t shl64(int64_t v, uint32_t s) { return (int64_t)((uint64_t)v << (s & 63u)); }
+MYL_FN int64_t shr64(int64_t v, uint32_t s) { return v >> (s & 63u); }
+MYL_FN myl_i128 shl128(myl_i128 v, uint32_t s) { return (myl_i128)((myl_u128)v << (s & 127u)); }
+MYL_FN myl_i128 shr128(myl_i128 v, uint32_t s) { return v >> (s & 127u); }
+MYL_FN int32_t wadd32(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
+MYL_FN int32_t wsub32(int32_t a, int32_t b) { return (int32_t)((uint32_t)a - (uint32_t)b); }
+MYL_FN int32_t wmul32(int32_t a, int32_t b) { return (int32_t)((uint32_t)a * (uint32_t)b); }
+MYL_FN int64_t wadd64(int64_t a, int64_t b) { return (int64_t)((uint64_t)a + (uint64_t)b); }
+MYL_FN int64_t wmul64(int64_t a, int64_t b) { return (int64_t)((uint64_t)a * (uint64_t)b); }
+
+// fixed_point.rs:15-35
+MYL_FN int16_t clamp_i16(int32_t x) { return x < -32768 ? (int16_t)-32768 : (x > 32767 ? (int16_t)32767 : (int16_t)x); }
+MYL_FN int16_t clamp_i16_i64(int64_t x) { return x < -32768 ? (int16_t)-32768 : (x > 32767 ? (int16_t)32767 : (int16_t)x); }
+MYL_FN int32_t clamp_i32_i64(int64_t x) { return x < (int64_t)INT32_MIN ? INT32_MIN : (x > (int64_t)INT32_MAX ? INT32_MAX : (int32_t)x); }
+
+// fixed_point.rs:39-53: arithmetic right shift, round half to even.
+MYL_FN int32_t rshift_round32(int32_t value, uint8_t shift) {
+    if (shift == 0) return value;
+    int32_t mask = wsub32(shl32(1, shift), 1);
+    int32_t half = shl32(1, (uint8_t)(shift - 1));
+    int32_t q = shr32(value, shift);
+    int32_t r = value & mask;
+    return (r > half || (r == half && (q & 1))) ? wadd32(q, 1) : q;
+}
+
+// fixed_point.rs:57-71
+MYL_FN int64_t rshift_round64(int64_t value, uint8_t shift) {
+    if (shift == 0) return value;
+    int64_t mask = (int64_t)((uint64_t)shl64(1, shift) - 1u);
+    int64_t half = shl64(1, (uint8_t)(shift - 1));
+    int64_t q = shr64(value, shift);
+    int64_t r = value & mask;
+    return (r > half || (r == half && (q & 1))) ? wadd64(q, 1) : q;
+}
+
+// fixed_point.rs:155-169
+MYL_FN myl_i128 rshift_round128(myl_i128 value, uint32_t shift) {
+    if (shift == 0) return value;
+    myl_i128 mask = (myl_i128)((myl_u128)shl128(1, shift) - 1u);
+    myl_i128 half = shl128(1, shift - 1u);
+    myl_i128 q = shr128(value, shift);
+    myl_i128 r = value & mask;
+    return (r > half || (r == half && (q & 1))) ? (myl_i128)((myl_u128)q + 1u) : q;
+}
+
+// fixed_point.rs:173-191: shift = in_frac as i8 - out_frac as i8 (wrapping);
+// a negative shift is an unrounded, wrapping left shift.
+MYL_FN int32_t rescale32(int32_t acc, uint8_t in_frac, uint8_t out_frac) {
+    int8_t sh = (int8_t)(uint8_t)((int8_t)in_frac - (int8_t)out_frac);
+    return sh >= 0 ? rshift_round32(acc, (uint8_t)sh) : shl32(acc, (uint8_t)(-(int32_t)sh));
+}
+MYL_FN int64_t rescale64(int64_t acc, uint8_t in_frac, uint8_t out_frac) {
+    int8_t sh = (int8_t)(uint8_t)((int8_t)in_frac - (int8_t)out_frac);
+    return sh >= 0 ? rshift_round64(acc, (uint8_t)sh) : shl64(acc, (uint8_t)(-(int32_t)sh));
+}
+
+// floor(2^32 / d) for d >= 1, by restoring long division (33 steps, integer only).
+MYL_FN uint64_t recip32(uint32_t d) {
+    uint64_t q = 0, r = 0;
+    // dividend 2^32 has its only set bit at position 32
+    for (int bit = 32; bit >= 0; --bit) {
+        r = (r << 1) | (bit == 32 ? 1u : 0u);
+        q <<= 1;
+        if (r >= d) { r -= d; q |= 1; }
+    }
+    return q;
+}
+
+// Unsigned n / d with the reciprocal m = recip32(d): at most one correction
+// (m = 2^32/d - e with 0 <= e < 1 and n < 2^32 put n*m/2^32 in (n/d - 1, n/d]).
+MYL_FN void udivmod32(uint32_t n, uint32_t d, uint64_t m, uint32_t* q, uint32_t* r) {
+    uint64_t q0 = ((uint64_t)n * m) >> 32;
+    uint64_t rem = (uint64_t)n - q0 * (uint64_t)d;
+    if (rem >= d) { q0 += 1; rem -= d; }
+    *q = (uint32_t)q0;
+    *r = (uint32_t)rem;
+}
+
+// softmax.rs:50-63 for one element: Rust i32 `/` and `%` (truncating), then
+// round to nearest, ties to even.  recip = recip32(|s|).
+MYL_FN int32_t softmax_div_round(int32_t num, int32_t s, uint64_t recip) {
+    uint32_t un = num < 0 ? 0u - (uint32_t)num : (uint32_t)num;
+    uint32_t us = s < 0 ? 0u - (uint32_t)s : (uint32_t)s;
+    uint32_t uq, ur;
+    udivmod32(un, us, recip, &uq, &ur);
+    bool neg_q = (num < 0) != (s < 0);
+    int32_t q = neg_q ? (int32_t)(0u - uq) : (int32_t)uq;
+    int32_t r = num < 0 ? (int32_t)(0u - ur) : (int32_t)ur;
+    int32_t ra = r < 0 ? (int32_t)(0u - (uint32_t)r) : r;
+    int32_t twice = wmul32(ra, 2);
+    int32_t den_abs = (int32_t)us;
+    if (twice > den_abs || (twice == den_abs && (q & 1)))
+        return ((num > 0) == (s > 0)) ? wadd32(q, 1) : wsub32(q, 1);
+    return q;
+}
+
+// Unsigned 32-bit n % d without a hardware divide (small loops only: LUT row
+// selection pos % n_pos, done once per launch).
+MYL_FN uint32_t umod32_slow(uint32_t n, uint32_t d) {
+    uint64_t m = recip32(d);
+    uint32_t q, r;
+    udivmod32(n, d, m, &q, &r);
+    return r;
+}
+
+// integer_math.rs:44-48 with shift 0: index arithmetic in i16 (wrapping).
+MYL_FN int16_t lut_lookup_i16(int16_t x, const int16_t* lut, uint32_t len, int16_t offset) {
+    int16_t idx = (int16_t)(uint16_t)((uint16_t)x + (uint16_t)offset);
+    int16_t hi = (int16_t)(uint16_t)((uint16_t)len - 1u);
+    if (idx < 0) idx = 0;
+    if (idx > hi) idx = hi;
+    return lut[(uint16_t)idx];
+}

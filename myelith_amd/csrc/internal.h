@@ -1,0 +1,41 @@
+// internal.h -- launchers shared between the kernel TUs and the C-ABI layer.
+// All pointers are device pointers; lengths are validated by the caller.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace myl {
+
+// y[m][r] = clamp_i16(rescale_i64(W[r].x[m], w_shifts[r] + act_frac, out_frac_pc ? out_frac_pc[r] : out_frac))
+hipError_t linear_w8a16(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, const uint8_t* w_shifts,
+                        uint8_t act_frac, uint8_t out_frac, const uint8_t* out_frac_pc, int16_t* out, int ldo,
+                        hipStream_t st);
+hipError_t linear_w8a16_mult(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, const int32_t* mult,
+                             const uint8_t* shift, int16_t* out, int ldo, hipStream_t st);
+hipError_t logits_w8(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, const uint8_t* row_shifts,
+                     uint8_t norm_frac, uint8_t logit_frac, int32_t* out, int ldo, hipStream_t st);
+hipError_t logits_w16(const int16_t* x, int M, int ldx, const int16_t* W, int N, int K, const uint8_t* row_shifts,
+                      uint8_t norm_frac, uint8_t logit_frac, int32_t* out, int ldo, hipStream_t st);
+hipError_t dot_raw_w8(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, int64_t* out, int ldo,
+                      hipStream_t st);
+hipError_t rmsnorm(const int16_t* x, int M, int ldx, const uint8_t* xs, const int8_t* g, const uint8_t* gs, int n,
+                   const int16_t* lut, int lut_len, uint8_t lut_input_shift, uint8_t lut_output_frac,
+                   int64_t inv_n_q20, uint8_t out_frac, int16_t* out, int ldo, hipStream_t st);
+hipError_t softmax(const int32_t* z, int M, int n, int ldz, const int16_t* lut, int lut_len, uint8_t lut_shift,
+                   uint8_t frac_bits, int32_t* out, int ldo, hipStream_t st);
+// scratch: 2 * q_len * kv_len int32
+hipError_t attention_generic(const int16_t* q, const int16_t* k, const int16_t* v, const uint8_t* mask, int q_len,
+                             int kv_len, int hd, int64_t score_mult, uint8_t score_shift, const int16_t* lut,
+                             int lut_len, uint8_t lut_shift, uint8_t prob_frac, int32_t* scratch, int16_t* out,
+                             hipStream_t st);
+// rows[i] = positions[i] % n_pos (computed by the caller)
+hipError_t rope(int16_t* q, int16_t* k, int n, int hd, const int16_t* cos_lut, const int16_t* sin_lut,
+                const int32_t* rows, uint8_t frac_bits, hipStream_t st);
+hipError_t add_bias(int16_t* out, const int16_t* b, const uint8_t* bs, int n, uint8_t out_frac, hipStream_t st);
+hipError_t silu_gate(const int16_t* gate, const int16_t* up, int n, const int16_t* silu, int silu_len,
+                     uint8_t gate_frac, uint8_t up_frac, uint8_t down_in_frac, uint8_t silu_in_frac, int16_t silu_off,
+                     uint8_t silu_out_frac, int16_t* h, hipStream_t st);
+hipError_t argmax(const int32_t* v, int M, int n, int ldv, int64_t* out, hipStream_t st);
+
+}  // namespace myl

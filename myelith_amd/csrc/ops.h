@@ -1,0 +1,117 @@
+// ops.h -- integer kernels of the forward path other than the GEMV.
+//
+// Each kernel restates one reference function (cited at the kernel) and is
+// exact: results equal the reference bit for bit, whatever the launch shape.
+#pragma once
+
+#include "fixed.h"
+
+namespace myl {
+
+constexpr int kBlock = 256;
+
+// ---- block reductions -------------------------------------------------------
+
+__device__ inline int32_t block_max_i32(int32_t v, int32_t* red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
+    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    v = red[0];
+    for (int i = 1; i < nw; ++i) v = max(v, red[i]);
+    return v;
+}
+
+__device__ inline uint32_t block_sum_u32(uint32_t v, uint32_t* red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += (uint32_t)__shfl_xor((int)v, off, 64);
+    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    v = 0;
+    for (int i = 0; i < nw; ++i) v += red[i];
+    return v;
+}
+
+// Exact i128 sum over the block (tree in LDS; red holds blockDim.x entries).
+__device__ inline myl_i128 block_sum_i128(myl_i128 v, myl_i128* red) {
+    __syncthreads();
+    red[threadIdx.x] = v;
+    __syncthreads();
+    for (int s = blockDim.x >> 1; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) red[threadIdx.x] = (myl_i128)((myl_u128)red[threadIdx.x] + (myl_u128)red[threadIdx.x + s]);
+        __syncthreads();
+    }
+    return red[0];
+}
+
+// ---- rmsnorm.rs:61-161 --------------------------------------------------------
+
+struct RmsParams {
+    const int16_t* lut; int lut_len;
+    uint8_t lut_input_shift, lut_output_frac;
+    int64_t inv_n_q20;
+};
+
+// Norm factor of one row: everything except the per-channel output.
+struct RmsFactor { bool zero; uint8_t ref_shift; int64_t lut_val; uint32_t norm_frac; };
+
+// Must be called by the whole block.  red128 needs blockDim.x entries.
+__device__ inline RmsFactor rms_factor(const int16_t* x, const uint8_t* xs, int n, const RmsParams& p,
+                                       myl_i128* red128, int32_t* red32) {
+    int32_t mx = 0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) mx = max(mx, (int32_t)xs[i]);
+    const uint8_t ref = (uint8_t)block_max_i32(mx, red32);
+    myl_i128 acc = 0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const uint32_t align = 2u * (uint32_t)(uint8_t)(ref - xs[i]);
+        const myl_i128 sq = (myl_i128)x[i] * (myl_i128)x[i];
+        acc = (myl_i128)((myl_u128)acc + (myl_u128)shl128(sq, align));
+    }
+    acc = block_sum_i128(acc, red128);
+    RmsFactor f;
+    f.ref_shift = ref;
+    f.zero = acc == 0;
+    f.lut_val = 0; f.norm_frac = 0;
+    if (!f.zero) {
+        const myl_i128 m = shr128((myl_i128)((myl_u128)acc * (myl_u128)(myl_i128)p.inv_n_q20), 20);
+        const myl_i128 max_idx = (myl_i128)(p.lut_len - 1);
+        uint32_t q = 0;
+        while (shr128(m, q) > max_idx) q += 2;
+        myl_i128 idx = rshift_round128(m, q);
+        if (idx > max_idx) idx = max_idx;
+        if (idx < 0) idx = 0;
+        f.lut_val = (int64_t)p.lut[(int)idx];
+        f.norm_frac = (uint32_t)p.lut_output_frac + (uint32_t)p.lut_input_shift / 2u + q / 2u;
+    }
+    return f;
+}
+
+__device__ inline int16_t rms_out(int16_t x, uint8_t xs, int8_t g, uint8_t gs, const RmsFactor& f, uint8_t out_frac) {
+    if (f.zero) return 0;
+    const int32_t total = (int32_t)f.norm_frac + (int32_t)gs + ((int32_t)xs - (int32_t)f.ref_shift);
+    const int32_t shift = total - (int32_t)out_frac;
+    const myl_i128 prod = (myl_i128)x * (myl_i128)f.lut_val * (myl_i128)g;
+    const myl_i128 s = shift >= 0 ? rshift_round128(prod, (uint32_t)shift) : shl128(prod, (uint32_t)(-shift));
+    const int32_t c = s < (myl_i128)INT32_MIN ? INT32_MIN : (s > (myl_i128)INT32_MAX ? INT32_MAX : (int32_t)s);
+    return clamp_i16(c);
+}
+
+// ---- softmax.rs:12-64 ----------------------------------------------------------
+
+__device__ inline int32_t exp_lookup(int32_t x, const int16_t* lut, uint32_t len, uint8_t shift, int32_t one) {
+    if (x <= 0) return one;
+    const uint32_t idx = (uint32_t)x >> (shift & 31u);
+    if (idx >= len) return 0;
+    return (int32_t)lut[idx];
+}
+
+__device__ inline int32_t sat_sub32(int32_t a, int32_t b) {
+    const int64_t d = (int64_t)a - (int64_t)b;
+    return d > INT32_MAX ? INT32_MAX : (d < INT32_MIN ? INT32_MIN : (int32_t)d);
+}
+
+}  // namespace myl

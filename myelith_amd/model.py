@@ -1,0 +1,152 @@
+"""IntegerModel on the GPU: the host mirror of INTEGER_LLM/runtime/src/model.rs.
+
+`IntegerModel` wraps a device-resident model of libmyl_hip.so (weights in HBM,
+KV cache in HBM) and keeps the reference's method names: forward_token
+(model.rs:229-311), embed_token (:323-331), run_layers (:339-356),
+head_logits (:360-399), greedy_next (:780-782).  `dekodieren_mit_digest`
+reproduces runtime/src/generate.rs:98-137 (the SHA-256 logits digest that is
+the parity contract between machines).
+
+Models are the seeded synthetic models of include/myl_synth.h: real
+checkpoints are not available where this runs.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import hashlib
+
+import numpy as np
+
+from ._lib import Luts, SynthSpec, lib
+from .backend import RocmBackend
+from .luts import LutSet
+
+# Architectures of the workloads (Qwen2.5 layout).
+QWEN25_05B = dict(vocab=151936, hidden=896, layers=24, heads=14, kv_heads=2, head_dim=64, inter=4864,
+                  lm_head_int16=0, attention_bias=1)
+QWEN25_7B = dict(vocab=152064, hidden=3584, layers=28, heads=28, kv_heads=4, head_dim=128, inter=18944,
+                 lm_head_int16=1, attention_bias=1)
+
+
+def make_spec(arch: dict, seed: int, max_pos: int, **over) -> dict:
+    spec = dict(arch)
+    spec.update(seed=seed, max_pos=max_pos)
+    spec.update(over)
+    return spec
+
+
+def luts_struct(luts: LutSet) -> tuple[Luts, tuple]:
+    arrs = tuple(np.ascontiguousarray(a, dtype=np.int16) for a in (luts.rsqrt, luts.silu, luts.exp, luts.cos, luts.sin))
+    s = Luts(arrs[0].ctypes.data, arrs[0].size, arrs[1].ctypes.data, arrs[1].size, arrs[2].ctypes.data, arrs[2].size,
+             arrs[3].ctypes.data, arrs[4].ctypes.data, arrs[3].size)
+    return s, arrs
+
+
+class IntegerModel:
+    """model.rs:120-163, device-resident."""
+
+    def __init__(self, backend: RocmBackend, spec: dict, luts: LutSet | None = None):
+        self.backend = backend
+        self.spec = dict(spec)
+        self.luts = luts or LutSet.for_head_dim(spec["head_dim"])
+        cspec = SynthSpec(**{k: int(spec[k]) for k, _ in SynthSpec._fields_})
+        cl, keep = luts_struct(self.luts)
+        h = C.c_void_p()
+        backend.check(lib().myl_model_create_synthetic(backend.handle, C.byref(cspec), C.byref(cl), C.byref(h)),
+                      "model_create_synthetic")
+        self._h = h
+        self.vocab_size = spec["vocab"]
+        self.hidden_size = spec["hidden"]
+        self.num_layers = spec["layers"]
+        self.num_kv_heads = spec["kv_heads"]
+        self.head_dim = spec["head_dim"]
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib().myl_model_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc, what):
+        self.backend.check(rc, what)
+
+    def reset(self) -> None:
+        """A fresh KV cache (KVCache::new, kv_cache.rs:14-16)."""
+        self._check(lib().myl_model_reset(self._h), "reset")
+
+    def forward_token(self, token_id: int, pos: int, want_logits: bool = True):
+        logits = np.zeros(self.vocab_size, np.int32) if want_logits else None
+        am = C.c_int64()
+        self._check(lib().myl_model_forward_token(self._h, token_id, pos,
+                                                  None if logits is None else logits.ctypes.data, C.byref(am)),
+                    "forward_token")
+        self.last_argmax = am.value
+        return logits
+
+    def decode_greedy(self, token: int, pos: int, n_steps: int, want_logits: bool = False):
+        """n_steps forward passes, each feeding its argmax to the next on the device."""
+        toks = np.zeros(n_steps, np.int64)
+        logits = np.zeros((n_steps, self.vocab_size), np.int32) if want_logits else None
+        self._check(lib().myl_model_decode_greedy(self._h, token, pos, n_steps, toks.ctypes.data,
+                                                  None if logits is None else logits.ctypes.data), "decode_greedy")
+        return toks, logits
+
+    def embed_token(self, token_id: int) -> np.ndarray:
+        h = np.zeros(self.hidden_size, np.int16)
+        self._check(lib().myl_model_embed_token(self._h, token_id, h.ctypes.data), "embed_token")
+        return h
+
+    def run_layers(self, hidden, pos: int, layer_start: int, layer_end: int) -> np.ndarray:
+        h = np.ascontiguousarray(hidden, dtype=np.int16).copy()
+        self._check(lib().myl_model_run_layers(self._h, h.ctypes.data, pos, layer_start, layer_end), "run_layers")
+        return h
+
+    def head_logits(self, hidden) -> np.ndarray:
+        h = np.ascontiguousarray(hidden, dtype=np.int16)
+        out = np.zeros(self.vocab_size, np.int32)
+        self._check(lib().myl_model_head_logits(self._h, h.ctypes.data, out.ctypes.data), "head_logits")
+        return out
+
+    def read_kv(self, layer: int, kv_head: int, n_pos: int):
+        k = np.zeros((n_pos, self.head_dim), np.int16)
+        v = np.zeros((n_pos, self.head_dim), np.int16)
+        self._check(lib().myl_model_read_kv(self._h, layer, kv_head, n_pos, k.ctypes.data, v.ctypes.data), "read_kv")
+        return k, v
+
+    def read_tensor(self, name: str, layer: int, nbytes: int, dtype=np.int8) -> np.ndarray:
+        buf = np.zeros(nbytes, np.uint8)
+        self._check(lib().myl_model_read_tensor(self._h, name.encode(), layer, buf.ctypes.data, nbytes), "read_tensor")
+        return buf.view(dtype)
+
+    @staticmethod
+    def greedy_next(logits) -> int:
+        """argmax_int (sampling.rs:8-18): the first maximum wins."""
+        return int(np.argmax(np.asarray(logits)))
+
+
+def dekodieren_mit_digest(model, token_ids, max_new_tokens: int):
+    """generate.rs:98-137 (greedy): prefill the prompt, then for each decode step
+    hash all logits as i32 LE followed by the chosen token as u32 LE.
+
+    Works with any object exposing forward_token(token, pos) and reset()."""
+    model.reset()
+    pos = 0
+    logits = None
+    for tid in token_ids:
+        logits = model.forward_token(int(tid), pos)
+        pos += 1
+    h = hashlib.sha256()
+    out = []
+    for _ in range(max_new_tokens):
+        h.update(np.ascontiguousarray(logits, dtype="<i4").tobytes())
+        nxt = int(np.argmax(logits))
+        h.update(np.uint32(nxt).astype("<u4").tobytes())
+        out.append(nxt)
+        logits = model.forward_token(nxt, pos)
+        pos += 1
+    return out, h.hexdigest()

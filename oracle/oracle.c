@@ -490,19 +490,17 @@ static uint8_t* gen_wshift(uint64_t seed, uint32_t layer, uint32_t role, size_t 
     return p;
 }
 
-static uint8_t* gen_range_u8(uint64_t seed, uint32_t layer, uint32_t role, size_t n, int lo, int hi) {
+static uint8_t* gen_small_u8(uint64_t seed, uint32_t layer, uint32_t role, size_t n) {
     uint8_t* p = (uint8_t*)xalloc(n);
     if (!p) return NULL;
-    uint64_t ts = myl_tensor_seed(seed, layer, role);
-    for (size_t i = 0; i < n; ++i) p[i] = (uint8_t)myl_draw_range(myl_splitmix_at(ts, i), lo, hi);
+    for (size_t i = 0; i < n; ++i) p[i] = (uint8_t)myl_synth_small(seed, layer, role, i);
     return p;
 }
 
-static int16_t* gen_range_i16(uint64_t seed, uint32_t layer, uint32_t role, size_t n, int lo, int hi) {
+static int16_t* gen_small_i16(uint64_t seed, uint32_t layer, uint32_t role, size_t n) {
     int16_t* p = (int16_t*)xalloc(n * sizeof(int16_t));
     if (!p) return NULL;
-    uint64_t ts = myl_tensor_seed(seed, layer, role);
-    for (size_t i = 0; i < n; ++i) p[i] = (int16_t)myl_draw_range(myl_splitmix_at(ts, i), lo, hi);
+    for (size_t i = 0; i < n; ++i) p[i] = (int16_t)myl_synth_small(seed, layer, role, i);
     return p;
 }
 
@@ -544,7 +542,7 @@ or_model* or_model_create_synthetic(const myl_synth_spec* spec, const myl_luts* 
     const size_t qN = (size_t)s.heads * hd, kvN = (size_t)s.kv_heads * hd;
 
     m->emb = gen_w8(seed, 0, MYL_R_EMB, V * H);
-    m->emb_shifts = gen_range_u8(seed, 0, MYL_R_EMB_SHIFT, V, 7, 9);
+    m->emb_shifts = gen_small_u8(seed, 0, MYL_R_EMB_SHIFT, V);
     if (s.lm_head_int16) {
         m->lm16 = (int16_t*)xalloc(V * H * sizeof(int16_t));
         uint64_t ts = myl_tensor_seed(seed, 0, MYL_R_LM16);
@@ -553,10 +551,10 @@ or_model* or_model_create_synthetic(const myl_synth_spec* spec, const myl_luts* 
 #pragma omp parallel for schedule(static) if (n > (1 << 20))
             for (long long i = 0; i < n; ++i) m->lm16[i] = myl_synth_w16(ts, (uint64_t)i);
         }
-        m->lm16_shifts = gen_range_u8(seed, 0, MYL_R_LM16_SHIFT, V, 17, 19);
+        m->lm16_shifts = gen_small_u8(seed, 0, MYL_R_LM16_SHIFT, V);
     }
     m->final_gamma = gen_w8(seed, 0, MYL_R_FINAL_GAMMA, H);
-    m->final_gamma_shifts = gen_range_u8(seed, 0, MYL_R_FINAL_GAMMA_SHIFT, H, 6, 7);
+    m->final_gamma_shifts = gen_small_u8(seed, 0, MYL_R_FINAL_GAMMA_SHIFT, H);
     m->final_norm_frac = myl_synth_final_norm_frac(seed);
     m->final_res_frac = (uint8_t*)xalloc(H);
     if (m->final_res_frac) {
@@ -575,9 +573,9 @@ or_model* or_model_create_synthetic(const myl_synth_spec* spec, const myl_luts* 
     for (uint32_t l = 0; l < s.layers; ++l) {
         or_layer* L = &m->layers[l];
         L->in_gamma = gen_w8(seed, l, MYL_R_IN_GAMMA, H);
-        L->in_gamma_shifts = gen_range_u8(seed, l, MYL_R_IN_GAMMA_SHIFT, H, 6, 7);
+        L->in_gamma_shifts = gen_small_u8(seed, l, MYL_R_IN_GAMMA_SHIFT, H);
         L->post_gamma = gen_w8(seed, l, MYL_R_POST_GAMMA, H);
-        L->post_gamma_shifts = gen_range_u8(seed, l, MYL_R_POST_GAMMA_SHIFT, H, 6, 7);
+        L->post_gamma_shifts = gen_small_u8(seed, l, MYL_R_POST_GAMMA_SHIFT, H);
         L->wq = gen_w8(seed, l, MYL_R_WQ, qN * H);  L->sq = gen_wshift(seed, l, MYL_R_SQ, qN, H);
         L->wk = gen_w8(seed, l, MYL_R_WK, kvN * H); L->sk = gen_wshift(seed, l, MYL_R_SK, kvN, H);
         L->wv = gen_w8(seed, l, MYL_R_WV, kvN * H); L->sv = gen_wshift(seed, l, MYL_R_SV, kvN, H);
@@ -586,12 +584,12 @@ or_model* or_model_create_synthetic(const myl_synth_spec* spec, const myl_luts* 
         L->wu = gen_w8(seed, l, MYL_R_WU, I * H);   L->su = gen_wshift(seed, l, MYL_R_SU, I, H);
         L->wd = gen_w8(seed, l, MYL_R_WD, H * I);   L->sd = gen_wshift(seed, l, MYL_R_SD, H, I);
         if (s.attention_bias) {
-            L->bq = gen_range_i16(seed, l, MYL_R_BQ, qN, -3000, 3000);
-            L->bk = gen_range_i16(seed, l, MYL_R_BK, kvN, -3000, 3000);
-            L->bv = gen_range_i16(seed, l, MYL_R_BV, kvN, -3000, 3000);
-            L->bq_s = gen_range_u8(seed, l, MYL_R_BQ_SHIFT, qN, 10, 13);
-            L->bk_s = gen_range_u8(seed, l, MYL_R_BK_SHIFT, kvN, 10, 13);
-            L->bv_s = gen_range_u8(seed, l, MYL_R_BV_SHIFT, kvN, 10, 13);
+            L->bq = gen_small_i16(seed, l, MYL_R_BQ, qN);
+            L->bk = gen_small_i16(seed, l, MYL_R_BK, kvN);
+            L->bv = gen_small_i16(seed, l, MYL_R_BV, kvN);
+            L->bq_s = gen_small_u8(seed, l, MYL_R_BQ_SHIFT, qN);
+            L->bk_s = gen_small_u8(seed, l, MYL_R_BK_SHIFT, kvN);
+            L->bv_s = gen_small_u8(seed, l, MYL_R_BV_SHIFT, kvN);
         }
         L->f = myl_synth_layer_fracs(seed, l);
         L->res_in_frac = (uint8_t*)xalloc(H);
