@@ -1,0 +1,263 @@
+#!/usr/bin/env python3
+"""Benchmark: Qwen2.5-7B-shape integer decode at batch 1 on one MI355X, plus
+the W8A16 GEMV sweep's HBM bandwidth, both bit-exact with the CPU reference.
+
+Workload (the BASELINE 7B decode configuration at batch 1): a Qwen2.5-7B
+architecture integer model (28 layers, hidden 3584, 28/4 heads, head_dim 128,
+intermediate 18944, vocab 152064, int16 LM head) with seeded synthetic int8
+weights and per-channel power-of-two scales; a 2048-token seeded prompt is
+prefilled (untimed), then `--warmup` + `--steps` greedy decode steps run at
+positions 2048.. (the RoPE LUT rows wrap at 2048).  Each step is one token:
+the timed region is `--steps` consecutive device-chained greedy steps.
+
+Also reported:
+  roofline     the dominant decode kernel (the fused gate/up W8A16 GEMV),
+               timed with HIP events around its launches in the same run;
+  gemv         the W8A16 sweep at M = 1 with multiplier requant, over
+               rotating weight copies (> 512 MB distinct) so the 256 MB
+               Infinity Cache cannot serve repeats;
+  cpu_baseline the CPU oracle (a single-thread restatement of the reference's
+               scalar Rust path) on a bounded sample of the same workload, on
+               this host's cores, after checking its logits equal the GPU's.
+
+Prints ONE JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model_name() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def class_bytes(spec: dict) -> dict:
+    """Algorithmic HBM bytes per launch of each decode kernel class (M = 1)."""
+    H, I, V = spec["hidden"], spec["inter"], spec["vocab"]
+    nq = spec["heads"] * spec["head_dim"]
+    nkv = spec["kv_heads"] * spec["head_dim"]
+    n_qkv = nq + 2 * nkv
+    lm_w = 2 if spec["lm_head_int16"] else 1
+    return {
+        # weights + x (i16) + out (i16) + per-row shift (u8) (+ bias i16 + bias shift u8)
+        "qkv": n_qkv * H + 2 * H + 2 * n_qkv + n_qkv * (1 + 3 * spec["attention_bias"]),
+        "o_proj": H * nq + 2 * nq + 2 * H + H + 2 * H + 4 * H,   # + residual in, 3 per-channel frac vectors
+        "gate_up": 2 * I * H + 2 * H + 2 * I + 2 * I,
+        "down": H * I + 2 * I + 2 * H + H + 2 * H + 4 * H,
+        "lm_head": lm_w * V * H + 2 * H + 4 * V + V,
+    }
+
+
+def gemv_sweep(backend, shapes, reps_target_bytes=6 << 30):
+    """M = 1 W8A16 GEMV with multiplier requant; bytes = N*K + 2K + 2N + 5N."""
+    import torch
+    out = {}
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1234)
+    for (N, K) in shapes:
+        per = N * K
+        copies = max(2, -(-(512 << 20) // per))  # >= 512 MB of distinct weights
+        Ws = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g) for _ in range(copies)]
+        x = torch.randint(-32767, 32768, (1, K), dtype=torch.int16, device="cuda", generator=g)
+        mult = torch.randint(1 << 29, (1 << 30) + 1, (N,), dtype=torch.int32, device="cuda", generator=g)
+        sh = torch.randint(20, 41, (N,), dtype=torch.uint8, device="cuda", generator=g)
+        y = torch.empty((1, N), dtype=torch.int16, device="cuda")
+        for W in Ws:  # warm-up
+            backend.linear_w8a16_mult_dev(x, W, mult, sh, out=y)
+        launches = max(copies, int(reps_target_bytes // per) // copies * copies)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(launches):
+            backend.linear_w8a16_mult_dev(x, Ws[i % copies], mult, sh, out=y)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / launches
+        nbytes = N * K + 2 * K + 2 * N + 5 * N
+        out[f"M1_N{N}_K{K}"] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                "bytes": nbytes, "launches": launches, "distinct_weight_MB": round(copies * per / 2**20)}
+        log(f"gemv N={N} K={K}: {ms * 1e3:.2f} us, {nbytes / (ms * 1e-3) / 1e9:.0f} GB/s")
+        del Ws
+        torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(spec, gpu_model, prompt, n_decode):
+    """Times the oracle (single thread) on a bounded sample: forward_token of a
+    short prompt + n_decode greedy steps of the same model; checks that the GPU
+    computes the same logits for the same tokens."""
+    import numpy as np
+    from myelith_amd.luts import LutSet
+    from oracle.binding import OracleModel, lib as olib
+    ospec = dict(spec)
+    ospec["max_pos"] = len(prompt) + n_decode + 1
+    t0 = time.time()
+    om = OracleModel(ospec, LutSet.for_head_dim(spec["head_dim"]), threads=1)
+    log(f"oracle model built in {time.time() - t0:.1f} s")
+    olib().or_set_threads(1)
+    pos = 0
+    logits = None
+    for t in prompt:
+        logits = om.forward_token(int(t), pos)
+        pos += 1
+    gpu_model.reset()
+    g_logits = gpu_model.prefill(prompt, 0)
+    if not np.array_equal(g_logits, logits):
+        raise SystemExit("bench: GPU logits differ from the CPU oracle; refusing to report a number")
+    times = []
+    for _ in range(n_decode):
+        tok = int(np.argmax(logits))
+        t1 = time.perf_counter()
+        logits = om.forward_token(tok, pos)
+        times.append(time.perf_counter() - t1)
+        g = gpu_model.forward_token(tok, pos)
+        if not np.array_equal(g, logits):
+            raise SystemExit("bench: GPU logits differ from the CPU oracle during decode")
+        pos += 1
+    om.close()
+    per_tok = sum(times) / len(times)
+    return {"value": round(1.0 / per_tok, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"oracle forward_token, 1 thread, {n_decode} greedy decode steps after a {len(prompt)}-token "
+                      f"prompt of the same 7B-shape model ({per_tok:.2f} s/token); logits checked equal to the GPU's",
+            "host_cpu": cpu_model_name(), "host_nproc": os.cpu_count()}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=240)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--ctx", type=int, default=2048)
+    ap.add_argument("--seed", type=int, default=7)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-gemv", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the integer decode path runs on a single MI355X "
+              "(multi-GPU sharding is a design note, not part of this build). Use --gpus 1.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    from myelith_amd.backend import RocmBackend
+    from myelith_amd.luts import LutSet
+    from myelith_amd.model import QWEN25_7B, IntegerModel, make_spec
+
+    assert torch.cuda.is_available(), "bench.py needs the GPU"
+    backend = RocmBackend(0)
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    backend.use_torch_stream()
+
+    total_steps = args.warmup + args.steps
+    spec = make_spec(QWEN25_7B, seed=args.seed, max_pos=args.ctx + total_steps + 8)
+    t0 = time.time()
+    model = IntegerModel(backend, spec, LutSet.for_head_dim(spec["head_dim"]))
+    log(f"7B-shape model built in HBM in {time.time() - t0:.1f} s")
+
+    rng = np.random.default_rng(args.seed)
+    prompt = rng.integers(0, spec["vocab"], args.ctx).astype(np.uint32)
+    t0 = time.time()
+    logits = model.prefill(prompt, 0)
+    log(f"prefilled {args.ctx} tokens in {time.time() - t0:.1f} s")
+    tok = int(np.argmax(logits))
+    pos = args.ctx
+
+    # warmup steps (also captures the step graph)
+    toks, _ = model.decode_greedy(tok, pos, args.warmup)
+    tok, pos = int(toks[-1]), pos + args.warmup
+
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    toks, _ = model.decode_greedy(tok, pos, args.steps)
+    e1.record()
+    torch.cuda.synchronize()
+    ms_total = e0.elapsed_time(e1)
+    ms_step = ms_total / args.steps
+    tok_s = 1000.0 / ms_step
+    log(f"decode: {args.steps} steps in {ms_total:.1f} ms -> {ms_step:.3f} ms/token, {tok_s:.1f} tok/s")
+
+    # per-kernel-class timing of 8 more steps of the same decode (HIP events
+    # around each launch on the decode stream)
+    model.timing(True)
+    model.decode_greedy(int(toks[-1]), pos + args.steps, 8)
+    classes = model.timing(False)
+    cb = class_bytes(spec)
+    per_class = {}
+    for k, (ms, n) in classes.items():
+        if n:
+            avg_us = ms / n * 1e3
+            d = {"avg_us": round(avg_us, 2), "launches": n, "total_ms": round(ms, 3)}
+            if k in cb:
+                d["GBps"] = round(cb[k] / (avg_us * 1e-6) / 1e9, 1)
+            per_class[k] = d
+    dom = max((k for k in per_class if k in cb), key=lambda k: per_class[k]["total_ms"])
+    achieved = per_class[dom]["GBps"]
+    log("kernel classes: " + ", ".join(f"{k} {v['avg_us']}us" for k, v in per_class.items()))
+
+    gemv = {}
+    if not args.no_gemv:
+        gemv = gemv_sweep(backend, [(3584, 3584), (18944, 3584), (3584, 18944), (152064, 3584)])
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(spec, model, [int(t) for t in prompt[:4]], 3)
+
+    step_bytes = 28 * (cb["qkv"] + cb["o_proj"] + cb["gate_up"] + cb["down"]) + cb["lm_head"]
+    kv_bytes = 2 * spec["layers"] * spec["kv_heads"] * spec["head_dim"] * 2 * (pos + args.steps // 2)
+    rec = {
+        "metric": "7B-shape int decode tok/s (bs=1) + W8A16 GEMV HBM GB/s, bit-exact",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int64",
+        "data": "synthetic: seeded int8 weights, per-channel power-of-two scales, theta_v 0.17.0 LUTs",
+        "config": {"workload": "qwen2.5-7b-shape integer decode, batch 1, 2048-token prefilled context, greedy",
+                   "batch": 1, "context": args.ctx, "positions": f"{args.ctx}-{args.ctx + total_steps - 1}",
+                   "seed": args.seed},
+        "decode_bytes_per_token": step_bytes + kv_bytes,
+        "decode_GBps": round((step_bytes + kv_bytes) / (ms_step * 1e-3) / 1e9, 1),
+        "roofline": {"bound": "hbm", "kernel": f"{dom} W8A16 GEMV in decode (M=1)",
+                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": cb[dom], "avg_us": per_class[dom]["avg_us"]},
+        "kernel_classes": per_class,
+        "gemv": gemv,
+        "cpu_baseline": cpu,
+        "gpu": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

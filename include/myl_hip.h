@@ -184,6 +184,19 @@ int myl_model_forward_token(myl_model* m, uint32_t token, uint32_t pos, int32_t*
  * may be NULL. */
 int myl_model_decode_greedy(myl_model* m, uint32_t token, uint32_t pos, uint32_t n_steps, int64_t* tokens_out,
                             int32_t* logits_out);
+/* The prompt loop of generate.rs:28-32: tokens[i] at position pos0 + i, the
+ * KV cache filled exactly as by n forward_token calls.  Only the last
+ * position's logits are computed (earlier ones are discarded by the
+ * reference's loop); last_logits (host, vocab) may be NULL. */
+int myl_model_prefill(myl_model* m, const uint32_t* tokens, uint32_t n, uint32_t pos0, int32_t* last_logits);
+/* Greedy steps after the first replay one captured HIP graph (default on);
+ * enable = 0 launches every kernel from the host instead. */
+int myl_model_set_graphs(myl_model* m, int enable);
+/* Per-kernel-class timing with HIP events around each launch (eager launches,
+ * no graphs while enabled).  enable = 1 starts; enable = 0 stops and returns
+ * per class the summed milliseconds and launch counts in the order embed,
+ * rmsnorm, qkv, attention, o_proj, gate_up, down, lm_head (8 entries each). */
+int myl_model_timing(myl_model* m, int enable, double* ms_out, uint64_t* counts_out);
 /* IntegerModel::embed_token (model.rs:323-331): hidden (host, hidden entries). */
 int myl_model_embed_token(myl_model* m, uint32_t token, int16_t* hidden);
 /* IntegerModel::run_layers (model.rs:339-356), hidden in/out on the host. */

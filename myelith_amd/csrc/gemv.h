@@ -49,8 +49,33 @@ __device__ inline int32_t sdot4(uint32_t a, uint32_t b, int32_t c) {
 
 // Stage x[m][k0 .. k0+len) of M rows into two signed byte planes (len is a
 // multiple of 16, zero-padded past K: hi = 0, lo' = -128 with w = 0 there).
+// With xvec, each thread converts 8 activations from one 16-byte load: the
+// high bytes of the int16 lanes form the hi plane, the low bytes XOR 0x80
+// (i.e. lo - 128) form the lo' plane.
 __device__ inline void stage_x_planes(const int16_t* __restrict__ x, int M, int ldx, int K, int k0,
-                                      int len, int8_t* hi, int8_t* lo) {
+                                      int len, int8_t* hi, int8_t* lo, bool xvec) {
+    if (xvec) {
+        const int n8 = len >> 3;
+        for (int m = 0; m < M; ++m) {
+            for (int i = threadIdx.x; i < n8; i += blockDim.x) {
+                const int kk = k0 + i * 8;
+                uint4 v = make_uint4(0, 0, 0, 0);
+                if (kk < K) v = *reinterpret_cast<const uint4*>(x + (size_t)m * ldx + kk);
+                const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+                uint32_t h[2], l[2];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const uint32_t d0 = d[2 * t], d1 = d[2 * t + 1];
+                    h[t] = ((d0 >> 8) & 0xFFu) | ((d0 >> 16) & 0xFF00u) | ((d1 << 8) & 0xFF0000u) | (d1 & 0xFF000000u);
+                    l[t] = ((d0 & 0xFFu) | ((d0 >> 8) & 0xFF00u) | ((d1 << 16) & 0xFF0000u) | ((d1 << 8) & 0xFF000000u))
+                           ^ 0x80808080u;
+                }
+                *reinterpret_cast<uint2*>(hi + m * len + i * 8) = make_uint2(h[0], h[1]);
+                *reinterpret_cast<uint2*>(lo + m * len + i * 8) = make_uint2(l[0], l[1]);
+            }
+        }
+        return;
+    }
     for (int m = 0; m < M; ++m) {
         for (int k = threadIdx.x; k < len; k += blockDim.x) {
             const int kk = k0 + k;
@@ -62,11 +87,14 @@ __device__ inline void stage_x_planes(const int16_t* __restrict__ x, int M, int 
 }
 
 // Core of the int8 kernel: the exact row sums of R rows x MT activation rows
-// for one wave, left in every lane of the wave.
-template <int R, int MT>
+// for one wave, left in every lane of the wave.  The wave walks its rows in
+// batches of U steps of 1 KiB per row: all U*R weight loads of a batch are
+// issued before any of them is consumed, and the first batch is issued before
+// the activations are staged, so the staging overlaps the weight stream.
+template <int R, int MT, int U>
 __device__ inline void gemv_i8_rows(const int16_t* __restrict__ x, int M, int ldx,
                                     const int8_t* __restrict__ W, int N, int K, int row0,
-                                    int8_t* hi_plane, int8_t* lo_plane, int kc,
+                                    int8_t* hi_plane, int8_t* lo_plane, int kc, bool xvec,
                                     int64_t (&tot)[R][MT]) {
     const int lane = threadIdx.x & (kWave - 1);
     int32_t ahi[R][MT], alo[R][MT], aws[R];
@@ -76,43 +104,67 @@ __device__ inline void gemv_i8_rows(const int16_t* __restrict__ x, int M, int ld
 #pragma unroll
         for (int m = 0; m < MT; ++m) { ahi[r][m] = 0; alo[r][m] = 0; }
     }
+    const int8_t* wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wrow[r] = W + (size_t)min(row0 + r, N - 1) * K;
+    bool rok[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) rok[r] = row0 + r < N;
+
     for (int k0 = 0; k0 < K; k0 += kc) {
         const int len = min(kc, K - k0);
+        uint4 w[U][R];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = u * (kWave * 16) + lane * 16;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                w[u][r] = (k < len && rok[r]) ? *reinterpret_cast<const uint4*>(wrow[r] + k0 + k) : make_uint4(0, 0, 0, 0);
+        }
         __syncthreads();
-        stage_x_planes(x, M, ldx, K, k0, len, hi_plane, lo_plane);
+        stage_x_planes(x, M, ldx, K, k0, len, hi_plane, lo_plane, xvec);
         __syncthreads();
-        for (int k = lane * 16; k < len; k += kWave * 16) {
-            uint4 w[R];
+        for (int kb = 0; kb < len; kb += U * kWave * 16) {
+            if (kb > 0) {
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int row = row0 + r;
-                if (row < N) w[r] = *reinterpret_cast<const uint4*>(W + (size_t)row * K + k0 + k);
-                else w[r] = make_uint4(0, 0, 0, 0);
-            }
+                for (int u = 0; u < U; ++u) {
+                    const int k = kb + u * (kWave * 16) + lane * 16;
 #pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                if (m < M) {
-                    const uint4 h = *reinterpret_cast<const uint4*>(hi_plane + m * len + k);
-                    const uint4 l = *reinterpret_cast<const uint4*>(lo_plane + m * len + k);
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        ahi[r][m] = sdot4(w[r].x, h.x, ahi[r][m]);
-                        ahi[r][m] = sdot4(w[r].y, h.y, ahi[r][m]);
-                        ahi[r][m] = sdot4(w[r].z, h.z, ahi[r][m]);
-                        ahi[r][m] = sdot4(w[r].w, h.w, ahi[r][m]);
-                        alo[r][m] = sdot4(w[r].x, l.x, alo[r][m]);
-                        alo[r][m] = sdot4(w[r].y, l.y, alo[r][m]);
-                        alo[r][m] = sdot4(w[r].z, l.z, alo[r][m]);
-                        alo[r][m] = sdot4(w[r].w, l.w, alo[r][m]);
-                    }
+                    for (int r = 0; r < R; ++r)
+                        w[u][r] = (k < len && rok[r]) ? *reinterpret_cast<const uint4*>(wrow[r] + k0 + k)
+                                                      : make_uint4(0, 0, 0, 0);
                 }
             }
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                aws[r] = sdot4(w[r].x, 0x01010101u, aws[r]);
-                aws[r] = sdot4(w[r].y, 0x01010101u, aws[r]);
-                aws[r] = sdot4(w[r].z, 0x01010101u, aws[r]);
-                aws[r] = sdot4(w[r].w, 0x01010101u, aws[r]);
+            for (int u = 0; u < U; ++u) {
+                const int k = kb + u * (kWave * 16) + lane * 16;
+                if (k < len) {
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        if (m < M) {
+                            const uint4 h = *reinterpret_cast<const uint4*>(hi_plane + m * len + k);
+                            const uint4 l = *reinterpret_cast<const uint4*>(lo_plane + m * len + k);
+#pragma unroll
+                            for (int r = 0; r < R; ++r) {
+                                ahi[r][m] = sdot4(w[u][r].x, h.x, ahi[r][m]);
+                                ahi[r][m] = sdot4(w[u][r].y, h.y, ahi[r][m]);
+                                ahi[r][m] = sdot4(w[u][r].z, h.z, ahi[r][m]);
+                                ahi[r][m] = sdot4(w[u][r].w, h.w, ahi[r][m]);
+                                alo[r][m] = sdot4(w[u][r].x, l.x, alo[r][m]);
+                                alo[r][m] = sdot4(w[u][r].y, l.y, alo[r][m]);
+                                alo[r][m] = sdot4(w[u][r].z, l.z, alo[r][m]);
+                                alo[r][m] = sdot4(w[u][r].w, l.w, alo[r][m]);
+                            }
+                        }
+                    }
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        aws[r] = sdot4(w[u][r].x, 0x01010101u, aws[r]);
+                        aws[r] = sdot4(w[u][r].y, 0x01010101u, aws[r]);
+                        aws[r] = sdot4(w[u][r].z, 0x01010101u, aws[r]);
+                        aws[r] = sdot4(w[u][r].w, 0x01010101u, aws[r]);
+                    }
+                }
             }
         }
     }
@@ -127,74 +179,118 @@ __device__ inline void gemv_i8_rows(const int16_t* __restrict__ x, int M, int ld
 }
 
 // One block = 4 waves x R rows.  The epilogue sees all R x MT sums of its wave.
-template <int R, int MT, class Epi>
+template <int R, int MT, int U, class Epi>
 __global__ __launch_bounds__(kGemvThreads) void gemv_i8_kernel(const int16_t* __restrict__ x, int M, int ldx,
                                                               const int8_t* __restrict__ W, int N, int K,
-                                                              int kc, Epi epi) {
+                                                              int kc, int xvec, Epi epi) {
     extern __shared__ __align__(16) int8_t lds[];
     const int wave = threadIdx.x / kWave;
     const int row0 = (blockIdx.x * kGemvWaves + wave) * R;
     int64_t tot[R][MT];
-    gemv_i8_rows<R, MT>(x, M, ldx, W, N, K, row0, lds, lds + MT * kc, kc, tot);
+    gemv_i8_rows<R, MT, U>(x, M, ldx, W, N, K, row0, lds, lds + MT * kc, kc, xvec != 0, tot);
     epi.apply(row0, N, M, threadIdx.x & (kWave - 1), tot);
 }
 
 // int16-weight kernel (LM head path A).  Planes are int16: hi = x >> 8,
-// lo = x & 255.
-template <int R, int MT, class Epi>
+// lo = x & 255; each lane reads 8 weights (16 B) per step.
+template <int R, int MT, int U, class Epi>
 __global__ __launch_bounds__(kGemvThreads) void gemv_i16_kernel(const int16_t* __restrict__ x, int M, int ldx,
                                                                const int16_t* __restrict__ W, int N, int K,
-                                                               int kc, Epi epi) {
+                                                               int kc, int xvec, Epi epi) {
     extern __shared__ __align__(16) int8_t lds_raw[];
     int16_t* hi_plane = reinterpret_cast<int16_t*>(lds_raw);
     int16_t* lo_plane = hi_plane + MT * kc;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int row0 = (blockIdx.x * kGemvWaves + wave) * R;
+    typedef short __attribute__((ext_vector_type(2))) s2;
     int32_t ahi[R][MT], alo[R][MT];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int m = 0; m < MT; ++m) { ahi[r][m] = 0; alo[r][m] = 0; }
+    const int16_t* wrow[R];
+    bool rok[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        wrow[r] = W + (size_t)min(row0 + r, N - 1) * K;
+        rok[r] = row0 + r < N;
+    }
     for (int k0 = 0; k0 < K; k0 += kc) {
         const int len = min(kc, K - k0);
+        uint4 w[U][R];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = u * (kWave * 8) + lane * 8;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                w[u][r] = (k < len && rok[r]) ? *reinterpret_cast<const uint4*>(wrow[r] + k0 + k) : make_uint4(0, 0, 0, 0);
+        }
         __syncthreads();
-        for (int m = 0; m < M; ++m) {
-            for (int k = threadIdx.x; k < len; k += blockDim.x) {
-                const int kk = k0 + k;
-                const int16_t v = kk < K ? x[(size_t)m * ldx + kk] : (int16_t)0;
-                hi_plane[m * len + k] = (int16_t)(v >> 8);
-                lo_plane[m * len + k] = (int16_t)(v & 255);
+        if (xvec) {
+            const int n8 = len >> 3;
+            for (int m = 0; m < M; ++m) {
+                for (int i = threadIdx.x; i < n8; i += blockDim.x) {
+                    const int kk = k0 + i * 8;
+                    uint4 v = make_uint4(0, 0, 0, 0);
+                    if (kk < K) v = *reinterpret_cast<const uint4*>(x + (size_t)m * ldx + kk);
+                    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+                    uint32_t h[4], l[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        h[t] = (((uint32_t)((int32_t)(d[t] << 16) >> 24)) & 0xFFFFu) | ((uint32_t)((int32_t)d[t] >> 24) << 16);
+                        l[t] = d[t] & 0x00FF00FFu;
+                    }
+                    *reinterpret_cast<uint4*>(hi_plane + m * len + i * 8) = make_uint4(h[0], h[1], h[2], h[3]);
+                    *reinterpret_cast<uint4*>(lo_plane + m * len + i * 8) = make_uint4(l[0], l[1], l[2], l[3]);
+                }
+            }
+        } else {
+            for (int m = 0; m < M; ++m) {
+                for (int k = threadIdx.x; k < len; k += blockDim.x) {
+                    const int kk = k0 + k;
+                    const int16_t v = kk < K ? x[(size_t)m * ldx + kk] : (int16_t)0;
+                    hi_plane[m * len + k] = (int16_t)(v >> 8);
+                    lo_plane[m * len + k] = (int16_t)(v & 255);
+                }
             }
         }
         __syncthreads();
-        for (int k = lane * 8; k < len; k += kWave * 8) {
-            uint4 w[R];
+        for (int kb = 0; kb < len; kb += U * kWave * 8) {
+            if (kb > 0) {
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int row = row0 + r;
-                if (row < N) w[r] = *reinterpret_cast<const uint4*>(W + (size_t)row * K + k0 + k);
-                else w[r] = make_uint4(0, 0, 0, 0);
+                for (int u = 0; u < U; ++u) {
+                    const int k = kb + u * (kWave * 8) + lane * 8;
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        w[u][r] = (k < len && rok[r]) ? *reinterpret_cast<const uint4*>(wrow[r] + k0 + k)
+                                                      : make_uint4(0, 0, 0, 0);
+                }
             }
 #pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                if (m < M) {
-                    const uint4 h = *reinterpret_cast<const uint4*>(hi_plane + m * len + k);
-                    const uint4 l = *reinterpret_cast<const uint4*>(lo_plane + m * len + k);
+            for (int u = 0; u < U; ++u) {
+                const int k = kb + u * (kWave * 8) + lane * 8;
+                if (k < len) {
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        typedef short __attribute__((ext_vector_type(2))) s2;
-                        auto d2 = [](uint32_t a, uint32_t b, int32_t c) {
-                            return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, a), __builtin_bit_cast(s2, b), c, false);
-                        };
-                        ahi[r][m] = d2(w[r].x, h.x, ahi[r][m]);
-                        ahi[r][m] = d2(w[r].y, h.y, ahi[r][m]);
-                        ahi[r][m] = d2(w[r].z, h.z, ahi[r][m]);
-                        ahi[r][m] = d2(w[r].w, h.w, ahi[r][m]);
-                        alo[r][m] = d2(w[r].x, l.x, alo[r][m]);
-                        alo[r][m] = d2(w[r].y, l.y, alo[r][m]);
-                        alo[r][m] = d2(w[r].z, l.z, alo[r][m]);
-                        alo[r][m] = d2(w[r].w, l.w, alo[r][m]);
+                    for (int m = 0; m < MT; ++m) {
+                        if (m < M) {
+                            const uint4 h = *reinterpret_cast<const uint4*>(hi_plane + m * len + k);
+                            const uint4 l = *reinterpret_cast<const uint4*>(lo_plane + m * len + k);
+#pragma unroll
+                            for (int r = 0; r < R; ++r) {
+                                auto d2 = [](uint32_t a, uint32_t b, int32_t c) {
+                                    return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, a), __builtin_bit_cast(s2, b), c, false);
+                                };
+                                ahi[r][m] = d2(w[u][r].x, h.x, ahi[r][m]);
+                                ahi[r][m] = d2(w[u][r].y, h.y, ahi[r][m]);
+                                ahi[r][m] = d2(w[u][r].z, h.z, ahi[r][m]);
+                                ahi[r][m] = d2(w[u][r].w, h.w, ahi[r][m]);
+                                alo[r][m] = d2(w[u][r].x, l.x, alo[r][m]);
+                                alo[r][m] = d2(w[u][r].y, l.y, alo[r][m]);
+                                alo[r][m] = d2(w[u][r].z, l.z, alo[r][m]);
+                                alo[r][m] = d2(w[u][r].w, l.w, alo[r][m]);
+                            }
+                        }
                     }
                 }
             }

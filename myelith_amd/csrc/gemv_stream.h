@@ -1,0 +1,237 @@
+// gemv_stream.h -- persistent, wave-streaming M = 1 GEMV for the decode step.
+//
+// The activation vector is staged once per block (the Src policy decides how:
+// plain int16, RMS-normalised on the fly, or reduced from the attention
+// accumulator), then every wave walks its own sequence of row groups
+//   g = wave_global, wave_global + waves_total, ...
+// with no further block-level synchronisation.  A group's weights are read in
+// batches of U steps of 1 KiB per row (int8) or 8 weights per lane (int16);
+// two register buffers alternate, so the loads of the next batch are in flight
+// while the current batch is multiplied.  The sums are exact (see gemv.h for
+// the byte-split bounds); the epilogue gets R rows per group.
+#pragma once
+
+#include "gemv.h"
+
+namespace myl {
+
+// A raw buffer descriptor over a whole weight matrix (gfx9-family dword 3).
+// Loads whose byte offset is at or past num_records return zero in hardware,
+// so out-of-range slots need no predicate: the loads stay straight-line code
+// and the compiler's in-order vmcnt accounting can keep a whole batch in
+// flight while the previous one is consumed.
+__device__ inline __amdgpu_buffer_rsrc_t weight_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ inline uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+}
+
+// ---- staging sources ----------------------------------------------------------
+
+// Plain int16 activations, converted to the two signed byte planes.
+struct SrcPlain {
+    const int16_t* x;
+    __device__ inline void stage_i8(int8_t* hi, int8_t* lo, int K, int kpad) const {
+        stage_x_planes(x, 1, K, K, 0, kpad, hi, lo, true);
+    }
+};
+
+template <int R, int U, int WAVES, class Src, class Epi>
+__global__ __launch_bounds__(WAVES * 64) void gemv_i8_stream(Src src, const int8_t* __restrict__ W, int N, int K,
+                                                            Epi epi) {
+    extern __shared__ __align__(16) int8_t lds[];
+    const int kpad = ((K + 15) >> 4) << 4;
+    int8_t* hi_plane = lds;
+    int8_t* lo_plane = lds + kpad;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int nw = gridDim.x * WAVES;
+    const int ngroups = (N + R - 1) / R;
+    const int nit = (K + kWave * 16 - 1) / (kWave * 16);  // 1 KiB steps per row
+    const int nb = (nit + U - 1) / U;                      // batches per group
+    typename Epi::State es;
+    epi.begin(es);
+
+    const uint32_t wbytes = (uint32_t)N * (uint32_t)K;  // < 2^32 (checked by the launcher)
+    const __amdgpu_buffer_rsrc_t wr = weight_rsrc(W, wbytes);
+    auto load = [&](uint4 (&buf)[U][R], int g, int kb) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = (kb * U + u) * (kWave * 16) + lane * 16;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int row = g * R + r;
+                const bool ok = k < K && row < N;
+                buf[u][r] = bload16(wr, ok ? (uint32_t)row * (uint32_t)K + (uint32_t)k : wbytes);
+            }
+        }
+    };
+    int32_t ahi[R], alo[R], aws[R];
+    auto reset = [&]() {
+#pragma unroll
+        for (int r = 0; r < R; ++r) { ahi[r] = 0; alo[r] = 0; aws[r] = 0; }
+    };
+    // Out-of-range slots hold zero weights, so they may read any staged
+    // column: the LDS offset is clamped into the planes.
+    auto compute = [&](const uint4 (&buf)[U][R], int kb) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = min((kb * U + u) * (kWave * 16) + lane * 16, kpad - 16);
+            const uint4 h = *reinterpret_cast<const uint4*>(hi_plane + k);
+            const uint4 l = *reinterpret_cast<const uint4*>(lo_plane + k);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                ahi[r] = sdot4(buf[u][r].x, h.x, ahi[r]);
+                ahi[r] = sdot4(buf[u][r].y, h.y, ahi[r]);
+                ahi[r] = sdot4(buf[u][r].z, h.z, ahi[r]);
+                ahi[r] = sdot4(buf[u][r].w, h.w, ahi[r]);
+                alo[r] = sdot4(buf[u][r].x, l.x, alo[r]);
+                alo[r] = sdot4(buf[u][r].y, l.y, alo[r]);
+                alo[r] = sdot4(buf[u][r].z, l.z, alo[r]);
+                alo[r] = sdot4(buf[u][r].w, l.w, alo[r]);
+                aws[r] = sdot4(buf[u][r].x, 0x01010101u, aws[r]);
+                aws[r] = sdot4(buf[u][r].y, 0x01010101u, aws[r]);
+                aws[r] = sdot4(buf[u][r].z, 0x01010101u, aws[r]);
+                aws[r] = sdot4(buf[u][r].w, 0x01010101u, aws[r]);
+            }
+        }
+    };
+    auto finish_group = [&](int g) {
+        int64_t tot[R][1];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            tot[r][0] = wave_sum_i64((int64_t)ahi[r] * 256 + (int64_t)alo[r] + (int64_t)aws[r] * 128);
+        epi.group(es, g * R, N, lane, tot);
+        reset();
+    };
+
+    uint4 A[U][R], B[U][R];
+    int g = blockIdx.x * WAVES + wave, kb = 0;
+    load(A, g, 0);
+    src.stage_i8(hi_plane, lo_plane, K, kpad);
+    epi.zero_duty();
+    __syncthreads();
+    reset();
+    while (g < ngroups) {
+        int g2 = g, kb2 = kb + 1;
+        if (kb2 == nb) { kb2 = 0; g2 = g + nw; }
+        load(B, g2, kb2);
+        compute(A, kb);
+        if (kb == nb - 1) finish_group(g);
+        g = g2;
+        kb = kb2;
+        if (g >= ngroups) break;
+        g2 = g;
+        kb2 = kb + 1;
+        if (kb2 == nb) { kb2 = 0; g2 = g + nw; }
+        load(A, g2, kb2);
+        compute(B, kb);
+        if (kb == nb - 1) finish_group(g);
+        g = g2;
+        kb = kb2;
+    }
+    epi.finish(es);
+}
+
+// int16 weights (LM head path A): planes of int16 hi = x >> 8 and lo = x & 255.
+struct SrcPlain16 {
+    const int16_t* x;
+};
+
+template <int R, int U, int WAVES, class Src16, class Epi>
+__global__ __launch_bounds__(WAVES * 64) void gemv_i16_stream(Src16 src, const int16_t* __restrict__ W, int N,
+                                                             int K, Epi epi) {
+    extern __shared__ __align__(16) int8_t lds_raw[];
+    const int kpad = ((K + 7) >> 3) << 3;
+    int16_t* hi_plane = reinterpret_cast<int16_t*>(lds_raw);
+    int16_t* lo_plane = hi_plane + kpad;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int nw = gridDim.x * WAVES;
+    const int ngroups = (N + R - 1) / R;
+    const int nit = (K + kWave * 8 - 1) / (kWave * 8);
+    const int nb = (nit + U - 1) / U;
+    typedef short __attribute__((ext_vector_type(2))) s2;
+    typename Epi::State es;
+    epi.begin(es);
+
+    const uint32_t wbytes = 2u * (uint32_t)N * (uint32_t)K;  // < 2^32 (checked by the launcher)
+    const __amdgpu_buffer_rsrc_t wr = weight_rsrc(W, wbytes);
+    auto load = [&](uint4 (&buf)[U][R], int g, int kb) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = (kb * U + u) * (kWave * 8) + lane * 8;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int row = g * R + r;
+                const bool ok = k < K && row < N;
+                buf[u][r] = bload16(wr, ok ? 2u * ((uint32_t)row * (uint32_t)K + (uint32_t)k) : wbytes);
+            }
+        }
+    };
+    int32_t ahi[R], alo[R];
+    auto reset = [&]() {
+#pragma unroll
+        for (int r = 0; r < R; ++r) { ahi[r] = 0; alo[r] = 0; }
+    };
+    auto d2 = [](uint32_t a, uint32_t b, int32_t c) {
+        return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, a), __builtin_bit_cast(s2, b), c, false);
+    };
+    auto compute = [&](const uint4 (&buf)[U][R], int kb) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = min((kb * U + u) * (kWave * 8) + lane * 8, kpad - 8);
+            const uint4 h = *reinterpret_cast<const uint4*>(hi_plane + k);
+            const uint4 l = *reinterpret_cast<const uint4*>(lo_plane + k);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                ahi[r] = d2(buf[u][r].x, h.x, ahi[r]);
+                ahi[r] = d2(buf[u][r].y, h.y, ahi[r]);
+                ahi[r] = d2(buf[u][r].z, h.z, ahi[r]);
+                ahi[r] = d2(buf[u][r].w, h.w, ahi[r]);
+                alo[r] = d2(buf[u][r].x, l.x, alo[r]);
+                alo[r] = d2(buf[u][r].y, l.y, alo[r]);
+                alo[r] = d2(buf[u][r].z, l.z, alo[r]);
+                alo[r] = d2(buf[u][r].w, l.w, alo[r]);
+            }
+        }
+    };
+    auto finish_group = [&](int g) {
+        int64_t tot[R][1];
+#pragma unroll
+        for (int r = 0; r < R; ++r) tot[r][0] = wave_sum_i64((int64_t)ahi[r] * 256 + (int64_t)alo[r]);
+        epi.group(es, g * R, N, lane, tot);
+        reset();
+    };
+
+    uint4 A[U][R], B[U][R];
+    int g = blockIdx.x * WAVES + wave, kb = 0;
+    load(A, g, 0);
+    src.stage_i16(hi_plane, lo_plane, K, kpad);
+    epi.zero_duty();
+    __syncthreads();
+    reset();
+    while (g < ngroups) {
+        int g2 = g, kb2 = kb + 1;
+        if (kb2 == nb) { kb2 = 0; g2 = g + nw; }
+        load(B, g2, kb2);
+        compute(A, kb);
+        if (kb == nb - 1) finish_group(g);
+        g = g2;
+        kb = kb2;
+        if (g >= ngroups) break;
+        g2 = g;
+        kb2 = kb + 1;
+        if (kb2 == nb) { kb2 = 0; g2 = g + nw; }
+        load(A, g2, kb2);
+        compute(B, kb);
+        if (kb == nb - 1) finish_group(g);
+        g = g2;
+        kb = kb2;
+    }
+    epi.finish(es);
+}
+
+}  // namespace myl

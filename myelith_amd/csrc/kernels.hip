@@ -11,24 +11,28 @@ namespace myl {
 // GEMV dispatch
 // ---------------------------------------------------------------------------
 
-template <int R, int MT, class Epi>
+inline int xvec_ok(const int16_t* x, int ldx) { return (((uintptr_t)x & 15) == 0) && (ldx % 8 == 0); }
+
+template <int R, int MT, int U, class Epi>
 static hipError_t launch_i8(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, const Epi& epi,
                             hipStream_t st) {
     // K-chunk staged in LDS per pass: both byte planes of MT rows fit 64 KiB.
     const int kc = min(kGemvLdsBytes / (2 * MT), ((K + 15) / 16) * 16);
     const int rows_per_block = R * kGemvWaves;
     const int blocks = (N + rows_per_block - 1) / rows_per_block;
-    gemv_i8_kernel<R, MT, Epi><<<blocks, kGemvThreads, (size_t)2 * MT * kc, st>>>(x, M, ldx, W, N, K, kc, epi);
+    gemv_i8_kernel<R, MT, U, Epi><<<blocks, kGemvThreads, (size_t)2 * MT * kc, st>>>(x, M, ldx, W, N, K, kc,
+                                                                                   xvec_ok(x, ldx), epi);
     return hipGetLastError();
 }
 
-template <int R, int MT, class Epi>
+template <int R, int MT, int U, class Epi>
 static hipError_t launch_i16(const int16_t* x, int M, int ldx, const int16_t* W, int N, int K, const Epi& epi,
                              hipStream_t st) {
     const int kc = min(kGemvLdsBytes / (4 * MT), ((K + 7) / 8) * 8);
     const int rows_per_block = R * kGemvWaves;
     const int blocks = (N + rows_per_block - 1) / rows_per_block;
-    gemv_i16_kernel<R, MT, Epi><<<blocks, kGemvThreads, (size_t)4 * MT * kc, st>>>(x, M, ldx, W, N, K, kc, epi);
+    gemv_i16_kernel<R, MT, U, Epi><<<blocks, kGemvThreads, (size_t)4 * MT * kc, st>>>(x, M, ldx, W, N, K, kc,
+                                                                                    xvec_ok(x, ldx), epi);
     return hipGetLastError();
 }
 
@@ -47,10 +51,12 @@ static hipError_t gemv_i8(const int16_t* x, int M, int ldx, const int8_t* W, int
         Epi e = epi.offset_m(m0);
         hipError_t rc;
         const int16_t* xm = x + (size_t)m0 * ldx;
-        if (mm == 1) rc = launch_i8<2, 1>(xm, mm, ldx, W, N, K, e, st);
-        else if (mm == 2) rc = launch_i8<2, 2>(xm, mm, ldx, W, N, K, e, st);
-        else if (mm <= 4) rc = launch_i8<2, 4>(xm, mm, ldx, W, N, K, e, st);
-        else rc = launch_i8<1, 8>(xm, mm, ldx, W, N, K, e, st);
+        // Few rows: one row per wave so that the grid still fills the chip.
+        const bool few = N < 8192;
+        if (mm == 1) rc = few ? launch_i8<1, 1, 4>(xm, mm, ldx, W, N, K, e, st) : launch_i8<2, 1, 4>(xm, mm, ldx, W, N, K, e, st);
+        else if (mm == 2) rc = launch_i8<2, 2, 4>(xm, mm, ldx, W, N, K, e, st);
+        else if (mm <= 4) rc = launch_i8<2, 4, 2>(xm, mm, ldx, W, N, K, e, st);
+        else rc = launch_i8<1, 8, 2>(xm, mm, ldx, W, N, K, e, st);
         if (rc != hipSuccess) return rc;
     }
     return hipSuccess;
@@ -70,8 +76,8 @@ static hipError_t gemv_i16(const int16_t* x, int M, int ldx, const int16_t* W, i
         Epi e = epi.offset_m(m0);
         hipError_t rc;
         const int16_t* xm = x + (size_t)m0 * ldx;
-        if (mm == 1) rc = launch_i16<2, 1>(xm, mm, ldx, W, N, K, e, st);
-        else rc = launch_i16<1, 4>(xm, mm, ldx, W, N, K, e, st);
+        if (mm == 1) rc = launch_i16<2, 1, 4>(xm, mm, ldx, W, N, K, e, st);
+        else rc = launch_i16<1, 4, 2>(xm, mm, ldx, W, N, K, e, st);
         if (rc != hipSuccess) return rc;
     }
     return hipSuccess;
@@ -124,11 +130,48 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const int16_t* __restri
     for (int i = threadIdx.x; i < n; i += blockDim.x) o[i] = rms_out(xr[i], xs[i], g[i], gs[i], f, out_frac);
 }
 
+// Rows of up to kRmsThreads * kRmsPer elements: every element is loaded once,
+// before the reductions, and stays in registers.
+constexpr int kRmsThreads = 1024;
+constexpr int kRmsPer = 4;
+__global__ __launch_bounds__(kRmsThreads) void rmsnorm_fast_kernel(const int16_t* __restrict__ x, int ldx,
+                                                                  const uint8_t* __restrict__ xs,
+                                                                  const int8_t* __restrict__ g,
+                                                                  const uint8_t* __restrict__ gs, int n, RmsParams p,
+                                                                  uint8_t out_frac, int16_t* __restrict__ out, int ldo) {
+    __shared__ myl_i128 red128[kRmsThreads / 64];
+    __shared__ int32_t red32[kRmsThreads / 64];
+    const int16_t* xr = x + (size_t)blockIdx.x * ldx;
+    int16_t xv[kRmsPer];
+    uint8_t sv[kRmsPer];
+    int8_t gv[kRmsPer];
+    uint8_t gsv[kRmsPer];
+#pragma unroll
+    for (int t = 0; t < kRmsPer; ++t) {
+        const int i = threadIdx.x + t * kRmsThreads;
+        const bool ok = i < n;
+        xv[t] = ok ? xr[i] : (int16_t)0;
+        sv[t] = ok ? xs[i] : (uint8_t)0;
+        gv[t] = ok ? g[i] : (int8_t)0;
+        gsv[t] = ok ? gs[i] : (uint8_t)0;
+    }
+    const RmsFactor f = rms_factor_regs<kRmsPer>(xv, sv, p, red128, red32);
+    int16_t* o = out + (size_t)blockIdx.x * ldo;
+#pragma unroll
+    for (int t = 0; t < kRmsPer; ++t) {
+        const int i = threadIdx.x + t * kRmsThreads;
+        if (i < n) o[i] = rms_out(xv[t], sv[t], gv[t], gsv[t], f, out_frac);
+    }
+}
+
 hipError_t rmsnorm(const int16_t* x, int M, int ldx, const uint8_t* xs, const int8_t* g, const uint8_t* gs, int n,
                    const int16_t* lut, int lut_len, uint8_t lut_input_shift, uint8_t lut_output_frac,
                    int64_t inv_n_q20, uint8_t out_frac, int16_t* out, int ldo, hipStream_t st) {
     RmsParams p{lut, lut_len, lut_input_shift, lut_output_frac, inv_n_q20};
-    rmsnorm_kernel<<<M, kBlock, 0, st>>>(x, ldx, xs, g, gs, n, p, out_frac, out, ldo);
+    if (n <= kRmsThreads * kRmsPer)
+        rmsnorm_fast_kernel<<<M, kRmsThreads, 0, st>>>(x, ldx, xs, g, gs, n, p, out_frac, out, ldo);
+    else
+        rmsnorm_kernel<<<M, kBlock, 0, st>>>(x, ldx, xs, g, gs, n, p, out_frac, out, ldo);
     return hipGetLastError();
 }
 

@@ -29,6 +29,7 @@
 //   Wo [H x nq], Wd [H x I], LM head [V x H] (int8 tied embedding or int16).
 #include "abi_internal.h"
 #include "gemv.h"
+#include "gemv_stream.h"
 #include "ops.h"
 #include "../../include/myl_synth.h"
 
@@ -41,8 +42,8 @@ using namespace myl;
 
 namespace {
 
-constexpr int kChunk = 256;          // attention positions per block
-constexpr int kChunkLog = 8;
+constexpr int kChunk = 64;           // attention positions per block
+constexpr int kChunkLog = 6;
 constexpr int kMaxGroup = 8;         // query heads per KV head handled by one block
 
 struct DecodeState {
@@ -84,17 +85,235 @@ __global__ void gen_w16_kernel(int16_t* __restrict__ dst, int row0, int K, uint6
 }
 
 // ---------------------------------------------------------------------------
+// RMSNorm fused across kernels (rmsnorm.rs:61-161)
+//
+// The producer of a residual-stream vector (embed, o_proj, down_proj) adds the
+// exact terms x_i^2 << 2(ref - x_shift_i) of the next RMSNorm into a
+// NormAcc: each 128-bit term is split into 42-bit limbs summed in u64 (no
+// limb sum can overflow for n < 2^10 * 2^10), spread over 64 slots to keep
+// atomic contention low.  The consumer GEMV rebuilds the 128-bit sum modulo
+// 2^128 (the reference's wrapping i128 additions), derives the LUT factor and
+// normalises the vector while staging it.
+// ---------------------------------------------------------------------------
+
+constexpr int kNormSlots = 64;
+constexpr uint64_t kLimbMask = (1ull << 42) - 1;
+struct NormAcc { unsigned long long v[kNormSlots][3]; };
+
+__device__ inline void add_sq_limbs(int16_t x, uint8_t xs, uint8_t ref, uint64_t (&l)[3]) {
+    const uint32_t align = 2u * (uint32_t)(uint8_t)(ref - xs);
+    const myl_u128 t = (myl_u128)shl128((myl_i128)((int64_t)x * (int64_t)x), align);
+    l[0] += (uint64_t)t & kLimbMask;
+    l[1] += (uint64_t)(t >> 42) & kLimbMask;
+    l[2] += (uint64_t)(t >> 84);
+}
+
+__device__ inline uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, off, 64);
+        const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), off, 64);
+        v += ((uint64_t)hi << 32) | lo;
+    }
+    return v;
+}
+
+// Block-level sum of per-thread limbs; thread 0 gets the totals.
+__device__ inline void block_sum_limbs(uint64_t (&l)[3], uint64_t* red /* [16][3] */) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) l[j] = wave_sum_u64(l[j]);
+    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0)
+        for (int j = 0; j < 3; ++j) red[w * 3 + j] = l[j];
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int j = 0; j < 3; ++j) {
+            uint64_t s = 0;
+            for (int i = 0; i < nw; ++i) s += red[i * 3 + j];
+            l[j] = s;
+        }
+}
+
+__device__ inline uint32_t bitlen128(myl_u128 v) {
+    const uint64_t hi = (uint64_t)(v >> 64), lo = (uint64_t)v;
+    return hi ? 128u - (uint32_t)__builtin_clzll(hi) : (lo ? 64u - (uint32_t)__builtin_clzll(lo) : 0u);
+}
+
+__device__ inline RmsFactor rms_factor_from_acc(myl_i128 acc, uint8_t ref, const RmsParams& p) {
+    RmsFactor f;
+    f.ref_shift = ref;
+    f.zero = acc == 0;
+    f.lut_val = 0;
+    f.norm_frac = 0;
+    if (!f.zero) {
+        const myl_i128 m = shr128((myl_i128)((myl_u128)acc * (myl_u128)(myl_i128)p.inv_n_q20), 20);
+        const myl_i128 max_idx = (myl_i128)(p.lut_len - 1);
+        // rmsnorm.rs:121-123 searches the smallest even q with m >> q <= max_idx.
+        // Every q below bitlen(m) - bitlen(max_idx) fails the test, so the
+        // search may start just under that bound (same q, few iterations).
+        uint32_t q = 0;
+        if (m > 0) {
+            const uint32_t bm = bitlen128((myl_u128)m), bi = bitlen128((myl_u128)max_idx);
+            if (bm > bi + 2) q = (bm - bi - 2) & ~1u;
+        }
+        while (shr128(m, q) > max_idx) q += 2;
+        myl_i128 idx = rshift_round128(m, q);
+        if (idx > max_idx) idx = max_idx;
+        if (idx < 0) idx = 0;
+        f.lut_val = (int64_t)p.lut[(int)idx];
+        f.norm_frac = (uint32_t)p.lut_output_frac + (uint32_t)p.lut_input_shift / 2u + q / 2u;
+    }
+    return f;
+}
+
+// Writes the norm sum of an n-vector computed by one block into slot 0 of acc
+// (the other slots are cleared): used where one block sees the whole vector.
+__device__ inline void block_seed_norm(const int16_t* x, const uint8_t* xs, uint8_t ref, int n, NormAcc* acc) {
+    __shared__ uint64_t red[16 * 3];
+    uint64_t l[3] = {0, 0, 0};
+    for (int i = threadIdx.x; i < n; i += blockDim.x) add_sq_limbs(x[i], xs[i], ref, l);
+    block_sum_limbs(l, red);
+    for (int i = threadIdx.x; i < kNormSlots * 3; i += blockDim.x) (&acc->v[0][0])[i] = 0;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int j = 0; j < 3; ++j) acc->v[0][j] = l[j];
+}
+
+__global__ __launch_bounds__(1024) void norm_seed_kernel(const int16_t* __restrict__ x, const uint8_t* __restrict__ xs,
+                                                         uint8_t ref, int n, NormAcc* acc) {
+    block_seed_norm(x, xs, ref, n, acc);
+}
+
+// int16 values -> the two signed byte planes (hi = v >> 8, lo' = (v & 255) - 128).
+__device__ inline void put_planes_i8(const int16_t (&v)[8], int8_t* hi, int8_t* lo) {
+    uint32_t h[2], l[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint32_t d0 = (uint32_t)(uint16_t)v[4 * t] | ((uint32_t)(uint16_t)v[4 * t + 1] << 16);
+        const uint32_t d1 = (uint32_t)(uint16_t)v[4 * t + 2] | ((uint32_t)(uint16_t)v[4 * t + 3] << 16);
+        h[t] = ((d0 >> 8) & 0xFFu) | ((d0 >> 16) & 0xFF00u) | ((d1 << 8) & 0xFF0000u) | (d1 & 0xFF000000u);
+        l[t] = ((d0 & 0xFFu) | ((d0 >> 8) & 0xFF00u) | ((d1 << 16) & 0xFF0000u) | ((d1 << 8) & 0xFF000000u)) ^ 0x80808080u;
+    }
+    *reinterpret_cast<uint2*>(hi) = make_uint2(h[0], h[1]);
+    *reinterpret_cast<uint2*>(lo) = make_uint2(l[0], l[1]);
+}
+
+// int16 values -> int16 planes (hi = v >> 8, lo = v & 255) for int16 weights.
+__device__ inline void put_planes_i16(const int16_t (&v)[8], int16_t* hi, int16_t* lo) {
+    int16_t h[8], l[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) { h[t] = (int16_t)(v[t] >> 8); l[t] = (int16_t)(v[t] & 255); }
+    *reinterpret_cast<uint4*>(hi) = *reinterpret_cast<const uint4*>(h);
+    *reinterpret_cast<uint4*>(lo) = *reinterpret_cast<const uint4*>(l);
+}
+
+// Staging source: RMSNorm of x (x_shifts xs, gamma g/gs) from a NormAcc.
+struct SrcNorm {
+    const int16_t* x;
+    const uint8_t* xs;
+    const int8_t* g;
+    const uint8_t* gs;
+    RmsParams p;
+    uint8_t ref, out_frac;
+    const NormAcc* acc;
+
+    __device__ inline RmsFactor factor() const {
+        __shared__ RmsFactor sf;
+        if (threadIdx.x < 64) {
+            uint64_t l[3];
+#pragma unroll
+            for (int j = 0; j < 3; ++j) l[j] = wave_sum_u64(acc->v[threadIdx.x][j]);
+            if (threadIdx.x == 0) {
+                const myl_i128 a = (myl_i128)((myl_u128)l[0] + ((myl_u128)l[1] << 42) + ((myl_u128)l[2] << 84));
+                sf = rms_factor_from_acc(a, ref, p);
+            }
+        }
+        __syncthreads();
+        return sf;
+    }
+    __device__ inline void values8(const RmsFactor& f, int k0, int K, int16_t (&v)[8]) const {
+        if (k0 >= K) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) v[t] = 0;
+            return;
+        }
+        const uint4 xv = *reinterpret_cast<const uint4*>(x + k0);
+        const uint2 sv = *reinterpret_cast<const uint2*>(xs + k0);
+        const uint2 gv = *reinterpret_cast<const uint2*>(g + k0);
+        const uint2 gsv = *reinterpret_cast<const uint2*>(gs + k0);
+        const int16_t* xe = reinterpret_cast<const int16_t*>(&xv);
+        const uint8_t* se = reinterpret_cast<const uint8_t*>(&sv);
+        const int8_t* ge = reinterpret_cast<const int8_t*>(&gv);
+        const uint8_t* gse = reinterpret_cast<const uint8_t*>(&gsv);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[t] = rms_out(xe[t], se[t], ge[t], gse[t], f, out_frac);
+    }
+    __device__ inline void stage_i8(int8_t* hi, int8_t* lo, int K, int kpad) const {
+        const RmsFactor f = factor();
+        for (int i = threadIdx.x; i < (kpad >> 3); i += blockDim.x) {
+            int16_t v[8];
+            values8(f, i * 8, K, v);
+            put_planes_i8(v, hi + i * 8, lo + i * 8);
+        }
+    }
+    __device__ inline void stage_i16(int16_t* hi, int16_t* lo, int K, int kpad) const {
+        const RmsFactor f = factor();
+        for (int i = threadIdx.x; i < (kpad >> 3); i += blockDim.x) {
+            int16_t v[8];
+            values8(f, i * 8, K, v);
+            put_planes_i16(v, hi + i * 8, lo + i * 8);
+        }
+    }
+};
+
+// Staging source: attention output from the exact P.V accumulator
+// (attention.rs:84-86 then model.rs:563-567).
+struct SrcAttn {
+    const unsigned long long* acc;
+    uint8_t v_frac, out_frac;
+    __device__ inline void stage_i8(int8_t* hi, int8_t* lo, int K, int kpad) const {
+        for (int i = threadIdx.x; i < (kpad >> 3); i += blockDim.x) {
+            int16_t v[8];
+            const int k0 = i * 8;
+            if (k0 < K) {
+                const uint4* a4 = reinterpret_cast<const uint4*>(acc + k0);
+                uint64_t a[8];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint4 q = a4[t];
+                    a[2 * t] = ((uint64_t)q.y << 32) | q.x;
+                    a[2 * t + 1] = ((uint64_t)q.w << 32) | q.z;
+                }
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const int16_t r = clamp_i16_i64(rshift_round64((int64_t)a[t], MYL_TV_PROB_FRAC_BITS));
+                    v[t] = clamp_i16(rescale32((int32_t)r, v_frac, out_frac));
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) v[t] = 0;
+            }
+            put_planes_i8(v, hi + i * 8, lo + i * 8);
+        }
+    }
+};
+
+// ---------------------------------------------------------------------------
 // embedding + step state (model.rs:241-248, 323-331)
 // ---------------------------------------------------------------------------
 
 // mode 0: token/pos from the arguments; mode 1: greedy continuation (token =
-// argmax of the previous step, pos + 1).  Resets the argmax key for this step.
+// argmax of the previous step, pos + 1).  Resets the argmax key for this step
+// and seeds the first layer's input-norm accumulator.
 __global__ __launch_bounds__(1024) void embed_kernel(DecodeState* st, int mode, int token_arg, int pos_arg,
                                                      uint32_t rope_rows, int vocab, const int8_t* __restrict__ E,
                                                      const uint8_t* __restrict__ emb_shifts,
-                                                     const uint8_t* __restrict__ res_frac0, int H,
-                                                     int64_t* __restrict__ tokens_out, int16_t* __restrict__ hidden) {
+                                                     const uint8_t* __restrict__ res_frac0, uint8_t ref0, int H,
+                                                     int64_t* __restrict__ tokens_out, int16_t* __restrict__ hidden,
+                                                     NormAcc* norm_acc) {
     __shared__ int32_t s_tok;
+    __shared__ uint64_t red[16 * 3];
     if (threadIdx.x == 0) {
         int32_t tok, pos;
         if (mode == 0) {
@@ -118,13 +337,24 @@ __global__ __launch_bounds__(1024) void embed_kernel(DecodeState* st, int mode, 
     const int tok = s_tok;
     const int8_t* row = E + (size_t)tok * H;
     const uint8_t sh = emb_shifts[tok];
-    for (int i = threadIdx.x; i < H; i += blockDim.x)
-        hidden[i] = clamp_i16(rescale32((int32_t)row[i], sh, res_frac0[i]));
+    uint64_t l[3] = {0, 0, 0};
+    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+        const int16_t v = clamp_i16(rescale32((int32_t)row[i], sh, res_frac0[i]));
+        hidden[i] = v;
+        add_sq_limbs(v, res_frac0[i], ref0, l);
+    }
+    block_sum_limbs(l, red);
+    for (int i = threadIdx.x; i < kNormSlots * 3; i += blockDim.x) (&norm_acc->v[0][0])[i] = 0;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int j = 0; j < 3; ++j) norm_acc->v[0][j] = l[j];
 }
 
 // ---------------------------------------------------------------------------
-// fused GEMV epilogues
+// fused GEMV epilogues (streaming interface: begin / group / zero_duty / finish)
 // ---------------------------------------------------------------------------
+
+struct NoState {};
 
 // q/k/v projection rows (pair-ordered) -> bias -> RoPE -> q buffer / KV cache.
 struct EpiQKV {
@@ -139,11 +369,13 @@ struct EpiQKV {
     int16_t* q_out;           // [nq]
     int16_t* kc;              // layer base [kv_heads][max_pos][hd]
     int16_t* vc;
-    EpiQKV offset_m(int) const { return *this; }
-    __device__ inline void one(int, int, int64_t) const {}
-    template <int R, int MT>
-    __device__ inline void apply(int row0, int N, int M, int lane, const int64_t (&tot)[R][MT]) const {
-        static_assert(R == 2, "the RoPE pair needs two rows per wave");
+    using State = NoState;
+    __device__ inline void begin(State&) const {}
+    __device__ inline void zero_duty() const {}
+    __device__ inline void finish(State&) const {}
+    template <int R>
+    __device__ inline void group(State&, int row0, int N, int lane, const int64_t (&tot)[R][1]) const {
+        static_assert(R == 2, "the RoPE pair needs two rows per group");
         if (lane != 0 || row0 >= N) return;
         const int seg = row0 < nq ? 0 : (row0 < nq + nkv ? 1 : 2);
         const int e = row0 - (seg == 0 ? 0 : (seg == 1 ? nq : nq + nkv));
@@ -178,6 +410,8 @@ struct EpiQKV {
 // o_proj / down_proj + residual add (model.rs:576-593, 612-671):
 //   o = clamp(rescale(acc, w_shift + act, acc_frac)); h = rescale(res_in, res_frac, acc_frac)
 //   out = clamp(rescale(h + o, acc_frac, out_frac))
+// plus the next RMSNorm's sum of squares of `out` into sum_out, and clearing
+// of a NormAcc whose consumer has already run.
 struct EpiResid {
     const uint8_t* shifts;
     uint8_t act_frac;
@@ -186,32 +420,59 @@ struct EpiResid {
     const uint8_t* out_frac;
     const int16_t* res_in;
     int16_t* out;
-    EpiResid offset_m(int) const { return *this; }
-    __device__ inline void one(int r, int, int64_t acc) const {
-        const uint8_t af = acc_frac[r];
-        const int16_t o = clamp_i16_i64(rescale64(acc, (uint8_t)(shifts[r] + act_frac), af));
-        const int64_t h = rescale64((int64_t)res_in[r], res_frac[r], af);
-        out[r] = clamp_i16_i64(rescale64(wadd64(h, (int64_t)o), af, out_frac[r]));
+    NormAcc* sum_out;
+    uint8_t ref_out;           // max over out_frac
+    NormAcc* clear;            // may be null
+    struct State { uint64_t l[3]; };
+    __device__ inline void begin(State& s) const { s.l[0] = s.l[1] = s.l[2] = 0; }
+    __device__ inline void zero_duty() const {
+        if (clear && blockIdx.x == 0)
+            for (int i = threadIdx.x; i < kNormSlots * 3; i += blockDim.x) (&clear->v[0][0])[i] = 0;
     }
-    template <int R, int MT>
-    __device__ inline void apply(int row0, int N, int M, int lane, const int64_t (&tot)[R][MT]) const {
+    template <int R>
+    __device__ inline void group(State& s, int row0, int N, int lane, const int64_t (&tot)[R][1]) const {
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (lane == r && row0 + r < N) one(row0 + r, 0, tot[r][0]);
+        for (int r = 0; r < R; ++r) {
+            if (lane == r && row0 + r < N) {
+                const int i = row0 + r;
+                const uint8_t af = acc_frac[i];
+                const int16_t o = clamp_i16_i64(rescale64(tot[r][0], (uint8_t)(shifts[i] + act_frac), af));
+                const int64_t h = rescale64((int64_t)res_in[i], res_frac[i], af);
+                const uint8_t of = out_frac[i];
+                const int16_t v = clamp_i16_i64(rescale64(wadd64(h, (int64_t)o), af, of));
+                out[i] = v;
+                add_sq_limbs(v, of, ref_out, s.l);
+            }
+        }
+    }
+    __device__ inline void finish(State& s) const {
+        __shared__ uint64_t red[16 * 3];
+        block_sum_limbs(s.l, red);
+        if (threadIdx.x == 0) {
+            const int slot = blockIdx.x & (kNormSlots - 1);
+            for (int j = 0; j < 3; ++j)
+                if (s.l[j]) atomicAdd(&sum_out->v[slot][j], (unsigned long long)s.l[j]);
+        }
     }
 };
 
-// gate row 2r and up row 2r+1 -> h[r] (mlp.rs:46-65).
+// gate row 2r and up row 2r+1 -> h[r] (mlp.rs:46-65); clears the attention
+// accumulator (its reader, o_proj, has finished).
 struct EpiSilu {
     const uint8_t* shifts;    // interleaved like the rows
     uint8_t act_frac, gate_frac, up_frac, down_in_frac;
     const int16_t* silu; uint32_t silu_len;
     int16_t* h;
-    EpiSilu offset_m(int) const { return *this; }
-    __device__ inline void one(int, int, int64_t) const {}
-    template <int R, int MT>
-    __device__ inline void apply(int row0, int N, int M, int lane, const int64_t (&tot)[R][MT]) const {
-        static_assert(R == 2, "gate and up share a wave");
+    unsigned long long* clear; int clear_n;
+    using State = NoState;
+    __device__ inline void begin(State&) const {}
+    __device__ inline void zero_duty() const {
+        for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < clear_n; i += gridDim.x * blockDim.x) clear[i] = 0;
+    }
+    __device__ inline void finish(State&) const {}
+    template <int R>
+    __device__ inline void group(State&, int row0, int N, int lane, const int64_t (&tot)[R][1]) const {
+        static_assert(R == 2, "gate and up share a group");
         if (lane != 0 || row0 >= N) return;
         const int16_t g = clamp_i16_i64(rescale64(tot[0][0], (uint8_t)(shifts[row0] + act_frac), gate_frac));
         const int16_t u = clamp_i16_i64(rescale64(tot[1][0], (uint8_t)(shifts[row0 + 1] + act_frac), up_frac));
@@ -222,20 +483,20 @@ struct EpiSilu {
     }
 };
 
-// LM head logits (model.rs:284-308) + first-maximum argmax (sampling.rs:8-18).
+// LM head logits (model.rs:284-308) + first-maximum argmax (sampling.rs:8-18):
+// per group the best key of its rows goes to one atomic, issued only when it
+// beats the current key.
 struct EpiHead {
     const uint8_t* shifts;
     uint8_t norm_frac;
     int32_t* logits;
     DecodeState* st;
-    EpiHead offset_m(int) const { return *this; }
-    __device__ inline void one(int r, int, int64_t acc) const {
-        const int32_t v = clamp_i32_i64(rescale64(acc, (uint8_t)(shifts[r] + norm_frac), MYL_TV_LOGIT_FRAC_BITS));
-        logits[r] = v;
-        atomicMax((unsigned long long*)&st->argmax_key, (unsigned long long)argmax_key(v, (uint32_t)r));
-    }
-    template <int R, int MT>
-    __device__ inline void apply(int row0, int N, int M, int lane, const int64_t (&tot)[R][MT]) const {
+    using State = NoState;
+    __device__ inline void begin(State&) const {}
+    __device__ inline void zero_duty() const {}
+    __device__ inline void finish(State&) const {}
+    template <int R>
+    __device__ inline void group(State&, int row0, int N, int lane, const int64_t (&tot)[R][1]) const {
         uint64_t best = 0;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -247,23 +508,43 @@ struct EpiHead {
                 best = k > best ? k : best;
             }
         }
-        if (lane == 0 && best) atomicMax((unsigned long long*)&st->argmax_key, (unsigned long long)best);
+        if (lane == 0 && best) {
+            const uint64_t cur = __hip_atomic_load(&st->argmax_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (best > cur) atomicMax((unsigned long long*)&st->argmax_key, (unsigned long long)best);
+        }
     }
 };
 
-template <int R, class Epi>
-hipError_t gemv_model(const int16_t* x, const int8_t* W, int N, int K, const Epi& e, hipStream_t s) {
-    const int kc = std::min(((K + 15) / 16) * 16, kGemvLdsBytes / 2);
-    const int blocks = (N + R * kGemvWaves - 1) / (R * kGemvWaves);
-    gemv_i8_kernel<R, 1, Epi><<<blocks, kGemvThreads, (size_t)2 * kc, s>>>(x, 1, K, W, N, K, kc, e);
+// Persistent grid: as many blocks as fit on the device, shrunk so that every
+// wave gets the same number of row groups (no tail of half-filled rounds).
+template <class Kern>
+int stream_grid(Kern kern, int waves_per_block, size_t lds, int ngroups, int cus) {
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, waves_per_block * 64, lds) != hipSuccess || occ < 1)
+        occ = 1;
+    const int waves_cap = occ * cus * waves_per_block;
+    const int per_wave = (ngroups + waves_cap - 1) / waves_cap;
+    const int waves = (ngroups + per_wave - 1) / per_wave;
+    return (waves + waves_per_block - 1) / waves_per_block;
+}
+
+template <int R, int U, int WAVES, class Src, class Epi>
+hipError_t stream_i8(const Src& src, const int8_t* W, int N, int K, const Epi& e, hipStream_t s, int cus) {
+    if ((uint64_t)N * (uint64_t)K > 0xFFFFFF00ull) return hipErrorInvalidValue;  // one buffer descriptor
+    const size_t lds = (size_t)2 * (((K + 15) >> 4) << 4);
+    auto kern = gemv_i8_stream<R, U, WAVES, Src, Epi>;
+    const int grid = stream_grid(kern, WAVES, lds, (N + R - 1) / R, cus);
+    kern<<<grid, WAVES * 64, lds, s>>>(src, W, N, K, e);
     return hipGetLastError();
 }
 
-template <int R, class Epi>
-hipError_t gemv_model16(const int16_t* x, const int16_t* W, int N, int K, const Epi& e, hipStream_t s) {
-    const int kc = std::min(((K + 7) / 8) * 8, kGemvLdsBytes / 4);
-    const int blocks = (N + R * kGemvWaves - 1) / (R * kGemvWaves);
-    gemv_i16_kernel<R, 1, Epi><<<blocks, kGemvThreads, (size_t)4 * kc, s>>>(x, 1, K, W, N, K, kc, e);
+template <int R, int U, int WAVES, class Src, class Epi>
+hipError_t stream_i16(const Src& src, const int16_t* W, int N, int K, const Epi& e, hipStream_t s, int cus) {
+    if (2ull * (uint64_t)N * (uint64_t)K > 0xFFFFFF00ull) return hipErrorInvalidValue;  // one buffer descriptor
+    const size_t lds = (size_t)4 * (((K + 7) >> 3) << 3);
+    auto kern = gemv_i16_stream<R, U, WAVES, Src, Epi>;
+    const int grid = stream_grid(kern, WAVES, lds, (N + R - 1) / R, cus);
+    kern<<<grid, WAVES * 64, lds, s>>>(src, W, N, K, e);
     return hipGetLastError();
 }
 
@@ -271,21 +552,34 @@ hipError_t gemv_model16(const int16_t* x, const int16_t* W, int N, int K, const 
 // decode attention over the KV cache (attention.rs:42-90), GQA (model.rs:508-511)
 // ---------------------------------------------------------------------------
 
-// scores[h][j] for the G query heads of KV head g, positions j of one chunk.
-// LPP = HD/8 lanes read one 16-byte slice each of a K row (coalesced rows).
+// scores[h][j] for the G query heads of KV head g, positions j of one chunk of
+// kChunk positions.  LPP = HD/8 lanes read one 16-byte slice each of a K row
+// (a wave reads whole rows: coalesced); every K load of the wave is issued
+// before the first dot product.  q . k is exact: q = 256*hi + lo with
+// v_dot2_i32_i16 on (k, hi) and (k, lo) (|partials| < 2^31 per 16-lane group).
 template <int HD>
 __global__ __launch_bounds__(256) void attn_scores_kernel(const DecodeState* __restrict__ st,
                                                          const int16_t* __restrict__ q, const int16_t* __restrict__ kc,
                                                          int max_pos, int G, int64_t score_mult, uint8_t score_shift,
                                                          int32_t* __restrict__ scores) {
     constexpr int LPP = HD / 8;
-    constexpr int PPW = 64 / LPP;
+    constexpr int PPW = 64 / LPP;                 // positions per wave per step
+    constexpr int STEPS = kChunk / 4 / PPW;       // steps per wave
     const int L = st->pos + 1;
     const int g = blockIdx.y;
     const int base = blockIdx.x * kChunk;
     if (base >= L) return;
     __shared__ __align__(16) int16_t qhi[kMaxGroup][HD];
     __shared__ __align__(16) int16_t qlo[kMaxGroup][HD];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LPP, slot = lane / LPP;
+    const int16_t* kg = kc + (size_t)g * max_pos * HD;
+    uint4 kv[STEPS];
+#pragma unroll
+    for (int it = 0; it < STEPS; ++it) {
+        const int j = base + wave * (kChunk / 4) + it * PPW + slot;
+        kv[it] = j < L ? *reinterpret_cast<const uint4*>(kg + (size_t)j * HD + sub * 8) : make_uint4(0, 0, 0, 0);
+    }
     for (int i = threadIdx.x; i < G * HD; i += blockDim.x) {
         const int h = i / HD, d = i - h * HD;  // HD is a compile-time power of two
         const int16_t v = q[(size_t)(g * G + h) * HD + d];
@@ -293,26 +587,22 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(const DecodeState* __r
         qlo[h][d] = (int16_t)(v & 255);
     }
     __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane % LPP, slot = lane / LPP;
-    const int16_t* kg = kc + (size_t)g * max_pos * HD;
     typedef short __attribute__((ext_vector_type(2))) s2;
-    for (int it = 0; it < kChunk / 4 / PPW; ++it) {
-        const int j = base + wave * (kChunk / 4) + it * PPW + slot;
-        uint4 kv = make_uint4(0, 0, 0, 0);
-        if (j < L) kv = *reinterpret_cast<const uint4*>(kg + (size_t)j * HD + sub * 8);
-        for (int h = 0; h < G; ++h) {
-            const uint4 qh = *reinterpret_cast<const uint4*>(&qhi[h][sub * 8]);
-            const uint4 ql = *reinterpret_cast<const uint4*>(&qlo[h][sub * 8]);
+    for (int h = 0; h < G; ++h) {
+        const uint4 qh = *reinterpret_cast<const uint4*>(&qhi[h][sub * 8]);
+        const uint4 ql = *reinterpret_cast<const uint4*>(&qlo[h][sub * 8]);
+#pragma unroll
+        for (int it = 0; it < STEPS; ++it) {
+            const int j = base + wave * (kChunk / 4) + it * PPW + slot;
             int32_t ahi = 0, alo = 0;
-            ahi = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv.x), __builtin_bit_cast(s2, qh.x), ahi, false);
-            ahi = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv.y), __builtin_bit_cast(s2, qh.y), ahi, false);
-            ahi = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv.z), __builtin_bit_cast(s2, qh.z), ahi, false);
-            ahi = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv.w), __builtin_bit_cast(s2, qh.w), ahi, false);
-            alo = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv.x), __builtin_bit_cast(s2, ql.x), alo, false);
-            alo = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv.y), __builtin_bit_cast(s2, ql.y), alo, false);
-            alo = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv.z), __builtin_bit_cast(s2, ql.z), alo, false);
-            alo = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv.w), __builtin_bit_cast(s2, ql.w), alo, false);
+            ahi = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv[it].x), __builtin_bit_cast(s2, qh.x), ahi, false);
+            ahi = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv[it].y), __builtin_bit_cast(s2, qh.y), ahi, false);
+            ahi = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv[it].z), __builtin_bit_cast(s2, qh.z), ahi, false);
+            ahi = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv[it].w), __builtin_bit_cast(s2, qh.w), ahi, false);
+            alo = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv[it].x), __builtin_bit_cast(s2, ql.x), alo, false);
+            alo = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv[it].y), __builtin_bit_cast(s2, ql.y), alo, false);
+            alo = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv[it].z), __builtin_bit_cast(s2, ql.z), alo, false);
+            alo = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv[it].w), __builtin_bit_cast(s2, ql.w), alo, false);
 #pragma unroll
             for (int off = LPP / 2; off > 0; off >>= 1) {
                 ahi += __shfl_xor(ahi, off, 64);
@@ -327,26 +617,46 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(const DecodeState* __r
     }
 }
 
-// Per query head: max score, sum of exp-LUT values, reciprocal of the divisor.
-__global__ __launch_bounds__(256) void attn_stats_kernel(const DecodeState* __restrict__ st,
-                                                        const int32_t* __restrict__ scores, int max_pos,
-                                                        const int16_t* __restrict__ lut, uint32_t lut_len,
-                                                        uint8_t lut_shift, AttnStat* __restrict__ stats) {
-    __shared__ int32_t red32[4];
-    __shared__ uint32_t redu[4];
+// Per query head: max score, sum of exp-LUT values (wrapping i32, like the
+// reference's i32 sum) and the reciprocal of the divisor.  1024 threads, each
+// holding up to kStatPer scores in registers across both reductions.
+constexpr int kStatThreads = 1024;
+constexpr int kStatPer = 4;
+__global__ __launch_bounds__(kStatThreads) void attn_stats_kernel(const DecodeState* __restrict__ st,
+                                                                 const int32_t* __restrict__ scores, int max_pos,
+                                                                 const int16_t* __restrict__ lut, uint32_t lut_len,
+                                                                 uint8_t lut_shift, AttnStat* __restrict__ stats) {
+    __shared__ int32_t red32[kStatThreads / 64];
+    __shared__ uint32_t redu[kStatThreads / 64];
     const int L = st->pos + 1;
     const int32_t* z = scores + (size_t)blockIdx.x * max_pos;
     const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
     const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
     int32_t mx = INT32_MIN;
-    for (int j = threadIdx.x; j < L; j += blockDim.x) mx = max(mx, z[j]);
-    const int32_t m = block_max_i32(mx, red32);
     uint32_t s = 0;
-    for (int j = threadIdx.x; j < L; j += blockDim.x) s += (uint32_t)exp_lookup(sat_sub32(m, z[j]), lut, lut_len, lut_shift, lut_one);
+    if (L <= kStatThreads * kStatPer) {
+        int32_t zz[kStatPer];
+#pragma unroll
+        for (int t = 0; t < kStatPer; ++t) {
+            const int j = threadIdx.x + t * kStatThreads;
+            zz[t] = j < L ? z[j] : INT32_MIN;
+        }
+#pragma unroll
+        for (int t = 0; t < kStatPer; ++t) mx = max(mx, zz[t]);
+        mx = block_max_i32(mx, red32);
+#pragma unroll
+        for (int t = 0; t < kStatPer; ++t)
+            if (threadIdx.x + t * kStatThreads < L) s += (uint32_t)exp_lookup(sat_sub32(mx, zz[t]), lut, lut_len, lut_shift, lut_one);
+    } else {
+        for (int j = threadIdx.x; j < L; j += blockDim.x) mx = max(mx, z[j]);
+        mx = block_max_i32(mx, red32);
+        for (int j = threadIdx.x; j < L; j += blockDim.x)
+            s += (uint32_t)exp_lookup(sat_sub32(mx, z[j]), lut, lut_len, lut_shift, lut_one);
+    }
     const int32_t S = (int32_t)block_sum_u32(s, redu);
     if (threadIdx.x == 0) {
         AttnStat a;
-        a.m = m;
+        a.m = mx;
         a.S = S;
         a.base = 0;
         a.rem = 0;
@@ -363,81 +673,70 @@ __global__ __launch_bounds__(256) void attn_stats_kernel(const DecodeState* __re
     }
 }
 
-// Probabilities of one chunk and their partial products with V, for the G
-// heads of KV head g: partial[chunk][h][d] (i64, exact).
+// Probabilities of one chunk and their products with V, for the G heads of KV
+// head g, added exactly (64-bit integer atomics: any order gives the same sum)
+// into acc[h * HD + d].
 template <int HD>
 __global__ __launch_bounds__(256) void attn_pv_kernel(const DecodeState* __restrict__ st,
                                                      const int32_t* __restrict__ scores, const AttnStat* __restrict__ stats,
                                                      const int16_t* __restrict__ vc, int max_pos, int G,
                                                      const int16_t* __restrict__ lut, uint32_t lut_len, uint8_t lut_shift,
-                                                     int64_t* __restrict__ partial, int nq) {
+                                                     unsigned long long* __restrict__ acc) {
     constexpr int TPR = HD / 2;           // threads per V row (one dim pair each)
     constexpr int STREAMS = 256 / TPR;    // position streams per block
+    constexpr int PER = kChunk / STREAMS; // positions per stream
     const int L = st->pos + 1;
     const int g = blockIdx.y;
     const int base = blockIdx.x * kChunk;
     if (base >= L) return;
     const int n = min(kChunk, L - base);
     __shared__ int32_t p[kMaxGroup][kChunk];
-    __shared__ int64_t red[STREAMS][2 * TPR];
+    __shared__ int64_t red[STREAMS][HD];
+    const int dp = threadIdx.x % TPR, stream = threadIdx.x / TPR;
+    const int16_t* vg = vc + (size_t)g * max_pos * HD;
+    uint32_t vv[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int t = stream + i * STREAMS;
+        vv[i] = t < n ? *reinterpret_cast<const uint32_t*>(vg + (size_t)(base + t) * HD + 2 * dp) : 0u;
+    }
     const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
     const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
-    for (int h = 0; h < G; ++h) {
-        const AttnStat a = stats[g * G + h];
-        const int32_t* z = scores + (size_t)(g * G + h) * max_pos + base;
-        for (int t = threadIdx.x; t < n; t += blockDim.x) {
-            int32_t pv;
+    for (int i = threadIdx.x; i < G * kChunk; i += blockDim.x) {
+        const int h = i >> kChunkLog, t = i & (kChunk - 1);
+        int32_t pv = 0;
+        if (t < n) {
+            const AttnStat a = stats[g * G + h];
             if (a.S == 0) {
                 pv = a.base + (((uint64_t)(base + t) < (uint64_t)(int64_t)a.rem) ? 1 : 0);
             } else {
-                const int32_t e = exp_lookup(sat_sub32(a.m, z[t]), lut, lut_len, lut_shift, lut_one);
+                const int32_t z = scores[(size_t)(g * G + h) * max_pos + base + t];
+                const int32_t e = exp_lookup(sat_sub32(a.m, z), lut, lut_len, lut_shift, lut_one);
                 pv = softmax_div_round(wmul32(e, one), a.S, a.recip);
             }
-            p[h][t] = pv;
         }
+        p[h][t] = pv;
     }
     __syncthreads();
-    const int dp = threadIdx.x % TPR, stream = threadIdx.x / TPR;
-    int64_t acc0[kMaxGroup], acc1[kMaxGroup];
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h) { acc0[h] = 0; acc1[h] = 0; }
-    const int16_t* vg = vc + (size_t)g * max_pos * HD;
-    for (int t = stream; t < n; t += STREAMS) {
-        const uint32_t pair = *reinterpret_cast<const uint32_t*>(vg + (size_t)(base + t) * HD + 2 * dp);
-        const int64_t v0 = (int16_t)(pair & 0xFFFFu), v1 = (int16_t)(pair >> 16);
-#pragma unroll
-        for (int h = 0; h < kMaxGroup; ++h) {
-            if (h < G) {
-                const int64_t pv = p[h][t];
-                acc0[h] = wadd64(acc0[h], pv * v0);
-                acc1[h] = wadd64(acc1[h], pv * v1);
-            }
-        }
-    }
     for (int h = 0; h < G; ++h) {
-        __syncthreads();
-        red[stream][2 * dp] = acc0[h];
-        red[stream][2 * dp + 1] = acc1[h];
+        int64_t a0 = 0, a1 = 0;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int64_t pv = p[h][stream + i * STREAMS];
+            a0 = wadd64(a0, pv * (int64_t)(int16_t)(vv[i] & 0xFFFFu));
+            a1 = wadd64(a1, pv * (int64_t)(int16_t)(vv[i] >> 16));
+        }
+        red[stream][2 * dp] = a0;
+        red[stream][2 * dp + 1] = a1;
         __syncthreads();
         if (threadIdx.x < HD) {
-            int64_t s = 0;
-            for (int k = 0; k < STREAMS; ++k) s = wadd64(s, red[k][threadIdx.x]);
-            partial[(size_t)blockIdx.x * nq + (size_t)(g * G + h) * HD + threadIdx.x] = s;
+            int64_t sum = 0;
+#pragma unroll
+            for (int k = 0; k < STREAMS; ++k) sum = wadd64(sum, red[k][threadIdx.x]);
+            atomicAdd(acc + (size_t)(g * G + h) * HD + threadIdx.x, (unsigned long long)sum);
         }
+        __syncthreads();
     }
-}
-
-// attn_out[i] = clamp(rescale(clamp(RNE(sum_c partial[c][i], 14)), v_frac, attn_out_frac)).
-__global__ void attn_reduce_kernel(const DecodeState* __restrict__ st, const int64_t* __restrict__ partial, int nq,
-                                   uint8_t v_frac, uint8_t attn_out_frac, int16_t* __restrict__ out) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= nq) return;
-    const int L = st->pos + 1;
-    const int chunks = (L + kChunk - 1) >> kChunkLog;
-    int64_t s = 0;
-    for (int c = 0; c < chunks; ++c) s = wadd64(s, partial[(size_t)c * nq + i]);
-    const int16_t a = clamp_i16_i64(rshift_round64(s, MYL_TV_PROB_FRAC_BITS));
-    out[i] = clamp_i16(rescale32((int32_t)a, v_frac, attn_out_frac));
 }
 
 // ---------------------------------------------------------------------------
@@ -453,6 +752,7 @@ struct LayerDev {
     uint8_t *in_gamma_s = nullptr, *post_gamma_s = nullptr;
     uint8_t *res_in = nullptr, *res_mid = nullptr, *acc_attn = nullptr, *acc_mlp = nullptr;
     const uint8_t* res_out = nullptr;  // next layer's res_in or the final segment
+    uint8_t ref_in = 0, ref_mid = 0, ref_out = 0;  // max of res_in / res_mid / res_out (rmsnorm.rs:96)
     myl_layer_fracs f{};
 };
 
@@ -484,11 +784,25 @@ struct myl_model {
     int32_t* logits = nullptr;
     int32_t* scores = nullptr;
     AttnStat* stats = nullptr;
-    int64_t* partial = nullptr;
+    unsigned long long* attn_acc = nullptr;  // [nq] exact P.V sums, cleared after each use
+    NormAcc* norm_a = nullptr;               // input-norm / final-norm sums of squares
+    NormAcc* norm_b = nullptr;               // post-attention-norm sums of squares
+    uint8_t ref_final = 0;
+    int cus = 0;
     DecodeState* state = nullptr;
     int64_t* tokens_dev = nullptr;
     uint32_t tokens_cap = 0;
     uint32_t n_cached = 0;
+    // decode step captured as a HIP graph (replayed per greedy step)
+    bool use_graphs = true;
+    hipGraph_t step_graph = nullptr;
+    hipGraphExec_t step_exec = nullptr;
+    const int64_t* graph_tokens = nullptr;
+    // per-kernel-class event timing (eager launches only)
+    bool timing = false;
+    std::vector<hipEvent_t> ev_pool;
+    size_t ev_used = 0;
+    std::vector<std::pair<int, size_t>> marks;  // (class, index of the start event; end = +1)
 
     template <class T> T* dalloc(size_t count) {
         void* p = nullptr;
@@ -498,11 +812,39 @@ struct myl_model {
     }
     ~myl_model() {
         if (ctx) (void)hipStreamSynchronize(ctx->stream);
+        if (step_exec) (void)hipGraphExecDestroy(step_exec);
+        if (step_graph) (void)hipGraphDestroy(step_graph);
+        for (hipEvent_t e : ev_pool) (void)hipEventDestroy(e);
         for (void* p : allocs) (void)hipFree(p);
     }
 };
 
 namespace {
+
+// Kernel classes of one decode step, for the per-class event timing.
+enum KClass { K_EMBED = 0, K_RMS, K_QKV, K_ATTN, K_O, K_GU, K_DOWN, K_HEAD, K_COUNT };
+
+struct TimedScope {
+    myl_model* m;
+    int cls;
+    size_t idx = 0;
+    TimedScope(myl_model* mm, int c) : m(mm), cls(c) {
+        if (!m->timing) return;
+        while (m->ev_pool.size() < m->ev_used + 2) {
+            hipEvent_t e;
+            if (hipEventCreate(&e) != hipSuccess) { m->timing = false; return; }
+            m->ev_pool.push_back(e);
+        }
+        idx = m->ev_used;
+        m->ev_used += 2;
+        (void)hipEventRecord(m->ev_pool[idx], m->ctx->stream);
+    }
+    ~TimedScope() {
+        if (!m->timing || m->ev_used < idx + 2) return;
+        (void)hipEventRecord(m->ev_pool[idx + 1], m->ctx->stream);
+        m->marks.push_back({cls, idx});
+    }
+};
 
 int ilog2_exact(int v) {
     int l = 0;
@@ -727,8 +1069,15 @@ int build(myl_model* m, const myl_luts* luts) {
         rc |= upload(m, L.acc_mlp, acc_m);
         if (rc) return MYL_E_HIP;
     }
-    for (uint32_t l = 0; l < s.layers; ++l)
-        m->layers[l].res_out = (l + 1 < s.layers) ? m->layers[l + 1].res_in : m->final_res;
+    auto vmax = [](const std::vector<uint8_t>& v) { uint8_t r = 0; for (uint8_t x : v) r = std::max(r, x); return r; };
+    m->ref_final = vmax(final_res);
+    for (uint32_t l = 0; l < s.layers; ++l) {
+        LayerDev& L = m->layers[l];
+        L.res_out = (l + 1 < s.layers) ? m->layers[l + 1].res_in : m->final_res;
+        L.ref_in = vmax(res_in[l]);
+        L.ref_mid = vmax(res_mid[l]);
+        L.ref_out = (l + 1 < s.layers) ? vmax(res_in[l + 1]) : m->ref_final;
+    }
 
     // caches, activations, scratch
     const size_t kv = (size_t)s.layers * s.kv_heads * (size_t)m->max_pos * hd;
@@ -743,40 +1092,53 @@ int build(myl_model* m, const myl_luts* luts) {
     m->logits = m->dalloc<int32_t>(V);
     m->scores = m->dalloc<int32_t>((size_t)s.heads * m->max_pos);
     m->stats = m->dalloc<AttnStat>(s.heads);
-    const int max_chunks = (m->max_pos + kChunk - 1) / kChunk;
-    m->partial = m->dalloc<int64_t>((size_t)max_chunks * nq);
+    m->attn_acc = m->dalloc<unsigned long long>((size_t)nq);
+    m->norm_a = m->dalloc<NormAcc>(1);
+    m->norm_b = m->dalloc<NormAcc>(1);
     m->state = m->dalloc<DecodeState>(1);
     if (!m->kcache || !m->vcache || !m->hidden || !m->norm || !m->q || !m->attn || !m->resid || !m->h ||
-        !m->logits || !m->scores || !m->stats || !m->partial || !m->state)
+        !m->logits || !m->scores || !m->stats || !m->attn_acc || !m->state || !m->norm_a || !m->norm_b)
         return c->fail(MYL_E_NOMEM, "activation allocation");
     if (hipMemsetAsync(m->kcache, 0, kv * 2, c->stream) != hipSuccess ||
         hipMemsetAsync(m->vcache, 0, kv * 2, c->stream) != hipSuccess ||
-        hipMemsetAsync(m->state, 0, sizeof(DecodeState), c->stream) != hipSuccess)
+        hipMemsetAsync(m->state, 0, sizeof(DecodeState), c->stream) != hipSuccess ||
+        hipMemsetAsync(m->attn_acc, 0, (size_t)nq * 8, c->stream) != hipSuccess ||
+        hipMemsetAsync(m->norm_a, 0, sizeof(NormAcc), c->stream) != hipSuccess ||
+        hipMemsetAsync(m->norm_b, 0, sizeof(NormAcc), c->stream) != hipSuccess)
         return MYL_E_HIP;
     return c->hip(hipStreamSynchronize(c->stream), "model build");
 }
 
-hipError_t rms(myl_model* m, const int16_t* x, const uint8_t* xs, const int8_t* g, const uint8_t* gs, uint8_t out_frac,
-               int16_t* out) {
-    return rmsnorm(x, 1, m->H, xs, g, gs, m->H, m->rsqrt, m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT,
-                   MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, out_frac, out, m->H, m->ctx->stream);
+RmsParams rms_params(const myl_model* m) {
+    return RmsParams{m->rsqrt, m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20};
 }
 
-// One transformer layer on m->hidden (model.rs:401-674); the result replaces m->hidden.
+// One transformer layer on m->hidden (model.rs:401-674); the result replaces
+// m->hidden and its input-norm sum is left in norm_a for the next consumer.
+//   qkv   : RMSNorm(hidden) staged from norm_a            -> q, KV cache
+//   attn  : scores, stats, P.V into attn_acc
+//   o     : attn_acc staged, residual 1 -> resid; sum -> norm_b; clears norm_a
+//   gu    : RMSNorm(resid) staged from norm_b             -> h; clears attn_acc
+//   down  : h, residual 2 -> hidden; sum -> norm_a; clears norm_b
 hipError_t layer_step(myl_model* m, int l) {
     const LayerDev& L = m->layers[l];
     const myl_layer_fracs& f = L.f;
     hipStream_t st = m->ctx->stream;
-    const int H = m->H, I = m->I, nq = m->nq, nkv = m->nkv, hd = m->hd, G = m->G;
+    const int H = m->H, I = m->I, nq = m->nq, nkv = m->nkv, hd = m->hd, G = m->G, cus = m->cus;
     const int kvh = (int)m->spec.kv_heads;
-    hipError_t e = rms(m, m->hidden, L.res_in, L.in_gamma, L.in_gamma_s, f.norm_attn_frac, m->norm);
-    if (e != hipSuccess) return e;
+    const RmsParams rp = rms_params(m);
+    hipError_t e;
     {
         const size_t layer_kv = (size_t)l * kvh * m->max_pos * hd;
         EpiQKV q{L.sqkv, L.bqkv, L.bsqkv, f.norm_attn_frac, f.q_frac, f.k_frac, f.v_frac, nq, nkv, m->hd_log,
                  m->max_pos, m->cos_lut, m->sin_lut, m->state, m->q, m->kcache + layer_kv, m->vcache + layer_kv};
-        e = gemv_model<2>(m->norm, L.wqkv, nq + 2 * nkv, H, q, st);
+        SrcNorm src{m->hidden, L.res_in, L.in_gamma, L.in_gamma_s, rp, L.ref_in, f.norm_attn_frac, m->norm_a};
+        {
+            TimedScope t(m, K_QKV);
+            e = stream_i8<2, 4, 4>(src, L.wqkv, nq + 2 * nkv, H, q, st, cus);
+        }
         if (e != hipSuccess) return e;
+        TimedScope ta(m, K_ATTN);
         const uint32_t ss = (uint32_t)f.q_frac + f.k_frac + 15u;
         const uint8_t score_shift = (uint8_t)(ss > MYL_TV_SCORE_FRAC_BITS ? ss - MYL_TV_SCORE_FRAC_BITS : 0);
         const uint8_t lut_shift = MYL_TV_SCORE_FRAC_BITS - MYL_TV_EXP_INPUT_FRAC;
@@ -790,54 +1152,71 @@ hipError_t layer_step(myl_model* m, int l) {
             attn_scores_kernel<64><<<dim3(chunks, kvh), 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, m->score_mult,
                                                                     score_shift, m->scores);
         }
-        attn_stats_kernel<<<m->spec.heads, 256, 0, st>>>(m->state, m->scores, m->max_pos, m->exp_lut,
-                                                         (uint32_t)m->exp_len, lut_shift, m->stats);
+        attn_stats_kernel<<<m->spec.heads, kStatThreads, 0, st>>>(m->state, m->scores, m->max_pos, m->exp_lut,
+                                                                  (uint32_t)m->exp_len, lut_shift, m->stats);
         if (hd == 128) {
             attn_pv_kernel<128><<<dim3(chunks, kvh), 256, 0, st>>>(m->state, m->scores, m->stats, vc, m->max_pos, G,
                                                                  m->exp_lut, (uint32_t)m->exp_len, lut_shift,
-                                                                 m->partial, nq);
+                                                                 m->attn_acc);
         } else {
             attn_pv_kernel<64><<<dim3(chunks, kvh), 256, 0, st>>>(m->state, m->scores, m->stats, vc, m->max_pos, G,
                                                                 m->exp_lut, (uint32_t)m->exp_len, lut_shift,
-                                                                m->partial, nq);
+                                                                m->attn_acc);
         }
-        attn_reduce_kernel<<<(nq + 255) / 256, 256, 0, st>>>(m->state, m->partial, nq, f.v_frac, f.attn_out_frac,
-                                                            m->attn);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     {
-        EpiResid o{L.so, f.attn_out_frac, L.acc_attn, L.res_in, L.res_mid, m->hidden, m->resid};
-        e = gemv_model<2>(m->attn, L.wo, H, nq, o, st);
+        TimedScope t(m, K_O);
+        SrcAttn src{m->attn_acc, f.v_frac, f.attn_out_frac};
+        EpiResid o{L.so, f.attn_out_frac, L.acc_attn, L.res_in, L.res_mid, m->hidden, m->resid, m->norm_b, L.ref_mid,
+                   m->norm_a};
+        e = stream_i8<1, 4, 4>(src, L.wo, H, nq, o, st, cus);
         if (e != hipSuccess) return e;
     }
-    e = rms(m, m->resid, L.res_mid, L.post_gamma, L.post_gamma_s, f.norm_mlp_frac, m->norm);
+    {
+        TimedScope t(m, K_GU);
+        SrcNorm src{m->resid, L.res_mid, L.post_gamma, L.post_gamma_s, rp, L.ref_mid, f.norm_mlp_frac, m->norm_b};
+        EpiSilu s{L.sgu, f.norm_mlp_frac, f.gate_frac, f.up_frac, f.down_in_frac, m->silu, (uint32_t)m->silu_len, m->h,
+                  m->attn_acc, nq};
+        e = stream_i8<2, 4, 4>(src, L.wgu, 2 * I, H, s, st, cus);
+    }
     if (e != hipSuccess) return e;
     {
-        EpiSilu s{L.sgu, f.norm_mlp_frac, f.gate_frac, f.up_frac, f.down_in_frac, m->silu, (uint32_t)m->silu_len, m->h};
-        e = gemv_model<2>(m->norm, L.wgu, 2 * I, H, s, st);
-        if (e != hipSuccess) return e;
-        EpiResid d{L.sd, f.down_in_frac, L.acc_mlp, L.res_mid, L.res_out, m->resid, m->hidden};
-        e = gemv_model<2>(m->h, L.wd, H, I, d, st);
+        TimedScope t(m, K_DOWN);
+        SrcPlain src{m->h};
+        EpiResid d{L.sd, f.down_in_frac, L.acc_mlp, L.res_mid, L.res_out, m->resid, m->hidden, m->norm_a, L.ref_out,
+                   m->norm_b};
+        e = stream_i8<1, 4, 4>(src, L.wd, H, I, d, st, cus);
     }
     return e;
 }
 
+// Final RMSNorm (staged from norm_a) + LM head + argmax (model.rs:264-308).
 hipError_t head_step(myl_model* m) {
     hipStream_t st = m->ctx->stream;
-    hipError_t e = rms(m, m->hidden, m->final_res, m->final_gamma, m->final_gamma_s, m->final_norm_frac, m->norm);
-    if (e != hipSuccess) return e;
+    TimedScope t(m, K_HEAD);
+    SrcNorm src{m->hidden, m->final_res, m->final_gamma, m->final_gamma_s, rms_params(m), m->ref_final,
+                m->final_norm_frac, m->norm_a};
     if (m->spec.lm_head_int16) {
         EpiHead hd{m->lm16_shifts, m->final_norm_frac, m->logits, m->state};
-        return gemv_model16<2>(m->norm, m->lm16, m->V, m->H, hd, st);
+        return stream_i16<2, 4, 4>(src, m->lm16, m->V, m->H, hd, st, m->cus);
     }
     EpiHead hd{m->emb_shifts, m->final_norm_frac, m->logits, m->state};
-    return gemv_model<2>(m->norm, m->emb, m->V, m->H, hd, st);
+    return stream_i8<2, 4, 4>(src, m->emb, m->V, m->H, hd, st, m->cus);
 }
 
 hipError_t embed_step(myl_model* m, int mode, int token, int pos, int64_t* tokens_dev) {
+    TimedScope t(m, K_EMBED);
     embed_kernel<<<1, 1024, 0, m->ctx->stream>>>(m->state, mode, token, pos, m->rope_rows, m->V, m->emb, m->emb_shifts,
-                                                  m->layers[0].res_in, m->H, tokens_dev, m->hidden);
+                                                  m->layers[0].res_in, m->layers[0].ref_in, m->H, tokens_dev, m->hidden,
+                                                  m->norm_a);
+    return hipGetLastError();
+}
+
+// The input-norm accumulator for a hidden vector supplied by the host.
+hipError_t seed_norm(myl_model* m, const uint8_t* xs, uint8_t ref) {
+    norm_seed_kernel<<<1, 1024, 0, m->ctx->stream>>>(m->hidden, xs, ref, m->H, m->norm_a);
     return hipGetLastError();
 }
 
@@ -848,9 +1227,70 @@ hipError_t full_step(myl_model* m, int mode, int token, int pos, int64_t* tokens
     return e;
 }
 
+// Captures one greedy step (mode 1: token and position come from the device
+// state) as a graph; replays are valid for any position.
+// Capture runs on the context's own stream (the caller's stream may be the
+// legacy null stream, which cannot capture); the graph is later launched on
+// whichever stream is active.
+hipError_t capture_step(myl_model* m) {
+    myl_ctx* c = m->ctx;
+    if (m->step_exec) { (void)hipGraphExecDestroy(m->step_exec); m->step_exec = nullptr; }
+    if (m->step_graph) { (void)hipGraphDestroy(m->step_graph); m->step_graph = nullptr; }
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return e;
+    hipStream_t active = c->stream;
+    c->stream = c->own_stream;
+    e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) { c->stream = active; return e; }
+    hipError_t le = full_step(m, 1, 0, 0, m->tokens_dev);
+    e = hipStreamEndCapture(c->stream, &m->step_graph);
+    c->stream = active;
+    if (le != hipSuccess) return le;
+    if (e != hipSuccess) return e;
+    e = hipGraphInstantiate(&m->step_exec, m->step_graph, nullptr, nullptr, 0);
+    if (e == hipSuccess) m->graph_tokens = m->tokens_dev;
+    return e;
+}
+
 }  // namespace
 
 extern "C" {
+
+int myl_model_set_graphs(myl_model* m, int enable) {
+    if (!m) return MYL_E_INVALID;
+    m->use_graphs = enable != 0;
+    return MYL_OK;
+}
+
+int myl_model_timing(myl_model* m, int enable, double* ms_out, uint64_t* counts_out) {
+    if (!m) return MYL_E_INVALID;
+    myl_ctx* c = m->ctx;
+    if (enable) {
+        m->timing = true;
+        m->ev_used = 0;
+        m->marks.clear();
+        return MYL_OK;
+    }
+    int rc = c->hip(hipStreamSynchronize(c->stream), "timing");
+    if (rc) return rc;
+    std::vector<double> ms(K_COUNT, 0.0);
+    std::vector<uint64_t> n(K_COUNT, 0);
+    for (auto& mk : m->marks) {
+        float t = 0.f;
+        if (hipEventElapsedTime(&t, m->ev_pool[mk.second], m->ev_pool[mk.second + 1]) == hipSuccess) {
+            ms[mk.first] += t;
+            n[mk.first] += 1;
+        }
+    }
+    m->timing = false;
+    m->ev_used = 0;
+    m->marks.clear();
+    for (int k = 0; k < K_COUNT; ++k) {
+        if (ms_out) ms_out[k] = ms[k];
+        if (counts_out) counts_out[k] = n[k];
+    }
+    return MYL_OK;
+}
 
 int myl_model_create_synthetic(myl_ctx* ctx, const myl_synth_spec* spec, const myl_luts* luts, myl_model** out) {
     if (!ctx || !spec || !luts || !out) return MYL_E_INVALID;
@@ -883,6 +1323,7 @@ int myl_model_create_synthetic(myl_ctx* ctx, const myl_synth_spec* spec, const m
     m->nq = (int)(s.heads * s.head_dim);
     m->nkv = (int)(s.kv_heads * s.head_dim);
     m->max_pos = (int)s.max_pos;
+    m->cus = ctx->prop.multiProcessorCount > 0 ? ctx->prop.multiProcessorCount : 1;
     int rc = build(m, luts);
     if (rc) {
         delete m;
@@ -943,11 +1384,14 @@ int myl_model_decode_greedy(myl_model* m, uint32_t token, uint32_t pos, uint32_t
     // Step 0 consumes the given token; step i >= 1 consumes step i-1's argmax.
     // The argmax of the last step is the next token, reported by tokens_out.
     hipError_t e = full_step(m, 0, (int)token, (int)pos, nullptr);
+    const bool graphs = m->use_graphs && !m->timing && n_steps > 2;
+    if (e == hipSuccess && graphs && (!m->step_exec || m->graph_tokens != m->tokens_dev)) e = capture_step(m);
     for (uint32_t i = 0; e == hipSuccess && i < n_steps; ++i) {
         if (logits_out)
             e = hipMemcpyAsync(logits_out + (size_t)i * m->V, m->logits, (size_t)m->V * 4, hipMemcpyDeviceToHost,
                                c->stream);
-        if (e == hipSuccess && i + 1 < n_steps) e = full_step(m, 1, 0, 0, m->tokens_dev);
+        if (e == hipSuccess && i + 1 < n_steps)
+            e = graphs ? hipGraphLaunch(m->step_exec, c->stream) : full_step(m, 1, 0, 0, m->tokens_dev);
     }
     int rc = c->hip(e, "decode");
     if (rc) return rc;
@@ -967,6 +1411,30 @@ int myl_model_decode_greedy(myl_model* m, uint32_t token, uint32_t pos, uint32_t
     toks[n_steps - 1] = key_index(s.argmax_key);
     if (tokens_out) std::memcpy(tokens_out, toks.data(), (size_t)n_steps * 8);
     return MYL_OK;
+}
+
+int myl_model_prefill(myl_model* m, const uint32_t* tokens, uint32_t n, uint32_t pos0, int32_t* last_logits) {
+    if (!m || (!tokens && n)) return MYL_E_INVALID;
+    myl_ctx* c = m->ctx;
+    if (n == 0) return MYL_OK;
+    if ((uint64_t)pos0 + n > (uint64_t)m->max_pos) return c->fail(MYL_E_INVALID, "prefill: beyond the KV capacity");
+    if (pos0 > m->n_cached) return c->fail(MYL_E_INVALID, "prefill: positions must be contiguous from 0");
+    for (uint32_t i = 0; i < n; ++i)
+        if (tokens[i] >= (uint32_t)m->V) return c->fail(MYL_E_INVALID, "prefill: token id out of range");
+    hipError_t e = hipSuccess;
+    for (uint32_t i = 0; e == hipSuccess && i < n; ++i) {
+        e = embed_step(m, 0, (int)tokens[i], (int)(pos0 + i), nullptr);
+        for (int l = 0; e == hipSuccess && l < (int)m->spec.layers; ++l) e = layer_step(m, l);
+    }
+    if (e == hipSuccess) e = head_step(m);
+    int rc = c->hip(e, "prefill");
+    if (rc) return rc;
+    m->n_cached = std::max(m->n_cached, pos0 + n);
+    if (last_logits) {
+        rc = c->hip(hipMemcpyAsync(last_logits, m->logits, (size_t)m->V * 4, hipMemcpyDeviceToHost, c->stream), "logits");
+        if (rc) return rc;
+    }
+    return c->hip(hipStreamSynchronize(c->stream), "prefill");
 }
 
 int myl_model_embed_token(myl_model* m, uint32_t token, int16_t* hidden) {
@@ -992,6 +1460,7 @@ int myl_model_run_layers(myl_model* m, int16_t* hidden, uint32_t pos, uint32_t l
     if (rc) return rc;
     rc = c->hip(hipMemcpyAsync(m->hidden, hidden, (size_t)m->H * 2, hipMemcpyHostToDevice, c->stream), "hidden");
     hipError_t e = hipSuccess;
+    if (!rc && layer_start < layer_end) e = seed_norm(m, m->layers[layer_start].res_in, m->layers[layer_start].ref_in);
     for (uint32_t l = layer_start; !rc && e == hipSuccess && l < layer_end; ++l) e = layer_step(m, (int)l);
     if (!rc) rc = c->hip(e, "run_layers");
     if (rc) return rc;
@@ -1004,6 +1473,8 @@ int myl_model_head_logits(myl_model* m, const int16_t* hidden, int32_t* logits) 
     if (!m || !hidden || !logits) return MYL_E_INVALID;
     myl_ctx* c = m->ctx;
     int rc = c->hip(hipMemcpyAsync(m->hidden, hidden, (size_t)m->H * 2, hipMemcpyHostToDevice, c->stream), "hidden");
+    if (rc) return rc;
+    rc = c->hip(seed_norm(m, m->final_res, m->ref_final), "head_logits");
     if (rc) return rc;
     rc = c->hip(head_step(m), "head_logits");
     if (rc) return rc;

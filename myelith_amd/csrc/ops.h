@@ -90,14 +90,77 @@ __device__ inline RmsFactor rms_factor(const int16_t* x, const uint8_t* xs, int 
     return f;
 }
 
+// Per-channel output of rmsnorm.rs:130-159.  |x * lut * gamma| < 2^37, so for
+// 0 <= shift <= 62 and for left shifts up to 25 bits the i64 computation is the
+// i128 one bit for bit; other shifts take the i128 path.
 __device__ inline int16_t rms_out(int16_t x, uint8_t xs, int8_t g, uint8_t gs, const RmsFactor& f, uint8_t out_frac) {
     if (f.zero) return 0;
     const int32_t total = (int32_t)f.norm_frac + (int32_t)gs + ((int32_t)xs - (int32_t)f.ref_shift);
     const int32_t shift = total - (int32_t)out_frac;
-    const myl_i128 prod = (myl_i128)x * (myl_i128)f.lut_val * (myl_i128)g;
+    const int64_t p64 = (int64_t)x * f.lut_val * (int64_t)g;
+    if (shift >= 0 && shift <= 62) return clamp_i16_i64(clamp_i32_i64(rshift_round64(p64, (uint8_t)shift)));
+    if (shift < 0 && shift >= -25) return clamp_i16_i64(clamp_i32_i64(p64 << (-shift)));
+    const myl_i128 prod = (myl_i128)p64;
     const myl_i128 s = shift >= 0 ? rshift_round128(prod, (uint32_t)shift) : shl128(prod, (uint32_t)(-shift));
     const int32_t c = s < (myl_i128)INT32_MIN ? INT32_MIN : (s > (myl_i128)INT32_MAX ? INT32_MAX : (int32_t)s);
     return clamp_i16(c);
+}
+
+// Exact i128 sum over a wave: 64-bit halves exchanged by shuffles, carry kept.
+__device__ inline myl_i128 wave_sum_i128(myl_i128 v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint64_t lo = (uint64_t)(myl_u128)v, hi = (uint64_t)((myl_u128)v >> 64);
+        const uint32_t l0 = (uint32_t)__shfl_xor((int)(uint32_t)lo, off, 64);
+        const uint32_t l1 = (uint32_t)__shfl_xor((int)(uint32_t)(lo >> 32), off, 64);
+        const uint32_t h0 = (uint32_t)__shfl_xor((int)(uint32_t)hi, off, 64);
+        const uint32_t h1 = (uint32_t)__shfl_xor((int)(uint32_t)(hi >> 32), off, 64);
+        const myl_u128 o = ((myl_u128)(((uint64_t)h1 << 32) | h0) << 64) | (((uint64_t)l1 << 32) | l0);
+        v = (myl_i128)((myl_u128)v + o);
+    }
+    return v;
+}
+
+// Norm factor for blocks of up to 1024 threads where each thread holds PER
+// elements (x, x_shift) in registers (invalid slots carry x = 0, xs = 0).
+template <int PER>
+__device__ inline RmsFactor rms_factor_regs(const int16_t (&x)[PER], const uint8_t (&xs)[PER], const RmsParams& p,
+                                            myl_i128* red128, int32_t* red32) {
+    int32_t mx = 0;
+#pragma unroll
+    for (int t = 0; t < PER; ++t) mx = max(mx, (int32_t)xs[t]);
+    const uint8_t ref = (uint8_t)block_max_i32(mx, red32);
+    myl_i128 acc = 0;
+#pragma unroll
+    for (int t = 0; t < PER; ++t) {
+        const uint32_t align = 2u * (uint32_t)(uint8_t)(ref - xs[t]);
+        const int64_t sq = (int64_t)x[t] * (int64_t)x[t];
+        acc = (myl_i128)((myl_u128)acc + (myl_u128)shl128((myl_i128)sq, align));
+    }
+    acc = wave_sum_i128(acc);
+    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red128[w] = acc;
+    __syncthreads();
+    acc = 0;
+    for (int i = 0; i < nw; ++i) acc = (myl_i128)((myl_u128)acc + (myl_u128)red128[i]);
+    RmsFactor f;
+    f.ref_shift = ref;
+    f.zero = acc == 0;
+    f.lut_val = 0;
+    f.norm_frac = 0;
+    if (!f.zero) {
+        const myl_i128 m = shr128((myl_i128)((myl_u128)acc * (myl_u128)(myl_i128)p.inv_n_q20), 20);
+        const myl_i128 max_idx = (myl_i128)(p.lut_len - 1);
+        uint32_t q = 0;
+        while (shr128(m, q) > max_idx) q += 2;
+        myl_i128 idx = rshift_round128(m, q);
+        if (idx > max_idx) idx = max_idx;
+        if (idx < 0) idx = 0;
+        f.lut_val = (int64_t)p.lut[(int)idx];
+        f.norm_frac = (uint32_t)p.lut_output_frac + (uint32_t)p.lut_input_shift / 2u + q / 2u;
+    }
+    return f;
 }
 
 // ---- softmax.rs:12-64 ----------------------------------------------------------

@@ -96,6 +96,29 @@ class IntegerModel:
                                                   None if logits is None else logits.ctypes.data), "decode_greedy")
         return toks, logits
 
+    def prefill(self, token_ids, pos0: int = 0, want_logits: bool = True):
+        """The prompt loop of generate.rs:28-32 in one call; returns the last logits."""
+        toks = np.ascontiguousarray(token_ids, dtype=np.uint32)
+        logits = np.zeros(self.vocab_size, np.int32) if want_logits else None
+        self._check(lib().myl_model_prefill(self._h, toks.ctypes.data, toks.size, pos0,
+                                            None if logits is None else logits.ctypes.data), "prefill")
+        return logits
+
+    def set_graphs(self, enable: bool) -> None:
+        self._check(lib().myl_model_set_graphs(self._h, int(enable)), "set_graphs")
+
+    KERNEL_CLASSES = ("embed", "rmsnorm", "qkv", "attention", "o_proj", "gate_up", "down", "lm_head")
+
+    def timing(self, enable: bool):
+        """Starts (True) or stops (False) per-kernel-class HIP event timing.
+        Stopping returns {class: (total_ms, launches)}."""
+        ms = np.zeros(8, np.float64)
+        n = np.zeros(8, np.uint64)
+        self._check(lib().myl_model_timing(self._h, int(enable), ms.ctypes.data, n.ctypes.data), "timing")
+        if enable:
+            return None
+        return {k: (float(ms[i]), int(n[i])) for i, k in enumerate(self.KERNEL_CLASSES)}
+
     def embed_token(self, token_id: int) -> np.ndarray:
         h = np.zeros(self.hidden_size, np.int16)
         self._check(lib().myl_model_embed_token(self._h, token_id, h.ctypes.data), "embed_token")
