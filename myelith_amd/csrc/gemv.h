@@ -25,6 +25,7 @@
 #pragma once
 
 #include "fixed.h"
+#include "wave.h"
 
 namespace myl {
 
@@ -32,16 +33,6 @@ constexpr int kWave = 64;
 constexpr int kGemvThreads = 256;
 constexpr int kGemvWaves = kGemvThreads / kWave;
 constexpr int kGemvLdsBytes = 64 * 1024;
-
-__device__ inline int64_t wave_sum_i64(int64_t v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        int lo = __shfl_xor((int)(uint32_t)v, off, kWave);
-        int hi = __shfl_xor((int)(uint32_t)((uint64_t)v >> 32), off, kWave);
-        v = wadd64(v, (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
-    }
-    return v;
-}
 
 __device__ inline int32_t sdot4(uint32_t a, uint32_t b, int32_t c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);

@@ -8,7 +8,21 @@
 // batches of U steps of 1 KiB per row (int8) or 8 weights per lane (int16);
 // two register buffers alternate, so the loads of the next batch are in flight
 // while the current batch is multiplied.  The sums are exact (see gemv.h for
-// the byte-split bounds); the epilogue gets R rows per group.
+// the byte-split bounds).
+//
+// The streaming loop touches global memory only through the weight loads.
+// vmcnt is one in-order counter for loads and stores alike, so any other
+// global access inside the loop (an epilogue operand, a LUT lookup, a store)
+// would make the next wait drain the prefetched batch.  Each finished group
+// therefore leaves its R exact sums, reduced to wave-uniform values with DPP,
+// in a per-wave LDS record; after the stream every lane applies the epilogue
+// to one recorded group, so all epilogue loads and stores of a wave overlap.
+//
+// Epilogue interface:
+//   State; begin(State&)                        per thread, before the stream
+//   group(State&, row0, N, const int64_t (&)[R]) per lane, one group each
+//   finish(State&)                               whole block, after the stream
+//                                                (may synchronise the block)
 #pragma once
 
 #include "gemv.h"
@@ -38,15 +52,39 @@ struct SrcPlain {
     }
 };
 
+// LDS bytes of a stream launch: the two activation planes plus the records.
+__host__ __device__ inline size_t stream_lds_bytes(int K, int elem, int waves, int gpw, int R) {
+    const size_t step = elem == 1 ? 16 : 8;
+    const size_t kpad = (((size_t)K + step - 1) / step) * step;
+    return 2 * kpad * (size_t)elem + (size_t)waves * gpw * R * 8;
+}
+
+template <int R, class Epi>
+__device__ inline void stream_epilogue(const int64_t* rec, int g0, int nw, int cnt, int N, int lane, Epi& epi,
+                                       typename Epi::State& es) {
+    for (int k = lane; k < cnt; k += kWave) {
+        int64_t tot[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) tot[r] = rec[k * R + r];
+        epi.group(es, (g0 + k * nw) * R, N, tot);
+    }
+}
+
+// gpw: the most groups any wave of the grid handles, ceil(ceil(N/R) / waves);
+// the launcher sizes the records from it.
 template <int R, int U, int WAVES, class Src, class Epi>
 __global__ __launch_bounds__(WAVES * 64) void gemv_i8_stream(Src src, const int8_t* __restrict__ W, int N, int K,
-                                                            Epi epi) {
+                                                            int gpw, Epi epi) {
     extern __shared__ __align__(16) int8_t lds[];
     const int kpad = ((K + 15) >> 4) << 4;
     int8_t* hi_plane = lds;
     int8_t* lo_plane = lds + kpad;
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
+    // wave-uniform by construction; readfirstlane lets the compiler keep the
+    // loop control in scalar registers (a vector loop would end every
+    // iteration with a full vmcnt drain)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    int64_t* rec = reinterpret_cast<int64_t*>(lds + 2 * kpad) + (size_t)wave * gpw * R;
     const int nw = gridDim.x * WAVES;
     const int ngroups = (N + R - 1) / R;
     const int nit = (K + kWave * 16 - 1) / (kWave * 16);  // 1 KiB steps per row
@@ -98,57 +136,68 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i8_stream(Src src, const int8
             }
         }
     };
-    auto finish_group = [&](int g) {
-        int64_t tot[R][1];
+    // The three partial sums are exact in i32 over the whole row (K <= 131072),
+    // so each is reduced in i32 and widened once.
+    int cnt = 0;
+    auto finish_group = [&]() {
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            tot[r][0] = wave_sum_i64((int64_t)ahi[r] * 256 + (int64_t)alo[r] + (int64_t)aws[r] * 128);
-        epi.group(es, g * R, N, lane, tot);
+        for (int r = 0; r < R; ++r) {
+            const int64_t t = (int64_t)wave_sum_i32(ahi[r]) * 256 + (int64_t)wave_sum_i32(alo[r]) +
+                              (int64_t)wave_sum_i32(aws[r]) * 128;
+            if (lane == 0) rec[cnt * R + r] = t;
+        }
+        ++cnt;
         reset();
     };
 
+    // Batch sequence of this wave: (g, kb) for g = g0, g0 + nw, ... and
+    // kb = 0 .. nb-1, taken two at a time; the loads of the batch after next
+    // are issued unconditionally (past the end they fall outside the buffer
+    // and return zeros), so the only branch inside the loop is uniform.
     uint4 A[U][R], B[U][R];
-    int g = blockIdx.x * WAVES + wave, kb = 0;
+    const int g0 = blockIdx.x * WAVES + wave;
+    int g = g0, kb = 0;
+    auto advance = [&](int& gg, int& kk) {
+        if (++kk == nb) { kk = 0; gg += nw; }
+    };
     load(A, g, 0);
     src.stage_i8(hi_plane, lo_plane, K, kpad);
-    epi.zero_duty();
     __syncthreads();
     reset();
     while (g < ngroups) {
-        int g2 = g, kb2 = kb + 1;
-        if (kb2 == nb) { kb2 = 0; g2 = g + nw; }
-        load(B, g2, kb2);
+        int g1 = g, kb1 = kb;
+        advance(g1, kb1);
+        load(B, g1, kb1);
         compute(A, kb);
-        if (kb == nb - 1) finish_group(g);
-        g = g2;
-        kb = kb2;
-        if (g >= ngroups) break;
-        g2 = g;
-        kb2 = kb + 1;
-        if (kb2 == nb) { kb2 = 0; g2 = g + nw; }
+        if (kb == nb - 1) finish_group();
+        int g2 = g1, kb2 = kb1;
+        advance(g2, kb2);
         load(A, g2, kb2);
-        compute(B, kb);
-        if (kb == nb - 1) finish_group(g);
+        if (g1 < ngroups) {
+            compute(B, kb1);
+            if (kb1 == nb - 1) finish_group();
+        }
         g = g2;
         kb = kb2;
     }
+    stream_epilogue<R>(rec, g0, nw, cnt, N, lane, epi, es);
     epi.finish(es);
 }
 
 // int16 weights (LM head path A): planes of int16 hi = x >> 8 and lo = x & 255.
-struct SrcPlain16 {
-    const int16_t* x;
-};
-
 template <int R, int U, int WAVES, class Src16, class Epi>
 __global__ __launch_bounds__(WAVES * 64) void gemv_i16_stream(Src16 src, const int16_t* __restrict__ W, int N,
-                                                             int K, Epi epi) {
+                                                             int K, int gpw, Epi epi) {
     extern __shared__ __align__(16) int8_t lds_raw[];
     const int kpad = ((K + 7) >> 3) << 3;
     int16_t* hi_plane = reinterpret_cast<int16_t*>(lds_raw);
     int16_t* lo_plane = hi_plane + kpad;
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
+    // wave-uniform by construction; readfirstlane lets the compiler keep the
+    // loop control in scalar registers (a vector loop would end every
+    // iteration with a full vmcnt drain)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    int64_t* rec = reinterpret_cast<int64_t*>(lds_raw + 4 * kpad) + (size_t)wave * gpw * R;
     const int nw = gridDim.x * WAVES;
     const int ngroups = (N + R - 1) / R;
     const int nit = (K + kWave * 8 - 1) / (kWave * 8);
@@ -198,39 +247,50 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i16_stream(Src16 src, const i
             }
         }
     };
-    auto finish_group = [&](int g) {
-        int64_t tot[R][1];
+    // Per lane the partials are below 2^31 (K <= 8192); across the wave they
+    // need 64 bits.
+    int cnt = 0;
+    auto finish_group = [&]() {
 #pragma unroll
-        for (int r = 0; r < R; ++r) tot[r][0] = wave_sum_i64((int64_t)ahi[r] * 256 + (int64_t)alo[r]);
-        epi.group(es, g * R, N, lane, tot);
+        for (int r = 0; r < R; ++r) {
+            const int64_t t = wave_sum_i64((int64_t)ahi[r] * 256 + (int64_t)alo[r]);
+            if (lane == 0) rec[cnt * R + r] = t;
+        }
+        ++cnt;
         reset();
     };
 
+    // Batch sequence of this wave: (g, kb) for g = g0, g0 + nw, ... and
+    // kb = 0 .. nb-1, taken two at a time; the loads of the batch after next
+    // are issued unconditionally (past the end they fall outside the buffer
+    // and return zeros), so the only branch inside the loop is uniform.
     uint4 A[U][R], B[U][R];
-    int g = blockIdx.x * WAVES + wave, kb = 0;
+    const int g0 = blockIdx.x * WAVES + wave;
+    int g = g0, kb = 0;
+    auto advance = [&](int& gg, int& kk) {
+        if (++kk == nb) { kk = 0; gg += nw; }
+    };
     load(A, g, 0);
     src.stage_i16(hi_plane, lo_plane, K, kpad);
-    epi.zero_duty();
     __syncthreads();
     reset();
     while (g < ngroups) {
-        int g2 = g, kb2 = kb + 1;
-        if (kb2 == nb) { kb2 = 0; g2 = g + nw; }
-        load(B, g2, kb2);
+        int g1 = g, kb1 = kb;
+        advance(g1, kb1);
+        load(B, g1, kb1);
         compute(A, kb);
-        if (kb == nb - 1) finish_group(g);
-        g = g2;
-        kb = kb2;
-        if (g >= ngroups) break;
-        g2 = g;
-        kb2 = kb + 1;
-        if (kb2 == nb) { kb2 = 0; g2 = g + nw; }
+        if (kb == nb - 1) finish_group();
+        int g2 = g1, kb2 = kb1;
+        advance(g2, kb2);
         load(A, g2, kb2);
-        compute(B, kb);
-        if (kb == nb - 1) finish_group(g);
+        if (g1 < ngroups) {
+            compute(B, kb1);
+            if (kb1 == nb - 1) finish_group();
+        }
         g = g2;
         kb = kb2;
     }
+    stream_epilogue<R>(rec, g0, nw, cnt, N, lane, epi, es);
     epi.finish(es);
 }
 

@@ -11,8 +11,8 @@
 //     rmsnorm      input_layernorm                                 (:416-426)
 //     gemv qkv     q/k/v rows + bias + RoPE, K/V appended to cache (:438-503)
 //     attn_scores  s_j = (i32)RNE(q.k_j * mult, shift)             (attention.rs:66-67)
-//     attn_stats   max, sum of exp-LUT, reciprocal of the sum      (softmax.rs:32-48)
-//     attn_pv      p_j = RNE(e_j * 2^14 / S), partial sum p_j v_j  (softmax.rs:50-63, attention.rs:75-81)
+//     attn_pv      max, sum of exp-LUT, reciprocal of the sum      (softmax.rs:32-48)
+//                  p_j = RNE(e_j * 2^14 / S), partial sum p_j v_j  (softmax.rs:50-63, attention.rs:75-81)
 //     attn_reduce  RNE(., 14), clamp, rescale v -> attn_out        (attention.rs:84-86, model.rs:563-567)
 //     gemv o       o_proj + residual add 1                         (:576-593)
 //     rmsnorm      post_attention_layernorm                        (:596-606)
@@ -43,8 +43,6 @@ using namespace myl;
 namespace {
 
 constexpr int kChunk = 64;           // attention positions per block
-constexpr int kChunkLog = 6;
-constexpr int kMaxGroup = 8;         // query heads per KV head handled by one block
 
 struct DecodeState {
     uint64_t argmax_key;  // packed (value, ~index) of the best logit so far
@@ -54,12 +52,6 @@ struct DecodeState {
     int32_t step;         // decode steps taken since the last set
 };
 
-struct AttnStat {
-    int32_t m;        // max score
-    int32_t S;        // sum of exp-LUT values (wrapping i32)
-    uint64_t recip;   // recip32(|S|) or recip32(L) when S == 0
-    int32_t base, rem;
-};
 
 __device__ inline uint64_t argmax_key(int32_t v, uint32_t idx) {
     return ((uint64_t)((uint32_t)v ^ 0x80000000u) << 32) | (uint64_t)(0xFFFFFFFFu - idx);
@@ -106,16 +98,6 @@ __device__ inline void add_sq_limbs(int16_t x, uint8_t xs, uint8_t ref, uint64_t
     l[0] += (uint64_t)t & kLimbMask;
     l[1] += (uint64_t)(t >> 42) & kLimbMask;
     l[2] += (uint64_t)(t >> 84);
-}
-
-__device__ inline uint64_t wave_sum_u64(uint64_t v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, off, 64);
-        const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), off, 64);
-        v += ((uint64_t)hi << 32) | lo;
-    }
-    return v;
 }
 
 // Block-level sum of per-thread limbs; thread 0 gets the totals.
@@ -351,7 +333,7 @@ __global__ __launch_bounds__(1024) void embed_kernel(DecodeState* st, int mode, 
 }
 
 // ---------------------------------------------------------------------------
-// fused GEMV epilogues (streaming interface: begin / group / zero_duty / finish)
+// fused GEMV epilogues (streaming interface: begin / group per lane / finish)
 // ---------------------------------------------------------------------------
 
 struct NoState {};
@@ -371,12 +353,11 @@ struct EpiQKV {
     int16_t* vc;
     using State = NoState;
     __device__ inline void begin(State&) const {}
-    __device__ inline void zero_duty() const {}
     __device__ inline void finish(State&) const {}
     template <int R>
-    __device__ inline void group(State&, int row0, int N, int lane, const int64_t (&tot)[R][1]) const {
+    __device__ inline void group(State&, int row0, int N, const int64_t (&tot)[R]) const {
         static_assert(R == 2, "the RoPE pair needs two rows per group");
-        if (lane != 0 || row0 >= N) return;
+        if (row0 >= N) return;
         const int seg = row0 < nq ? 0 : (row0 < nq + nkv ? 1 : 2);
         const int e = row0 - (seg == 0 ? 0 : (seg == 1 ? nq : nq + nkv));
         const uint8_t frac = seg == 0 ? q_frac : (seg == 1 ? k_frac : v_frac);
@@ -387,7 +368,7 @@ struct EpiQKV {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const int d = row0 + t;
-            int16_t v = clamp_i16_i64(rescale64(tot[t][0], (uint8_t)(shifts[d] + act_frac), frac));
+            int16_t v = clamp_i16_i64(rescale64(tot[t], (uint8_t)(shifts[d] + act_frac), frac));
             if (bias) v = clamp_i16_i64((int64_t)v + (int64_t)rescale32((int32_t)bias[d], bias_sh[d], frac));
             y[t] = v;
         }
@@ -425,18 +406,14 @@ struct EpiResid {
     NormAcc* clear;            // may be null
     struct State { uint64_t l[3]; };
     __device__ inline void begin(State& s) const { s.l[0] = s.l[1] = s.l[2] = 0; }
-    __device__ inline void zero_duty() const {
-        if (clear && blockIdx.x == 0)
-            for (int i = threadIdx.x; i < kNormSlots * 3; i += blockDim.x) (&clear->v[0][0])[i] = 0;
-    }
     template <int R>
-    __device__ inline void group(State& s, int row0, int N, int lane, const int64_t (&tot)[R][1]) const {
+    __device__ inline void group(State& s, int row0, int N, const int64_t (&tot)[R]) const {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            if (lane == r && row0 + r < N) {
+            if (row0 + r < N) {
                 const int i = row0 + r;
                 const uint8_t af = acc_frac[i];
-                const int16_t o = clamp_i16_i64(rescale64(tot[r][0], (uint8_t)(shifts[i] + act_frac), af));
+                const int16_t o = clamp_i16_i64(rescale64(tot[r], (uint8_t)(shifts[i] + act_frac), af));
                 const int64_t h = rescale64((int64_t)res_in[i], res_frac[i], af);
                 const uint8_t of = out_frac[i];
                 const int16_t v = clamp_i16_i64(rescale64(wadd64(h, (int64_t)o), af, of));
@@ -446,6 +423,8 @@ struct EpiResid {
         }
     }
     __device__ inline void finish(State& s) const {
+        if (clear && blockIdx.x == 0)
+            for (int i = threadIdx.x; i < kNormSlots * 3; i += blockDim.x) (&clear->v[0][0])[i] = 0;
         __shared__ uint64_t red[16 * 3];
         block_sum_limbs(s.l, red);
         if (threadIdx.x == 0) {
@@ -466,16 +445,15 @@ struct EpiSilu {
     unsigned long long* clear; int clear_n;
     using State = NoState;
     __device__ inline void begin(State&) const {}
-    __device__ inline void zero_duty() const {
+    __device__ inline void finish(State&) const {
         for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < clear_n; i += gridDim.x * blockDim.x) clear[i] = 0;
     }
-    __device__ inline void finish(State&) const {}
     template <int R>
-    __device__ inline void group(State&, int row0, int N, int lane, const int64_t (&tot)[R][1]) const {
+    __device__ inline void group(State&, int row0, int N, const int64_t (&tot)[R]) const {
         static_assert(R == 2, "gate and up share a group");
-        if (lane != 0 || row0 >= N) return;
-        const int16_t g = clamp_i16_i64(rescale64(tot[0][0], (uint8_t)(shifts[row0] + act_frac), gate_frac));
-        const int16_t u = clamp_i16_i64(rescale64(tot[1][0], (uint8_t)(shifts[row0 + 1] + act_frac), up_frac));
+        if (row0 >= N) return;
+        const int16_t g = clamp_i16_i64(rescale64(tot[0], (uint8_t)(shifts[row0] + act_frac), gate_frac));
+        const int16_t u = clamp_i16_i64(rescale64(tot[1], (uint8_t)(shifts[row0 + 1] + act_frac), up_frac));
         const int32_t g_dom = rescale32((int32_t)g, gate_frac, MYL_TV_SILU_IN_FRAC);
         const int16_t act = lut_lookup_i16((int16_t)g_dom, silu, silu_len, (int16_t)MYL_TV_SILU_LUT_OFFSET);
         const int64_t prod = (int64_t)act * (int64_t)u;
@@ -484,31 +462,31 @@ struct EpiSilu {
 };
 
 // LM head logits (model.rs:284-308) + first-maximum argmax (sampling.rs:8-18):
-// per group the best key of its rows goes to one atomic, issued only when it
-// beats the current key.
+// each lane keeps the best key of its rows; per wave the maximum goes to one
+// atomic, issued only when it beats the current key.
 struct EpiHead {
     const uint8_t* shifts;
     uint8_t norm_frac;
     int32_t* logits;
     DecodeState* st;
-    using State = NoState;
-    __device__ inline void begin(State&) const {}
-    __device__ inline void zero_duty() const {}
-    __device__ inline void finish(State&) const {}
+    struct State { uint64_t best; };
+    __device__ inline void begin(State& s) const { s.best = 0; }
     template <int R>
-    __device__ inline void group(State&, int row0, int N, int lane, const int64_t (&tot)[R][1]) const {
-        uint64_t best = 0;
+    __device__ inline void group(State& s, int row0, int N, const int64_t (&tot)[R]) const {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             if (row0 + r < N) {
-                const int32_t v = clamp_i32_i64(rescale64(tot[r][0], (uint8_t)(shifts[row0 + r] + norm_frac),
+                const int32_t v = clamp_i32_i64(rescale64(tot[r], (uint8_t)(shifts[row0 + r] + norm_frac),
                                                           MYL_TV_LOGIT_FRAC_BITS));
-                if (lane == r) logits[row0 + r] = v;
+                logits[row0 + r] = v;
                 const uint64_t k = argmax_key(v, (uint32_t)(row0 + r));
-                best = k > best ? k : best;
+                s.best = k > s.best ? k : s.best;
             }
         }
-        if (lane == 0 && best) {
+    }
+    __device__ inline void finish(State& s) const {
+        const uint64_t best = wave_max_u64(s.best);
+        if ((threadIdx.x & 63) == 0 && best) {
             const uint64_t cur = __hip_atomic_load(&st->argmax_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (best > cur) atomicMax((unsigned long long*)&st->argmax_key, (unsigned long long)best);
         }
@@ -517,34 +495,49 @@ struct EpiHead {
 
 // Persistent grid: as many blocks as fit on the device, shrunk so that every
 // wave gets the same number of row groups (no tail of half-filled rounds).
+// Returns the grid and, in gpw, the most groups one wave handles.
 template <class Kern>
-int stream_grid(Kern kern, int waves_per_block, size_t lds, int ngroups, int cus) {
+int stream_grid(Kern kern, int waves_per_block, size_t lds, int ngroups, int cus, int* gpw) {
     int occ = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, waves_per_block * 64, lds) != hipSuccess || occ < 1)
         occ = 1;
     const int waves_cap = occ * cus * waves_per_block;
     const int per_wave = (ngroups + waves_cap - 1) / waves_cap;
     const int waves = (ngroups + per_wave - 1) / per_wave;
-    return (waves + waves_per_block - 1) / waves_per_block;
+    const int grid = (waves + waves_per_block - 1) / waves_per_block;
+    const int nw = grid * waves_per_block;
+    *gpw = (ngroups + nw - 1) / nw;
+    return grid;
 }
+
+// Records are sized for up to kGpwReserve groups per wave when the occupancy
+// is computed; larger counts still run correctly (the LDS grows to fit).
+constexpr int kGpwReserve = 16;
+constexpr size_t kStreamLdsMax = 64 * 1024;
 
 template <int R, int U, int WAVES, class Src, class Epi>
 hipError_t stream_i8(const Src& src, const int8_t* W, int N, int K, const Epi& e, hipStream_t s, int cus) {
-    if ((uint64_t)N * (uint64_t)K > 0xFFFFFF00ull) return hipErrorInvalidValue;  // one buffer descriptor
-    const size_t lds = (size_t)2 * (((K + 15) >> 4) << 4);
+    // one buffer descriptor; i32 partial sums exact for K <= 131072
+    if ((uint64_t)N * (uint64_t)K > 0xFFFFFF00ull || K > 131072 || N < 1 || K < 1) return hipErrorInvalidValue;
     auto kern = gemv_i8_stream<R, U, WAVES, Src, Epi>;
-    const int grid = stream_grid(kern, WAVES, lds, (N + R - 1) / R, cus);
-    kern<<<grid, WAVES * 64, lds, s>>>(src, W, N, K, e);
+    int gpw = 0;
+    const int grid = stream_grid(kern, WAVES, stream_lds_bytes(K, 1, WAVES, kGpwReserve, R), (N + R - 1) / R, cus, &gpw);
+    const size_t lds = stream_lds_bytes(K, 1, WAVES, gpw, R);
+    if (lds > kStreamLdsMax) return hipErrorInvalidValue;
+    kern<<<grid, WAVES * 64, lds, s>>>(src, W, N, K, gpw, e);
     return hipGetLastError();
 }
 
 template <int R, int U, int WAVES, class Src, class Epi>
 hipError_t stream_i16(const Src& src, const int16_t* W, int N, int K, const Epi& e, hipStream_t s, int cus) {
-    if (2ull * (uint64_t)N * (uint64_t)K > 0xFFFFFF00ull) return hipErrorInvalidValue;  // one buffer descriptor
-    const size_t lds = (size_t)4 * (((K + 7) >> 3) << 3);
+    // one buffer descriptor; per-lane i32 partials exact for K <= 8192
+    if (2ull * (uint64_t)N * (uint64_t)K > 0xFFFFFF00ull || K > 8192 || N < 1 || K < 1) return hipErrorInvalidValue;
     auto kern = gemv_i16_stream<R, U, WAVES, Src, Epi>;
-    const int grid = stream_grid(kern, WAVES, lds, (N + R - 1) / R, cus);
-    kern<<<grid, WAVES * 64, lds, s>>>(src, W, N, K, e);
+    int gpw = 0;
+    const int grid = stream_grid(kern, WAVES, stream_lds_bytes(K, 2, WAVES, kGpwReserve, R), (N + R - 1) / R, cus, &gpw);
+    const size_t lds = stream_lds_bytes(K, 2, WAVES, gpw, R);
+    if (lds > kStreamLdsMax) return hipErrorInvalidValue;
+    kern<<<grid, WAVES * 64, lds, s>>>(src, W, N, K, gpw, e);
     return hipGetLastError();
 }
 
@@ -552,190 +545,184 @@ hipError_t stream_i16(const Src& src, const int16_t* W, int N, int K, const Epi&
 // decode attention over the KV cache (attention.rs:42-90), GQA (model.rs:508-511)
 // ---------------------------------------------------------------------------
 
-// scores[h][j] for the G query heads of KV head g, positions j of one chunk of
-// kChunk positions.  LPP = HD/8 lanes read one 16-byte slice each of a K row
-// (a wave reads whole rows: coalesced); every K load of the wave is issued
-// before the first dot product.  q . k is exact: q = 256*hi + lo with
-// v_dot2_i32_i16 on (k, hi) and (k, lo) (|partials| < 2^31 per 16-lane group).
+// Launch shape shared by the two attention kernels: grid
+// dim3(8 * G, ceil(chunks / 8), kv_heads), 256 threads; block (x, y, z) works
+// on query head x >> 3 of KV head z and on position chunk y * 8 + (x & 7).
+// Workgroups are dispatched to the 8 XCDs round robin in linear-id order (x
+// fastest, and gridDim.x is a multiple of 8), so the G head blocks of one
+// chunk run on one XCD and share its L2 copy of the K or V rows.
+struct AttnBlock {
+    int h, c, g;
+    __device__ AttnBlock() : h((int)blockIdx.x >> 3), c((int)blockIdx.y * 8 + ((int)blockIdx.x & 7)), g((int)blockIdx.z) {}
+};
+
+// int16 pairs -> (hi pair, lo pair) with v = 256 * hi + lo, lo in [0, 255].
+__device__ inline void split_pair(uint32_t v, uint32_t& hi, uint32_t& lo) {
+    const int32_t a = (int16_t)(v & 0xFFFFu), b = (int16_t)(v >> 16);
+    hi = ((uint32_t)(uint16_t)(int16_t)(a >> 8)) | ((uint32_t)(uint16_t)(int16_t)(b >> 8) << 16);
+    lo = (v & 0x00FF00FFu);
+}
+
+// s_j = (i32)RNE(q . k_j * mult, shift) for one query head and kChunk
+// positions (attention.rs:66-67).  LPP = HD / 8 lanes hold 16 bytes of a K
+// row each (a wave reads whole rows, coalesced); q . k is exact as
+// 256 * sum(k * q_hi) + sum(k * q_lo) on v_dot2_i32_i16 (|partials| < 2^31),
+// the row sums over the LPP lanes are DPP moves.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_scores_kernel(const DecodeState* __restrict__ st,
                                                          const int16_t* __restrict__ q, const int16_t* __restrict__ kc,
-                                                         int max_pos, int G, int64_t score_mult, uint8_t score_shift,
-                                                         int32_t* __restrict__ scores) {
+                                                         int max_pos, int G, int chunks, int64_t score_mult,
+                                                         uint8_t score_shift, int32_t* __restrict__ scores) {
     constexpr int LPP = HD / 8;
     constexpr int PPW = 64 / LPP;                 // positions per wave per step
     constexpr int STEPS = kChunk / 4 / PPW;       // steps per wave
+    static_assert(LPP == 8 || LPP == 16, "row sums cover 8 or 16 lanes");
+    const AttnBlock b;
+    if (b.c >= chunks) return;
     const int L = st->pos + 1;
-    const int g = blockIdx.y;
-    const int base = blockIdx.x * kChunk;
+    const int base = b.c * kChunk;
     if (base >= L) return;
-    __shared__ __align__(16) int16_t qhi[kMaxGroup][HD];
-    __shared__ __align__(16) int16_t qlo[kMaxGroup][HD];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane % LPP, slot = lane / LPP;
-    const int16_t* kg = kc + (size_t)g * max_pos * HD;
+    const int16_t* kg = kc + (size_t)b.g * max_pos * HD;
     uint4 kv[STEPS];
 #pragma unroll
     for (int it = 0; it < STEPS; ++it) {
         const int j = base + wave * (kChunk / 4) + it * PPW + slot;
         kv[it] = j < L ? *reinterpret_cast<const uint4*>(kg + (size_t)j * HD + sub * 8) : make_uint4(0, 0, 0, 0);
     }
-    for (int i = threadIdx.x; i < G * HD; i += blockDim.x) {
-        const int h = i / HD, d = i - h * HD;  // HD is a compile-time power of two
-        const int16_t v = q[(size_t)(g * G + h) * HD + d];
-        qhi[h][d] = (int16_t)(v >> 8);
-        qlo[h][d] = (int16_t)(v & 255);
-    }
-    __syncthreads();
+    const int head = b.g * G + b.h;
+    const uint4 qv = *reinterpret_cast<const uint4*>(q + (size_t)head * HD + sub * 8);
+    uint4 qh, ql;
+    split_pair(qv.x, qh.x, ql.x);
+    split_pair(qv.y, qh.y, ql.y);
+    split_pair(qv.z, qh.z, ql.z);
+    split_pair(qv.w, qh.w, ql.w);
     typedef short __attribute__((ext_vector_type(2))) s2;
-    for (int h = 0; h < G; ++h) {
-        const uint4 qh = *reinterpret_cast<const uint4*>(&qhi[h][sub * 8]);
-        const uint4 ql = *reinterpret_cast<const uint4*>(&qlo[h][sub * 8]);
+    auto d2 = [](uint32_t a, uint32_t c, int32_t acc) {
+        return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, a), __builtin_bit_cast(s2, c), acc, false);
+    };
 #pragma unroll
-        for (int it = 0; it < STEPS; ++it) {
-            const int j = base + wave * (kChunk / 4) + it * PPW + slot;
-            int32_t ahi = 0, alo = 0;
-            ahi = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv[it].x), __builtin_bit_cast(s2, qh.x), ahi, false);
-            ahi = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv[it].y), __builtin_bit_cast(s2, qh.y), ahi, false);
-            ahi = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv[it].z), __builtin_bit_cast(s2, qh.z), ahi, false);
-            ahi = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv[it].w), __builtin_bit_cast(s2, qh.w), ahi, false);
-            alo = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv[it].x), __builtin_bit_cast(s2, ql.x), alo, false);
-            alo = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv[it].y), __builtin_bit_cast(s2, ql.y), alo, false);
-            alo = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv[it].z), __builtin_bit_cast(s2, ql.z), alo, false);
-            alo = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, kv[it].w), __builtin_bit_cast(s2, ql.w), alo, false);
-#pragma unroll
-            for (int off = LPP / 2; off > 0; off >>= 1) {
-                ahi += __shfl_xor(ahi, off, 64);
-                alo += __shfl_xor(alo, off, 64);
-            }
-            if (sub == 0 && j < L) {
-                const int64_t dot = (int64_t)ahi * 256 + (int64_t)alo;
-                scores[(size_t)(g * G + h) * max_pos + j] =
-                    (int32_t)rshift_round64(wmul64(dot, score_mult), score_shift);
-            }
-        }
-    }
-}
-
-// Per query head: max score, sum of exp-LUT values (wrapping i32, like the
-// reference's i32 sum) and the reciprocal of the divisor.  1024 threads, each
-// holding up to kStatPer scores in registers across both reductions.
-constexpr int kStatThreads = 1024;
-constexpr int kStatPer = 4;
-__global__ __launch_bounds__(kStatThreads) void attn_stats_kernel(const DecodeState* __restrict__ st,
-                                                                 const int32_t* __restrict__ scores, int max_pos,
-                                                                 const int16_t* __restrict__ lut, uint32_t lut_len,
-                                                                 uint8_t lut_shift, AttnStat* __restrict__ stats) {
-    __shared__ int32_t red32[kStatThreads / 64];
-    __shared__ uint32_t redu[kStatThreads / 64];
-    const int L = st->pos + 1;
-    const int32_t* z = scores + (size_t)blockIdx.x * max_pos;
-    const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
-    const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
-    int32_t mx = INT32_MIN;
-    uint32_t s = 0;
-    if (L <= kStatThreads * kStatPer) {
-        int32_t zz[kStatPer];
-#pragma unroll
-        for (int t = 0; t < kStatPer; ++t) {
-            const int j = threadIdx.x + t * kStatThreads;
-            zz[t] = j < L ? z[j] : INT32_MIN;
-        }
-#pragma unroll
-        for (int t = 0; t < kStatPer; ++t) mx = max(mx, zz[t]);
-        mx = block_max_i32(mx, red32);
-#pragma unroll
-        for (int t = 0; t < kStatPer; ++t)
-            if (threadIdx.x + t * kStatThreads < L) s += (uint32_t)exp_lookup(sat_sub32(mx, zz[t]), lut, lut_len, lut_shift, lut_one);
-    } else {
-        for (int j = threadIdx.x; j < L; j += blockDim.x) mx = max(mx, z[j]);
-        mx = block_max_i32(mx, red32);
-        for (int j = threadIdx.x; j < L; j += blockDim.x)
-            s += (uint32_t)exp_lookup(sat_sub32(mx, z[j]), lut, lut_len, lut_shift, lut_one);
-    }
-    const int32_t S = (int32_t)block_sum_u32(s, redu);
-    if (threadIdx.x == 0) {
-        AttnStat a;
-        a.m = mx;
-        a.S = S;
-        a.base = 0;
-        a.rem = 0;
-        if (S == 0) {
-            uint32_t qq, rr;
-            a.recip = recip32((uint32_t)L);
-            udivmod32((uint32_t)one, (uint32_t)L, a.recip, &qq, &rr);
-            a.base = (int32_t)qq;
-            a.rem = wsub32(one, wmul32(a.base, L));
+    for (int it = 0; it < STEPS; ++it) {
+        const int j = base + wave * (kChunk / 4) + it * PPW + slot;
+        int32_t ahi = 0, alo = 0;
+        ahi = d2(kv[it].x, qh.x, ahi);
+        ahi = d2(kv[it].y, qh.y, ahi);
+        ahi = d2(kv[it].z, qh.z, ahi);
+        ahi = d2(kv[it].w, qh.w, ahi);
+        alo = d2(kv[it].x, ql.x, alo);
+        alo = d2(kv[it].y, ql.y, alo);
+        alo = d2(kv[it].z, ql.z, alo);
+        alo = d2(kv[it].w, ql.w, alo);
+        if (LPP == 16) {
+            ahi = row_sum16_i32(ahi);
+            alo = row_sum16_i32(alo);
         } else {
-            a.recip = recip32(S < 0 ? 0u - (uint32_t)S : (uint32_t)S);
+            ahi = row_sum8_i32(ahi);
+            alo = row_sum8_i32(alo);
         }
-        stats[blockIdx.x] = a;
+        if (sub == 0 && j < L) {
+            const int64_t dot = (int64_t)ahi * 256 + (int64_t)alo;
+            scores[(size_t)head * max_pos + j] = (int32_t)rshift_round64(wmul64(dot, score_mult), score_shift);
+        }
     }
 }
 
-// Probabilities of one chunk and their products with V, for the G heads of KV
-// head g, added exactly (64-bit integer atomics: any order gives the same sum)
-// into acc[h * HD + d].
+// Softmax of one query head (softmax.rs:12-64) and the exact partial P.V of
+// one chunk (attention.rs:75-81).  Every block first recomputes its head's
+// statistics over all L scores -- m = max, S = wrapping i32 sum of the exp
+// LUT, the reciprocal of |S| -- then p_j = RNE(e_j * 2^14 / S) (or the
+// uniform split when S == 0) for its chunk, then sum_j p_j v_j per dimension
+// in i64, added to the accumulator with 64-bit atomics (exact, order-free).
 template <int HD>
 __global__ __launch_bounds__(256) void attn_pv_kernel(const DecodeState* __restrict__ st,
-                                                     const int32_t* __restrict__ scores, const AttnStat* __restrict__ stats,
-                                                     const int16_t* __restrict__ vc, int max_pos, int G,
-                                                     const int16_t* __restrict__ lut, uint32_t lut_len, uint8_t lut_shift,
-                                                     unsigned long long* __restrict__ acc) {
+                                                     const int32_t* __restrict__ scores,
+                                                     const int16_t* __restrict__ vc, int max_pos, int G, int chunks,
+                                                     const int16_t* __restrict__ lut, uint32_t lut_len,
+                                                     uint8_t lut_shift, unsigned long long* __restrict__ acc) {
     constexpr int TPR = HD / 2;           // threads per V row (one dim pair each)
     constexpr int STREAMS = 256 / TPR;    // position streams per block
     constexpr int PER = kChunk / STREAMS; // positions per stream
+    constexpr int ZPER = 16;              // scores held in registers per thread
+    const AttnBlock b;
+    if (b.c >= chunks) return;
     const int L = st->pos + 1;
-    const int g = blockIdx.y;
-    const int base = blockIdx.x * kChunk;
+    const int base = b.c * kChunk;
     if (base >= L) return;
     const int n = min(kChunk, L - base);
-    __shared__ int32_t p[kMaxGroup][kChunk];
+    const int head = b.g * G + b.h;
+    __shared__ int32_t p[kChunk];
     __shared__ int64_t red[STREAMS][HD];
+    __shared__ int32_t redm[4];
+    __shared__ uint32_t reds[4];
     const int dp = threadIdx.x % TPR, stream = threadIdx.x / TPR;
-    const int16_t* vg = vc + (size_t)g * max_pos * HD;
+    const int16_t* vg = vc + (size_t)b.g * max_pos * HD;
     uint32_t vv[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int t = stream + i * STREAMS;
         vv[i] = t < n ? *reinterpret_cast<const uint32_t*>(vg + (size_t)(base + t) * HD + 2 * dp) : 0u;
     }
+    const int32_t* z = scores + (size_t)head * max_pos;
     const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
     const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
-    for (int i = threadIdx.x; i < G * kChunk; i += blockDim.x) {
-        const int h = i >> kChunkLog, t = i & (kChunk - 1);
+    int32_t mx = INT32_MIN;
+    uint32_t s = 0;
+    if (L <= 256 * ZPER) {
+        int32_t zz[ZPER];
+#pragma unroll
+        for (int t = 0; t < ZPER; ++t) {
+            const int j = threadIdx.x + t * 256;
+            zz[t] = j < L ? z[j] : INT32_MIN;
+        }
+#pragma unroll
+        for (int t = 0; t < ZPER; ++t) mx = max(mx, zz[t]);
+        mx = block_max_i32_dpp(mx, redm);
+#pragma unroll
+        for (int t = 0; t < ZPER; ++t)
+            if (threadIdx.x + t * 256 < L) s += (uint32_t)exp_lookup(sat_sub32(mx, zz[t]), lut, lut_len, lut_shift, lut_one);
+    } else {
+        for (int j = threadIdx.x; j < L; j += 256) mx = max(mx, z[j]);
+        mx = block_max_i32_dpp(mx, redm);
+        for (int j = threadIdx.x; j < L; j += 256)
+            s += (uint32_t)exp_lookup(sat_sub32(mx, z[j]), lut, lut_len, lut_shift, lut_one);
+    }
+    const int32_t S = (int32_t)block_sum_u32_dpp(s, reds);
+    if (threadIdx.x < kChunk) {
+        const int t = threadIdx.x;
         int32_t pv = 0;
         if (t < n) {
-            const AttnStat a = stats[g * G + h];
-            if (a.S == 0) {
-                pv = a.base + (((uint64_t)(base + t) < (uint64_t)(int64_t)a.rem) ? 1 : 0);
+            if (S == 0) {
+                const uint64_t rl = recip32((uint32_t)L);
+                uint32_t qq, rr;
+                udivmod32((uint32_t)one, (uint32_t)L, rl, &qq, &rr);
+                const int32_t ubase = (int32_t)qq;
+                const int32_t urem = wsub32(one, wmul32(ubase, L));
+                pv = ubase + (((uint64_t)(base + t) < (uint64_t)(int64_t)urem) ? 1 : 0);
             } else {
-                const int32_t z = scores[(size_t)(g * G + h) * max_pos + base + t];
-                const int32_t e = exp_lookup(sat_sub32(a.m, z), lut, lut_len, lut_shift, lut_one);
-                pv = softmax_div_round(wmul32(e, one), a.S, a.recip);
+                const uint64_t rs = recip32(S < 0 ? 0u - (uint32_t)S : (uint32_t)S);
+                const int32_t e = exp_lookup(sat_sub32(mx, z[base + t]), lut, lut_len, lut_shift, lut_one);
+                pv = softmax_div_round(wmul32(e, one), S, rs);
             }
         }
-        p[h][t] = pv;
+        p[t] = pv;
     }
     __syncthreads();
-    for (int h = 0; h < G; ++h) {
-        int64_t a0 = 0, a1 = 0;
+    int64_t a0 = 0, a1 = 0;
 #pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int64_t pv = p[h][stream + i * STREAMS];
-            a0 = wadd64(a0, pv * (int64_t)(int16_t)(vv[i] & 0xFFFFu));
-            a1 = wadd64(a1, pv * (int64_t)(int16_t)(vv[i] >> 16));
-        }
-        red[stream][2 * dp] = a0;
-        red[stream][2 * dp + 1] = a1;
-        __syncthreads();
-        if (threadIdx.x < HD) {
-            int64_t sum = 0;
+    for (int i = 0; i < PER; ++i) {
+        const int64_t pv = p[stream + i * STREAMS];
+        a0 = wadd64(a0, pv * (int64_t)(int16_t)(vv[i] & 0xFFFFu));
+        a1 = wadd64(a1, pv * (int64_t)(int16_t)(vv[i] >> 16));
+    }
+    red[stream][2 * dp] = a0;
+    red[stream][2 * dp + 1] = a1;
+    __syncthreads();
+    if (threadIdx.x < HD) {
+        int64_t sum = 0;
 #pragma unroll
-            for (int k = 0; k < STREAMS; ++k) sum = wadd64(sum, red[k][threadIdx.x]);
-            atomicAdd(acc + (size_t)(g * G + h) * HD + threadIdx.x, (unsigned long long)sum);
-        }
-        __syncthreads();
+        for (int k = 0; k < STREAMS; ++k) sum = wadd64(sum, red[k][threadIdx.x]);
+        atomicAdd(acc + (size_t)head * HD + threadIdx.x, (unsigned long long)sum);
     }
 }
 
@@ -783,7 +770,6 @@ struct myl_model {
     int16_t *hidden = nullptr, *norm = nullptr, *q = nullptr, *attn = nullptr, *resid = nullptr, *h = nullptr;
     int32_t* logits = nullptr;
     int32_t* scores = nullptr;
-    AttnStat* stats = nullptr;
     unsigned long long* attn_acc = nullptr;  // [nq] exact P.V sums, cleared after each use
     NormAcc* norm_a = nullptr;               // input-norm / final-norm sums of squares
     NormAcc* norm_b = nullptr;               // post-attention-norm sums of squares
@@ -1091,13 +1077,12 @@ int build(myl_model* m, const myl_luts* luts) {
     m->h = m->dalloc<int16_t>(I);
     m->logits = m->dalloc<int32_t>(V);
     m->scores = m->dalloc<int32_t>((size_t)s.heads * m->max_pos);
-    m->stats = m->dalloc<AttnStat>(s.heads);
     m->attn_acc = m->dalloc<unsigned long long>((size_t)nq);
     m->norm_a = m->dalloc<NormAcc>(1);
     m->norm_b = m->dalloc<NormAcc>(1);
     m->state = m->dalloc<DecodeState>(1);
     if (!m->kcache || !m->vcache || !m->hidden || !m->norm || !m->q || !m->attn || !m->resid || !m->h ||
-        !m->logits || !m->scores || !m->stats || !m->attn_acc || !m->state || !m->norm_a || !m->norm_b)
+        !m->logits || !m->scores || !m->attn_acc || !m->state || !m->norm_a || !m->norm_b)
         return c->fail(MYL_E_NOMEM, "activation allocation");
     if (hipMemsetAsync(m->kcache, 0, kv * 2, c->stream) != hipSuccess ||
         hipMemsetAsync(m->vcache, 0, kv * 2, c->stream) != hipSuccess ||
@@ -1116,7 +1101,7 @@ RmsParams rms_params(const myl_model* m) {
 // One transformer layer on m->hidden (model.rs:401-674); the result replaces
 // m->hidden and its input-norm sum is left in norm_a for the next consumer.
 //   qkv   : RMSNorm(hidden) staged from norm_a            -> q, KV cache
-//   attn  : scores, stats, P.V into attn_acc
+//   attn  : scores, then softmax + P.V into attn_acc
 //   o     : attn_acc staged, residual 1 -> resid; sum -> norm_b; clears norm_a
 //   gu    : RMSNorm(resid) staged from norm_b             -> h; clears attn_acc
 //   down  : h, residual 2 -> hidden; sum -> norm_a; clears norm_b
@@ -1135,7 +1120,7 @@ hipError_t layer_step(myl_model* m, int l) {
         SrcNorm src{m->hidden, L.res_in, L.in_gamma, L.in_gamma_s, rp, L.ref_in, f.norm_attn_frac, m->norm_a};
         {
             TimedScope t(m, K_QKV);
-            e = stream_i8<2, 4, 4>(src, L.wqkv, nq + 2 * nkv, H, q, st, cus);
+            e = stream_i8<2, 2, 4>(src, L.wqkv, nq + 2 * nkv, H, q, st, cus);
         }
         if (e != hipSuccess) return e;
         TimedScope ta(m, K_ATTN);
@@ -1145,23 +1130,17 @@ hipError_t layer_step(myl_model* m, int l) {
         const int chunks = (m->max_pos + kChunk - 1) / kChunk;
         const int16_t* kc = m->kcache + layer_kv;
         const int16_t* vc = m->vcache + layer_kv;
+        const dim3 agrid(8 * G, (chunks + 7) / 8, kvh);
         if (hd == 128) {
-            attn_scores_kernel<128><<<dim3(chunks, kvh), 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, m->score_mult,
-                                                                     score_shift, m->scores);
+            attn_scores_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, chunks, m->score_mult,
+                                                          score_shift, m->scores);
+            attn_pv_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, G, chunks, m->exp_lut,
+                                                      (uint32_t)m->exp_len, lut_shift, m->attn_acc);
         } else {
-            attn_scores_kernel<64><<<dim3(chunks, kvh), 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, m->score_mult,
-                                                                    score_shift, m->scores);
-        }
-        attn_stats_kernel<<<m->spec.heads, kStatThreads, 0, st>>>(m->state, m->scores, m->max_pos, m->exp_lut,
-                                                                  (uint32_t)m->exp_len, lut_shift, m->stats);
-        if (hd == 128) {
-            attn_pv_kernel<128><<<dim3(chunks, kvh), 256, 0, st>>>(m->state, m->scores, m->stats, vc, m->max_pos, G,
-                                                                 m->exp_lut, (uint32_t)m->exp_len, lut_shift,
-                                                                 m->attn_acc);
-        } else {
-            attn_pv_kernel<64><<<dim3(chunks, kvh), 256, 0, st>>>(m->state, m->scores, m->stats, vc, m->max_pos, G,
-                                                                m->exp_lut, (uint32_t)m->exp_len, lut_shift,
-                                                                m->attn_acc);
+            attn_scores_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, chunks, m->score_mult,
+                                                         score_shift, m->scores);
+            attn_pv_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, G, chunks, m->exp_lut,
+                                                     (uint32_t)m->exp_len, lut_shift, m->attn_acc);
         }
         e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -1171,7 +1150,7 @@ hipError_t layer_step(myl_model* m, int l) {
         SrcAttn src{m->attn_acc, f.v_frac, f.attn_out_frac};
         EpiResid o{L.so, f.attn_out_frac, L.acc_attn, L.res_in, L.res_mid, m->hidden, m->resid, m->norm_b, L.ref_mid,
                    m->norm_a};
-        e = stream_i8<1, 4, 4>(src, L.wo, H, nq, o, st, cus);
+        e = stream_i8<1, 2, 8>(src, L.wo, H, nq, o, st, cus);
         if (e != hipSuccess) return e;
     }
     {
@@ -1187,7 +1166,7 @@ hipError_t layer_step(myl_model* m, int l) {
         SrcPlain src{m->h};
         EpiResid d{L.sd, f.down_in_frac, L.acc_mlp, L.res_mid, L.res_out, m->resid, m->hidden, m->norm_a, L.ref_out,
                    m->norm_b};
-        e = stream_i8<1, 4, 4>(src, L.wd, H, I, d, st, cus);
+        e = stream_i8<1, 4, 16>(src, L.wd, H, I, d, st, cus);
     }
     return e;
 }
@@ -1302,7 +1281,6 @@ int myl_model_create_synthetic(myl_ctx* ctx, const myl_synth_spec* spec, const m
         return ctx->fail(MYL_E_INVALID, "model: heads must divide evenly into KV heads and tile hidden");
     if (s.head_dim != 64 && s.head_dim != 128)
         return ctx->fail(MYL_E_UNSUPPORTED, "model: the fused decode path takes head_dim 64 or 128");
-    if (s.heads / s.kv_heads > kMaxGroup) return ctx->fail(MYL_E_UNSUPPORTED, "model: more than 8 query heads per KV head");
     if (s.hidden % 16 || s.inter % 16) return ctx->fail(MYL_E_UNSUPPORTED, "model: hidden and intermediate must be multiples of 16");
     if (!luts->rsqrt || luts->rsqrt_len < 2 || !luts->silu || !luts->silu_len || !luts->exp || !luts->cos ||
         !luts->sin || luts->rope_len < s.head_dim / 2)
