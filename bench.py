@@ -13,9 +13,11 @@ the timed region is `--steps` consecutive device-chained greedy steps.
 Also reported:
   roofline     the dominant decode kernel (the fused gate/up W8A16 GEMV),
                timed with HIP events around its launches in the same run;
-  gemv         the W8A16 sweep at M = 1 with multiplier requant, over
+  w8a16_sweep  the isolated W8A16 matmul sweep, M in {1, 8, 64, 512} x the
+               four (N, K) shapes, multiplier requant; M <= 8 streams over
                rotating weight copies (> 512 MB distinct) so the 256 MB
-               Infinity Cache cannot serve repeats;
+               Infinity Cache cannot serve repeats, M >= 64 runs on the int8
+               matrix cores and reports TOP/s;
   cpu_baseline the CPU oracle (a single-thread restatement of the reference's
                scalar Rust path) on a bounded sample of the same workload, on
                this host's cores, after checking its logits equal the GPU's.
@@ -69,35 +71,44 @@ def class_bytes(spec: dict) -> dict:
     }
 
 
-def gemv_sweep(backend, shapes, reps_target_bytes=6 << 30):
-    """M = 1 W8A16 GEMV with multiplier requant; bytes = N*K + 2K + 2N + 5N."""
+def w8a16_sweep(backend, shapes, ms=(1, 8, 64, 512), target_bytes=6 << 30, target_ops=4e12):
+    """The isolated W8A16 matmul sweep with multiplier requant: y = clamp16(RNE(W.x * mult, shift)).
+    Algorithmic bytes N*K + 2MK + 2MN + 5N (i32 mult + u8 shift), ops 2MNK.
+    At M = 1 the launches rotate over >= 512 MB of distinct weight copies so
+    the 256 MB Infinity Cache cannot serve repeats; larger M are MFMA-bound
+    and reuse one copy."""
     import torch
     out = {}
     g = torch.Generator(device="cuda")
     g.manual_seed(1234)
     for (N, K) in shapes:
         per = N * K
-        copies = max(2, -(-(512 << 20) // per))  # >= 512 MB of distinct weights
+        copies = max(2, -(-(512 << 20) // per))
         Ws = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g) for _ in range(copies)]
-        x = torch.randint(-32767, 32768, (1, K), dtype=torch.int16, device="cuda", generator=g)
         mult = torch.randint(1 << 29, (1 << 30) + 1, (N,), dtype=torch.int32, device="cuda", generator=g)
         sh = torch.randint(20, 41, (N,), dtype=torch.uint8, device="cuda", generator=g)
-        y = torch.empty((1, N), dtype=torch.int16, device="cuda")
-        for W in Ws:  # warm-up
-            backend.linear_w8a16_mult_dev(x, W, mult, sh, out=y)
-        launches = max(copies, int(reps_target_bytes // per) // copies * copies)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for i in range(launches):
-            backend.linear_w8a16_mult_dev(x, Ws[i % copies], mult, sh, out=y)
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / launches
-        nbytes = N * K + 2 * K + 2 * N + 5 * N
-        out[f"M1_N{N}_K{K}"] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                                "bytes": nbytes, "launches": launches, "distinct_weight_MB": round(copies * per / 2**20)}
-        log(f"gemv N={N} K={K}: {ms * 1e3:.2f} us, {nbytes / (ms * 1e-3) / 1e9:.0f} GB/s")
+        for M in ms:
+            x = torch.clamp(torch.round(torch.randn((M, K), device="cuda", generator=g) * 2000), -32767, 32767).to(torch.int16)
+            y = torch.empty((M, N), dtype=torch.int16, device="cuda")
+            nc = copies if M <= 8 else 1
+            for W in Ws[:nc]:  # warm-up
+                backend.linear_w8a16_mult_dev(x, W, mult, sh, out=y)
+            launches = max(nc, int(min(target_bytes // per, target_ops // (2 * M * per))) // nc * nc)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(launches):
+                backend.linear_w8a16_mult_dev(x, Ws[i % nc], mult, sh, out=y)
+            e1.record()
+            torch.cuda.synchronize()
+            ms_ = e0.elapsed_time(e1) / launches
+            nbytes = per + 2 * M * K + 2 * M * N + 5 * N
+            rec = {"us": round(ms_ * 1e3, 2), "GBps": round(nbytes / (ms_ * 1e-3) / 1e9, 1),
+                   "TOPs": round(2 * M * per / (ms_ * 1e-3) / 1e12, 1), "bytes": nbytes, "launches": launches,
+                   "distinct_weight_MB": round(nc * per / 2**20)}
+            out[f"M{M}_N{N}_K{K}"] = rec
+            log(f"w8a16 M={M} N={N} K={K}: {rec['us']} us, {rec['GBps']} GB/s, {rec['TOPs']} TOP/s")
+            del x, y
         del Ws
         torch.cuda.empty_cache()
     return out
@@ -220,11 +231,11 @@ def main() -> int:
 
     gemv = {}
     if not args.no_gemv:
-        gemv = gemv_sweep(backend, [(3584, 3584), (18944, 3584), (3584, 18944), (152064, 3584)])
+        gemv = w8a16_sweep(backend, [(3584, 3584), (18944, 3584), (3584, 18944), (152064, 3584)])
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(spec, model, [int(t) for t in prompt[:4]], 3)
+        cpu = cpu_baseline(spec, model, [int(t) for t in prompt[:4]], 12)
 
     step_bytes = 28 * (cb["qkv"] + cb["o_proj"] + cb["gate_up"] + cb["down"]) + cb["lm_head"]
     kv_bytes = 2 * spec["layers"] * spec["kv_heads"] * spec["head_dim"] * 2 * (pos + args.steps // 2)
@@ -251,7 +262,7 @@ def main() -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": cb[dom], "avg_us": per_class[dom]["avg_us"]},
         "kernel_classes": per_class,
-        "gemv": gemv,
+        "w8a16_sweep": gemv,
         "cpu_baseline": cpu,
         "gpu": torch.cuda.get_device_name(0),
     }

@@ -40,6 +40,29 @@ void* myl_ctx::scratch(size_t bytes) {
     return scratch_ptr;
 }
 
+// Products with more outputs than this never split K (their tiles alone fill
+// the chip), so the accumulator stays at most 32 MiB.
+static constexpr size_t kMmAccCap = (size_t)4 << 20;
+
+const myl::MmCtx* myl_ctx::mm_ctx(size_t elems) {
+    mm.cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1;
+    if (elems > mm.acc_elems && elems <= kMmAccCap) {
+        (void)hipStreamSynchronize(stream);
+        if (mm.acc) (void)hipFree(mm.acc);
+        mm.acc = nullptr;
+        mm.acc_elems = 0;
+        void* p = nullptr;
+        if (hipMalloc(&p, elems * 8) != hipSuccess) return nullptr;
+        if (hipMemset(p, 0, elems * 8) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+            (void)hipFree(p);
+            return nullptr;
+        }
+        mm.acc = (unsigned long long*)p;
+        mm.acc_elems = elems;
+    }
+    return &mm;
+}
+
 extern "C" {
 
 const char* myl_backend_name(void) { return "rocm"; }
@@ -69,6 +92,7 @@ void myl_destroy(myl_ctx* ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->scratch_ptr) (void)hipFree(ctx->scratch_ptr);
+    if (ctx->mm.acc) (void)hipFree(ctx->mm.acc);
     (void)hipStreamSynchronize(ctx->own_stream);
     (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
@@ -378,8 +402,9 @@ int myl_linear_w8a16_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, c
     if (!ctx) return MYL_E_INVALID;
     int rc = check_gemv(ctx, M, ldx, N, K, ldo, "linear_w8a16_dev");
     if (rc || M == 0 || N == 0) return rc;
+    const MmCtx* mm = ctx->mm_ctx(M > 8 ? M * N : 0);
     return ctx->hip(linear_w8a16(x, (int)M, (int)ldx, W, (int)N, (int)K, w_shifts, act_frac, out_frac, out_frac_pc,
-                                 out, (int)ldo, ctx->stream), "linear_w8a16_dev");
+                                 out, (int)ldo, ctx->stream, mm), "linear_w8a16_dev");
 }
 
 int myl_linear_w8a16_mult_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, const int8_t* W, size_t N,
@@ -387,8 +412,9 @@ int myl_linear_w8a16_mult_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t l
     if (!ctx) return MYL_E_INVALID;
     int rc = check_gemv(ctx, M, ldx, N, K, ldo, "linear_w8a16_mult_dev");
     if (rc || M == 0 || N == 0) return rc;
-    return ctx->hip(linear_w8a16_mult(x, (int)M, (int)ldx, W, (int)N, (int)K, mult, shift, out, (int)ldo, ctx->stream),
-                    "linear_w8a16_mult_dev");
+    const MmCtx* mm = ctx->mm_ctx(M > 8 ? M * N : 0);
+    return ctx->hip(linear_w8a16_mult(x, (int)M, (int)ldx, W, (int)N, (int)K, mult, shift, out, (int)ldo, ctx->stream,
+                                      mm), "linear_w8a16_mult_dev");
 }
 
 int myl_logits_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, const void* W, int w_bits, size_t N,
@@ -397,12 +423,13 @@ int myl_logits_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, const v
     if (!ctx) return MYL_E_INVALID;
     int rc = check_gemv(ctx, M, ldx, N, K, ldo, "logits_dev");
     if (rc || M == 0 || N == 0) return rc;
+    const MmCtx* mm = ctx->mm_ctx(M > 8 ? M * N : 0);
     if (w_bits == 8)
         return ctx->hip(logits_w8(x, (int)M, (int)ldx, (const int8_t*)W, (int)N, (int)K, row_shifts, norm_frac,
-                                  logit_frac, out, (int)ldo, ctx->stream), "logits_dev");
+                                  logit_frac, out, (int)ldo, ctx->stream, mm), "logits_dev");
     if (w_bits == 16)
         return ctx->hip(logits_w16(x, (int)M, (int)ldx, (const int16_t*)W, (int)N, (int)K, row_shifts, norm_frac,
-                                   logit_frac, out, (int)ldo, ctx->stream), "logits_dev");
+                                   logit_frac, out, (int)ldo, ctx->stream, mm), "logits_dev");
     return ctx->fail(MYL_E_INVALID, "logits_dev: w_bits must be 8 or 16");
 }
 
@@ -411,7 +438,9 @@ int myl_dot_i8_i16_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, con
     if (!ctx) return MYL_E_INVALID;
     int rc = check_gemv(ctx, M, ldx, N, K, ldo, "dot_i8_i16_dev");
     if (rc || M == 0 || N == 0) return rc;
-    return ctx->hip(dot_raw_w8(x, (int)M, (int)ldx, W, (int)N, (int)K, out, (int)ldo, ctx->stream), "dot_i8_i16_dev");
+    const MmCtx* mm = ctx->mm_ctx(M > 8 ? M * N : 0);
+    return ctx->hip(dot_raw_w8(x, (int)M, (int)ldx, W, (int)N, (int)K, out, (int)ldo, ctx->stream, mm),
+                    "dot_i8_i16_dev");
 }
 
 int myl_rmsnorm_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, const uint8_t* x_shifts,

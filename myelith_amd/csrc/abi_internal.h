@@ -16,9 +16,13 @@ struct myl_ctx {
     std::string err;
     void* scratch_ptr = nullptr;
     size_t scratch_bytes = 0;
+    myl::MmCtx mm{};                   // split-K accumulator of the matrix-core path
 
     int fail(int code, const std::string& msg);
     int hip(hipError_t e, const char* what);
     // Grow-only device scratch for host-slice staging (valid until the next call).
     void* scratch(size_t bytes);
+    // The matrix-core launch context with an all-zero accumulator of at least
+    // `elems` entries (grown on demand; nullptr only when allocation fails).
+    const myl::MmCtx* mm_ctx(size_t elems);
 };

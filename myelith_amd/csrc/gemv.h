@@ -11,7 +11,7 @@
 //   sum w*x = 256*sum(w*hi) + sum(w*lo') + 128*sum(w)
 // and each of the three sums is a chain of v_dot4_i32_i8 (4 int8 MACs per
 // instruction).  Per lane and in total each partial is bounded by
-// 127*128*K < 2^31 for K <= 131072, so the i32 partials are exact and are
+// 128*128*K < 2^31 for K < 131072, so the i32 partials are exact and are
 // widened to i64 only once, after the cross-lane reduction.
 //
 // int16 weights (LM head, model.rs:285-296): x = 256*hi + lo with lo in

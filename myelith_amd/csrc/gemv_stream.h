@@ -136,7 +136,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i8_stream(Src src, const int8
             }
         }
     };
-    // The three partial sums are exact in i32 over the whole row (K <= 131072),
+    // The three partial sums are exact in i32 over the whole row (K < 131072),
     // so each is reduced in i32 and widened once.
     int cnt = 0;
     auto finish_group = [&]() {

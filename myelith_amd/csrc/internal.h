@@ -7,18 +7,33 @@
 
 namespace myl {
 
+// Matrix-core (M > 8) launch context: the device's CU count and an i64
+// split-K accumulator of acc_elems entries that is all zeros between calls
+// (the split-K epilogue clears what it reads).  acc may be null: the
+// products then run without K splitting.
+struct MmCtx {
+    unsigned long long* acc = nullptr;
+    size_t acc_elems = 0;
+    int cus = 256;
+};
+
 // y[m][r] = clamp_i16(rescale_i64(W[r].x[m], w_shifts[r] + act_frac, out_frac_pc ? out_frac_pc[r] : out_frac))
 hipError_t linear_w8a16(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, const uint8_t* w_shifts,
                         uint8_t act_frac, uint8_t out_frac, const uint8_t* out_frac_pc, int16_t* out, int ldo,
-                        hipStream_t st);
+                        hipStream_t st,
+                        const MmCtx* mm = nullptr);
 hipError_t linear_w8a16_mult(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, const int32_t* mult,
-                             const uint8_t* shift, int16_t* out, int ldo, hipStream_t st);
+                             const uint8_t* shift, int16_t* out, int ldo, hipStream_t st,
+                        const MmCtx* mm = nullptr);
 hipError_t logits_w8(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, const uint8_t* row_shifts,
-                     uint8_t norm_frac, uint8_t logit_frac, int32_t* out, int ldo, hipStream_t st);
+                     uint8_t norm_frac, uint8_t logit_frac, int32_t* out, int ldo, hipStream_t st,
+                        const MmCtx* mm = nullptr);
 hipError_t logits_w16(const int16_t* x, int M, int ldx, const int16_t* W, int N, int K, const uint8_t* row_shifts,
-                      uint8_t norm_frac, uint8_t logit_frac, int32_t* out, int ldo, hipStream_t st);
+                      uint8_t norm_frac, uint8_t logit_frac, int32_t* out, int ldo, hipStream_t st,
+                        const MmCtx* mm = nullptr);
 hipError_t dot_raw_w8(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, int64_t* out, int ldo,
-                      hipStream_t st);
+                      hipStream_t st,
+                        const MmCtx* mm = nullptr);
 hipError_t rmsnorm(const int16_t* x, int M, int ldx, const uint8_t* xs, const int8_t* g, const uint8_t* gs, int n,
                    const int16_t* lut, int lut_len, uint8_t lut_input_shift, uint8_t lut_output_frac,
                    int64_t inv_n_q20, uint8_t out_frac, int16_t* out, int ldo, hipStream_t st);

@@ -517,8 +517,8 @@ constexpr size_t kStreamLdsMax = 64 * 1024;
 
 template <int R, int U, int WAVES, class Src, class Epi>
 hipError_t stream_i8(const Src& src, const int8_t* W, int N, int K, const Epi& e, hipStream_t s, int cus) {
-    // one buffer descriptor; i32 partial sums exact for K <= 131072
-    if ((uint64_t)N * (uint64_t)K > 0xFFFFFF00ull || K > 131072 || N < 1 || K < 1) return hipErrorInvalidValue;
+    // one buffer descriptor; i32 partial sums exact for K < 131072
+    if ((uint64_t)N * (uint64_t)K > 0xFFFFFF00ull || K >= 131072 || N < 1 || K < 1) return hipErrorInvalidValue;
     auto kern = gemv_i8_stream<R, U, WAVES, Src, Epi>;
     int gpw = 0;
     const int grid = stream_grid(kern, WAVES, stream_lds_bytes(K, 1, WAVES, kGpwReserve, R), (N + R - 1) / R, cus, &gpw);

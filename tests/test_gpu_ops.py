@@ -100,7 +100,7 @@ SWEEP = [(3584, 3584), (18944, 3584), (3584, 18944), (152064, 3584)]
 
 
 @pytest.mark.parametrize("N,K", SWEEP)
-@pytest.mark.parametrize("M", [1, 8, 64])
+@pytest.mark.parametrize("M", [1, 8, 64, 512])
 def test_w8a16_sweep_shapes_dev(backend, oracle, M, N, K):
     """The W8A16 sweep shapes (M x N x K), shift requant and multiplier requant."""
     import torch
@@ -125,6 +125,82 @@ def test_w8a16_sweep_shapes_dev(backend, oracle, M, N, K):
     s2 = (ws.astype(np.int32) + 11 - 10 + k).astype(np.uint8)
     got = backend.linear_w8a16_mult_dev(xd, Wd, torch.from_numpy(m2).cuda(), torch.from_numpy(s2).cuda())
     assert np.array_equal(got.cpu().numpy(), oracle.linear_batch(x, W, ws, 11, 10))
+
+
+# ---- matrix-core path (M > 8): every tile shape, with and without K splits ----------
+
+MM_CASES = [(9, 37, 48), (33, 100, 208), (64, 130, 3584), (130, 257, 1040), (300, 64, 18944), (17, 5, 16)]
+
+
+@pytest.mark.parametrize("tile", [0, 1, 2, 3])
+@pytest.mark.parametrize("ksplit", [1, 3])
+def test_mfma_tiles_and_splits(backend, oracle, monkeypatch, tile, ksplit):
+    """Odd M/N/K (partial tiles, K tails of 16 bytes) through each forced tile
+    shape and K split, against the oracle; shift and multiplier requant."""
+    import torch
+    monkeypatch.setenv("MYL_MM_TILE", str(tile))
+    monkeypatch.setenv("MYL_MM_KSPLIT", str(ksplit))
+    oracle.lib().or_set_threads(16)
+    for M, N, K in MM_CASES:
+        case(f"mfma tile={tile} ksplit={ksplit} M={M} N={N} K={K}")
+        r = rng(M * 31 + N * 7 + K + tile)
+        x = gauss16(r, M * K).reshape(M, K)
+        x[0, :4] = (-32768, 32767, -1, 0)
+        W = r.integers(-128, 128, (N, K)).astype(np.int8)
+        ws = r.integers(8, 14, N).astype(np.uint8)
+        xd, Wd = torch.from_numpy(x).cuda(), torch.from_numpy(W).cuda()
+        got = backend.linear_w8a16_dev(xd, Wd, torch.from_numpy(ws).cuda(), 11, 10).cpu().numpy()
+        assert np.array_equal(got, oracle.linear_batch(x, W, ws, 11, 10)), (M, N, K)
+        mult = r.integers(1 << 29, (1 << 30) + 1, N).astype(np.int32)
+        sh = r.integers(20, 41, N).astype(np.uint8)
+        got = backend.linear_w8a16_mult_dev(xd, Wd, torch.from_numpy(mult).cuda(), torch.from_numpy(sh).cuda())
+        assert np.array_equal(got.cpu().numpy(), oracle.linear_mult(x, W, mult, sh)), (M, N, K)
+        raw = backend.dot_i8_i16_dev(xd, Wd).cpu().numpy()
+        assert np.array_equal(raw, x.astype(np.int64) @ W.astype(np.int64).T), (M, N, K)
+
+
+def test_mfma_extremes(backend):
+    """All-extreme operands: every partial sum at its bound (K = 18944)."""
+    import torch
+    case("mfma extremes")
+    K = 18944
+    x = np.full((16, K), -32768, np.int16)
+    x[1] = 32767
+    x[2, ::2] = -32768
+    x[2, 1::2] = 32767
+    x[3] = -1
+    W = np.full((40, K), -128, np.int8)
+    W[1] = 127
+    W[2, ::2] = -128
+    W[2, 1::2] = 127
+    got = backend.dot_i8_i16_dev(torch.from_numpy(x).cuda(), torch.from_numpy(W).cuda()).cpu().numpy()
+    assert np.array_equal(got, x.astype(np.int64) @ W.astype(np.int64).T)
+
+
+@pytest.mark.parametrize("M", [64, 512])
+@pytest.mark.parametrize("N,K", SWEEP)
+def test_mfma_full_size_exact_sums(backend, M, N, K):
+    """Full sweep sizes: the exact i64 sums equal a float64 matmul on the GPU
+    (every partial sum is an integer below 2^53, so float64 is exact), and
+    the shift-requant output equals the requant of those sums."""
+    import torch
+    case(f"mfma full size M={M} N={N} K={K}")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(M + N + K)
+    x = torch.randint(-32768, 32768, (M, K), dtype=torch.int16, device="cuda", generator=g)
+    W = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g)
+    raw = backend.dot_i8_i16_dev(x, W)
+    ref = (x.double() @ W.double().T).to(torch.int64)
+    assert torch.equal(raw, ref)
+    del ref
+    # the requant epilogue on the same sums: rows 0..255 against the oracle's rescale
+    from oracle import binding as ob
+    ws = torch.randint(8, 14, (N,), dtype=torch.uint8, device="cuda", generator=g)
+    y = backend.linear_w8a16_dev(x, W, ws, 11, 10)
+    r = raw[:, :256].cpu().numpy()
+    wsn = ws[:256].cpu().numpy()
+    exp = np.vectorize(lambda a, s: max(-32768, min(32767, ob.rescale_i64(int(a), int(s) + 11, 10))))(r, wsn[None, :])
+    assert np.array_equal(y[:, :256].cpu().numpy(), exp.astype(np.int16))
 
 
 @pytest.mark.parametrize("bits", [8, 16])
