@@ -163,6 +163,17 @@ int myl_softmax_dev(myl_ctx* ctx, const int32_t* logits, size_t M, size_t n, siz
 /* M rows of argmax_int (sampling.rs:8-18). */
 int myl_argmax_dev(myl_ctx* ctx, const int32_t* values, size_t M, size_t n, size_t ldv, int64_t* out_index);
 
+/* Integer log-softmax at a target token per row (no reference counterpart:
+ * the reference evaluates perplexity in f64, runtime/src/bin/perplexity_probe.rs:55-67).
+ * For logits z (Q6, model.rs:284-308) and target t:
+ *   m = max z;  S = sum_j exp_lut[(m - z_j) << 2] (0 past the table);
+ *   out = (z_t - m) * 2^10 - ln_q16(S)   (Q16, int64)
+ * where ln_q16(S) = RNE((((e - 14) << 16) + f) * 744261118, 30) with
+ * e = floor(log2 S) and f the first 16 fraction bits of log2(S / 2^e) by
+ * repeated squaring of the Q62 mantissa.  targets[m] < 0 gives 0. */
+int myl_logsoftmax_dev(myl_ctx* ctx, const int32_t* logits, size_t M, size_t n, size_t ldz, const int16_t* exp_lut,
+                       size_t lut_len, const int64_t* targets, int64_t* out);
+
 /* ======================================================================
  * 3. Device-resident model (runtime/src/model.rs, kv_cache.rs)
  * ==================================================================== */
@@ -209,6 +220,33 @@ int myl_model_read_kv(myl_model* m, uint32_t layer, uint32_t kv_head, uint32_t n
 /* Device copy of a named weight tensor (the synthetic generator's output),
  * for verification; same names as the oracle's tensor table. */
 int myl_model_read_tensor(myl_model* m, const char* name, uint32_t layer, void* host_out, size_t bytes);
+
+/* ---- batched forward: rows of (sequence, position, token) -------------------
+ * Generalises the prompt loop of generate.rs:28-32 to many sequences with
+ * their own KV caches; row r computes what IntegerModel::forward_token
+ * (model.rs:229-311) computes for token[r] at pos[r] on sequence seq[r]. */
+
+/* Allocates KV caches for n_seqs sequences (max_pos positions each, separate
+ * from the single-sequence cache) and empties them. */
+int myl_model_batch_begin(myl_model* m, uint32_t n_seqs);
+/* One forward over n_rows rows.  Per sequence the rows' positions must be
+ * distinct, contiguous and start at or before its cached length (a re-run
+ * position overwrites, as KVCache::write does).  logits (host, n_rows x vocab)
+ * and argmax_out (host, n_rows; first maximum, sampling.rs:8-18) may be NULL. */
+int myl_model_forward_batch(myl_model* m, uint32_t n_rows, const uint32_t* seq, const uint32_t* pos,
+                            const uint32_t* tokens, int32_t* logits, int64_t* argmax_out);
+/* Device pointer of the last batch's logits ([n_rows x vocab] int32), valid
+ * until the next batched call. */
+int myl_model_batch_logits_dev(myl_model* m, const int32_t** logits_dev);
+/* Greedy decode of n_rows sequences in lock step (generate.rs:38-50 per
+ * sequence): step 0 consumes tokens[r] at pos[r], step i the argmax of step
+ * i-1 at pos[r] + i.  tokens_out (host, n_steps x n_rows) gets the argmax of
+ * every step. */
+int myl_model_batch_decode_greedy(myl_model* m, uint32_t n_rows, const uint32_t* seq, const uint32_t* pos,
+                                  const uint32_t* tokens, uint32_t n_steps, int64_t* tokens_out);
+/* KVCache::read (kv_cache.rs:43-52) of one batch sequence. */
+int myl_model_batch_read_kv(myl_model* m, uint32_t seq, uint32_t layer, uint32_t kv_head, uint32_t n_pos,
+                            int16_t* k_out, int16_t* v_out);
 
 #ifdef __cplusplus
 }

@@ -64,6 +64,7 @@ SIGNATURES: dict[str, tuple] = {
     "myl_rmsnorm_dev": (INT, [P, P, sz, sz, P, P, P, sz, P, sz, u8, u8, i64, u8, P, sz]),
     "myl_softmax_dev": (INT, [P, P, sz, sz, sz, P, sz, u8, u8, P, sz]),
     "myl_argmax_dev": (INT, [P, P, sz, sz, sz, P]),
+    "myl_logsoftmax_dev": (INT, [P, P, sz, sz, sz, P, sz, P, P]),
     "myl_model_create_synthetic": (INT, [P, C.POINTER(SynthSpec), C.POINTER(Luts), C.POINTER(P)]),
     "myl_model_destroy": (None, [P]),
     "myl_model_reset": (INT, [P]),
@@ -77,6 +78,11 @@ SIGNATURES: dict[str, tuple] = {
     "myl_model_head_logits": (INT, [P, P, P]),
     "myl_model_read_kv": (INT, [P, u32, u32, u32, P, P]),
     "myl_model_read_tensor": (INT, [P, C.c_char_p, u32, P, sz]),
+    "myl_model_batch_begin": (INT, [P, u32]),
+    "myl_model_forward_batch": (INT, [P, u32, P, P, P, P, P]),
+    "myl_model_batch_logits_dev": (INT, [P, C.POINTER(P)]),
+    "myl_model_batch_decode_greedy": (INT, [P, u32, P, P, P, u32, P]),
+    "myl_model_batch_read_kv": (INT, [P, u32, u32, u32, u32, P, P]),
 }
 
 _lib = None

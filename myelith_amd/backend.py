@@ -269,3 +269,18 @@ class RocmBackend:
             out = torch.empty(M, dtype=torch.int64, device=v.device)
         self.check(lib().myl_argmax_dev(self._h, v.data_ptr(), M, n, v.stride(0), out.data_ptr()), "argmax_dev")
         return out
+
+    def logsoftmax_dev(self, z, exp_lut, targets, out=None):
+        """Integer log-softmax at targets[m] per row, Q16 int64 (build-defined;
+        the reference's perplexity probe uses f64, perplexity_probe.rs:55-67)."""
+        import torch
+        M, n = z.shape
+        lut = exp_lut if isinstance(exp_lut, torch.Tensor) else torch.from_numpy(
+            np.ascontiguousarray(exp_lut, dtype=np.int16)).to(z.device)
+        t = targets if isinstance(targets, torch.Tensor) else torch.as_tensor(
+            np.asarray(targets, dtype=np.int64), device=z.device)
+        if out is None:
+            out = torch.empty(M, dtype=torch.int64, device=z.device)
+        self.check(lib().myl_logsoftmax_dev(self._h, z.data_ptr(), M, n, z.stride(0), lut.data_ptr(), lut.numel(),
+                                            t.data_ptr(), out.data_ptr()), "logsoftmax_dev")
+        return out

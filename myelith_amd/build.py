@@ -27,6 +27,7 @@ DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-p
 SOURCES = {  # source -> is HIP device code
     "kernels.hip": True,
     "model.hip": True,
+    "batch.hip": True,
     "abi.cpp": False,
 }
 

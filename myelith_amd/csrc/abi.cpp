@@ -477,4 +477,15 @@ int myl_argmax_dev(myl_ctx* ctx, const int32_t* values, size_t M, size_t n, size
     return ctx->hip(argmax(values, (int)M, (int)n, (int)ldv, out_index, ctx->stream), "argmax_dev");
 }
 
+int myl_logsoftmax_dev(myl_ctx* ctx, const int32_t* logits, size_t M, size_t n, size_t ldz, const int16_t* exp_lut,
+                       size_t lut_len, const int64_t* targets, int64_t* out) {
+    if (!ctx) return MYL_E_INVALID;
+    if (n == 0) return ctx->fail(MYL_E_INVALID, "logsoftmax_dev: empty rows");
+    if (ldz < n || !fits_int(M) || !fits_int(n) || !fits_int(ldz) || !fits_int(lut_len))
+        return ctx->fail(MYL_E_INVALID, "logsoftmax_dev: bad shape");
+    if (M == 0) return MYL_OK;
+    return ctx->hip(logsoftmax(logits, (int)M, (int)n, (int)ldz, exp_lut, (int)lut_len, targets, out, ctx->stream),
+                    "logsoftmax_dev");
+}
+
 }  // extern "C"

@@ -1,0 +1,739 @@
+// batch.hip -- the batched forward of the device-resident model: R rows, each
+// one (sequence, position, token), through all layers at once.
+//
+// The reference has no batching: prefill is a loop of forward_token calls
+// (INTEGER_LLM/runtime/src/generate.rs:28-32) and each sequence owns a KV
+// cache (runtime/src/kv_cache.rs).  Row r of a batch computes exactly what
+// forward_token(token[r], pos[r]) computes on sequence seq[r]'s cache, because
+// every op is per token except attention, and attention for position p reads
+// only cached positions <= p (kv_cache.rs:43-52): the K/V rows of all rows of
+// a batch are appended before any row attends.  One batch therefore serves
+// teacher-forced prefill (many positions of few sequences, the projections on
+// the int8 matrix cores) and batched decode (one position of many sequences).
+//
+// Per layer (model.rs:401-674):
+//   rmsnorm          X -> Xn                                  (rmsnorm.rs:61-161)
+//   q/k/v product    Xn -> QKV, requant + bias                (linear.rs:43-70,132-145)
+//   rope_scatter     RoPE on q/k pairs, q -> Q, k/v -> caches (rope.rs:17-31, model.rs:458-503)
+//   attention        scores, softmax statistics, P.V          (attention.rs:42-90, softmax.rs:12-64)
+//   o_proj           A -> X2 with residual 1                  (model.rs:563-593)
+//   rmsnorm          X2 -> Xn
+//   gate/up product  Xn -> GU; SiLU gating GU -> Hh           (mlp.rs:28-65)
+//   down_proj        Hh -> X with residual 2                  (mlp.rs:66-74, model.rs:612-671)
+// then the final norm, the LM head over every row (model.rs:264-308) and a
+// first-maximum argmax per row (sampling.rs:8-18).
+#include "gemm_dispatch.h"
+#include "model_internal.h"
+#include "ops.h"
+#include "wave.h"
+
+#include <algorithm>
+#include <cstring>
+#include <string>
+#include <vector>
+
+using namespace myl;
+
+namespace myl {
+
+struct BatchState {
+    int n_seqs = 0;
+    std::vector<uint32_t> len;           // cached positions per sequence
+    int16_t* kc = nullptr;               // [seq][layer][kv_head][max_pos][head_dim]
+    int16_t* vc = nullptr;
+    int rows_cap = 0, lmax_cap = 0;
+    int32_t* rows = nullptr;             // [4][rows_cap]: seq, pos, rope row, token
+    int16_t *X = nullptr, *Xn = nullptr, *X2 = nullptr, *QKV = nullptr, *Q = nullptr, *A = nullptr;
+    int16_t *GU = nullptr, *Hh = nullptr;
+    int32_t* logits = nullptr;           // [rows_cap][V]
+    int64_t* argmax = nullptr;           // [rows_cap]
+    int64_t* tokens_out = nullptr;       // greedy chains: [steps][rows]
+    size_t tokens_out_cap = 0;
+    int32_t* scores = nullptr;           // [rows_cap][heads][lmax_cap]
+    int32_t* stats = nullptr;            // [rows_cap][heads][2]: max, wrapping exp sum
+    unsigned long long* pv = nullptr;    // [rows_cap][nq], zero between uses
+    std::vector<void*> allocs_rows;      // row buffers (regrown together)
+    std::vector<void*> allocs_scores;
+};
+
+void batch_free(BatchState* b) {
+    if (!b) return;
+    for (void* p : b->allocs_rows) (void)hipFree(p);
+    for (void* p : b->allocs_scores) (void)hipFree(p);
+    if (b->kc) (void)hipFree(b->kc);
+    if (b->vc) (void)hipFree(b->vc);
+    if (b->tokens_out) (void)hipFree(b->tokens_out);
+    delete b;
+}
+
+}  // namespace myl
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// epilogues (one per product; see gemm_dispatch.h for the interface)
+// ---------------------------------------------------------------------------
+
+template <class D>
+struct EpiApply {
+    template <int R, int MT>
+    __device__ inline void apply(int row0, int N, int M, int lane, const int64_t (&tot)[R][MT]) const {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                if (lane == r * MT + m && row0 + r < N && m < M)
+                    static_cast<const D*>(this)->one(row0 + r, m, tot[r][m]);
+    }
+};
+
+// q/k/v rows (pair-ordered within each head): requant to the segment's frac,
+// then the bias (linear.rs:132-145).
+struct EpiQKVRows : EpiApply<EpiQKVRows> {
+    const uint8_t* shifts;
+    const int16_t* bias;      // or null
+    const uint8_t* bias_sh;
+    uint8_t act_frac, q_frac, k_frac, v_frac;
+    int nq, nkv;
+    int16_t* out; int ldo;
+    EpiQKVRows offset_m(int m0) const { EpiQKVRows e = *this; e.out += (size_t)m0 * ldo; return e; }
+    __device__ inline void one(int n, int m, int64_t acc) const {
+        const uint8_t frac = n < nq ? q_frac : (n < nq + nkv ? k_frac : v_frac);
+        int16_t v = clamp_i16_i64(rescale64(acc, (uint8_t)(shifts[n] + act_frac), frac));
+        if (bias) v = clamp_i16_i64((int64_t)v + (int64_t)rescale32((int32_t)bias[n], bias_sh[n], frac));
+        out[(size_t)m * ldo + n] = v;
+    }
+};
+
+// o_proj / down_proj with the residual add (model.rs:576-593, 612-671):
+// o = clamp(rescale(acc, w_shift + act, acc_frac)), h = rescale(res, res_frac,
+// acc_frac), out = clamp(rescale(h + o, acc_frac, out_frac)).
+struct EpiResidRows : EpiApply<EpiResidRows> {
+    const uint8_t* shifts;
+    uint8_t act_frac;
+    const uint8_t* acc_frac;
+    const uint8_t* res_frac;
+    const uint8_t* out_frac;
+    const int16_t* res; int ldr;
+    int16_t* out; int ldo;
+    EpiResidRows offset_m(int m0) const {
+        EpiResidRows e = *this;
+        e.res += (size_t)m0 * ldr;
+        e.out += (size_t)m0 * ldo;
+        return e;
+    }
+    __device__ inline void one(int n, int m, int64_t acc) const {
+        const uint8_t af = acc_frac[n];
+        const int16_t o = clamp_i16_i64(rescale64(acc, (uint8_t)(shifts[n] + act_frac), af));
+        const int64_t h = rescale64((int64_t)res[(size_t)m * ldr + n], res_frac[n], af);
+        out[(size_t)m * ldo + n] = clamp_i16_i64(rescale64(wadd64(h, (int64_t)o), af, out_frac[n]));
+    }
+};
+
+// gate (even rows) and up (odd rows) requantized to their own fracs (mlp.rs:46-53).
+struct EpiGURows : EpiApply<EpiGURows> {
+    const uint8_t* shifts;
+    uint8_t act_frac, gate_frac, up_frac;
+    int16_t* out; int ldo;
+    EpiGURows offset_m(int m0) const { EpiGURows e = *this; e.out += (size_t)m0 * ldo; return e; }
+    __device__ inline void one(int n, int m, int64_t acc) const {
+        const uint8_t frac = (n & 1) ? up_frac : gate_frac;
+        out[(size_t)m * ldo + n] = clamp_i16_i64(rescale64(acc, (uint8_t)(shifts[n] + act_frac), frac));
+    }
+};
+
+// ---------------------------------------------------------------------------
+// row kernels
+// ---------------------------------------------------------------------------
+
+// model.rs:241-248 per row.
+__global__ __launch_bounds__(256) void embed_rows_kernel(const int32_t* __restrict__ tok, const int8_t* __restrict__ E,
+                                                         const uint8_t* __restrict__ emb_shifts,
+                                                         const uint8_t* __restrict__ res_frac0, int H,
+                                                         int16_t* __restrict__ X) {
+    const int r = blockIdx.x;
+    const int t = tok[r];
+    const int8_t* row = E + (size_t)t * H;
+    const uint8_t sh = emb_shifts[t];
+    for (int i = threadIdx.x; i < H; i += blockDim.x)
+        X[(size_t)r * H + i] = clamp_i16(rescale32((int32_t)row[i], sh, res_frac0[i]));
+}
+
+// RoPE of the q/k pairs (rope.rs:17-31, LUT row pos % rows, model.rs:469-473),
+// q to Q [R x nq] in head-major order, k (post-RoPE) and v to the sequence's
+// cache at its position (model.rs:481-503).  Grid (ceil(pairs / 256), R).
+__global__ __launch_bounds__(256) void rope_scatter_kernel(const int16_t* __restrict__ qkv, int ldq, const int32_t* __restrict__ rows,
+                                                           int rows_cap, int nq, int nkv, int hd_log,
+                                                           const int16_t* __restrict__ cos_lut,
+                                                           const int16_t* __restrict__ sin_lut, int16_t* __restrict__ Q,
+                                                           int16_t* __restrict__ kc, int16_t* __restrict__ vc,
+                                                           size_t seq_stride, int kvh, int max_pos) {
+    const int r = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int npairs = (nq + 2 * nkv) >> 1;
+    if (i >= npairs) return;
+    const int n0 = 2 * i;
+    const int seg = n0 < nq ? 0 : (n0 < nq + nkv ? 1 : 2);
+    const int e = n0 - (seg == 0 ? 0 : (seg == 1 ? nq : nq + nkv));
+    const int hd = 1 << hd_log, half = hd >> 1;
+    const int head = e >> hd_log;
+    const int p = (e & (hd - 1)) >> 1;
+    int16_t y0 = qkv[(size_t)r * ldq + n0], y1 = qkv[(size_t)r * ldq + n0 + 1];
+    const int seq = rows[r], pos = rows[rows_cap + r], rope_row = rows[2 * rows_cap + r];
+    if (seg < 2) {
+        const int32_t c = cos_lut[(size_t)rope_row * half + p];
+        const int32_t s = sin_lut[(size_t)rope_row * half + p];
+        const int32_t x0 = y0, x1 = y1;
+        y0 = clamp_i16(rshift_round32(wsub32(wmul32(x0, c), wmul32(x1, s)), MYL_TV_ROPE_FRAC_BITS));
+        y1 = clamp_i16(rshift_round32(wadd32(wmul32(x1, c), wmul32(x0, s)), MYL_TV_ROPE_FRAC_BITS));
+    }
+    int16_t* dst;
+    if (seg == 0) dst = Q + (size_t)r * nq + (size_t)head * hd;
+    else dst = (seg == 1 ? kc : vc) + (size_t)seq * seq_stride + ((size_t)head * max_pos + pos) * hd;
+    dst[p] = y0;
+    dst[p + half] = y1;
+}
+
+// int16 pairs -> (hi pair, lo pair) with v = 256 * hi + lo, lo in [0, 255].
+__device__ inline void split_pair16(uint32_t v, uint32_t& hi, uint32_t& lo) {
+    const int32_t a = (int16_t)(v & 0xFFFFu), b = (int16_t)(v >> 16);
+    hi = ((uint32_t)(uint16_t)(int16_t)(a >> 8)) | ((uint32_t)(uint16_t)(int16_t)(b >> 8) << 16);
+    lo = (v & 0x00FF00FFu);
+}
+
+constexpr int kRowChunk = 64;  // positions per attention block
+
+// s_j = (i32)RNE(q . k_j * mult, shift) (attention.rs:66-67) for the G query
+// heads of KV head g, row r, positions j of chunk c.  Grid (chunks, kvh, R).
+// LPP = HD / 8 lanes read one K row (16 bytes each); q . k is exact as
+// 256 * sum(k * q_hi) + sum(k * q_lo) on v_dot2_i32_i16.
+template <int HD>
+__global__ __launch_bounds__(256) void rows_scores_kernel(const int32_t* __restrict__ rows, int rows_cap,
+                                                          const int16_t* __restrict__ Q, int nq,
+                                                          const int16_t* __restrict__ kc, size_t seq_stride,
+                                                          int max_pos, int G, int64_t score_mult, uint8_t score_shift,
+                                                          int32_t* __restrict__ scores, int heads, int lcap) {
+    constexpr int LPP = HD / 8;
+    constexpr int PPP = 256 / LPP;             // positions per pass
+    constexpr int PASSES = kRowChunk / PPP;
+    const int c = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
+    const int seq = rows[r], L = rows[rows_cap + r] + 1;
+    const int base = c * kRowChunk;
+    if (base >= L) return;
+    const int sub = threadIdx.x % LPP, slot = threadIdx.x / LPP;
+    const int16_t* kg = kc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD;
+    typedef short __attribute__((ext_vector_type(2))) s2;
+    auto d2 = [](uint32_t a, uint32_t b, int32_t acc) {
+        return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, a), __builtin_bit_cast(s2, b), acc, false);
+    };
+    uint4 kv[PASSES];
+#pragma unroll
+    for (int it = 0; it < PASSES; ++it) {
+        const int j = base + it * PPP + slot;
+        kv[it] = j < L ? *reinterpret_cast<const uint4*>(kg + (size_t)j * HD + sub * 8) : make_uint4(0, 0, 0, 0);
+    }
+    for (int h = 0; h < G; ++h) {
+        const int head = g * G + h;
+        const uint4 qv = *reinterpret_cast<const uint4*>(Q + (size_t)r * nq + (size_t)head * HD + sub * 8);
+        uint4 qh, ql;
+        split_pair16(qv.x, qh.x, ql.x);
+        split_pair16(qv.y, qh.y, ql.y);
+        split_pair16(qv.z, qh.z, ql.z);
+        split_pair16(qv.w, qh.w, ql.w);
+        int32_t* srow = scores + ((size_t)r * heads + head) * lcap;
+#pragma unroll
+        for (int it = 0; it < PASSES; ++it) {
+            const int j = base + it * PPP + slot;
+            int32_t ahi = 0, alo = 0;
+            ahi = d2(kv[it].x, qh.x, ahi);
+            ahi = d2(kv[it].y, qh.y, ahi);
+            ahi = d2(kv[it].z, qh.z, ahi);
+            ahi = d2(kv[it].w, qh.w, ahi);
+            alo = d2(kv[it].x, ql.x, alo);
+            alo = d2(kv[it].y, ql.y, alo);
+            alo = d2(kv[it].z, ql.z, alo);
+            alo = d2(kv[it].w, ql.w, alo);
+            if (LPP == 16) {
+                ahi = row_sum16_i32(ahi);
+                alo = row_sum16_i32(alo);
+            } else {
+                ahi = row_sum8_i32(ahi);
+                alo = row_sum8_i32(alo);
+            }
+            if (sub == 0 && j < L) {
+                const int64_t dot = (int64_t)ahi * 256 + (int64_t)alo;
+                srow[j] = (int32_t)rshift_round64(wmul64(dot, score_mult), score_shift);
+            }
+        }
+    }
+}
+
+// Softmax statistics of one (row, head) over its L scores (softmax.rs:32-41):
+// m = max, S = wrapping i32 sum of the exp LUT values.  Grid (heads, R).
+__global__ __launch_bounds__(256) void rows_stats_kernel(const int32_t* __restrict__ rows, int rows_cap,
+                                                         const int32_t* __restrict__ scores, int heads, int lcap,
+                                                         const int16_t* __restrict__ lut, uint32_t lut_len,
+                                                         uint8_t lut_shift, int32_t* __restrict__ stats) {
+    __shared__ int32_t redm[4];
+    __shared__ uint32_t reds[4];
+    const int h = blockIdx.x, r = blockIdx.y;
+    const int L = rows[rows_cap + r] + 1;
+    const int32_t* z = scores + ((size_t)r * heads + h) * lcap;
+    const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
+    int32_t mx = INT32_MIN;
+    for (int j = threadIdx.x; j < L; j += 256) mx = max(mx, z[j]);
+    mx = block_max_i32_dpp(mx, redm);
+    uint32_t s = 0;
+    for (int j = threadIdx.x; j < L; j += 256) s += (uint32_t)exp_lookup(sat_sub32(mx, z[j]), lut, lut_len, lut_shift, lut_one);
+    const uint32_t S = block_sum_u32_dpp(s, reds);
+    if (threadIdx.x == 0) {
+        stats[((size_t)r * heads + h) * 2] = mx;
+        stats[((size_t)r * heads + h) * 2 + 1] = (int32_t)S;
+    }
+}
+
+// p_j = RNE(e_j * 2^14 / S) (or the uniform split when S == 0, softmax.rs:42-63)
+// for the G heads of KV head g and the positions of chunk c, then the exact
+// partial P.V per dimension (attention.rs:75-81) added into pv with 64-bit
+// atomics.  Grid (chunks, kvh, R).
+template <int HD>
+__global__ __launch_bounds__(256) void rows_pv_kernel(const int32_t* __restrict__ rows, int rows_cap,
+                                                      const int32_t* __restrict__ scores,
+                                                      const int32_t* __restrict__ stats, int heads, int lcap,
+                                                      const int16_t* __restrict__ vc, size_t seq_stride, int max_pos,
+                                                      int G, const int16_t* __restrict__ lut, uint32_t lut_len,
+                                                      uint8_t lut_shift, unsigned long long* __restrict__ pv, int nq) {
+    constexpr int TPR = HD / 2;             // threads per V row (one dimension pair each)
+    constexpr int STREAMS = 256 / TPR;      // position streams
+    constexpr int PER = kRowChunk / STREAMS;
+    constexpr int GMAX = 16;
+    __shared__ int32_t p[GMAX][kRowChunk];
+    __shared__ int64_t red[STREAMS][HD];
+    const int c = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
+    const int seq = rows[r], L = rows[rows_cap + r] + 1;
+    const int base = c * kRowChunk;
+    if (base >= L) return;
+    const int n = min(kRowChunk, L - base);
+    const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
+    const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
+    for (int t = threadIdx.x; t < G * kRowChunk; t += 256) {
+        const int h = t / kRowChunk, j = t % kRowChunk;
+        const int head = g * G + h;
+        int32_t pv_ = 0;
+        if (j < n) {
+            const int32_t mx = stats[((size_t)r * heads + head) * 2];
+            const int32_t S = stats[((size_t)r * heads + head) * 2 + 1];
+            if (S == 0) {
+                const uint64_t rl = recip32((uint32_t)L);
+                uint32_t qq, rr;
+                udivmod32((uint32_t)one, (uint32_t)L, rl, &qq, &rr);
+                const int32_t ubase = (int32_t)qq;
+                const int32_t urem = wsub32(one, wmul32(ubase, L));
+                pv_ = ubase + (((uint64_t)(base + j) < (uint64_t)(int64_t)urem) ? 1 : 0);
+            } else {
+                const uint64_t rs = recip32(S < 0 ? 0u - (uint32_t)S : (uint32_t)S);
+                const int32_t z = scores[((size_t)r * heads + head) * lcap + base + j];
+                const int32_t e = exp_lookup(sat_sub32(mx, z), lut, lut_len, lut_shift, lut_one);
+                pv_ = softmax_div_round(wmul32(e, one), S, rs);
+            }
+        }
+        p[h][j] = pv_;
+    }
+    __syncthreads();
+    const int dp = threadIdx.x % TPR, stream = threadIdx.x / TPR;
+    const int16_t* vg = vc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD;
+    uint32_t vv[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int t = stream + i * STREAMS;
+        vv[i] = t < n ? *reinterpret_cast<const uint32_t*>(vg + (size_t)(base + t) * HD + 2 * dp) : 0u;
+    }
+    for (int h = 0; h < G; ++h) {
+        int64_t a0 = 0, a1 = 0;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int64_t pj = p[h][stream + i * STREAMS];
+            a0 = wadd64(a0, pj * (int64_t)(int16_t)(vv[i] & 0xFFFFu));
+            a1 = wadd64(a1, pj * (int64_t)(int16_t)(vv[i] >> 16));
+        }
+        red[stream][2 * dp] = a0;
+        red[stream][2 * dp + 1] = a1;
+        __syncthreads();
+        if (threadIdx.x < HD) {
+            int64_t sum = 0;
+#pragma unroll
+            for (int k = 0; k < STREAMS; ++k) sum = wadd64(sum, red[k][threadIdx.x]);
+            atomicAdd(pv + (size_t)r * nq + (size_t)(g * G + h) * HD + threadIdx.x, (unsigned long long)sum);
+        }
+        __syncthreads();
+    }
+}
+
+// attention.rs:84-86 then model.rs:563-567; clears pv.  Grid R.
+__global__ __launch_bounds__(256) void rows_attn_out_kernel(unsigned long long* __restrict__ pv, int nq,
+                                                            uint8_t v_frac, uint8_t out_frac, int16_t* __restrict__ A) {
+    const int r = blockIdx.x;
+    for (int i = threadIdx.x; i < nq; i += 256) {
+        unsigned long long* a = pv + (size_t)r * nq + i;
+        const int16_t v = clamp_i16_i64(rshift_round64((int64_t)*a, MYL_TV_PROB_FRAC_BITS));
+        *a = 0;
+        A[(size_t)r * nq + i] = clamp_i16(rescale32((int32_t)v, v_frac, out_frac));
+    }
+}
+
+// mlp.rs:55-65 per row: h = clamp(rescale(silu(g) * u, 8 + up_frac, down_in_frac)).
+__global__ __launch_bounds__(256) void silu_rows_kernel(const int16_t* __restrict__ GU, int I,
+                                                        const int16_t* __restrict__ silu, uint32_t silu_len,
+                                                        uint8_t gate_frac, uint8_t up_frac, uint8_t down_in_frac,
+                                                        int16_t* __restrict__ Hh) {
+    const int r = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= I) return;
+    const uint32_t gu = *reinterpret_cast<const uint32_t*>(GU + (size_t)r * 2 * I + 2 * i);
+    const int16_t g = (int16_t)(gu & 0xFFFFu), u = (int16_t)(gu >> 16);
+    const int32_t g_dom = rescale32((int32_t)g, gate_frac, MYL_TV_SILU_IN_FRAC);
+    const int16_t act = lut_lookup_i16((int16_t)g_dom, silu, silu_len, (int16_t)MYL_TV_SILU_LUT_OFFSET);
+    const int64_t prod = (int64_t)act * (int64_t)u;
+    Hh[(size_t)r * I + i] = clamp_i16_i64(rescale64(prod, (uint8_t)(MYL_TV_SILU_OUT_FRAC + up_frac), down_in_frac));
+}
+
+// Greedy continuation: row r's next token is its argmax; positions advance.
+__global__ void rows_advance_kernel(int32_t* __restrict__ rows, int rows_cap, int R, const int64_t* __restrict__ am,
+                                    uint32_t rope_rows, int64_t* __restrict__ tokens_out) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= R) return;
+    const int64_t t = am[r];
+    rows[3 * rows_cap + r] = (int32_t)t;
+    tokens_out[r] = t;
+    const int pos = rows[rows_cap + r] + 1;
+    rows[rows_cap + r] = pos;
+    rows[2 * rows_cap + r] = (int32_t)umod32_slow((uint32_t)pos, rope_rows);
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+template <class T>
+T* balloc(std::vector<void*>& list, size_t count) {
+    void* p = nullptr;
+    if (hipMalloc(&p, count * sizeof(T) ? count * sizeof(T) : 1) != hipSuccess) return nullptr;
+    list.push_back(p);
+    return (T*)p;
+}
+
+size_t seq_stride(const myl_model* m) {
+    return (size_t)m->spec.layers * m->spec.kv_heads * (size_t)m->max_pos * m->hd;
+}
+
+int ensure_rows(myl_model* m, int R) {
+    BatchState* b = m->batch;
+    if (R <= b->rows_cap) return MYL_OK;
+    myl_ctx* c = m->ctx;
+    (void)hipStreamSynchronize(c->stream);
+    for (void* p : b->allocs_rows) (void)hipFree(p);
+    b->allocs_rows.clear();
+    b->rows_cap = 0;
+    const size_t H = m->H, I = m->I, V = m->V, nq = m->nq, nqkv = m->nq + 2 * m->nkv;
+    auto& L = b->allocs_rows;
+    b->rows = balloc<int32_t>(L, 4 * (size_t)R);
+    b->X = balloc<int16_t>(L, R * H);
+    b->Xn = balloc<int16_t>(L, R * H);
+    b->X2 = balloc<int16_t>(L, R * H);
+    b->QKV = balloc<int16_t>(L, R * nqkv);
+    b->Q = balloc<int16_t>(L, R * nq);
+    b->A = balloc<int16_t>(L, R * nq);
+    b->GU = balloc<int16_t>(L, R * 2 * I);
+    b->Hh = balloc<int16_t>(L, R * I);
+    b->logits = balloc<int32_t>(L, R * V);
+    b->argmax = balloc<int64_t>(L, R);
+    b->stats = balloc<int32_t>(L, (size_t)R * m->spec.heads * 2);
+    b->pv = balloc<unsigned long long>(L, R * nq);
+    for (void* p : L)
+        if (!p) return c->fail(MYL_E_NOMEM, "batch: row buffer allocation");
+    if (hipMemsetAsync(b->pv, 0, R * nq * 8, c->stream) != hipSuccess) return c->fail(MYL_E_HIP, "batch: pv clear");
+    b->rows_cap = R;
+    b->lmax_cap = 0;  // scores are sized by rows too
+    return MYL_OK;
+}
+
+int ensure_scores(myl_model* m, int lmax) {
+    BatchState* b = m->batch;
+    if (lmax <= b->lmax_cap) return MYL_OK;
+    myl_ctx* c = m->ctx;
+    (void)hipStreamSynchronize(c->stream);
+    for (void* p : b->allocs_scores) (void)hipFree(p);
+    b->allocs_scores.clear();
+    b->lmax_cap = 0;
+    const int cap = ((lmax + kRowChunk - 1) / kRowChunk) * kRowChunk;
+    b->scores = balloc<int32_t>(b->allocs_scores, (size_t)b->rows_cap * m->spec.heads * cap);
+    if (!b->scores) return c->fail(MYL_E_NOMEM, "batch: score buffer allocation");
+    b->lmax_cap = cap;
+    return MYL_OK;
+}
+
+// One batched forward over the rows already uploaded to b->rows; lmax is the
+// largest position + 1 among them.
+hipError_t forward_rows(myl_model* m, int R, int lmax) {
+    BatchState* b = m->batch;
+    myl_ctx* c = m->ctx;
+    hipStream_t st = c->stream;
+    const int H = m->H, I = m->I, V = m->V, nq = m->nq, nkv = m->nkv, hd = m->hd, G = m->G;
+    const int nqkv = nq + 2 * nkv, heads = (int)m->spec.heads, kvh = (int)m->spec.kv_heads;
+    const MmCtx* mm = c->mm_ctx((size_t)R * std::max(2 * I, nqkv));
+    const size_t sstride = seq_stride(m);
+    const int chunks = (lmax + kRowChunk - 1) / kRowChunk;
+    const uint8_t lut_shift = MYL_TV_SCORE_FRAC_BITS - MYL_TV_EXP_INPUT_FRAC;
+    hipError_t e;
+    embed_rows_kernel<<<R, 256, 0, st>>>(b->rows + 3 * b->rows_cap, m->emb, m->emb_shifts, m->layers[0].res_in, H, b->X);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    for (int l = 0; l < (int)m->spec.layers; ++l) {
+        const LayerDev& Ld = m->layers[l];
+        const myl_layer_fracs& f = Ld.f;
+        if ((e = rmsnorm(b->X, R, H, Ld.res_in, Ld.in_gamma, Ld.in_gamma_s, H, m->rsqrt, m->rsqrt_len,
+                         MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, f.norm_attn_frac, b->Xn, H,
+                         st)) != hipSuccess)
+            return e;
+        EpiQKVRows eq{};
+        eq.shifts = Ld.sqkv; eq.bias = Ld.bqkv; eq.bias_sh = Ld.bsqkv;
+        eq.act_frac = f.norm_attn_frac; eq.q_frac = f.q_frac; eq.k_frac = f.k_frac; eq.v_frac = f.v_frac;
+        eq.nq = nq; eq.nkv = nkv; eq.out = b->QKV; eq.ldo = nqkv;
+        if ((e = gemv_i8(b->Xn, R, H, Ld.wqkv, nqkv, H, eq, st, mm)) != hipSuccess) return e;
+        int16_t* kc = b->kc + (size_t)l * kvh * m->max_pos * hd;
+        int16_t* vc = b->vc + (size_t)l * kvh * m->max_pos * hd;
+        rope_scatter_kernel<<<dim3((nqkv / 2 + 255) / 256, R), 256, 0, st>>>(
+            b->QKV, nqkv, b->rows, b->rows_cap, nq, nkv, m->hd_log, m->cos_lut, m->sin_lut, b->Q, kc, vc, sstride, kvh,
+            m->max_pos);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        const uint32_t ss = (uint32_t)f.q_frac + f.k_frac + 15u;
+        const uint8_t score_shift = (uint8_t)(ss > MYL_TV_SCORE_FRAC_BITS ? ss - MYL_TV_SCORE_FRAC_BITS : 0);
+        const dim3 ag(chunks, kvh, R);
+        if (hd == 128)
+            rows_scores_kernel<128><<<ag, 256, 0, st>>>(b->rows, b->rows_cap, b->Q, nq, kc, sstride, m->max_pos, G,
+                                                        m->score_mult, score_shift, b->scores, heads, b->lmax_cap);
+        else
+            rows_scores_kernel<64><<<ag, 256, 0, st>>>(b->rows, b->rows_cap, b->Q, nq, kc, sstride, m->max_pos, G,
+                                                       m->score_mult, score_shift, b->scores, heads, b->lmax_cap);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        rows_stats_kernel<<<dim3(heads, R), 256, 0, st>>>(b->rows, b->rows_cap, b->scores, heads, b->lmax_cap,
+                                                          m->exp_lut, (uint32_t)m->exp_len, lut_shift, b->stats);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (hd == 128)
+            rows_pv_kernel<128><<<ag, 256, 0, st>>>(b->rows, b->rows_cap, b->scores, b->stats, heads, b->lmax_cap, vc,
+                                                    sstride, m->max_pos, G, m->exp_lut, (uint32_t)m->exp_len,
+                                                    lut_shift, b->pv, nq);
+        else
+            rows_pv_kernel<64><<<ag, 256, 0, st>>>(b->rows, b->rows_cap, b->scores, b->stats, heads, b->lmax_cap, vc,
+                                                   sstride, m->max_pos, G, m->exp_lut, (uint32_t)m->exp_len,
+                                                   lut_shift, b->pv, nq);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        rows_attn_out_kernel<<<R, 256, 0, st>>>(b->pv, nq, f.v_frac, f.attn_out_frac, b->A);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        EpiResidRows eo{};
+        eo.shifts = Ld.so; eo.act_frac = f.attn_out_frac; eo.acc_frac = Ld.acc_attn; eo.res_frac = Ld.res_in;
+        eo.out_frac = Ld.res_mid; eo.res = b->X; eo.ldr = H; eo.out = b->X2; eo.ldo = H;
+        if ((e = gemv_i8(b->A, R, nq, Ld.wo, H, nq, eo, st, mm)) != hipSuccess) return e;
+        if ((e = rmsnorm(b->X2, R, H, Ld.res_mid, Ld.post_gamma, Ld.post_gamma_s, H, m->rsqrt, m->rsqrt_len,
+                         MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, f.norm_mlp_frac, b->Xn, H,
+                         st)) != hipSuccess)
+            return e;
+        EpiGURows eg{};
+        eg.shifts = Ld.sgu; eg.act_frac = f.norm_mlp_frac; eg.gate_frac = f.gate_frac; eg.up_frac = f.up_frac;
+        eg.out = b->GU; eg.ldo = 2 * I;
+        if ((e = gemv_i8(b->Xn, R, H, Ld.wgu, 2 * I, H, eg, st, mm)) != hipSuccess) return e;
+        silu_rows_kernel<<<dim3((I + 255) / 256, R), 256, 0, st>>>(b->GU, I, m->silu, (uint32_t)m->silu_len,
+                                                                   f.gate_frac, f.up_frac, f.down_in_frac, b->Hh);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        EpiResidRows ed{};
+        ed.shifts = Ld.sd; ed.act_frac = f.down_in_frac; ed.acc_frac = Ld.acc_mlp; ed.res_frac = Ld.res_mid;
+        ed.out_frac = Ld.res_out; ed.res = b->X2; ed.ldr = H; ed.out = b->X; ed.ldo = H;
+        if ((e = gemv_i8(b->Hh, R, I, Ld.wd, H, I, ed, st, mm)) != hipSuccess) return e;
+    }
+    if ((e = rmsnorm(b->X, R, H, m->final_res, m->final_gamma, m->final_gamma_s, H, m->rsqrt, m->rsqrt_len,
+                     MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, m->final_norm_frac, b->Xn, H,
+                     st)) != hipSuccess)
+        return e;
+    if (m->spec.lm_head_int16) {
+        EpiLogits el{m->lm16_shifts, m->final_norm_frac, MYL_TV_LOGIT_FRAC_BITS, b->logits, V};
+        if ((e = gemv_i16(b->Xn, R, H, m->lm16, V, H, el, st)) != hipSuccess) return e;
+    } else {
+        EpiLogits el{m->emb_shifts, m->final_norm_frac, MYL_TV_LOGIT_FRAC_BITS, b->logits, V};
+        if ((e = gemv_i8(b->Xn, R, H, m->emb, V, H, el, st, mm)) != hipSuccess) return e;
+    }
+    return argmax(b->logits, R, V, V, b->argmax, st);
+}
+
+// Checks the rows against the sequences' cached lengths and uploads them.
+// Per sequence the batch's positions must be distinct and fill [p0, p0 + n)
+// with p0 <= cached length (a re-run position overwrites, as KVCache::write
+// does); the cached length becomes max(len, p0 + n).
+int upload_rows(myl_model* m, uint32_t R, const uint32_t* seq, const uint32_t* pos, const uint32_t* tok, int* lmax) {
+    BatchState* b = m->batch;
+    myl_ctx* c = m->ctx;
+    std::vector<std::vector<uint32_t>> per(b->n_seqs);
+    int lm = 0;
+    for (uint32_t r = 0; r < R; ++r) {
+        if (seq[r] >= (uint32_t)b->n_seqs) return c->fail(MYL_E_INVALID, "batch: sequence index out of range");
+        if (pos[r] >= (uint32_t)m->max_pos) return c->fail(MYL_E_INVALID, "batch: position beyond the KV capacity");
+        if (tok[r] >= (uint32_t)m->V) return c->fail(MYL_E_INVALID, "batch: token id out of range");
+        per[seq[r]].push_back(pos[r]);
+        lm = std::max(lm, (int)pos[r] + 1);
+    }
+    std::vector<uint32_t> end(b->n_seqs, 0);
+    for (int s = 0; s < b->n_seqs; ++s) {
+        std::vector<uint32_t>& p = per[s];
+        if (p.empty()) continue;
+        std::sort(p.begin(), p.end());
+        for (size_t i = 1; i < p.size(); ++i)
+            if (p[i] != p[i - 1] + 1)
+                return c->fail(MYL_E_INVALID, "batch: positions of a sequence must be distinct and contiguous");
+        if (p[0] > b->len[s]) return c->fail(MYL_E_INVALID, "batch: positions must continue the sequence's cache");
+        end[s] = p.back() + 1;
+    }
+    int rc = ensure_rows(m, (int)R);
+    if (!rc) rc = ensure_scores(m, lm);
+    if (rc) return rc;
+    std::vector<int32_t> t(4 * (size_t)b->rows_cap, 0);
+    for (uint32_t r = 0; r < R; ++r) {
+        t[r] = (int32_t)seq[r];
+        t[b->rows_cap + r] = (int32_t)pos[r];
+        t[2 * b->rows_cap + r] = (int32_t)(pos[r] % m->rope_rows);
+        t[3 * b->rows_cap + r] = (int32_t)tok[r];
+    }
+    rc = c->hip(hipMemcpyAsync(b->rows, t.data(), t.size() * 4, hipMemcpyHostToDevice, c->stream), "batch rows");
+    if (rc) return rc;
+    // the pageable source must stay alive until the copy has been consumed
+    rc = c->hip(hipStreamSynchronize(c->stream), "batch rows");
+    if (rc) return rc;
+    for (int s = 0; s < b->n_seqs; ++s) b->len[s] = std::max(b->len[s], end[s]);
+    *lmax = lm;
+    return MYL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int myl_model_batch_begin(myl_model* m, uint32_t n_seqs) {
+    if (!m || n_seqs == 0) return MYL_E_INVALID;
+    myl_ctx* c = m->ctx;
+    if (m->G > 16) return c->fail(MYL_E_UNSUPPORTED, "batch: at most 16 query heads per KV head");
+    if (m->batch && m->batch->n_seqs == (int)n_seqs) {
+        std::fill(m->batch->len.begin(), m->batch->len.end(), 0u);
+        return MYL_OK;
+    }
+    (void)hipStreamSynchronize(c->stream);
+    if (m->batch) batch_free(m->batch);
+    m->batch = new (std::nothrow) BatchState();
+    if (!m->batch) return MYL_E_NOMEM;
+    BatchState* b = m->batch;
+    b->n_seqs = (int)n_seqs;
+    b->len.assign(n_seqs, 0u);
+    const size_t bytes = seq_stride(m) * n_seqs * 2;
+    if (hipMalloc(&b->kc, bytes) != hipSuccess || hipMalloc(&b->vc, bytes) != hipSuccess) {
+        batch_free(b);
+        m->batch = nullptr;
+        return c->fail(MYL_E_NOMEM, "batch: KV cache allocation");
+    }
+    if (hipMemsetAsync(b->kc, 0, bytes, c->stream) != hipSuccess || hipMemsetAsync(b->vc, 0, bytes, c->stream) != hipSuccess)
+        return c->fail(MYL_E_HIP, "batch: KV cache clear");
+    return c->hip(hipStreamSynchronize(c->stream), "batch_begin");
+}
+
+int myl_model_forward_batch(myl_model* m, uint32_t n_rows, const uint32_t* seq, const uint32_t* pos,
+                            const uint32_t* tokens, int32_t* logits, int64_t* argmax_out) {
+    if (!m || !seq || !pos || !tokens) return MYL_E_INVALID;
+    myl_ctx* c = m->ctx;
+    if (!m->batch) return c->fail(MYL_E_INVALID, "forward_batch: call myl_model_batch_begin first");
+    if (n_rows == 0) return MYL_OK;
+    int lmax = 0;
+    int rc = upload_rows(m, n_rows, seq, pos, tokens, &lmax);
+    if (rc) return rc;
+    rc = c->hip(forward_rows(m, (int)n_rows, lmax), "forward_batch");
+    if (rc) return rc;
+    BatchState* b = m->batch;
+    if (logits) {
+        rc = c->hip(hipMemcpyAsync(logits, b->logits, (size_t)n_rows * m->V * 4, hipMemcpyDeviceToHost, c->stream),
+                    "logits");
+        if (rc) return rc;
+    }
+    if (argmax_out) {
+        rc = c->hip(hipMemcpyAsync(argmax_out, b->argmax, (size_t)n_rows * 8, hipMemcpyDeviceToHost, c->stream), "argmax");
+        if (rc) return rc;
+    }
+    return c->hip(hipStreamSynchronize(c->stream), "forward_batch");
+}
+
+int myl_model_batch_logits_dev(myl_model* m, const int32_t** logits_dev) {
+    if (!m || !logits_dev) return MYL_E_INVALID;
+    if (!m->batch || !m->batch->logits) return m->ctx->fail(MYL_E_INVALID, "batch_logits_dev: no batch has run");
+    *logits_dev = m->batch->logits;
+    return MYL_OK;
+}
+
+int myl_model_batch_decode_greedy(myl_model* m, uint32_t n_rows, const uint32_t* seq, const uint32_t* pos,
+                                  const uint32_t* tokens, uint32_t n_steps, int64_t* tokens_out) {
+    if (!m || !seq || !pos || !tokens) return MYL_E_INVALID;
+    myl_ctx* c = m->ctx;
+    if (!m->batch) return c->fail(MYL_E_INVALID, "batch_decode: call myl_model_batch_begin first");
+    if (n_rows == 0 || n_steps == 0) return MYL_OK;
+    for (uint32_t r = 0; r < n_rows; ++r)
+        if ((uint64_t)pos[r] + n_steps > (uint64_t)m->max_pos)
+            return c->fail(MYL_E_INVALID, "batch_decode: positions beyond the KV capacity");
+    std::vector<uint32_t> seen(m->batch->n_seqs, 0);
+    for (uint32_t r = 0; r < n_rows; ++r) {
+        if (seq[r] >= (uint32_t)m->batch->n_seqs) return c->fail(MYL_E_INVALID, "batch_decode: sequence out of range");
+        if (seen[seq[r]]++) return c->fail(MYL_E_INVALID, "batch_decode: one row per sequence");
+    }
+    int lmax = 0;
+    int rc = upload_rows(m, n_rows, seq, pos, tokens, &lmax);
+    if (rc) return rc;
+    BatchState* b = m->batch;
+    const size_t need = (size_t)n_steps * n_rows;
+    if (need > b->tokens_out_cap) {
+        (void)hipStreamSynchronize(c->stream);
+        if (b->tokens_out) (void)hipFree(b->tokens_out);
+        b->tokens_out = nullptr;
+        b->tokens_out_cap = 0;
+        if (hipMalloc(&b->tokens_out, need * 8) != hipSuccess) return c->fail(MYL_E_NOMEM, "batch_decode: tokens");
+        b->tokens_out_cap = need;
+    }
+    rc = ensure_scores(m, lmax + (int)n_steps);
+    if (rc) return rc;
+    hipError_t e = hipSuccess;
+    for (uint32_t s = 0; s < n_steps && e == hipSuccess; ++s) {
+        e = forward_rows(m, (int)n_rows, lmax + (int)s);
+        if (e == hipSuccess) {
+            rows_advance_kernel<<<(n_rows + 255) / 256, 256, 0, c->stream>>>(b->rows, b->rows_cap, (int)n_rows,
+                                                                             b->argmax, m->rope_rows,
+                                                                             b->tokens_out + (size_t)s * n_rows);
+            e = hipGetLastError();
+        }
+    }
+    rc = c->hip(e, "batch_decode");
+    if (rc) return rc;
+    for (uint32_t r = 0; r < n_rows; ++r) b->len[seq[r]] = std::max(b->len[seq[r]], pos[r] + n_steps);
+    if (tokens_out) {
+        rc = c->hip(hipMemcpyAsync(tokens_out, b->tokens_out, need * 8, hipMemcpyDeviceToHost, c->stream), "tokens");
+        if (rc) return rc;
+    }
+    return c->hip(hipStreamSynchronize(c->stream), "batch_decode");
+}
+
+int myl_model_batch_read_kv(myl_model* m, uint32_t seq, uint32_t layer, uint32_t kv_head, uint32_t n_pos,
+                            int16_t* k_out, int16_t* v_out) {
+    if (!m) return MYL_E_INVALID;
+    myl_ctx* c = m->ctx;
+    if (!m->batch || seq >= (uint32_t)m->batch->n_seqs || layer >= m->spec.layers || kv_head >= m->spec.kv_heads ||
+        n_pos > (uint32_t)m->max_pos)
+        return c->fail(MYL_E_INVALID, "batch_read_kv: out of range");
+    const size_t off = seq * seq_stride(m) + (((size_t)layer * m->spec.kv_heads + kv_head) * m->max_pos) * m->hd;
+    const size_t bytes = (size_t)n_pos * m->hd * 2;
+    int rc = 0;
+    if (k_out) rc = c->hip(hipMemcpyAsync(k_out, m->batch->kc + off, bytes, hipMemcpyDeviceToHost, c->stream), "k");
+    if (!rc && v_out) rc = c->hip(hipMemcpyAsync(v_out, m->batch->vc + off, bytes, hipMemcpyDeviceToHost, c->stream), "v");
+    if (rc) return rc;
+    return c->hip(hipStreamSynchronize(c->stream), "batch_read_kv");
+}
+
+}  // extern "C"

@@ -131,3 +131,36 @@ MYL_FN int16_t lut_lookup_i16(int16_t x, const int16_t* lut, uint32_t len, int16
     if (idx > hi) idx = hi;
     return lut[(uint16_t)idx];
 }
+
+// ---- integer log-softmax (build-defined; the reference computes it in f64,
+// runtime/src/bin/perplexity_probe.rs:55-67) ------------------------------------
+//
+// log2(S) for S >= 1 as (e, f): e = floor(log2 S) and f the first 16 fraction
+// bits of log2(S / 2^e), by repeated squaring of the Q62 mantissa (the binary
+// logarithm algorithm: squaring doubles the logarithm, an overflow past 2
+// emits a 1 bit).  Integer only; the same on every machine.
+MYL_FN void log2_q16(uint64_t S, int32_t* e_out, uint32_t* f_out) {
+    if (S == 0) S = 1;
+    int32_t e = 63;
+    while (!(S >> e)) --e;
+    uint64_t x = S << (62 - e);  // S < 2^63, so e <= 62: x in [2^62, 2^63)
+    uint32_t f = 0;
+    for (int i = 0; i < 16; ++i) {
+        x = (uint64_t)(((myl_u128)x * (myl_u128)x) >> 62);  // in [2^62, 2^64)
+        f <<= 1;
+        if (x >> 63) { x >>= 1; f |= 1u; }
+    }
+    *e_out = e;
+    *f_out = f;
+}
+
+// ln(S / 2^14) in Q16: RNE((((e - 14) << 16) + f) * round(ln 2 * 2^30), 30).
+#define MYL_LN2_Q30 744261118LL
+MYL_FN int64_t ln_q16_of_sum(uint64_t S) {
+    int32_t e;
+    uint32_t f;
+    log2_q16(S, &e, &f);
+    const int64_t v = (int64_t)(e - 14) * 65536 + (int64_t)f;
+    return rshift_round64(wmul64(v, MYL_LN2_Q30), 30);
+}
+

@@ -200,6 +200,182 @@ __device__ inline void mm_w8_tile(const int16_t* __restrict__ x, int M, int ldx,
         }
 }
 
+// ---- int16 weights (the LM head of model.rs:285-296) --------------------------
+//
+// Both operands are split: x = Xa + 128 with Xa = 256*xh + xl', and likewise
+// w = Wa + 128.  Then per k
+//   x*w = 65536*xh*wh + 256*(xh*wl' + xl'*wh) + xl'*wl' + 128*Wa + 128*Xa + 16384
+// so four int8 products per tile plus the row sums of Wa (from the B
+// fragments) and of Xa (from the A fragments).  A zero-padded slot (x = w = 0,
+// i.e. Xa = Wa = -128) contributes exactly 0, so the constant term counts
+// every processed slot.  Partial sums stay exact in i32 for K < 65536
+// (|Wa|, |Xa| <= 32768).
+
+template <int WM, int WN, int WAVES_M, int WAVES_N>
+struct Mm16Shape {
+    static constexpr int kThreads = WAVES_M * WAVES_N * 64;
+    static constexpr int BM = 32 * WM * WAVES_M;
+    static constexpr int BN = 32 * WN * WAVES_N;
+    static constexpr int kPlaneA = BM * kMmStride;
+    static constexpr int kPlaneB = BN * kMmStride;
+    static constexpr int kStage = 2 * kPlaneA + 2 * kPlaneB;
+    static constexpr size_t kLds = 2 * (size_t)kStage;
+    static constexpr int XCH = BM * kMmBK / 8;
+    static constexpr int WCH = BN * kMmBK / 8;
+    static constexpr int XPT = (XCH + kThreads - 1) / kThreads;
+    static constexpr int WPT = (WCH + kThreads - 1) / kThreads;
+};
+
+template <int WM, int WN, int WAVES_M, int WAVES_N, class Sink>
+__device__ inline void mm_w16_tile(const int16_t* __restrict__ x, int M, int ldx, const int16_t* __restrict__ W,
+                                   int N, int K, int m0, int n0, int kb, int ke, int8_t* lds, const Sink& sink) {
+    using S = Mm16Shape<WM, WN, WAVES_M, WAVES_N>;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+
+    uint4 xr[S::XPT], wr[S::WPT];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < S::XPT; ++i) {
+            const int c = tid + i * S::kThreads;
+            const int row = c / (kMmBK / 8), kc = c % (kMmBK / 8);
+            const int gm = m0 + row, gk = k0 + kc * 8;
+            xr[i] = (c < S::XCH && gm < M && gk < ke) ? *reinterpret_cast<const uint4*>(x + (size_t)gm * ldx + gk)
+                                                      : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < S::WPT; ++i) {
+            const int c = tid + i * S::kThreads;
+            const int row = c / (kMmBK / 8), kc = c % (kMmBK / 8);
+            const int gn = n0 + row, gk = k0 + kc * 8;
+            wr[i] = (c < S::WCH && gn < N && gk < ke) ? *reinterpret_cast<const uint4*>(W + (size_t)gn * K + gk)
+                                                      : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto swrite = [&](int8_t* st) {
+        int8_t* ah = st;
+        int8_t* al = st + S::kPlaneA;
+        int8_t* bh = st + 2 * S::kPlaneA;
+        int8_t* bl = bh + S::kPlaneB;
+#pragma unroll
+        for (int i = 0; i < S::XPT; ++i) {
+            const int c = tid + i * S::kThreads;
+            if (c < S::XCH) {
+                const int row = c / (kMmBK / 8), kc = c % (kMmBK / 8);
+                uint2 h, l;
+                split_planes8(xr[i], h, l);
+                *reinterpret_cast<uint2*>(ah + row * kMmStride + kc * 8) = h;
+                *reinterpret_cast<uint2*>(al + row * kMmStride + kc * 8) = l;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < S::WPT; ++i) {
+            const int c = tid + i * S::kThreads;
+            if (c < S::WCH) {
+                const int row = c / (kMmBK / 8), kc = c % (kMmBK / 8);
+                uint2 h, l;
+                split_planes8(wr[i], h, l);
+                *reinterpret_cast<uint2*>(bh + row * kMmStride + kc * 8) = h;
+                *reinterpret_cast<uint2*>(bl + row * kMmStride + kc * 8) = l;
+            }
+        }
+    };
+
+    v16i32_t hh[WM][WN], hl[WM][WN], lh[WM][WN], ll[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) { hh[i][j][r] = 0; hl[i][j][r] = 0; lh[i][j][r] = 0; ll[i][j][r] = 0; }
+    int32_t ws[WN], xs[WM];
+#pragma unroll
+    for (int j = 0; j < WN; ++j) ws[j] = 0;
+#pragma unroll
+    for (int i = 0; i < WM; ++i) xs[i] = 0;
+    auto sum16 = [](const v4i32_t& h, const v4i32_t& l, int32_t acc) {
+        int32_t sh = 0, sl = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            sh = sdot4((uint32_t)h[t], 0x01010101u, sh);
+            sl = sdot4((uint32_t)l[t], 0x01010101u, sl);
+        }
+        return acc + sh * 256 + sl;
+    };
+
+    auto compute = [&](const int8_t* st) {
+        const int8_t* ah = st;
+        const int8_t* al = st + S::kPlaneA;
+        const int8_t* bh = st + 2 * S::kPlaneA;
+        const int8_t* bl = bh + S::kPlaneB;
+#pragma unroll
+        for (int s = 0; s < kMmBK / 32; ++s) {
+            const int koff = s * 32 + (lane >> 5) * 16;
+            v4i32_t a_h[WM], a_l[WM], b_h[WN], b_l[WN];
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+                const int row = (wn * WN + j) * 32 + (lane & 31);
+                b_h[j] = *reinterpret_cast<const v4i32_t*>(bh + row * kMmStride + koff);
+                b_l[j] = *reinterpret_cast<const v4i32_t*>(bl + row * kMmStride + koff);
+            }
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+                const int row = (wm * WM + i) * 32 + (lane & 31);
+                a_h[i] = *reinterpret_cast<const v4i32_t*>(ah + row * kMmStride + koff);
+                a_l[i] = *reinterpret_cast<const v4i32_t*>(al + row * kMmStride + koff);
+            }
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+#pragma unroll
+                for (int i = 0; i < WM; ++i) {
+                    hh[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_h[i], b_h[j], hh[i][j], 0, 0, 0);
+                    hl[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_h[i], b_l[j], hl[i][j], 0, 0, 0);
+                    lh[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_l[i], b_h[j], lh[i][j], 0, 0, 0);
+                    ll[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_l[i], b_l[j], ll[i][j], 0, 0, 0);
+                }
+                ws[j] = sum16(b_h[j], b_l[j], ws[j]);
+            }
+#pragma unroll
+            for (int i = 0; i < WM; ++i) xs[i] = sum16(a_h[i], a_l[i], xs[i]);
+        }
+    };
+
+    const int nk = (ke - kb + kMmBK - 1) / kMmBK;
+    gload(kb);
+    swrite(lds);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        int8_t* cur = lds + (kt & 1) * S::kStage;
+        const bool more = kt + 1 < nk;
+        if (more) gload(kb + (kt + 1) * kMmBK);
+        compute(cur);
+        if (more) swrite(lds + ((kt + 1) & 1) * S::kStage);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int j = 0; j < WN; ++j) ws[j] += __shfl_xor(ws[j], 32);
+#pragma unroll
+    for (int i = 0; i < WM; ++i) xs[i] += __shfl_xor(xs[i], 32);
+    const int64_t cterm = (int64_t)16384 * (int64_t)nk * kMmBK;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const int n = n0 + (wn * WN + j) * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int ml = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const int32_t xsum = __shfl(xs[i], ml);  // row ml's sum lives in lane ml
+                const int m = m0 + (wm * WM + i) * 32 + ml;
+                const int64_t v = (int64_t)hh[i][j][r] * 65536 + ((int64_t)hl[i][j][r] + (int64_t)lh[i][j][r]) * 256 +
+                                  (int64_t)ll[i][j][r] + ((int64_t)ws[j] + (int64_t)xsum) * 128 + cterm;
+                if (m < M && n < N) sink(n, m, v);
+            }
+        }
+}
+
 // Tile index of this block (XCD-aware order, see above); -1 when idle.
 __device__ inline int mm_tile_index(int ntiles) {
     const int b = blockIdx.x;
@@ -261,6 +437,20 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void mm_w8_splitk_kernel(
     if (kb >= ke) return;
     mm_w8_tile<WM, WN, WAVES_M, WAVES_N>(x, M, ldx, W, N, K, (int)tm * S::BM, (int)tn * S::BN, kb, ke, lds,
                                          SinkAtomic{acc, N});
+}
+
+template <int WM, int WN, int WAVES_M, int WAVES_N, class Epi>
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void mm_w16_kernel(const int16_t* __restrict__ x, int M,
+                                                                       int ldx, const int16_t* __restrict__ W, int N,
+                                                                       int K, Divider tiles_m, int ntiles, Epi epi) {
+    using S = Mm16Shape<WM, WN, WAVES_M, WAVES_N>;
+    extern __shared__ __align__(16) int8_t lds[];
+    const int t = mm_tile_index(ntiles);
+    if (t < 0) return;
+    uint32_t tn, tm;
+    tiles_m.divmod((uint32_t)t, tn, tm);
+    mm_w16_tile<WM, WN, WAVES_M, WAVES_N>(x, M, ldx, W, N, K, (int)tm * S::BM, (int)tn * S::BN, 0, K, lds,
+                                          SinkEpi<Epi>{epi});
 }
 
 // Epilogue over the split-K accumulator; clears it for the next call.

@@ -1,160 +1,12 @@
 // kernels.hip -- launchers for the GEMV and the op kernels of the integer
 // forward path (gfx950).  Host-side shape checks live in abi.cpp; everything
 // here assumes validated arguments.
-#include "internal.h"
-#include "gemm_mfma.h"
-#include "gemv.h"
+#include "gemm_dispatch.h"
+#include "../../include/myl_theta_v.h"
 #include "ops.h"
-
-#include <cstdlib>
+#include "wave.h"
 
 namespace myl {
-
-// ---------------------------------------------------------------------------
-// GEMV dispatch
-// ---------------------------------------------------------------------------
-
-inline int xvec_ok(const int16_t* x, int ldx) { return (((uintptr_t)x & 15) == 0) && (ldx % 8 == 0); }
-
-template <int R, int MT, int U, class Epi>
-static hipError_t launch_i8(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, const Epi& epi,
-                            hipStream_t st) {
-    // K-chunk staged in LDS per pass: both byte planes of MT rows fit 64 KiB.
-    const int kc = min(kGemvLdsBytes / (2 * MT), ((K + 15) / 16) * 16);
-    const int rows_per_block = R * kGemvWaves;
-    const int blocks = (N + rows_per_block - 1) / rows_per_block;
-    gemv_i8_kernel<R, MT, U, Epi><<<blocks, kGemvThreads, (size_t)2 * MT * kc, st>>>(x, M, ldx, W, N, K, kc,
-                                                                                   xvec_ok(x, ldx), epi);
-    return hipGetLastError();
-}
-
-template <int R, int MT, int U, class Epi>
-static hipError_t launch_i16(const int16_t* x, int M, int ldx, const int16_t* W, int N, int K, const Epi& epi,
-                             hipStream_t st) {
-    const int kc = min(kGemvLdsBytes / (4 * MT), ((K + 7) / 8) * 8);
-    const int rows_per_block = R * kGemvWaves;
-    const int blocks = (N + rows_per_block - 1) / rows_per_block;
-    gemv_i16_kernel<R, MT, U, Epi><<<blocks, kGemvThreads, (size_t)4 * MT * kc, st>>>(x, M, ldx, W, N, K, kc,
-                                                                                    xvec_ok(x, ldx), epi);
-    return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------
-// Matrix-core path (M > 8 activation rows)
-// ---------------------------------------------------------------------------
-
-// Tile shapes (activation rows x weight rows per block).
-enum MmTile { MM_128x128 = 0, MM_128x64 = 1, MM_64x128 = 2, MM_64x64 = 3 };
-
-// Overrides for tile sweeps: MYL_MM_TILE (an MmTile) and MYL_MM_KSPLIT.
-static int mm_env(const char* name) {
-    const char* v = std::getenv(name);
-    return v && *v ? std::atoi(v) : -1;
-}
-
-template <int WM, int WN, int WAVES_M, int WAVES_N, class Epi>
-static hipError_t mm_launch(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, const Epi& epi,
-                            int ksplit, const MmCtx* mm, hipStream_t st) {
-    using S = MmShape<WM, WN, WAVES_M, WAVES_N>;
-    const int tiles_m = (M + S::BM - 1) / S::BM, tiles_n = (N + S::BN - 1) / S::BN;
-    const int ntiles = tiles_m * tiles_n;
-    if (ksplit <= 1) {
-        const int grid = 8 * ((ntiles + 7) / 8);
-        mm_w8_kernel<WM, WN, WAVES_M, WAVES_N, Epi><<<grid, S::kThreads, S::kLds, st>>>(
-            x, M, ldx, W, N, K, Divider::of((uint32_t)tiles_m), ntiles, epi);
-        return hipGetLastError();
-    }
-    const int nkb = (K + kMmBK - 1) / kMmBK;
-    const int kslice = ((nkb + ksplit - 1) / ksplit) * kMmBK;
-    const int ns = (K + kslice - 1) / kslice;
-    const int nitems = ntiles * ns;
-    const int grid = 8 * ((nitems + 7) / 8);
-    mm_w8_splitk_kernel<WM, WN, WAVES_M, WAVES_N><<<grid, S::kThreads, S::kLds, st>>>(
-        x, M, ldx, W, N, K, Divider::of((uint32_t)tiles_m), Divider::of((uint32_t)ntiles), nitems, kslice, mm->acc);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const int colb = (N + 255) / 256;
-    const int rows = std::max(1, std::min(M, (mm->cus * 8 + colb - 1) / colb));
-    mm_splitk_finish_kernel<Epi><<<dim3(colb, rows), 256, 0, st>>>(mm->acc, M, N, epi);
-    return hipGetLastError();
-}
-
-// Tile and K split, from a sweep of the W8A16 shapes on MI355X: 64-row tiles
-// (two waves per SIMD) beat 128-row tiles at every M; 64 x 128 wins once M
-// is large.  K is split (slices of >= 1024 bytes) only when the tiles alone
-// leave CUs idle.
-template <class Epi>
-static hipError_t mm_i8(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, const Epi& epi,
-                        const MmCtx* mm, hipStream_t st) {
-    const int cus = mm ? mm->cus : 256;
-    int tile = mm_env("MYL_MM_TILE");
-    if (tile < 0 || tile > 3) tile = M <= 512 ? MM_64x64 : MM_64x128;
-    const int bm = (tile == MM_128x128 || tile == MM_128x64) ? 128 : 64;
-    const int bn = (tile == MM_128x128 || tile == MM_64x128) ? 128 : 64;
-    const int ntiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
-    const bool can_split = mm && mm->acc && (size_t)M * (size_t)N <= mm->acc_elems;
-    int ks = mm_env("MYL_MM_KSPLIT");
-    if (ks < 1) {
-        ks = 1;
-        if (ntiles < cus) ks = std::min((cus + ntiles - 1) / ntiles, std::max(1, K / 1024));
-    }
-    if (!can_split) ks = 1;
-    switch (tile) {
-        case MM_128x128: return mm_launch<2, 2, 2, 2>(x, M, ldx, W, N, K, epi, ks, mm, st);
-        case MM_128x64: return mm_launch<2, 1, 2, 2>(x, M, ldx, W, N, K, epi, ks, mm, st);
-        case MM_64x128: return mm_launch<1, 2, 2, 2>(x, M, ldx, W, N, K, epi, ks, mm, st);
-        default: return mm_launch<1, 1, 2, 2>(x, M, ldx, W, N, K, epi, ks, mm, st);
-    }
-}
-
-template <class Epi>
-static hipError_t gemv_i8(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, const Epi& epi,
-                          hipStream_t st, const MmCtx* mm) {
-    const bool fast = (K % 16 == 0) && (((uintptr_t)W & 15) == 0) && K < 131072;
-    if (!fast) {
-        dim3 grid((N + 255) / 256, M);
-        gemv_generic_kernel<int8_t, Epi><<<grid, 256, 0, st>>>(x, M, ldx, W, N, K, epi);
-        return hipGetLastError();
-    }
-    // More than 8 activation rows: the int8 matrix cores (16-byte aligned rows).
-    if (M > 8 && xvec_ok(x, ldx)) return mm_i8(x, M, ldx, W, N, K, epi, mm, st);
-    // Activation rows in groups of at most 8.
-    for (int m0 = 0; m0 < M; m0 += 8) {
-        const int mm_rows = min(8, M - m0);
-        Epi e = epi.offset_m(m0);
-        hipError_t rc;
-        const int16_t* xm = x + (size_t)m0 * ldx;
-        // Few rows: one row per wave so that the grid still fills the chip.
-        const bool few = N < 8192;
-        if (mm_rows == 1) rc = few ? launch_i8<1, 1, 4>(xm, mm_rows, ldx, W, N, K, e, st) : launch_i8<2, 1, 4>(xm, mm_rows, ldx, W, N, K, e, st);
-        else if (mm_rows == 2) rc = launch_i8<2, 2, 4>(xm, mm_rows, ldx, W, N, K, e, st);
-        else if (mm_rows <= 4) rc = launch_i8<2, 4, 2>(xm, mm_rows, ldx, W, N, K, e, st);
-        else rc = launch_i8<1, 8, 2>(xm, mm_rows, ldx, W, N, K, e, st);
-        if (rc != hipSuccess) return rc;
-    }
-    return hipSuccess;
-}
-
-template <class Epi>
-static hipError_t gemv_i16(const int16_t* x, int M, int ldx, const int16_t* W, int N, int K, const Epi& epi,
-                           hipStream_t st) {
-    const bool fast = (K % 8 == 0) && (((uintptr_t)W & 15) == 0) && K <= 8192;
-    if (!fast) {
-        dim3 grid((N + 255) / 256, M);
-        gemv_generic_kernel<int16_t, Epi><<<grid, 256, 0, st>>>(x, M, ldx, W, N, K, epi);
-        return hipGetLastError();
-    }
-    for (int m0 = 0; m0 < M; m0 += 4) {
-        const int mm = min(4, M - m0);
-        Epi e = epi.offset_m(m0);
-        hipError_t rc;
-        const int16_t* xm = x + (size_t)m0 * ldx;
-        if (mm == 1) rc = launch_i16<2, 1, 4>(xm, mm, ldx, W, N, K, e, st);
-        else rc = launch_i16<1, 4, 2>(xm, mm, ldx, W, N, K, e, st);
-        if (rc != hipSuccess) return rc;
-    }
-    return hipSuccess;
-}
 
 hipError_t linear_w8a16(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, const uint8_t* w_shifts,
                         uint8_t act_frac, uint8_t out_frac, const uint8_t* out_frac_pc, int16_t* out, int ldo,
@@ -451,6 +303,46 @@ __global__ __launch_bounds__(kBlock) void argmax_kernel(const int32_t* __restric
         __syncthreads();
     }
     if (threadIdx.x == 0) out[blockIdx.x] = (int64_t)(0xFFFFFFFFu - (uint32_t)(red[0] & 0xFFFFFFFFu));
+}
+
+// Integer log-softmax of one row at its target (build-defined, see fixed.h):
+//   m = max z;  S = sum_j lut[(m - z_j) << 2] (0 past the table; logits are
+//   Q6 and the exp LUT's input is Q8);  lp = (z_target - m) * 2^10 - ln_q16(S)
+// in Q16.  One block per row; targets < 0 give 0.
+__global__ __launch_bounds__(kBlock) void logsoftmax_kernel(const int32_t* __restrict__ z, int n, int ldz,
+                                                           const int16_t* __restrict__ lut, uint32_t lut_len,
+                                                           const int64_t* __restrict__ targets,
+                                                           int64_t* __restrict__ out) {
+    __shared__ int32_t red32[kBlock / 64];
+    __shared__ uint64_t red64[kBlock / 64];
+    const int32_t* row = z + (size_t)blockIdx.x * ldz;
+    int32_t mx = INT32_MIN;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) mx = max(mx, row[i]);
+    const int32_t m = block_max_i32(mx, red32);
+    constexpr uint32_t sh = MYL_TV_EXP_INPUT_FRAC - MYL_TV_LOGIT_FRAC_BITS;
+    int64_t s = 0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const uint64_t d = (uint64_t)((int64_t)m - (int64_t)row[i]) << sh;
+        s += d < lut_len ? (int64_t)lut[d] : 0;
+    }
+    s = wave_sum_i64(s);
+    if ((threadIdx.x & 63) == 0) red64[threadIdx.x >> 6] = (uint64_t)s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int64_t S = 0;
+        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) S += (int64_t)red64[w];
+        const int64_t t = targets[blockIdx.x];
+        int64_t lp = 0;
+        if (t >= 0 && t < n)
+            lp = ((int64_t)row[t] - (int64_t)m) * 1024 - ln_q16_of_sum(S < 1 ? 1u : (uint64_t)S);
+        out[blockIdx.x] = lp;
+    }
+}
+
+hipError_t logsoftmax(const int32_t* z, int M, int n, int ldz, const int16_t* lut, int lut_len, const int64_t* targets,
+                      int64_t* out, hipStream_t st) {
+    logsoftmax_kernel<<<M, kBlock, 0, st>>>(z, n, ldz, lut, (uint32_t)lut_len, targets, out);
+    return hipGetLastError();
 }
 
 hipError_t argmax(const int32_t* v, int M, int n, int ldv, int64_t* out, hipStream_t st) {

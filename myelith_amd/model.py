@@ -146,10 +146,66 @@ class IntegerModel:
         self._check(lib().myl_model_read_tensor(self._h, name.encode(), layer, buf.ctypes.data, nbytes), "read_tensor")
         return buf.view(dtype)
 
+    # ---- batched forward (many sequences, each with its own KV cache) ----
+
+    def batch_begin(self, n_seqs: int) -> None:
+        """KV caches for n_seqs sequences, all empty."""
+        self._check(lib().myl_model_batch_begin(self._h, n_seqs), "batch_begin")
+        self.n_seqs = n_seqs
+
+    def forward_batch(self, seq, pos, tokens, want_logits: bool = True):
+        """Rows (seq[r], pos[r], tokens[r]); row r equals forward_token(tokens[r], pos[r])
+        on sequence seq[r].  Returns (logits [R x vocab] or None, argmax [R])."""
+        s = np.ascontiguousarray(seq, dtype=np.uint32)
+        p = np.ascontiguousarray(pos, dtype=np.uint32)
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        R = s.size
+        assert p.size == R and t.size == R
+        logits = np.zeros((R, self.vocab_size), np.int32) if want_logits else None
+        am = np.zeros(R, np.int64)
+        self._check(lib().myl_model_forward_batch(self._h, R, s.ctypes.data, p.ctypes.data, t.ctypes.data,
+                                                  None if logits is None else logits.ctypes.data, am.ctypes.data),
+                    "forward_batch")
+        return logits, am
+
+    def batch_logits_dev(self, rows: int):
+        """The last batch's logits as a torch view on the device (no copy)."""
+        import torch
+        ptr = C.c_void_p()
+        self._check(lib().myl_model_batch_logits_dev(self._h, C.byref(ptr)), "batch_logits_dev")
+        return _device_view_i32(ptr.value, rows, self.vocab_size)
+
+    def batch_decode_greedy(self, seq, pos, tokens, n_steps: int):
+        """Lock-step greedy decode of len(seq) sequences; returns [n_steps x rows] argmax tokens."""
+        s = np.ascontiguousarray(seq, dtype=np.uint32)
+        p = np.ascontiguousarray(pos, dtype=np.uint32)
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.zeros((n_steps, s.size), np.int64)
+        self._check(lib().myl_model_batch_decode_greedy(self._h, s.size, s.ctypes.data, p.ctypes.data, t.ctypes.data,
+                                                        n_steps, out.ctypes.data), "batch_decode_greedy")
+        return out
+
+    def batch_read_kv(self, seq: int, layer: int, kv_head: int, n_pos: int):
+        k = np.zeros((n_pos, self.head_dim), np.int16)
+        v = np.zeros((n_pos, self.head_dim), np.int16)
+        self._check(lib().myl_model_batch_read_kv(self._h, seq, layer, kv_head, n_pos, k.ctypes.data, v.ctypes.data),
+                    "batch_read_kv")
+        return k, v
+
     @staticmethod
     def greedy_next(logits) -> int:
         """argmax_int (sampling.rs:8-18): the first maximum wins."""
         return int(np.argmax(np.asarray(logits)))
+
+
+def _device_view_i32(ptr: int, rows: int, cols: int):
+    """A torch int32 tensor over device memory owned by the library."""
+    import torch
+
+    class _Arr:
+        __cuda_array_interface__ = {"shape": (rows, cols), "typestr": "<i4", "data": (ptr, False), "version": 3,
+                                    "strides": None}
+    return torch.as_tensor(_Arr(), device="cuda")
 
 
 def dekodieren_mit_digest(model, token_ids, max_new_tokens: int):

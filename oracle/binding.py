@@ -77,6 +77,9 @@ def _declare(L) -> None:
         "or_mlp_int": (C.c_int, [P, P, P, P, sz, sz, P, P, P, P, sz, u8, u8, u8, u8, u8, i16, u8, P, P]),
         "or_argmax_int": (i64, [P, sz]),
         "or_splitmix64": (None, [u64, C.POINTER(u64), C.POINTER(u64)]),
+        "or_log2_q16": (None, [u64, C.POINTER(i32), C.POINTER(u32)]),
+        "or_ln_q16": (i64, [u64]),
+        "or_logsoftmax_at": (i64, [P, sz, P, sz, i64]),
         "or_model_create_synthetic": (P, [C.POINTER(SynthSpec), C.POINTER(Luts)]),
         "or_model_destroy": (None, [P]), "or_model_reset": (None, [P]),
         "or_set_threads": (None, [C.c_int]),
@@ -246,6 +249,23 @@ def mlp_int(x, W_gate, W_up, W_down, hidden, inter, gs, us, ds, silu, in_frac, g
 def argmax_int(v) -> int:
     a = _arr(v, np.int32)
     return lib().or_argmax_int(ptr(a), len(a))
+
+
+# ---- integer log-softmax (build-defined) ---------------------------------------
+def log2_q16(S: int) -> tuple[int, int]:
+    e, f = i32(), u32()
+    lib().or_log2_q16(S, C.byref(e), C.byref(f))
+    return e.value, f.value
+
+
+def ln_q16(S: int) -> int:
+    return lib().or_ln_q16(S)
+
+
+def logsoftmax_at(z, exp_lut, target: int) -> int:
+    a = _arr(z, np.int32)
+    lut = _arr(exp_lut, np.int16)
+    return lib().or_logsoftmax_at(ptr(a), len(a), ptr(lut), len(lut), target)
 
 
 # ---- model -------------------------------------------------------------------

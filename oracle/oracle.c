@@ -443,6 +443,47 @@ void or_splitmix64(uint64_t state, uint64_t* new_state, uint64_t* out) {
     *out = myl_mix64(s);
 }
 
+/* ---- integer log-softmax (build-defined) --------------------------------
+ * The binary logarithm by repeated squaring: with x = S / 2^e in [1, 2),
+ * log2(x^2) = 2 log2(x), so each squaring shifts the next fraction bit of
+ * log2(x) into the integer part; a square >= 2 means that bit is 1 and is
+ * halved back into [1, 2).  x is held in Q62 and each square truncated. */
+void or_log2_q16(uint64_t S, int32_t* e_out, uint32_t* f_out) {
+    if (S == 0) S = 1;
+    int32_t e = 0;
+    for (uint64_t t = S; t > 1; t >>= 1) ++e;
+    uint64_t x = S << (62 - e);
+    uint32_t f = 0;
+    for (int i = 0; i < 16; ++i) {
+        u128 sq = (u128)x * (u128)x;
+        x = (uint64_t)(sq >> 62);
+        f <<= 1;
+        if (x >= (1ULL << 63)) { x >>= 1; f |= 1u; }
+    }
+    *e_out = e;
+    *f_out = f;
+}
+
+int64_t or_ln_q16(uint64_t S) {
+    int32_t e;
+    uint32_t f;
+    or_log2_q16(S, &e, &f);
+    int64_t v = (int64_t)(e - 14) * 65536 + (int64_t)f;
+    return or_rshift_round_i64(mul64(v, 744261118LL), 30);
+}
+
+int64_t or_logsoftmax_at(const int32_t* z, size_t n, const int16_t* exp_lut, size_t lut_len, int64_t target) {
+    if (n == 0 || target < 0 || (uint64_t)target >= n) return 0;
+    int32_t m = z[0];
+    for (size_t j = 1; j < n; ++j) if (z[j] > m) m = z[j];
+    int64_t S = 0;
+    for (size_t j = 0; j < n; ++j) {
+        uint64_t d = (uint64_t)((int64_t)m - (int64_t)z[j]) << 2;  /* Q6 logits -> Q8 LUT input */
+        if (d < lut_len) S += exp_lut[d];
+    }
+    return ((int64_t)z[target] - (int64_t)m) * 1024 - or_ln_q16(S < 1 ? 1u : (uint64_t)S);
+}
+
 /* ---- model.rs / kv_cache.rs -------------------------------------------- */
 
 typedef struct {

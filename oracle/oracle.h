@@ -98,6 +98,16 @@ int or_mlp_int(const int16_t* x, const int8_t* W_gate, const int8_t* W_up, const
 int64_t or_argmax_int(const int32_t* v, size_t n);                       /* sampling.rs:8-18 */
 void or_splitmix64(uint64_t state, uint64_t* new_state, uint64_t* out);  /* prng.rs:7-14 */
 
+/* ---- integer log-softmax (build-defined; no reference counterpart: the
+ * reference's perplexity probe works in f64, perplexity_probe.rs:55-67) --- */
+/* floor(log2 S) and 16 fraction bits of log2(S / 2^e) by repeated squaring
+ * of the Q62 mantissa; S = 0 is taken as 1. */
+void or_log2_q16(uint64_t S, int32_t* e, uint32_t* f);
+/* ln(S / 2^14) in Q16: RNE((((e - 14) << 16) + f) * 744261118, 30). */
+int64_t or_ln_q16(uint64_t S);
+/* (z[t] - max z) * 2^10 - ln_q16(sum_j exp_lut[(max z - z_j) << 2]), Q16. */
+int64_t or_logsoftmax_at(const int32_t* z, size_t n, const int16_t* exp_lut, size_t lut_len, int64_t target);
+
 /* ---- model.rs / kv_cache.rs ------------------------------------------- */
 typedef struct or_model or_model;
 /* Builds the seeded synthetic model of include/myl_synth.h on the host. */

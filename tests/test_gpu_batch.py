@@ -1,0 +1,153 @@
+"""GPU parity of the batched forward (many sequences, each with its own KV
+cache) and of the integer log-softmax, against the oracle.
+
+The reference has no batching (generate.rs:28-32 loops forward_token), so a
+batch row (seq, pos, token) must equal forward_token(token, pos) run on that
+sequence alone, bit for bit: logits, argmax, KV cache and greedy tokens.
+Batches above 8 rows take the int8 matrix-core products, batches of up to 8
+the streaming GEMVs; both are exercised.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import case
+from test_gpu_model import build, tiny
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_rows(om, seqs_tokens):
+    """Per sequence, forward_token over its tokens from position 0: logits [T x V]."""
+    out = []
+    for toks in seqs_tokens:
+        om.reset()
+        out.append(np.stack([om.forward_token(int(t), p) for p, t in enumerate(toks)]))
+    return out
+
+
+def compare_batch_kv(gm, om, spec, seq, toks):
+    om.reset()
+    for p, t in enumerate(toks):
+        om.forward_token(int(t), p)
+    for l in range(spec["layers"]):
+        for h in range(spec["kv_heads"]):
+            gk, gv = gm.batch_read_kv(seq, l, h, len(toks))
+            ok, ov = om.read_kv(l, h, len(toks))
+            assert np.array_equal(gk, ok), ("K", seq, l, h)
+            assert np.array_equal(gv, ov), ("V", seq, l, h)
+
+
+@pytest.mark.parametrize("hd,lm16,bias,kvh", [(64, 0, 1, 2), (128, 1, 1, 2), (128, 0, 0, 4)])
+def test_batch_rows_interleaved(backend, hd, lm16, bias, kvh):
+    """Three sequences of different lengths, rows interleaved and unsorted, in
+    a 34-row batch (matrix cores) then a 4-row continuation (GEMV)."""
+    spec = tiny(hd, lm16, bias, kvh)
+    case(f"batch rows {spec}")
+    gm, om = build(backend, spec)
+    r = np.random.default_rng(hd * 7 + kvh)
+    lens1 = [10, 5, 19]
+    toks = [r.integers(0, spec["vocab"], 30) for _ in lens1]
+    rows = [(s, p) for s, n in enumerate(lens1) for p in range(n)]
+    order = r.permutation(len(rows))
+    rows = [rows[i] for i in order]
+    gm.batch_begin(3)
+    seq = [s for s, _ in rows]
+    pos = [p for _, p in rows]
+    tk = [int(toks[s][p]) for s, p in rows]
+    logits, am = gm.forward_batch(seq, pos, tk)
+    ref = oracle_rows(om, [toks[s][:30] for s in range(3)])
+    for i, (s, p) in enumerate(rows):
+        assert np.array_equal(logits[i], ref[s][p]), ("row", s, p)
+        assert am[i] == int(np.argmax(ref[s][p]))
+    # continuation: seq 0 positions 10..12, seq 2 position 19 (4 rows -> GEMV path)
+    rows2 = [(0, 10), (2, 19), (0, 11), (0, 12)]
+    logits2, _ = gm.forward_batch([s for s, _ in rows2], [p for _, p in rows2], [int(toks[s][p]) for s, p in rows2])
+    for i, (s, p) in enumerate(rows2):
+        assert np.array_equal(logits2[i], ref[s][p]), ("continuation", s, p)
+    compare_batch_kv(gm, om, spec, 0, toks[0][:13])
+    compare_batch_kv(gm, om, spec, 2, toks[2][:20])
+    # the invalid cases the boundary rejects
+    with pytest.raises(ValueError):
+        gm.forward_batch([1, 1], [7, 9], [1, 2])  # gap and beyond the cached length
+    with pytest.raises(ValueError):
+        gm.forward_batch([3], [0], [1])  # no such sequence
+
+
+def test_batch_decode_greedy_lock_step(backend):
+    """Four sequences prefilled to different lengths, then 12 lock-step greedy
+    steps on the device: each sequence's tokens equal its own greedy run."""
+    spec = tiny(128, 1, 1, 2)
+    case("batch greedy decode")
+    gm, om = build(backend, spec)
+    r = np.random.default_rng(3)
+    prompts = [r.integers(0, spec["vocab"], n) for n in (3, 9, 1, 6)]
+    gm.batch_begin(4)
+    rows = [(s, p) for s, pr in enumerate(prompts) for p in range(len(pr))]
+    _, am = gm.forward_batch([s for s, _ in rows], [p for _, p in rows], [int(prompts[s][p]) for s, p in rows])
+    last = {s: i for i, (s, p) in enumerate(rows)}  # the last row of each sequence
+    first = [int(am[last[s]]) for s in range(4)]
+    steps = 12
+    toks = gm.batch_decode_greedy(range(4), [len(p) for p in prompts], first, steps)
+    for s, pr in enumerate(prompts):
+        om.reset()
+        logits = None
+        for p, t in enumerate(pr):
+            logits = om.forward_token(int(t), p)
+        nxt = int(np.argmax(logits))
+        assert nxt == first[s]
+        exp = []
+        pos = len(pr)
+        for _ in range(steps):
+            logits = om.forward_token(nxt, pos)
+            nxt = int(np.argmax(logits))
+            exp.append(nxt)
+            pos += 1
+        assert [int(t) for t in toks[:, s]] == exp, s
+
+
+def test_logsoftmax_dev(backend, oracle):
+    import torch
+    from myelith_amd.luts import exp_lut
+    lut = exp_lut()
+    r = np.random.default_rng(17)
+    for M, n in ((1, 1), (3, 7), (5, 1000), (4, 152064)):
+        case(f"logsoftmax M={M} n={n}")
+        z = r.integers(-30000, 30000, (M, n)).astype(np.int32)
+        z[:, 0] = z[:, -1]
+        t = r.integers(0, n, M).astype(np.int64)
+        t[0] = -1
+        got = backend.logsoftmax_dev(torch.from_numpy(z).cuda(), lut, t).cpu().numpy()
+        exp = np.array([oracle.logsoftmax_at(z[i], lut, int(t[i])) for i in range(M)], np.int64)
+        assert np.array_equal(got, exp)
+
+
+def test_qwen7b_teacher_forced_rows(backend):
+    """Qwen2.5-7B architecture at full size (int16 LM head on the matrix
+    cores): two sequences x 20 teacher-forced positions in one 40-row batch;
+    every row's logits and the per-sequence integer log-softmax sums equal the
+    oracle's."""
+    import torch
+    from myelith_amd.model import QWEN25_7B, make_spec
+    from oracle.binding import logsoftmax_at
+    spec = make_spec(QWEN25_7B, seed=7, max_pos=64)
+    case("qwen2.5-7b teacher-forced 2 x 20")
+    gm, om = build(backend, spec)
+    r = np.random.default_rng(44)
+    T = 20
+    toks = [r.integers(0, spec["vocab"], T) for _ in range(2)]
+    gm.batch_begin(2)
+    seq = [s for s in range(2) for _ in range(T)]
+    pos = [p for _ in range(2) for p in range(T)]
+    logits, _ = gm.forward_batch(seq, pos, [int(toks[s][p]) for s, p in zip(seq, pos)])
+    ref = oracle_rows(om, toks)
+    for i, (s, p) in enumerate(zip(seq, pos)):
+        assert np.array_equal(logits[i], ref[s][p]), ("row", s, p)
+    lut = gm.luts.exp
+    targets = np.array([int(toks[s][p + 1]) if p + 1 < T else -1 for s, p in zip(seq, pos)], np.int64)
+    lp = backend.logsoftmax_dev(gm.batch_logits_dev(len(seq)), lut, targets).cpu().numpy()
+    for s in range(2):
+        exp = sum(logsoftmax_at(ref[s][p], lut, int(toks[s][p + 1])) for p in range(T - 1))
+        assert int(lp[s * T:(s + 1) * T].sum()) == exp
+    torch.cuda.synchronize()

@@ -435,3 +435,62 @@ def test_digest_byte_layout():
     assert len(b) == 2 * 4 * 4
     # FIPS 180-4 KAT for the hash itself ("abc")
     assert hashlib.sha256(b"abc").hexdigest() == "ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad"
+
+
+# ---- integer log-softmax (build-defined; pinned by closed forms) ---------------
+
+def _samples_u64(seed=5):
+    r = np.random.default_rng(seed)
+    s = [1, 2, 3, 5, 16383, 16384, 16385, (1 << 40) - 1, 1 << 40, (1 << 46) + 12345]
+    s += [1 << k for k in range(0, 47)] + [(1 << k) - 1 for k in range(2, 47)] + [(1 << k) + 1 for k in range(1, 47)]
+    s += [int(v) for v in r.integers(1, 1 << 46, 2000, dtype=np.int64)]
+    return s
+
+
+def test_log2_q16_closed_form(oracle):
+    """e = floor(log2 S) exactly; f = the first 16 fraction bits of log2(S / 2^e)
+    up to the truncation of each squaring (which can only lower it, by at
+    most one unit at these widths); powers of two have f = 0."""
+    for S in _samples_u64():
+        e, f = oracle.log2_q16(S)
+        assert e == S.bit_length() - 1, S
+        true = (math.log2(S) - e) * 65536
+        assert 0 <= f <= 65535
+        assert math.floor(true) - 1 <= f <= math.floor(true + 1e-9), (S, f, true)
+        if S & (S - 1) == 0:
+            assert f == 0
+    assert oracle.log2_q16(0) == (0, 0)  # S = 0 is taken as 1
+
+
+def test_ln_q16_closed_form(oracle):
+    """ln(S / 2^14) in Q16 to within two units; exact zero at S = 2^14 and the
+    exact RNE of k * ln2 at powers of two."""
+    for S in _samples_u64(6):
+        got = oracle.ln_q16(S)
+        assert abs(got - math.log(S / 16384) * 65536) <= 2.0, S
+    assert oracle.ln_q16(16384) == 0
+    for k in range(0, 47):
+        v = (k - 14) * 65536 * 744261118
+        assert oracle.ln_q16(1 << k) == oracle.rshift_round_i64(v, 30)
+
+
+def test_logsoftmax_matches_float_log_softmax(oracle):
+    """Against the float64 log-softmax of the same Q6 logits: the exp LUT is
+    exp(-x) to Q14, so the integer result is within 2e-3 nats."""
+    from myelith_amd.luts import exp_lut
+    lut = exp_lut()
+    r = np.random.default_rng(11)
+    for n in (1, 2, 17, 1000, 152064):
+        z = r.integers(-20000, 20000, n).astype(np.int32)
+        if n > 2:
+            z[1] = z[0]  # ties
+        zf = z.astype(np.float64) / 64.0
+        mx = zf.max()
+        lse = mx + math.log(np.exp(zf - mx).sum())
+        for t in {0, n // 2, n - 1, int(np.argmax(z))}:
+            got = oracle.logsoftmax_at(z, lut, t)
+            assert abs(got / 65536.0 - (zf[t] - lse)) < 2e-3, (n, t)
+    # one dominant logit: S = 2^14 exactly, so the maximum scores 0
+    z = np.array([5000, -100000, -200000], np.int32)
+    assert oracle.logsoftmax_at(z, lut, 0) == 0
+    assert oracle.logsoftmax_at(z, lut, 3) == 0 and oracle.logsoftmax_at(z, lut, -1) == 0
