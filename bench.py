@@ -18,6 +18,11 @@ Also reported:
                rotating weight copies (> 512 MB distinct) so the 256 MB
                Infinity Cache cannot serve repeats, M >= 64 runs on the int8
                matrix cores and reports TOP/s;
+  teacher_forced_prefill  4 x 1024 Zipf(1.1) token ids through the batched
+               forward on the matrix cores, with the integer log-softmax
+               summed per sequence;
+  batched_decode  lock-step greedy decode of 8 and 32 sequences over
+               2048-token contexts;
   cpu_baseline the CPU oracle (a single-thread restatement of the reference's
                scalar Rust path) on a bounded sample of the same workload, on
                this host's cores, after checking its logits equal the GPU's.
@@ -114,6 +119,90 @@ def w8a16_sweep(backend, shapes, ms=(1, 8, 64, 512), target_bytes=6 << 30, targe
     return out
 
 
+def zipf_tokens(rng, vocab: int, n: int, s: float = 1.1):
+    """Token ids drawn Zipf(s) over [0, vocab) by a seeded inverse CDF."""
+    import numpy as np
+    w = 1.0 / np.arange(1, vocab + 1, dtype=np.float64) ** s
+    cdf = np.cumsum(w)
+    cdf /= cdf[-1]
+    return np.minimum(np.searchsorted(cdf, rng.random(n)), vocab - 1).astype(np.uint32)
+
+
+def teacher_forced_prefill(model, backend, seed: int, B: int = 4, T: int = 1024):
+    """B sequences x T Zipf(1.1) token ids through the batched forward (all
+    rows at once, the projections on the int8 matrix cores), full-sequence
+    logits left in HBM, then the integer log-softmax at every next token,
+    summed per sequence (Q16).  Ops: 2 * 7,070,285,824 MAC per token
+    (int16 LM head included) plus causal attention."""
+    import numpy as np
+    import torch
+    rng = np.random.default_rng(seed + 4)
+    toks = zipf_tokens(rng, model.vocab_size, B * T).reshape(B, T)
+    seq = np.repeat(np.arange(B), T)
+    pos = np.tile(np.arange(T), B)
+    tgt = np.concatenate([np.append(toks[b, 1:].astype(np.int64), -1) for b in range(B)])
+    tgt_d = torch.from_numpy(tgt).cuda()
+    lut = torch.from_numpy(np.ascontiguousarray(model.luts.exp, dtype=np.int16)).cuda()
+    times = []
+    for _ in range(2):  # the first run also allocates the row buffers
+        model.batch_begin(B)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model.forward_batch(seq, pos, toks.ravel(), want_logits=False)
+        lp = backend.logsoftmax_dev(model.batch_logits_dev(B * T), lut, tgt_d)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    sums = lp.view(B, T).sum(dim=1).cpu().tolist()
+    sec = times[-1]
+    mac_tok = 7070285824
+    attn_mac = sum(p + 1 for p in range(T)) * B * 28 * 28 * 128 * 2
+    ops = 2 * (mac_tok * B * T + attn_mac)
+    log(f"teacher-forced prefill {B}x{T}: {sec * 1e3:.1f} ms, {B * T / sec:.0f} tok/s, {ops / sec / 1e12:.1f} TOP/s")
+    return {"batch": B, "seq_len": T, "tokens": "Zipf(1.1) over the vocab, seeded", "ms": round(sec * 1e3, 2),
+            "tok_s": round(B * T / sec, 1), "TOPs": round(ops / sec / 1e12, 1), "ops": ops,
+            "logsoftmax_sum_q16": [int(v) for v in sums]}
+
+
+def batched_decode(model, seed: int, batches=(8, 32), ctx: int = 2048, steps: int = 32):
+    """B sequences, each with a seeded 2048-token context prefilled through
+    the batched forward (untimed, in chunks of at most 4096 rows), then
+    `steps` lock-step greedy decode steps on the device (timed)."""
+    import numpy as np
+    import torch
+    out = {}
+    for B in batches:
+        rng = np.random.default_rng(seed + B)
+        prompts = rng.integers(0, model.vocab_size, (B, ctx)).astype(np.uint32)
+        model.batch_begin(B)
+        chunk = max(1, 4096 // B)
+        last = None
+        t0 = time.perf_counter()
+        for p0 in range(0, ctx, chunk):
+            n = min(chunk, ctx - p0)
+            seq = np.repeat(np.arange(B), n)
+            pos = np.tile(np.arange(p0, p0 + n), B)
+            _, am = model.forward_batch(seq, pos, prompts[:, p0:p0 + n].ravel(), want_logits=False)
+            last = am.reshape(B, n)[:, -1]
+        t_pre = time.perf_counter() - t0
+        model.batch_decode_greedy(np.arange(B), np.full(B, ctx), last, 2)  # warm-up
+        model.batch_begin(B)  # the same prompts again: the context is rebuilt
+        for p0 in range(0, ctx, chunk):
+            n = min(chunk, ctx - p0)
+            seq = np.repeat(np.arange(B), n)
+            pos = np.tile(np.arange(p0, p0 + n), B)
+            model.forward_batch(seq, pos, prompts[:, p0:p0 + n].ravel(), want_logits=False)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model.batch_decode_greedy(np.arange(B), np.full(B, ctx), last, steps)
+        torch.cuda.synchronize()
+        sec = time.perf_counter() - t0
+        out[f"B{B}"] = {"context": ctx, "steps": steps, "ms_per_step": round(sec / steps * 1e3, 3),
+                        "tok_s": round(B * steps / sec, 1), "prefill_s": round(t_pre, 2)}
+        log(f"batched decode B={B}: {sec / steps * 1e3:.2f} ms/step, {B * steps / sec:.0f} tok/s "
+            f"(context prefill {t_pre:.1f} s)")
+    return out
+
+
 def cpu_baseline(spec, gpu_model, prompt, n_decode):
     """Times the oracle (single thread) on a bounded sample: forward_token of a
     short prompt + n_decode greedy steps of the same model; checks that the GPU
@@ -163,6 +252,7 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=7)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
+    ap.add_argument("--no-batch", action="store_true", help="skip the batched decode and teacher-forced prefill")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -233,6 +323,11 @@ def main() -> int:
     if not args.no_gemv:
         gemv = w8a16_sweep(backend, [(3584, 3584), (18944, 3584), (3584, 18944), (152064, 3584)])
 
+    prefill_tf, batch_dec = None, None
+    if not args.no_batch:
+        prefill_tf = teacher_forced_prefill(model, backend, args.seed)
+        batch_dec = batched_decode(model, args.seed)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(spec, model, [int(t) for t in prompt[:4]], 12)
@@ -263,6 +358,8 @@ def main() -> int:
                      "bytes_per_launch": cb[dom], "avg_us": per_class[dom]["avg_us"]},
         "kernel_classes": per_class,
         "w8a16_sweep": gemv,
+        "teacher_forced_prefill": prefill_tf,
+        "batched_decode": batch_dec,
         "cpu_baseline": cpu,
         "gpu": torch.cuda.get_device_name(0),
     }

@@ -1,6 +1,6 @@
 // gemm_dispatch.h -- shape dispatch of the W8A16 / W16A16 products: the
-// streaming GEMV kernels for up to 8 activation rows, the int8 matrix cores
-// above.  Shared by the op launchers (kernels.hip) and the batched forward
+// GEMV kernels for one activation row, the int8 matrix cores for more
+// rows.  Shared by the op launchers (kernels.hip) and the batched forward
 // (batch.hip), which plug in their own epilogues.
 //
 // An epilogue type provides
@@ -48,7 +48,7 @@ inline hipError_t launch_i16(const int16_t* x, int M, int ldx, const int16_t* W,
 }
 
 // ---------------------------------------------------------------------------
-// Matrix-core path (M > 8 activation rows)
+// Matrix-core path (M > 1 activation rows)
 // ---------------------------------------------------------------------------
 
 // Tile shapes (activation rows x weight rows per block).
@@ -124,8 +124,10 @@ inline hipError_t gemv_i8(const int16_t* x, int M, int ldx, const int8_t* W, int
         gemv_generic_kernel<int8_t, Epi><<<grid, 256, 0, st>>>(x, M, ldx, W, N, K, epi);
         return hipGetLastError();
     }
-    // More than 8 activation rows: the int8 matrix cores (16-byte aligned rows).
-    if (M > 8 && xvec_ok(x, ldx)) return mm_i8(x, M, ldx, W, N, K, epi, mm, st);
+    // More than one activation row: the int8 matrix cores (16-byte aligned
+    // rows).  Up to 64 rows are one tile row, so the weights stream once; the
+    // multi-row GEMV below reached only ~0.6 TB/s at 8 rows on MI355X.
+    if (M > 1 && xvec_ok(x, ldx)) return mm_i8(x, M, ldx, W, N, K, epi, mm, st);
     // Activation rows in groups of at most 8.
     for (int m0 = 0; m0 < M; m0 += 8) {
         const int mm_rows = min(8, M - m0);
@@ -152,8 +154,8 @@ inline hipError_t gemv_i16(const int16_t* x, int M, int ldx, const int16_t* W, i
         gemv_generic_kernel<int16_t, Epi><<<grid, 256, 0, st>>>(x, M, ldx, W, N, K, epi);
         return hipGetLastError();
     }
-    // More than 8 activation rows: the int8 matrix cores, four byte-plane products.
-    if (M > 8 && xvec_ok(x, ldx) && K < 65536) {
+    // More than one activation row: the int8 matrix cores, four byte-plane products.
+    if (M > 1 && xvec_ok(x, ldx) && K < 65536) {
         using S = Mm16Shape<1, 1, 2, 2>;
         const int tiles_m = (M + S::BM - 1) / S::BM, ntiles = tiles_m * ((N + S::BN - 1) / S::BN);
         mm_w16_kernel<1, 1, 2, 2, Epi><<<8 * ((ntiles + 7) / 8), S::kThreads, S::kLds, st>>>(

@@ -7,7 +7,7 @@
 
 namespace myl {
 
-// Matrix-core (M > 8) launch context: the device's CU count and an i64
+// Matrix-core (M > 1) launch context: the device's CU count and an i64
 // split-K accumulator of acc_elems entries that is all zeros between calls
 // (the split-K epilogue clears what it reads).  acc may be null: the
 // products then run without K splitting.
