@@ -23,6 +23,7 @@ Also reported:
                summed per sequence;
   batched_decode  lock-step greedy decode of 8 and 32 sequences over
                2048-token contexts;
+  moe_layer    the Qwen1.5-MoE-shaped integer MoE layer on 4096 tokens;
   cpu_baseline the CPU oracle (a single-thread restatement of the reference's
                scalar Rust path) on a bounded sample of the same workload, on
                this host's cores, after checking its logits equal the GPU's.
@@ -203,6 +204,36 @@ def batched_decode(model, seed: int, batches=(8, 32), ctx: int = 2048, steps: in
     return out
 
 
+def moe_layer(backend, seed: int, T: int = 4096):
+    """The Qwen1.5-MoE-A2.7B-shaped integer MoE layer (60 experts x 1408, top-4,
+    shared expert 5632, hidden 2048) on 4096 seeded Gaussian tokens with Zipf(1.0)
+    expert load: route, stable dispatch, grouped experts on the matrix cores,
+    combine.  Ops 2 * (60*2048 + 4*3*1408*2048 + 3*5632*2048) per token; weights
+    553,771,008 bytes."""
+    import torch
+    from myelith_amd.moe import MoeLayer, moe_spec
+    layer = MoeLayer(backend, moe_spec(seed))
+    x = layer.synth_input(T)
+    out = torch.empty_like(x)
+    for _ in range(2):
+        layer.forward(x, out)
+    reps = 5
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        layer.forward(x, out)
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / reps
+    r = layer.route(T)
+    ops = 2 * T * (60 * 2048 + 4 * 3 * 1408 * 2048 + 3 * 5632 * 2048)
+    layer.close()
+    top = [int(v) for v in r["counts"][:4]]
+    log(f"moe layer {T} tokens: {sec * 1e3:.2f} ms, {T / sec:.0f} tok/s, {ops / sec / 1e12:.1f} TOP/s, "
+        f"top expert loads {top}")
+    return {"tokens": T, "ms": round(sec * 1e3, 3), "tok_s": round(T / sec, 1), "TOPs": round(ops / sec / 1e12, 1),
+            "ops": ops, "weight_bytes": 553771008, "expert_load_top4": top, "includes_host_sync": True}
+
+
 def cpu_baseline(spec, gpu_model, prompt, n_decode):
     """Times the oracle (single thread) on a bounded sample: forward_token of a
     short prompt + n_decode greedy steps of the same model; checks that the GPU
@@ -323,10 +354,11 @@ def main() -> int:
     if not args.no_gemv:
         gemv = w8a16_sweep(backend, [(3584, 3584), (18944, 3584), (3584, 18944), (152064, 3584)])
 
-    prefill_tf, batch_dec = None, None
+    prefill_tf, batch_dec, moe = None, None, None
     if not args.no_batch:
         prefill_tf = teacher_forced_prefill(model, backend, args.seed)
         batch_dec = batched_decode(model, args.seed)
+        moe = moe_layer(backend, args.seed)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -360,6 +392,7 @@ def main() -> int:
         "w8a16_sweep": gemv,
         "teacher_forced_prefill": prefill_tf,
         "batched_decode": batch_dec,
+        "moe_layer": moe,
         "cpu_baseline": cpu,
         "gpu": torch.cuda.get_device_name(0),
     }

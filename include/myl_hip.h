@@ -47,6 +47,7 @@ extern "C" {
 
 typedef struct myl_ctx myl_ctx;
 typedef struct myl_model myl_model;
+typedef struct myl_moe myl_moe;
 
 /* ---- backend identity: rocm.rs:71-82 (name / hardware_family / feature_tag) */
 const char* myl_backend_name(void);     /* "rocm"    */
@@ -247,6 +248,37 @@ int myl_model_batch_decode_greedy(myl_model* m, uint32_t n_rows, const uint32_t*
 /* KVCache::read (kv_cache.rs:43-52) of one batch sequence. */
 int myl_model_batch_read_kv(myl_model* m, uint32_t seq, uint32_t layer, uint32_t kv_head, uint32_t n_pos,
                             int16_t* k_out, int16_t* v_out);
+
+/* ======================================================================
+ * 4. Integer MoE layer (no reference counterpart: the reference is dense,
+ *    README/Whitepaper/myelith-whitepaper-v0.3-en.md:662).  Semantics, each
+ *    step a reference primitive:
+ *      router   r_e = clamp_i32(clamp_i32(rescale_i64(W_r[e] . x, 15 + 8, 8)) + bias_e)
+ *               (LM-head requant, model.rs:284-308; Q8 logits)
+ *      top-k    k first maxima, lowest index on ties (sampling.rs:8-18)
+ *      gates    softmax_int of the k logits, shift 0, frac 14 (softmax.rs:24-64)
+ *      dispatch per expert, its tokens in ascending token order
+ *      experts  mlp_int (mlp.rs:28-74); shared expert likewise
+ *      combine  clamp_i16(RNE(sum_k g_k y_k + 2^14 s, 14)) in i64
+ * ==================================================================== */
+
+/* Builds the seeded synthetic layer of include/myl_synth.h in HBM;
+ * router_bias holds n_experts Q8 biases. */
+int myl_moe_create_synthetic(myl_ctx* ctx, const myl_moe_spec* spec, const int32_t* router_bias, const myl_luts* luts,
+                             myl_moe** out);
+void myl_moe_destroy(myl_moe* m);
+/* The layer's synthetic input for n_tokens tokens (device, [n_tokens x hidden]). */
+int myl_moe_synth_input(myl_moe* m, uint32_t n_tokens, int16_t* x_dev);
+/* out_dev [n_tokens x hidden] = the layer on x_dev [n_tokens x hidden] (device,
+ * 16-byte aligned).  Synchronises once with the host (the experts' token
+ * counts size the grouped products). */
+int myl_moe_forward(myl_moe* m, const int16_t* x_dev, uint32_t n_tokens, int16_t* out_dev);
+/* Routing of the last forward (host arrays, any may be NULL): ids and gates
+ * [n_tokens x top_k] (descending logit, lowest expert first on ties), counts
+ * [n_experts], offsets [n_experts + 1], list_tok [n_tokens x top_k] (expert-
+ * major, ascending token order within an expert). */
+int myl_moe_read_route(myl_moe* m, uint32_t n_tokens, int32_t* ids, int32_t* gates, int32_t* counts, int32_t* offsets,
+                       int32_t* list_tok);
 
 #ifdef __cplusplus
 }

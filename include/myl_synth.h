@@ -63,7 +63,7 @@ enum myl_role {
     MYL_R_BQ, MYL_R_BK, MYL_R_BV, MYL_R_BQ_SHIFT, MYL_R_BK_SHIFT, MYL_R_BV_SHIFT,
     MYL_R_RES_IN, MYL_R_RES_MID, MYL_R_LAYER_FRACS, MYL_R_MODEL_FRACS,
     MYL_R_MAT, MYL_R_MAT_SHIFT, MYL_R_MAT_MULT, MYL_R_ACT,
-    MYL_R_ROUTER, MYL_R_ROUTER_SHIFT
+    MYL_R_ROUTER, MYL_R_ROUTER_SHIFT, MYL_R_MOE_OUT_FRAC
 };
 
 /* int8 weight element, uniform in [-127, 127] (BASELINE weight distribution). */
@@ -166,6 +166,23 @@ MYL_HD int32_t myl_synth_small(uint64_t model_seed, uint32_t layer, uint32_t rol
     int32_t lo, hi;
     myl_synth_small_range(role, &lo, &hi);
     return myl_draw_range(myl_splitmix_at(myl_tensor_seed(model_seed, layer, role), i), lo, hi);
+}
+
+/* ---- the synthetic MoE layer (myl_moe_spec) ---------------------------------
+ * Expert e's gate/up/down weights and row shifts use the model roles
+ * MYL_R_WG/WU/WD and MYL_R_SG/SU/SD with `layer` = e; the shared expert uses
+ * layer = n_experts.  The router is [n_experts x hidden] (MYL_R_ROUTER); the
+ * input is Gaussian int16 with sd 2000 (MYL_R_ACT, element t * hidden + i). */
+#define MYL_MOE_X_FRAC        8   /* input fractional bits */
+#define MYL_MOE_ROUTER_FRAC   8   /* router logits: the exp LUT's input frac */
+#define MYL_MOE_ROUTER_SHIFT  15  /* router row shift: logit sd ~0.8 at sd-2000 inputs */
+#define MYL_MOE_GATE_FRAC     10
+#define MYL_MOE_UP_FRAC       10
+#define MYL_MOE_DOWN_IN_FRAC  11
+
+/* Per-channel output fractional bits of every expert (and the layer). */
+MYL_HD uint8_t myl_synth_moe_out_frac(uint64_t model_seed, uint64_t ch) {
+    return myl_synth_res_frac(myl_tensor_seed(model_seed, 0, MYL_R_MOE_OUT_FRAC), ch);
 }
 
 /* Model-wide scalars. */

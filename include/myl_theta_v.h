@@ -64,6 +64,16 @@ typedef struct myl_synth_spec {
     int32_t  attention_bias; /* Qwen2.5 carries q/k/v biases (loader.rs:751-781) */
 } myl_synth_spec;
 
+/* Shape and seed of a synthetic integer MoE layer (Qwen1.5-MoE-A2.7B shape:
+ * hidden 2048, 60 routed experts of intermediate 1408, top-4, one shared
+ * expert of intermediate 5632).  The reference has no MoE; the layer's
+ * integer semantics are the build's own, composed from reference primitives
+ * (include/myl_hip.h, myl_moe_forward). */
+typedef struct myl_moe_spec {
+    uint64_t seed;
+    uint32_t hidden, n_experts, inter, top_k, shared_inter;
+} myl_moe_spec;
+
 #ifdef __cplusplus
 }
 #endif

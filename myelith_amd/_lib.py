@@ -26,6 +26,12 @@ class SynthSpec(C.Structure):
                 ("lm_head_int16", i32), ("attention_bias", i32)]
 
 
+class MoeSpec(C.Structure):
+    """myl_moe_spec (include/myl_theta_v.h)."""
+    _fields_ = [("seed", u64), ("hidden", u32), ("n_experts", u32), ("inter", u32), ("top_k", u32),
+                ("shared_inter", u32)]
+
+
 class Luts(C.Structure):
     """myl_luts (include/myl_theta_v.h)."""
     _fields_ = [("rsqrt", P), ("rsqrt_len", sz), ("silu", P), ("silu_len", sz), ("exp", P),
@@ -83,6 +89,11 @@ SIGNATURES: dict[str, tuple] = {
     "myl_model_batch_logits_dev": (INT, [P, C.POINTER(P)]),
     "myl_model_batch_decode_greedy": (INT, [P, u32, P, P, P, u32, P]),
     "myl_model_batch_read_kv": (INT, [P, u32, u32, u32, u32, P, P]),
+    "myl_moe_create_synthetic": (INT, [P, C.POINTER(MoeSpec), P, C.POINTER(Luts), C.POINTER(P)]),
+    "myl_moe_destroy": (None, [P]),
+    "myl_moe_synth_input": (INT, [P, u32, P]),
+    "myl_moe_forward": (INT, [P, P, u32, P]),
+    "myl_moe_read_route": (INT, [P, u32, P, P, P, P, P]),
 }
 
 _lib = None

@@ -28,6 +28,7 @@ SOURCES = {  # source -> is HIP device code
     "kernels.hip": True,
     "model.hip": True,
     "batch.hip": True,
+    "moe.hip": True,
     "abi.cpp": False,
 }
 

@@ -453,6 +453,35 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void mm_w16_kernel(const in
                                           SinkEpi<Epi>{epi});
 }
 
+// ---- grouped products (MoE experts) ------------------------------------------
+//
+// One launch covers every expert: work item t = (expert e, row tile m0,
+// column tile n0) of a table built from the experts' row counts.  Expert e
+// owns activation rows [offsets[e], offsets[e + 1]) of x and the weight
+// matrix W + e * w_stride; the epilogue gets (e, n, global row, sum).
+struct MmWork { int e, m0, n0, pad; };
+
+template <class EpiG>
+struct SinkGrouped {
+    const EpiG& epi;
+    int e, row0;
+    __device__ inline void operator()(int n, int m, int64_t v) const { epi.one(e, n, row0 + m, v); }
+};
+
+template <int WM, int WN, int WAVES_M, int WAVES_N, class EpiG>
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void mm_w8_grouped_kernel(
+    const int16_t* __restrict__ x, int ldx, const int8_t* __restrict__ W, size_t w_stride, int N, int K,
+    const int* __restrict__ offsets, const MmWork* __restrict__ work, int nwork, EpiG epi) {
+    extern __shared__ __align__(16) int8_t lds[];
+    const int t = mm_tile_index(nwork);
+    if (t < 0) return;
+    const MmWork wk = work[t];
+    const int row0 = offsets[wk.e];
+    const int Me = offsets[wk.e + 1] - row0;
+    mm_w8_tile<WM, WN, WAVES_M, WAVES_N>(x + (size_t)row0 * ldx, Me, ldx, W + (size_t)wk.e * w_stride, N, K, wk.m0,
+                                         wk.n0, 0, K, lds, SinkGrouped<EpiG>{epi, wk.e, row0});
+}
+
 // Epilogue over the split-K accumulator; clears it for the next call.
 // grid (ceil(N / 256), rows): block (x, y) handles columns x * 256 .. of rows
 // y, y + gridDim.y, ...

@@ -1,0 +1,526 @@
+// moe.hip -- an integer mixture-of-experts layer (Qwen1.5-MoE-A2.7B shape) on
+// the device: route, dispatch, grouped experts, combine.
+//
+// The reference has no MoE (its whitepaper chooses dense models), so the
+// layer's semantics are defined here from the reference's own primitives, and
+// the CPU oracle restates the same definition:
+//   router    r_e = clamp_i32(clamp_i32(rescale_i64(W_r[e] . x, 15 + 8, 8)) + bias_e)
+//             (the LM-head requant of model.rs:284-308, Q8 logits, plus an
+//             integer bias per expert)
+//   top-k     k times the first maximum of the remaining logits (argmax_int,
+//             sampling.rs:8-18): descending value, lowest index on ties
+//   gates     softmax_int over the k selected logits, exp LUT, shift 0,
+//             frac 14 (softmax.rs:24-64)
+//   dispatch  per expert, its (token, slot) pairs in ascending token order
+//   experts   mlp_int (mlp.rs:28-74) with the expert's gate/up/down weights;
+//             output per channel at the layer's output fracs
+//   shared    mlp_int with the shared expert's weights, same output fracs
+//   combine   out = clamp_i16(RNE(sum_k g_k * y_k + 2^14 * s, 14)) in i64
+//             (the weighted sum and single rounding of attention.rs:75-86)
+//
+// Device pipeline: router product (matrix cores) -> top-k + gates + counts ->
+// (counts to the host: offsets and the grouped work tables) -> dispatch
+// (stable, one block per expert) -> gather -> grouped gate/up product ->
+// SiLU gating -> grouped down product -> shared expert (dense products) ->
+// combine.
+#include "gemm_dispatch.h"
+#include "model_internal.h"
+#include "ops.h"
+#include "rows_epi.h"
+#include "wave.h"
+#include "../../include/myl_synth.h"
+
+#include <algorithm>
+#include <vector>
+
+using namespace myl;
+
+struct myl_moe {
+    myl_ctx* ctx = nullptr;
+    myl_moe_spec spec{};
+    int H = 0, E = 0, I = 0, K = 0, S = 0;
+    std::vector<void*> allocs;
+    // weights
+    int8_t* wr = nullptr;          // [E x H]
+    uint8_t* r_shift = nullptr;    // [E]
+    int32_t* r_bias = nullptr;     // [E]
+    int8_t* wgu = nullptr;         // [E][2I x H], gate row r at 2r, up row r at 2r+1
+    uint8_t* sgu = nullptr;        // [E][2I]
+    int8_t* wd = nullptr;          // [E][H x I]
+    uint8_t* sd = nullptr;         // [E][H]
+    int8_t* wgu_s = nullptr;       // shared [2S x H]
+    uint8_t* sgu_s = nullptr;
+    int8_t* wd_s = nullptr;        // shared [H x S]
+    uint8_t* sd_s = nullptr;
+    uint8_t* out_frac = nullptr;   // [H]
+    int16_t *silu = nullptr, *exp_lut = nullptr;
+    int silu_len = 0, exp_len = 0;
+    // per-call buffers (grown on demand)
+    int cap_t = 0;
+    std::vector<void*> bufs;
+    int32_t* logits = nullptr;     // [T x E]
+    int32_t* ids = nullptr;        // [T x K]
+    int32_t* gates = nullptr;      // [T x K]
+    int32_t* counts = nullptr;     // [E]
+    int32_t* offsets = nullptr;    // [E + 1]
+    int32_t* list_tok = nullptr;   // [T x K]
+    int32_t* slotpos = nullptr;    // [T x K]
+    int16_t *Xg = nullptr, *GU = nullptr, *Hh = nullptr, *Y = nullptr;
+    int16_t *GUs = nullptr, *Hs = nullptr, *Sh = nullptr;
+    MmWork* work = nullptr;
+    int work_cap = 0;
+    std::vector<int32_t> counts_host;
+
+    template <class T> T* dalloc(std::vector<void*>& list, size_t count) {
+        void* p = nullptr;
+        if (hipMalloc(&p, count * sizeof(T) ? count * sizeof(T) : 1) != hipSuccess) return nullptr;
+        list.push_back(p);
+        return (T*)p;
+    }
+    ~myl_moe() {
+        if (ctx) (void)hipStreamSynchronize(ctx->stream);
+        for (void* p : bufs) (void)hipFree(p);
+        for (void* p : allocs) (void)hipFree(p);
+        if (work) (void)hipFree(work);
+    }
+};
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// synthetic weights (include/myl_synth.h)
+// ---------------------------------------------------------------------------
+
+// dst row (row * rstride + roff) of a [*, K] matrix from stream tseed (row-major).
+__global__ void moe_gen_kernel(int8_t* __restrict__ dst, int rows, int K, int rstride, int roff, uint64_t tseed) {
+    const int r = blockIdx.y;
+    for (int k = blockIdx.x * blockDim.x + threadIdx.x; k < K; k += gridDim.x * blockDim.x)
+        dst[((size_t)r * rstride + roff) * K + k] = myl_synth_w8(tseed, (uint64_t)r * K + k);
+}
+
+hipError_t gen(myl_moe* m, int8_t* dst, int rows, int K, int rstride, int roff, uint64_t tseed) {
+    for (int r0 = 0; r0 < rows; r0 += 65535) {
+        const int nr = std::min(65535, rows - r0);
+        moe_gen_kernel<<<dim3((unsigned)std::min((K + 255) / 256, 64), (unsigned)nr), 256, 0, m->ctx->stream>>>(
+            dst + (size_t)r0 * rstride * K, nr, K, rstride, roff, tseed);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+__global__ void moe_input_kernel(int16_t* __restrict__ x, size_t n, uint64_t tseed) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        x[i] = myl_synth_gauss16(tseed, i, 2000);
+}
+
+// ---------------------------------------------------------------------------
+// route: bias, top-k, gates, counts
+// ---------------------------------------------------------------------------
+
+// One thread per token.  E <= 256, K <= 16.
+__global__ __launch_bounds__(256) void moe_topk_kernel(const int32_t* __restrict__ logits, int T, int E, int K,
+                                                       const int32_t* __restrict__ bias,
+                                                       const int16_t* __restrict__ lut, uint32_t lut_len,
+                                                       int32_t* __restrict__ ids, int32_t* __restrict__ gates,
+                                                       int32_t* __restrict__ counts) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    const int32_t* z = logits + (size_t)t * E;
+    uint32_t taken[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int32_t sel[16];
+    int sid[16];
+    for (int k = 0; k < K; ++k) {
+        int best = -1;
+        int32_t bv = INT32_MIN;
+        for (int e = 0; e < E; ++e) {
+            if (taken[e >> 5] & (1u << (e & 31))) continue;
+            const int32_t v = clamp_i32_i64((int64_t)z[e] + (int64_t)bias[e]);
+            if (best < 0 || v > bv) { best = e; bv = v; }
+        }
+        taken[best >> 5] |= 1u << (best & 31);
+        sel[k] = bv;
+        sid[k] = best;
+    }
+    // softmax.rs:24-64 over the K selected logits (lut_shift 0, frac 14)
+    const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
+    const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
+    int32_t mx = sel[0];
+    for (int k = 1; k < K; ++k) mx = max(mx, sel[k]);
+    uint32_t s = 0;
+    for (int k = 0; k < K; ++k) s += (uint32_t)exp_lookup(sat_sub32(mx, sel[k]), lut, lut_len, 0, lut_one);
+    const int32_t S = (int32_t)s;
+    for (int k = 0; k < K; ++k) {
+        int32_t g;
+        if (S == 0) {
+            const uint64_t rl = recip32((uint32_t)K);
+            uint32_t qq, rr;
+            udivmod32((uint32_t)one, (uint32_t)K, rl, &qq, &rr);
+            const int32_t base = (int32_t)qq;
+            const int32_t rem = wsub32(one, wmul32(base, K));
+            g = base + ((int64_t)k < (int64_t)rem ? 1 : 0);
+        } else {
+            const uint64_t rs = recip32(S < 0 ? 0u - (uint32_t)S : (uint32_t)S);
+            const int32_t e = exp_lookup(sat_sub32(mx, sel[k]), lut, lut_len, 0, lut_one);
+            g = softmax_div_round(wmul32(e, one), S, rs);
+        }
+        ids[(size_t)t * K + k] = sid[k];
+        gates[(size_t)t * K + k] = g;
+        atomicAdd(counts + sid[k], 1);
+    }
+}
+
+// Stable dispatch: block e lists the tokens routed to expert e in ascending
+// token order at offsets[e].., and records each (token, slot)'s list position.
+__global__ __launch_bounds__(256) void moe_dispatch_kernel(const int32_t* __restrict__ ids, int T, int K,
+                                                           const int32_t* __restrict__ offsets,
+                                                           int32_t* __restrict__ list_tok,
+                                                           int32_t* __restrict__ slotpos) {
+    __shared__ int32_t wsum[4];
+    const int e = blockIdx.x;
+    int32_t run = offsets[e];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int base = 0; base < T; base += 256) {
+        const int t = base + (int)threadIdx.x;
+        int slot = -1;
+        if (t < T)
+            for (int k = 0; k < K; ++k)
+                if (ids[(size_t)t * K + k] == e) slot = k;
+        const uint64_t bal = __ballot(slot >= 0);
+        const int before = __popcll(bal & ((1ull << lane) - 1ull));
+        if (lane == 0) wsum[wave] = __popcll(bal);
+        __syncthreads();
+        int woff = 0, tot = 0;
+        for (int w = 0; w < 4; ++w) {
+            if (w < wave) woff += wsum[w];
+            tot += wsum[w];
+        }
+        if (slot >= 0) {
+            const int p = run + woff + before;
+            list_tok[p] = t;
+            slotpos[(size_t)t * K + slot] = p;
+        }
+        run += tot;
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(256) void moe_gather_kernel(const int16_t* __restrict__ x, int H,
+                                                         const int32_t* __restrict__ list_tok,
+                                                         int16_t* __restrict__ Xg) {
+    const int p = blockIdx.x;
+    const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)list_tok[p] * H);
+    uint4* dst = reinterpret_cast<uint4*>(Xg + (size_t)p * H);
+    for (int i = threadIdx.x; i < H / 8; i += 256) dst[i] = src[i];
+}
+
+// mlp.rs:55-65 per row.
+__global__ __launch_bounds__(256) void moe_silu_kernel(const int16_t* __restrict__ GU, int I,
+                                                       const int16_t* __restrict__ silu, uint32_t silu_len,
+                                                       int16_t* __restrict__ Hh) {
+    const int r = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= I) return;
+    const uint32_t gu = *reinterpret_cast<const uint32_t*>(GU + (size_t)r * 2 * I + 2 * i);
+    const int16_t g = (int16_t)(gu & 0xFFFFu), u = (int16_t)(gu >> 16);
+    const int32_t g_dom = rescale32((int32_t)g, MYL_MOE_GATE_FRAC, MYL_TV_SILU_IN_FRAC);
+    const int16_t act = lut_lookup_i16((int16_t)g_dom, silu, silu_len, (int16_t)MYL_TV_SILU_LUT_OFFSET);
+    const int64_t prod = (int64_t)act * (int64_t)u;
+    Hh[(size_t)r * I + i] = clamp_i16_i64(rescale64(prod, (uint8_t)(MYL_TV_SILU_OUT_FRAC + MYL_MOE_UP_FRAC),
+                                                    MYL_MOE_DOWN_IN_FRAC));
+}
+
+// out = clamp_i16(RNE(sum_k g_k * y_k + 2^14 * s, 14)).  Grid (ceil(H / 256), T).
+__global__ __launch_bounds__(256) void moe_combine_kernel(const int32_t* __restrict__ gates,
+                                                          const int32_t* __restrict__ slotpos, int K,
+                                                          const int16_t* __restrict__ Y, const int16_t* __restrict__ Sh,
+                                                          int H, int16_t* __restrict__ out) {
+    const int t = blockIdx.y;
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= H) return;
+    int64_t acc = (int64_t)Sh[(size_t)t * H + c] * (int64_t)(1 << MYL_TV_PROB_FRAC_BITS);
+    for (int k = 0; k < K; ++k) {
+        const int p = slotpos[(size_t)t * K + k];
+        acc = wadd64(acc, (int64_t)gates[(size_t)t * K + k] * (int64_t)Y[(size_t)p * H + c]);
+    }
+    out[(size_t)t * H + c] = clamp_i16_i64(rshift_round64(acc, MYL_TV_PROB_FRAC_BITS));
+}
+
+// ---------------------------------------------------------------------------
+// grouped epilogues
+// ---------------------------------------------------------------------------
+
+struct EpiExpertGU {
+    const uint8_t* shifts;  // [E][2I]
+    int n2;                 // 2I
+    int16_t* out;           // [rows x 2I]
+    __device__ inline void one(int e, int n, int row, int64_t acc) const {
+        const uint8_t frac = (n & 1) ? MYL_MOE_UP_FRAC : MYL_MOE_GATE_FRAC;
+        out[(size_t)row * n2 + n] =
+            clamp_i16_i64(rescale64(acc, (uint8_t)(shifts[(size_t)e * n2 + n] + MYL_MOE_X_FRAC), frac));
+    }
+};
+
+struct EpiExpertDown {
+    const uint8_t* shifts;    // [E][H]
+    const uint8_t* out_frac;  // [H]
+    int H;
+    int16_t* out;             // [rows x H]
+    __device__ inline void one(int e, int n, int row, int64_t acc) const {
+        out[(size_t)row * H + n] = clamp_i16_i64(
+            rescale64(acc, (uint8_t)(shifts[(size_t)e * H + n] + MYL_MOE_DOWN_IN_FRAC), out_frac[n]));
+    }
+};
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+template <class T>
+int upload(myl_moe* m, T* dst, const std::vector<T>& src) {
+    return m->ctx->hip(hipMemcpyAsync(dst, src.data(), src.size() * sizeof(T), hipMemcpyHostToDevice, m->ctx->stream),
+                       "moe upload");
+}
+
+std::vector<uint8_t> shifts_for(uint64_t seed, uint32_t layer, uint32_t role, size_t rows, size_t K) {
+    std::vector<uint8_t> v(rows);
+    const uint64_t ts = myl_tensor_seed(seed, layer, role);
+    for (size_t r = 0; r < rows; ++r) v[r] = myl_synth_wshift(ts, r, K);
+    return v;
+}
+
+int build(myl_moe* m, const int32_t* router_bias, const myl_luts* luts) {
+    myl_ctx* c = m->ctx;
+    const uint64_t seed = m->spec.seed;
+    const size_t H = m->H, E = m->E, I = m->I, S = m->S;
+    auto& A = m->allocs;
+    m->wr = m->dalloc<int8_t>(A, E * H);
+    m->r_shift = m->dalloc<uint8_t>(A, E);
+    m->r_bias = m->dalloc<int32_t>(A, E);
+    m->wgu = m->dalloc<int8_t>(A, E * 2 * I * H);
+    m->sgu = m->dalloc<uint8_t>(A, E * 2 * I);
+    m->wd = m->dalloc<int8_t>(A, E * H * I);
+    m->sd = m->dalloc<uint8_t>(A, E * H);
+    m->wgu_s = m->dalloc<int8_t>(A, 2 * S * H);
+    m->sgu_s = m->dalloc<uint8_t>(A, 2 * S);
+    m->wd_s = m->dalloc<int8_t>(A, H * S);
+    m->sd_s = m->dalloc<uint8_t>(A, H);
+    m->out_frac = m->dalloc<uint8_t>(A, H);
+    m->silu = m->dalloc<int16_t>(A, luts->silu_len);
+    m->exp_lut = m->dalloc<int16_t>(A, luts->exp_len);
+    m->counts = m->dalloc<int32_t>(A, E);
+    m->offsets = m->dalloc<int32_t>(A, E + 1);
+    for (void* p : A)
+        if (!p) return c->fail(MYL_E_NOMEM, "moe: weight allocation");
+    m->silu_len = (int)luts->silu_len;
+    m->exp_len = (int)luts->exp_len;
+    int rc = 0;
+    rc |= upload(m, m->silu, std::vector<int16_t>(luts->silu, luts->silu + luts->silu_len));
+    rc |= upload(m, m->exp_lut, std::vector<int16_t>(luts->exp, luts->exp + luts->exp_len));
+    rc |= upload(m, m->r_shift, std::vector<uint8_t>(E, (uint8_t)MYL_MOE_ROUTER_SHIFT));
+    rc |= upload(m, m->r_bias, std::vector<int32_t>(router_bias, router_bias + E));
+    std::vector<uint8_t> of(H);
+    for (size_t i = 0; i < H; ++i) of[i] = myl_synth_moe_out_frac(seed, i);
+    rc |= upload(m, m->out_frac, of);
+    if (rc) return rc;
+    hipError_t e = gen(m, m->wr, (int)E, (int)H, 1, 0, myl_tensor_seed(seed, 0, MYL_R_ROUTER));
+    std::vector<uint8_t> sgu(E * 2 * I), sd(E * H);
+    for (size_t x = 0; x <= E && e == hipSuccess; ++x) {  // x == E: the shared expert
+        const bool shared = x == E;
+        const size_t inter = shared ? S : I;
+        int8_t* wgu = shared ? m->wgu_s : m->wgu + x * 2 * I * H;
+        int8_t* wd = shared ? m->wd_s : m->wd + x * H * I;
+        e = gen(m, wgu, (int)inter, (int)H, 2, 0, myl_tensor_seed(seed, (uint32_t)x, MYL_R_WG));
+        if (e == hipSuccess) e = gen(m, wgu, (int)inter, (int)H, 2, 1, myl_tensor_seed(seed, (uint32_t)x, MYL_R_WU));
+        if (e == hipSuccess) e = gen(m, wd, (int)H, (int)inter, 1, 0, myl_tensor_seed(seed, (uint32_t)x, MYL_R_WD));
+        const auto sg = shifts_for(seed, (uint32_t)x, MYL_R_SG, inter, H);
+        const auto su = shifts_for(seed, (uint32_t)x, MYL_R_SU, inter, H);
+        const auto sdv = shifts_for(seed, (uint32_t)x, MYL_R_SD, H, inter);
+        if (shared) {
+            std::vector<uint8_t> s2(2 * S);
+            for (size_t r = 0; r < S; ++r) { s2[2 * r] = sg[r]; s2[2 * r + 1] = su[r]; }
+            rc |= upload(m, m->sgu_s, s2);
+            rc |= upload(m, m->sd_s, sdv);
+        } else {
+            for (size_t r = 0; r < I; ++r) { sgu[x * 2 * I + 2 * r] = sg[r]; sgu[x * 2 * I + 2 * r + 1] = su[r]; }
+            std::copy(sdv.begin(), sdv.end(), sd.begin() + x * H);
+        }
+    }
+    if (e != hipSuccess) return c->hip(e, "moe weight generation");
+    rc |= upload(m, m->sgu, sgu);
+    rc |= upload(m, m->sd, sd);
+    if (rc) return rc;
+    return c->hip(hipStreamSynchronize(c->stream), "moe build");
+}
+
+int ensure(myl_moe* m, int T) {
+    if (T <= m->cap_t) return MYL_OK;
+    myl_ctx* c = m->ctx;
+    (void)hipStreamSynchronize(c->stream);
+    for (void* p : m->bufs) (void)hipFree(p);
+    m->bufs.clear();
+    m->cap_t = 0;
+    const size_t TT = T, H = m->H, E = m->E, I = m->I, S = m->S, R = TT * m->K;
+    auto& B = m->bufs;
+    m->logits = m->dalloc<int32_t>(B, TT * E);
+    m->ids = m->dalloc<int32_t>(B, R);
+    m->gates = m->dalloc<int32_t>(B, R);
+    m->list_tok = m->dalloc<int32_t>(B, R);
+    m->slotpos = m->dalloc<int32_t>(B, R);
+    m->Xg = m->dalloc<int16_t>(B, R * H);
+    m->GU = m->dalloc<int16_t>(B, R * 2 * I);
+    m->Hh = m->dalloc<int16_t>(B, R * I);
+    m->Y = m->dalloc<int16_t>(B, R * H);
+    m->GUs = m->dalloc<int16_t>(B, TT * 2 * S);
+    m->Hs = m->dalloc<int16_t>(B, TT * S);
+    m->Sh = m->dalloc<int16_t>(B, TT * H);
+    for (void* p : B)
+        if (!p) return c->fail(MYL_E_NOMEM, "moe: buffer allocation");
+    m->cap_t = T;
+    return MYL_OK;
+}
+
+// Work table of a grouped product: (expert, m-tile, n-tile), m fastest.
+void work_table(const std::vector<int32_t>& counts, int bm, int bn, int N, std::vector<MmWork>& out) {
+    out.clear();
+    for (int e = 0; e < (int)counts.size(); ++e)
+        for (int n0 = 0; n0 < N; n0 += bn)
+            for (int m0 = 0; m0 < counts[e]; m0 += bm) out.push_back(MmWork{e, m0, n0, 0});
+}
+
+}  // namespace
+
+extern "C" {
+
+int myl_moe_create_synthetic(myl_ctx* ctx, const myl_moe_spec* spec, const int32_t* router_bias, const myl_luts* luts,
+                             myl_moe** out) {
+    if (!ctx || !spec || !router_bias || !luts || !out) return MYL_E_INVALID;
+    *out = nullptr;
+    const myl_moe_spec& s = *spec;
+    if (!s.hidden || !s.n_experts || !s.inter || !s.top_k || !s.shared_inter)
+        return ctx->fail(MYL_E_INVALID, "moe: every dimension must be > 0");
+    if (s.n_experts > 256 || s.top_k > 16 || s.top_k > s.n_experts)
+        return ctx->fail(MYL_E_UNSUPPORTED, "moe: at most 256 experts and top-16");
+    if (s.hidden % 16 || s.inter % 16 || s.shared_inter % 16)
+        return ctx->fail(MYL_E_UNSUPPORTED, "moe: hidden and intermediate sizes must be multiples of 16");
+    if (!luts->silu || !luts->silu_len || !luts->exp || !luts->exp_len) return ctx->fail(MYL_E_INVALID, "moe: LUTs");
+    (void)hipSetDevice(ctx->device);
+    myl_moe* m = new (std::nothrow) myl_moe();
+    if (!m) return MYL_E_NOMEM;
+    m->ctx = ctx;
+    m->spec = s;
+    m->H = (int)s.hidden;
+    m->E = (int)s.n_experts;
+    m->I = (int)s.inter;
+    m->K = (int)s.top_k;
+    m->S = (int)s.shared_inter;
+    int rc = build(m, router_bias, luts);
+    if (rc) {
+        delete m;
+        return rc;
+    }
+    *out = m;
+    return MYL_OK;
+}
+
+void myl_moe_destroy(myl_moe* m) { delete m; }
+
+int myl_moe_synth_input(myl_moe* m, uint32_t n_tokens, int16_t* x_dev) {
+    if (!m || !x_dev) return MYL_E_INVALID;
+    const size_t n = (size_t)n_tokens * m->H;
+    moe_input_kernel<<<(unsigned)std::min<size_t>((n + 255) / 256, 65535), 256, 0, m->ctx->stream>>>(
+        x_dev, n, myl_tensor_seed(m->spec.seed, 0, MYL_R_ACT));
+    return m->ctx->hip(hipGetLastError(), "moe_synth_input");
+}
+
+int myl_moe_forward(myl_moe* m, const int16_t* x_dev, uint32_t n_tokens, int16_t* out_dev) {
+    if (!m || !x_dev || !out_dev) return MYL_E_INVALID;
+    myl_ctx* c = m->ctx;
+    if (n_tokens == 0) return MYL_OK;
+    if (n_tokens > (1u << 24)) return c->fail(MYL_E_INVALID, "moe_forward: too many tokens");
+    if (((uintptr_t)x_dev & 15) || ((uintptr_t)out_dev & 15))
+        return c->fail(MYL_E_INVALID, "moe_forward: x and out must be 16-byte aligned");
+    const int T = (int)n_tokens, H = m->H, E = m->E, I = m->I, K = m->K, S = m->S;
+    int rc = ensure(m, T);
+    if (rc) return rc;
+    hipStream_t st = c->stream;
+    const MmCtx* mm = c->mm_ctx((size_t)T * std::max(E, 2 * S));
+    hipError_t e;
+    // router logits (Q8, the LM-head requant), then top-k, gates and counts
+    EpiLogits el{m->r_shift, (uint8_t)MYL_MOE_X_FRAC, (uint8_t)MYL_MOE_ROUTER_FRAC, m->logits, E};
+    if ((e = gemv_i8(x_dev, T, H, m->wr, E, H, el, st, mm)) != hipSuccess) return c->hip(e, "moe router");
+    if ((e = hipMemsetAsync(m->counts, 0, (size_t)E * 4, st)) != hipSuccess) return c->hip(e, "moe counts");
+    moe_topk_kernel<<<(T + 255) / 256, 256, 0, st>>>(m->logits, T, E, K, m->r_bias, m->exp_lut, (uint32_t)m->exp_len,
+                                                     m->ids, m->gates, m->counts);
+    if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe top-k");
+    m->counts_host.assign(E, 0);
+    rc = c->hip(hipMemcpyAsync(m->counts_host.data(), m->counts, (size_t)E * 4, hipMemcpyDeviceToHost, st), "counts");
+    if (!rc) rc = c->hip(hipStreamSynchronize(st), "counts");
+    if (rc) return rc;
+    std::vector<int32_t> offs(E + 1, 0);
+    for (int x = 0; x < E; ++x) offs[x + 1] = offs[x] + m->counts_host[x];
+    // grouped work tables: gate/up (N = 2I) and down (N = H), 64 x 128 tiles
+    using GT = MmShape<1, 2, 2, 2>;
+    std::vector<MmWork> wgu, wdn;
+    work_table(m->counts_host, GT::BM, GT::BN, 2 * I, wgu);
+    work_table(m->counts_host, GT::BM, GT::BN, H, wdn);
+    const int need = (int)(wgu.size() + wdn.size());
+    if (need > m->work_cap) {
+        if (m->work) (void)hipFree(m->work);
+        m->work = nullptr;
+        m->work_cap = 0;
+        if (hipMalloc(&m->work, (size_t)need * sizeof(MmWork)) != hipSuccess) return c->fail(MYL_E_NOMEM, "moe work");
+        m->work_cap = need;
+    }
+    std::vector<MmWork> all(wgu);
+    all.insert(all.end(), wdn.begin(), wdn.end());
+    rc = c->hip(hipMemcpyAsync(m->work, all.data(), all.size() * sizeof(MmWork), hipMemcpyHostToDevice, st), "work");
+    if (!rc) rc = c->hip(hipMemcpyAsync(m->offsets, offs.data(), offs.size() * 4, hipMemcpyHostToDevice, st), "offs");
+    if (rc) return rc;
+    // dispatch (stable), gather, grouped experts
+    moe_dispatch_kernel<<<E, 256, 0, st>>>(m->ids, T, K, m->offsets, m->list_tok, m->slotpos);
+    const int R = T * K;
+    moe_gather_kernel<<<R, 256, 0, st>>>(x_dev, H, m->list_tok, m->Xg);
+    if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe dispatch");
+    if (!wgu.empty()) {
+        EpiExpertGU eg{m->sgu, 2 * I, m->GU};
+        mm_w8_grouped_kernel<1, 2, 2, 2, EpiExpertGU><<<8 * (((int)wgu.size() + 7) / 8), GT::kThreads, GT::kLds, st>>>(
+            m->Xg, H, m->wgu, (size_t)2 * I * H, 2 * I, H, m->offsets, m->work, (int)wgu.size(), eg);
+        if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe gate/up");
+        moe_silu_kernel<<<dim3((I + 255) / 256, R), 256, 0, st>>>(m->GU, I, m->silu, (uint32_t)m->silu_len, m->Hh);
+        EpiExpertDown ed{m->sd, m->out_frac, H, m->Y};
+        mm_w8_grouped_kernel<1, 2, 2, 2, EpiExpertDown><<<8 * (((int)wdn.size() + 7) / 8), GT::kThreads, GT::kLds, st>>>(
+            m->Hh, I, m->wd, (size_t)H * I, H, I, m->offsets, m->work + wgu.size(), (int)wdn.size(), ed);
+        if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe down");
+    }
+    // shared expert: dense products over every token
+    EpiGURows egs{};
+    egs.shifts = m->sgu_s; egs.act_frac = MYL_MOE_X_FRAC; egs.gate_frac = MYL_MOE_GATE_FRAC;
+    egs.up_frac = MYL_MOE_UP_FRAC; egs.out = m->GUs; egs.ldo = 2 * S;
+    if ((e = gemv_i8(x_dev, T, H, m->wgu_s, 2 * S, H, egs, st, mm)) != hipSuccess) return c->hip(e, "shared gate/up");
+    moe_silu_kernel<<<dim3((S + 255) / 256, T), 256, 0, st>>>(m->GUs, S, m->silu, (uint32_t)m->silu_len, m->Hs);
+    EpiShift eds{m->sd_s, m->out_frac, (uint8_t)MYL_MOE_DOWN_IN_FRAC, 0, m->Sh, H};
+    if ((e = gemv_i8(m->Hs, T, S, m->wd_s, H, S, eds, st, mm)) != hipSuccess) return c->hip(e, "shared down");
+    moe_combine_kernel<<<dim3((H + 255) / 256, T), 256, 0, st>>>(m->gates, m->slotpos, K, m->Y, m->Sh, H, out_dev);
+    return c->hip(hipGetLastError(), "moe combine");
+}
+
+int myl_moe_read_route(myl_moe* m, uint32_t n_tokens, int32_t* ids, int32_t* gates, int32_t* counts, int32_t* offsets,
+                       int32_t* list_tok) {
+    if (!m) return MYL_E_INVALID;
+    myl_ctx* c = m->ctx;
+    if ((int)n_tokens > m->cap_t) return c->fail(MYL_E_INVALID, "moe_read_route: more tokens than the last call");
+    const size_t R = (size_t)n_tokens * m->K;
+    hipStream_t st = c->stream;
+    int rc = 0;
+    if (ids) rc = c->hip(hipMemcpyAsync(ids, m->ids, R * 4, hipMemcpyDeviceToHost, st), "ids");
+    if (!rc && gates) rc = c->hip(hipMemcpyAsync(gates, m->gates, R * 4, hipMemcpyDeviceToHost, st), "gates");
+    if (!rc && counts) rc = c->hip(hipMemcpyAsync(counts, m->counts, (size_t)m->E * 4, hipMemcpyDeviceToHost, st), "counts");
+    if (!rc && offsets)
+        rc = c->hip(hipMemcpyAsync(offsets, m->offsets, (size_t)(m->E + 1) * 4, hipMemcpyDeviceToHost, st), "offsets");
+    if (!rc && list_tok) rc = c->hip(hipMemcpyAsync(list_tok, m->list_tok, R * 4, hipMemcpyDeviceToHost, st), "list");
+    if (rc) return rc;
+    return c->hip(hipStreamSynchronize(st), "moe_read_route");
+}
+
+}  // extern "C"

@@ -46,6 +46,11 @@ class SynthSpec(C.Structure):
                 ("lm_head_int16", i32), ("attention_bias", i32)]
 
 
+class MoeSpec(C.Structure):
+    _fields_ = [("seed", u64), ("hidden", u32), ("n_experts", u32), ("inter", u32), ("top_k", u32),
+                ("shared_inter", u32)]
+
+
 class Luts(C.Structure):
     _fields_ = [("rsqrt", P), ("rsqrt_len", sz), ("silu", P), ("silu_len", sz), ("exp", P),
                 ("exp_len", sz), ("cos", P), ("sin", P), ("rope_len", sz)]
@@ -81,6 +86,13 @@ def _declare(L) -> None:
         "or_ln_q16": (i64, [u64]),
         "or_logsoftmax_at": (i64, [P, sz, P, sz, i64]),
         "or_model_create_synthetic": (P, [C.POINTER(SynthSpec), C.POINTER(Luts)]),
+        "or_moe_create_synthetic": (P, [C.POINTER(MoeSpec), P, C.POINTER(Luts)]),
+        "or_moe_destroy": (None, [P]),
+        "or_moe_synth_input": (None, [P, u32, P]),
+        "or_moe_route": (C.c_int, [P, P, u32, P, P, P, P, P]),
+        "or_moe_token": (C.c_int, [P, P, P, P, P]),
+        "or_moe_expert": (C.c_int, [P, P, u32, P]),
+        "or_moe_router_logits": (None, [P, P, P]),
         "or_model_destroy": (None, [P]), "or_model_reset": (None, [P]),
         "or_set_threads": (None, [C.c_int]),
         "or_model_forward_token": (C.c_int, [P, u32, u32, P]),
@@ -337,3 +349,63 @@ class OracleModel:
             raise KeyError(name)
         buf = (C.c_char * n.value).from_address(p)
         return np.frombuffer(bytes(buf), dtype=dtype)
+
+
+class OracleMoe:
+    """The build-defined integer MoE layer (include/myl_hip.h section 4) on the CPU."""
+
+    def __init__(self, spec: dict, bias, luts, threads: int = 1):
+        self.spec = dict(spec)
+        self._cspec = MoeSpec(**{k: int(spec[k]) for k, _ in MoeSpec._fields_})
+        self._luts, self._keep = make_luts_struct(luts)
+        self.bias = _arr(bias, np.int32)
+        lib().or_set_threads(threads)
+        self._h = lib().or_moe_create_synthetic(C.byref(self._cspec), ptr(self.bias), C.byref(self._luts))
+        if not self._h:
+            raise ValueError("oracle MoE creation failed")
+
+    def close(self) -> None:
+        if self._h:
+            lib().or_moe_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def synth_input(self, n_tokens: int) -> np.ndarray:
+        x = np.zeros((n_tokens, self.spec["hidden"]), np.int16)
+        lib().or_moe_synth_input(self._h, n_tokens, ptr(x))
+        return x
+
+    def route(self, x) -> dict:
+        x = _arr(x, np.int16)
+        T = x.shape[0]
+        K, E = self.spec["top_k"], self.spec["n_experts"]
+        ids = np.zeros((T, K), np.int32)
+        gates = np.zeros((T, K), np.int32)
+        counts = np.zeros(E, np.int32)
+        offsets = np.zeros(E + 1, np.int32)
+        lst = np.zeros(T * K, np.int32)
+        _check(lib().or_moe_route(self._h, ptr(x), T, ptr(ids), ptr(gates), ptr(counts), ptr(offsets), ptr(lst)),
+               "moe_route")
+        return dict(ids=ids, gates=gates, counts=counts, offsets=offsets, list_tok=lst)
+
+    def token(self, xt, ids_t, gates_t) -> np.ndarray:
+        out = np.zeros(self.spec["hidden"], np.int16)
+        _check(lib().or_moe_token(self._h, ptr(_arr(xt, np.int16)), ptr(_arr(ids_t, np.int32)),
+                                  ptr(_arr(gates_t, np.int32)), ptr(out)), "moe_token")
+        return out
+
+    def expert(self, xt, expert: int) -> np.ndarray:
+        out = np.zeros(self.spec["hidden"], np.int16)
+        _check(lib().or_moe_expert(self._h, ptr(_arr(xt, np.int16)), expert, ptr(out)), "moe_expert")
+        return out
+
+    def router_logits(self, xt) -> np.ndarray:
+        z = np.zeros(self.spec["n_experts"], np.int32)
+        lib().or_moe_router_logits(self._h, ptr(_arr(xt, np.int16)), ptr(z))
+        return z
+

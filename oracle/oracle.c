@@ -859,3 +859,194 @@ const void* or_model_tensor(const or_model* m, const char* name, uint32_t layer,
     if (!strcmp(name, "final_norm_frac")) { *bytes = 1; return &m->final_norm_frac; }
     return NULL;
 }
+
+/* ---- integer MoE layer (build-defined; the reference has no MoE) ---------
+ * The definition the GPU layer implements (include/myl_hip.h, section 4),
+ * restated with the reference primitives above: router logits by the LM-head
+ * requant plus an integer bias, top-k by repeated first maxima, softmax_int
+ * gates, mlp_int experts, one i64 weighted sum and one rounding. */
+struct or_moe {
+    myl_moe_spec spec;
+    int8_t* wr;          /* [E x H] */
+    int32_t* bias;       /* [E] */
+    int8_t *wg, *wu, *wd;          /* per expert and shared (index E): [I x H], [I x H], [H x I] */
+    uint8_t *sg, *su, *sd;
+    size_t* woff;        /* element offset of expert x's gate/up and down matrices */
+    size_t* soff;        /* offset of expert x's gate/up shifts; down shifts at x * H */
+    uint8_t* out_frac;   /* [H] */
+    int16_t* silu; size_t silu_len;
+    int16_t* exp_lut; size_t exp_len;
+};
+
+static void moe_fill_w8(int8_t* dst, size_t rows, size_t K, uint64_t tseed) {
+    size_t n = rows * K;
+#pragma omp parallel for schedule(static) if (n > (1 << 20))
+    for (size_t i = 0; i < n; ++i) dst[i] = myl_synth_w8(tseed, i);
+}
+
+void or_moe_destroy(or_moe* m) {
+    if (!m) return;
+    free(m->wr); free(m->bias); free(m->wg); free(m->wu); free(m->wd);
+    free(m->sg); free(m->su); free(m->sd); free(m->woff); free(m->soff);
+    free(m->out_frac); free(m->silu); free(m->exp_lut);
+    free(m);
+}
+
+or_moe* or_moe_create_synthetic(const myl_moe_spec* spec, const int32_t* router_bias, const myl_luts* luts) {
+    const size_t H = spec->hidden, E = spec->n_experts, I = spec->inter, S = spec->shared_inter;
+    if (!H || !E || !I || !S || !spec->top_k || spec->top_k > E) return NULL;
+    or_moe* m = (or_moe*)calloc(1, sizeof(or_moe));
+    if (!m) return NULL;
+    m->spec = *spec;
+    const uint64_t seed = spec->seed;
+    size_t wtot = 0, stot = 0;
+    m->woff = (size_t*)malloc((E + 1) * sizeof(size_t));
+    m->soff = (size_t*)malloc((E + 1) * sizeof(size_t));
+    for (size_t x = 0; x <= E; ++x) {
+        const size_t inter = x == E ? S : I;
+        m->woff[x] = wtot;
+        m->soff[x] = stot;
+        wtot += inter * H;
+        stot += inter;
+    }
+    m->wr = (int8_t*)malloc(E * H);
+    m->bias = (int32_t*)malloc(E * sizeof(int32_t));
+    m->wg = (int8_t*)malloc(wtot);
+    m->wu = (int8_t*)malloc(wtot);
+    m->wd = (int8_t*)malloc(wtot);
+    m->sg = (uint8_t*)malloc(stot);
+    m->su = (uint8_t*)malloc(stot);
+    m->sd = (uint8_t*)malloc((E + 1) * H);
+    m->out_frac = (uint8_t*)malloc(H);
+    m->silu = (int16_t*)malloc(luts->silu_len * sizeof(int16_t));
+    m->exp_lut = (int16_t*)malloc(luts->exp_len * sizeof(int16_t));
+    if (!m->woff || !m->soff || !m->wr || !m->bias || !m->wg || !m->wu || !m->wd || !m->sg || !m->su || !m->sd ||
+        !m->out_frac || !m->silu || !m->exp_lut) {
+        or_moe_destroy(m);
+        return NULL;
+    }
+    memcpy(m->bias, router_bias, E * sizeof(int32_t));
+    memcpy(m->silu, luts->silu, luts->silu_len * sizeof(int16_t));
+    memcpy(m->exp_lut, luts->exp, luts->exp_len * sizeof(int16_t));
+    m->silu_len = luts->silu_len;
+    m->exp_len = luts->exp_len;
+    moe_fill_w8(m->wr, E, H, myl_tensor_seed(seed, 0, MYL_R_ROUTER));
+    for (size_t i = 0; i < H; ++i) m->out_frac[i] = myl_synth_moe_out_frac(seed, i);
+    for (size_t x = 0; x <= E; ++x) {
+        const size_t inter = x == E ? S : I;
+        moe_fill_w8(m->wg + m->woff[x], inter, H, myl_tensor_seed(seed, (uint32_t)x, MYL_R_WG));
+        moe_fill_w8(m->wu + m->woff[x], inter, H, myl_tensor_seed(seed, (uint32_t)x, MYL_R_WU));
+        moe_fill_w8(m->wd + m->woff[x], H, inter, myl_tensor_seed(seed, (uint32_t)x, MYL_R_WD));
+        const uint64_t tg = myl_tensor_seed(seed, (uint32_t)x, MYL_R_SG), tu = myl_tensor_seed(seed, (uint32_t)x, MYL_R_SU),
+                       td = myl_tensor_seed(seed, (uint32_t)x, MYL_R_SD);
+        for (size_t r = 0; r < inter; ++r) {
+            m->sg[m->soff[x] + r] = myl_synth_wshift(tg, r, H);
+            m->su[m->soff[x] + r] = myl_synth_wshift(tu, r, H);
+        }
+        for (size_t r = 0; r < H; ++r) m->sd[x * H + r] = myl_synth_wshift(td, r, inter);
+    }
+    return m;
+}
+
+void or_moe_synth_input(const or_moe* m, uint32_t T, int16_t* x) {
+    const size_t n = (size_t)T * m->spec.hidden;
+    const uint64_t ts = myl_tensor_seed(m->spec.seed, 0, MYL_R_ACT);
+#pragma omp parallel for schedule(static) if (n > (1 << 16))
+    for (size_t i = 0; i < n; ++i) x[i] = myl_synth_gauss16(ts, i, 2000);
+}
+
+/* Router, top-k and gates of every token; counts, offsets and the stable
+ * expert-major token lists.  Any output may be NULL except ids and gates. */
+int or_moe_route(const or_moe* m, const int16_t* x, uint32_t T, int32_t* ids, int32_t* gates, int32_t* counts,
+                 int32_t* offsets, int32_t* list_tok) {
+    const size_t H = m->spec.hidden, E = m->spec.n_experts, K = m->spec.top_k;
+    int rc = 0;
+#pragma omp parallel for schedule(static) if (g_threads > 1) num_threads(g_threads)
+    for (uint32_t t = 0; t < T; ++t) {
+        const int16_t* xt = x + (size_t)t * H;
+        int32_t z[256], sel[16], g[16];
+        int taken[256];
+        for (size_t e = 0; e < E; ++e) {
+            int64_t d = or_dot_i8_i16(m->wr + e * H, xt, H);
+            int32_t r = or_clamp_i32(or_rescale_i64(d, MYL_MOE_ROUTER_SHIFT + MYL_MOE_X_FRAC, MYL_MOE_ROUTER_FRAC));
+            z[e] = or_clamp_i32((int64_t)r + (int64_t)m->bias[e]);
+            taken[e] = 0;
+        }
+        for (size_t k = 0; k < K; ++k) {
+            size_t best = E;
+            for (size_t e = 0; e < E; ++e)
+                if (!taken[e] && (best == E || z[e] > z[best])) best = e;
+            taken[best] = 1;
+            sel[k] = z[best];
+            ids[(size_t)t * K + k] = (int32_t)best;
+        }
+        if (or_softmax_int(sel, K, m->exp_lut, m->exp_len, 0, MYL_TV_PROB_FRAC_BITS, g)) rc = -1;
+        for (size_t k = 0; k < K; ++k) gates[(size_t)t * K + k] = g[k];
+    }
+    if (rc) return rc;
+    if (counts || offsets || list_tok) {
+        int32_t* c = (int32_t*)calloc(E, sizeof(int32_t));
+        if (!c) return -3;
+        for (size_t i = 0; i < (size_t)T * K; ++i) c[ids[i]]++;
+        if (counts) memcpy(counts, c, E * sizeof(int32_t));
+        int32_t run = 0;
+        for (size_t e = 0; e < E; ++e) {
+            if (offsets) offsets[e] = run;
+            if (list_tok)
+                for (uint32_t t = 0; t < T; ++t)
+                    for (size_t k = 0; k < K; ++k)
+                        if ((size_t)ids[(size_t)t * K + k] == e) list_tok[run++] = (int32_t)t;
+            if (!list_tok) run += c[e];
+        }
+        if (offsets) offsets[E] = run;
+        free(c);
+    }
+    return 0;
+}
+
+/* The layer's output for one token given its route (ids, gates). */
+int or_moe_token(const or_moe* m, const int16_t* xt, const int32_t* ids_t, const int32_t* gates_t, int16_t* out) {
+    const size_t H = m->spec.hidden, E = m->spec.n_experts, K = m->spec.top_k;
+    int16_t* y = (int16_t*)malloc(H * sizeof(int16_t));
+    int64_t* acc = (int64_t*)malloc(H * sizeof(int64_t));
+    if (!y || !acc) { free(y); free(acc); return -3; }
+    int rc = 0;
+    for (size_t k = 0; k <= K && !rc; ++k) {  /* k == K: the shared expert */
+        const size_t x = k == K ? E : (size_t)ids_t[k];
+        const size_t inter = x == E ? m->spec.shared_inter : m->spec.inter;
+        rc = or_mlp_int(xt, m->wg + m->woff[x], m->wu + m->woff[x], m->wd + m->woff[x], H, inter,
+                        m->sg + m->soff[x], m->su + m->soff[x], m->sd + x * H, m->silu, m->silu_len, MYL_MOE_X_FRAC,
+                        MYL_MOE_GATE_FRAC, MYL_MOE_UP_FRAC, MYL_MOE_DOWN_IN_FRAC, MYL_TV_SILU_IN_FRAC,
+                        MYL_TV_SILU_LUT_OFFSET, MYL_TV_SILU_OUT_FRAC, m->out_frac, y);
+        for (size_t c = 0; c < H && !rc; ++c) {
+            const int64_t w = k == K ? (int64_t)1 << MYL_TV_PROB_FRAC_BITS : (int64_t)gates_t[k];
+            const int64_t term = mul64(w, (int64_t)y[c]);
+            acc[c] = k == 0 ? term : add64(acc[c], term);
+        }
+    }
+    if (!rc)
+        for (size_t c = 0; c < H; ++c) out[c] = or_clamp_i16_from_i64(or_rshift_round_i64(acc[c], MYL_TV_PROB_FRAC_BITS));
+    free(y); free(acc);
+    return rc;
+}
+
+/* One expert's mlp_int output (x == n_experts: the shared expert), for tests. */
+int or_moe_expert(const or_moe* m, const int16_t* xt, uint32_t expert, int16_t* out) {
+    const size_t H = m->spec.hidden, E = m->spec.n_experts;
+    if (expert > E) return -1;
+    const size_t inter = expert == E ? m->spec.shared_inter : m->spec.inter;
+    return or_mlp_int(xt, m->wg + m->woff[expert], m->wu + m->woff[expert], m->wd + m->woff[expert], H, inter,
+                      m->sg + m->soff[expert], m->su + m->soff[expert], m->sd + expert * H, m->silu, m->silu_len,
+                      MYL_MOE_X_FRAC, MYL_MOE_GATE_FRAC, MYL_MOE_UP_FRAC, MYL_MOE_DOWN_IN_FRAC, MYL_TV_SILU_IN_FRAC,
+                      MYL_TV_SILU_LUT_OFFSET, MYL_TV_SILU_OUT_FRAC, m->out_frac, out);
+}
+
+/* Router logits (after the bias) of one token, for tests. */
+void or_moe_router_logits(const or_moe* m, const int16_t* xt, int32_t* z) {
+    const size_t H = m->spec.hidden, E = m->spec.n_experts;
+    for (size_t e = 0; e < E; ++e) {
+        int64_t d = or_dot_i8_i16(m->wr + e * H, xt, H);
+        int32_t r = or_clamp_i32(or_rescale_i64(d, MYL_MOE_ROUTER_SHIFT + MYL_MOE_X_FRAC, MYL_MOE_ROUTER_FRAC));
+        z[e] = or_clamp_i32((int64_t)r + (int64_t)m->bias[e]);
+    }
+}

@@ -129,6 +129,17 @@ int or_model_read_kv(const or_model* m, uint32_t layer, uint32_t kv_head, uint32
 /* Raw tensor access for tests (NULL if the name is unknown). */
 const void* or_model_tensor(const or_model* m, const char* name, uint32_t layer, size_t* bytes);
 
+/* ---- integer MoE layer (build-defined; include/myl_hip.h section 4) ---- */
+typedef struct or_moe or_moe;
+or_moe* or_moe_create_synthetic(const myl_moe_spec* spec, const int32_t* router_bias, const myl_luts* luts);
+void or_moe_destroy(or_moe* m);
+void or_moe_synth_input(const or_moe* m, uint32_t T, int16_t* x);
+int or_moe_route(const or_moe* m, const int16_t* x, uint32_t T, int32_t* ids, int32_t* gates, int32_t* counts,
+                 int32_t* offsets, int32_t* list_tok);
+int or_moe_token(const or_moe* m, const int16_t* xt, const int32_t* ids_t, const int32_t* gates_t, int16_t* out);
+int or_moe_expert(const or_moe* m, const int16_t* xt, uint32_t expert, int16_t* out);
+void or_moe_router_logits(const or_moe* m, const int16_t* xt, int32_t* z);
+
 #ifdef __cplusplus
 }
 #endif
