@@ -284,6 +284,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--no-batch", action="store_true", help="skip the batched decode and teacher-forced prefill")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="also run three 256 MiB device-to-device copies: the known-size kernel that calibrates "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -354,6 +357,14 @@ def main() -> int:
     if not args.no_gemv:
         gemv = w8a16_sweep(backend, [(3584, 3584), (18944, 3584), (3584, 18944), (152064, 3584)])
 
+    if args.traffic_probe:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     prefill_tf, batch_dec, moe = None, None, None
     if not args.no_batch:
         prefill_tf = teacher_forced_prefill(model, backend, args.seed)
@@ -363,6 +374,17 @@ def main() -> int:
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(spec, model, [int(t) for t in prompt[:4]], 12)
+
+    # HBM bytes per launch of the dominant kernel, measured by two rocprofv3
+    # PMC passes (FETCH_SIZE, WRITE_SIZE) scaled by a known-size copy; see
+    # profiles/decode_7b_pmc_traffic.md for the commands and calibration.
+    traffic, traffic_src = None, None
+    tp = ROOT / "profiles" / "decode_7b_pmc_traffic.json"
+    if tp.exists():
+        tk = json.loads(tp.read_text())["kernels"].get(dom)
+        if tk:
+            traffic = tk["traffic_bytes"]
+            traffic_src = "profiles/decode_7b_pmc_traffic.json: FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (copy-calibrated)"
 
     step_bytes = 28 * (cb["qkv"] + cb["o_proj"] + cb["gate_up"] + cb["down"]) + cb["lm_head"]
     kv_bytes = 2 * spec["layers"] * spec["kv_heads"] * spec["head_dim"] * 2 * (pos + args.steps // 2)
@@ -386,7 +408,7 @@ def main() -> int:
         "decode_GBps": round((step_bytes + kv_bytes) / (ms_step * 1e-3) / 1e9, 1),
         "roofline": {"bound": "hbm", "kernel": f"{dom} W8A16 GEMV in decode (M=1)",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
                      "bytes_per_launch": cb[dom], "avg_us": per_class[dom]["avg_us"]},
         "kernel_classes": per_class,
         "w8a16_sweep": gemv,
