@@ -72,7 +72,9 @@ __device__ inline void stream_epilogue(const int64_t* rec, int g0, int nw, int c
 
 // gpw: the most groups any wave of the grid handles, ceil(ceil(N/R) / waves);
 // the launcher sizes the records from it.
-template <int R, int U, int WAVES, class Src, class Epi>
+// PF2: both register buffers are loaded before the activations are staged, so
+// two batches stream while a slow staging source (RMSNorm) runs.
+template <int R, int U, int WAVES, class Src, class Epi, bool PF2 = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_i8_stream(Src src, const int8_t* __restrict__ W, int N, int K,
                                                             int gpw, Epi epi) {
     extern __shared__ __align__(16) int8_t lds[];
@@ -160,25 +162,55 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i8_stream(Src src, const int8
     auto advance = [&](int& gg, int& kk) {
         if (++kk == nb) { kk = 0; gg += nw; }
     };
-    load(A, g, 0);
-    src.stage_i8(hi_plane, lo_plane, K, kpad);
-    __syncthreads();
-    reset();
-    while (g < ngroups) {
+    if (PF2) {
+        // A and B both in flight during staging; each round consumes A then
+        // B and reloads both two batches ahead.
         int g1 = g, kb1 = kb;
         advance(g1, kb1);
+        load(A, g, 0);
         load(B, g1, kb1);
-        compute(A, kb);
-        if (kb == nb - 1) finish_group();
-        int g2 = g1, kb2 = kb1;
-        advance(g2, kb2);
-        load(A, g2, kb2);
-        if (g1 < ngroups) {
-            compute(B, kb1);
-            if (kb1 == nb - 1) finish_group();
+        src.stage_i8(hi_plane, lo_plane, K, kpad);
+        __syncthreads();
+        reset();
+        while (g < ngroups) {
+            compute(A, kb);
+            if (kb == nb - 1) finish_group();
+            int g2 = g1, kb2 = kb1;
+            advance(g2, kb2);
+            load(A, g2, kb2);
+            if (g1 < ngroups) {
+                compute(B, kb1);
+                if (kb1 == nb - 1) finish_group();
+            }
+            int g3 = g2, kb3 = kb2;
+            advance(g3, kb3);
+            load(B, g3, kb3);
+            g = g2;
+            kb = kb2;
+            g1 = g3;
+            kb1 = kb3;
         }
-        g = g2;
-        kb = kb2;
+    } else {
+        load(A, g, 0);
+        src.stage_i8(hi_plane, lo_plane, K, kpad);
+        __syncthreads();
+        reset();
+        while (g < ngroups) {
+            int g1 = g, kb1 = kb;
+            advance(g1, kb1);
+            load(B, g1, kb1);
+            compute(A, kb);
+            if (kb == nb - 1) finish_group();
+            int g2 = g1, kb2 = kb1;
+            advance(g2, kb2);
+            load(A, g2, kb2);
+            if (g1 < ngroups) {
+                compute(B, kb1);
+                if (kb1 == nb - 1) finish_group();
+            }
+            g = g2;
+            kb = kb2;
+        }
     }
     stream_epilogue<R>(rec, g0, nw, cnt, N, lane, epi, es);
     epi.finish(es);

@@ -113,8 +113,38 @@ __device__ inline uint32_t bitlen128(myl_u128 v) {
     return hi ? 128u - (uint32_t)__builtin_clzll(hi) : (lo ? 64u - (uint32_t)__builtin_clzll(lo) : 0u);
 }
 
+// The same factor in 64-bit arithmetic when the sum and m = (sum * inv_n) >> 20
+// fit (always, for int16 inputs with fractional-bit spreads below 16): the
+// i128 emulation is the slow part of the serial setup every block runs.
+__device__ inline bool rms_factor_u64(myl_i128 acc, uint8_t ref, const RmsParams& p, RmsFactor& f) {
+    const uint64_t hi = (uint64_t)((myl_u128)acc >> 64), lo = (uint64_t)acc;
+    if (hi != 0 || (lo >> 63) != 0) return false;
+    const uint64_t ph = __umul64hi(lo, (uint64_t)p.inv_n_q20), pl = lo * (uint64_t)p.inv_n_q20;
+    if ((ph >> 20) != 0 || p.inv_n_q20 < 0) return false;
+    f.ref_shift = ref;
+    f.zero = lo == 0;
+    f.lut_val = 0;
+    f.norm_frac = 0;
+    if (!f.zero) {
+        const uint64_t m = (ph << 44) | (pl >> 20);
+        const uint64_t max_idx = (uint64_t)(p.lut_len - 1);
+        uint32_t q = 0;
+        if (m > 0) {
+            const uint32_t bm = 64u - (uint32_t)__builtin_clzll(m), bi = 64u - (uint32_t)__builtin_clzll(max_idx | 1u);
+            if (bm > bi + 2) q = (bm - bi - 2) & ~1u;
+        }
+        while ((m >> q) > max_idx) q += 2;
+        int64_t idx = rshift_round64((int64_t)m, (uint8_t)q);
+        if (idx > (int64_t)max_idx) idx = (int64_t)max_idx;
+        f.lut_val = (int64_t)p.lut[(int)idx];
+        f.norm_frac = (uint32_t)p.lut_output_frac + (uint32_t)p.lut_input_shift / 2u + q / 2u;
+    }
+    return true;
+}
+
 __device__ inline RmsFactor rms_factor_from_acc(myl_i128 acc, uint8_t ref, const RmsParams& p) {
     RmsFactor f;
+    if (rms_factor_u64(acc, ref, p, f)) return f;
     f.ref_shift = ref;
     f.zero = acc == 0;
     f.lut_val = 0;
@@ -506,11 +536,11 @@ int stream_grid(Kern kern, int waves_per_block, size_t lds, int ngroups, int cus
 constexpr int kGpwReserve = 16;
 constexpr size_t kStreamLdsMax = 64 * 1024;
 
-template <int R, int U, int WAVES, class Src, class Epi>
+template <int R, int U, int WAVES, bool PF2 = false, class Src, class Epi>
 hipError_t stream_i8(const Src& src, const int8_t* W, int N, int K, const Epi& e, hipStream_t s, int cus) {
     // one buffer descriptor; i32 partial sums exact for K < 131072
     if ((uint64_t)N * (uint64_t)K > 0xFFFFFF00ull || K >= 131072 || N < 1 || K < 1) return hipErrorInvalidValue;
-    auto kern = gemv_i8_stream<R, U, WAVES, Src, Epi>;
+    auto kern = gemv_i8_stream<R, U, WAVES, Src, Epi, PF2>;
     int gpw = 0;
     const int grid = stream_grid(kern, WAVES, stream_lds_bytes(K, 1, WAVES, kGpwReserve, R), (N + R - 1) / R, cus, &gpw);
     const size_t lds = stream_lds_bytes(K, 1, WAVES, gpw, R);
@@ -1038,7 +1068,7 @@ hipError_t layer_step(myl_model* m, int l) {
         SrcNorm src{m->hidden, L.res_in, L.in_gamma, L.in_gamma_s, rp, L.ref_in, f.norm_attn_frac, m->norm_a};
         {
             TimedScope t(m, K_QKV);
-            e = stream_i8<2, 2, 4>(src, L.wqkv, nq + 2 * nkv, H, q, st, cus);
+            e = stream_i8<2, 2, 16>(src, L.wqkv, nq + 2 * nkv, H, q, st, cus);
         }
         if (e != hipSuccess) return e;
         TimedScope ta(m, K_ATTN);
@@ -1076,7 +1106,7 @@ hipError_t layer_step(myl_model* m, int l) {
         SrcNorm src{m->resid, L.res_mid, L.post_gamma, L.post_gamma_s, rp, L.ref_mid, f.norm_mlp_frac, m->norm_b};
         EpiSilu s{L.sgu, f.norm_mlp_frac, f.gate_frac, f.up_frac, f.down_in_frac, m->silu, (uint32_t)m->silu_len, m->h,
                   m->attn_acc, nq};
-        e = stream_i8<2, 4, 4>(src, L.wgu, 2 * I, H, s, st, cus);
+        e = stream_i8<2, 4, 8, true>(src, L.wgu, 2 * I, H, s, st, cus);
     }
     if (e != hipSuccess) return e;
     {
@@ -1097,10 +1127,10 @@ hipError_t head_step(myl_model* m) {
                 m->final_norm_frac, m->norm_a};
     if (m->spec.lm_head_int16) {
         EpiHead hd{m->lm16_shifts, m->final_norm_frac, m->logits, m->state};
-        return stream_i16<2, 4, 4>(src, m->lm16, m->V, m->H, hd, st, m->cus);
+        return stream_i16<2, 4, 8>(src, m->lm16, m->V, m->H, hd, st, m->cus);
     }
     EpiHead hd{m->emb_shifts, m->final_norm_frac, m->logits, m->state};
-    return stream_i8<2, 4, 4>(src, m->emb, m->V, m->H, hd, st, m->cus);
+    return stream_i8<2, 4, 8, true>(src, m->emb, m->V, m->H, hd, st, m->cus);
 }
 
 hipError_t embed_step(myl_model* m, int mode, int token, int pos, int64_t* tokens_dev) {
