@@ -44,7 +44,11 @@ void* myl_ctx::scratch(size_t bytes) {
 // the chip), so the accumulator stays at most 32 MiB.
 static constexpr size_t kMmAccCap = (size_t)4 << 20;
 
-const myl::MmCtx* myl_ctx::mm_ctx(size_t elems) {
+// Activation planes beyond this stay with the tiled kernel (1 GiB: 4096
+// rows of the widest product, K = 18944, need 155 MiB).
+static constexpr size_t kMmPlaneCap = (size_t)1 << 30;
+
+const myl::MmCtx* myl_ctx::mm_ctx(size_t elems, size_t plane_bytes) {
     mm.cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1;
     if (elems > mm.acc_elems && elems <= kMmAccCap) {
         (void)hipStreamSynchronize(stream);
@@ -59,6 +63,17 @@ const myl::MmCtx* myl_ctx::mm_ctx(size_t elems) {
         }
         mm.acc = (unsigned long long*)p;
         mm.acc_elems = elems;
+    }
+    if (plane_bytes > mm.planes_bytes && plane_bytes <= kMmPlaneCap) {
+        (void)hipStreamSynchronize(stream);
+        if (mm.planes) (void)hipFree(mm.planes);
+        mm.planes = nullptr;
+        mm.planes_bytes = 0;
+        void* p = nullptr;
+        if (hipMalloc(&p, plane_bytes) == hipSuccess) {
+            mm.planes = (int8_t*)p;
+            mm.planes_bytes = plane_bytes;
+        }
     }
     return &mm;
 }
@@ -93,6 +108,7 @@ void myl_destroy(myl_ctx* ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->scratch_ptr) (void)hipFree(ctx->scratch_ptr);
     if (ctx->mm.acc) (void)hipFree(ctx->mm.acc);
+    if (ctx->mm.planes) (void)hipFree(ctx->mm.planes);
     (void)hipStreamSynchronize(ctx->own_stream);
     (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
@@ -402,7 +418,7 @@ int myl_linear_w8a16_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, c
     if (!ctx) return MYL_E_INVALID;
     int rc = check_gemv(ctx, M, ldx, N, K, ldo, "linear_w8a16_dev");
     if (rc || M == 0 || N == 0) return rc;
-    const MmCtx* mm = ctx->mm_ctx(M > 1 ? M * N : 0);
+    const MmCtx* mm = ctx->mm_ctx(M > 1 ? M * N : 0, M >= 256 ? 2 * M * K : 0);
     return ctx->hip(linear_w8a16(x, (int)M, (int)ldx, W, (int)N, (int)K, w_shifts, act_frac, out_frac, out_frac_pc,
                                  out, (int)ldo, ctx->stream, mm), "linear_w8a16_dev");
 }
@@ -412,7 +428,7 @@ int myl_linear_w8a16_mult_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t l
     if (!ctx) return MYL_E_INVALID;
     int rc = check_gemv(ctx, M, ldx, N, K, ldo, "linear_w8a16_mult_dev");
     if (rc || M == 0 || N == 0) return rc;
-    const MmCtx* mm = ctx->mm_ctx(M > 1 ? M * N : 0);
+    const MmCtx* mm = ctx->mm_ctx(M > 1 ? M * N : 0, M >= 256 ? 2 * M * K : 0);
     return ctx->hip(linear_w8a16_mult(x, (int)M, (int)ldx, W, (int)N, (int)K, mult, shift, out, (int)ldo, ctx->stream,
                                       mm), "linear_w8a16_mult_dev");
 }
@@ -423,7 +439,7 @@ int myl_logits_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, const v
     if (!ctx) return MYL_E_INVALID;
     int rc = check_gemv(ctx, M, ldx, N, K, ldo, "logits_dev");
     if (rc || M == 0 || N == 0) return rc;
-    const MmCtx* mm = ctx->mm_ctx(M > 1 ? M * N : 0);
+    const MmCtx* mm = ctx->mm_ctx(M > 1 ? M * N : 0, M >= 256 ? 2 * M * K : 0);
     if (w_bits == 8)
         return ctx->hip(logits_w8(x, (int)M, (int)ldx, (const int8_t*)W, (int)N, (int)K, row_shifts, norm_frac,
                                   logit_frac, out, (int)ldo, ctx->stream, mm), "logits_dev");
@@ -438,7 +454,7 @@ int myl_dot_i8_i16_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, con
     if (!ctx) return MYL_E_INVALID;
     int rc = check_gemv(ctx, M, ldx, N, K, ldo, "dot_i8_i16_dev");
     if (rc || M == 0 || N == 0) return rc;
-    const MmCtx* mm = ctx->mm_ctx(M > 1 ? M * N : 0);
+    const MmCtx* mm = ctx->mm_ctx(M > 1 ? M * N : 0, M >= 256 ? 2 * M * K : 0);
     return ctx->hip(dot_raw_w8(x, (int)M, (int)ldx, W, (int)N, (int)K, out, (int)ldo, ctx->stream, mm),
                     "dot_i8_i16_dev");
 }

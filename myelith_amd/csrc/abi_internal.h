@@ -23,6 +23,7 @@ struct myl_ctx {
     // Grow-only device scratch for host-slice staging (valid until the next call).
     void* scratch(size_t bytes);
     // The matrix-core launch context with an all-zero accumulator of at least
-    // `elems` entries (grown on demand; nullptr only when allocation fails).
-    const myl::MmCtx* mm_ctx(size_t elems);
+    // `elems` entries and an activation-plane buffer of at least plane_bytes
+    // (both grown on demand within caps; nullptr only when allocation fails).
+    const myl::MmCtx* mm_ctx(size_t elems, size_t plane_bytes = 0);
 };

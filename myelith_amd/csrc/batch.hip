@@ -409,7 +409,7 @@ hipError_t forward_rows(myl_model* m, int R, int lmax) {
     hipStream_t st = c->stream;
     const int H = m->H, I = m->I, V = m->V, nq = m->nq, nkv = m->nkv, hd = m->hd, G = m->G;
     const int nqkv = nq + 2 * nkv, heads = (int)m->spec.heads, kvh = (int)m->spec.kv_heads;
-    const MmCtx* mm = c->mm_ctx((size_t)R * std::max(2 * I, nqkv));
+    const MmCtx* mm = c->mm_ctx((size_t)R * std::max(2 * I, nqkv), R >= 256 ? (size_t)2 * R * std::max(I, H) : 0);
     const size_t sstride = seq_stride(m);
     const int chunks = (lmax + kRowChunk - 1) / kRowChunk;
     const uint8_t lut_shift = MYL_TV_SCORE_FRAC_BITS - MYL_TV_EXP_INPUT_FRAC;

@@ -10,6 +10,7 @@
 #pragma once
 
 #include "gemm_mfma.h"
+#include "gemm_mfma2.h"
 #include "gemv.h"
 #include "internal.h"
 
@@ -95,6 +96,19 @@ template <class Epi>
 inline hipError_t mm_i8(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, const Epi& epi,
                         const MmCtx* mm, hipStream_t st) {
     const int cus = mm ? mm->cus : 256;
+    // Large M: split the activations into byte planes once and run the
+    // pipelined int8 product (gemm_mfma2.h) when its tiles fill the chip.
+    if (M >= 256 && K % 64 == 0 && mm && mm->planes && (size_t)2 * M * K <= mm->planes_bytes &&
+        mm_env("MYL_MM_TILE") < 0) {
+        const bool wide = M > 1024;
+        const int tiles = wide ? mm2_tiles<2, 4, 4, 2, 3>(M, N) : mm2_tiles<2, 2, 4, 2, 3>(M, N);
+        if (tiles >= cus) {
+            hipError_t e = split_planes(x, M, ldx, K, mm->planes, st);
+            if (e != hipSuccess) return e;
+            return wide ? mm2_launch<2, 4, 4, 2, 3>(mm->planes, M, W, N, K, epi, st)
+                        : mm2_launch<2, 2, 4, 2, 3>(mm->planes, M, W, N, K, epi, st);
+        }
+    }
     int tile = mm_env("MYL_MM_TILE");
     if (tile < 0 || tile > 3) tile = M <= 512 ? MM_64x64 : MM_64x128;
     const int bm = (tile == MM_128x128 || tile == MM_128x64) ? 128 : 64;

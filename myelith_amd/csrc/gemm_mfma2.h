@@ -1,0 +1,193 @@
+// gemm_mfma2.h -- the large-M W8A16 product on the int8 matrix cores.
+//
+// y[m][n] = epilogue(n, m, sum_k W[n][k] * x[m][k])  (exact i64 sums)
+//
+// The activations are split once, before the product, into byte planes laid
+// out as interleaved rows of an int8 matrix A' [2M x K]: row 2m = hi(x_m) =
+// x_m >> 8, row 2m + 1 = lo'(x_m) = (x_m & 255) - 128.  The product is then a
+// plain int8 GEMM over 2M rows, C' = A' . W^T, and
+//   sum_k w*x = 256 * C'[2m][n] + C'[2m+1][n] + 128 * sum_k W[n][k]
+// with the row sums of W taken by v_dot4 on the B fragments.  In the 32x32
+// accumulator layout rows 2m and 2m+1 land in registers r and r+1 of the same
+// lane, so the combination needs no data movement.
+//
+// Tiling (gfx950, 160 KB LDS): a block of WM x WN waves owns BR = 32*MB*WM
+// rows of A' and BN = 32*NB*WN weight rows; K advances 64 bytes per stage
+// through STAGES LDS buffers filled by direct global-to-LDS loads
+// (global_load_lds_dwordx4: each wave instruction writes 1 KiB = 16 rows x 64
+// bytes), issued STAGES-1 stages ahead and awaited with an explicit vmcnt.
+// The four 16-byte chunks of LDS row r sit at slot chunk ^ ((r >> 2) & 3), so
+// the 16-byte fragment reads of consecutive rows fall on distinct banks.
+// K must be a multiple of 64; rows past the matrix clamp to its last row
+// (their outputs are discarded), so every load stays in bounds.
+#pragma once
+
+#include "gemm_mfma.h"
+
+namespace myl {
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// x int16 [M x K] -> Ap int8 [2M x K]: row 2m = hi(x_m), row 2m+1 = lo'(x_m).
+template <int = 0>
+__global__ __launch_bounds__(256) void split_planes_kernel(const int16_t* __restrict__ x, int M, int ldx, int K, int8_t* __restrict__ Ap) {
+    const int m = blockIdx.y;
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;  // 8-element chunk
+    if (m >= M || c * 8 >= K) return;
+    const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)m * ldx + c * 8);
+    uint2 h, l;
+    split_planes8(v, h, l);
+    *reinterpret_cast<uint2*>(Ap + (size_t)(2 * m) * K + c * 8) = h;
+    *reinterpret_cast<uint2*>(Ap + (size_t)(2 * m + 1) * K + c * 8) = l;
+}
+
+__device__ inline constexpr int waitcnt_vm(int v) { return (v & 0xF) | (0x7 << 4) | (0xF << 8) | (((v >> 4) & 0x3) << 14); }
+
+template <int MB, int NB, int WM_, int WN_, int STAGES>
+struct Mm2 {
+    static constexpr int kThreads = WM_ * WN_ * 64;
+    static constexpr int BR = 32 * MB * WM_;   // A' rows per block (2 per token)
+    static constexpr int BN = 32 * NB * WN_;   // weight rows per block
+    static constexpr int kStageBytes = (BR + BN) * 64;
+    static constexpr size_t kLds = (size_t)STAGES * kStageBytes;
+    static constexpr int kChunks = (BR + BN) * 4;          // 16-byte chunks per stage
+    static constexpr int kLoads = kChunks / kThreads;      // per thread per stage
+    static_assert(kChunks % kThreads == 0, "whole wave loads");
+};
+
+// LDS layout of a stage: BR A' rows then BN weight rows, 64 bytes each; the
+// four 16-byte chunks of row r sit at chunk slot c ^ ((r >> 2) & 3).
+template <int MB, int NB, int WM_, int WN_, int STAGES, class Sink>
+__device__ inline void mm2_tile(const int8_t* __restrict__ Ap, int R2, const int8_t* __restrict__ W, int N, int K,
+                                int r0, int n0, int8_t* lds, const Sink& sink) {
+    using S = Mm2<MB, NB, WM_, WN_, STAGES>;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave % WM_, wn = wave / WM_;
+    const int nk = K / 64;
+    // Each wave-level load moves 16 rows (64 lanes x 16 bytes): lane l takes
+    // row (l >> 2) of the group and the global chunk whose swizzled slot is l & 3.
+    auto issue = [&](int kt, int buf) {
+        int8_t* st = lds + buf * S::kStageBytes;
+#pragma unroll
+        for (int i = 0; i < S::kLoads; ++i) {
+            const int grp = wave + i * (S::kThreads / 64);   // 16-row group index in the stage
+            const int row = grp * 16 + (lane >> 2);          // stage row: A' rows first
+            const int slot = lane & 3;
+            const int chunk = slot ^ ((row >> 2) & 3);
+            const int8_t* src;
+            if (row < S::BR) {
+                const int gr = min(r0 + row, R2 - 1);
+                src = Ap + (size_t)gr * K + kt * 64 + chunk * 16;
+            } else {
+                const int gn = min(n0 + row - S::BR, N - 1);
+                src = W + (size_t)gn * K + kt * 64 + chunk * 16;
+            }
+            __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(st + grp * 1024), 16, 0, 0);
+        }
+    };
+    v16i32_t acc[MB][NB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+    int32_t rs[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) rs[j] = 0;
+
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < nk) issue(s, s);
+    for (int kt = 0; kt < nk; ++kt) {
+        // stage kt complete: later stages may still be in flight
+        if (kt + STAGES - 2 < nk) __builtin_amdgcn_s_waitcnt(waitcnt_vm(S::kLoads * (STAGES - 2)));
+        else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        __syncthreads();
+        if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+        const int8_t* st = lds + (kt % STAGES) * S::kStageBytes;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int chunk = 2 * s + (lane >> 5);
+            v4i32_t a[MB], b[NB];
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int row = S::BR + (wn * NB + j) * 32 + (lane & 31);
+                b[j] = *reinterpret_cast<const v4i32_t*>(st + row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4));
+            }
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+                const int row = (wm * MB + i) * 32 + (lane & 31);
+                a[i] = *reinterpret_cast<const v4i32_t*>(st + row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4));
+            }
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+#pragma unroll
+                for (int i = 0; i < MB; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+                rs[j] = sdot4((uint32_t)b[j][0], 0x01010101u, rs[j]);
+                rs[j] = sdot4((uint32_t)b[j][1], 0x01010101u, rs[j]);
+                rs[j] = sdot4((uint32_t)b[j][2], 0x01010101u, rs[j]);
+                rs[j] = sdot4((uint32_t)b[j][3], 0x01010101u, rs[j]);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) rs[j] += __shfl_xor(rs[j], 32);
+    // accumulator rows 8*(r/4) + 4*(lane/32) + r%4: registers (r, r+1), r even,
+    // hold the hi and lo' rows of one token.
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int n = n0 + (wn * NB + j) * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const int arow = r0 + (wm * MB + i) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const int m = arow >> 1;
+                if (arow < R2 && n < N)
+                    sink(n, m, (int64_t)acc[i][j][r] * 256 + (int64_t)acc[i][j][r + 1] + (int64_t)rs[j] * 128);
+            }
+        }
+}
+
+template <int MB, int NB, int WM_, int WN_, int STAGES, class Epi>
+__global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_kernel(const int8_t* __restrict__ Ap, int R2, const int8_t* __restrict__ W,
+                                                             int N, int K, Divider tiles_r, int ntiles, Epi epi) {
+    using S = Mm2<MB, NB, WM_, WN_, STAGES>;
+    extern __shared__ __align__(16) int8_t lds[];
+    const int t = mm_tile_index(ntiles);
+    if (t < 0) return;
+    uint32_t tn, tr;
+    tiles_r.divmod((uint32_t)t, tn, tr);
+    mm2_tile<MB, NB, WM_, WN_, STAGES>(Ap, R2, W, N, K, (int)tr * S::BR, (int)tn * S::BN, lds, SinkEpi<Epi>{epi});
+}
+
+template <int MB, int NB, int WM_, int WN_, int STAGES, class Epi>
+hipError_t mm2_launch(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, hipStream_t st) {
+    using S = Mm2<MB, NB, WM_, WN_, STAGES>;
+    const int R2 = 2 * M;
+    const int tiles_r = (R2 + S::BR - 1) / S::BR, ntiles = tiles_r * ((N + S::BN - 1) / S::BN);
+    auto kern = mm2_kernel<MB, NB, WM_, WN_, STAGES, Epi>;
+    if (S::kLds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
+        if (e != hipSuccess) return e;
+    }
+    kern<<<8 * ((ntiles + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, R2, W, N, K, Divider::of((uint32_t)tiles_r), ntiles, epi);
+    return hipGetLastError();
+}
+
+// Block tiles of a launch shape (for the dispatch's tile count).
+template <int MB, int NB, int WM_, int WN_, int STAGES>
+inline int mm2_tiles(int M, int N) {
+    using S = Mm2<MB, NB, WM_, WN_, STAGES>;
+    return ((2 * M + S::BR - 1) / S::BR) * ((N + S::BN - 1) / S::BN);
+}
+
+
+inline hipError_t split_planes(const int16_t* x, int M, int ldx, int K, int8_t* Ap, hipStream_t st) {
+    split_planes_kernel<><<<dim3((K / 8 + 255) / 256, M), 256, 0, st>>>(x, M, ldx, K, Ap);
+    return hipGetLastError();
+}
+
+}  // namespace myl

@@ -15,6 +15,10 @@ struct MmCtx {
     unsigned long long* acc = nullptr;
     size_t acc_elems = 0;
     int cus = 256;
+    // byte planes of the activations for the large-M product (gemm_mfma2.h);
+    // null or too small: that product is not used
+    int8_t* planes = nullptr;
+    size_t planes_bytes = 0;
 };
 
 // y[m][r] = clamp_i16(rescale_i64(W[r].x[m], w_shifts[r] + act_frac, out_frac_pc ? out_frac_pc[r] : out_frac))

@@ -177,6 +177,31 @@ def test_mfma_extremes(backend):
     assert np.array_equal(got, x.astype(np.int64) @ W.astype(np.int64).T)
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 30000, 192), (1030, 8000, 128), (4096, 4608, 3584), (2049, 37888, 64)])
+def test_mfma_large_m_byte_plane_product(backend, oracle, M, N, K):
+    """M >= 256: activations split into interleaved byte-plane rows, the pipelined
+    int8 product over 2M rows (odd M and N, the smallest K, the 7B q/k/v
+    shape).  Exact sums against float64; the requant on sampled rows against
+    the oracle."""
+    import torch
+    case(f"mfma2 M={M} N={N} K={K}")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(M * 3 + N + K)
+    x = torch.randint(-32768, 32768, (M, K), dtype=torch.int16, device="cuda", generator=g)
+    x[0, :2] = torch.tensor([-32768, 32767], dtype=torch.int16)
+    W = torch.randint(-128, 128, (N, K), dtype=torch.int8, device="cuda", generator=g)
+    raw = backend.dot_i8_i16_dev(x, W)
+    assert torch.equal(raw, (x.double() @ W.double().T).to(torch.int64))
+    del raw
+    ws = torch.randint(8, 14, (N,), dtype=torch.uint8, device="cuda", generator=g)
+    y = backend.linear_w8a16_dev(x, W, ws, 11, 10).cpu().numpy()
+    rows = sorted({0, 1, M // 2, M - 1})
+    xs = x[rows].cpu().numpy()
+    oracle.lib().or_set_threads(16)
+    exp = oracle.linear_batch(xs, W.cpu().numpy(), ws.cpu().numpy(), 11, 10)
+    assert np.array_equal(y[rows], exp)
+
+
 @pytest.mark.parametrize("M", [64, 512])
 @pytest.mark.parametrize("N,K", SWEEP)
 def test_mfma_full_size_exact_sums(backend, M, N, K):
