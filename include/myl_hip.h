@@ -280,6 +280,91 @@ int myl_moe_forward(myl_moe* m, const int16_t* x_dev, uint32_t n_tokens, int16_t
 int myl_moe_read_route(myl_moe* m, uint32_t n_tokens, int32_t* ids, int32_t* gates, int32_t* counts, int32_t* offsets,
                        int32_t* list_tok);
 
+/* ====================================================================
+ * 5. Artifacts: the reference's model directory format and the uploader
+ *
+ * An artifact directory (runtime/src/loader.rs:322-600) holds theta_v.json,
+ * model_config.json, weights_manifest.json with one raw little-endian file
+ * per tensor (+ a _shifts.bin of one u8 per row), scales.json and luts.json
+ * with its *.lut.bin tables.  myl_artifact_open() performs every check of
+ * load_model (loader.rs:611-636) and build_model (:712-849) that does not
+ * need the tensor bytes: theta_v version against MYL_TV_VERSION, the SHA-256
+ * of the three manifest files against theta_v.json, model_config.json
+ * dimensions, manifest dtype / shape / file size rules, shift ranges,
+ * scale = 2^-shift, per-channel shift lengths, the LUT tables (read and
+ * hashed), and the presence of every tensor, scale and LUT the model consumes.
+ * Tensor files are hashed by myl_artifact_verify() or while
+ * myl_model_load_artifact() streams them to the device; a mismatch refuses
+ * the artifact, as load_weights does (loader.rs:364-372).
+ * ==================================================================== */
+
+typedef struct myl_artifact myl_artifact;
+
+/* Opens and checks an artifact directory.  On failure *out is NULL and the
+ * message is written to err (err_cap bytes, may be 0). */
+int myl_artifact_open(const char* dir, myl_artifact** out, char* err, size_t err_cap);
+void myl_artifact_close(myl_artifact* a);
+const char* myl_artifact_last_error(const myl_artifact* a);
+int myl_artifact_dims(const myl_artifact* a, myl_model_dims* out);
+/* Reads every tensor and shifts file of the manifest and checks its SHA-256
+ * (loader.rs:364-399); host only. */
+int myl_artifact_verify(myl_artifact* a);
+/* A LUT by its luts.json key (cos, sin, exp, silu, rsqrt); *len = its length.
+ * out may be NULL to query the length. */
+int myl_artifact_lut(const myl_artifact* a, const char* name, int16_t* out, size_t cap, size_t* len);
+/* The activation scales of one layer (loader.rs:784-797): nine scalar fracs
+ * and the per-channel residual segments res_in / res_mid [hidden] (either may
+ * be NULL). */
+int myl_artifact_layer_scales(const myl_artifact* a, uint32_t layer, myl_layer_fracs* fracs, uint8_t* res_in,
+                              uint8_t* res_mid);
+/* model.norm (final_norm_frac) and model.norm.input [hidden] (loader.rs:737-742). */
+int myl_artifact_final_scales(const myl_artifact* a, uint8_t* final_norm_frac, uint8_t* final_res);
+
+/* SHA-256 of n bytes as 64 lowercase hex digits plus NUL (loader.rs:600-605). */
+int myl_sha256_hex(const void* data, size_t n, char out[65]);
+
+/* Builds the device model of an opened artifact with a KV cache of max_pos
+ * positions (0 = model_config max_context): the tensors are streamed from
+ * their files through pinned staging buffers to HBM and hashed on the way.
+ * The model is ready for every myl_model_* call. */
+int myl_model_load_artifact(myl_ctx* ctx, const myl_artifact* a, uint32_t max_pos, myl_model** out);
+
+/* An empty device model of the given dimensions and LUTs (the shape of
+ * build_model, loader.rs:712-849), filled by the calls below and sealed by
+ * myl_model_finalize().  This is the path for a host that loads artifacts
+ * itself (the Rust loader.rs) and hands over the tensors of its IntegerModel. */
+int myl_model_create(myl_ctx* ctx, const myl_model_dims* dims, uint32_t max_pos, const myl_luts* luts,
+                     myl_model** out);
+/* Uploads one tensor by its reference name (the HF original_name of the
+ * manifest): model.embed_tokens.weight, model.norm.weight, lm_head.weight
+ * (bits 8: the untied int8 head; bits 16: the int16 head),
+ * model.layers.<l>.{input_layernorm,post_attention_layernorm}.weight,
+ * model.layers.<l>.self_attn.{q,k,v,o}_proj.weight,
+ * model.layers.<l>.mlp.{gate,up,down}_proj.weight and, with attention_bias,
+ * model.layers.<l>.self_attn.{q,k,v}_proj.bias (int16).  data is the
+ * row-major tensor (int8, or int16 for bits 16), shape its dimensions, and
+ * shifts one u8 per row (per element for 1-D tensors), n_shifts = shape[0].
+ * The int8 lm_head.weight of an artifact that also carries the int16 head is
+ * accepted and not stored (model.rs:285 reads only the int16 head then). */
+int myl_model_upload_tensor(myl_model* m, const char* name, const void* data, int bits, const uint64_t* shape,
+                            uint32_t ndim, const uint8_t* shifts, size_t n_shifts);
+/* The inverse: the tensor in the reference layout and its per-row shifts
+ * (bytes = element count * bits / 8; shifts may be NULL). */
+int myl_model_download_tensor(myl_model* m, const char* name, int bits, void* data, size_t bytes, uint8_t* shifts,
+                              size_t n_shifts);
+/* LayerScales of one layer (loader.rs:784-797) and the final segment. */
+int myl_model_set_layer_scales(myl_model* m, uint32_t layer, const myl_layer_fracs* fracs, const uint8_t* res_in,
+                               const uint8_t* res_mid);
+int myl_model_set_final_scales(myl_model* m, uint8_t final_norm_frac, const uint8_t* final_res);
+/* Reads the scales back (either array may be NULL). */
+int myl_model_get_layer_scales(myl_model* m, uint32_t layer, myl_layer_fracs* fracs, uint8_t* res_in,
+                               uint8_t* res_mid);
+int myl_model_get_final_scales(myl_model* m, uint8_t* final_norm_frac, uint8_t* final_res);
+/* Checks that every tensor and scale has arrived (the require_* checks of
+ * loader.rs:690-710, naming the first missing item) and derives the
+ * per-channel accumulation scales.  Forward calls fail until it succeeds. */
+int myl_model_finalize(myl_model* m);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,6 +17,8 @@
 #include <stdint.h>
 #include <stddef.h>
 
+#include "myl_theta_v.h"
+
 #if defined(__HIPCC__)
 #define MYL_HD __host__ __device__ static inline
 #else
@@ -119,11 +121,6 @@ MYL_HD uint8_t myl_synth_wshift(uint64_t tseed, uint64_t row, uint64_t K) {
 }
 
 /* Per-layer activation fractional bits of the synthetic model. */
-typedef struct {
-    uint8_t norm_attn_frac, q_frac, k_frac, v_frac, attn_out_frac;
-    uint8_t norm_mlp_frac, gate_frac, up_frac, down_in_frac;
-} myl_layer_fracs;
-
 MYL_HD myl_layer_fracs myl_synth_layer_fracs(uint64_t model_seed, uint32_t layer) {
     uint64_t s = myl_tensor_seed(model_seed, layer, MYL_R_LAYER_FRACS);
     myl_layer_fracs f;

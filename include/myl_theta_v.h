@@ -34,6 +34,11 @@
 #define MYL_TV_LOGIT_FRAC_BITS   6
 #define MYL_TV_ROPE_ROWS         2048
 
+/* The theta_v version this numeric contract is (spec.json theta_v.version);
+ * an artifact calibrated under another version is refused
+ * (loader.rs:56-72, verify_version_against_spec). */
+#define MYL_TV_VERSION "0.17.0"
+
 #define MYL_TV_RSQRT_LEN 32768
 #define MYL_TV_SILU_LEN  16384
 #define MYL_TV_EXP_LEN   16385
@@ -52,6 +57,29 @@ typedef struct myl_luts {
     const int16_t* cos;
     const int16_t* sin;   size_t rope_len;
 } myl_luts;
+
+/* The nine scalar activation fractional bits of one layer, in the order of
+ * LayerScales (runtime/src/model.rs; filled by loader.rs:784-797 from the
+ * scales.json keys <p>.input_layernorm, <p>.self_attn.{q,k,v}_proj,
+ * <p>.self_attn, <p>.post_attention_layernorm, <p>.mlp.{gate,up}_proj and
+ * <p>.mlp.down_proj.input). */
+typedef struct myl_layer_fracs {
+    uint8_t norm_attn_frac, q_frac, k_frac, v_frac, attn_out_frac;
+    uint8_t norm_mlp_frac, gate_frac, up_frac, down_in_frac;
+} myl_layer_fracs;
+
+/* Dimensions of an artifact's model (model_config.json, loader.rs:240-275,
+ * ModelDims) plus the LM-head form the artifact carries.  lm_head_int16 = 1:
+ * an int16 LM head with per-row shifts (loader.rs:304-352, model.rs:285-296);
+ * 0: the int8 head (lm_head.weight, or the embedding when tied;
+ * model.rs:297-307). */
+typedef struct myl_model_dims {
+    uint32_t vocab, hidden, layers, heads, kv_heads, head_dim, inter;
+    uint32_t max_context;
+    int32_t  tie_word_embeddings;
+    int32_t  attention_bias;
+    int32_t  lm_head_int16;
+} myl_model_dims;
 
 /* Shape and seed of a synthetic integer model (Qwen2.5 layout, model.rs:94-163).
  * lm_head_int16 = 1 selects the int16 LM head (model.rs:285-296, path A);

@@ -32,6 +32,19 @@ class MoeSpec(C.Structure):
                 ("shared_inter", u32)]
 
 
+class LayerFracs(C.Structure):
+    """myl_layer_fracs (include/myl_theta_v.h): LayerScales of model.rs."""
+    _fields_ = [("norm_attn_frac", u8), ("q_frac", u8), ("k_frac", u8), ("v_frac", u8), ("attn_out_frac", u8),
+                ("norm_mlp_frac", u8), ("gate_frac", u8), ("up_frac", u8), ("down_in_frac", u8)]
+
+
+class ModelDims(C.Structure):
+    """myl_model_dims (include/myl_theta_v.h): ModelDims of loader.rs."""
+    _fields_ = [("vocab", u32), ("hidden", u32), ("layers", u32), ("heads", u32), ("kv_heads", u32),
+                ("head_dim", u32), ("inter", u32), ("max_context", u32), ("tie_word_embeddings", i32),
+                ("attention_bias", i32), ("lm_head_int16", i32)]
+
+
 class Luts(C.Structure):
     """myl_luts (include/myl_theta_v.h)."""
     _fields_ = [("rsqrt", P), ("rsqrt_len", sz), ("silu", P), ("silu_len", sz), ("exp", P),
@@ -94,6 +107,24 @@ SIGNATURES: dict[str, tuple] = {
     "myl_moe_synth_input": (INT, [P, u32, P]),
     "myl_moe_forward": (INT, [P, P, u32, P]),
     "myl_moe_read_route": (INT, [P, u32, P, P, P, P, P]),
+    "myl_artifact_open": (INT, [C.c_char_p, C.POINTER(P), C.c_char_p, sz]),
+    "myl_artifact_close": (None, [P]),
+    "myl_artifact_last_error": (C.c_char_p, [P]),
+    "myl_artifact_dims": (INT, [P, C.POINTER(ModelDims)]),
+    "myl_artifact_verify": (INT, [P]),
+    "myl_artifact_lut": (INT, [P, C.c_char_p, P, sz, C.POINTER(sz)]),
+    "myl_artifact_layer_scales": (INT, [P, u32, C.POINTER(LayerFracs), P, P]),
+    "myl_artifact_final_scales": (INT, [P, C.POINTER(u8), P]),
+    "myl_sha256_hex": (INT, [P, sz, C.c_char_p]),
+    "myl_model_load_artifact": (INT, [P, P, u32, C.POINTER(P)]),
+    "myl_model_create": (INT, [P, C.POINTER(ModelDims), u32, C.POINTER(Luts), C.POINTER(P)]),
+    "myl_model_upload_tensor": (INT, [P, C.c_char_p, P, INT, C.POINTER(u64), u32, P, sz]),
+    "myl_model_download_tensor": (INT, [P, C.c_char_p, INT, P, sz, P, sz]),
+    "myl_model_set_layer_scales": (INT, [P, u32, C.POINTER(LayerFracs), P, P]),
+    "myl_model_set_final_scales": (INT, [P, u8, P]),
+    "myl_model_get_layer_scales": (INT, [P, u32, C.POINTER(LayerFracs), P, P]),
+    "myl_model_get_final_scales": (INT, [P, C.POINTER(u8), P]),
+    "myl_model_finalize": (INT, [P]),
 }
 
 _lib = None

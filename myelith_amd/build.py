@@ -29,7 +29,9 @@ SOURCES = {  # source -> is HIP device code
     "model.hip": True,
     "batch.hip": True,
     "moe.hip": True,
+    "model_io.hip": True,
     "abi.cpp": False,
+    "artifact.cpp": False,
 }
 
 

@@ -486,8 +486,8 @@ hipError_t forward_rows(myl_model* m, int R, int lmax) {
         EpiLogits el{m->lm16_shifts, m->final_norm_frac, MYL_TV_LOGIT_FRAC_BITS, b->logits, V};
         if ((e = gemv_i16(b->Xn, R, H, m->lm16, V, H, el, st)) != hipSuccess) return e;
     } else {
-        EpiLogits el{m->emb_shifts, m->final_norm_frac, MYL_TV_LOGIT_FRAC_BITS, b->logits, V};
-        if ((e = gemv_i8(b->Xn, R, H, m->emb, V, H, el, st, mm)) != hipSuccess) return e;
+        EpiLogits el{m->lm8_shifts, m->final_norm_frac, MYL_TV_LOGIT_FRAC_BITS, b->logits, V};
+        if ((e = gemv_i8(b->Xn, R, H, m->lm8, V, H, el, st, mm)) != hipSuccess) return e;
     }
     return argmax(b->logits, R, V, V, b->argmax, st);
 }
@@ -545,6 +545,7 @@ extern "C" {
 
 int myl_model_batch_begin(myl_model* m, uint32_t n_seqs) {
     if (!m || n_seqs == 0) return MYL_E_INVALID;
+    if (int nr = m->not_ready()) return nr;
     myl_ctx* c = m->ctx;
     if (m->G > 16) return c->fail(MYL_E_UNSUPPORTED, "batch: at most 16 query heads per KV head");
     if (m->batch && m->batch->n_seqs == (int)n_seqs) {
@@ -572,6 +573,7 @@ int myl_model_batch_begin(myl_model* m, uint32_t n_seqs) {
 int myl_model_forward_batch(myl_model* m, uint32_t n_rows, const uint32_t* seq, const uint32_t* pos,
                             const uint32_t* tokens, int32_t* logits, int64_t* argmax_out) {
     if (!m || !seq || !pos || !tokens) return MYL_E_INVALID;
+    if (int nr = m->not_ready()) return nr;
     myl_ctx* c = m->ctx;
     if (!m->batch) return c->fail(MYL_E_INVALID, "forward_batch: call myl_model_batch_begin first");
     if (n_rows == 0) return MYL_OK;
@@ -603,6 +605,7 @@ int myl_model_batch_logits_dev(myl_model* m, const int32_t** logits_dev) {
 int myl_model_batch_decode_greedy(myl_model* m, uint32_t n_rows, const uint32_t* seq, const uint32_t* pos,
                                   const uint32_t* tokens, uint32_t n_steps, int64_t* tokens_out) {
     if (!m || !seq || !pos || !tokens) return MYL_E_INVALID;
+    if (int nr = m->not_ready()) return nr;
     myl_ctx* c = m->ctx;
     if (!m->batch) return c->fail(MYL_E_INVALID, "batch_decode: call myl_model_batch_begin first");
     if (n_rows == 0 || n_steps == 0) return MYL_OK;

@@ -837,10 +837,13 @@ int pair_row(int o, int hd) {
     return head * hd + (w < half ? 2 * w : 2 * (w - half) + 1);
 }
 
-int build(myl_model* m, const myl_luts* luts) {
+// Allocates every device buffer of a model of m's dimensions, uploads the
+// LUTs and the row maps, and clears the caches.  Tensors and scales are
+// written afterwards by the synthetic generator (synth_fill) or the uploader
+// (model_io.hip); model_finalize() seals the model.
+int alloc_impl(myl_model* m, const myl_luts* luts) {
     myl_ctx* c = m->ctx;
     const myl_synth_spec& s = m->spec;
-    const uint64_t seed = s.seed;
     const int H = m->H, I = m->I, V = m->V, hd = m->hd, nq = m->nq, nkv = m->nkv;
     const int nqkv = nq + 2 * nkv;
 
@@ -871,7 +874,7 @@ int build(myl_model* m, const myl_luts* luts) {
         m->score_mult = (int64_t)(above < below ? r + 1 : r);
     }
 
-    // embedding / LM head / final norm
+    // embedding / LM heads / final norm
     m->emb = m->dalloc<int8_t>((size_t)V * H);
     m->emb_shifts = m->dalloc<uint8_t>(V);
     m->final_gamma = m->dalloc<int8_t>(H);
@@ -879,52 +882,38 @@ int build(myl_model* m, const myl_luts* luts) {
     m->final_res = m->dalloc<uint8_t>(H);
     if (!m->emb || !m->emb_shifts || !m->final_gamma || !m->final_gamma_s || !m->final_res)
         return c->fail(MYL_E_NOMEM, "embedding allocation");
-    if (gen_w8(m, m->emb, nullptr, V, H, myl_tensor_seed(seed, 0, MYL_R_EMB)) != hipSuccess) return MYL_E_HIP;
-    rc |= upload(m, m->emb_shifts, small_u8(seed, 0, MYL_R_EMB_SHIFT, V));
     if (s.lm_head_int16) {
         m->lm16 = m->dalloc<int16_t>((size_t)V * H);
         m->lm16_shifts = m->dalloc<uint8_t>(V);
         if (!m->lm16 || !m->lm16_shifts) return c->fail(MYL_E_NOMEM, "LM head allocation");
-        if (gen_w16(m, m->lm16, V, H, myl_tensor_seed(seed, 0, MYL_R_LM16)) != hipSuccess) return MYL_E_HIP;
-        rc |= upload(m, m->lm16_shifts, small_u8(seed, 0, MYL_R_LM16_SHIFT, V));
+    } else if (!m->tied) {
+        m->lm8 = m->dalloc<int8_t>((size_t)V * H);
+        m->lm8_shifts = m->dalloc<uint8_t>(V);
+        if (!m->lm8 || !m->lm8_shifts) return c->fail(MYL_E_NOMEM, "LM head allocation");
     }
-    if (gen_w8(m, m->final_gamma, nullptr, 1, H, myl_tensor_seed(seed, 0, MYL_R_FINAL_GAMMA)) != hipSuccess) return MYL_E_HIP;
-    rc |= upload(m, m->final_gamma_s, small_u8(seed, 0, MYL_R_FINAL_GAMMA_SHIFT, H));
-    std::vector<uint8_t> final_res(H);
-    {
-        const uint64_t ts = myl_tensor_seed(seed, 0, MYL_R_FINAL_RES_FRAC);
-        for (int i = 0; i < H; ++i) final_res[i] = myl_synth_res_frac(ts, i);
+    if (m->tied) {
+        m->lm8 = m->emb;
+        m->lm8_shifts = m->emb_shifts;
     }
-    rc |= upload(m, m->final_res, final_res);
-    m->final_norm_frac = myl_synth_final_norm_frac(seed);
 
-    // layers
-    std::vector<int32_t> qkv_rows(nqkv);
-    for (int o = 0; o < nq; ++o) qkv_rows[o] = pair_row(o, hd);
-    for (int o = 0; o < nkv; ++o) qkv_rows[nq + o] = nq + pair_row(o, hd);
-    for (int o = 0; o < nkv; ++o) qkv_rows[nq + nkv + o] = nq + nkv + pair_row(o, hd);
-    int32_t* qkv_rows_dev = m->dalloc<int32_t>(nqkv);
-    std::vector<int32_t> gu_rows(2 * (size_t)I);
-    for (int r = 0; r < I; ++r) { gu_rows[r] = 2 * r; gu_rows[I + r] = 2 * r + 1; }
-    int32_t* gu_rows_dev = m->dalloc<int32_t>(2 * (size_t)I);
-    if (!qkv_rows_dev || !gu_rows_dev) return c->fail(MYL_E_NOMEM, "row tables");
-    rc |= upload(m, qkv_rows_dev, qkv_rows);
-    rc |= upload(m, gu_rows_dev, gu_rows);
+    // Stored row of each logical output row: q/k/v heads pair-ordered for the
+    // fused RoPE, gate and up rows interleaved for the fused SiLU product.
+    m->qkv_map.resize(nqkv);
+    for (int o = 0; o < nq; ++o) m->qkv_map[o] = pair_row(o, hd);
+    for (int o = 0; o < nkv; ++o) m->qkv_map[nq + o] = nq + pair_row(o, hd);
+    for (int o = 0; o < nkv; ++o) m->qkv_map[nq + nkv + o] = nq + nkv + pair_row(o, hd);
+    m->gu_map.resize(2 * (size_t)I);
+    for (int r = 0; r < I; ++r) { m->gu_map[r] = 2 * r; m->gu_map[I + r] = 2 * r + 1; }
+    m->qkv_map_dev = m->dalloc<int32_t>(nqkv);
+    m->gu_map_dev = m->dalloc<int32_t>(2 * (size_t)I);
+    if (!m->qkv_map_dev || !m->gu_map_dev) return c->fail(MYL_E_NOMEM, "row tables");
+    rc |= upload(m, m->qkv_map_dev, m->qkv_map);
+    rc |= upload(m, m->gu_map_dev, m->gu_map);
+    if (rc) return MYL_E_HIP;
 
-    std::vector<std::vector<uint8_t>> res_in(s.layers), res_mid(s.layers);
-    for (uint32_t l = 0; l < s.layers; ++l) {
-        res_in[l].resize(H);
-        res_mid[l].resize(H);
-        const uint64_t ti = myl_tensor_seed(seed, l, MYL_R_RES_IN), tm = myl_tensor_seed(seed, l, MYL_R_RES_MID);
-        for (int i = 0; i < H; ++i) {
-            res_in[l][i] = myl_synth_res_frac(ti, i);
-            res_mid[l][i] = myl_synth_res_frac(tm, i);
-        }
-    }
     m->layers.resize(s.layers);
     for (uint32_t l = 0; l < s.layers; ++l) {
         LayerDev& L = m->layers[l];
-        L.f = myl_synth_layer_fracs(seed, l);
         L.wqkv = m->dalloc<int8_t>((size_t)nqkv * H);
         L.wo = m->dalloc<int8_t>((size_t)H * nq);
         L.wgu = m->dalloc<int8_t>((size_t)2 * I * H);
@@ -949,6 +938,129 @@ int build(myl_model* m, const myl_luts* luts) {
         if (!L.wqkv || !L.wo || !L.wgu || !L.wd || !L.sqkv || !L.so || !L.sgu || !L.sd || !L.in_gamma ||
             !L.post_gamma || !L.in_gamma_s || !L.post_gamma_s || !L.res_in || !L.res_mid || !L.acc_attn || !L.acc_mlp)
             return c->fail(MYL_E_NOMEM, "layer allocation");
+    }
+    m->h_res_in.assign(s.layers, std::vector<uint8_t>(H, 0));
+    m->h_res_mid.assign(s.layers, std::vector<uint8_t>(H, 0));
+    m->h_final_res.assign(H, 0);
+    m->have.assign(myl::kModelSlots + (size_t)myl::kLayerSlots * s.layers, 0);
+    m->scales_have.assign(s.layers, 0);
+    m->final_have = false;
+    m->ready = false;
+
+    // caches, activations, scratch
+    const size_t kv = (size_t)s.layers * s.kv_heads * (size_t)m->max_pos * hd;
+    m->kcache = m->dalloc<int16_t>(kv);
+    m->vcache = m->dalloc<int16_t>(kv);
+    m->hidden = m->dalloc<int16_t>(H);
+    m->norm = m->dalloc<int16_t>(H);
+    m->q = m->dalloc<int16_t>(nq);
+    m->attn = m->dalloc<int16_t>(nq);
+    m->resid = m->dalloc<int16_t>(H);
+    m->h = m->dalloc<int16_t>(I);
+    m->logits = m->dalloc<int32_t>(V);
+    m->scores = m->dalloc<int32_t>((size_t)s.heads * m->max_pos);
+    m->attn_acc = m->dalloc<unsigned long long>((size_t)nq);
+    m->norm_a = m->dalloc<NormAcc>(1);
+    m->norm_b = m->dalloc<NormAcc>(1);
+    m->state = m->dalloc<DecodeState>(1);
+    if (!m->kcache || !m->vcache || !m->hidden || !m->norm || !m->q || !m->attn || !m->resid || !m->h ||
+        !m->logits || !m->scores || !m->attn_acc || !m->state || !m->norm_a || !m->norm_b)
+        return c->fail(MYL_E_NOMEM, "activation allocation");
+    if (hipMemsetAsync(m->kcache, 0, kv * 2, c->stream) != hipSuccess ||
+        hipMemsetAsync(m->vcache, 0, kv * 2, c->stream) != hipSuccess ||
+        hipMemsetAsync(m->state, 0, sizeof(DecodeState), c->stream) != hipSuccess ||
+        hipMemsetAsync(m->attn_acc, 0, (size_t)nq * 8, c->stream) != hipSuccess ||
+        hipMemsetAsync(m->norm_a, 0, sizeof(NormAcc), c->stream) != hipSuccess ||
+        hipMemsetAsync(m->norm_b, 0, sizeof(NormAcc), c->stream) != hipSuccess)
+        return MYL_E_HIP;
+    return c->hip(hipStreamSynchronize(c->stream), "model allocation");
+}
+
+// Checks that every tensor and scale has arrived, derives the accumulation
+// scales of the two residual adds, min(res_in, res_mid) and
+// min(res_mid, res_out) per channel (model.rs:576-581,612-617), and the
+// per-segment maxima the RMSNorm reference shift takes (rmsnorm.rs:96).
+int finalize_impl(myl_model* m) {
+    myl_ctx* c = m->ctx;
+    const myl_synth_spec& s = m->spec;
+    const int H = m->H;
+    for (size_t i = 0; i < m->have.size(); ++i) {
+        if (m->have[i] || !myl::slot_required(m, i)) continue;
+        return c->fail(MYL_E_INVALID, "model: missing tensor " + myl::slot_name(m, i));
+    }
+    for (uint32_t l = 0; l < s.layers; ++l)
+        if (!m->scales_have[l])
+            return c->fail(MYL_E_INVALID, "model: missing activation scales of layer " + std::to_string(l));
+    if (!m->final_have) return c->fail(MYL_E_INVALID, "model: missing final norm scales (model.norm)");
+    auto vmax = [](const std::vector<uint8_t>& v) { uint8_t r = 0; for (uint8_t x : v) r = std::max(r, x); return r; };
+    int rc = upload(m, m->final_res, m->h_final_res);
+    m->ref_final = vmax(m->h_final_res);
+    for (uint32_t l = 0; l < s.layers && !rc; ++l) {
+        LayerDev& L = m->layers[l];
+        const std::vector<uint8_t>& in = m->h_res_in[l];
+        const std::vector<uint8_t>& mid = m->h_res_mid[l];
+        const std::vector<uint8_t>& out = (l + 1 < s.layers) ? m->h_res_in[l + 1] : m->h_final_res;
+        std::vector<uint8_t> acc_a(H), acc_m(H);
+        for (int i = 0; i < H; ++i) {
+            acc_a[i] = std::min(in[i], mid[i]);
+            acc_m[i] = std::min(mid[i], out[i]);
+        }
+        rc |= upload(m, L.res_in, in);
+        rc |= upload(m, L.res_mid, mid);
+        rc |= upload(m, L.acc_attn, acc_a);
+        rc |= upload(m, L.acc_mlp, acc_m);
+        // The uploads read host vectors that live until the synchronisation below.
+        rc |= c->hip(hipStreamSynchronize(c->stream), "model finalize");
+        L.res_out = (l + 1 < s.layers) ? m->layers[l + 1].res_in : m->final_res;
+        L.ref_in = vmax(in);
+        L.ref_mid = vmax(mid);
+        L.ref_out = vmax(out);
+    }
+    if (rc) return MYL_E_HIP;
+    // A captured decode step holds the previous scales as kernel arguments.
+    if (m->step_exec) (void)hipGraphExecDestroy(m->step_exec);
+    if (m->step_graph) (void)hipGraphDestroy(m->step_graph);
+    m->step_exec = nullptr;
+    m->step_graph = nullptr;
+    int r = c->hip(hipStreamSynchronize(c->stream), "model finalize");
+    if (!r) m->ready = true;
+    return r;
+}
+
+// The seeded synthetic model of include/myl_synth.h, generated in place.
+int synth_fill(myl_model* m) {
+    myl_ctx* c = m->ctx;
+    const myl_synth_spec& s = m->spec;
+    const uint64_t seed = s.seed;
+    const int H = m->H, I = m->I, V = m->V, nq = m->nq, nkv = m->nkv;
+    const int nqkv = nq + 2 * nkv;
+    const std::vector<int32_t>& qkv_rows = m->qkv_map;
+    int rc = 0;
+    if (gen_w8(m, m->emb, nullptr, V, H, myl_tensor_seed(seed, 0, MYL_R_EMB)) != hipSuccess) return MYL_E_HIP;
+    rc |= upload(m, m->emb_shifts, small_u8(seed, 0, MYL_R_EMB_SHIFT, V));
+    if (s.lm_head_int16) {
+        if (gen_w16(m, m->lm16, V, H, myl_tensor_seed(seed, 0, MYL_R_LM16)) != hipSuccess) return MYL_E_HIP;
+        rc |= upload(m, m->lm16_shifts, small_u8(seed, 0, MYL_R_LM16_SHIFT, V));
+    }
+    if (gen_w8(m, m->final_gamma, nullptr, 1, H, myl_tensor_seed(seed, 0, MYL_R_FINAL_GAMMA)) != hipSuccess) return MYL_E_HIP;
+    rc |= upload(m, m->final_gamma_s, small_u8(seed, 0, MYL_R_FINAL_GAMMA_SHIFT, H));
+    {
+        const uint64_t ts = myl_tensor_seed(seed, 0, MYL_R_FINAL_RES_FRAC);
+        for (int i = 0; i < H; ++i) m->h_final_res[i] = myl_synth_res_frac(ts, i);
+    }
+    m->final_norm_frac = myl_synth_final_norm_frac(seed);
+    for (uint32_t l = 0; l < s.layers; ++l) {
+        const uint64_t ti = myl_tensor_seed(seed, l, MYL_R_RES_IN), tm = myl_tensor_seed(seed, l, MYL_R_RES_MID);
+        for (int i = 0; i < H; ++i) {
+            m->h_res_in[l][i] = myl_synth_res_frac(ti, i);
+            m->h_res_mid[l][i] = myl_synth_res_frac(tm, i);
+        }
+    }
+    const int32_t* qkv_rows_dev = m->qkv_map_dev;
+    const int32_t* gu_rows_dev = m->gu_map_dev;
+    for (uint32_t l = 0; l < s.layers; ++l) {
+        LayerDev& L = m->layers[l];
+        L.f = myl_synth_layer_fracs(seed, l);
         hipError_t e = gen_w8(m, L.wqkv, qkv_rows_dev, nq, H, myl_tensor_seed(seed, l, MYL_R_WQ));
         if (e == hipSuccess) e = gen_w8(m, L.wqkv, qkv_rows_dev + nq, nkv, H, myl_tensor_seed(seed, l, MYL_R_WK));
         if (e == hipSuccess) e = gen_w8(m, L.wqkv, qkv_rows_dev + nq + nkv, nkv, H, myl_tensor_seed(seed, l, MYL_R_WV));
@@ -991,55 +1103,12 @@ int build(myl_model* m, const myl_luts* luts) {
         rc |= upload(m, L.sd, wshifts(seed, l, MYL_R_SD, H, I));
         rc |= upload(m, L.in_gamma_s, small_u8(seed, l, MYL_R_IN_GAMMA_SHIFT, H));
         rc |= upload(m, L.post_gamma_s, small_u8(seed, l, MYL_R_POST_GAMMA_SHIFT, H));
-        const std::vector<uint8_t>& out_frac = (l + 1 < s.layers) ? res_in[l + 1] : final_res;
-        std::vector<uint8_t> acc_a(H), acc_m(H);
-        for (int i = 0; i < H; ++i) {
-            acc_a[i] = std::min(res_in[l][i], res_mid[l][i]);   // model.rs:576-581
-            acc_m[i] = std::min(res_mid[l][i], out_frac[i]);    // model.rs:612-617
-        }
-        rc |= upload(m, L.res_in, res_in[l]);
-        rc |= upload(m, L.res_mid, res_mid[l]);
-        rc |= upload(m, L.acc_attn, acc_a);
-        rc |= upload(m, L.acc_mlp, acc_m);
         if (rc) return MYL_E_HIP;
     }
-    auto vmax = [](const std::vector<uint8_t>& v) { uint8_t r = 0; for (uint8_t x : v) r = std::max(r, x); return r; };
-    m->ref_final = vmax(final_res);
-    for (uint32_t l = 0; l < s.layers; ++l) {
-        LayerDev& L = m->layers[l];
-        L.res_out = (l + 1 < s.layers) ? m->layers[l + 1].res_in : m->final_res;
-        L.ref_in = vmax(res_in[l]);
-        L.ref_mid = vmax(res_mid[l]);
-        L.ref_out = (l + 1 < s.layers) ? vmax(res_in[l + 1]) : m->ref_final;
-    }
-
-    // caches, activations, scratch
-    const size_t kv = (size_t)s.layers * s.kv_heads * (size_t)m->max_pos * hd;
-    m->kcache = m->dalloc<int16_t>(kv);
-    m->vcache = m->dalloc<int16_t>(kv);
-    m->hidden = m->dalloc<int16_t>(H);
-    m->norm = m->dalloc<int16_t>(H);
-    m->q = m->dalloc<int16_t>(nq);
-    m->attn = m->dalloc<int16_t>(nq);
-    m->resid = m->dalloc<int16_t>(H);
-    m->h = m->dalloc<int16_t>(I);
-    m->logits = m->dalloc<int32_t>(V);
-    m->scores = m->dalloc<int32_t>((size_t)s.heads * m->max_pos);
-    m->attn_acc = m->dalloc<unsigned long long>((size_t)nq);
-    m->norm_a = m->dalloc<NormAcc>(1);
-    m->norm_b = m->dalloc<NormAcc>(1);
-    m->state = m->dalloc<DecodeState>(1);
-    if (!m->kcache || !m->vcache || !m->hidden || !m->norm || !m->q || !m->attn || !m->resid || !m->h ||
-        !m->logits || !m->scores || !m->attn_acc || !m->state || !m->norm_a || !m->norm_b)
-        return c->fail(MYL_E_NOMEM, "activation allocation");
-    if (hipMemsetAsync(m->kcache, 0, kv * 2, c->stream) != hipSuccess ||
-        hipMemsetAsync(m->vcache, 0, kv * 2, c->stream) != hipSuccess ||
-        hipMemsetAsync(m->state, 0, sizeof(DecodeState), c->stream) != hipSuccess ||
-        hipMemsetAsync(m->attn_acc, 0, (size_t)nq * 8, c->stream) != hipSuccess ||
-        hipMemsetAsync(m->norm_a, 0, sizeof(NormAcc), c->stream) != hipSuccess ||
-        hipMemsetAsync(m->norm_b, 0, sizeof(NormAcc), c->stream) != hipSuccess)
-        return MYL_E_HIP;
-    return c->hip(hipStreamSynchronize(c->stream), "model build");
+    std::fill(m->have.begin(), m->have.end(), 1);
+    std::fill(m->scales_have.begin(), m->scales_have.end(), 1);
+    m->final_have = true;
+    return finalize_impl(m);
 }
 
 RmsParams rms_params(const myl_model* m) {
@@ -1129,8 +1198,8 @@ hipError_t head_step(myl_model* m) {
         EpiHead hd{m->lm16_shifts, m->final_norm_frac, m->logits, m->state};
         return stream_i16<2, 4, 8>(src, m->lm16, m->V, m->H, hd, st, m->cus);
     }
-    EpiHead hd{m->emb_shifts, m->final_norm_frac, m->logits, m->state};
-    return stream_i8<2, 4, 8, true>(src, m->emb, m->V, m->H, hd, st, m->cus);
+    EpiHead hd{m->lm8_shifts, m->final_norm_frac, m->logits, m->state};
+    return stream_i8<2, 4, 8, true>(src, m->lm8, m->V, m->H, hd, st, m->cus);
 }
 
 hipError_t embed_step(myl_model* m, int mode, int token, int pos, int64_t* tokens_dev) {
@@ -1181,6 +1250,51 @@ hipError_t capture_step(myl_model* m) {
 
 }  // namespace
 
+namespace myl {
+
+int model_setup(myl_ctx* ctx, const myl_synth_spec& s, bool tied, const myl_luts* luts, myl_model** out) {
+    *out = nullptr;
+    if (!s.hidden || !s.layers || !s.heads || !s.kv_heads || !s.head_dim || !s.inter || !s.vocab || !s.max_pos)
+        return ctx->fail(MYL_E_INVALID, "model: every dimension must be > 0");
+    if (s.heads % s.kv_heads || s.heads * s.head_dim != s.hidden)
+        return ctx->fail(MYL_E_INVALID, "model: heads must divide evenly into KV heads and tile hidden");
+    if (s.head_dim != 64 && s.head_dim != 128)
+        return ctx->fail(MYL_E_UNSUPPORTED, "model: the fused decode path takes head_dim 64 or 128");
+    if (s.hidden % 16 || s.inter % 16) return ctx->fail(MYL_E_UNSUPPORTED, "model: hidden and intermediate must be multiples of 16");
+    if (!luts->rsqrt || luts->rsqrt_len < 2 || !luts->silu || !luts->silu_len || !luts->exp || !luts->cos ||
+        !luts->sin || luts->rope_len < s.head_dim / 2)
+        return ctx->fail(MYL_E_INVALID, "model: incomplete LUT set");
+    if ((uint64_t)s.vocab * s.hidden > (uint64_t)INT32_MAX * 16)
+        return ctx->fail(MYL_E_UNSUPPORTED, "model: embedding too large");
+    (void)hipSetDevice(ctx->device);
+    myl_model* m = new (std::nothrow) myl_model();
+    if (!m) return MYL_E_NOMEM;
+    m->ctx = ctx;
+    m->spec = s;
+    m->tied = tied;
+    m->H = (int)s.hidden;
+    m->I = (int)s.inter;
+    m->V = (int)s.vocab;
+    m->hd = (int)s.head_dim;
+    m->hd_log = ilog2_exact(m->hd);
+    m->G = (int)(s.heads / s.kv_heads);
+    m->nq = (int)(s.heads * s.head_dim);
+    m->nkv = (int)(s.kv_heads * s.head_dim);
+    m->max_pos = (int)s.max_pos;
+    m->cus = ctx->prop.multiProcessorCount > 0 ? ctx->prop.multiProcessorCount : 1;
+    int rc = alloc_impl(m, luts);
+    if (rc) {
+        delete m;
+        return rc;
+    }
+    *out = m;
+    return MYL_OK;
+}
+
+int model_finalize(myl_model* m) { return finalize_impl(m); }
+
+}  // namespace myl
+
 extern "C" {
 
 int myl_model_set_graphs(myl_model* m, int enable) {
@@ -1222,35 +1336,10 @@ int myl_model_timing(myl_model* m, int enable, double* ms_out, uint64_t* counts_
 int myl_model_create_synthetic(myl_ctx* ctx, const myl_synth_spec* spec, const myl_luts* luts, myl_model** out) {
     if (!ctx || !spec || !luts || !out) return MYL_E_INVALID;
     *out = nullptr;
-    const myl_synth_spec& s = *spec;
-    if (!s.hidden || !s.layers || !s.heads || !s.kv_heads || !s.head_dim || !s.inter || !s.vocab || !s.max_pos)
-        return ctx->fail(MYL_E_INVALID, "model: every dimension must be > 0");
-    if (s.heads % s.kv_heads || s.heads * s.head_dim != s.hidden)
-        return ctx->fail(MYL_E_INVALID, "model: heads must divide evenly into KV heads and tile hidden");
-    if (s.head_dim != 64 && s.head_dim != 128)
-        return ctx->fail(MYL_E_UNSUPPORTED, "model: the fused decode path takes head_dim 64 or 128");
-    if (s.hidden % 16 || s.inter % 16) return ctx->fail(MYL_E_UNSUPPORTED, "model: hidden and intermediate must be multiples of 16");
-    if (!luts->rsqrt || luts->rsqrt_len < 2 || !luts->silu || !luts->silu_len || !luts->exp || !luts->cos ||
-        !luts->sin || luts->rope_len < s.head_dim / 2)
-        return ctx->fail(MYL_E_INVALID, "model: incomplete LUT set");
-    if ((uint64_t)s.vocab * s.hidden > (uint64_t)INT32_MAX * 16)
-        return ctx->fail(MYL_E_UNSUPPORTED, "model: embedding too large");
-    (void)hipSetDevice(ctx->device);
-    myl_model* m = new (std::nothrow) myl_model();
-    if (!m) return MYL_E_NOMEM;
-    m->ctx = ctx;
-    m->spec = s;
-    m->H = (int)s.hidden;
-    m->I = (int)s.inter;
-    m->V = (int)s.vocab;
-    m->hd = (int)s.head_dim;
-    m->hd_log = ilog2_exact(m->hd);
-    m->G = (int)(s.heads / s.kv_heads);
-    m->nq = (int)(s.heads * s.head_dim);
-    m->nkv = (int)(s.kv_heads * s.head_dim);
-    m->max_pos = (int)s.max_pos;
-    m->cus = ctx->prop.multiProcessorCount > 0 ? ctx->prop.multiProcessorCount : 1;
-    int rc = build(m, luts);
+    myl_model* m = nullptr;
+    // The synthetic int8 head is the tied embedding (model.rs:297-307).
+    int rc = myl::model_setup(ctx, *spec, /*tied=*/true, luts, &m);
+    if (!rc) rc = synth_fill(m);
     if (rc) {
         delete m;
         return rc;
@@ -1269,6 +1358,7 @@ int myl_model_reset(myl_model* m) {
 
 int myl_model_forward_token(myl_model* m, uint32_t token, uint32_t pos, int32_t* logits, int64_t* argmax_out) {
     if (!m) return MYL_E_INVALID;
+    if (int nr = m->not_ready()) return nr;
     myl_ctx* c = m->ctx;
     if (token >= (uint32_t)m->V) return c->fail(MYL_E_INVALID, "forward_token: token id out of range");
     if (pos >= (uint32_t)m->max_pos) return c->fail(MYL_E_INVALID, "forward_token: position beyond the KV capacity");
@@ -1295,6 +1385,7 @@ int myl_model_forward_token(myl_model* m, uint32_t token, uint32_t pos, int32_t*
 int myl_model_decode_greedy(myl_model* m, uint32_t token, uint32_t pos, uint32_t n_steps, int64_t* tokens_out,
                             int32_t* logits_out) {
     if (!m) return MYL_E_INVALID;
+    if (int nr = m->not_ready()) return nr;
     myl_ctx* c = m->ctx;
     if (n_steps == 0) return MYL_OK;
     if (token >= (uint32_t)m->V) return c->fail(MYL_E_INVALID, "decode: token id out of range");
@@ -1341,6 +1432,7 @@ int myl_model_decode_greedy(myl_model* m, uint32_t token, uint32_t pos, uint32_t
 
 int myl_model_prefill(myl_model* m, const uint32_t* tokens, uint32_t n, uint32_t pos0, int32_t* last_logits) {
     if (!m || (!tokens && n)) return MYL_E_INVALID;
+    if (int nr = m->not_ready()) return nr;
     myl_ctx* c = m->ctx;
     if (n == 0) return MYL_OK;
     if ((uint64_t)pos0 + n > (uint64_t)m->max_pos) return c->fail(MYL_E_INVALID, "prefill: beyond the KV capacity");
@@ -1365,6 +1457,7 @@ int myl_model_prefill(myl_model* m, const uint32_t* tokens, uint32_t n, uint32_t
 
 int myl_model_embed_token(myl_model* m, uint32_t token, int16_t* hidden) {
     if (!m || !hidden) return MYL_E_INVALID;
+    if (int nr = m->not_ready()) return nr;
     myl_ctx* c = m->ctx;
     if (token >= (uint32_t)m->V) return c->fail(MYL_E_INVALID, "embed_token: token id out of range");
     int rc = c->hip(embed_step(m, 0, (int)token, 0, nullptr), "embed_token");
@@ -1376,6 +1469,7 @@ int myl_model_embed_token(myl_model* m, uint32_t token, int16_t* hidden) {
 
 int myl_model_run_layers(myl_model* m, int16_t* hidden, uint32_t pos, uint32_t layer_start, uint32_t layer_end) {
     if (!m || !hidden) return MYL_E_INVALID;
+    if (int nr = m->not_ready()) return nr;
     myl_ctx* c = m->ctx;
     if (layer_end > m->spec.layers || layer_start > layer_end || pos >= (uint32_t)m->max_pos)
         return c->fail(MYL_E_INVALID, "run_layers: bad layer range or position");
@@ -1397,6 +1491,7 @@ int myl_model_run_layers(myl_model* m, int16_t* hidden, uint32_t pos, uint32_t l
 
 int myl_model_head_logits(myl_model* m, const int16_t* hidden, int32_t* logits) {
     if (!m || !hidden || !logits) return MYL_E_INVALID;
+    if (int nr = m->not_ready()) return nr;
     myl_ctx* c = m->ctx;
     int rc = c->hip(hipMemcpyAsync(m->hidden, hidden, (size_t)m->H * 2, hipMemcpyHostToDevice, c->stream), "hidden");
     if (rc) return rc;

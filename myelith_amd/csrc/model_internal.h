@@ -5,6 +5,7 @@
 #include "abi_internal.h"
 #include "../../include/myl_synth.h"
 
+#include <string>
 #include <utility>
 #include <vector>
 
@@ -41,6 +42,14 @@ struct LayerDev {
 struct BatchState;  // batch.hip
 void batch_free(BatchState* b);
 
+// What a model receives before it is sealed: model-wide tensors, then
+// kLayerSlots tensors per layer (index kModelSlots + layer * kLayerSlots + slot).
+enum ModelSlot { SLOT_EMB, SLOT_LM8, SLOT_LM16, SLOT_FINAL_GAMMA, kModelSlots };
+enum LayerSlot {
+    SLOT_IN_GAMMA, SLOT_POST_GAMMA, SLOT_Q, SLOT_K, SLOT_V, SLOT_O, SLOT_GATE, SLOT_UP, SLOT_DOWN,
+    SLOT_BQ, SLOT_BK, SLOT_BV, kLayerSlots
+};
+
 }  // namespace myl
 
 using myl::DecodeState;
@@ -63,6 +72,22 @@ struct myl_model {
     uint8_t* final_gamma_s = nullptr;
     uint8_t* final_res = nullptr;
     uint8_t final_norm_frac = 0;
+    // the int8 LM head (model.rs:297-307): the embedding when tied, else its own
+    bool tied = true;
+    int8_t* lm8 = nullptr;
+    uint8_t* lm8_shifts = nullptr;
+    // stored row of each logical output row (q/k/v pair-ordered, gate/up interleaved)
+    std::vector<int32_t> qkv_map, gu_map;
+    int32_t *qkv_map_dev = nullptr, *gu_map_dev = nullptr;
+    // host copies of the per-channel residual scales, and what has arrived
+    std::vector<std::vector<uint8_t>> h_res_in, h_res_mid;
+    std::vector<uint8_t> h_final_res;
+    std::vector<uint8_t> have;         // per ModelSlot / LayerSlot
+    std::vector<uint8_t> scales_have;  // per layer
+    bool final_have = false;
+    bool ready = false;                // sealed by myl::model_finalize
+    void* io = nullptr;                // upload staging (model_io.hip) while tensors arrive
+    void (*io_free)(void*) = nullptr;
     int16_t *rsqrt = nullptr, *silu = nullptr, *exp_lut = nullptr, *cos_lut = nullptr, *sin_lut = nullptr;
     int rsqrt_len = 0, silu_len = 0, exp_len = 0;
     int64_t inv_n_q20 = 0;
@@ -99,13 +124,53 @@ struct myl_model {
         return (T*)p;
     }
     myl::BatchState* batch = nullptr;  // per-sequence KV caches and row buffers
+
+    // MYL_OK when the model is sealed, else the error of a forward call.
+    int not_ready() {
+        return ready ? 0 : ctx->fail(MYL_E_INVALID, "model: not finalized (tensors or scales missing)");
+    }
     ~myl_model() {
         if (ctx) (void)hipStreamSynchronize(ctx->stream);
         if (step_exec) (void)hipGraphExecDestroy(step_exec);
         if (step_graph) (void)hipGraphDestroy(step_graph);
         for (hipEvent_t e : ev_pool) (void)hipEventDestroy(e);
         if (batch) myl::batch_free(batch);
+        if (io) io_free(io);
         for (void* p : allocs) (void)hipFree(p);
     }
 };
 
+
+namespace myl {
+
+// Validates the dimensions, allocates the model and its buffers (model.hip).
+int model_setup(myl_ctx* ctx, const myl_synth_spec& s, bool tied, const myl_luts* luts, myl_model** out);
+// Checks completeness and derives the accumulation scales (model.hip).
+int model_finalize(myl_model* m);
+
+inline bool slot_required(const myl_model* m, size_t i) {
+    if (i < (size_t)kModelSlots) {
+        if (i == SLOT_LM8) return !m->tied && !m->spec.lm_head_int16;
+        if (i == SLOT_LM16) return m->spec.lm_head_int16 != 0;
+        return true;
+    }
+    const int t = (int)((i - kModelSlots) % kLayerSlots);
+    return t < SLOT_BQ || m->spec.attention_bias;
+}
+
+// The reference name of a slot (the HF original_name of the manifest).
+inline std::string slot_name(const myl_model* m, size_t i) {
+    static const char* model_names[kModelSlots] = {"model.embed_tokens.weight", "lm_head.weight", "lm_head.weight",
+                                                    "model.norm.weight"};
+    static const char* layer_names[kLayerSlots] = {
+        "input_layernorm.weight", "post_attention_layernorm.weight", "self_attn.q_proj.weight",
+        "self_attn.k_proj.weight", "self_attn.v_proj.weight", "self_attn.o_proj.weight", "mlp.gate_proj.weight",
+        "mlp.up_proj.weight", "mlp.down_proj.weight", "self_attn.q_proj.bias", "self_attn.k_proj.bias",
+        "self_attn.v_proj.bias"};
+    (void)m;
+    if (i < (size_t)kModelSlots) return model_names[i];
+    const size_t l = (i - kModelSlots) / kLayerSlots, t = (i - kModelSlots) % kLayerSlots;
+    return "model.layers." + std::to_string(l) + "." + layer_names[t];
+}
+
+}  // namespace myl

@@ -98,6 +98,15 @@ class LutSet:
         self.cos, self.sin = rope_luts(head_dim)
 
     @classmethod
+    def from_tables(cls, head_dim: int, rsqrt, silu, exp, cos, sin) -> "LutSet":
+        """A set holding given tables (an artifact's luts.json)."""
+        self = cls.__new__(cls)
+        self.head_dim = head_dim
+        for name, t in (("rsqrt", rsqrt), ("silu", silu), ("exp", exp), ("cos", cos), ("sin", sin)):
+            setattr(self, name, np.ascontiguousarray(t, dtype=np.int16))
+        return self
+
+    @classmethod
     def for_head_dim(cls, head_dim: int) -> "LutSet":
         if head_dim not in cls._cache:
             cls._cache[head_dim] = cls(head_dim)

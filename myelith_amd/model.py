@@ -17,7 +17,7 @@ import hashlib
 
 import numpy as np
 
-from ._lib import Luts, SynthSpec, lib
+from ._lib import LayerFracs, Luts, ModelDims, SynthSpec, lib
 from .backend import RocmBackend
 from .luts import LutSet
 
@@ -45,21 +45,109 @@ def luts_struct(luts: LutSet) -> tuple[Luts, tuple]:
 class IntegerModel:
     """model.rs:120-163, device-resident."""
 
-    def __init__(self, backend: RocmBackend, spec: dict, luts: LutSet | None = None):
+    def __init__(self, backend: RocmBackend, spec: dict, luts: LutSet | None = None, _handle=None):
+        """The seeded synthetic model of `spec` (include/myl_synth.h); the
+        classmethods `create` and `from_artifact` build the other kinds."""
         self.backend = backend
         self.spec = dict(spec)
         self.luts = luts or LutSet.for_head_dim(spec["head_dim"])
-        cspec = SynthSpec(**{k: int(spec[k]) for k, _ in SynthSpec._fields_})
-        cl, keep = luts_struct(self.luts)
-        h = C.c_void_p()
-        backend.check(lib().myl_model_create_synthetic(backend.handle, C.byref(cspec), C.byref(cl), C.byref(h)),
-                      "model_create_synthetic")
-        self._h = h
+        if _handle is None:
+            cspec = SynthSpec(**{k: int(spec[k]) for k, _ in SynthSpec._fields_})
+            cl, keep = luts_struct(self.luts)
+            _handle = C.c_void_p()
+            backend.check(lib().myl_model_create_synthetic(backend.handle, C.byref(cspec), C.byref(cl),
+                                                           C.byref(_handle)), "model_create_synthetic")
+        self._h = _handle
         self.vocab_size = spec["vocab"]
         self.hidden_size = spec["hidden"]
         self.num_layers = spec["layers"]
         self.num_kv_heads = spec["kv_heads"]
         self.head_dim = spec["head_dim"]
+        self.tied = bool(spec.get("tie_word_embeddings", True))
+
+    @classmethod
+    def create(cls, backend: RocmBackend, dims: dict, max_pos: int, luts: LutSet | None = None) -> "IntegerModel":
+        """An empty model of `dims` (ModelDims keys of _lib.ModelDims) to be
+        filled by upload_tensor / set_*_scales and sealed by finalize()."""
+        luts = luts or LutSet.for_head_dim(dims["head_dim"])
+        cd = ModelDims(**{k: int(dims.get(k, 0)) for k, _ in ModelDims._fields_})
+        cl, keep = luts_struct(luts)
+        h = C.c_void_p()
+        backend.check(lib().myl_model_create(backend.handle, C.byref(cd), max_pos, C.byref(cl), C.byref(h)),
+                      "model_create")
+        spec = {k: int(getattr(cd, k)) for k, _ in ModelDims._fields_}
+        spec["max_pos"] = max_pos or spec["max_context"]
+        return cls(backend, spec, luts, _handle=h)
+
+    @classmethod
+    def from_artifact(cls, backend: RocmBackend, artifact, max_pos: int = 0) -> "IntegerModel":
+        """load_model (loader.rs:611-636): the model of an artifact directory
+        (a path or an opened myelith_amd.artifact.Artifact) streamed to HBM."""
+        from .artifact import Artifact
+        art = artifact if isinstance(artifact, Artifact) else Artifact(artifact)
+        try:
+            h = C.c_void_p()
+            backend.check(lib().myl_model_load_artifact(backend.handle, art.handle, max_pos, C.byref(h)),
+                          "model_load_artifact")
+            spec = dict(art.dims)
+            spec["max_pos"] = max_pos or spec["max_context"]
+            luts = LutSet.from_tables(spec["head_dim"], **{n: art.lut(n) for n in ("rsqrt", "silu", "exp", "cos", "sin")})
+            return cls(backend, spec, luts, _handle=h)
+        finally:
+            if art is not artifact:
+                art.close()
+
+    # ---- tensors and scales in the reference layout ----
+
+    def upload_tensor(self, name: str, data, shifts) -> None:
+        """One tensor by its HF name (include/myl_hip.h, myl_model_upload_tensor);
+        int16 data selects the 16-bit form (the int16 LM head, biases)."""
+        a = np.ascontiguousarray(data)
+        bits = 16 if a.dtype == np.int16 else 8
+        if bits == 8:
+            a = a.astype(np.int8, copy=False)
+        sh = np.ascontiguousarray(shifts, dtype=np.uint8)
+        shape = (C.c_uint64 * a.ndim)(*a.shape)
+        self._check(lib().myl_model_upload_tensor(self._h, name.encode(), a.ctypes.data, bits, shape, a.ndim,
+                                                  sh.ctypes.data, sh.size), f"upload {name}")
+
+    def download_tensor(self, name: str, shape, bits: int = 8):
+        """The tensor `name` in the reference layout and its per-row shifts."""
+        a = np.zeros(shape, np.int16 if bits == 16 else np.int8)
+        sh = np.zeros(a.shape[0], np.uint8)
+        self._check(lib().myl_model_download_tensor(self._h, name.encode(), bits, a.ctypes.data, a.nbytes,
+                                                    sh.ctypes.data, sh.size), f"download {name}")
+        return a, sh
+
+    def set_layer_scales(self, layer: int, fracs: dict, res_in, res_mid) -> None:
+        f = LayerFracs(**{k: int(fracs[k]) for k, _ in LayerFracs._fields_})
+        ri = np.ascontiguousarray(res_in, dtype=np.uint8)
+        rm = np.ascontiguousarray(res_mid, dtype=np.uint8)
+        assert ri.size == self.hidden_size and rm.size == self.hidden_size
+        self._check(lib().myl_model_set_layer_scales(self._h, layer, C.byref(f), ri.ctypes.data, rm.ctypes.data),
+                    "set_layer_scales")
+
+    def set_final_scales(self, final_norm_frac: int, final_res) -> None:
+        fr = np.ascontiguousarray(final_res, dtype=np.uint8)
+        assert fr.size == self.hidden_size
+        self._check(lib().myl_model_set_final_scales(self._h, final_norm_frac, fr.ctypes.data), "set_final_scales")
+
+    def layer_scales(self, layer: int):
+        f = LayerFracs()
+        ri = np.zeros(self.hidden_size, np.uint8)
+        rm = np.zeros(self.hidden_size, np.uint8)
+        self._check(lib().myl_model_get_layer_scales(self._h, layer, C.byref(f), ri.ctypes.data, rm.ctypes.data),
+                    "layer_scales")
+        return {k: int(getattr(f, k)) for k, _ in LayerFracs._fields_}, ri, rm
+
+    def final_scales(self):
+        nf = C.c_uint8()
+        fr = np.zeros(self.hidden_size, np.uint8)
+        self._check(lib().myl_model_get_final_scales(self._h, C.byref(nf), fr.ctypes.data), "final_scales")
+        return int(nf.value), fr
+
+    def finalize(self) -> None:
+        self._check(lib().myl_model_finalize(self._h), "finalize")
 
     def close(self) -> None:
         if getattr(self, "_h", None):
