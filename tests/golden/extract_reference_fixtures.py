@@ -9,7 +9,14 @@ It copies DATA only (inputs, expected outputs, hashes), never source:
     INTEGER_LLM/conformance/vectors/op/{linear_w8a16_identity,rmsnorm_basic,softmax_basic}.golden.json
     -> tests/golden/op_vectors.json (tensor data + metadata + declared SHA-256);
   - the LUT hashes of both scale packs
-    INTEGER_LLM/scale_packs/qwen2.5-{0.5b,7b}/luts.json -> tests/golden/lut_hashes.json.
+    INTEGER_LLM/scale_packs/qwen2.5-{0.5b,7b}/luts.json -> tests/golden/lut_hashes.json;
+  - the layer and e2e conformance vectors of Qwen2.5-0.5B without their bulk
+    data: each vector's name, level, metadata scalars, declared tensor hashes,
+    and the small integer arrays (position, prompt and generated token ids)
+    INTEGER_LLM/conformance/vectors/{layer,e2e}/*.golden.json
+    -> tests/golden/model_vector_index.json.  The hidden-state payloads need
+    the calibrated 0.5B weights to mean anything; their hashes pin the seeded
+    layer-input generator.
 
 The GPU machines never see /root/reference; the tests read only these files.
 """
@@ -43,7 +50,22 @@ def main() -> None:
         meta = json.loads((REF / "scale_packs" / pack / "luts.json").read_text())
         hashes[pack] = {k: {"sha256": v["hash"], "length": v["length"]} for k, v in meta.items()}
     (OUT / "lut_hashes.json").write_text(json.dumps(hashes, indent=1, sort_keys=True) + "\n")
-    print("wrote", OUT / "op_vectors.json", "and", OUT / "lut_hashes.json")
+    index = {}
+    for level in ("layer", "e2e"):
+        for src in sorted((REF / "conformance" / "vectors" / level).glob("*.golden.json")):
+            gv = json.loads(src.read_text())
+            meta = {k: v for k, v in gv["metadata"].items() if not isinstance(v, list)}
+            tensors = {}
+            for side in ("inputs", "outputs"):
+                for name, t in gv[side].items():
+                    e = {"dtype": t["dtype"], "shape": t.get("shape"), "hash": t["hash"]}
+                    if len(t["data"]) <= 64:
+                        e["data"] = t["data"]
+                    tensors[f"{side}.{name}"] = e
+            index[gv["name"]] = {"source": f"INTEGER_LLM/conformance/vectors/{level}/{src.name}", "level": gv["level"],
+                                 "theta_v_hash": gv["theta_v_hash"], "metadata": meta, "tensors": tensors}
+    (OUT / "model_vector_index.json").write_text(json.dumps(index, indent=1, sort_keys=True) + "\n")
+    print("wrote", OUT / "op_vectors.json", OUT / "lut_hashes.json", "and", OUT / "model_vector_index.json")
 
 
 if __name__ == "__main__":
