@@ -7,7 +7,7 @@
  * binds through `extern "C"`, replacing the delegating stub.  Every compute
  * entry point is bit-identical to the reference Rust kernel it names.
  *
- * Three layers:
+ * Sections:
  *   1. Backend-trait mirror (host slices in, host slices out), one function per
  *      method of `trait Backend` (INTEGER_LLM/kernels/src/backend.rs:23-127) and
  *      per free function that runtime/src/model.rs calls directly
@@ -17,7 +17,11 @@
  *      asynchronous on the context's stream, with a batch dimension M.
  *   3. A device-resident model (`myl_model_*`): forward_token / run_layers /
  *      head_logits of runtime/src/model.rs:229-399 with weights uploaded once
- *      and the KV cache of runtime/src/kv_cache.rs held in HBM.
+ *      and the KV cache of runtime/src/kv_cache.rs held in HBM; batched rows
+ *      over per-sequence KV caches.
+ *   4. An integer MoE layer (`myl_moe_*`, build-defined).
+ *   5. The reference's artifact directory format (`myl_artifact_*`,
+ *      runtime/src/loader.rs) and tensor uploads into a device model.
  *
  * Status codes: 0 = ok; MYL_E_INVALID where the reference panics (assert!,
  * empty slices, length mismatches); MYL_E_HIP for runtime failures;
