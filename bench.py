@@ -283,7 +283,9 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=7)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
-    ap.add_argument("--no-batch", action="store_true", help="skip the batched decode and teacher-forced prefill")
+    ap.add_argument("--no-batch", action="store_true",
+                    help="skip the batched decode, teacher-forced prefill and MoE sections")
+    ap.add_argument("--no-batched-decode", action="store_true", help="skip only the batched decode section")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="also run three 256 MiB device-to-device copies: the known-size kernel that calibrates "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -307,7 +309,12 @@ def main() -> int:
     backend.use_torch_stream()
 
     total_steps = args.warmup + args.steps
-    spec = make_spec(QWEN25_7B, seed=args.seed, max_pos=args.ctx + total_steps + 8)
+    # KV capacity: the decode run, and the teacher-forced prefill (1024 positions)
+    # and batched decode (2048 + 32) sections when they run
+    need = args.ctx + total_steps + 8
+    if not args.no_batch:
+        need = max(need, 1024 + 8 if args.no_batched_decode else 2048 + 32 + 8)
+    spec = make_spec(QWEN25_7B, seed=args.seed, max_pos=need)
     t0 = time.time()
     model = IntegerModel(backend, spec, LutSet.for_head_dim(spec["head_dim"]))
     log(f"7B-shape model built in HBM in {time.time() - t0:.1f} s")
@@ -368,7 +375,8 @@ def main() -> int:
     prefill_tf, batch_dec, moe = None, None, None
     if not args.no_batch:
         prefill_tf = teacher_forced_prefill(model, backend, args.seed)
-        batch_dec = batched_decode(model, args.seed)
+        if not args.no_batched_decode:
+            batch_dec = batched_decode(model, args.seed)
         moe = moe_layer(backend, args.seed)
 
     cpu = None
