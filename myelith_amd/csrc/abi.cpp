@@ -418,7 +418,7 @@ int myl_linear_w8a16_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, c
     if (!ctx) return MYL_E_INVALID;
     int rc = check_gemv(ctx, M, ldx, N, K, ldo, "linear_w8a16_dev");
     if (rc || M == 0 || N == 0) return rc;
-    const MmCtx* mm = ctx->mm_ctx(M > 1 ? M * N : 0, M >= 256 ? 2 * M * K : 0);
+    const MmCtx* mm = ctx->mm_ctx(M > 1 ? M * N : 0, M >= 2 ? 2 * M * K : 0);
     return ctx->hip(linear_w8a16(x, (int)M, (int)ldx, W, (int)N, (int)K, w_shifts, act_frac, out_frac, out_frac_pc,
                                  out, (int)ldo, ctx->stream, mm), "linear_w8a16_dev");
 }
@@ -428,7 +428,7 @@ int myl_linear_w8a16_mult_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t l
     if (!ctx) return MYL_E_INVALID;
     int rc = check_gemv(ctx, M, ldx, N, K, ldo, "linear_w8a16_mult_dev");
     if (rc || M == 0 || N == 0) return rc;
-    const MmCtx* mm = ctx->mm_ctx(M > 1 ? M * N : 0, M >= 256 ? 2 * M * K : 0);
+    const MmCtx* mm = ctx->mm_ctx(M > 1 ? M * N : 0, M >= 2 ? 2 * M * K : 0);
     return ctx->hip(linear_w8a16_mult(x, (int)M, (int)ldx, W, (int)N, (int)K, mult, shift, out, (int)ldo, ctx->stream,
                                       mm), "linear_w8a16_mult_dev");
 }
@@ -439,7 +439,7 @@ int myl_logits_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, const v
     if (!ctx) return MYL_E_INVALID;
     int rc = check_gemv(ctx, M, ldx, N, K, ldo, "logits_dev");
     if (rc || M == 0 || N == 0) return rc;
-    const MmCtx* mm = ctx->mm_ctx(M > 1 ? M * N : 0, M >= 256 ? 2 * M * K : 0);
+    const MmCtx* mm = ctx->mm_ctx(M > 1 ? M * N : 0, M >= 2 ? 2 * M * K : 0);
     if (w_bits == 8)
         return ctx->hip(logits_w8(x, (int)M, (int)ldx, (const int8_t*)W, (int)N, (int)K, row_shifts, norm_frac,
                                   logit_frac, out, (int)ldo, ctx->stream, mm), "logits_dev");
@@ -454,7 +454,7 @@ int myl_dot_i8_i16_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, con
     if (!ctx) return MYL_E_INVALID;
     int rc = check_gemv(ctx, M, ldx, N, K, ldo, "dot_i8_i16_dev");
     if (rc || M == 0 || N == 0) return rc;
-    const MmCtx* mm = ctx->mm_ctx(M > 1 ? M * N : 0, M >= 256 ? 2 * M * K : 0);
+    const MmCtx* mm = ctx->mm_ctx(M > 1 ? M * N : 0, M >= 2 ? 2 * M * K : 0);
     return ctx->hip(dot_raw_w8(x, (int)M, (int)ldx, W, (int)N, (int)K, out, (int)ldo, ctx->stream, mm),
                     "dot_i8_i16_dev");
 }

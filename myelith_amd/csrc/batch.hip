@@ -25,6 +25,7 @@
 #include "gemm_dispatch.h"
 #include "model_internal.h"
 #include "ops.h"
+#include "rows_attn.h"
 #include "rows_epi.h"
 #include "wave.h"
 
@@ -48,11 +49,14 @@ struct BatchState {
     int16_t *GU = nullptr, *Hh = nullptr;
     int32_t* logits = nullptr;           // [rows_cap][V]
     int64_t* argmax = nullptr;           // [rows_cap]
+    uint64_t* argmax_part = nullptr;     // [rows_cap][ceil(V / kArgChunk)] best keys per chunk
     int64_t* tokens_out = nullptr;       // greedy chains: [steps][rows]
     size_t tokens_out_cap = 0;
     int32_t* scores = nullptr;           // [rows_cap][heads][lmax_cap]
     int32_t* stats = nullptr;            // [rows_cap][heads][2]: max, wrapping exp sum
-    unsigned long long* pv = nullptr;    // [rows_cap][nq], zero between uses
+    int64_t* part = nullptr;             // [lmax_cap / 256][rows_cap][nq]: exact P.V per position range
+    AttnTile* tiles = nullptr;           // rows grouped by sequence for the attention kernels
+    int ntiles = 0, tiles_cap = 0;
     std::vector<void*> allocs_rows;      // row buffers (regrown together)
     std::vector<void*> allocs_scores;
 };
@@ -64,6 +68,7 @@ void batch_free(BatchState* b) {
     if (b->kc) (void)hipFree(b->kc);
     if (b->vc) (void)hipFree(b->vc);
     if (b->tokens_out) (void)hipFree(b->tokens_out);
+    if (b->tiles) (void)hipFree(b->tiles);
     delete b;
 }
 
@@ -123,80 +128,6 @@ __global__ __launch_bounds__(256) void rope_scatter_kernel(const int16_t* __rest
     dst[p + half] = y1;
 }
 
-// int16 pairs -> (hi pair, lo pair) with v = 256 * hi + lo, lo in [0, 255].
-__device__ inline void split_pair16(uint32_t v, uint32_t& hi, uint32_t& lo) {
-    const int32_t a = (int16_t)(v & 0xFFFFu), b = (int16_t)(v >> 16);
-    hi = ((uint32_t)(uint16_t)(int16_t)(a >> 8)) | ((uint32_t)(uint16_t)(int16_t)(b >> 8) << 16);
-    lo = (v & 0x00FF00FFu);
-}
-
-constexpr int kRowChunk = 64;  // positions per attention block
-
-// s_j = (i32)RNE(q . k_j * mult, shift) (attention.rs:66-67) for the G query
-// heads of KV head g, row r, positions j of chunk c.  Grid (chunks, kvh, R).
-// LPP = HD / 8 lanes read one K row (16 bytes each); q . k is exact as
-// 256 * sum(k * q_hi) + sum(k * q_lo) on v_dot2_i32_i16.
-template <int HD>
-__global__ __launch_bounds__(256) void rows_scores_kernel(const int32_t* __restrict__ rows, int rows_cap,
-                                                          const int16_t* __restrict__ Q, int nq,
-                                                          const int16_t* __restrict__ kc, size_t seq_stride,
-                                                          int max_pos, int G, int64_t score_mult, uint8_t score_shift,
-                                                          int32_t* __restrict__ scores, int heads, int lcap) {
-    constexpr int LPP = HD / 8;
-    constexpr int PPP = 256 / LPP;             // positions per pass
-    constexpr int PASSES = kRowChunk / PPP;
-    const int c = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
-    const int seq = rows[r], L = rows[rows_cap + r] + 1;
-    const int base = c * kRowChunk;
-    if (base >= L) return;
-    const int sub = threadIdx.x % LPP, slot = threadIdx.x / LPP;
-    const int16_t* kg = kc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD;
-    typedef short __attribute__((ext_vector_type(2))) s2;
-    auto d2 = [](uint32_t a, uint32_t b, int32_t acc) {
-        return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, a), __builtin_bit_cast(s2, b), acc, false);
-    };
-    uint4 kv[PASSES];
-#pragma unroll
-    for (int it = 0; it < PASSES; ++it) {
-        const int j = base + it * PPP + slot;
-        kv[it] = j < L ? *reinterpret_cast<const uint4*>(kg + (size_t)j * HD + sub * 8) : make_uint4(0, 0, 0, 0);
-    }
-    for (int h = 0; h < G; ++h) {
-        const int head = g * G + h;
-        const uint4 qv = *reinterpret_cast<const uint4*>(Q + (size_t)r * nq + (size_t)head * HD + sub * 8);
-        uint4 qh, ql;
-        split_pair16(qv.x, qh.x, ql.x);
-        split_pair16(qv.y, qh.y, ql.y);
-        split_pair16(qv.z, qh.z, ql.z);
-        split_pair16(qv.w, qh.w, ql.w);
-        int32_t* srow = scores + ((size_t)r * heads + head) * lcap;
-#pragma unroll
-        for (int it = 0; it < PASSES; ++it) {
-            const int j = base + it * PPP + slot;
-            int32_t ahi = 0, alo = 0;
-            ahi = d2(kv[it].x, qh.x, ahi);
-            ahi = d2(kv[it].y, qh.y, ahi);
-            ahi = d2(kv[it].z, qh.z, ahi);
-            ahi = d2(kv[it].w, qh.w, ahi);
-            alo = d2(kv[it].x, ql.x, alo);
-            alo = d2(kv[it].y, ql.y, alo);
-            alo = d2(kv[it].z, ql.z, alo);
-            alo = d2(kv[it].w, ql.w, alo);
-            if (LPP == 16) {
-                ahi = row_sum16_i32(ahi);
-                alo = row_sum16_i32(alo);
-            } else {
-                ahi = row_sum8_i32(ahi);
-                alo = row_sum8_i32(alo);
-            }
-            if (sub == 0 && j < L) {
-                const int64_t dot = (int64_t)ahi * 256 + (int64_t)alo;
-                srow[j] = (int32_t)rshift_round64(wmul64(dot, score_mult), score_shift);
-            }
-        }
-    }
-}
-
 // Softmax statistics of one (row, head) over its L scores (softmax.rs:32-41):
 // m = max, S = wrapping i32 sum of the exp LUT values.  Grid (heads, R).
 __global__ __launch_bounds__(256) void rows_stats_kernel(const int32_t* __restrict__ rows, int rows_cap,
@@ -218,95 +149,6 @@ __global__ __launch_bounds__(256) void rows_stats_kernel(const int32_t* __restri
     if (threadIdx.x == 0) {
         stats[((size_t)r * heads + h) * 2] = mx;
         stats[((size_t)r * heads + h) * 2 + 1] = (int32_t)S;
-    }
-}
-
-// p_j = RNE(e_j * 2^14 / S) (or the uniform split when S == 0, softmax.rs:42-63)
-// for the G heads of KV head g and the positions of chunk c, then the exact
-// partial P.V per dimension (attention.rs:75-81) added into pv with 64-bit
-// atomics.  Grid (chunks, kvh, R).
-template <int HD>
-__global__ __launch_bounds__(256) void rows_pv_kernel(const int32_t* __restrict__ rows, int rows_cap,
-                                                      const int32_t* __restrict__ scores,
-                                                      const int32_t* __restrict__ stats, int heads, int lcap,
-                                                      const int16_t* __restrict__ vc, size_t seq_stride, int max_pos,
-                                                      int G, const int16_t* __restrict__ lut, uint32_t lut_len,
-                                                      uint8_t lut_shift, unsigned long long* __restrict__ pv, int nq) {
-    constexpr int TPR = HD / 2;             // threads per V row (one dimension pair each)
-    constexpr int STREAMS = 256 / TPR;      // position streams
-    constexpr int PER = kRowChunk / STREAMS;
-    constexpr int GMAX = 16;
-    __shared__ int32_t p[GMAX][kRowChunk];
-    __shared__ int64_t red[STREAMS][HD];
-    const int c = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
-    const int seq = rows[r], L = rows[rows_cap + r] + 1;
-    const int base = c * kRowChunk;
-    if (base >= L) return;
-    const int n = min(kRowChunk, L - base);
-    const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
-    const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
-    for (int t = threadIdx.x; t < G * kRowChunk; t += 256) {
-        const int h = t / kRowChunk, j = t % kRowChunk;
-        const int head = g * G + h;
-        int32_t pv_ = 0;
-        if (j < n) {
-            const int32_t mx = stats[((size_t)r * heads + head) * 2];
-            const int32_t S = stats[((size_t)r * heads + head) * 2 + 1];
-            if (S == 0) {
-                const uint64_t rl = recip32((uint32_t)L);
-                uint32_t qq, rr;
-                udivmod32((uint32_t)one, (uint32_t)L, rl, &qq, &rr);
-                const int32_t ubase = (int32_t)qq;
-                const int32_t urem = wsub32(one, wmul32(ubase, L));
-                pv_ = ubase + (((uint64_t)(base + j) < (uint64_t)(int64_t)urem) ? 1 : 0);
-            } else {
-                const uint64_t rs = recip32(S < 0 ? 0u - (uint32_t)S : (uint32_t)S);
-                const int32_t z = scores[((size_t)r * heads + head) * lcap + base + j];
-                const int32_t e = exp_lookup(sat_sub32(mx, z), lut, lut_len, lut_shift, lut_one);
-                pv_ = softmax_div_round(wmul32(e, one), S, rs);
-            }
-        }
-        p[h][j] = pv_;
-    }
-    __syncthreads();
-    const int dp = threadIdx.x % TPR, stream = threadIdx.x / TPR;
-    const int16_t* vg = vc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD;
-    uint32_t vv[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int t = stream + i * STREAMS;
-        vv[i] = t < n ? *reinterpret_cast<const uint32_t*>(vg + (size_t)(base + t) * HD + 2 * dp) : 0u;
-    }
-    for (int h = 0; h < G; ++h) {
-        int64_t a0 = 0, a1 = 0;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int64_t pj = p[h][stream + i * STREAMS];
-            a0 = wadd64(a0, pj * (int64_t)(int16_t)(vv[i] & 0xFFFFu));
-            a1 = wadd64(a1, pj * (int64_t)(int16_t)(vv[i] >> 16));
-        }
-        red[stream][2 * dp] = a0;
-        red[stream][2 * dp + 1] = a1;
-        __syncthreads();
-        if (threadIdx.x < HD) {
-            int64_t sum = 0;
-#pragma unroll
-            for (int k = 0; k < STREAMS; ++k) sum = wadd64(sum, red[k][threadIdx.x]);
-            atomicAdd(pv + (size_t)r * nq + (size_t)(g * G + h) * HD + threadIdx.x, (unsigned long long)sum);
-        }
-        __syncthreads();
-    }
-}
-
-// attention.rs:84-86 then model.rs:563-567; clears pv.  Grid R.
-__global__ __launch_bounds__(256) void rows_attn_out_kernel(unsigned long long* __restrict__ pv, int nq,
-                                                            uint8_t v_frac, uint8_t out_frac, int16_t* __restrict__ A) {
-    const int r = blockIdx.x;
-    for (int i = threadIdx.x; i < nq; i += 256) {
-        unsigned long long* a = pv + (size_t)r * nq + i;
-        const int16_t v = clamp_i16_i64(rshift_round64((int64_t)*a, MYL_TV_PROB_FRAC_BITS));
-        *a = 0;
-        A[(size_t)r * nq + i] = clamp_i16(rescale32((int32_t)v, v_frac, out_frac));
     }
 }
 
@@ -376,11 +218,10 @@ int ensure_rows(myl_model* m, int R) {
     b->Hh = balloc<int16_t>(L, R * I);
     b->logits = balloc<int32_t>(L, R * V);
     b->argmax = balloc<int64_t>(L, R);
+    b->argmax_part = balloc<uint64_t>(L, (size_t)R * ((V + kArgChunk - 1) / kArgChunk));
     b->stats = balloc<int32_t>(L, (size_t)R * m->spec.heads * 2);
-    b->pv = balloc<unsigned long long>(L, R * nq);
     for (void* p : L)
         if (!p) return c->fail(MYL_E_NOMEM, "batch: row buffer allocation");
-    if (hipMemsetAsync(b->pv, 0, R * nq * 8, c->stream) != hipSuccess) return c->fail(MYL_E_HIP, "batch: pv clear");
     b->rows_cap = R;
     b->lmax_cap = 0;  // scores are sized by rows too
     return MYL_OK;
@@ -394,9 +235,10 @@ int ensure_scores(myl_model* m, int lmax) {
     for (void* p : b->allocs_scores) (void)hipFree(p);
     b->allocs_scores.clear();
     b->lmax_cap = 0;
-    const int cap = ((lmax + kRowChunk - 1) / kRowChunk) * kRowChunk;
+    const int cap = ((lmax + kAttnRange - 1) / kAttnRange) * kAttnRange;
     b->scores = balloc<int32_t>(b->allocs_scores, (size_t)b->rows_cap * m->spec.heads * cap);
-    if (!b->scores) return c->fail(MYL_E_NOMEM, "batch: score buffer allocation");
+    b->part = balloc<int64_t>(b->allocs_scores, (size_t)(cap / kAttnRange) * b->rows_cap * m->nq);
+    if (!b->scores || !b->part) return c->fail(MYL_E_NOMEM, "batch: score buffer allocation");
     b->lmax_cap = cap;
     return MYL_OK;
 }
@@ -409,9 +251,9 @@ hipError_t forward_rows(myl_model* m, int R, int lmax) {
     hipStream_t st = c->stream;
     const int H = m->H, I = m->I, V = m->V, nq = m->nq, nkv = m->nkv, hd = m->hd, G = m->G;
     const int nqkv = nq + 2 * nkv, heads = (int)m->spec.heads, kvh = (int)m->spec.kv_heads;
-    const MmCtx* mm = c->mm_ctx((size_t)R * std::max(2 * I, nqkv), R >= 256 ? (size_t)2 * R * std::max(I, H) : 0);
+    const MmCtx* mm = c->mm_ctx((size_t)R * std::max(2 * I, nqkv), R >= 2 ? (size_t)2 * R * std::max(I, H) : 0);
     const size_t sstride = seq_stride(m);
-    const int chunks = (lmax + kRowChunk - 1) / kRowChunk;
+    const int ranges = (lmax + kAttnRange - 1) / kAttnRange;
     const uint8_t lut_shift = MYL_TV_SCORE_FRAC_BITS - MYL_TV_EXP_INPUT_FRAC;
     hipError_t e;
     embed_rows_kernel<<<R, 256, 0, st>>>(b->rows + 3 * b->rows_cap, m->emb, m->emb_shifts, m->layers[0].res_in, H, b->X);
@@ -436,27 +278,31 @@ hipError_t forward_rows(myl_model* m, int R, int lmax) {
         if ((e = hipGetLastError()) != hipSuccess) return e;
         const uint32_t ss = (uint32_t)f.q_frac + f.k_frac + 15u;
         const uint8_t score_shift = (uint8_t)(ss > MYL_TV_SCORE_FRAC_BITS ? ss - MYL_TV_SCORE_FRAC_BITS : 0);
-        const dim3 ag(chunks, kvh, R);
+        const dim3 ag(b->ntiles, kvh, ranges);
+        const size_t pst = (size_t)b->rows_cap * nq;
         if (hd == 128)
-            rows_scores_kernel<128><<<ag, 256, 0, st>>>(b->rows, b->rows_cap, b->Q, nq, kc, sstride, m->max_pos, G,
-                                                        m->score_mult, score_shift, b->scores, heads, b->lmax_cap);
+            rows_qk_kernel<128><<<ag, kAttnThreads, attn_qk_lds<128>(), st>>>(
+                b->tiles, b->rows, b->rows_cap, b->Q, nq, kc, sstride, m->max_pos, G, m->score_mult, score_shift,
+                b->scores, heads, b->lmax_cap);
         else
-            rows_scores_kernel<64><<<ag, 256, 0, st>>>(b->rows, b->rows_cap, b->Q, nq, kc, sstride, m->max_pos, G,
-                                                       m->score_mult, score_shift, b->scores, heads, b->lmax_cap);
+            rows_qk_kernel<64><<<ag, kAttnThreads, attn_qk_lds<64>(), st>>>(
+                b->tiles, b->rows, b->rows_cap, b->Q, nq, kc, sstride, m->max_pos, G, m->score_mult, score_shift,
+                b->scores, heads, b->lmax_cap);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         rows_stats_kernel<<<dim3(heads, R), 256, 0, st>>>(b->rows, b->rows_cap, b->scores, heads, b->lmax_cap,
                                                           m->exp_lut, (uint32_t)m->exp_len, lut_shift, b->stats);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         if (hd == 128)
-            rows_pv_kernel<128><<<ag, 256, 0, st>>>(b->rows, b->rows_cap, b->scores, b->stats, heads, b->lmax_cap, vc,
-                                                    sstride, m->max_pos, G, m->exp_lut, (uint32_t)m->exp_len,
-                                                    lut_shift, b->pv, nq);
+            rows_pv_kernel<128><<<ag, kAttnThreads, attn_pv_lds<128>(), st>>>(b->tiles, b->rows, b->rows_cap, b->scores, b->stats, heads,
+                                                             b->lmax_cap, vc, sstride, m->max_pos, G, m->exp_lut,
+                                                             (uint32_t)m->exp_len, lut_shift, b->part, pst, nq);
         else
-            rows_pv_kernel<64><<<ag, 256, 0, st>>>(b->rows, b->rows_cap, b->scores, b->stats, heads, b->lmax_cap, vc,
-                                                   sstride, m->max_pos, G, m->exp_lut, (uint32_t)m->exp_len,
-                                                   lut_shift, b->pv, nq);
+            rows_pv_kernel<64><<<ag, kAttnThreads, attn_pv_lds<64>(), st>>>(b->tiles, b->rows, b->rows_cap, b->scores, b->stats, heads,
+                                                            b->lmax_cap, vc, sstride, m->max_pos, G, m->exp_lut,
+                                                            (uint32_t)m->exp_len, lut_shift, b->part, pst, nq);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        rows_attn_out_kernel<<<R, 256, 0, st>>>(b->pv, nq, f.v_frac, f.attn_out_frac, b->A);
+        rows_attn_out_kernel<<<dim3((nq + 255) / 256, R), 256, 0, st>>>(b->part, pst, b->rows, b->rows_cap, nq, f.v_frac,
+                                                                        f.attn_out_frac, b->A);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         EpiResidRows eo{};
         eo.shifts = Ld.so; eo.act_frac = f.attn_out_frac; eo.acc_frac = Ld.acc_attn; eo.res_frac = Ld.res_in;
@@ -489,7 +335,7 @@ hipError_t forward_rows(myl_model* m, int R, int lmax) {
         EpiLogits el{m->lm8_shifts, m->final_norm_frac, MYL_TV_LOGIT_FRAC_BITS, b->logits, V};
         if ((e = gemv_i8(b->Xn, R, H, m->lm8, V, H, el, st, mm)) != hipSuccess) return e;
     }
-    return argmax(b->logits, R, V, V, b->argmax, st);
+    return argmax_rows(b->logits, R, V, V, b->argmax, b->argmax_part, st);
 }
 
 // Checks the rows against the sequences' cached lengths and uploads them.
@@ -522,6 +368,32 @@ int upload_rows(myl_model* m, uint32_t R, const uint32_t* seq, const uint32_t* p
     int rc = ensure_rows(m, (int)R);
     if (!rc) rc = ensure_scores(m, lm);
     if (rc) return rc;
+    // attention tiles: each sequence's rows in position order, at most
+    // kAttnQV / G rows (and kAttnTileRows) per tile
+    const int tr = std::max(1, std::min(kAttnTileRows, kAttnQV / m->G));
+    std::vector<std::pair<uint64_t, uint32_t>> order(R);
+    for (uint32_t r = 0; r < R; ++r) order[r] = {((uint64_t)seq[r] << 32) | pos[r], r};
+    std::sort(order.begin(), order.end());
+    std::vector<AttnTile> tiles;
+    for (uint32_t i = 0; i < R;) {
+        AttnTile t{};
+        t.seq = (int32_t)(order[i].first >> 32);
+        while (i < R && t.n < tr && (int32_t)(order[i].first >> 32) == t.seq) t.row[t.n++] = (int32_t)order[i++].second;
+        tiles.push_back(t);
+    }
+    if ((int)tiles.size() > b->tiles_cap) {
+        (void)hipStreamSynchronize(c->stream);
+        if (b->tiles) (void)hipFree(b->tiles);
+        b->tiles = nullptr;
+        b->tiles_cap = 0;
+        if (hipMalloc(&b->tiles, tiles.size() * sizeof(AttnTile)) != hipSuccess)
+            return c->fail(MYL_E_NOMEM, "batch: tile table allocation");
+        b->tiles_cap = (int)tiles.size();
+    }
+    b->ntiles = (int)tiles.size();
+    rc = c->hip(hipMemcpyAsync(b->tiles, tiles.data(), tiles.size() * sizeof(AttnTile), hipMemcpyHostToDevice,
+                               c->stream), "batch tiles");
+    if (rc) return rc;
     std::vector<int32_t> t(4 * (size_t)b->rows_cap, 0);
     for (uint32_t r = 0; r < R; ++r) {
         t[r] = (int32_t)seq[r];
@@ -548,6 +420,22 @@ int myl_model_batch_begin(myl_model* m, uint32_t n_seqs) {
     if (int nr = m->not_ready()) return nr;
     myl_ctx* c = m->ctx;
     if (m->G > 16) return c->fail(MYL_E_UNSUPPORTED, "batch: at most 16 query heads per KV head");
+    {
+        // The matrix-core P.V splits probabilities into bytes; they stay within
+        // [0, 2^14] when every exp-table entry is non-negative (S >= e_j).
+        std::vector<int16_t> lut(m->exp_len);
+        int rc = c->hip(hipMemcpy(lut.data(), m->exp_lut, lut.size() * 2, hipMemcpyDeviceToHost), "batch: exp table");
+        if (rc) return rc;
+        for (int16_t v : lut)
+            if (v < 0) return c->fail(MYL_E_UNSUPPORTED, "batch: the exp table has negative entries");
+        const std::pair<const void*, size_t> big[4] = {{(const void*)rows_qk_kernel<128>, attn_qk_lds<128>()},
+                                                       {(const void*)rows_qk_kernel<64>, attn_qk_lds<64>()},
+                                                       {(const void*)rows_pv_kernel<128>, attn_pv_lds<128>()},
+                                                       {(const void*)rows_pv_kernel<64>, attn_pv_lds<64>()}};
+        for (const auto& k : big)
+            if (hipFuncSetAttribute(k.first, hipFuncAttributeMaxDynamicSharedMemorySize, (int)k.second) != hipSuccess)
+                return c->fail(MYL_E_HIP, "batch: attention LDS size");
+    }
     if (m->batch && m->batch->n_seqs == (int)n_seqs) {
         std::fill(m->batch->len.begin(), m->batch->len.end(), 0u);
         return MYL_OK;

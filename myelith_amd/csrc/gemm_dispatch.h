@@ -109,6 +109,15 @@ inline hipError_t mm_i8(const int16_t* x, int M, int ldx, const int8_t* W, int N
                         : mm2_launch<2, 2, 4, 2, 3>(mm->planes, M, W, N, K, epi, st);
         }
     }
+    // Few rows (batched decode): the same pipelined product on 64 or 128
+    // plane rows, K split to fill the chip.
+    if (M <= 64 && K % 64 == 0 && mm && mm->planes && mm->acc && (size_t)2 * M * K <= mm->planes_bytes &&
+        mm_env("MYL_MM_TILE") < 0) {
+        hipError_t e = split_planes(x, M, ldx, K, mm->planes, st);
+        if (e != hipSuccess) return e;
+        return M <= 32 ? mm2_launch_splitk<2, 1, 1, 4, 4>(mm->planes, M, W, N, K, epi, mm, st)
+                       : mm2_launch_splitk<2, 1, 2, 4, 4>(mm->planes, M, W, N, K, epi, mm, st);
+    }
     int tile = mm_env("MYL_MM_TILE");
     if (tile < 0 || tile > 3) tile = M <= 512 ? MM_64x64 : MM_64x128;
     const int bm = (tile == MM_128x128 || tile == MM_128x64) ? 128 : 64;

@@ -23,6 +23,9 @@
 #pragma once
 
 #include "gemm_mfma.h"
+#include "internal.h"
+
+#include <algorithm>
 
 namespace myl {
 
@@ -57,14 +60,15 @@ struct Mm2 {
 
 // LDS layout of a stage: BR A' rows then BN weight rows, 64 bytes each; the
 // four 16-byte chunks of row r sit at chunk slot c ^ ((r >> 2) & 3).
+// K runs over [kb, ke) (multiples of 64).
 template <int MB, int NB, int WM_, int WN_, int STAGES, class Sink>
 __device__ inline void mm2_tile(const int8_t* __restrict__ Ap, int R2, const int8_t* __restrict__ W, int N, int K,
-                                int r0, int n0, int8_t* lds, const Sink& sink) {
+                                int kb, int ke, int r0, int n0, int8_t* lds, const Sink& sink) {
     using S = Mm2<MB, NB, WM_, WN_, STAGES>;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave % WM_, wn = wave / WM_;
-    const int nk = K / 64;
+    const int nk = (ke - kb) / 64;
     // Each wave-level load moves 16 rows (64 lanes x 16 bytes): lane l takes
     // row (l >> 2) of the group and the global chunk whose swizzled slot is l & 3.
     auto issue = [&](int kt, int buf) {
@@ -78,10 +82,10 @@ __device__ inline void mm2_tile(const int8_t* __restrict__ Ap, int R2, const int
             const int8_t* src;
             if (row < S::BR) {
                 const int gr = min(r0 + row, R2 - 1);
-                src = Ap + (size_t)gr * K + kt * 64 + chunk * 16;
+                src = Ap + (size_t)gr * K + kb + kt * 64 + chunk * 16;
             } else {
                 const int gn = min(n0 + row - S::BR, N - 1);
-                src = W + (size_t)gn * K + kt * 64 + chunk * 16;
+                src = W + (size_t)gn * K + kb + kt * 64 + chunk * 16;
             }
             __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(st + grp * 1024), 16, 0, 0);
         }
@@ -160,7 +164,28 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_kernel(const int8_t* __res
     if (t < 0) return;
     uint32_t tn, tr;
     tiles_r.divmod((uint32_t)t, tn, tr);
-    mm2_tile<MB, NB, WM_, WN_, STAGES>(Ap, R2, W, N, K, (int)tr * S::BR, (int)tn * S::BN, lds, SinkEpi<Epi>{epi});
+    mm2_tile<MB, NB, WM_, WN_, STAGES>(Ap, R2, W, N, K, 0, K, (int)tr * S::BR, (int)tn * S::BN, lds, SinkEpi<Epi>{epi});
+}
+
+// Split-K form: item t -> (slice t / ntiles, tile t % ntiles); the exact
+// partial sums of each slice are added into acc [M x N] (i64, zero-kept; the
+// finish kernel applies the epilogue and clears it).
+template <int MB, int NB, int WM_, int WN_, int STAGES>
+__global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_splitk_kernel(const int8_t* __restrict__ Ap, int R2,
+                                                                    const int8_t* __restrict__ W, int N, int K,
+                                                                    Divider tiles_r, Divider ntiles, int nitems,
+                                                                    int kslice, unsigned long long* __restrict__ acc) {
+    using S = Mm2<MB, NB, WM_, WN_, STAGES>;
+    extern __shared__ __align__(16) int8_t lds[];
+    const int t = mm_tile_index(nitems);
+    if (t < 0) return;
+    uint32_t ks, tile, tn, tr;
+    ntiles.divmod((uint32_t)t, ks, tile);
+    tiles_r.divmod(tile, tn, tr);
+    const int kb = (int)ks * kslice, ke = min(K, kb + kslice);
+    if (kb >= ke) return;
+    mm2_tile<MB, NB, WM_, WN_, STAGES>(Ap, R2, W, N, K, kb, ke, (int)tr * S::BR, (int)tn * S::BN, lds,
+                                       SinkAtomic{acc, N});
 }
 
 template <int MB, int NB, int WM_, int WN_, int STAGES, class Epi>
@@ -174,6 +199,37 @@ hipError_t mm2_launch(const int8_t* Ap, int M, const int8_t* W, int N, int K, co
         if (e != hipSuccess) return e;
     }
     kern<<<8 * ((ntiles + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, R2, W, N, K, Divider::of((uint32_t)tiles_r), ntiles, epi);
+    return hipGetLastError();
+}
+
+// Few activation rows (2M <= BR): weights stream once, K split across blocks
+// when the tiles alone leave CUs idle (slices of at least 8 stages of 64
+// bytes), partial sums through the i64 accumulator.
+template <int MB, int NB, int WM_, int WN_, int STAGES, class Epi>
+hipError_t mm2_launch_splitk(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, const MmCtx* mm,
+                             hipStream_t st) {
+    using S = Mm2<MB, NB, WM_, WN_, STAGES>;
+    const int R2 = 2 * M;
+    const int tiles_r = (R2 + S::BR - 1) / S::BR, ntiles = tiles_r * ((N + S::BN - 1) / S::BN);
+    const int nkb = K / 64;
+    int ks = 1;
+    if (ntiles < mm->cus && (size_t)M * N <= mm->acc_elems)
+        ks = std::max(1, std::min((2 * mm->cus + ntiles - 1) / ntiles, nkb / 8));
+    if (ks <= 1) return mm2_launch<MB, NB, WM_, WN_, STAGES>(Ap, M, W, N, K, epi, st);
+    const int kslice = ((nkb + ks - 1) / ks) * 64;
+    const int ns = (K + kslice - 1) / kslice, nitems = ntiles * ns;
+    auto kern = mm2_splitk_kernel<MB, NB, WM_, WN_, STAGES>;
+    if (S::kLds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
+        if (e != hipSuccess) return e;
+    }
+    kern<<<8 * ((nitems + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, R2, W, N, K, Divider::of((uint32_t)tiles_r),
+                                                              Divider::of((uint32_t)ntiles), nitems, kslice, mm->acc);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int colb = (N + 255) / 256;
+    const int rows = std::max(1, std::min(M, (mm->cus * 8 + colb - 1) / colb));
+    mm_splitk_finish_kernel<Epi><<<dim3(colb, rows), 256, 0, st>>>(mm->acc, M, N, epi);
     return hipGetLastError();
 }
 

@@ -56,6 +56,10 @@ hipError_t silu_gate(const int16_t* gate, const int16_t* up, int n, const int16_
                      uint8_t gate_frac, uint8_t up_frac, uint8_t down_in_frac, uint8_t silu_in_frac, int16_t silu_off,
                      uint8_t silu_out_frac, int16_t* h, hipStream_t st);
 hipError_t argmax(const int32_t* v, int M, int n, int ldv, int64_t* out, hipStream_t st);
+// The same over long rows with more blocks: per-chunk maxima into part
+// [M][ceil(n / kArgChunk)], then one reduction per row.
+constexpr int kArgChunk = 8192;
+hipError_t argmax_rows(const int32_t* v, int M, int n, int ldv, int64_t* out, uint64_t* part, hipStream_t st);
 // build-defined integer log-softmax at a target per row (Q16)
 hipError_t logsoftmax(const int32_t* z, int M, int n, int ldz, const int16_t* lut, int lut_len, const int64_t* targets,
                       int64_t* out, hipStream_t st);

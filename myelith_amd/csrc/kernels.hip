@@ -350,4 +350,39 @@ hipError_t argmax(const int32_t* v, int M, int n, int ldv, int64_t* out, hipStre
     return hipGetLastError();
 }
 
+// Best key of chunk blockIdx.x of row blockIdx.y.
+__global__ __launch_bounds__(kBlock) void argmax_part_kernel(const int32_t* __restrict__ v, int n, int ldv,
+                                                            uint64_t* __restrict__ part, int nch) {
+    __shared__ uint64_t red[kBlock];
+    const int32_t* row = v + (size_t)blockIdx.y * ldv;
+    const int i0 = blockIdx.x * kArgChunk, i1 = min(n, i0 + kArgChunk);
+    uint64_t best = 0;
+    for (int i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+        const uint64_t key = argmax_key(row[i], (uint32_t)i);
+        best = key > best ? key : best;
+    }
+    red[threadIdx.x] = best;
+    __syncthreads();
+    for (int s = blockDim.x >> 1; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) red[threadIdx.x] = red[threadIdx.x] > red[threadIdx.x + s] ? red[threadIdx.x] : red[threadIdx.x + s];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) part[(size_t)blockIdx.y * nch + blockIdx.x] = red[0];
+}
+
+__global__ __launch_bounds__(64) void argmax_final_kernel(const uint64_t* __restrict__ part, int nch,
+                                                         int64_t* __restrict__ out) {
+    uint64_t best = 0;
+    for (int c = threadIdx.x; c < nch; c += 64) best = max(best, part[(size_t)blockIdx.x * nch + c]);
+    best = wave_max_u64(best);
+    if (threadIdx.x == 0) out[blockIdx.x] = (int64_t)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFu));
+}
+
+hipError_t argmax_rows(const int32_t* v, int M, int n, int ldv, int64_t* out, uint64_t* part, hipStream_t st) {
+    const int nch = (n + kArgChunk - 1) / kArgChunk;
+    argmax_part_kernel<<<dim3(nch, M), kBlock, 0, st>>>(v, n, ldv, part, nch);
+    argmax_final_kernel<<<M, 64, 0, st>>>(part, nch, out);
+    return hipGetLastError();
+}
+
 }  // namespace myl

@@ -444,7 +444,7 @@ int myl_moe_forward(myl_moe* m, const int16_t* x_dev, uint32_t n_tokens, int16_t
     int rc = ensure(m, T);
     if (rc) return rc;
     hipStream_t st = c->stream;
-    const MmCtx* mm = c->mm_ctx((size_t)T * std::max(E, 2 * S), T >= 256 ? (size_t)2 * T * std::max(H, S) : 0);
+    const MmCtx* mm = c->mm_ctx((size_t)T * std::max(E, 2 * S), T >= 2 ? (size_t)2 * T * std::max(H, S) : 0);
     hipError_t e;
     // router logits (Q8, the LM-head requant), then top-k, gates and counts
     EpiLogits el{m->r_shift, (uint8_t)MYL_MOE_X_FRAC, (uint8_t)MYL_MOE_ROUTER_FRAC, m->logits, E};

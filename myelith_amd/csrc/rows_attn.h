@@ -1,0 +1,373 @@
+// rows_attn.h -- integer attention of batched rows on the int8 matrix cores
+// (attention.rs:42-90 with softmax.rs:12-64, one sequence's KV cache per row).
+//
+// Rows of one sequence form a tile; a tile's G query heads per KV head are
+// stacked into at most 128 query vectors (qv = row * G + head), so one block
+// reads each K/V position once for all of them.  Both products run as plain
+// int8 MFMAs on byte planes: an int16 x = 256*hi + lo' + 128 (hi = x >> 8,
+// lo' = (x & 255) - 128), and for two such operands
+//   sum_d a_d b_d = 65536*sum(ah bh) + 256*sum(ah bl' + al' bh) + sum(al' bl')
+//                   + 128*sum_d a_d + 128*sum_d b_d - 16384*D
+// (D terms; exact for any int16 values).  The three plane sums fit int32:
+// |hi|, |lo'| <= 128, so each is at most 2^15 per term, over D <= 256 terms.
+//
+//   rows_qk_kernel   s_j = (i32)RNE(q . k_j * mult, shift) for j <= pos, written
+//                    to scores[row][head][j]                  (attention.rs:66-67)
+//   rows_stats_kernel (batch.hip) max and wrapping exp-LUT sum per (row, head)
+//   rows_pv_kernel   p_j = RNE(e_j 2^14 / S) (or the uniform split when S = 0,
+//                    softmax.rs:42-63), then sum_j p_j v_j exactly as int64 per
+//                    256-position range, written to part[range][row][q dim];
+//                    p in [0, 2^14] (a non-negative exp table) so p >> 8 <= 64.
+//                    The range's P planes and transposed V planes are built in
+//                    LDS in one phase (every load in flight at once), then the
+//                    products run over its 32-position steps
+//   rows_attn_out    sums the ranges, RNE by 14, clamps (attention.rs:84-86),
+//                    then the attn_out rescale (model.rs:563-567)
+// Each kernel's grid is (tiles, KV heads, 256-position ranges); a block whose
+// range starts past every position of its tile returns at once.
+#pragma once
+
+#include "gemm_mfma.h"
+#include "gemv.h"
+#include "ops.h"
+#include "wave.h"
+
+namespace myl {
+
+constexpr int kAttnTileRows = 32;  // rows a tile can list
+constexpr int kAttnQV = 128;       // query vectors per tile (G x rows)
+constexpr int kAttnRange = 256;    // positions per block
+constexpr int kAttnThreads = 512;
+
+struct AttnTile {
+    int32_t seq, n;
+    int32_t row[kAttnTileRows];
+};
+
+// LDS bytes of rows_qk_kernel: Q planes for MT*32 vectors and K planes for
+// `sub` positions, MT*32 + sub <= 192 rows of (HD + 16) bytes, two planes
+// (55 KB at HD 128: two blocks per CU).
+template <int HD>
+constexpr size_t attn_qk_lds() { return (size_t)2 * 192 * (HD + 16); }
+
+// LDS bytes of rows_pv_kernel: P planes for kAttnQV vectors and V planes for
+// HD dimensions, each a row of the range's positions (+16 bytes of padding).
+template <int HD>
+constexpr size_t attn_pv_lds() { return (size_t)2 * (kAttnQV + HD) * (kAttnRange + 16); }
+
+// Sum of the eight int16 values of a 16-byte chunk.
+__device__ inline int32_t sum8_i16(const uint4 x) {
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+    int32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s += (int32_t)(int16_t)(w[i] & 0xFFFFu) + (int32_t)(int16_t)(w[i] >> 16);
+    return s;
+}
+
+// Sum over the CH lanes (CH = 16 or 8, aligned rows of a wave) holding one vector.
+template <int CH>
+__device__ inline int32_t chunk_row_sum(int32_t v) {
+    return CH == 16 ? row_sum16_i32(v) : row_sum8_i32(v);
+}
+
+// Positions per K pass: (query tiles) x (position tiles) stays at 4-8 wave tasks.
+__device__ inline int attn_sub(int MT) { return MT <= 2 ? 128 : 64; }
+
+// Row, head and position of each query vector of the block's tile.
+struct AttnQv {
+    int32_t row[kAttnQV], head[kAttnQV], pos[kAttnQV];
+};
+
+__device__ inline int attn_setup(const AttnTile* __restrict__ tiles, const int32_t* __restrict__ rows, int rows_cap,
+                                 int G, int g, AttnQv& qv, int* s_pmax, int& QV) {
+    const AttnTile* T = tiles + blockIdx.x;
+    const int n = T->n;
+    QV = n * G;
+    const int tid = threadIdx.x;
+    if (tid < QV) {
+        int i = 0, h = tid;  // tid / G and tid % G without a divide (QV <= 128)
+        while (h >= G) {
+            h -= G;
+            ++i;
+        }
+        const int r = T->row[i];
+        qv.row[tid] = r;
+        qv.head[tid] = g * G + h;
+        qv.pos[tid] = rows[rows_cap + r];
+    }
+    if (tid == 0) {
+        int pm = 0;
+        for (int i = 0; i < n; ++i) pm = max(pm, rows[rows_cap + T->row[i]]);
+        *s_pmax = pm;
+    }
+    __syncthreads();
+    return T->seq;
+}
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void rows_qk_kernel(
+    const AttnTile* __restrict__ tiles, const int32_t* __restrict__ rows, int rows_cap, const int16_t* __restrict__ Q,
+    int nq, const int16_t* __restrict__ kc, size_t seq_stride, int max_pos, int G, int64_t mult, uint8_t shift,
+    int32_t* __restrict__ scores, int heads, int lcap) {
+    constexpr int S = HD + 16;  // LDS row stride of a plane
+    extern __shared__ __align__(16) int8_t lds[];
+    __shared__ AttnQv qv;
+    __shared__ int32_t q_sum[kAttnQV];
+    __shared__ int32_t k_sum[256];
+    __shared__ int s_pmax;
+    const int g = blockIdx.y, j0 = blockIdx.z * kAttnRange;
+    int QV;
+    const int seq = attn_setup(tiles, rows, rows_cap, G, g, qv, &s_pmax, QV);
+    const int pmax = s_pmax;
+    if (j0 > pmax) return;
+    const int jend = min(j0 + kAttnRange, pmax + 1);
+    const int MT = (QV + 31) / 32, sub = attn_sub(MT), NT = sub / 32;
+    const int nt_log = sub == 128 ? 2 : 1;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int8_t* qh = lds;
+    int8_t* ql = qh + MT * 32 * S;
+    int8_t* kh = ql + MT * 32 * S;
+    int8_t* kl = kh + sub * S;
+    constexpr int CH = HD / 8;  // 16-byte chunks per vector (a power of two)
+    constexpr int CH_LOG = HD == 128 ? 4 : 3;
+    // Whole CH-lane rows are active together (the loop bounds are multiples
+    // of CH), so the row sums see every chunk of a vector.
+    for (int t = tid; t < MT * 32 * CH; t += kAttnThreads) {
+        const int v = t >> CH_LOG, c = t & (CH - 1);
+        uint4 x = make_uint4(0, 0, 0, 0);
+        if (v < QV) x = *reinterpret_cast<const uint4*>(Q + (size_t)qv.row[v] * nq + (size_t)qv.head[v] * HD + c * 8);
+        uint2 h, l;
+        split_planes8(x, h, l);
+        *reinterpret_cast<uint2*>(qh + v * S + c * 8) = h;
+        *reinterpret_cast<uint2*>(ql + v * S + c * 8) = l;
+        const int32_t sv = chunk_row_sum<CH>(sum8_i16(x));
+        if (c == 0 && v < QV) q_sum[v] = sv;
+    }
+    const int16_t* kg = kc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD;
+    for (int js = j0; js < jend; js += sub) {
+        for (int t = tid; t < sub * CH; t += kAttnThreads) {
+            const int p = t >> CH_LOG, c = t & (CH - 1);
+            const int j = js + p;
+            const uint4 x = j < max_pos ? *reinterpret_cast<const uint4*>(kg + (size_t)j * HD + c * 8) : make_uint4(0, 0, 0, 0);
+            uint2 h, l;
+            split_planes8(x, h, l);
+            *reinterpret_cast<uint2*>(kh + p * S + c * 8) = h;
+            *reinterpret_cast<uint2*>(kl + p * S + c * 8) = l;
+            const int32_t sk = chunk_row_sum<CH>(sum8_i16(x));
+            if (c == 0) k_sum[p] = sk;
+        }
+        __syncthreads();
+        for (int task = wave; task < MT * NT; task += kAttnThreads / 64) {
+            const int mt = task >> nt_log, nt = task & (NT - 1);
+            v16i32_t hh, mid, ll;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) hh[r] = mid[r] = ll[r] = 0;
+            const int ar = mt * 32 + (lane & 31), br = nt * 32 + (lane & 31);
+#pragma unroll
+            for (int ks = 0; ks < HD / 32; ++ks) {
+                const int off = ks * 32 + 16 * (lane >> 5);
+                const v4i32_t ah = *reinterpret_cast<const v4i32_t*>(qh + ar * S + off);
+                const v4i32_t al = *reinterpret_cast<const v4i32_t*>(ql + ar * S + off);
+                const v4i32_t bh = *reinterpret_cast<const v4i32_t*>(kh + br * S + off);
+                const v4i32_t bl = *reinterpret_cast<const v4i32_t*>(kl + br * S + off);
+                hh = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bh, hh, 0, 0, 0);
+                mid = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bl, mid, 0, 0, 0);
+                mid = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bh, mid, 0, 0, 0);
+                ll = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bl, ll, 0, 0, 0);
+            }
+            // lane: position column br; registers r: vectors 8*(r/4) + 4*(lane/32) + r%4
+            const int j = js + br;
+            const int64_t kterm = 128 * (int64_t)k_sum[br] - 16384 * (int64_t)HD;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int v = mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (v < QV && j <= qv.pos[v]) {
+                    const int64_t dot = 65536 * (int64_t)hh[r] + 256 * (int64_t)mid[r] + (int64_t)ll[r] +
+                                        128 * (int64_t)q_sum[v] + kterm;
+                    scores[((size_t)qv.row[v] * heads + qv.head[v]) * lcap + j] =
+                        (int32_t)rshift_round64(wmul64(dot, mult), shift);
+                }
+            }
+        }
+        __syncthreads();  // the next pass overwrites the K planes
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
+    const AttnTile* __restrict__ tiles, const int32_t* __restrict__ rows, int rows_cap,
+    const int32_t* __restrict__ scores, const int32_t* __restrict__ stats, int heads, int lcap,
+    const int16_t* __restrict__ vc, size_t seq_stride, int max_pos, int G, const int16_t* __restrict__ lut,
+    uint32_t lut_len, uint8_t lut_shift, int64_t* __restrict__ part, size_t part_stride, int nq) {
+    constexpr int RS = kAttnRange + 16;  // LDS row stride: the range's positions of one vector / dimension
+    constexpr int NT = HD / 32;
+    constexpr int CH = HD / 8, CH_LOG = HD == 128 ? 4 : 3;
+    extern __shared__ __align__(16) int8_t lds[];
+    int8_t* ph = lds;
+    int8_t* pl = ph + kAttnQV * RS;
+    int8_t* vh = pl + kAttnQV * RS;
+    int8_t* vl = vh + HD * RS;
+    __shared__ AttnQv qv;
+    __shared__ int32_t q_m[kAttnQV], q_s[kAttnQV], q_ub[kAttnQV], q_ur[kAttnQV];
+    __shared__ uint64_t q_rs[kAttnQV];
+    __shared__ int32_t p_sum[kAttnQV], v_sum[HD];
+    __shared__ int s_pmax;
+    const int g = blockIdx.y, range = blockIdx.z, j0 = range * kAttnRange;
+    int QV;
+    const int seq = attn_setup(tiles, rows, rows_cap, G, g, qv, &s_pmax, QV);
+    const int pmax = s_pmax;
+    if (j0 > pmax) return;
+    const int nk = (min(j0 + kAttnRange, pmax + 1) - j0 + 31) / 32;  // 32-position steps
+    const int MT = (QV + 31) / 32;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
+    const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
+    if (tid < kAttnQV) {
+        p_sum[tid] = 0;
+        if (tid < QV) {
+            const size_t si = ((size_t)qv.row[tid] * heads + qv.head[tid]) * 2;
+            const int32_t S = stats[si + 1];
+            q_m[tid] = stats[si];
+            q_s[tid] = S;
+            q_rs[tid] = recip32(S < 0 ? 0u - (uint32_t)S : (uint32_t)S);
+            const uint32_t L = (uint32_t)qv.pos[tid] + 1u;
+            uint32_t qq, rr;
+            udivmod32((uint32_t)one, L, recip32(L), &qq, &rr);
+            q_ub[tid] = (int32_t)qq;
+            q_ur[tid] = wsub32(one, wmul32((int32_t)qq, (int32_t)L));
+        }
+    }
+    if (tid < HD) v_sum[tid] = 0;
+    __syncthreads();
+    // P planes [vector][position]: a wave per vector, its lanes over the
+    // range's 4-position groups (8 * nk <= 64 of them)
+    for (int v = wave; v < MT * 32; v += kAttnThreads / 64) {
+        const int q4 = lane;
+        const int jb = j0 + 4 * q4;
+        uint32_t hw = 0, lw = 0x80808080u;  // p = 0: hi 0, lo' -128
+        int32_t ps = 0;
+        if (q4 < 8 * nk && v < QV && jb <= qv.pos[v]) {
+            const int pos = qv.pos[v];
+            const int4 z = *reinterpret_cast<const int4*>(scores + ((size_t)qv.row[v] * heads + qv.head[v]) * lcap + jb);
+            const int32_t zz[4] = {z.x, z.y, z.z, z.w};
+            lw = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int j = jb + k;
+                int32_t p = 0;
+                if (j <= pos) {
+                    if (q_s[v] == 0) {
+                        p = q_ub[v] + (((uint64_t)j < (uint64_t)(int64_t)q_ur[v]) ? 1 : 0);
+                    } else {
+                        const int32_t e = exp_lookup(sat_sub32(q_m[v], zz[k]), lut, lut_len, lut_shift, lut_one);
+                        p = softmax_div_round(wmul32(e, one), q_s[v], q_rs[v]);
+                    }
+                }
+                ps += p;
+                hw |= ((uint32_t)(p >> 8) & 0xFFu) << (8 * k);
+                lw |= ((uint32_t)((p & 255) - 128) & 0xFFu) << (8 * k);
+            }
+        }
+        if (q4 < 8 * nk) {
+            *reinterpret_cast<uint32_t*>(ph + v * RS + 4 * q4) = hw;
+            *reinterpret_cast<uint32_t*>(pl + v * RS + 4 * q4) = lw;
+        }
+        ps = wave_sum_i32(ps);
+        if (lane == 0) p_sum[v] = ps;
+    }
+    // V planes transposed to [dimension][position]: 8 dimensions x 4 positions per item
+    const int16_t* vg = vc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD;
+    for (int t = tid; t < CH * 8 * nk; t += kAttnThreads) {
+        const int c = t & (CH - 1), q4 = t >> CH_LOG;
+        uint4 w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int j = j0 + 4 * q4 + k;
+            w[k] = j < max_pos ? *reinterpret_cast<const uint4*>(vg + (size_t)j * HD + c * 8) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            uint32_t hw = 0, lw = 0;
+            int32_t vs = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t word = (e >> 1) == 0 ? w[k].x : ((e >> 1) == 1 ? w[k].y : ((e >> 1) == 2 ? w[k].z : w[k].w));
+                const int32_t x = (int16_t)((e & 1) ? (word >> 16) : (word & 0xFFFFu));
+                vs += x;
+                hw |= ((uint32_t)(x >> 8) & 0xFFu) << (8 * k);
+                lw |= ((uint32_t)((x & 255) - 128) & 0xFFu) << (8 * k);
+            }
+            const int d = c * 8 + e;
+            *reinterpret_cast<uint32_t*>(vh + d * RS + 4 * q4) = hw;
+            *reinterpret_cast<uint32_t*>(vl + d * RS + 4 * q4) = lw;
+            atomicAdd(&v_sum[d], vs);
+        }
+    }
+    __syncthreads();
+    // wave tasks: (query tile, dimension tile) pairs, at most two per wave
+    const int ntask = MT * NT;
+    v16i32_t acc[2][3];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 3; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0;
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+        const int task = wave + a * (kAttnThreads / 64);
+        if (task >= ntask) continue;
+        const int mt = task / NT, nt = task - mt * NT;
+        const int8_t* ah_row = ph + (mt * 32 + (lane & 31)) * RS + 16 * (lane >> 5);
+        const int8_t* al_row = pl + (mt * 32 + (lane & 31)) * RS + 16 * (lane >> 5);
+        const int8_t* bh_row = vh + (nt * 32 + (lane & 31)) * RS + 16 * (lane >> 5);
+        const int8_t* bl_row = vl + (nt * 32 + (lane & 31)) * RS + 16 * (lane >> 5);
+        for (int kk = 0; kk < nk; ++kk) {
+            const v4i32_t ah = *reinterpret_cast<const v4i32_t*>(ah_row + 32 * kk);
+            const v4i32_t al = *reinterpret_cast<const v4i32_t*>(al_row + 32 * kk);
+            const v4i32_t bh = *reinterpret_cast<const v4i32_t*>(bh_row + 32 * kk);
+            const v4i32_t bl = *reinterpret_cast<const v4i32_t*>(bl_row + 32 * kk);
+            acc[a][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bh, acc[a][0], 0, 0, 0);
+            acc[a][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bl, acc[a][1], 0, 0, 0);
+            acc[a][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bh, acc[a][1], 0, 0, 0);
+            acc[a][2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bl, acc[a][2], 0, 0, 0);
+        }
+    }
+    const int64_t cterm = 16384 * 32 * (int64_t)nk;
+    int64_t* out = part + (size_t)range * part_stride;
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+        const int task = wave + a * (kAttnThreads / 64);
+        if (task >= ntask) continue;
+        const int mt = task / NT, nt = task - mt * NT;
+        const int d = nt * 32 + (lane & 31);
+        const int64_t dterm = 128 * (int64_t)v_sum[d] - cterm;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int v = mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (v < QV)
+                out[(size_t)qv.row[v] * nq + (size_t)qv.head[v] * HD + d] =
+                    65536 * (int64_t)acc[a][0][r] + 256 * (int64_t)acc[a][1][r] + (int64_t)acc[a][2][r] +
+                    128 * (int64_t)p_sum[v] + dterm;
+        }
+    }
+}
+
+// attention.rs:84-86 then model.rs:563-567: the ranges' exact sums, one
+// rounding, the attn_out rescale.  Grid (ceil(nq / 256), R).
+__global__ __launch_bounds__(256) void rows_attn_out_kernel(const int64_t* __restrict__ part, size_t part_stride,
+                                                            const int32_t* __restrict__ rows, int rows_cap, int nq,
+                                                            uint8_t v_frac, uint8_t out_frac, int16_t* __restrict__ A) {
+    const int r = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= nq) return;
+    const int nr = rows[rows_cap + r] / kAttnRange + 1;
+    int64_t s = 0;
+    for (int c = 0; c < nr; ++c) s = wadd64(s, part[(size_t)c * part_stride + (size_t)r * nq + i]);
+    const int16_t v = clamp_i16_i64(rshift_round64(s, MYL_TV_PROB_FRAC_BITS));
+    A[(size_t)r * nq + i] = clamp_i16(rescale32((int32_t)v, v_frac, out_frac));
+}
+
+}  // namespace myl
