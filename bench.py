@@ -18,6 +18,8 @@ Also reported:
                rotating weight copies (> 512 MB distinct) so the 256 MB
                Infinity Cache cannot serve repeats, M >= 64 runs on the int8
                matrix cores and reports TOP/s;
+  e2e_0.5b     the Qwen2.5-0.5B-shape model end to end at batch 1: 256-token
+               prompt, 128 greedy decode tokens;
   teacher_forced_prefill  4 x 1024 Zipf(1.1) token ids through the batched
                forward on the matrix cores, with the integer log-softmax
                summed per sequence;
@@ -204,6 +206,46 @@ def batched_decode(model, seed: int, batches=(8, 32), ctx: int = 2048, steps: in
     return out
 
 
+def e2e_05b(backend, seed: int, prompt_len: int = 256, n_decode: int = 128):
+    """The Qwen2.5-0.5B-shape model (24 layers, hidden 896, 14/2 heads,
+    head_dim 64, intermediate 4864, vocab 151936, tied int8 LM head) end to
+    end at batch 1: a 256-token seeded prompt through forward_token (the
+    reference's prompt loop, generate.rs:28-32), then 128 greedy decode steps
+    chained on the device.  Bytes per decode token: 357,826,560 of layer
+    weights + 136,134,656 of LM head + 12,288 per cached position of KV."""
+    import numpy as np
+    import torch
+    from myelith_amd.luts import LutSet
+    from myelith_amd.model import QWEN25_05B, IntegerModel, make_spec
+    spec = make_spec(QWEN25_05B, seed=seed + 5, max_pos=prompt_len + n_decode + 8)
+    model = IntegerModel(backend, spec, LutSet.for_head_dim(spec["head_dim"]))
+    rng = np.random.default_rng(seed + 5)
+    prompt = rng.integers(0, spec["vocab"], prompt_len).astype(np.uint32)
+    logits = model.prefill(prompt[:8], 0)  # warm-up (also captures the step graph below)
+    model.decode_greedy(int(np.argmax(logits)), 8, 4)
+    model.reset()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    logits = model.prefill(prompt, 0)
+    ev[1].record()
+    toks, _ = model.decode_greedy(int(np.argmax(logits)), prompt_len, n_decode)
+    ev[2].record()
+    torch.cuda.synchronize()
+    pre_ms, dec_ms = ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2])
+    ctx_avg = prompt_len + n_decode / 2
+    tok_bytes = 357826560 + 136134656 + 12288 * ctx_avg
+    model.close()
+    out = {"prompt_tokens": prompt_len, "decode_tokens": n_decode, "prompt_ms": round(pre_ms, 2),
+           "decode_ms_per_token": round(dec_ms / n_decode, 4), "decode_tok_s": round(n_decode / dec_ms * 1e3, 1),
+           "end_to_end_ms": round(pre_ms + dec_ms, 2), "decode_bytes_per_token": int(tok_bytes),
+           "decode_GBps": round(tok_bytes / (dec_ms / n_decode * 1e-3) / 1e9, 1),
+           "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / tok_bytes, 1)}
+    log(f"0.5B e2e: prompt {prompt_len} in {pre_ms:.1f} ms, decode {dec_ms / n_decode:.3f} ms/token "
+        f"({out['decode_tok_s']} tok/s, {out['decode_GBps']} GB/s)")
+    return out
+
+
 def moe_layer(backend, seed: int, T: int = 4096):
     """The Qwen1.5-MoE-A2.7B-shaped integer MoE layer (60 experts x 1408, top-4,
     shared expert 5632, hidden 2048) on 4096 seeded Gaussian tokens with Zipf(1.0)
@@ -372,6 +414,10 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
+    e2e_small = None
+    if not args.no_batch:
+        e2e_small = e2e_05b(backend, args.seed)
+
     prefill_tf, batch_dec, moe = None, None, None
     if not args.no_batch:
         prefill_tf = teacher_forced_prefill(model, backend, args.seed)
@@ -420,6 +466,7 @@ def main() -> int:
                      "bytes_per_launch": cb[dom], "avg_us": per_class[dom]["avg_us"]},
         "kernel_classes": per_class,
         "w8a16_sweep": gemv,
+        "e2e_0.5b": e2e_small,
         "teacher_forced_prefill": prefill_tf,
         "batched_decode": batch_dec,
         "moe_layer": moe,

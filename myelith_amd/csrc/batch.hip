@@ -49,6 +49,7 @@ struct BatchState {
     int16_t *GU = nullptr, *Hh = nullptr;
     int32_t* logits = nullptr;           // [rows_cap][V]
     int64_t* argmax = nullptr;           // [rows_cap]
+    int32_t* xsum = nullptr;             // [rows_cap] sums of the final-norm rows (int16 head product)
     uint64_t* argmax_part = nullptr;     // [rows_cap][ceil(V / kArgChunk)] best keys per chunk
     int64_t* tokens_out = nullptr;       // greedy chains: [steps][rows]
     size_t tokens_out_cap = 0;
@@ -218,6 +219,7 @@ int ensure_rows(myl_model* m, int R) {
     b->Hh = balloc<int16_t>(L, R * I);
     b->logits = balloc<int32_t>(L, R * V);
     b->argmax = balloc<int64_t>(L, R);
+    b->xsum = balloc<int32_t>(L, R);
     b->argmax_part = balloc<uint64_t>(L, (size_t)R * ((V + kArgChunk - 1) / kArgChunk));
     b->stats = balloc<int32_t>(L, (size_t)R * m->spec.heads * 2);
     for (void* p : L)
@@ -330,7 +332,23 @@ hipError_t forward_rows(myl_model* m, int R, int lmax) {
         return e;
     if (m->spec.lm_head_int16) {
         EpiLogits el{m->lm16_shifts, m->final_norm_frac, MYL_TV_LOGIT_FRAC_BITS, b->logits, V};
-        if ((e = gemv_i16(b->Xn, R, H, m->lm16, V, H, el, st)) != hipSuccess) return e;
+        if (R >= 256 && H % 64 == 0 && mm && mm->planes && (size_t)2 * R * H <= mm->planes_bytes) {
+            // many rows: byte planes of both operands, one int8 product
+            if (!m->lm16_planes_ok) {
+                if (!m->lm16_planes) {
+                    m->lm16_planes = m->dalloc<int8_t>((size_t)2 * V * H);
+                    m->lm16_wsum = m->dalloc<int32_t>(V);
+                    if (!m->lm16_planes || !m->lm16_wsum) return hipErrorOutOfMemory;
+                }
+                if ((e = split_planes_sum(m->lm16, V, H, H, m->lm16_planes, m->lm16_wsum, st)) != hipSuccess) return e;
+                m->lm16_planes_ok = true;
+            }
+            if ((e = split_planes_sum(b->Xn, R, H, H, mm->planes, b->xsum, st)) != hipSuccess) return e;
+            if ((e = mm2w16_launch(mm->planes, b->xsum, R, m->lm16_planes, m->lm16_wsum, V, H, el, st)) != hipSuccess)
+                return e;
+        } else if ((e = gemv_i16(b->Xn, R, H, m->lm16, V, H, el, st)) != hipSuccess) {
+            return e;
+        }
     } else {
         EpiLogits el{m->lm8_shifts, m->final_norm_frac, MYL_TV_LOGIT_FRAC_BITS, b->logits, V};
         if ((e = gemv_i8(b->Xn, R, H, m->lm8, V, H, el, st, mm)) != hipSuccess) return e;

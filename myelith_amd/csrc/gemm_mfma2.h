@@ -24,6 +24,7 @@
 
 #include "gemm_mfma.h"
 #include "internal.h"
+#include "wave.h"
 
 #include <algorithm>
 
@@ -60,10 +61,13 @@ struct Mm2 {
 
 // LDS layout of a stage: BR A' rows then BN weight rows, 64 bytes each; the
 // four 16-byte chunks of row r sit at chunk slot c ^ ((r >> 2) & 3).
-// K runs over [kb, ke) (multiples of 64).
-template <int MB, int NB, int WM_, int WN_, int STAGES, class Sink>
-__device__ inline void mm2_tile(const int8_t* __restrict__ Ap, int R2, const int8_t* __restrict__ W, int N, int K,
-                                int kb, int ke, int r0, int n0, int8_t* lds, const Sink& sink) {
+// The pipelined main loop: acc[i][j] = A' tile i x W tile j over K in
+// [kb, ke) (multiples of 64); rs[j] = the lane's weight-row sum (summed over
+// the lane pair l, l + 32 only after the loop).
+template <int MB, int NB, int WM_, int WN_, int STAGES>
+__device__ inline void mm2_main(const int8_t* __restrict__ Ap, int R2, const int8_t* __restrict__ W, int N, int K,
+                                int kb, int ke, int r0, int n0, int8_t* lds, v16i32_t (&acc)[MB][NB],
+                                int32_t (&rs)[NB]) {
     using S = Mm2<MB, NB, WM_, WN_, STAGES>;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -90,14 +94,12 @@ __device__ inline void mm2_tile(const int8_t* __restrict__ Ap, int R2, const int
             __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(st + grp * 1024), 16, 0, 0);
         }
     };
-    v16i32_t acc[MB][NB];
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
         for (int j = 0; j < NB; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-    int32_t rs[NB];
 #pragma unroll
     for (int j = 0; j < NB; ++j) rs[j] = 0;
 
@@ -136,6 +138,18 @@ __device__ inline void mm2_tile(const int8_t* __restrict__ Ap, int R2, const int
             }
         }
     }
+}
+
+// K runs over [kb, ke) (multiples of 64).
+template <int MB, int NB, int WM_, int WN_, int STAGES, class Sink>
+__device__ inline void mm2_tile(const int8_t* __restrict__ Ap, int R2, const int8_t* __restrict__ W, int N, int K,
+                                int kb, int ke, int r0, int n0, int8_t* lds, const Sink& sink) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave % WM_, wn = wave / WM_;
+    v16i32_t acc[MB][NB];
+    int32_t rs[NB];
+    mm2_main<MB, NB, WM_, WN_, STAGES>(Ap, R2, W, N, K, kb, ke, r0, n0, lds, acc, rs);
 #pragma unroll
     for (int j = 0; j < NB; ++j) rs[j] += __shfl_xor(rs[j], 32);
     // accumulator rows 8*(r/4) + 4*(lane/32) + r%4: registers (r, r+1), r even,
@@ -165,6 +179,106 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_kernel(const int8_t* __res
     uint32_t tn, tr;
     tiles_r.divmod((uint32_t)t, tn, tr);
     mm2_tile<MB, NB, WM_, WN_, STAGES>(Ap, R2, W, N, K, 0, K, (int)tr * S::BR, (int)tn * S::BN, lds, SinkEpi<Epi>{epi});
+}
+
+// int16 weights as byte planes: Wp [2N x K] with row 2n = hi(w_n), row
+// 2n+1 = lo'(w_n), and wsum[n] = sum_k w_n[k]; likewise xsum[m] for the
+// activations.  One int8 product over 2M x 2N plane rows yields the four
+// plane products of each (m, n): in the 32x32 accumulator layout rows 2m and
+// 2m+1 sit in registers r, r+1 of one lane and columns 2n, 2n+1 in lanes
+// l, l^1, so a DPP swap of lane pairs assembles
+//   x.w = 65536*hh + 256*(h lo' + lo' h) + lo' lo' + 128*(xsum + wsum) - 16384*K.
+template <int MB, int NB, int WM_, int WN_, int STAGES, class Sink>
+__device__ inline void mm2w16_tile(const int8_t* __restrict__ Ap, int R2, const int8_t* __restrict__ Wp, int N2,
+                                   int K, const int32_t* __restrict__ xsum, const int32_t* __restrict__ wsum, int r0,
+                                   int n0, int8_t* lds, const Sink& sink) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave % WM_, wn = wave / WM_;
+    v16i32_t acc[MB][NB];
+    int32_t rs[NB];
+    mm2_main<MB, NB, WM_, WN_, STAGES>(Ap, R2, Wp, N2, K, 0, K, r0, n0, lds, acc, rs);
+    const int64_t kterm = 16384 * (int64_t)K;
+    const bool even = (lane & 1) == 0;
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int np = n0 + (wn * NB + j) * 32 + (lane & 31);
+            const int n = np >> 1;
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const int32_t a0 = acc[i][j][r], a1 = acc[i][j][r + 1];
+                const int32_t b0 = dpp_mov<dpp::kXor1>(a0), b1 = dpp_mov<dpp::kXor1>(a1);
+                const int arow = r0 + (wm * MB + i) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const int m = arow >> 1;
+                if (even && arow < R2 && np < N2)
+                    sink(n, m, 65536 * (int64_t)a0 + 256 * ((int64_t)a1 + (int64_t)b0) + (int64_t)b1 +
+                                   128 * ((int64_t)xsum[m] + (int64_t)wsum[n]) - kterm);
+            }
+        }
+}
+
+template <int MB, int NB, int WM_, int WN_, int STAGES, class Epi>
+__global__ __launch_bounds__(WM_ * WN_ * 64) void mm2w16_kernel(const int8_t* __restrict__ Ap, int R2,
+                                                                const int8_t* __restrict__ Wp, int N2, int K,
+                                                                const int32_t* __restrict__ xsum,
+                                                                const int32_t* __restrict__ wsum, Divider tiles_r,
+                                                                int ntiles, Epi epi) {
+    using S = Mm2<MB, NB, WM_, WN_, STAGES>;
+    extern __shared__ __align__(16) int8_t lds[];
+    const int t = mm_tile_index(ntiles);
+    if (t < 0) return;
+    uint32_t tn, tr;
+    tiles_r.divmod((uint32_t)t, tn, tr);
+    mm2w16_tile<MB, NB, WM_, WN_, STAGES>(Ap, R2, Wp, N2, K, xsum, wsum, (int)tr * S::BR, (int)tn * S::BN, lds,
+                                          SinkEpi<Epi>{epi});
+}
+
+// x int16 [M x K] -> planes as split_planes_kernel, plus xsum[m] = sum_k x[m][k].
+// One block per row.
+template <int = 0>
+__global__ __launch_bounds__(256) void split_planes_sum_kernel(const int16_t* __restrict__ x, int ldx, int K,
+                                                               int8_t* __restrict__ Ap, int32_t* __restrict__ xsum) {
+    __shared__ int32_t red[4];
+    const int m = blockIdx.x;
+    int32_t s = 0;
+    for (int c = threadIdx.x; c * 8 < K; c += 256) {
+        const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)m * ldx + c * 8);
+        uint2 h, l;
+        split_planes8(v, h, l);
+        *reinterpret_cast<uint2*>(Ap + (size_t)(2 * m) * K + c * 8) = h;
+        *reinterpret_cast<uint2*>(Ap + (size_t)(2 * m + 1) * K + c * 8) = l;
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) s += (int32_t)(int16_t)(w[q] & 0xFFFFu) + (int32_t)(int16_t)(w[q] >> 16);
+    }
+    s = wave_sum_i32(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) xsum[m] = red[0] + red[1] + red[2] + red[3];
+}
+
+// Plane rows and sums of int16 rows (the weights of mm2w16, or activations).
+inline hipError_t split_planes_sum(const int16_t* x, int M, int ldx, int K, int8_t* Ap, int32_t* xsum, hipStream_t st) {
+    split_planes_sum_kernel<><<<M, 256, 0, st>>>(x, ldx, K, Ap, xsum);
+    return hipGetLastError();
+}
+
+// The int16-weight product for many rows: A' and xsum from split_planes_sum,
+// Wp and wsum prepared once the same way.  Tiles of 256 A' rows x 256 W' rows.
+template <class Epi>
+hipError_t mm2w16_launch(const int8_t* Ap, const int32_t* xsum, int M, const int8_t* Wp, const int32_t* wsum, int N,
+                         int K, const Epi& epi, hipStream_t st) {
+    using S = Mm2<2, 4, 4, 2, 3>;
+    const int R2 = 2 * M, N2 = 2 * N;
+    const int tiles_r = (R2 + S::BR - 1) / S::BR, ntiles = tiles_r * ((N2 + S::BN - 1) / S::BN);
+    auto kern = mm2w16_kernel<2, 4, 4, 2, 3, Epi>;
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
+    if (e != hipSuccess) return e;
+    kern<<<8 * ((ntiles + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, R2, Wp, N2, K, xsum, wsum,
+                                                              Divider::of((uint32_t)tiles_r), ntiles, epi);
+    return hipGetLastError();
 }
 
 // Split-K form: item t -> (slice t / ntiles, tile t % ntiles); the exact

@@ -68,6 +68,11 @@ struct myl_model {
     uint8_t* emb_shifts = nullptr;
     int16_t* lm16 = nullptr;
     uint8_t* lm16_shifts = nullptr;
+    // byte planes of lm16 [2V x H] and its row sums, for the many-row head
+    // product; built on first use, invalidated by an upload of the head
+    int8_t* lm16_planes = nullptr;
+    int32_t* lm16_wsum = nullptr;
+    bool lm16_planes_ok = false;
     int8_t* final_gamma = nullptr;
     uint8_t* final_gamma_s = nullptr;
     uint8_t* final_res = nullptr;

@@ -243,6 +243,7 @@ int put_tensor(myl_model* m, Staging& st, const Target& t, Reader& rd, const uin
         if (int rc = st.release()) return rc;
     }
     m->have[t.slot] = 1;
+    if (t.slot == myl::SLOT_LM16) m->lm16_planes_ok = false;
     return MYL_OK;
 }
 

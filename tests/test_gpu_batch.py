@@ -75,6 +75,30 @@ def test_batch_rows_interleaved(backend, hd, lm16, bias, kvh):
         gm.forward_batch([3], [0], [1])  # no such sequence
 
 
+@pytest.mark.parametrize("hd,lm16", [(128, 1), (64, 0)])
+def test_batch_many_rows(backend, hd, lm16):
+    """340 rows in one batch (the large-M products, byte-plane int16 head):
+    a 300-position sequence (two 256-position attention ranges, tiles of many
+    rows) and a 40-position one, rows shuffled; every row's logits, the argmax
+    and both KV caches equal the oracle's."""
+    spec = tiny(hd, lm16, 1, 2)
+    case(f"batch many rows {spec}")
+    gm, om = build(backend, spec)
+    r = np.random.default_rng(hd + 3 * lm16)
+    lens = [300, 40]
+    toks = [r.integers(0, spec["vocab"], n) for n in lens]
+    rows = [(s, p) for s, n in enumerate(lens) for p in range(n)]
+    rows = [rows[i] for i in r.permutation(len(rows))]
+    gm.batch_begin(2)
+    logits, am = gm.forward_batch([s for s, _ in rows], [p for _, p in rows], [int(toks[s][p]) for s, p in rows])
+    ref = oracle_rows(om, toks)
+    for i, (s, p) in enumerate(rows):
+        assert np.array_equal(logits[i], ref[s][p]), ("row", s, p)
+        assert am[i] == int(np.argmax(ref[s][p]))
+    compare_batch_kv(gm, om, spec, 0, toks[0])
+    compare_batch_kv(gm, om, spec, 1, toks[1])
+
+
 def test_batch_decode_greedy_lock_step(backend):
     """Four sequences prefilled to different lengths, then 12 lock-step greedy
     steps on the device: each sequence's tokens equal its own greedy run."""
