@@ -169,6 +169,24 @@ __global__ __launch_bounds__(256) void silu_rows_kernel(const int16_t* __restric
     Hh[(size_t)r * I + i] = clamp_i16_i64(rescale64(prod, (uint8_t)(MYL_TV_SILU_OUT_FRAC + up_frac), down_in_frac));
 }
 
+// silu_rows_kernel writing byte planes [2R x I] of h for the down product.
+__global__ __launch_bounds__(256) void silu_planes_kernel(const int16_t* __restrict__ GU, int I,
+                                                          const int16_t* __restrict__ silu, uint32_t silu_len,
+                                                          uint8_t gate_frac, uint8_t up_frac, uint8_t down_in_frac,
+                                                          int8_t* __restrict__ planes) {
+    const int r = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= I) return;
+    const uint32_t gu = *reinterpret_cast<const uint32_t*>(GU + (size_t)r * 2 * I + 2 * i);
+    const int16_t g = (int16_t)(gu & 0xFFFFu), u = (int16_t)(gu >> 16);
+    const int32_t g_dom = rescale32((int32_t)g, gate_frac, MYL_TV_SILU_IN_FRAC);
+    const int16_t act = lut_lookup_i16((int16_t)g_dom, silu, silu_len, (int16_t)MYL_TV_SILU_LUT_OFFSET);
+    const int64_t prod = (int64_t)act * (int64_t)u;
+    const int32_t h = clamp_i16_i64(rescale64(prod, (uint8_t)(MYL_TV_SILU_OUT_FRAC + up_frac), down_in_frac));
+    planes[(size_t)(2 * r) * I + i] = (int8_t)(h >> 8);
+    planes[(size_t)(2 * r + 1) * I + i] = (int8_t)((h & 255) - 128);
+}
+
 // Greedy continuation: row r's next token is its argmax; positions advance.
 __global__ void rows_advance_kernel(int32_t* __restrict__ rows, int rows_cap, int R, const int64_t* __restrict__ am,
                                     uint32_t rope_rows, int64_t* __restrict__ tokens_out) {
@@ -256,6 +274,10 @@ hipError_t forward_rows(myl_model* m, int R, int lmax) {
     const MmCtx* mm = c->mm_ctx((size_t)R * std::max(2 * I, nqkv), R >= 2 ? (size_t)2 * R * std::max(I, H) : 0);
     const size_t sstride = seq_stride(m);
     const int ranges = (lmax + kAttnRange - 1) / kAttnRange;
+    // producers write the products' byte planes directly when every product
+    // of the layer runs on planes
+    const bool planes = mm_planes_ok(R, H, mm) && mm_planes_ok(R, I, mm) && mm_planes_ok(R, nq, mm) &&
+                        rmsnorm_planes_ok(H) && xvec_ok(b->X, H);
     const uint8_t lut_shift = MYL_TV_SCORE_FRAC_BITS - MYL_TV_EXP_INPUT_FRAC;
     hipError_t e;
     embed_rows_kernel<<<R, 256, 0, st>>>(b->rows + 3 * b->rows_cap, m->emb, m->emb_shifts, m->layers[0].res_in, H, b->X);
@@ -263,15 +285,23 @@ hipError_t forward_rows(myl_model* m, int R, int lmax) {
     for (int l = 0; l < (int)m->spec.layers; ++l) {
         const LayerDev& Ld = m->layers[l];
         const myl_layer_fracs& f = Ld.f;
-        if ((e = rmsnorm(b->X, R, H, Ld.res_in, Ld.in_gamma, Ld.in_gamma_s, H, m->rsqrt, m->rsqrt_len,
-                         MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, f.norm_attn_frac, b->Xn, H,
-                         st)) != hipSuccess)
-            return e;
         EpiQKVRows eq{};
         eq.shifts = Ld.sqkv; eq.bias = Ld.bqkv; eq.bias_sh = Ld.bsqkv;
         eq.act_frac = f.norm_attn_frac; eq.q_frac = f.q_frac; eq.k_frac = f.k_frac; eq.v_frac = f.v_frac;
         eq.nq = nq; eq.nkv = nkv; eq.out = b->QKV; eq.ldo = nqkv;
-        if ((e = gemv_i8(b->Xn, R, H, Ld.wqkv, nqkv, H, eq, st, mm)) != hipSuccess) return e;
+        if (planes) {
+            if ((e = rmsnorm_planes(b->X, R, H, Ld.res_in, Ld.in_gamma, Ld.in_gamma_s, H, m->rsqrt, m->rsqrt_len,
+                                    MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, f.norm_attn_frac,
+                                    mm->planes, st)) != hipSuccess ||
+                (e = mm_planes(mm->planes, R, Ld.wqkv, nqkv, H, eq, mm, st)) != hipSuccess)
+                return e;
+        } else {
+            if ((e = rmsnorm(b->X, R, H, Ld.res_in, Ld.in_gamma, Ld.in_gamma_s, H, m->rsqrt, m->rsqrt_len,
+                             MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, f.norm_attn_frac, b->Xn,
+                             H, st)) != hipSuccess ||
+                (e = gemv_i8(b->Xn, R, H, Ld.wqkv, nqkv, H, eq, st, mm)) != hipSuccess)
+                return e;
+        }
         int16_t* kc = b->kc + (size_t)l * kvh * m->max_pos * hd;
         int16_t* vc = b->vc + (size_t)l * kvh * m->max_pos * hd;
         rope_scatter_kernel<<<dim3((nqkv / 2 + 255) / 256, R), 256, 0, st>>>(
@@ -304,27 +334,41 @@ hipError_t forward_rows(myl_model* m, int R, int lmax) {
                                                             (uint32_t)m->exp_len, lut_shift, b->part, pst, nq);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         rows_attn_out_kernel<<<dim3((nq + 255) / 256, R), 256, 0, st>>>(b->part, pst, b->rows, b->rows_cap, nq, f.v_frac,
-                                                                        f.attn_out_frac, b->A);
+                                                                        f.attn_out_frac, b->A,
+                                                                        planes ? mm->planes : nullptr);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         EpiResidRows eo{};
         eo.shifts = Ld.so; eo.act_frac = f.attn_out_frac; eo.acc_frac = Ld.acc_attn; eo.res_frac = Ld.res_in;
         eo.out_frac = Ld.res_mid; eo.res = b->X; eo.ldr = H; eo.out = b->X2; eo.ldo = H;
-        if ((e = gemv_i8(b->A, R, nq, Ld.wo, H, nq, eo, st, mm)) != hipSuccess) return e;
-        if ((e = rmsnorm(b->X2, R, H, Ld.res_mid, Ld.post_gamma, Ld.post_gamma_s, H, m->rsqrt, m->rsqrt_len,
-                         MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, f.norm_mlp_frac, b->Xn, H,
-                         st)) != hipSuccess)
-            return e;
+        e = planes ? mm_planes(mm->planes, R, Ld.wo, H, nq, eo, mm, st) : gemv_i8(b->A, R, nq, Ld.wo, H, nq, eo, st, mm);
+        if (e != hipSuccess) return e;
         EpiGURows eg{};
         eg.shifts = Ld.sgu; eg.act_frac = f.norm_mlp_frac; eg.gate_frac = f.gate_frac; eg.up_frac = f.up_frac;
         eg.out = b->GU; eg.ldo = 2 * I;
-        if ((e = gemv_i8(b->Xn, R, H, Ld.wgu, 2 * I, H, eg, st, mm)) != hipSuccess) return e;
-        silu_rows_kernel<<<dim3((I + 255) / 256, R), 256, 0, st>>>(b->GU, I, m->silu, (uint32_t)m->silu_len,
-                                                                   f.gate_frac, f.up_frac, f.down_in_frac, b->Hh);
+        if (planes) {
+            if ((e = rmsnorm_planes(b->X2, R, H, Ld.res_mid, Ld.post_gamma, Ld.post_gamma_s, H, m->rsqrt,
+                                    m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20,
+                                    f.norm_mlp_frac, mm->planes, st)) != hipSuccess ||
+                (e = mm_planes(mm->planes, R, Ld.wgu, 2 * I, H, eg, mm, st)) != hipSuccess)
+                return e;
+            silu_planes_kernel<<<dim3((I + 255) / 256, R), 256, 0, st>>>(b->GU, I, m->silu, (uint32_t)m->silu_len,
+                                                                         f.gate_frac, f.up_frac, f.down_in_frac,
+                                                                         mm->planes);
+        } else {
+            if ((e = rmsnorm(b->X2, R, H, Ld.res_mid, Ld.post_gamma, Ld.post_gamma_s, H, m->rsqrt, m->rsqrt_len,
+                             MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, f.norm_mlp_frac, b->Xn,
+                             H, st)) != hipSuccess ||
+                (e = gemv_i8(b->Xn, R, H, Ld.wgu, 2 * I, H, eg, st, mm)) != hipSuccess)
+                return e;
+            silu_rows_kernel<<<dim3((I + 255) / 256, R), 256, 0, st>>>(b->GU, I, m->silu, (uint32_t)m->silu_len,
+                                                                       f.gate_frac, f.up_frac, f.down_in_frac, b->Hh);
+        }
         if ((e = hipGetLastError()) != hipSuccess) return e;
         EpiResidRows ed{};
         ed.shifts = Ld.sd; ed.act_frac = f.down_in_frac; ed.acc_frac = Ld.acc_mlp; ed.res_frac = Ld.res_mid;
         ed.out_frac = Ld.res_out; ed.res = b->X2; ed.ldr = H; ed.out = b->X; ed.ldo = H;
-        if ((e = gemv_i8(b->Hh, R, I, Ld.wd, H, I, ed, st, mm)) != hipSuccess) return e;
+        e = planes ? mm_planes(mm->planes, R, Ld.wd, H, I, ed, mm, st) : gemv_i8(b->Hh, R, I, Ld.wd, H, I, ed, st, mm);
+        if (e != hipSuccess) return e;
     }
     if ((e = rmsnorm(b->X, R, H, m->final_res, m->final_gamma, m->final_gamma_s, H, m->rsqrt, m->rsqrt_len,
                      MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, m->final_norm_frac, b->Xn, H,

@@ -88,6 +88,29 @@ inline hipError_t mm_launch(const int16_t* x, int M, int ldx, const int8_t* W, i
     return hipGetLastError();
 }
 
+// Whether the W8A16 product of M rows over K runs on byte planes (and a
+// producer may write them directly): every M >= 2 with K a multiple of 64
+// and room in the context's plane buffer.
+inline bool mm_planes_ok(int M, int K, const MmCtx* mm) {
+    return M >= 2 && K % 64 == 0 && mm && mm->planes && mm->acc && (size_t)2 * M * K <= mm->planes_bytes &&
+           mm_env("MYL_MM_TILE") < 0;
+}
+
+// The product on planes Ap [2M x K] (mm_planes_ok): few rows stream the
+// weights once in 64 or 128 plane-row tiles (K split until the chip is
+// full, or half full past 32 rows); more rows take 256 x 128 block tiles,
+// 256 x 256 past 1024 rows, when those give every CU a tile.
+template <class Epi>
+inline hipError_t mm_planes(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, const MmCtx* mm,
+                            hipStream_t st) {
+    const int cus = mm->cus;
+    // few rows: partial sums cost little, so K is split until every CU has work
+    if (M <= 32) return mm2_launch_splitk<2, 1, 1, 4, 4>(Ap, M, W, N, K, epi, mm, cus, st);
+    if (M > 1024 && mm2_tiles<2, 4, 4, 2, 3>(M, N) >= cus) return mm2_launch<2, 4, 4, 2, 3>(Ap, M, W, N, K, epi, st);
+    if (M > 64 && mm2_tiles<2, 2, 4, 2, 3>(M, N) >= cus) return mm2_launch<2, 2, 4, 2, 3>(Ap, M, W, N, K, epi, st);
+    return mm2_launch_splitk<2, 1, 2, 4, 4>(Ap, M, W, N, K, epi, mm, cus / 2, st);
+}
+
 // Tile and K split, from a sweep of the W8A16 shapes on MI355X: 64-row tiles
 // (two waves per SIMD) beat 128-row tiles at every M; 64 x 128 wins once M
 // is large.  K is split (slices of >= 1024 bytes) only when the tiles alone
@@ -96,27 +119,12 @@ template <class Epi>
 inline hipError_t mm_i8(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, const Epi& epi,
                         const MmCtx* mm, hipStream_t st) {
     const int cus = mm ? mm->cus : 256;
-    // Large M: split the activations into byte planes once and run the
-    // pipelined int8 product (gemm_mfma2.h) when its tiles fill the chip.
-    if (M >= 256 && K % 64 == 0 && mm && mm->planes && (size_t)2 * M * K <= mm->planes_bytes &&
-        mm_env("MYL_MM_TILE") < 0) {
-        const bool wide = M > 1024;
-        const int tiles = wide ? mm2_tiles<2, 4, 4, 2, 3>(M, N) : mm2_tiles<2, 2, 4, 2, 3>(M, N);
-        if (tiles >= cus) {
-            hipError_t e = split_planes(x, M, ldx, K, mm->planes, st);
-            if (e != hipSuccess) return e;
-            return wide ? mm2_launch<2, 4, 4, 2, 3>(mm->planes, M, W, N, K, epi, st)
-                        : mm2_launch<2, 2, 4, 2, 3>(mm->planes, M, W, N, K, epi, st);
-        }
-    }
-    // Few rows (batched decode): the same pipelined product on 64 or 128
-    // plane rows, K split to fill the chip.
-    if (M <= 64 && K % 64 == 0 && mm && mm->planes && mm->acc && (size_t)2 * M * K <= mm->planes_bytes &&
-        mm_env("MYL_MM_TILE") < 0) {
+    // The activations split once into byte planes, then the pipelined int8
+    // product (gemm_mfma2.h).
+    if (mm_planes_ok(M, K, mm)) {
         hipError_t e = split_planes(x, M, ldx, K, mm->planes, st);
         if (e != hipSuccess) return e;
-        return M <= 32 ? mm2_launch_splitk<2, 1, 1, 4, 4>(mm->planes, M, W, N, K, epi, mm, st)
-                       : mm2_launch_splitk<2, 1, 2, 4, 4>(mm->planes, M, W, N, K, epi, mm, st);
+        return mm_planes(mm->planes, M, W, N, K, epi, mm, st);
     }
     int tile = mm_env("MYL_MM_TILE");
     if (tile < 0 || tile > 3) tile = M <= 512 ? MM_64x64 : MM_64x128;

@@ -316,18 +316,18 @@ hipError_t mm2_launch(const int8_t* Ap, int M, const int8_t* W, int N, int K, co
     return hipGetLastError();
 }
 
-// Few activation rows (2M <= BR): weights stream once, K split across blocks
-// when the tiles alone leave CUs idle (slices of at least 8 stages of 64
-// bytes), partial sums through the i64 accumulator.
+// Weights stream once per row tile; K split across blocks when there are
+// fewer tiles than `fill` (slices of at least 8 stages of 64 bytes), partial
+// sums through the i64 accumulator.
 template <int MB, int NB, int WM_, int WN_, int STAGES, class Epi>
 hipError_t mm2_launch_splitk(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, const MmCtx* mm,
-                             hipStream_t st) {
+                             int fill, hipStream_t st) {
     using S = Mm2<MB, NB, WM_, WN_, STAGES>;
     const int R2 = 2 * M;
     const int tiles_r = (R2 + S::BR - 1) / S::BR, ntiles = tiles_r * ((N + S::BN - 1) / S::BN);
     const int nkb = K / 64;
     int ks = 1;
-    if (ntiles < mm->cus && (size_t)M * N <= mm->acc_elems)
+    if (ntiles < fill && (size_t)M * N <= mm->acc_elems)
         ks = std::max(1, std::min((2 * mm->cus + ntiles - 1) / ntiles, nkb / 8));
     if (ks <= 1) return mm2_launch<MB, NB, WM_, WN_, STAGES>(Ap, M, W, N, K, epi, st);
     const int kslice = ((nkb + ks - 1) / ks) * 64;

@@ -56,6 +56,12 @@ hipError_t silu_gate(const int16_t* gate, const int16_t* up, int n, const int16_
                      uint8_t gate_frac, uint8_t up_frac, uint8_t down_in_frac, uint8_t silu_in_frac, int16_t silu_off,
                      uint8_t silu_out_frac, int16_t* h, hipStream_t st);
 hipError_t argmax(const int32_t* v, int M, int n, int ldv, int64_t* out, hipStream_t st);
+// RMSNorm rows written as byte planes [2M x n] (hi row 2m, lo' row 2m + 1) for
+// the int8 products; rows of up to rmsnorm_planes_ok(n) elements.
+bool rmsnorm_planes_ok(int n);
+hipError_t rmsnorm_planes(const int16_t* x, int M, int ldx, const uint8_t* xs, const int8_t* g, const uint8_t* gs,
+                          int n, const int16_t* lut, int lut_len, uint8_t lut_input_shift, uint8_t lut_output_frac,
+                          int64_t inv_n_q20, uint8_t out_frac, int8_t* planes, hipStream_t st);
 // The same over long rows with more blocks: per-chunk maxima into part
 // [M][ceil(n / kArgChunk)], then one reduction per row.
 constexpr int kArgChunk = 8192;

@@ -63,7 +63,8 @@ __global__ __launch_bounds__(kRmsThreads) void rmsnorm_fast_kernel(const int16_t
                                                                   const uint8_t* __restrict__ xs,
                                                                   const int8_t* __restrict__ g,
                                                                   const uint8_t* __restrict__ gs, int n, RmsParams p,
-                                                                  uint8_t out_frac, int16_t* __restrict__ out, int ldo) {
+                                                                  uint8_t out_frac, int16_t* __restrict__ out, int ldo,
+                                                                  int8_t* __restrict__ planes) {
     __shared__ myl_i128 red128[kRmsThreads / 64];
     __shared__ int32_t red32[kRmsThreads / 64];
     const int16_t* xr = x + (size_t)blockIdx.x * ldx;
@@ -81,6 +82,20 @@ __global__ __launch_bounds__(kRmsThreads) void rmsnorm_fast_kernel(const int16_t
         gsv[t] = ok ? gs[i] : (uint8_t)0;
     }
     const RmsFactor f = rms_factor_regs<kRmsPer>(xv, sv, p, red128, red32);
+    if (planes) {
+        // byte planes of the output row: hi at row 2m, lo' at row 2m + 1
+        int8_t* ph = planes + (size_t)(2 * blockIdx.x) * n;
+#pragma unroll
+        for (int t = 0; t < kRmsPer; ++t) {
+            const int i = threadIdx.x + t * kRmsThreads;
+            if (i < n) {
+                const int32_t y = rms_out(xv[t], sv[t], gv[t], gsv[t], f, out_frac);
+                ph[i] = (int8_t)(y >> 8);
+                ph[n + i] = (int8_t)((y & 255) - 128);
+            }
+        }
+        return;
+    }
     int16_t* o = out + (size_t)blockIdx.x * ldo;
 #pragma unroll
     for (int t = 0; t < kRmsPer; ++t) {
@@ -94,9 +109,20 @@ hipError_t rmsnorm(const int16_t* x, int M, int ldx, const uint8_t* xs, const in
                    int64_t inv_n_q20, uint8_t out_frac, int16_t* out, int ldo, hipStream_t st) {
     RmsParams p{lut, lut_len, lut_input_shift, lut_output_frac, inv_n_q20};
     if (n <= kRmsThreads * kRmsPer)
-        rmsnorm_fast_kernel<<<M, kRmsThreads, 0, st>>>(x, ldx, xs, g, gs, n, p, out_frac, out, ldo);
+        rmsnorm_fast_kernel<<<M, kRmsThreads, 0, st>>>(x, ldx, xs, g, gs, n, p, out_frac, out, ldo, nullptr);
     else
         rmsnorm_kernel<<<M, kBlock, 0, st>>>(x, ldx, xs, g, gs, n, p, out_frac, out, ldo);
+    return hipGetLastError();
+}
+
+bool rmsnorm_planes_ok(int n) { return n <= kRmsThreads * kRmsPer; }
+
+hipError_t rmsnorm_planes(const int16_t* x, int M, int ldx, const uint8_t* xs, const int8_t* g, const uint8_t* gs,
+                          int n, const int16_t* lut, int lut_len, uint8_t lut_input_shift, uint8_t lut_output_frac,
+                          int64_t inv_n_q20, uint8_t out_frac, int8_t* planes, hipStream_t st) {
+    if (!rmsnorm_planes_ok(n)) return hipErrorInvalidValue;
+    RmsParams p{lut, lut_len, lut_input_shift, lut_output_frac, inv_n_q20};
+    rmsnorm_fast_kernel<<<M, kRmsThreads, 0, st>>>(x, ldx, xs, g, gs, n, p, out_frac, nullptr, 0, planes);
     return hipGetLastError();
 }
 

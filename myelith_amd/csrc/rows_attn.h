@@ -300,8 +300,11 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
                 lw |= ((uint32_t)((x & 255) - 128) & 0xFFu) << (8 * k);
             }
             const int d = c * 8 + e;
-            *reinterpret_cast<uint32_t*>(vh + d * RS + 4 * q4) = hw;
-            *reinterpret_cast<uint32_t*>(vl + d * RS + 4 * q4) = lw;
+            // 16-byte position chunk (q4 >> 2) at slot chunk ^ (d >> 3): rows
+            // eight apart no longer share banks
+            const int off = (((q4 >> 2) ^ (c & 15)) << 4) + 4 * (q4 & 3);
+            *reinterpret_cast<uint32_t*>(vh + d * RS + off) = hw;
+            *reinterpret_cast<uint32_t*>(vl + d * RS + off) = lw;
             atomicAdd(&v_sum[d], vs);
         }
     }
@@ -322,13 +325,16 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
         const int mt = task / NT, nt = task - mt * NT;
         const int8_t* ah_row = ph + (mt * 32 + (lane & 31)) * RS + 16 * (lane >> 5);
         const int8_t* al_row = pl + (mt * 32 + (lane & 31)) * RS + 16 * (lane >> 5);
-        const int8_t* bh_row = vh + (nt * 32 + (lane & 31)) * RS + 16 * (lane >> 5);
-        const int8_t* bl_row = vl + (nt * 32 + (lane & 31)) * RS + 16 * (lane >> 5);
+        const int dr = nt * 32 + (lane & 31);
+        const int8_t* bh_row = vh + dr * RS;
+        const int8_t* bl_row = vl + dr * RS;
+        const int sw = (dr >> 3) & 15;
         for (int kk = 0; kk < nk; ++kk) {
+            const int slot = ((2 * kk + (lane >> 5)) ^ sw) << 4;
             const v4i32_t ah = *reinterpret_cast<const v4i32_t*>(ah_row + 32 * kk);
             const v4i32_t al = *reinterpret_cast<const v4i32_t*>(al_row + 32 * kk);
-            const v4i32_t bh = *reinterpret_cast<const v4i32_t*>(bh_row + 32 * kk);
-            const v4i32_t bl = *reinterpret_cast<const v4i32_t*>(bl_row + 32 * kk);
+            const v4i32_t bh = *reinterpret_cast<const v4i32_t*>(bh_row + slot);
+            const v4i32_t bl = *reinterpret_cast<const v4i32_t*>(bl_row + slot);
             acc[a][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bh, acc[a][0], 0, 0, 0);
             acc[a][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bl, acc[a][1], 0, 0, 0);
             acc[a][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bh, acc[a][1], 0, 0, 0);
@@ -356,10 +362,12 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
 }
 
 // attention.rs:84-86 then model.rs:563-567: the ranges' exact sums, one
-// rounding, the attn_out rescale.  Grid (ceil(nq / 256), R).
+// rounding, the attn_out rescale; into A, or as byte planes when planes is
+// given.  Grid (ceil(nq / 256), R).
 __global__ __launch_bounds__(256) void rows_attn_out_kernel(const int64_t* __restrict__ part, size_t part_stride,
                                                             const int32_t* __restrict__ rows, int rows_cap, int nq,
-                                                            uint8_t v_frac, uint8_t out_frac, int16_t* __restrict__ A) {
+                                                            uint8_t v_frac, uint8_t out_frac, int16_t* __restrict__ A,
+                                                            int8_t* __restrict__ planes) {
     const int r = blockIdx.y;
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= nq) return;
@@ -367,7 +375,13 @@ __global__ __launch_bounds__(256) void rows_attn_out_kernel(const int64_t* __res
     int64_t s = 0;
     for (int c = 0; c < nr; ++c) s = wadd64(s, part[(size_t)c * part_stride + (size_t)r * nq + i]);
     const int16_t v = clamp_i16_i64(rshift_round64(s, MYL_TV_PROB_FRAC_BITS));
-    A[(size_t)r * nq + i] = clamp_i16(rescale32((int32_t)v, v_frac, out_frac));
+    const int16_t a = clamp_i16(rescale32((int32_t)v, v_frac, out_frac));
+    if (planes) {  // byte planes [2R x nq] for the o_proj product
+        planes[(size_t)(2 * r) * nq + i] = (int8_t)(a >> 8);
+        planes[(size_t)(2 * r + 1) * nq + i] = (int8_t)((a & 255) - 128);
+    } else {
+        A[(size_t)r * nq + i] = a;
+    }
 }
 
 }  // namespace myl
