@@ -98,15 +98,16 @@ inline bool mm_planes_ok(int M, int K, const MmCtx* mm) {
 
 // The product on planes Ap [2M x K] (mm_planes_ok): few rows stream the
 // weights once in 64 or 128 plane-row tiles (K split until the chip is
-// full, or half full past 32 rows); more rows take 256 x 128 block tiles,
-// 256 x 256 past 1024 rows, when those give every CU a tile.
+// full, or half full past 32 rows); more rows take 256 x 128 block tiles
+// (72 KB of LDS: two blocks per CU, which measured faster than 256 x 256
+// tiles at one block per CU for every shape from 512 to 4096 rows) when
+// those give every CU a tile.
 template <class Epi>
 inline hipError_t mm_planes(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, const MmCtx* mm,
                             hipStream_t st) {
     const int cus = mm->cus;
     // few rows: partial sums cost little, so K is split until every CU has work
     if (M <= 32) return mm2_launch_splitk<2, 1, 1, 4, 4>(Ap, M, W, N, K, epi, mm, cus, st);
-    if (M > 1024 && mm2_tiles<2, 4, 4, 2, 3>(M, N) >= cus) return mm2_launch<2, 4, 4, 2, 3>(Ap, M, W, N, K, epi, st);
     if (M > 64 && mm2_tiles<2, 2, 4, 2, 3>(M, N) >= cus) return mm2_launch<2, 2, 4, 2, 3>(Ap, M, W, N, K, epi, st);
     return mm2_launch_splitk<2, 1, 2, 4, 4>(Ap, M, W, N, K, epi, mm, cus / 2, st);
 }

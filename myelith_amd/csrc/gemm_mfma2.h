@@ -266,14 +266,14 @@ inline hipError_t split_planes_sum(const int16_t* x, int M, int ldx, int K, int8
 }
 
 // The int16-weight product for many rows: A' and xsum from split_planes_sum,
-// Wp and wsum prepared once the same way.  Tiles of 256 A' rows x 256 W' rows.
+// Wp and wsum prepared once the same way.  Tiles of 256 A' rows x 128 W' rows.
 template <class Epi>
 hipError_t mm2w16_launch(const int8_t* Ap, const int32_t* xsum, int M, const int8_t* Wp, const int32_t* wsum, int N,
                          int K, const Epi& epi, hipStream_t st) {
-    using S = Mm2<2, 4, 4, 2, 3>;
+    using S = Mm2<2, 2, 4, 2, 3>;
     const int R2 = 2 * M, N2 = 2 * N;
     const int tiles_r = (R2 + S::BR - 1) / S::BR, ntiles = tiles_r * ((N2 + S::BN - 1) / S::BN);
-    auto kern = mm2w16_kernel<2, 4, 4, 2, 3, Epi>;
+    auto kern = mm2w16_kernel<2, 2, 4, 2, 3, Epi>;
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
     if (e != hipSuccess) return e;
     kern<<<8 * ((ntiles + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, R2, Wp, N2, K, xsum, wsum,
