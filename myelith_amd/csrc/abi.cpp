@@ -4,6 +4,7 @@
 // MYL_E_INVALID; the arithmetic itself lives in the kernels.
 #include "abi_internal.h"
 
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -41,7 +42,9 @@ void* myl_ctx::scratch(size_t bytes) {
 }
 
 // Products with more outputs than this never split K (their tiles alone fill
-// the chip), so the accumulator stays at most 32 MiB.
+// the chip), so the accumulator stays at most 32 MiB; a request beyond the
+// cap still gets a capped accumulator, which the byte-plane products of
+// smaller outputs need.
 static constexpr size_t kMmAccCap = (size_t)4 << 20;
 
 // Activation planes beyond this stay with the tiled kernel (1 GiB: 4096
@@ -50,7 +53,8 @@ static constexpr size_t kMmPlaneCap = (size_t)1 << 30;
 
 const myl::MmCtx* myl_ctx::mm_ctx(size_t elems, size_t plane_bytes) {
     mm.cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1;
-    if (elems > mm.acc_elems && elems <= kMmAccCap) {
+    elems = std::min(elems, kMmAccCap);
+    if (elems > mm.acc_elems) {
         (void)hipStreamSynchronize(stream);
         if (mm.acc) (void)hipFree(mm.acc);
         mm.acc = nullptr;

@@ -162,11 +162,8 @@ __global__ __launch_bounds__(256) void silu_rows_kernel(const int16_t* __restric
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= I) return;
     const uint32_t gu = *reinterpret_cast<const uint32_t*>(GU + (size_t)r * 2 * I + 2 * i);
-    const int16_t g = (int16_t)(gu & 0xFFFFu), u = (int16_t)(gu >> 16);
-    const int32_t g_dom = rescale32((int32_t)g, gate_frac, MYL_TV_SILU_IN_FRAC);
-    const int16_t act = lut_lookup_i16((int16_t)g_dom, silu, silu_len, (int16_t)MYL_TV_SILU_LUT_OFFSET);
-    const int64_t prod = (int64_t)act * (int64_t)u;
-    Hh[(size_t)r * I + i] = clamp_i16_i64(rescale64(prod, (uint8_t)(MYL_TV_SILU_OUT_FRAC + up_frac), down_in_frac));
+    Hh[(size_t)r * I + i] = (int16_t)silu_mul((int16_t)(gu & 0xFFFFu), (int16_t)(gu >> 16), silu, silu_len, gate_frac,
+                                              up_frac, down_in_frac);
 }
 
 // silu_rows_kernel writing byte planes [2R x I] of h for the down product.
@@ -178,11 +175,8 @@ __global__ __launch_bounds__(256) void silu_planes_kernel(const int16_t* __restr
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= I) return;
     const uint32_t gu = *reinterpret_cast<const uint32_t*>(GU + (size_t)r * 2 * I + 2 * i);
-    const int16_t g = (int16_t)(gu & 0xFFFFu), u = (int16_t)(gu >> 16);
-    const int32_t g_dom = rescale32((int32_t)g, gate_frac, MYL_TV_SILU_IN_FRAC);
-    const int16_t act = lut_lookup_i16((int16_t)g_dom, silu, silu_len, (int16_t)MYL_TV_SILU_LUT_OFFSET);
-    const int64_t prod = (int64_t)act * (int64_t)u;
-    const int32_t h = clamp_i16_i64(rescale64(prod, (uint8_t)(MYL_TV_SILU_OUT_FRAC + up_frac), down_in_frac));
+    const int32_t h = silu_mul((int16_t)(gu & 0xFFFFu), (int16_t)(gu >> 16), silu, silu_len, gate_frac, up_frac,
+                               down_in_frac);
     planes[(size_t)(2 * r) * I + i] = (int8_t)(h >> 8);
     planes[(size_t)(2 * r + 1) * I + i] = (int8_t)((h & 255) - 128);
 }
@@ -271,13 +265,19 @@ hipError_t forward_rows(myl_model* m, int R, int lmax) {
     hipStream_t st = c->stream;
     const int H = m->H, I = m->I, V = m->V, nq = m->nq, nkv = m->nkv, hd = m->hd, G = m->G;
     const int nqkv = nq + 2 * nkv, heads = (int)m->spec.heads, kvh = (int)m->spec.kv_heads;
-    const MmCtx* mm = c->mm_ctx((size_t)R * std::max(2 * I, nqkv), R >= 2 ? (size_t)2 * R * std::max(I, H) : 0);
+    // planes: [2R x max(I, H)] for every product, plus [2R x H] after the
+    // first 2R x I bytes for the gate/up input when the SiLU is fused
+    const size_t plane_req = R < 2 ? 0 : (size_t)2 * R * (R > 64 ? (size_t)I + H : (size_t)std::max(I, H));
+    const MmCtx* mm = c->mm_ctx((size_t)R * std::max(2 * I, nqkv), plane_req);
     const size_t sstride = seq_stride(m);
     const int ranges = (lmax + kAttnRange - 1) / kAttnRange;
     // producers write the products' byte planes directly when every product
     // of the layer runs on planes
     const bool planes = mm_planes_ok(R, H, mm) && mm_planes_ok(R, I, mm) && mm_planes_ok(R, nq, mm) &&
                         rmsnorm_planes_ok(H) && xvec_ok(b->X, H);
+    // the gate/up product applies the SiLU and writes the down product's
+    // planes itself (lane-pair epilogue) when its tiles need no K split
+    const bool fuse_silu = planes && R > 64 && (size_t)2 * R * ((size_t)I + H) <= mm->planes_bytes;
     const uint8_t lut_shift = MYL_TV_SCORE_FRAC_BITS - MYL_TV_EXP_INPUT_FRAC;
     hipError_t e;
     embed_rows_kernel<<<R, 256, 0, st>>>(b->rows + 3 * b->rows_cap, m->emb, m->emb_shifts, m->layers[0].res_in, H, b->X);
@@ -345,7 +345,16 @@ hipError_t forward_rows(myl_model* m, int R, int lmax) {
         EpiGURows eg{};
         eg.shifts = Ld.sgu; eg.act_frac = f.norm_mlp_frac; eg.gate_frac = f.gate_frac; eg.up_frac = f.up_frac;
         eg.out = b->GU; eg.ldo = 2 * I;
-        if (planes) {
+        if (fuse_silu) {
+            int8_t* xin = mm->planes + (size_t)2 * R * I;
+            EpiGUSiluPlanes es{Ld.sgu, f.norm_mlp_frac, f.gate_frac, f.up_frac, f.down_in_frac,
+                               m->silu, (uint32_t)m->silu_len, mm->planes, I};
+            if ((e = rmsnorm_planes(b->X2, R, H, Ld.res_mid, Ld.post_gamma, Ld.post_gamma_s, H, m->rsqrt,
+                                    m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20,
+                                    f.norm_mlp_frac, xin, st)) != hipSuccess ||
+                (e = mm_planes_pair(xin, R, Ld.wgu, 2 * I, H, es, mm, st)) != hipSuccess)
+                return e;
+        } else if (planes) {
             if ((e = rmsnorm_planes(b->X2, R, H, Ld.res_mid, Ld.post_gamma, Ld.post_gamma_s, H, m->rsqrt,
                                     m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20,
                                     f.norm_mlp_frac, mm->planes, st)) != hipSuccess ||
@@ -388,7 +397,7 @@ hipError_t forward_rows(myl_model* m, int R, int lmax) {
                 m->lm16_planes_ok = true;
             }
             if ((e = split_planes_sum(b->Xn, R, H, H, mm->planes, b->xsum, st)) != hipSuccess) return e;
-            if ((e = mm2w16_launch(mm->planes, b->xsum, R, m->lm16_planes, m->lm16_wsum, V, H, el, st)) != hipSuccess)
+            if ((e = mm2w16_launch(mm->planes, b->xsum, R, m->lm16_planes, m->lm16_wsum, V, H, el, mm->cus, st)) != hipSuccess)
                 return e;
         } else if ((e = gemv_i16(b->Xn, R, H, m->lm16, V, H, el, st)) != hipSuccess) {
             return e;

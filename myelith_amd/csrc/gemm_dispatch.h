@@ -96,20 +96,41 @@ inline bool mm_planes_ok(int M, int K, const MmCtx* mm) {
            mm_env("MYL_MM_TILE") < 0;
 }
 
+// Whether 256 x 256 tiles with 128-byte K stages fill the chip well enough
+// (mm_planes).
+inline bool mm_wide_tiles(int M, int N, int K, int cus) {
+    return K % 128 == 0 && mm2_tiles<2, 2, 4, 4, 2, 128>(M, N) >= cus + cus / 2;
+}
+
 // The product on planes Ap [2M x K] (mm_planes_ok): few rows stream the
 // weights once in 64 or 128 plane-row tiles (K split until the chip is
-// full, or half full past 32 rows); more rows take 256 x 128 block tiles
-// (72 KB of LDS: two blocks per CU, which measured faster than 256 x 256
-// tiles at one block per CU for every shape from 512 to 4096 rows) when
-// those give every CU a tile.
+// full, or half full past 32 rows).  More rows take 256 x 256 block tiles of
+// 16 waves with 128-byte K stages (128 KB of LDS, one block per CU) when the
+// grid holds at least 1.5 such tiles per CU: 12-25% faster than the
+// alternative on MI355X for 2048-4096 rows of the 7B projections.  Smaller
+// grids, where the last partial wave of big tiles costs more than the stage
+// width gains (about 15% slower at 1.2 tiles per CU), take 256 x 128 tiles
+// with 64-byte stages (72 KB of LDS, two blocks per CU) when those give
+// every CU a tile.
 template <class Epi>
 inline hipError_t mm_planes(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, const MmCtx* mm,
                             hipStream_t st) {
     const int cus = mm->cus;
     // few rows: partial sums cost little, so K is split until every CU has work
     if (M <= 32) return mm2_launch_splitk<2, 1, 1, 4, 4>(Ap, M, W, N, K, epi, mm, cus, st);
+    if (M > 64 && mm_wide_tiles(M, N, K, cus)) return mm2_launch<2, 2, 4, 4, 2, 128>(Ap, M, W, N, K, epi, st);
     if (M > 64 && mm2_tiles<2, 2, 4, 2, 3>(M, N) >= cus) return mm2_launch<2, 2, 4, 2, 3>(Ap, M, W, N, K, epi, st);
     return mm2_launch_splitk<2, 1, 2, 4, 4>(Ap, M, W, N, K, epi, mm, cus / 2, st);
+}
+
+// The gate/up product with the lane-pair epilogue (EpiGUSiluPlanes), for
+// more than 64 rows: the tiles of mm_planes without a K split.
+template <class Epi>
+inline hipError_t mm_planes_pair(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi,
+                                 const MmCtx* mm, hipStream_t st) {
+    if (M <= 64 || N % 2 != 0 || K % 64 != 0) return hipErrorInvalidValue;
+    if (mm_wide_tiles(M, N, K, mm->cus)) return mm2_pair_launch<2, 2, 4, 4, 2, 128>(Ap, M, W, N, K, epi, st);
+    return mm2_pair_launch<2, 2, 4, 2, 3, 64>(Ap, M, W, N, K, epi, st);
 }
 
 // Tile and K split, from a sweep of the W8A16 shapes on MI355X: 64-row tiles

@@ -12,14 +12,17 @@
 // lane, so the combination needs no data movement.
 //
 // Tiling (gfx950, 160 KB LDS): a block of WM x WN waves owns BR = 32*MB*WM
-// rows of A' and BN = 32*NB*WN weight rows; K advances 64 bytes per stage
-// through STAGES LDS buffers filled by direct global-to-LDS loads
-// (global_load_lds_dwordx4: each wave instruction writes 1 KiB = 16 rows x 64
-// bytes), issued STAGES-1 stages ahead and awaited with an explicit vmcnt.
-// The four 16-byte chunks of LDS row r sit at slot chunk ^ ((r >> 2) & 3), so
-// the 16-byte fragment reads of consecutive rows fall on distinct banks.
-// K must be a multiple of 64; rows past the matrix clamp to its last row
-// (their outputs are discarded), so every load stays in bounds.
+// rows of A' and BN = 32*NB*WN weight rows; K advances KS = 64 or 128 bytes
+// per stage through STAGES LDS buffers filled by direct global-to-LDS loads
+// (global_load_lds_dwordx4: each wave instruction writes 1 KiB = 1024/KS rows
+// x KS bytes), issued STAGES-1 stages ahead and awaited with an explicit
+// vmcnt.  128-byte stages read whole cache lines of every row per load
+// instruction and halve the barriers per K; they pay off for grids of many
+// large tiles.  The KS/16 chunks of LDS row r sit at slot
+// chunk ^ ((r / (256/KS)) % (KS/16)), so the 16-byte fragment reads of 16
+// consecutive rows cover all 64 banks once.  K must be a multiple of KS; rows
+// past the matrix clamp to its last row (their outputs are discarded), so
+// every load stays in bounds.
 #pragma once
 
 #include "gemm_mfma.h"
@@ -47,49 +50,54 @@ __global__ __launch_bounds__(256) void split_planes_kernel(const int16_t* __rest
 
 __device__ inline constexpr int waitcnt_vm(int v) { return (v & 0xF) | (0x7 << 4) | (0xF << 8) | (((v >> 4) & 0x3) << 14); }
 
-template <int MB, int NB, int WM_, int WN_, int STAGES>
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS = 64>
 struct Mm2 {
+    static_assert(KS == 64 || KS == 128, "stage width");
     static constexpr int kThreads = WM_ * WN_ * 64;
     static constexpr int BR = 32 * MB * WM_;   // A' rows per block (2 per token)
     static constexpr int BN = 32 * NB * WN_;   // weight rows per block
-    static constexpr int kStageBytes = (BR + BN) * 64;
+    static constexpr int kCpr = KS / 16;       // 16-byte chunks per stage row
+    static constexpr int kRowsPerLoad = 64 / kCpr;
+    static constexpr int kSwzRows = 256 / KS;  // rows sharing one swizzle slot
+    static constexpr int kStageBytes = (BR + BN) * KS;
     static constexpr size_t kLds = (size_t)STAGES * kStageBytes;
-    static constexpr int kChunks = (BR + BN) * 4;          // 16-byte chunks per stage
+    static constexpr int kChunks = (BR + BN) * kCpr;       // 16-byte chunks per stage
     static constexpr int kLoads = kChunks / kThreads;      // per thread per stage
     static_assert(kChunks % kThreads == 0, "whole wave loads");
+    __device__ static int slot(int row, int chunk) { return chunk ^ ((row / kSwzRows) & (kCpr - 1)); }
 };
 
-// LDS layout of a stage: BR A' rows then BN weight rows, 64 bytes each; the
-// four 16-byte chunks of row r sit at chunk slot c ^ ((r >> 2) & 3).
+// LDS layout of a stage: BR A' rows then BN weight rows, KS bytes each, the
+// chunks of each row at Mm2::slot.
 // The pipelined main loop: acc[i][j] = A' tile i x W tile j over K in
-// [kb, ke) (multiples of 64); rs[j] = the lane's weight-row sum (summed over
+// [kb, ke) (multiples of KS); rs[j] = the lane's weight-row sum (summed over
 // the lane pair l, l + 32 only after the loop).
-template <int MB, int NB, int WM_, int WN_, int STAGES>
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS = 64>
 __device__ inline void mm2_main(const int8_t* __restrict__ Ap, int R2, const int8_t* __restrict__ W, int N, int K,
                                 int kb, int ke, int r0, int n0, int8_t* lds, v16i32_t (&acc)[MB][NB],
                                 int32_t (&rs)[NB]) {
-    using S = Mm2<MB, NB, WM_, WN_, STAGES>;
+    using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave % WM_, wn = wave / WM_;
-    const int nk = (ke - kb) / 64;
-    // Each wave-level load moves 16 rows (64 lanes x 16 bytes): lane l takes
-    // row (l >> 2) of the group and the global chunk whose swizzled slot is l & 3.
+    const int nk = (ke - kb) / KS;
+    // Each wave-level load moves 1 KiB (64 lanes x 16 bytes) of 1024/KS rows:
+    // lane l takes row l / (KS/16) of the group and the global chunk whose
+    // swizzled slot is l % (KS/16) (the swizzle is its own inverse).
     auto issue = [&](int kt, int buf) {
         int8_t* st = lds + buf * S::kStageBytes;
 #pragma unroll
         for (int i = 0; i < S::kLoads; ++i) {
-            const int grp = wave + i * (S::kThreads / 64);   // 16-row group index in the stage
-            const int row = grp * 16 + (lane >> 2);          // stage row: A' rows first
-            const int slot = lane & 3;
-            const int chunk = slot ^ ((row >> 2) & 3);
+            const int grp = wave + i * (S::kThreads / 64);   // 1 KiB row-group index in the stage
+            const int row = grp * S::kRowsPerLoad + lane / S::kCpr;  // stage row: A' rows first
+            const int chunk = S::slot(row, lane & (S::kCpr - 1));
             const int8_t* src;
             if (row < S::BR) {
                 const int gr = min(r0 + row, R2 - 1);
-                src = Ap + (size_t)gr * K + kb + kt * 64 + chunk * 16;
+                src = Ap + (size_t)gr * K + kb + kt * KS + chunk * 16;
             } else {
                 const int gn = min(n0 + row - S::BR, N - 1);
-                src = W + (size_t)gn * K + kb + kt * 64 + chunk * 16;
+                src = W + (size_t)gn * K + kb + kt * KS + chunk * 16;
             }
             __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(st + grp * 1024), 16, 0, 0);
         }
@@ -114,18 +122,18 @@ __device__ inline void mm2_main(const int8_t* __restrict__ Ap, int R2, const int
         if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
         const int8_t* st = lds + (kt % STAGES) * S::kStageBytes;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
+        for (int s = 0; s < KS / 32; ++s) {
             const int chunk = 2 * s + (lane >> 5);
             v4i32_t a[MB], b[NB];
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
                 const int row = S::BR + (wn * NB + j) * 32 + (lane & 31);
-                b[j] = *reinterpret_cast<const v4i32_t*>(st + row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4));
+                b[j] = *reinterpret_cast<const v4i32_t*>(st + row * KS + (S::slot(row, chunk) << 4));
             }
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
                 const int row = (wm * MB + i) * 32 + (lane & 31);
-                a[i] = *reinterpret_cast<const v4i32_t*>(st + row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4));
+                a[i] = *reinterpret_cast<const v4i32_t*>(st + row * KS + (S::slot(row, chunk) << 4));
             }
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
@@ -140,8 +148,8 @@ __device__ inline void mm2_main(const int8_t* __restrict__ Ap, int R2, const int
     }
 }
 
-// K runs over [kb, ke) (multiples of 64).
-template <int MB, int NB, int WM_, int WN_, int STAGES, class Sink>
+// K runs over [kb, ke) (multiples of KS).
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class Sink>
 __device__ inline void mm2_tile(const int8_t* __restrict__ Ap, int R2, const int8_t* __restrict__ W, int N, int K,
                                 int kb, int ke, int r0, int n0, int8_t* lds, const Sink& sink) {
     const int lane = threadIdx.x & 63;
@@ -149,7 +157,7 @@ __device__ inline void mm2_tile(const int8_t* __restrict__ Ap, int R2, const int
     const int wm = wave % WM_, wn = wave / WM_;
     v16i32_t acc[MB][NB];
     int32_t rs[NB];
-    mm2_main<MB, NB, WM_, WN_, STAGES>(Ap, R2, W, N, K, kb, ke, r0, n0, lds, acc, rs);
+    mm2_main<MB, NB, WM_, WN_, STAGES, KS>(Ap, R2, W, N, K, kb, ke, r0, n0, lds, acc, rs);
 #pragma unroll
     for (int j = 0; j < NB; ++j) rs[j] += __shfl_xor(rs[j], 32);
     // accumulator rows 8*(r/4) + 4*(lane/32) + r%4: registers (r, r+1), r even,
@@ -169,16 +177,63 @@ __device__ inline void mm2_tile(const int8_t* __restrict__ Ap, int R2, const int
         }
 }
 
-template <int MB, int NB, int WM_, int WN_, int STAGES, class Epi>
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class Epi>
 __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_kernel(const int8_t* __restrict__ Ap, int R2, const int8_t* __restrict__ W,
                                                              int N, int K, Divider tiles_r, int ntiles, Epi epi) {
-    using S = Mm2<MB, NB, WM_, WN_, STAGES>;
+    using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     extern __shared__ __align__(16) int8_t lds[];
     const int t = mm_tile_index(ntiles);
     if (t < 0) return;
     uint32_t tn, tr;
     tiles_r.divmod((uint32_t)t, tn, tr);
-    mm2_tile<MB, NB, WM_, WN_, STAGES>(Ap, R2, W, N, K, 0, K, (int)tr * S::BR, (int)tn * S::BN, lds, SinkEpi<Epi>{epi});
+    mm2_tile<MB, NB, WM_, WN_, STAGES, KS>(Ap, R2, W, N, K, 0, K, (int)tr * S::BR, (int)tn * S::BN, lds, SinkEpi<Epi>{epi});
+}
+
+// As mm2_kernel, with an epilogue over lane pairs (columns 2i, 2i+1 of one
+// row): Epi::pair(n, m, sum, valid) is called by all lanes together.
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class Epi>
+__global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_pair_kernel(const int8_t* __restrict__ Ap, int R2,
+                                                                  const int8_t* __restrict__ W, int N, int K,
+                                                                  Divider tiles_r, int ntiles, Epi epi) {
+    using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
+    extern __shared__ __align__(16) int8_t lds[];
+    const int t = mm_tile_index(ntiles);
+    if (t < 0) return;
+    uint32_t tn, tr;
+    tiles_r.divmod((uint32_t)t, tn, tr);
+    const int r0 = (int)tr * S::BR, n0 = (int)tn * S::BN;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave % WM_, wn = wave / WM_;
+    v16i32_t acc[MB][NB];
+    int32_t rs[NB];
+    mm2_main<MB, NB, WM_, WN_, STAGES, KS>(Ap, R2, W, N, K, 0, K, r0, n0, lds, acc, rs);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) rs[j] += __shfl_xor(rs[j], 32);
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int n = n0 + (wn * NB + j) * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const int arow = r0 + (wm * MB + i) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                epi.pair(n, arow >> 1, (int64_t)acc[i][j][r] * 256 + (int64_t)acc[i][j][r + 1] + (int64_t)rs[j] * 128,
+                         arow < R2 && n < N);
+            }
+        }
+}
+
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class Epi>
+hipError_t mm2_pair_launch(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, hipStream_t st) {
+    using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
+    const int R2 = 2 * M;
+    const int tiles_r = (R2 + S::BR - 1) / S::BR, ntiles = tiles_r * ((N + S::BN - 1) / S::BN);
+    auto kern = mm2_pair_kernel<MB, NB, WM_, WN_, STAGES, KS, Epi>;
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
+    if (e != hipSuccess) return e;
+    kern<<<8 * ((ntiles + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, R2, W, N, K, Divider::of((uint32_t)tiles_r), ntiles, epi);
+    return hipGetLastError();
 }
 
 // int16 weights as byte planes: Wp [2N x K] with row 2n = hi(w_n), row
@@ -188,7 +243,7 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_kernel(const int8_t* __res
 // 2m+1 sit in registers r, r+1 of one lane and columns 2n, 2n+1 in lanes
 // l, l^1, so a DPP swap of lane pairs assembles
 //   x.w = 65536*hh + 256*(h lo' + lo' h) + lo' lo' + 128*(xsum + wsum) - 16384*K.
-template <int MB, int NB, int WM_, int WN_, int STAGES, class Sink>
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class Sink>
 __device__ inline void mm2w16_tile(const int8_t* __restrict__ Ap, int R2, const int8_t* __restrict__ Wp, int N2,
                                    int K, const int32_t* __restrict__ xsum, const int32_t* __restrict__ wsum, int r0,
                                    int n0, int8_t* lds, const Sink& sink) {
@@ -197,7 +252,7 @@ __device__ inline void mm2w16_tile(const int8_t* __restrict__ Ap, int R2, const 
     const int wm = wave % WM_, wn = wave / WM_;
     v16i32_t acc[MB][NB];
     int32_t rs[NB];
-    mm2_main<MB, NB, WM_, WN_, STAGES>(Ap, R2, Wp, N2, K, 0, K, r0, n0, lds, acc, rs);
+    mm2_main<MB, NB, WM_, WN_, STAGES, KS>(Ap, R2, Wp, N2, K, 0, K, r0, n0, lds, acc, rs);
     const int64_t kterm = 16384 * (int64_t)K;
     const bool even = (lane & 1) == 0;
 #pragma unroll
@@ -219,19 +274,19 @@ __device__ inline void mm2w16_tile(const int8_t* __restrict__ Ap, int R2, const 
         }
 }
 
-template <int MB, int NB, int WM_, int WN_, int STAGES, class Epi>
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class Epi>
 __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2w16_kernel(const int8_t* __restrict__ Ap, int R2,
                                                                 const int8_t* __restrict__ Wp, int N2, int K,
                                                                 const int32_t* __restrict__ xsum,
                                                                 const int32_t* __restrict__ wsum, Divider tiles_r,
                                                                 int ntiles, Epi epi) {
-    using S = Mm2<MB, NB, WM_, WN_, STAGES>;
+    using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     extern __shared__ __align__(16) int8_t lds[];
     const int t = mm_tile_index(ntiles);
     if (t < 0) return;
     uint32_t tn, tr;
     tiles_r.divmod((uint32_t)t, tn, tr);
-    mm2w16_tile<MB, NB, WM_, WN_, STAGES>(Ap, R2, Wp, N2, K, xsum, wsum, (int)tr * S::BR, (int)tn * S::BN, lds,
+    mm2w16_tile<MB, NB, WM_, WN_, STAGES, KS>(Ap, R2, Wp, N2, K, xsum, wsum, (int)tr * S::BR, (int)tn * S::BN, lds,
                                           SinkEpi<Epi>{epi});
 }
 
@@ -266,19 +321,31 @@ inline hipError_t split_planes_sum(const int16_t* x, int M, int ldx, int K, int8
 }
 
 // The int16-weight product for many rows: A' and xsum from split_planes_sum,
-// Wp and wsum prepared once the same way.  Tiles of 256 A' rows x 128 W' rows.
-template <class Epi>
-hipError_t mm2w16_launch(const int8_t* Ap, const int32_t* xsum, int M, const int8_t* Wp, const int32_t* wsum, int N,
-                         int K, const Epi& epi, hipStream_t st) {
-    using S = Mm2<2, 2, 4, 2, 3>;
+// Wp and wsum prepared once the same way.  Tiles of 256 A' rows x 256 W' rows
+// with 128-byte stages when the grid holds at least four tiles per CU (and
+// K % 128 == 0), else 256 x 128 tiles with 64-byte stages.
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class Epi>
+hipError_t mm2w16_launch_cfg(const int8_t* Ap, const int32_t* xsum, int M, const int8_t* Wp, const int32_t* wsum,
+                             int N, int K, const Epi& epi, hipStream_t st) {
+    using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     const int R2 = 2 * M, N2 = 2 * N;
     const int tiles_r = (R2 + S::BR - 1) / S::BR, ntiles = tiles_r * ((N2 + S::BN - 1) / S::BN);
-    auto kern = mm2w16_kernel<2, 2, 4, 2, 3, Epi>;
+    auto kern = mm2w16_kernel<MB, NB, WM_, WN_, STAGES, KS, Epi>;
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
     if (e != hipSuccess) return e;
     kern<<<8 * ((ntiles + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, R2, Wp, N2, K, xsum, wsum,
                                                               Divider::of((uint32_t)tiles_r), ntiles, epi);
     return hipGetLastError();
+}
+
+template <class Epi>
+hipError_t mm2w16_launch(const int8_t* Ap, const int32_t* xsum, int M, const int8_t* Wp, const int32_t* wsum, int N,
+                         int K, const Epi& epi, int cus, hipStream_t st) {
+    using W = Mm2<2, 2, 4, 4, 2, 128>;
+    const int wide_tiles = ((2 * M + W::BR - 1) / W::BR) * ((2 * N + W::BN - 1) / W::BN);
+    if (K % 128 == 0 && wide_tiles >= 4 * cus)
+        return mm2w16_launch_cfg<2, 2, 4, 4, 2, 128>(Ap, xsum, M, Wp, wsum, N, K, epi, st);
+    return mm2w16_launch_cfg<2, 2, 4, 2, 3, 64>(Ap, xsum, M, Wp, wsum, N, K, epi, st);
 }
 
 // Split-K form: item t -> (slice t / ntiles, tile t % ntiles); the exact
@@ -298,16 +365,17 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_splitk_kernel(const int8_t
     tiles_r.divmod(tile, tn, tr);
     const int kb = (int)ks * kslice, ke = min(K, kb + kslice);
     if (kb >= ke) return;
-    mm2_tile<MB, NB, WM_, WN_, STAGES>(Ap, R2, W, N, K, kb, ke, (int)tr * S::BR, (int)tn * S::BN, lds,
-                                       SinkAtomic{acc, N});
+    mm2_tile<MB, NB, WM_, WN_, STAGES, 64>(Ap, R2, W, N, K, kb, ke, (int)tr * S::BR, (int)tn * S::BN, lds,
+                                           SinkAtomic{acc, N});
 }
 
-template <int MB, int NB, int WM_, int WN_, int STAGES, class Epi>
+// K % KS == 0.
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS = 64, class Epi>
 hipError_t mm2_launch(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, hipStream_t st) {
-    using S = Mm2<MB, NB, WM_, WN_, STAGES>;
+    using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     const int R2 = 2 * M;
     const int tiles_r = (R2 + S::BR - 1) / S::BR, ntiles = tiles_r * ((N + S::BN - 1) / S::BN);
-    auto kern = mm2_kernel<MB, NB, WM_, WN_, STAGES, Epi>;
+    auto kern = mm2_kernel<MB, NB, WM_, WN_, STAGES, KS, Epi>;
     if (S::kLds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
         if (e != hipSuccess) return e;
@@ -348,9 +416,9 @@ hipError_t mm2_launch_splitk(const int8_t* Ap, int M, const int8_t* W, int N, in
 }
 
 // Block tiles of a launch shape (for the dispatch's tile count).
-template <int MB, int NB, int WM_, int WN_, int STAGES>
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS = 64>
 inline int mm2_tiles(int M, int N) {
-    using S = Mm2<MB, NB, WM_, WN_, STAGES>;
+    using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     return ((2 * M + S::BR - 1) / S::BR) * ((N + S::BN - 1) / S::BN);
 }
 

@@ -104,10 +104,129 @@ __global__ __launch_bounds__(kRmsThreads) void rmsnorm_fast_kernel(const int16_t
     }
 }
 
+// Many rows: 256 threads per row, each thread owning PER chunks of 8
+// consecutive elements loaded as one 16-byte (x) and 8-byte (shifts, gamma)
+// vector each; rows of n % 8 == 0 elements, 16-byte aligned.  The sum of
+// squares stays in 64 bits for elements at the largest shift (align 0) and
+// takes the exact 128-bit path only for the others.
+constexpr int kRowsThreads = 256;
+
+__device__ inline uint8_t byte_of(const uint2& v, int q) {
+    return (uint8_t)(((q < 4 ? v.x : v.y) >> (8 * (q & 3))) & 0xFFu);
+}
+
+template <int PER>
+__global__ __launch_bounds__(kRowsThreads) void rmsnorm_rows_kernel(const int16_t* __restrict__ x, int ldx,
+                                                                    const uint8_t* __restrict__ xs,
+                                                                    const int8_t* __restrict__ g,
+                                                                    const uint8_t* __restrict__ gs, int n,
+                                                                    RmsParams p, uint8_t out_frac,
+                                                                    int16_t* __restrict__ out, int ldo,
+                                                                    int8_t* __restrict__ planes) {
+    __shared__ myl_i128 red128[kRowsThreads / 64];
+    __shared__ int32_t red32[kRowsThreads / 64];
+    const int16_t* xr = x + (size_t)blockIdx.x * ldx;
+    const int nc = n >> 3;
+    uint4 xv[PER];
+    uint2 sv[PER];
+    int32_t mx = 0;
+#pragma unroll
+    for (int t = 0; t < PER; ++t) {
+        const int c = threadIdx.x + t * kRowsThreads;
+        xv[t] = make_uint4(0, 0, 0, 0);
+        sv[t] = make_uint2(0, 0);
+        if (c < nc) {
+            xv[t] = *reinterpret_cast<const uint4*>(xr + 8 * c);
+            sv[t] = *reinterpret_cast<const uint2*>(xs + 8 * c);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) mx = max(mx, (int32_t)byte_of(sv[t], q));
+        }
+    }
+    const uint8_t ref = (uint8_t)block_max_i32(mx, red32);
+    uint64_t acc64 = 0;
+    myl_i128 acc = 0;
+#pragma unroll
+    for (int t = 0; t < PER; ++t) {
+        const uint32_t w[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int32_t xi = (int32_t)(int16_t)((w[q >> 1] >> (16 * (q & 1))) & 0xFFFFu);
+            const uint32_t sq = (uint32_t)(xi * xi);   // <= 2^30
+            const uint32_t align = 2u * (uint32_t)(uint8_t)(ref - byte_of(sv[t], q));
+            if (align == 0) acc64 += sq;
+            else acc = (myl_i128)((myl_u128)acc + (myl_u128)shl128((myl_i128)sq, align));
+        }
+    }
+    acc = (myl_i128)((myl_u128)acc + (myl_u128)acc64);
+    acc = wave_sum_i128(acc);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red128[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    acc = 0;
+#pragma unroll
+    for (int i = 0; i < kRowsThreads / 64; ++i) acc = (myl_i128)((myl_u128)acc + (myl_u128)red128[i]);
+    const RmsFactor f = rms_factor_of(acc, ref, p);
+#pragma unroll
+    for (int t = 0; t < PER; ++t) {
+        const int c = threadIdx.x + t * kRowsThreads;
+        if (c >= nc) continue;
+        const uint2 gv = *reinterpret_cast<const uint2*>(g + 8 * c);
+        const uint2 gsv = *reinterpret_cast<const uint2*>(gs + 8 * c);
+        const uint32_t w[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+        int32_t y[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            y[q] = rms_out((int16_t)((w[q >> 1] >> (16 * (q & 1))) & 0xFFFFu), byte_of(sv[t], q),
+                           (int8_t)byte_of(gv, q), byte_of(gsv, q), f, out_frac);
+        if (planes) {
+            uint32_t h[2] = {0, 0}, l[2] = {0, 0};
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                h[q >> 2] |= ((uint32_t)(y[q] >> 8) & 0xFFu) << (8 * (q & 3));
+                l[q >> 2] |= ((uint32_t)((y[q] & 255) - 128) & 0xFFu) << (8 * (q & 3));
+            }
+            int8_t* ph = planes + (size_t)(2 * blockIdx.x) * n + 8 * c;
+            *reinterpret_cast<uint2*>(ph) = make_uint2(h[0], h[1]);
+            *reinterpret_cast<uint2*>(ph + n) = make_uint2(l[0], l[1]);
+        } else {
+            uint32_t o[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                o[q] = ((uint32_t)y[2 * q] & 0xFFFFu) | ((uint32_t)y[2 * q + 1] << 16);
+            *reinterpret_cast<uint4*>(out + (size_t)blockIdx.x * ldo + 8 * c) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+    }
+}
+
+// The row kernel's PER for n elements (0: not applicable).
+inline int rms_rows_per(int n) {
+    if (n % 8 != 0) return 0;
+    const int nc = n / 8;
+    return nc <= kRowsThreads ? 1 : nc <= 2 * kRowsThreads ? 2 : nc <= 4 * kRowsThreads ? 4 : 0;
+}
+
+// Row kernel launch when M rows fill the chip and the layout allows it.
+bool rmsnorm_rows(const int16_t* x, int M, int ldx, const uint8_t* xs, const int8_t* g, const uint8_t* gs, int n,
+                  const RmsParams& p, uint8_t out_frac, int16_t* out, int ldo, int8_t* planes, hipStream_t st) {
+    const int per = rms_rows_per(n);
+    const bool aligned = ((uintptr_t)x % 16 == 0) && ldx % 8 == 0 && ((uintptr_t)xs % 8 == 0) &&
+                         ((uintptr_t)g % 8 == 0) && ((uintptr_t)gs % 8 == 0) &&
+                         (planes ? (uintptr_t)planes % 8 == 0 : ((uintptr_t)out % 16 == 0 && ldo % 8 == 0));
+    if (M < 256 || per == 0 || !aligned) return false;
+    if (per == 1)
+        rmsnorm_rows_kernel<1><<<M, kRowsThreads, 0, st>>>(x, ldx, xs, g, gs, n, p, out_frac, out, ldo, planes);
+    else if (per == 2)
+        rmsnorm_rows_kernel<2><<<M, kRowsThreads, 0, st>>>(x, ldx, xs, g, gs, n, p, out_frac, out, ldo, planes);
+    else
+        rmsnorm_rows_kernel<4><<<M, kRowsThreads, 0, st>>>(x, ldx, xs, g, gs, n, p, out_frac, out, ldo, planes);
+    return true;
+}
+
 hipError_t rmsnorm(const int16_t* x, int M, int ldx, const uint8_t* xs, const int8_t* g, const uint8_t* gs, int n,
                    const int16_t* lut, int lut_len, uint8_t lut_input_shift, uint8_t lut_output_frac,
                    int64_t inv_n_q20, uint8_t out_frac, int16_t* out, int ldo, hipStream_t st) {
     RmsParams p{lut, lut_len, lut_input_shift, lut_output_frac, inv_n_q20};
+    if (rmsnorm_rows(x, M, ldx, xs, g, gs, n, p, out_frac, out, ldo, nullptr, st)) return hipGetLastError();
     if (n <= kRmsThreads * kRmsPer)
         rmsnorm_fast_kernel<<<M, kRmsThreads, 0, st>>>(x, ldx, xs, g, gs, n, p, out_frac, out, ldo, nullptr);
     else
@@ -122,6 +241,7 @@ hipError_t rmsnorm_planes(const int16_t* x, int M, int ldx, const uint8_t* xs, c
                           int64_t inv_n_q20, uint8_t out_frac, int8_t* planes, hipStream_t st) {
     if (!rmsnorm_planes_ok(n)) return hipErrorInvalidValue;
     RmsParams p{lut, lut_len, lut_input_shift, lut_output_frac, inv_n_q20};
+    if (rmsnorm_rows(x, M, ldx, xs, g, gs, n, p, out_frac, nullptr, 0, planes, st)) return hipGetLastError();
     rmsnorm_fast_kernel<<<M, kRmsThreads, 0, st>>>(x, ldx, xs, g, gs, n, p, out_frac, nullptr, 0, planes);
     return hipGetLastError();
 }

@@ -59,23 +59,15 @@ struct RmsParams {
 // Norm factor of one row: everything except the per-channel output.
 struct RmsFactor { bool zero; uint8_t ref_shift; int64_t lut_val; uint32_t norm_frac; };
 
-// Must be called by the whole block.  red128 needs blockDim.x entries.
-__device__ inline RmsFactor rms_factor(const int16_t* x, const uint8_t* xs, int n, const RmsParams& p,
-                                       myl_i128* red128, int32_t* red32) {
-    int32_t mx = 0;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) mx = max(mx, (int32_t)xs[i]);
-    const uint8_t ref = (uint8_t)block_max_i32(mx, red32);
-    myl_i128 acc = 0;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const uint32_t align = 2u * (uint32_t)(uint8_t)(ref - xs[i]);
-        const myl_i128 sq = (myl_i128)x[i] * (myl_i128)x[i];
-        acc = (myl_i128)((myl_u128)acc + (myl_u128)shl128(sq, align));
-    }
-    acc = block_sum_i128(acc, red128);
+// The factor from the aligned sum of squares acc and the largest input
+// shift ref (rmsnorm.rs:96-126): mean = acc * inv_n >> 20, scaled down by
+// an even q until it indexes the rsqrt LUT.
+__device__ inline RmsFactor rms_factor_of(myl_i128 acc, uint8_t ref, const RmsParams& p) {
     RmsFactor f;
     f.ref_shift = ref;
     f.zero = acc == 0;
-    f.lut_val = 0; f.norm_frac = 0;
+    f.lut_val = 0;
+    f.norm_frac = 0;
     if (!f.zero) {
         const myl_i128 m = shr128((myl_i128)((myl_u128)acc * (myl_u128)(myl_i128)p.inv_n_q20), 20);
         const myl_i128 max_idx = (myl_i128)(p.lut_len - 1);
@@ -90,6 +82,22 @@ __device__ inline RmsFactor rms_factor(const int16_t* x, const uint8_t* xs, int 
     return f;
 }
 
+// Must be called by the whole block.  red128 needs blockDim.x entries.
+__device__ inline RmsFactor rms_factor(const int16_t* x, const uint8_t* xs, int n, const RmsParams& p,
+                                       myl_i128* red128, int32_t* red32) {
+    int32_t mx = 0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) mx = max(mx, (int32_t)xs[i]);
+    const uint8_t ref = (uint8_t)block_max_i32(mx, red32);
+    myl_i128 acc = 0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const uint32_t align = 2u * (uint32_t)(uint8_t)(ref - xs[i]);
+        const myl_i128 sq = (myl_i128)x[i] * (myl_i128)x[i];
+        acc = (myl_i128)((myl_u128)acc + (myl_u128)shl128(sq, align));
+    }
+    acc = block_sum_i128(acc, red128);
+    return rms_factor_of(acc, ref, p);
+}
+
 // Per-channel output of rmsnorm.rs:130-159.  |x * lut * gamma| < 2^37, so for
 // 0 <= shift <= 62 and for left shifts up to 25 bits the i64 computation is the
 // i128 one bit for bit; other shifts take the i128 path.
@@ -97,7 +105,8 @@ __device__ inline int16_t rms_out(int16_t x, uint8_t xs, int8_t g, uint8_t gs, c
     if (f.zero) return 0;
     const int32_t total = (int32_t)f.norm_frac + (int32_t)gs + ((int32_t)xs - (int32_t)f.ref_shift);
     const int32_t shift = total - (int32_t)out_frac;
-    const int64_t p64 = (int64_t)x * f.lut_val * (int64_t)g;
+    // |x * g| < 2^22 and the LUT value is an int16: one 32 x 32 -> 64 product
+    const int64_t p64 = (int64_t)((int32_t)x * (int32_t)g) * (int64_t)(int32_t)f.lut_val;
     if (shift >= 0 && shift <= 62) return clamp_i16_i64(clamp_i32_i64(rshift_round64(p64, (uint8_t)shift)));
     if (shift < 0 && shift >= -25) return clamp_i16_i64(clamp_i32_i64(p64 << (-shift)));
     const myl_i128 prod = (myl_i128)p64;
@@ -144,23 +153,7 @@ __device__ inline RmsFactor rms_factor_regs(const int16_t (&x)[PER], const uint8
     __syncthreads();
     acc = 0;
     for (int i = 0; i < nw; ++i) acc = (myl_i128)((myl_u128)acc + (myl_u128)red128[i]);
-    RmsFactor f;
-    f.ref_shift = ref;
-    f.zero = acc == 0;
-    f.lut_val = 0;
-    f.norm_frac = 0;
-    if (!f.zero) {
-        const myl_i128 m = shr128((myl_i128)((myl_u128)acc * (myl_u128)(myl_i128)p.inv_n_q20), 20);
-        const myl_i128 max_idx = (myl_i128)(p.lut_len - 1);
-        uint32_t q = 0;
-        while (shr128(m, q) > max_idx) q += 2;
-        myl_i128 idx = rshift_round128(m, q);
-        if (idx > max_idx) idx = max_idx;
-        if (idx < 0) idx = 0;
-        f.lut_val = (int64_t)p.lut[(int)idx];
-        f.norm_frac = (uint32_t)p.lut_output_frac + (uint32_t)p.lut_input_shift / 2u + q / 2u;
-    }
-    return f;
+    return rms_factor_of(acc, ref, p);
 }
 
 // ---- softmax.rs:12-64 ----------------------------------------------------------

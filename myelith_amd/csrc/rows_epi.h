@@ -4,6 +4,8 @@
 #pragma once
 
 #include "fixed.h"
+#include "wave.h"
+#include "../../include/myl_theta_v.h"
 
 namespace myl {
 
@@ -72,6 +74,41 @@ struct EpiGURows : EpiApply<EpiGURows> {
     __device__ inline void one(int n, int m, int64_t acc) const {
         const uint8_t frac = (n & 1) ? up_frac : gate_frac;
         out[(size_t)m * ldo + n] = clamp_i16_i64(rescale64(acc, (uint8_t)(shifts[n] + act_frac), frac));
+    }
+};
+
+// mlp.rs:55-65 for one element: h = clamp(rescale(silu(g) * u, 8 + up_frac,
+// down_in_frac)), silu(g) from the LUT over g in the LUT's input domain.
+__device__ inline int32_t silu_mul(int16_t g, int16_t u, const int16_t* __restrict__ silu, uint32_t silu_len,
+                                   uint8_t gate_frac, uint8_t up_frac, uint8_t down_in_frac) {
+    const int32_t g_dom = rescale32((int32_t)g, gate_frac, MYL_TV_SILU_IN_FRAC);
+    const int16_t act = lut_lookup_i16((int16_t)g_dom, silu, silu_len, (int16_t)MYL_TV_SILU_LUT_OFFSET);
+    const int64_t prod = (int64_t)act * (int64_t)u;
+    return clamp_i16_i64(rescale64(prod, (uint8_t)(MYL_TV_SILU_OUT_FRAC + up_frac), down_in_frac));
+}
+
+// The gate/up product fused with the SiLU gate and the byte-plane split of
+// its output: weight rows 2i (gate) and 2i+1 (up) land in lanes l and l ^ 1
+// of the accumulator layout, so a DPP swap hands the even lane both values,
+// and h_i of row m goes straight to planes[2m][i] (hi) and
+// planes[2m+1][i] (lo'), the down product's operand [2M x I].  pair() must
+// be called by every lane of the wave together; `valid` marks lanes whose
+// (n, m) lies inside the product.
+struct EpiGUSiluPlanes {
+    const uint8_t* shifts;
+    uint8_t act_frac, gate_frac, up_frac, down_in_frac;
+    const int16_t* silu; uint32_t silu_len;
+    int8_t* planes; int I;
+    __device__ inline void pair(int n, int m, int64_t acc, bool valid) const {
+        int32_t v = 0;
+        if (valid) v = clamp_i16_i64(rescale64(acc, (uint8_t)(shifts[n] + act_frac), (n & 1) ? up_frac : gate_frac));
+        const int32_t o = dpp_mov<dpp::kXor1>(v);
+        if (valid && (n & 1) == 0) {
+            const int32_t h = silu_mul((int16_t)v, (int16_t)o, silu, silu_len, gate_frac, up_frac, down_in_frac);
+            const int i = n >> 1;
+            planes[(size_t)(2 * m) * I + i] = (int8_t)(h >> 8);
+            planes[(size_t)(2 * m + 1) * I + i] = (int8_t)((h & 255) - 128);
+        }
     }
 };
 

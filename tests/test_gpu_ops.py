@@ -273,6 +273,32 @@ def test_rmsnorm(backend, oracle, luts64, n):
         backend.rmsnorm([1], [0], [1], [0], lut, 7, 8, 1 << 20, 6)
 
 
+@pytest.mark.parametrize("n", [896, 3584, 4096, 8192, 904])
+def test_rmsnorm_many_rows(backend, oracle, luts64, n):
+    """256 rows and more take the vectorized row kernel (8-element chunks,
+    64-bit sums at the largest shift, 128-bit for the others); each row must
+    match the oracle, with per-channel shift spreads up to 20 bits, rows of
+    extreme values and an all-zero row."""
+    import torch
+    case(f"rmsnorm rows M=300 n={n}")
+    r = rng(n + 17)
+    M = 300
+    x = np.stack([gauss16(r, n, sigma=[40, 3000, 30000][m % 3]) for m in range(M)])
+    x[7] = 0
+    x[11] = -32768
+    x[12] = 32767
+    g = r.integers(-127, 128, n).astype(np.int8)
+    gs = r.integers(4, 9, n).astype(np.uint8)
+    inv = oracle.inv_n_q20(n)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    for xs in (np.full(n, 9, np.uint8), r.integers(0, 21, n).astype(np.uint8)):
+        for of in (10, 3):
+            got = backend.rmsnorm_dev(T(x), T(xs), T(g), T(gs), T(luts64.rsqrt), 8, 8, inv, of).cpu().numpy()
+            for m in range(M):
+                ref = oracle.rmsnorm_i16(x[m], xs, g, gs, luts64.rsqrt, 8, 8, inv, of)
+                assert np.array_equal(got[m], ref), (n, m, of)
+
+
 @pytest.mark.parametrize("n", [1, 4, 33, 2304, 152064])
 def test_softmax(backend, oracle, n):
     case(f"softmax n={n}")
