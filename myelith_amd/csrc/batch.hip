@@ -43,6 +43,8 @@ struct BatchState {
     std::vector<uint32_t> len;           // cached positions per sequence
     int16_t* kc = nullptr;               // [seq][layer][kv_head][max_pos][head_dim]
     int16_t* vc = nullptr;
+    bool owns_kv = true;                 // false: kc / vc are the model's single-sequence caches
+    int head_rows = 0;                   // rows the logits buffer holds (0: every row)
     int rows_cap = 0, lmax_cap = 0;
     int32_t* rows = nullptr;             // [4][rows_cap]: seq, pos, rope row, token
     int16_t *X = nullptr, *Xn = nullptr, *X2 = nullptr, *QKV = nullptr, *Q = nullptr, *A = nullptr;
@@ -66,8 +68,8 @@ void batch_free(BatchState* b) {
     if (!b) return;
     for (void* p : b->allocs_rows) (void)hipFree(p);
     for (void* p : b->allocs_scores) (void)hipFree(p);
-    if (b->kc) (void)hipFree(b->kc);
-    if (b->vc) (void)hipFree(b->vc);
+    if (b->owns_kv && b->kc) (void)hipFree(b->kc);
+    if (b->owns_kv && b->vc) (void)hipFree(b->vc);
     if (b->tokens_out) (void)hipFree(b->tokens_out);
     if (b->tiles) (void)hipFree(b->tiles);
     delete b;
@@ -210,8 +212,7 @@ size_t seq_stride(const myl_model* m) {
     return (size_t)m->spec.layers * m->spec.kv_heads * (size_t)m->max_pos * m->hd;
 }
 
-int ensure_rows(myl_model* m, int R) {
-    BatchState* b = m->batch;
+int ensure_rows(myl_model* m, BatchState* b, int R) {
     if (R <= b->rows_cap) return MYL_OK;
     myl_ctx* c = m->ctx;
     (void)hipStreamSynchronize(c->stream);
@@ -229,7 +230,7 @@ int ensure_rows(myl_model* m, int R) {
     b->A = balloc<int16_t>(L, R * nq);
     b->GU = balloc<int16_t>(L, R * 2 * I);
     b->Hh = balloc<int16_t>(L, R * I);
-    b->logits = balloc<int32_t>(L, R * V);
+    b->logits = balloc<int32_t>(L, (b->head_rows > 0 ? std::min<size_t>(R, b->head_rows) : R) * V);
     b->argmax = balloc<int64_t>(L, R);
     b->xsum = balloc<int32_t>(L, R);
     b->argmax_part = balloc<uint64_t>(L, (size_t)R * ((V + kArgChunk - 1) / kArgChunk));
@@ -241,8 +242,7 @@ int ensure_rows(myl_model* m, int R) {
     return MYL_OK;
 }
 
-int ensure_scores(myl_model* m, int lmax) {
-    BatchState* b = m->batch;
+int ensure_scores(myl_model* m, BatchState* b, int lmax) {
     if (lmax <= b->lmax_cap) return MYL_OK;
     myl_ctx* c = m->ctx;
     (void)hipStreamSynchronize(c->stream);
@@ -258,9 +258,10 @@ int ensure_scores(myl_model* m, int lmax) {
 }
 
 // One batched forward over the rows already uploaded to b->rows; lmax is the
-// largest position + 1 among them.
-hipError_t forward_rows(myl_model* m, int R, int lmax) {
-    BatchState* b = m->batch;
+// largest position + 1 among them.  The final norm and LM head run over rows
+// [h0, R) only, into logits_out [(R - h0) x V] and argmax_out [R - h0].
+hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, int32_t* logits_out,
+                        int64_t* argmax_out) {
     myl_ctx* c = m->ctx;
     hipStream_t st = c->stream;
     const int H = m->H, I = m->I, V = m->V, nq = m->nq, nkv = m->nkv, hd = m->hd, G = m->G;
@@ -379,13 +380,16 @@ hipError_t forward_rows(myl_model* m, int R, int lmax) {
         e = planes ? mm_planes(mm->planes, R, Ld.wd, H, I, ed, mm, st) : gemv_i8(b->Hh, R, I, Ld.wd, H, I, ed, st, mm);
         if (e != hipSuccess) return e;
     }
-    if ((e = rmsnorm(b->X, R, H, m->final_res, m->final_gamma, m->final_gamma_s, H, m->rsqrt, m->rsqrt_len,
-                     MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, m->final_norm_frac, b->Xn, H,
-                     st)) != hipSuccess)
+    // final norm and head over rows [h0, R)
+    const int HR = R - h0;
+    if (HR <= 0) return hipSuccess;
+    if ((e = rmsnorm(b->X + (size_t)h0 * H, HR, H, m->final_res, m->final_gamma, m->final_gamma_s, H, m->rsqrt,
+                     m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20,
+                     m->final_norm_frac, b->Xn, H, st)) != hipSuccess)
         return e;
     if (m->spec.lm_head_int16) {
-        EpiLogits el{m->lm16_shifts, m->final_norm_frac, MYL_TV_LOGIT_FRAC_BITS, b->logits, V};
-        if (R >= 256 && H % 64 == 0 && mm && mm->planes && (size_t)2 * R * H <= mm->planes_bytes) {
+        EpiLogits el{m->lm16_shifts, m->final_norm_frac, MYL_TV_LOGIT_FRAC_BITS, logits_out, V};
+        if (HR >= 256 && H % 64 == 0 && mm && mm->planes && (size_t)2 * HR * H <= mm->planes_bytes) {
             // many rows: byte planes of both operands, one int8 product
             if (!m->lm16_planes_ok) {
                 if (!m->lm16_planes) {
@@ -396,25 +400,26 @@ hipError_t forward_rows(myl_model* m, int R, int lmax) {
                 if ((e = split_planes_sum(m->lm16, V, H, H, m->lm16_planes, m->lm16_wsum, st)) != hipSuccess) return e;
                 m->lm16_planes_ok = true;
             }
-            if ((e = split_planes_sum(b->Xn, R, H, H, mm->planes, b->xsum, st)) != hipSuccess) return e;
-            if ((e = mm2w16_launch(mm->planes, b->xsum, R, m->lm16_planes, m->lm16_wsum, V, H, el, mm->cus, st)) != hipSuccess)
+            if ((e = split_planes_sum(b->Xn, HR, H, H, mm->planes, b->xsum, st)) != hipSuccess) return e;
+            if ((e = mm2w16_launch(mm->planes, b->xsum, HR, m->lm16_planes, m->lm16_wsum, V, H, el, mm->cus, st)) !=
+                hipSuccess)
                 return e;
-        } else if ((e = gemv_i16(b->Xn, R, H, m->lm16, V, H, el, st)) != hipSuccess) {
+        } else if ((e = gemv_i16(b->Xn, HR, H, m->lm16, V, H, el, st)) != hipSuccess) {
             return e;
         }
     } else {
-        EpiLogits el{m->lm8_shifts, m->final_norm_frac, MYL_TV_LOGIT_FRAC_BITS, b->logits, V};
-        if ((e = gemv_i8(b->Xn, R, H, m->lm8, V, H, el, st, mm)) != hipSuccess) return e;
+        EpiLogits el{m->lm8_shifts, m->final_norm_frac, MYL_TV_LOGIT_FRAC_BITS, logits_out, V};
+        if ((e = gemv_i8(b->Xn, HR, H, m->lm8, V, H, el, st, mm)) != hipSuccess) return e;
     }
-    return argmax_rows(b->logits, R, V, V, b->argmax, b->argmax_part, st);
+    return argmax_rows(logits_out, HR, V, V, argmax_out, b->argmax_part, st);
 }
 
 // Checks the rows against the sequences' cached lengths and uploads them.
 // Per sequence the batch's positions must be distinct and fill [p0, p0 + n)
 // with p0 <= cached length (a re-run position overwrites, as KVCache::write
 // does); the cached length becomes max(len, p0 + n).
-int upload_rows(myl_model* m, uint32_t R, const uint32_t* seq, const uint32_t* pos, const uint32_t* tok, int* lmax) {
-    BatchState* b = m->batch;
+int upload_rows(myl_model* m, BatchState* b, uint32_t R, const uint32_t* seq, const uint32_t* pos, const uint32_t* tok,
+                int* lmax) {
     myl_ctx* c = m->ctx;
     std::vector<std::vector<uint32_t>> per(b->n_seqs);
     int lm = 0;
@@ -436,8 +441,8 @@ int upload_rows(myl_model* m, uint32_t R, const uint32_t* seq, const uint32_t* p
         if (p[0] > b->len[s]) return c->fail(MYL_E_INVALID, "batch: positions must continue the sequence's cache");
         end[s] = p.back() + 1;
     }
-    int rc = ensure_rows(m, (int)R);
-    if (!rc) rc = ensure_scores(m, lm);
+    int rc = ensure_rows(m, b, (int)R);
+    if (!rc) rc = ensure_scores(m, b, lm);
     if (rc) return rc;
     // attention tiles: each sequence's rows in position order, at most
     // kAttnQV / G rows (and kAttnTileRows) per tile
@@ -482,7 +487,73 @@ int upload_rows(myl_model* m, uint32_t R, const uint32_t* seq, const uint32_t* p
     return MYL_OK;
 }
 
+// Whether the row path can run this model, and its kernels' LDS limits.
+int row_path_setup(myl_model* m) {
+    myl_ctx* c = m->ctx;
+    if (m->G > 16) return c->fail(MYL_E_UNSUPPORTED, "batch: at most 16 query heads per KV head");
+    // The matrix-core P.V splits probabilities into bytes; they stay within
+    // [0, 2^14] when every exp-table entry is non-negative (S >= e_j).
+    std::vector<int16_t> lut(m->exp_len);
+    int rc = c->hip(hipMemcpy(lut.data(), m->exp_lut, lut.size() * 2, hipMemcpyDeviceToHost), "batch: exp table");
+    if (rc) return rc;
+    for (int16_t v : lut)
+        if (v < 0) return c->fail(MYL_E_UNSUPPORTED, "batch: the exp table has negative entries");
+    const std::pair<const void*, size_t> big[4] = {{(const void*)rows_qk_kernel<128>, attn_qk_lds<128>()},
+                                                   {(const void*)rows_qk_kernel<64>, attn_qk_lds<64>()},
+                                                   {(const void*)rows_pv_kernel<128>, attn_pv_lds<128>()},
+                                                   {(const void*)rows_pv_kernel<64>, attn_pv_lds<64>()}};
+    for (const auto& k : big)
+        if (hipFuncSetAttribute(k.first, hipFuncAttributeMaxDynamicSharedMemorySize, (int)k.second) != hipSuccess)
+            return c->fail(MYL_E_HIP, "batch: attention LDS size");
+    return MYL_OK;
+}
+
 }  // namespace
+
+namespace myl {
+
+// Rows per batched prompt chunk (bounds the row and score buffers).
+constexpr uint32_t kPromptChunk = 2048;
+
+int prompt_rows(myl_model* m, const uint32_t* tokens, uint32_t n, uint32_t pos0) {
+    myl_ctx* c = m->ctx;
+    if (m->prompt_ok < 0) {
+        const int rc = row_path_setup(m);
+        if (rc && rc != MYL_E_UNSUPPORTED) return rc;
+        m->prompt_ok = rc ? 0 : 1;
+    }
+    if (!m->prompt_ok) return MYL_E_UNSUPPORTED;
+    if (!m->prompt) {
+        BatchState* b = new (std::nothrow) BatchState();
+        if (!b) return MYL_E_NOMEM;
+        b->n_seqs = 1;
+        b->len.assign(1, 0u);
+        b->kc = m->kcache;
+        b->vc = m->vcache;
+        b->owns_kv = false;
+        b->head_rows = 1;
+        m->prompt = b;
+    }
+    BatchState* b = m->prompt;
+    b->len[0] = m->n_cached;
+    std::vector<uint32_t> seq, pos;
+    for (uint32_t i0 = 0; i0 < n; i0 += kPromptChunk) {
+        const uint32_t k = std::min(kPromptChunk, n - i0);
+        seq.assign(k, 0u);
+        pos.resize(k);
+        for (uint32_t i = 0; i < k; ++i) pos[i] = pos0 + i0 + i;
+        int lmax = 0;
+        int rc = upload_rows(m, b, k, seq.data(), pos.data(), tokens + i0, &lmax);
+        if (rc) return rc;
+        // only the chunk that ends the prompt needs its last row's logits
+        const int h0 = i0 + k == n ? (int)k - 1 : (int)k;
+        rc = c->hip(forward_rows(m, b, (int)k, lmax, h0, m->logits, b->argmax), "prefill rows");
+        if (rc) return rc;
+    }
+    return MYL_OK;
+}
+
+}  // namespace myl
 
 extern "C" {
 
@@ -490,23 +561,7 @@ int myl_model_batch_begin(myl_model* m, uint32_t n_seqs) {
     if (!m || n_seqs == 0) return MYL_E_INVALID;
     if (int nr = m->not_ready()) return nr;
     myl_ctx* c = m->ctx;
-    if (m->G > 16) return c->fail(MYL_E_UNSUPPORTED, "batch: at most 16 query heads per KV head");
-    {
-        // The matrix-core P.V splits probabilities into bytes; they stay within
-        // [0, 2^14] when every exp-table entry is non-negative (S >= e_j).
-        std::vector<int16_t> lut(m->exp_len);
-        int rc = c->hip(hipMemcpy(lut.data(), m->exp_lut, lut.size() * 2, hipMemcpyDeviceToHost), "batch: exp table");
-        if (rc) return rc;
-        for (int16_t v : lut)
-            if (v < 0) return c->fail(MYL_E_UNSUPPORTED, "batch: the exp table has negative entries");
-        const std::pair<const void*, size_t> big[4] = {{(const void*)rows_qk_kernel<128>, attn_qk_lds<128>()},
-                                                       {(const void*)rows_qk_kernel<64>, attn_qk_lds<64>()},
-                                                       {(const void*)rows_pv_kernel<128>, attn_pv_lds<128>()},
-                                                       {(const void*)rows_pv_kernel<64>, attn_pv_lds<64>()}};
-        for (const auto& k : big)
-            if (hipFuncSetAttribute(k.first, hipFuncAttributeMaxDynamicSharedMemorySize, (int)k.second) != hipSuccess)
-                return c->fail(MYL_E_HIP, "batch: attention LDS size");
-    }
+    if (int rc = row_path_setup(m)) return rc;
     if (m->batch && m->batch->n_seqs == (int)n_seqs) {
         std::fill(m->batch->len.begin(), m->batch->len.end(), 0u);
         return MYL_OK;
@@ -537,11 +592,11 @@ int myl_model_forward_batch(myl_model* m, uint32_t n_rows, const uint32_t* seq, 
     if (!m->batch) return c->fail(MYL_E_INVALID, "forward_batch: call myl_model_batch_begin first");
     if (n_rows == 0) return MYL_OK;
     int lmax = 0;
-    int rc = upload_rows(m, n_rows, seq, pos, tokens, &lmax);
-    if (rc) return rc;
-    rc = c->hip(forward_rows(m, (int)n_rows, lmax), "forward_batch");
-    if (rc) return rc;
     BatchState* b = m->batch;
+    int rc = upload_rows(m, b, n_rows, seq, pos, tokens, &lmax);
+    if (rc) return rc;
+    rc = c->hip(forward_rows(m, b, (int)n_rows, lmax, 0, b->logits, b->argmax), "forward_batch");
+    if (rc) return rc;
     if (logits) {
         rc = c->hip(hipMemcpyAsync(logits, b->logits, (size_t)n_rows * m->V * 4, hipMemcpyDeviceToHost, c->stream),
                     "logits");
@@ -577,9 +632,9 @@ int myl_model_batch_decode_greedy(myl_model* m, uint32_t n_rows, const uint32_t*
         if (seen[seq[r]]++) return c->fail(MYL_E_INVALID, "batch_decode: one row per sequence");
     }
     int lmax = 0;
-    int rc = upload_rows(m, n_rows, seq, pos, tokens, &lmax);
-    if (rc) return rc;
     BatchState* b = m->batch;
+    int rc = upload_rows(m, b, n_rows, seq, pos, tokens, &lmax);
+    if (rc) return rc;
     const size_t need = (size_t)n_steps * n_rows;
     if (need > b->tokens_out_cap) {
         (void)hipStreamSynchronize(c->stream);
@@ -589,11 +644,11 @@ int myl_model_batch_decode_greedy(myl_model* m, uint32_t n_rows, const uint32_t*
         if (hipMalloc(&b->tokens_out, need * 8) != hipSuccess) return c->fail(MYL_E_NOMEM, "batch_decode: tokens");
         b->tokens_out_cap = need;
     }
-    rc = ensure_scores(m, lmax + (int)n_steps);
+    rc = ensure_scores(m, b, lmax + (int)n_steps);
     if (rc) return rc;
     hipError_t e = hipSuccess;
     for (uint32_t s = 0; s < n_steps && e == hipSuccess; ++s) {
-        e = forward_rows(m, (int)n_rows, lmax + (int)s);
+        e = forward_rows(m, b, (int)n_rows, lmax + (int)s, 0, b->logits, b->argmax);
         if (e == hipSuccess) {
             rows_advance_kernel<<<(n_rows + 255) / 256, 256, 0, c->stream>>>(b->rows, b->rows_cap, (int)n_rows,
                                                                              b->argmax, m->rope_rows,

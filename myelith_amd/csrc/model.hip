@@ -1439,14 +1439,24 @@ int myl_model_prefill(myl_model* m, const uint32_t* tokens, uint32_t n, uint32_t
     if (pos0 > m->n_cached) return c->fail(MYL_E_INVALID, "prefill: positions must be contiguous from 0");
     for (uint32_t i = 0; i < n; ++i)
         if (tokens[i] >= (uint32_t)m->V) return c->fail(MYL_E_INVALID, "prefill: token id out of range");
-    hipError_t e = hipSuccess;
-    for (uint32_t i = 0; e == hipSuccess && i < n; ++i) {
-        e = embed_step(m, 0, (int)tokens[i], (int)(pos0 + i), nullptr);
-        for (int l = 0; e == hipSuccess && l < (int)m->spec.layers; ++l) e = layer_step(m, l);
+    // Long prompts run as one batch of rows over this cache (each row equals
+    // forward_token at its position); short ones, or models the row path
+    // cannot take, token by token as the reference's prompt loop does.
+    int rc = MYL_E_UNSUPPORTED;
+    if (n >= myl::kPromptRows) {
+        rc = myl::prompt_rows(m, tokens, n, pos0);
+        if (rc && rc != MYL_E_UNSUPPORTED) return rc;
     }
-    if (e == hipSuccess) e = head_step(m);
-    int rc = c->hip(e, "prefill");
-    if (rc) return rc;
+    if (rc == MYL_E_UNSUPPORTED) {
+        hipError_t e = hipSuccess;
+        for (uint32_t i = 0; e == hipSuccess && i < n; ++i) {
+            e = embed_step(m, 0, (int)tokens[i], (int)(pos0 + i), nullptr);
+            for (int l = 0; e == hipSuccess && l < (int)m->spec.layers; ++l) e = layer_step(m, l);
+        }
+        if (e == hipSuccess) e = head_step(m);
+        rc = c->hip(e, "prefill");
+        if (rc) return rc;
+    }
     m->n_cached = std::max(m->n_cached, pos0 + n);
     if (last_logits) {
         rc = c->hip(hipMemcpyAsync(last_logits, m->logits, (size_t)m->V * 4, hipMemcpyDeviceToHost, c->stream), "logits");

@@ -41,6 +41,12 @@ struct LayerDev {
 
 struct BatchState;  // batch.hip
 void batch_free(BatchState* b);
+// A prompt of n >= kPromptRows tokens at positions pos0.. as one batch of
+// rows over the model's own KV cache (batch.hip); writes the last logits to
+// the model's logits.  Returns MYL_E_UNSUPPORTED when the row path cannot
+// take this model (then the caller runs the tokens one at a time).
+constexpr uint32_t kPromptRows = 16;
+int prompt_rows(myl_model* m, const uint32_t* tokens, uint32_t n, uint32_t pos0);
 
 // What a model receives before it is sealed: model-wide tensors, then
 // kLayerSlots tensors per layer (index kModelSlots + layer * kLayerSlots + slot).
@@ -129,6 +135,8 @@ struct myl_model {
         return (T*)p;
     }
     myl::BatchState* batch = nullptr;  // per-sequence KV caches and row buffers
+    myl::BatchState* prompt = nullptr; // row buffers of batched prompts (KV: kcache / vcache)
+    int prompt_ok = -1;                // row path usable for prompts: -1 not yet checked
 
     // MYL_OK when the model is sealed, else the error of a forward call.
     int not_ready() {
@@ -140,6 +148,7 @@ struct myl_model {
         if (step_graph) (void)hipGraphDestroy(step_graph);
         for (hipEvent_t e : ev_pool) (void)hipEventDestroy(e);
         if (batch) myl::batch_free(batch);
+        if (prompt) myl::batch_free(prompt);
         if (io) io_free(io);
         for (void* p : allocs) (void)hipFree(p);
     }

@@ -152,3 +152,42 @@ def test_qwen7b_fullsize_decode(backend):
     toks_g, dig_g = dekodieren_mit_digest(gm, prompt, 4)
     toks_o, dig_o = dekodieren_mit_digest(om, prompt, 4)
     assert toks_g == toks_o and dig_g == dig_o
+
+
+@pytest.mark.parametrize("hd,lm16,kvh", [(128, 1, 2), (64, 0, 1)])
+def test_prefill_rows_match_the_token_loop(backend, hd, lm16, kvh):
+    """Prompts of 16 tokens and more run as one batch of rows over the
+    model's own KV cache: the last logits, every cached K/V entry and the
+    greedy continuation equal the reference's token-by-token prompt loop
+    (generate.rs:28-32), also when a second prompt continues the cache."""
+    spec = tiny(hd, lm16, 1, kvh, layers=2, max_pos=640)
+    case(f"prefill rows hd={hd} lm16={lm16} kvh={kvh}")
+    gm, om = build(backend, spec)
+    r = np.random.default_rng(hd * 7 + lm16)
+    p1 = [int(t) for t in r.integers(0, spec["vocab"], 300)]
+    p2 = [int(t) for t in r.integers(0, spec["vocab"], 40)]
+    g = gm.prefill(p1, 0)
+    o = None
+    for pos, t in enumerate(p1):
+        o = om.forward_token(t, pos)
+    assert np.array_equal(g, o)
+    compare_kv(gm, om, spec, 300)
+    g = gm.prefill(p2, 300)
+    for i, t in enumerate(p2):
+        o = om.forward_token(t, 300 + i)
+    assert np.array_equal(g, o)
+    compare_kv(gm, om, spec, 340)
+    first = int(np.argmax(o))
+    toks, _ = gm.decode_greedy(first, 340, 12)
+    want = []
+    t = first
+    for i in range(12):
+        o = om.forward_token(t, 340 + i)
+        t = int(np.argmax(o))
+        want.append(t)
+    assert [int(x) for x in toks] == want
+    # a short prompt (token loop) after the row path, re-running positions
+    g = gm.prefill(p2[:5], 338)
+    for i, t in enumerate(p2[:5]):
+        o = om.forward_token(t, 338 + i)
+    assert np.array_equal(g, o)
