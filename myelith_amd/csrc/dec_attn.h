@@ -1,0 +1,198 @@
+// dec_attn.h -- integer attention of one query row per KV cache
+// (attention.rs:42-90 with softmax.rs:12-64): the decode step's attention,
+// shared by the single-sequence step and by decode batches (one row per
+// sequence).  A block covers one query head and kChunk positions.
+#pragma once
+
+#include "ops.h"
+#include "wave.h"
+
+namespace myl {
+
+constexpr int kChunk = 64;  // attention positions per block
+
+// int16 pairs -> (hi pair, lo pair) with v = 256 * hi + lo, lo in [0, 255].
+__device__ inline void split_pair(uint32_t v, uint32_t& hi, uint32_t& lo) {
+    const int32_t a = (int16_t)(v & 0xFFFFu), b = (int16_t)(v >> 16);
+    hi = ((uint32_t)(uint16_t)(int16_t)(a >> 8)) | ((uint32_t)(uint16_t)(int16_t)(b >> 8) << 16);
+    lo = (v & 0x00FF00FFu);
+}
+
+// z_j = (i32)RNE(q . k_j * mult, shift) for j in [base, min(base + kChunk, L))
+// (attention.rs:66-67); q is one head's vector, kg the KV head's K rows, z
+// the head's score row.  LPP = HD / 8 lanes hold 16 bytes of a K row each
+// (a wave reads whole rows, coalesced); q . k is exact as
+// 256 * sum(k * q_hi) + sum(k * q_lo) on v_dot2_i32_i16 (|partials| < 2^31),
+// the row sums over the LPP lanes are DPP moves.  256 threads.
+template <int HD>
+__device__ inline void dec_scores(int L, int base, const int16_t* __restrict__ q, const int16_t* __restrict__ kg,
+                                  int64_t score_mult, uint8_t score_shift, int32_t* __restrict__ z) {
+    constexpr int LPP = HD / 8;
+    constexpr int PPW = 64 / LPP;                 // positions per wave per step
+    constexpr int STEPS = kChunk / 4 / PPW;       // steps per wave
+    static_assert(LPP == 8 || LPP == 16, "row sums cover 8 or 16 lanes");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LPP, slot = lane / LPP;
+    uint4 kv[STEPS];
+#pragma unroll
+    for (int it = 0; it < STEPS; ++it) {
+        const int j = base + wave * (kChunk / 4) + it * PPW + slot;
+        kv[it] = j < L ? *reinterpret_cast<const uint4*>(kg + (size_t)j * HD + sub * 8) : make_uint4(0, 0, 0, 0);
+    }
+    const uint4 qv = *reinterpret_cast<const uint4*>(q + sub * 8);
+    uint4 qh, ql;
+    split_pair(qv.x, qh.x, ql.x);
+    split_pair(qv.y, qh.y, ql.y);
+    split_pair(qv.z, qh.z, ql.z);
+    split_pair(qv.w, qh.w, ql.w);
+    typedef short __attribute__((ext_vector_type(2))) s2;
+    auto d2 = [](uint32_t a, uint32_t c, int32_t acc) {
+        return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, a), __builtin_bit_cast(s2, c), acc, false);
+    };
+#pragma unroll
+    for (int it = 0; it < STEPS; ++it) {
+        const int j = base + wave * (kChunk / 4) + it * PPW + slot;
+        int32_t ahi = 0, alo = 0;
+        ahi = d2(kv[it].x, qh.x, ahi);
+        ahi = d2(kv[it].y, qh.y, ahi);
+        ahi = d2(kv[it].z, qh.z, ahi);
+        ahi = d2(kv[it].w, qh.w, ahi);
+        alo = d2(kv[it].x, ql.x, alo);
+        alo = d2(kv[it].y, ql.y, alo);
+        alo = d2(kv[it].z, ql.z, alo);
+        alo = d2(kv[it].w, ql.w, alo);
+        if (LPP == 16) {
+            ahi = row_sum16_i32(ahi);
+            alo = row_sum16_i32(alo);
+        } else {
+            ahi = row_sum8_i32(ahi);
+            alo = row_sum8_i32(alo);
+        }
+        if (sub == 0 && j < L) {
+            const int64_t dot = (int64_t)ahi * 256 + (int64_t)alo;
+            z[j] = (int32_t)rshift_round64(wmul64(dot, score_mult), score_shift);
+        }
+    }
+}
+
+// Softmax statistics of one query head over its L scores (softmax.rs:32-41):
+// m = max, S = wrapping i32 sum of the exp LUT.  Whole block (256 threads).
+__device__ inline void dec_stats(int L, const int32_t* __restrict__ z, const int16_t* __restrict__ lut,
+                                 uint32_t lut_len, uint8_t lut_shift, int32_t& m, int32_t& S) {
+    constexpr int ZPER = 16;  // scores held in registers per thread
+    __shared__ int32_t redm[4];
+    __shared__ uint32_t reds[4];
+    const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
+    int32_t mx = INT32_MIN;
+    uint32_t s = 0;
+    if (L <= 256 * ZPER) {
+        int32_t zz[ZPER];
+#pragma unroll
+        for (int t = 0; t < ZPER; ++t) {
+            const int j = threadIdx.x + t * 256;
+            zz[t] = j < L ? z[j] : INT32_MIN;
+        }
+#pragma unroll
+        for (int t = 0; t < ZPER; ++t) mx = max(mx, zz[t]);
+        mx = block_max_i32_dpp(mx, redm);
+#pragma unroll
+        for (int t = 0; t < ZPER; ++t)
+            if (threadIdx.x + t * 256 < L) s += (uint32_t)exp_lookup(sat_sub32(mx, zz[t]), lut, lut_len, lut_shift, lut_one);
+    } else {
+        for (int j = threadIdx.x; j < L; j += 256) mx = max(mx, z[j]);
+        mx = block_max_i32_dpp(mx, redm);
+        for (int j = threadIdx.x; j < L; j += 256)
+            s += (uint32_t)exp_lookup(sat_sub32(mx, z[j]), lut, lut_len, lut_shift, lut_one);
+    }
+    m = mx;
+    S = (int32_t)block_sum_u32_dpp(s, reds);
+}
+
+// The exact partial P.V of one chunk (attention.rs:75-81) given the head's
+// statistics: p_j = RNE(e_j * 2^14 / S) (or the uniform split when S == 0,
+// softmax.rs:42-63), then sum_j p_j v_j per dimension in i64, added to
+// acc[0 .. HD) with 64-bit atomics (exact, order-free).  vv holds the chunk's
+// V pairs (dec_load_v).  Whole block (256 threads).
+template <int HD>
+struct DecV {
+    static constexpr int TPR = HD / 2;           // threads per V row (one dim pair each)
+    static constexpr int STREAMS = 256 / TPR;    // position streams per block
+    static constexpr int PER = kChunk / STREAMS; // positions per stream
+    uint32_t vv[PER];
+};
+
+template <int HD>
+__device__ inline void dec_load_v(int L, int base, const int16_t* __restrict__ vg, DecV<HD>& v) {
+    const int n = min(kChunk, L - base);
+    const int dp = threadIdx.x % DecV<HD>::TPR, stream = threadIdx.x / DecV<HD>::TPR;
+#pragma unroll
+    for (int i = 0; i < DecV<HD>::PER; ++i) {
+        const int t = stream + i * DecV<HD>::STREAMS;
+        v.vv[i] = t < n ? *reinterpret_cast<const uint32_t*>(vg + (size_t)(base + t) * HD + 2 * dp) : 0u;
+    }
+}
+
+template <int HD>
+__device__ inline void dec_pv_chunk(int L, int base, const int32_t* __restrict__ z, const DecV<HD>& v,
+                                    const int16_t* __restrict__ lut, uint32_t lut_len, uint8_t lut_shift, int32_t mx,
+                                    int32_t S, unsigned long long* __restrict__ acc) {
+    constexpr int STREAMS = DecV<HD>::STREAMS, PER = DecV<HD>::PER;
+    const int n = min(kChunk, L - base);
+    __shared__ int32_t p[kChunk];
+    __shared__ int64_t red[STREAMS][HD];
+    const int dp = threadIdx.x % DecV<HD>::TPR, stream = threadIdx.x / DecV<HD>::TPR;
+    const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
+    const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
+    if (threadIdx.x < kChunk) {
+        const int t = threadIdx.x;
+        int32_t pv = 0;
+        if (t < n) {
+            if (S == 0) {
+                const uint64_t rl = recip32((uint32_t)L);
+                uint32_t qq, rr;
+                udivmod32((uint32_t)one, (uint32_t)L, rl, &qq, &rr);
+                const int32_t ubase = (int32_t)qq;
+                const int32_t urem = wsub32(one, wmul32(ubase, L));
+                pv = ubase + (((uint64_t)(base + t) < (uint64_t)(int64_t)urem) ? 1 : 0);
+            } else {
+                const uint64_t rs = recip32(S < 0 ? 0u - (uint32_t)S : (uint32_t)S);
+                const int32_t e = exp_lookup(sat_sub32(mx, z[base + t]), lut, lut_len, lut_shift, lut_one);
+                pv = softmax_div_round(wmul32(e, one), S, rs);
+            }
+        }
+        p[t] = pv;
+    }
+    __syncthreads();
+    int64_t a0 = 0, a1 = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int64_t pv = p[stream + i * STREAMS];
+        a0 = wadd64(a0, pv * (int64_t)(int16_t)(v.vv[i] & 0xFFFFu));
+        a1 = wadd64(a1, pv * (int64_t)(int16_t)(v.vv[i] >> 16));
+    }
+    red[stream][2 * dp] = a0;
+    red[stream][2 * dp + 1] = a1;
+    __syncthreads();
+    if (threadIdx.x < HD) {
+        int64_t sum = 0;
+#pragma unroll
+        for (int k = 0; k < STREAMS; ++k) sum = wadd64(sum, red[k][threadIdx.x]);
+        atomicAdd(acc + threadIdx.x, (unsigned long long)sum);
+    }
+}
+
+// Statistics and P.V of one chunk in one block: every block of a head
+// recomputes the head's statistics over all L scores (cheap for one row;
+// the V loads are in flight meanwhile).
+template <int HD>
+__device__ inline void dec_pv(int L, int base, const int32_t* __restrict__ z, const int16_t* __restrict__ vg,
+                              const int16_t* __restrict__ lut, uint32_t lut_len, uint8_t lut_shift,
+                              unsigned long long* __restrict__ acc) {
+    DecV<HD> v;
+    dec_load_v<HD>(L, base, vg, v);
+    int32_t mx, S;
+    dec_stats(L, z, lut, lut_len, lut_shift, mx, S);
+    dec_pv_chunk<HD>(L, base, z, v, lut, lut_len, lut_shift, mx, S, acc);
+}
+
+}  // namespace myl

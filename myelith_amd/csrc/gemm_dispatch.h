@@ -116,7 +116,10 @@ template <class Epi>
 inline hipError_t mm_planes(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, const MmCtx* mm,
                             hipStream_t st) {
     const int cus = mm->cus;
-    // few rows: partial sums cost little, so K is split until every CU has work
+    // few rows: partial sums cost little, so K is split until every CU has
+    // work (up to 16 tokens: one 32-row plane tile, and K split for up to two
+    // items per CU, 5-10% faster on MI355X than 64-row tiles)
+    if (M <= 16) return mm2_launch_splitk<1, 1, 1, 4, 4>(Ap, M, W, N, K, epi, mm, 2 * cus, st);
     if (M <= 32) return mm2_launch_splitk<2, 1, 1, 4, 4>(Ap, M, W, N, K, epi, mm, cus, st);
     if (M > 64 && mm_wide_tiles(M, N, K, cus)) return mm2_launch<2, 2, 4, 4, 2, 128>(Ap, M, W, N, K, epi, st);
     if (M > 64 && mm2_tiles<2, 2, 4, 2, 3>(M, N) >= cus) return mm2_launch<2, 2, 4, 2, 3>(Ap, M, W, N, K, epi, st);

@@ -61,9 +61,12 @@ struct Mm2 {
     static constexpr int kSwzRows = 256 / KS;  // rows sharing one swizzle slot
     static constexpr int kStageBytes = (BR + BN) * KS;
     static constexpr size_t kLds = (size_t)STAGES * kStageBytes;
-    static constexpr int kChunks = (BR + BN) * kCpr;       // 16-byte chunks per stage
-    static constexpr int kLoads = kChunks / kThreads;      // per thread per stage
-    static_assert(kChunks % kThreads == 0, "whole wave loads");
+    // 1 KiB wave loads per stage, dealt round-robin to the waves: every wave
+    // issues kLoadsMin or kLoadsMax of them
+    static constexpr int kGroups = (BR + BN) / kRowsPerLoad;
+    static constexpr int kLoadsMin = kGroups / (kThreads / 64);
+    static constexpr int kLoadsMax = (kGroups + kThreads / 64 - 1) / (kThreads / 64);
+    static_assert((BR + BN) % kRowsPerLoad == 0, "whole 1 KiB loads");
     __device__ static int slot(int row, int chunk) { return chunk ^ ((row / kSwzRows) & (kCpr - 1)); }
 };
 
@@ -87,8 +90,9 @@ __device__ inline void mm2_main(const int8_t* __restrict__ Ap, int R2, const int
     auto issue = [&](int kt, int buf) {
         int8_t* st = lds + buf * S::kStageBytes;
 #pragma unroll
-        for (int i = 0; i < S::kLoads; ++i) {
+        for (int i = 0; i < S::kLoadsMax; ++i) {
             const int grp = wave + i * (S::kThreads / 64);   // 1 KiB row-group index in the stage
+            if (i >= S::kLoadsMin && grp >= S::kGroups) break;  // wave-uniform
             const int row = grp * S::kRowsPerLoad + lane / S::kCpr;  // stage row: A' rows first
             const int chunk = S::slot(row, lane & (S::kCpr - 1));
             const int8_t* src;
@@ -115,8 +119,10 @@ __device__ inline void mm2_main(const int8_t* __restrict__ Ap, int R2, const int
     for (int s = 0; s < STAGES - 1; ++s)
         if (s < nk) issue(s, s);
     for (int kt = 0; kt < nk; ++kt) {
-        // stage kt complete: later stages may still be in flight
-        if (kt + STAGES - 2 < nk) __builtin_amdgcn_s_waitcnt(waitcnt_vm(S::kLoads * (STAGES - 2)));
+        // stage kt complete: later stages may still be in flight (loads
+        // retire in order; a wave with kLoadsMax loads per stage waits for
+        // a few of the next stage's too)
+        if (kt + STAGES - 2 < nk) __builtin_amdgcn_s_waitcnt(waitcnt_vm(S::kLoadsMin * (STAGES - 2)));
         else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
         __syncthreads();
         if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);

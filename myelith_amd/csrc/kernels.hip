@@ -104,7 +104,7 @@ __global__ __launch_bounds__(kRmsThreads) void rmsnorm_fast_kernel(const int16_t
     }
 }
 
-// Many rows: 256 threads per row, each thread owning PER chunks of 8
+// 256 threads per row, each thread owning PER chunks of 8
 // consecutive elements loaded as one 16-byte (x) and 8-byte (shifts, gamma)
 // vector each; rows of n % 8 == 0 elements, 16-byte aligned.  The sum of
 // squares stays in 64 bits for elements at the largest shift (align 0) and
@@ -205,14 +205,14 @@ inline int rms_rows_per(int n) {
     return nc <= kRowsThreads ? 1 : nc <= 2 * kRowsThreads ? 2 : nc <= 4 * kRowsThreads ? 4 : 0;
 }
 
-// Row kernel launch when M rows fill the chip and the layout allows it.
+// Row kernel launch when the layout allows it.
 bool rmsnorm_rows(const int16_t* x, int M, int ldx, const uint8_t* xs, const int8_t* g, const uint8_t* gs, int n,
                   const RmsParams& p, uint8_t out_frac, int16_t* out, int ldo, int8_t* planes, hipStream_t st) {
     const int per = rms_rows_per(n);
     const bool aligned = ((uintptr_t)x % 16 == 0) && ldx % 8 == 0 && ((uintptr_t)xs % 8 == 0) &&
                          ((uintptr_t)g % 8 == 0) && ((uintptr_t)gs % 8 == 0) &&
                          (planes ? (uintptr_t)planes % 8 == 0 : ((uintptr_t)out % 16 == 0 && ldo % 8 == 0));
-    if (M < 256 || per == 0 || !aligned) return false;
+    if (M < 1 || per == 0 || !aligned) return false;
     if (per == 1)
         rmsnorm_rows_kernel<1><<<M, kRowsThreads, 0, st>>>(x, ldx, xs, g, gs, n, p, out_frac, out, ldo, planes);
     else if (per == 2)

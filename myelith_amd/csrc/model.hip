@@ -31,6 +31,7 @@
 #include "gemv.h"
 #include "gemv_stream.h"
 #include "ops.h"
+#include "dec_attn.h"
 #include "../../include/myl_synth.h"
 #include "model_internal.h"
 
@@ -43,7 +44,6 @@ using namespace myl;
 
 namespace {
 
-constexpr int kChunk = 64;           // attention positions per block
 
 
 
@@ -108,68 +108,6 @@ __device__ inline void block_sum_limbs(uint64_t (&l)[3], uint64_t* red /* [16][3
         }
 }
 
-__device__ inline uint32_t bitlen128(myl_u128 v) {
-    const uint64_t hi = (uint64_t)(v >> 64), lo = (uint64_t)v;
-    return hi ? 128u - (uint32_t)__builtin_clzll(hi) : (lo ? 64u - (uint32_t)__builtin_clzll(lo) : 0u);
-}
-
-// The same factor in 64-bit arithmetic when the sum and m = (sum * inv_n) >> 20
-// fit (always, for int16 inputs with fractional-bit spreads below 16): the
-// i128 emulation is the slow part of the serial setup every block runs.
-__device__ inline bool rms_factor_u64(myl_i128 acc, uint8_t ref, const RmsParams& p, RmsFactor& f) {
-    const uint64_t hi = (uint64_t)((myl_u128)acc >> 64), lo = (uint64_t)acc;
-    if (hi != 0 || (lo >> 63) != 0) return false;
-    const uint64_t ph = __umul64hi(lo, (uint64_t)p.inv_n_q20), pl = lo * (uint64_t)p.inv_n_q20;
-    if ((ph >> 20) != 0 || p.inv_n_q20 < 0) return false;
-    f.ref_shift = ref;
-    f.zero = lo == 0;
-    f.lut_val = 0;
-    f.norm_frac = 0;
-    if (!f.zero) {
-        const uint64_t m = (ph << 44) | (pl >> 20);
-        const uint64_t max_idx = (uint64_t)(p.lut_len - 1);
-        uint32_t q = 0;
-        if (m > 0) {
-            const uint32_t bm = 64u - (uint32_t)__builtin_clzll(m), bi = 64u - (uint32_t)__builtin_clzll(max_idx | 1u);
-            if (bm > bi + 2) q = (bm - bi - 2) & ~1u;
-        }
-        while ((m >> q) > max_idx) q += 2;
-        int64_t idx = rshift_round64((int64_t)m, (uint8_t)q);
-        if (idx > (int64_t)max_idx) idx = (int64_t)max_idx;
-        f.lut_val = (int64_t)p.lut[(int)idx];
-        f.norm_frac = (uint32_t)p.lut_output_frac + (uint32_t)p.lut_input_shift / 2u + q / 2u;
-    }
-    return true;
-}
-
-__device__ inline RmsFactor rms_factor_from_acc(myl_i128 acc, uint8_t ref, const RmsParams& p) {
-    RmsFactor f;
-    if (rms_factor_u64(acc, ref, p, f)) return f;
-    f.ref_shift = ref;
-    f.zero = acc == 0;
-    f.lut_val = 0;
-    f.norm_frac = 0;
-    if (!f.zero) {
-        const myl_i128 m = shr128((myl_i128)((myl_u128)acc * (myl_u128)(myl_i128)p.inv_n_q20), 20);
-        const myl_i128 max_idx = (myl_i128)(p.lut_len - 1);
-        // rmsnorm.rs:121-123 searches the smallest even q with m >> q <= max_idx.
-        // Every q below bitlen(m) - bitlen(max_idx) fails the test, so the
-        // search may start just under that bound (same q, few iterations).
-        uint32_t q = 0;
-        if (m > 0) {
-            const uint32_t bm = bitlen128((myl_u128)m), bi = bitlen128((myl_u128)max_idx);
-            if (bm > bi + 2) q = (bm - bi - 2) & ~1u;
-        }
-        while (shr128(m, q) > max_idx) q += 2;
-        myl_i128 idx = rshift_round128(m, q);
-        if (idx > max_idx) idx = max_idx;
-        if (idx < 0) idx = 0;
-        f.lut_val = (int64_t)p.lut[(int)idx];
-        f.norm_frac = (uint32_t)p.lut_output_frac + (uint32_t)p.lut_input_shift / 2u + q / 2u;
-    }
-    return f;
-}
-
 // Writes the norm sum of an n-vector computed by one block into slot 0 of acc
 // (the other slots are cleared): used where one block sees the whole vector.
 __device__ inline void block_seed_norm(const int16_t* x, const uint8_t* xs, uint8_t ref, int n, NormAcc* acc) {
@@ -229,7 +167,7 @@ struct SrcNorm {
             for (int j = 0; j < 3; ++j) l[j] = wave_sum_u64(acc->v[threadIdx.x][j]);
             if (threadIdx.x == 0) {
                 const myl_i128 a = (myl_i128)((myl_u128)l[0] + ((myl_u128)l[1] << 42) + ((myl_u128)l[2] << 84));
-                sf = rms_factor_from_acc(a, ref, p);
+                sf = rms_factor_of(a, ref, p);
             }
         }
         __syncthreads();
@@ -577,174 +515,35 @@ struct AttnBlock {
     __device__ AttnBlock() : h((int)blockIdx.x >> 3), c((int)blockIdx.y * 8 + ((int)blockIdx.x & 7)), g((int)blockIdx.z) {}
 };
 
-// int16 pairs -> (hi pair, lo pair) with v = 256 * hi + lo, lo in [0, 255].
-__device__ inline void split_pair(uint32_t v, uint32_t& hi, uint32_t& lo) {
-    const int32_t a = (int16_t)(v & 0xFFFFu), b = (int16_t)(v >> 16);
-    hi = ((uint32_t)(uint16_t)(int16_t)(a >> 8)) | ((uint32_t)(uint16_t)(int16_t)(b >> 8) << 16);
-    lo = (v & 0x00FF00FFu);
-}
-
-// s_j = (i32)RNE(q . k_j * mult, shift) for one query head and kChunk
-// positions (attention.rs:66-67).  LPP = HD / 8 lanes hold 16 bytes of a K
-// row each (a wave reads whole rows, coalesced); q . k is exact as
-// 256 * sum(k * q_hi) + sum(k * q_lo) on v_dot2_i32_i16 (|partials| < 2^31),
-// the row sums over the LPP lanes are DPP moves.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_scores_kernel(const DecodeState* __restrict__ st,
                                                          const int16_t* __restrict__ q, const int16_t* __restrict__ kc,
                                                          int max_pos, int G, int chunks, int64_t score_mult,
                                                          uint8_t score_shift, int32_t* __restrict__ scores) {
-    constexpr int LPP = HD / 8;
-    constexpr int PPW = 64 / LPP;                 // positions per wave per step
-    constexpr int STEPS = kChunk / 4 / PPW;       // steps per wave
-    static_assert(LPP == 8 || LPP == 16, "row sums cover 8 or 16 lanes");
     const AttnBlock b;
     if (b.c >= chunks) return;
     const int L = st->pos + 1;
     const int base = b.c * kChunk;
     if (base >= L) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane % LPP, slot = lane / LPP;
-    const int16_t* kg = kc + (size_t)b.g * max_pos * HD;
-    uint4 kv[STEPS];
-#pragma unroll
-    for (int it = 0; it < STEPS; ++it) {
-        const int j = base + wave * (kChunk / 4) + it * PPW + slot;
-        kv[it] = j < L ? *reinterpret_cast<const uint4*>(kg + (size_t)j * HD + sub * 8) : make_uint4(0, 0, 0, 0);
-    }
     const int head = b.g * G + b.h;
-    const uint4 qv = *reinterpret_cast<const uint4*>(q + (size_t)head * HD + sub * 8);
-    uint4 qh, ql;
-    split_pair(qv.x, qh.x, ql.x);
-    split_pair(qv.y, qh.y, ql.y);
-    split_pair(qv.z, qh.z, ql.z);
-    split_pair(qv.w, qh.w, ql.w);
-    typedef short __attribute__((ext_vector_type(2))) s2;
-    auto d2 = [](uint32_t a, uint32_t c, int32_t acc) {
-        return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, a), __builtin_bit_cast(s2, c), acc, false);
-    };
-#pragma unroll
-    for (int it = 0; it < STEPS; ++it) {
-        const int j = base + wave * (kChunk / 4) + it * PPW + slot;
-        int32_t ahi = 0, alo = 0;
-        ahi = d2(kv[it].x, qh.x, ahi);
-        ahi = d2(kv[it].y, qh.y, ahi);
-        ahi = d2(kv[it].z, qh.z, ahi);
-        ahi = d2(kv[it].w, qh.w, ahi);
-        alo = d2(kv[it].x, ql.x, alo);
-        alo = d2(kv[it].y, ql.y, alo);
-        alo = d2(kv[it].z, ql.z, alo);
-        alo = d2(kv[it].w, ql.w, alo);
-        if (LPP == 16) {
-            ahi = row_sum16_i32(ahi);
-            alo = row_sum16_i32(alo);
-        } else {
-            ahi = row_sum8_i32(ahi);
-            alo = row_sum8_i32(alo);
-        }
-        if (sub == 0 && j < L) {
-            const int64_t dot = (int64_t)ahi * 256 + (int64_t)alo;
-            scores[(size_t)head * max_pos + j] = (int32_t)rshift_round64(wmul64(dot, score_mult), score_shift);
-        }
-    }
+    dec_scores<HD>(L, base, q + (size_t)head * HD, kc + (size_t)b.g * max_pos * HD, score_mult, score_shift,
+                   scores + (size_t)head * max_pos);
 }
 
-// Softmax of one query head (softmax.rs:12-64) and the exact partial P.V of
-// one chunk (attention.rs:75-81).  Every block first recomputes its head's
-// statistics over all L scores -- m = max, S = wrapping i32 sum of the exp
-// LUT, the reciprocal of |S| -- then p_j = RNE(e_j * 2^14 / S) (or the
-// uniform split when S == 0) for its chunk, then sum_j p_j v_j per dimension
-// in i64, added to the accumulator with 64-bit atomics (exact, order-free).
 template <int HD>
 __global__ __launch_bounds__(256) void attn_pv_kernel(const DecodeState* __restrict__ st,
                                                      const int32_t* __restrict__ scores,
                                                      const int16_t* __restrict__ vc, int max_pos, int G, int chunks,
                                                      const int16_t* __restrict__ lut, uint32_t lut_len,
                                                      uint8_t lut_shift, unsigned long long* __restrict__ acc) {
-    constexpr int TPR = HD / 2;           // threads per V row (one dim pair each)
-    constexpr int STREAMS = 256 / TPR;    // position streams per block
-    constexpr int PER = kChunk / STREAMS; // positions per stream
-    constexpr int ZPER = 16;              // scores held in registers per thread
     const AttnBlock b;
     if (b.c >= chunks) return;
     const int L = st->pos + 1;
     const int base = b.c * kChunk;
     if (base >= L) return;
-    const int n = min(kChunk, L - base);
     const int head = b.g * G + b.h;
-    __shared__ int32_t p[kChunk];
-    __shared__ int64_t red[STREAMS][HD];
-    __shared__ int32_t redm[4];
-    __shared__ uint32_t reds[4];
-    const int dp = threadIdx.x % TPR, stream = threadIdx.x / TPR;
-    const int16_t* vg = vc + (size_t)b.g * max_pos * HD;
-    uint32_t vv[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int t = stream + i * STREAMS;
-        vv[i] = t < n ? *reinterpret_cast<const uint32_t*>(vg + (size_t)(base + t) * HD + 2 * dp) : 0u;
-    }
-    const int32_t* z = scores + (size_t)head * max_pos;
-    const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
-    const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
-    int32_t mx = INT32_MIN;
-    uint32_t s = 0;
-    if (L <= 256 * ZPER) {
-        int32_t zz[ZPER];
-#pragma unroll
-        for (int t = 0; t < ZPER; ++t) {
-            const int j = threadIdx.x + t * 256;
-            zz[t] = j < L ? z[j] : INT32_MIN;
-        }
-#pragma unroll
-        for (int t = 0; t < ZPER; ++t) mx = max(mx, zz[t]);
-        mx = block_max_i32_dpp(mx, redm);
-#pragma unroll
-        for (int t = 0; t < ZPER; ++t)
-            if (threadIdx.x + t * 256 < L) s += (uint32_t)exp_lookup(sat_sub32(mx, zz[t]), lut, lut_len, lut_shift, lut_one);
-    } else {
-        for (int j = threadIdx.x; j < L; j += 256) mx = max(mx, z[j]);
-        mx = block_max_i32_dpp(mx, redm);
-        for (int j = threadIdx.x; j < L; j += 256)
-            s += (uint32_t)exp_lookup(sat_sub32(mx, z[j]), lut, lut_len, lut_shift, lut_one);
-    }
-    const int32_t S = (int32_t)block_sum_u32_dpp(s, reds);
-    if (threadIdx.x < kChunk) {
-        const int t = threadIdx.x;
-        int32_t pv = 0;
-        if (t < n) {
-            if (S == 0) {
-                const uint64_t rl = recip32((uint32_t)L);
-                uint32_t qq, rr;
-                udivmod32((uint32_t)one, (uint32_t)L, rl, &qq, &rr);
-                const int32_t ubase = (int32_t)qq;
-                const int32_t urem = wsub32(one, wmul32(ubase, L));
-                pv = ubase + (((uint64_t)(base + t) < (uint64_t)(int64_t)urem) ? 1 : 0);
-            } else {
-                const uint64_t rs = recip32(S < 0 ? 0u - (uint32_t)S : (uint32_t)S);
-                const int32_t e = exp_lookup(sat_sub32(mx, z[base + t]), lut, lut_len, lut_shift, lut_one);
-                pv = softmax_div_round(wmul32(e, one), S, rs);
-            }
-        }
-        p[t] = pv;
-    }
-    __syncthreads();
-    int64_t a0 = 0, a1 = 0;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int64_t pv = p[stream + i * STREAMS];
-        a0 = wadd64(a0, pv * (int64_t)(int16_t)(vv[i] & 0xFFFFu));
-        a1 = wadd64(a1, pv * (int64_t)(int16_t)(vv[i] >> 16));
-    }
-    red[stream][2 * dp] = a0;
-    red[stream][2 * dp + 1] = a1;
-    __syncthreads();
-    if (threadIdx.x < HD) {
-        int64_t sum = 0;
-#pragma unroll
-        for (int k = 0; k < STREAMS; ++k) sum = wadd64(sum, red[k][threadIdx.x]);
-        atomicAdd(acc + (size_t)head * HD + threadIdx.x, (unsigned long long)sum);
-    }
+    dec_pv<HD>(L, base, scores + (size_t)head * max_pos, vc + (size_t)b.g * max_pos * HD, lut, lut_len, lut_shift,
+               acc + (size_t)head * HD);
 }
 
 // ---------------------------------------------------------------------------

@@ -59,11 +59,46 @@ struct RmsParams {
 // Norm factor of one row: everything except the per-channel output.
 struct RmsFactor { bool zero; uint8_t ref_shift; int64_t lut_val; uint32_t norm_frac; };
 
+__device__ inline uint32_t bitlen128(myl_u128 v) {
+    const uint64_t hi = (uint64_t)(v >> 64), lo = (uint64_t)v;
+    return hi ? 128u - (uint32_t)__builtin_clzll(hi) : (lo ? 64u - (uint32_t)__builtin_clzll(lo) : 0u);
+}
+
+// The same factor in 64-bit arithmetic when the sum and m = (sum * inv_n) >> 20
+// fit (always, for int16 inputs with fractional-bit spreads below 16): the
+// i128 emulation is the slow part of the serial setup every block runs.
+__device__ inline bool rms_factor_u64(myl_i128 acc, uint8_t ref, const RmsParams& p, RmsFactor& f) {
+    const uint64_t hi = (uint64_t)((myl_u128)acc >> 64), lo = (uint64_t)acc;
+    if (hi != 0 || (lo >> 63) != 0) return false;
+    const uint64_t ph = __umul64hi(lo, (uint64_t)p.inv_n_q20), pl = lo * (uint64_t)p.inv_n_q20;
+    if ((ph >> 20) != 0 || p.inv_n_q20 < 0) return false;
+    f.ref_shift = ref;
+    f.zero = lo == 0;
+    f.lut_val = 0;
+    f.norm_frac = 0;
+    if (!f.zero) {
+        const uint64_t m = (ph << 44) | (pl >> 20);
+        const uint64_t max_idx = (uint64_t)(p.lut_len - 1);
+        uint32_t q = 0;
+        if (m > 0) {
+            const uint32_t bm = 64u - (uint32_t)__builtin_clzll(m), bi = 64u - (uint32_t)__builtin_clzll(max_idx | 1u);
+            if (bm > bi + 2) q = (bm - bi - 2) & ~1u;
+        }
+        while ((m >> q) > max_idx) q += 2;
+        int64_t idx = rshift_round64((int64_t)m, (uint8_t)q);
+        if (idx > (int64_t)max_idx) idx = (int64_t)max_idx;
+        f.lut_val = (int64_t)p.lut[(int)idx];
+        f.norm_frac = (uint32_t)p.lut_output_frac + (uint32_t)p.lut_input_shift / 2u + q / 2u;
+    }
+    return true;
+}
+
 // The factor from the aligned sum of squares acc and the largest input
 // shift ref (rmsnorm.rs:96-126): mean = acc * inv_n >> 20, scaled down by
 // an even q until it indexes the rsqrt LUT.
 __device__ inline RmsFactor rms_factor_of(myl_i128 acc, uint8_t ref, const RmsParams& p) {
     RmsFactor f;
+    if (rms_factor_u64(acc, ref, p, f)) return f;
     f.ref_shift = ref;
     f.zero = acc == 0;
     f.lut_val = 0;
@@ -71,7 +106,14 @@ __device__ inline RmsFactor rms_factor_of(myl_i128 acc, uint8_t ref, const RmsPa
     if (!f.zero) {
         const myl_i128 m = shr128((myl_i128)((myl_u128)acc * (myl_u128)(myl_i128)p.inv_n_q20), 20);
         const myl_i128 max_idx = (myl_i128)(p.lut_len - 1);
+        // rmsnorm.rs:121-123 searches the smallest even q with m >> q <= max_idx.
+        // Every q below bitlen(m) - bitlen(max_idx) fails the test, so the
+        // search may start just under that bound (same q, few iterations).
         uint32_t q = 0;
+        if (m > 0) {
+            const uint32_t bm = bitlen128((myl_u128)m), bi = bitlen128((myl_u128)max_idx);
+            if (bm > bi + 2) q = (bm - bi - 2) & ~1u;
+        }
         while (shr128(m, q) > max_idx) q += 2;
         myl_i128 idx = rshift_round128(m, q);
         if (idx > max_idx) idx = max_idx;
