@@ -328,6 +328,8 @@ def main() -> int:
     ap.add_argument("--no-batch", action="store_true",
                     help="skip the batched decode, teacher-forced prefill and MoE sections")
     ap.add_argument("--no-batched-decode", action="store_true", help="skip only the batched decode section")
+    ap.add_argument("--section", choices=("prefill", "batched", "moe", "e2e"),
+                    help="run only this section (for profiling) and print its record as one JSON line")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="also run three 256 MiB device-to-device copies: the known-size kernel that calibrates "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -349,6 +351,21 @@ def main() -> int:
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
     backend.use_torch_stream()
+
+    if args.section:
+        rec = None
+        if args.section == "moe":
+            rec = moe_layer(backend, args.seed)
+        elif args.section == "e2e":
+            rec = e2e_05b(backend, args.seed)
+        else:
+            spec = make_spec(QWEN25_7B, seed=args.seed, max_pos=1024 + 8 if args.section == "prefill" else 2048 + 40)
+            model = IntegerModel(backend, spec, LutSet.for_head_dim(spec["head_dim"]))
+            rec = (teacher_forced_prefill(model, backend, args.seed) if args.section == "prefill"
+                   else batched_decode(model, args.seed))
+            model.close()
+        print(json.dumps({"section": args.section, "record": rec}), flush=True)
+        return 0
 
     total_steps = args.warmup + args.steps
     # KV capacity: the decode run, and the teacher-forced prefill (1024 positions)
