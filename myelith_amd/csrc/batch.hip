@@ -277,8 +277,8 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
     const bool planes = mm_planes_ok(R, H, mm) && mm_planes_ok(R, I, mm) && mm_planes_ok(R, nq, mm) &&
                         rmsnorm_planes_ok(H) && xvec_ok(b->X, H);
     // the gate/up product applies the SiLU and writes the down product's
-    // planes itself (lane-pair epilogue) when its tiles need no K split
-    const bool fuse_silu = planes && R > 64 && (size_t)2 * R * ((size_t)I + H) <= mm->planes_bytes;
+    // planes itself (staged epilogue) when its tiles need no K split
+    const bool fuse_silu = planes && R > 64 && I % 8 == 0 && (size_t)2 * R * ((size_t)I + H) <= mm->planes_bytes;
     const uint8_t lut_shift = MYL_TV_SCORE_FRAC_BITS - MYL_TV_EXP_INPUT_FRAC;
     hipError_t e;
     embed_rows_kernel<<<R, 256, 0, st>>>(b->rows + 3 * b->rows_cap, m->emb, m->emb_shifts, m->layers[0].res_in, H, b->X);
@@ -353,7 +353,7 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
             if ((e = rmsnorm_planes(b->X2, R, H, Ld.res_mid, Ld.post_gamma, Ld.post_gamma_s, H, m->rsqrt,
                                     m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20,
                                     f.norm_mlp_frac, xin, st)) != hipSuccess ||
-                (e = mm_planes_pair(xin, R, Ld.wgu, 2 * I, H, es, mm, st)) != hipSuccess)
+                (e = mm_planes_staged(xin, R, Ld.wgu, 2 * I, H, es, mm, st)) != hipSuccess)
                 return e;
         } else if (planes) {
             if ((e = rmsnorm_planes(b->X2, R, H, Ld.res_mid, Ld.post_gamma, Ld.post_gamma_s, H, m->rsqrt,

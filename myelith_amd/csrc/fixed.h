@@ -114,6 +114,28 @@ MYL_FN int32_t softmax_div_round(int32_t num, int32_t s, uint64_t recip) {
     return q;
 }
 
+// softmax_div_round for 0 <= num < 2^31 and s >= 1 with one 32-bit reciprocal
+// m = min(floor(2^32 / s), 2^32 - 1): q0 = (num * m) >> 32 is q or q - 1
+// (num * m / 2^32 > num / s - 1 for num < 2^32), one correction gives the
+// truncating quotient and remainder, then the same half-even step with the
+// same wrapping i32 doubling of the remainder.
+MYL_FN uint32_t recip32_u32(uint32_t s) {
+    const uint64_t m = recip32(s);
+    return m > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)m;
+}
+MYL_FN int32_t softmax_div_round_pos(int32_t num, int32_t s, uint32_t m) {
+    const uint32_t un = (uint32_t)num, us = (uint32_t)s;
+    uint32_t q = (uint32_t)(((uint64_t)un * m) >> 32);
+    uint32_t r = un - q * us;
+    if (r >= us) {
+        q += 1;
+        r -= us;
+    }
+    const int32_t twice = wmul32((int32_t)r, 2);
+    if (twice > s || (twice == s && (q & 1u))) return wadd32((int32_t)q, 1);
+    return (int32_t)q;
+}
+
 // Unsigned 32-bit n % d without a hardware divide (small loops only: LUT row
 // selection pos % n_pos, done once per launch).
 MYL_FN uint32_t umod32_slow(uint32_t n, uint32_t d) {

@@ -126,14 +126,14 @@ inline hipError_t mm_planes(const int8_t* Ap, int M, const int8_t* W, int N, int
     return mm2_launch_splitk<2, 1, 2, 4, 4>(Ap, M, W, N, K, epi, mm, cus / 2, st);
 }
 
-// The gate/up product with the lane-pair epilogue (EpiGUSiluPlanes), for
-// more than 64 rows: the tiles of mm_planes without a K split.
+// The gate/up product with the staged epilogue (EpiGUSiluPlanes), for more
+// than 64 rows and N % 16 == 0: the tiles of mm_planes without a K split.
 template <class Epi>
-inline hipError_t mm_planes_pair(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi,
-                                 const MmCtx* mm, hipStream_t st) {
-    if (M <= 64 || N % 2 != 0 || K % 64 != 0) return hipErrorInvalidValue;
-    if (mm_wide_tiles(M, N, K, mm->cus)) return mm2_pair_launch<2, 2, 4, 4, 2, 128>(Ap, M, W, N, K, epi, st);
-    return mm2_pair_launch<2, 2, 4, 2, 3, 64>(Ap, M, W, N, K, epi, st);
+inline hipError_t mm_planes_staged(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi,
+                                   const MmCtx* mm, hipStream_t st) {
+    if (M <= 64 || N % 16 != 0 || K % 64 != 0) return hipErrorInvalidValue;
+    if (mm_wide_tiles(M, N, K, mm->cus)) return mm2_staged_launch<2, 2, 4, 4, 2, 128>(Ap, M, W, N, K, epi, st);
+    return mm2_staged_launch<2, 2, 4, 2, 3, 64>(Ap, M, W, N, K, epi, st);
 }
 
 // Tile and K split, from a sweep of the W8A16 shapes on MI355X: 64-row tiles

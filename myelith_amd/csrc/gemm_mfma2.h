@@ -195,13 +195,19 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_kernel(const int8_t* __res
     mm2_tile<MB, NB, WM_, WN_, STAGES, KS>(Ap, R2, W, N, K, 0, K, (int)tr * S::BR, (int)tn * S::BN, lds, SinkEpi<Epi>{epi});
 }
 
-// As mm2_kernel, with an epilogue over lane pairs (columns 2i, 2i+1 of one
-// row): Epi::pair(n, m, sum, valid) is called by all lanes together.
+// As mm2_kernel, with a staged epilogue for products whose output columns
+// pair up (2i, 2i+1 -> element i of an output row): every accumulator value
+// is first reduced to an int16 by Epi::stage(n, sum) and parked in LDS as a
+// [BR/2 x BN] tile (the K stages are free by then); the block then hands
+// Epi::emit(m, i0, v) the 16 staged values of columns 2 i0 .. 2 i0 + 15 of
+// row m, for 8-column chunks of N / 2 (N % 16 == 0), so the outputs leave in
+// whole 8-byte pieces.
 template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class Epi>
-__global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_pair_kernel(const int8_t* __restrict__ Ap, int R2,
-                                                                  const int8_t* __restrict__ W, int N, int K,
-                                                                  Divider tiles_r, int ntiles, Epi epi) {
+__global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_staged_kernel(const int8_t* __restrict__ Ap, int R2,
+                                                                    const int8_t* __restrict__ W, int N, int K,
+                                                                    Divider tiles_r, int ntiles, Epi epi) {
     using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
+    static_assert((size_t)(S::BR / 2) * S::BN * 2 <= S::kLds, "staged tile fits the stage buffers");
     extern __shared__ __align__(16) int8_t lds[];
     const int t = mm_tile_index(ntiles);
     if (t < 0) return;
@@ -216,26 +222,41 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_pair_kernel(const int8_t* 
     mm2_main<MB, NB, WM_, WN_, STAGES, KS>(Ap, R2, W, N, K, 0, K, r0, n0, lds, acc, rs);
 #pragma unroll
     for (int j = 0; j < NB; ++j) rs[j] += __shfl_xor(rs[j], 32);
+    __syncthreads();  // every wave is past its last stage read
+    int16_t* tile = reinterpret_cast<int16_t*>(lds);  // [BR / 2][BN]
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            const int n = n0 + (wn * NB + j) * 32 + (lane & 31);
+            const int nl = (wn * NB + j) * 32 + (lane & 31);
+            const int n = n0 + nl;
 #pragma unroll
             for (int r = 0; r < 16; r += 2) {
-                const int arow = r0 + (wm * MB + i) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                epi.pair(n, arow >> 1, (int64_t)acc[i][j][r] * 256 + (int64_t)acc[i][j][r + 1] + (int64_t)rs[j] * 128,
-                         arow < R2 && n < N);
+                const int arl = (wm * MB + i) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                int16_t v = 0;
+                if (r0 + arl < R2 && n < N)
+                    v = epi.stage(n, (int64_t)acc[i][j][r] * 256 + (int64_t)acc[i][j][r + 1] + (int64_t)rs[j] * 128);
+                tile[(arl >> 1) * S::BN + nl] = v;
             }
         }
+    __syncthreads();
+    constexpr int kChunks = S::BN / 16;  // 8-column output chunks per tile row
+    const int m0 = r0 >> 1, i00 = n0 >> 1;
+    for (int c = threadIdx.x; c < (S::BR / 2) * kChunks; c += S::kThreads) {
+        const int ml = c / kChunks, ic = c % kChunks;  // powers of two
+        const int m = m0 + ml, i0 = i00 + ic * 8;
+        if (2 * m >= R2 || 2 * i0 >= N) continue;
+        const uint4* src = reinterpret_cast<const uint4*>(tile + ml * S::BN + ic * 16);
+        epi.emit(m, i0, src[0], src[1]);
+    }
 }
 
 template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class Epi>
-hipError_t mm2_pair_launch(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, hipStream_t st) {
+hipError_t mm2_staged_launch(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, hipStream_t st) {
     using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     const int R2 = 2 * M;
     const int tiles_r = (R2 + S::BR - 1) / S::BR, ntiles = tiles_r * ((N + S::BN - 1) / S::BN);
-    auto kern = mm2_pair_kernel<MB, NB, WM_, WN_, STAGES, KS, Epi>;
+    auto kern = mm2_staged_kernel<MB, NB, WM_, WN_, STAGES, KS, Epi>;
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
     if (e != hipSuccess) return e;
     kern<<<8 * ((ntiles + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, R2, W, N, K, Divider::of((uint32_t)tiles_r), ntiles, epi);

@@ -131,30 +131,53 @@ __global__ __launch_bounds__(kAttnThreads) void rows_qk_kernel(
     int8_t* kl = kh + sub * S;
     constexpr int CH = HD / 8;  // 16-byte chunks per vector (a power of two)
     constexpr int CH_LOG = HD == 128 ? 4 : 3;
-    // Whole CH-lane rows are active together (the loop bounds are multiples
-    // of CH), so the row sums see every chunk of a vector.
-    for (int t = tid; t < MT * 32 * CH; t += kAttnThreads) {
-        const int v = t >> CH_LOG, c = t & (CH - 1);
-        uint4 x = make_uint4(0, 0, 0, 0);
-        if (v < QV) x = *reinterpret_cast<const uint4*>(Q + (size_t)qv.row[v] * nq + (size_t)qv.head[v] * HD + c * 8);
-        uint2 h, l;
-        split_planes8(x, h, l);
-        *reinterpret_cast<uint2*>(qh + v * S + c * 8) = h;
-        *reinterpret_cast<uint2*>(ql + v * S + c * 8) = l;
-        const int32_t sv = chunk_row_sum<CH>(sum8_i16(x));
-        if (c == 0 && v < QV) q_sum[v] = sv;
+    // Whole CH-lane rows are active together (the bounds are multiples of
+    // 64 lanes), so the row sums see every chunk of a vector.  Each staging
+    // pass issues all of a thread's loads before using any.
+    constexpr int kQit = kAttnQV * CH / kAttnThreads;   // Q chunks per thread
+    constexpr int kKit = 128 * CH / kAttnThreads;       // K chunks per thread (sub <= 128)
+    {
+        uint4 qx[kQit];
+#pragma unroll
+        for (int i = 0; i < kQit; ++i) {
+            const int t = tid + i * kAttnThreads;
+            const int v = t >> CH_LOG, c = t & (CH - 1);
+            qx[i] = v < QV ? *reinterpret_cast<const uint4*>(Q + (size_t)qv.row[v] * nq + (size_t)qv.head[v] * HD + c * 8)
+                           : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < kQit; ++i) {
+            const int t = tid + i * kAttnThreads;
+            if (t >= MT * 32 * CH) break;  // wave-uniform
+            const int v = t >> CH_LOG, c = t & (CH - 1);
+            uint2 h, l;
+            split_planes8(qx[i], h, l);
+            *reinterpret_cast<uint2*>(qh + v * S + c * 8) = h;
+            *reinterpret_cast<uint2*>(ql + v * S + c * 8) = l;
+            const int32_t sv = chunk_row_sum<CH>(sum8_i16(qx[i]));
+            if (c == 0 && v < QV) q_sum[v] = sv;
+        }
     }
     const int16_t* kg = kc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD;
     for (int js = j0; js < jend; js += sub) {
-        for (int t = tid; t < sub * CH; t += kAttnThreads) {
+        uint4 kx[kKit];
+#pragma unroll
+        for (int i = 0; i < kKit; ++i) {
+            const int t = tid + i * kAttnThreads;
+            const int j = js + (t >> CH_LOG), c = t & (CH - 1);
+            kx[i] = t < sub * CH && j < max_pos ? *reinterpret_cast<const uint4*>(kg + (size_t)j * HD + c * 8)
+                                                : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < kKit; ++i) {
+            const int t = tid + i * kAttnThreads;
+            if (t >= sub * CH) break;  // wave-uniform
             const int p = t >> CH_LOG, c = t & (CH - 1);
-            const int j = js + p;
-            const uint4 x = j < max_pos ? *reinterpret_cast<const uint4*>(kg + (size_t)j * HD + c * 8) : make_uint4(0, 0, 0, 0);
             uint2 h, l;
-            split_planes8(x, h, l);
+            split_planes8(kx[i], h, l);
             *reinterpret_cast<uint2*>(kh + p * S + c * 8) = h;
             *reinterpret_cast<uint2*>(kl + p * S + c * 8) = l;
-            const int32_t sk = chunk_row_sum<CH>(sum8_i16(x));
+            const int32_t sk = chunk_row_sum<CH>(sum8_i16(kx[i]));
             if (c == 0) k_sum[p] = sk;
         }
         __syncthreads();
@@ -211,6 +234,7 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
     __shared__ AttnQv qv;
     __shared__ int32_t q_m[kAttnQV], q_s[kAttnQV], q_ub[kAttnQV], q_ur[kAttnQV];
     __shared__ uint64_t q_rs[kAttnQV];
+    __shared__ uint32_t q_r32[kAttnQV];
     __shared__ int32_t p_sum[kAttnQV], v_sum[HD];
     __shared__ int s_pmax;
     const int g = blockIdx.y, range = blockIdx.z, j0 = range * kAttnRange;
@@ -232,6 +256,7 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
             q_m[tid] = stats[si];
             q_s[tid] = S;
             q_rs[tid] = recip32(S < 0 ? 0u - (uint32_t)S : (uint32_t)S);
+            q_r32[tid] = S > 0 ? recip32_u32((uint32_t)S) : 0u;
             const uint32_t L = (uint32_t)qv.pos[tid] + 1u;
             uint32_t qq, rr;
             udivmod32((uint32_t)one, L, recip32(L), &qq, &rr);
@@ -241,17 +266,44 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
     }
     if (tid < HD) v_sum[tid] = 0;
     __syncthreads();
+    // Every score load of the wave and every V load of the thread is issued
+    // before any of them is used (one memory latency instead of one per
+    // vector and per item).
+    constexpr int kVpw = kAttnQV / (kAttnThreads / 64);      // vectors per wave
+    constexpr int kVit = (CH * 64 + kAttnThreads - 1) / kAttnThreads;  // V items per thread
+    const int q4 = lane, jb = j0 + 4 * q4;
+    int4 zv[kVpw];
+#pragma unroll
+    for (int i = 0; i < kVpw; ++i) {
+        const int v = wave + i * (kAttnThreads / 64);
+        zv[i] = make_int4(0, 0, 0, 0);
+        if (q4 < 8 * nk && v < QV && jb <= qv.pos[v])
+            zv[i] = *reinterpret_cast<const int4*>(scores + ((size_t)qv.row[v] * heads + qv.head[v]) * lcap + jb);
+    }
+    const int16_t* vg = vc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD;
+    uint4 vw[kVit][4];
+#pragma unroll
+    for (int i = 0; i < kVit; ++i) {
+        const int t = tid + i * kAttnThreads;
+        const int c = t & (CH - 1), vq4 = t >> CH_LOG;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int j = j0 + 4 * vq4 + k;
+            vw[i][k] = t < CH * 8 * nk && j < max_pos ? *reinterpret_cast<const uint4*>(vg + (size_t)j * HD + c * 8)
+                                                      : make_uint4(0, 0, 0, 0);
+        }
+    }
     // P planes [vector][position]: a wave per vector, its lanes over the
     // range's 4-position groups (8 * nk <= 64 of them)
-    for (int v = wave; v < MT * 32; v += kAttnThreads / 64) {
-        const int q4 = lane;
-        const int jb = j0 + 4 * q4;
+#pragma unroll
+    for (int i = 0; i < kVpw; ++i) {
+        const int v = wave + i * (kAttnThreads / 64);
+        if (v >= MT * 32) break;  // wave-uniform
         uint32_t hw = 0, lw = 0x80808080u;  // p = 0: hi 0, lo' -128
         int32_t ps = 0;
         if (q4 < 8 * nk && v < QV && jb <= qv.pos[v]) {
             const int pos = qv.pos[v];
-            const int4 z = *reinterpret_cast<const int4*>(scores + ((size_t)qv.row[v] * heads + qv.head[v]) * lcap + jb);
-            const int32_t zz[4] = {z.x, z.y, z.z, z.w};
+            const int32_t zz[4] = {zv[i].x, zv[i].y, zv[i].z, zv[i].w};
             lw = 0;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -262,7 +314,10 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
                         p = q_ub[v] + (((uint64_t)j < (uint64_t)(int64_t)q_ur[v]) ? 1 : 0);
                     } else {
                         const int32_t e = exp_lookup(sat_sub32(q_m[v], zz[k]), lut, lut_len, lut_shift, lut_one);
-                        p = softmax_div_round(wmul32(e, one), q_s[v], q_rs[v]);
+                        // e * 2^14 >= 0 (a non-negative exp table); the
+                        // sum is positive unless it wrapped
+                        p = q_s[v] > 0 ? softmax_div_round_pos(wmul32(e, one), q_s[v], q_r32[v])
+                                       : softmax_div_round(wmul32(e, one), q_s[v], q_rs[v]);
                     }
                 }
                 ps += p;
@@ -278,15 +333,12 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
         if (lane == 0) p_sum[v] = ps;
     }
     // V planes transposed to [dimension][position]: 8 dimensions x 4 positions per item
-    const int16_t* vg = vc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD;
-    for (int t = tid; t < CH * 8 * nk; t += kAttnThreads) {
-        const int c = t & (CH - 1), q4 = t >> CH_LOG;
-        uint4 w[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int j = j0 + 4 * q4 + k;
-            w[k] = j < max_pos ? *reinterpret_cast<const uint4*>(vg + (size_t)j * HD + c * 8) : make_uint4(0, 0, 0, 0);
-        }
+    for (int i = 0; i < kVit; ++i) {
+        const int t = tid + i * kAttnThreads;
+        if (t >= CH * 8 * nk) break;
+        const int c = t & (CH - 1), vq4 = t >> CH_LOG;
+        const uint4 (&w)[4] = vw[i];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             uint32_t hw = 0, lw = 0;
@@ -300,9 +352,9 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
                 lw |= ((uint32_t)((x & 255) - 128) & 0xFFu) << (8 * k);
             }
             const int d = c * 8 + e;
-            // 16-byte position chunk (q4 >> 2) at slot chunk ^ (d >> 3): rows
+            // 16-byte position chunk (vq4 >> 2) at slot chunk ^ (d >> 3): rows
             // eight apart no longer share banks
-            const int off = (((q4 >> 2) ^ (c & 15)) << 4) + 4 * (q4 & 3);
+            const int off = (((vq4 >> 2) ^ (c & 15)) << 4) + 4 * (vq4 & 3);
             *reinterpret_cast<uint32_t*>(vh + d * RS + off) = hw;
             *reinterpret_cast<uint32_t*>(vl + d * RS + off) = lw;
             atomicAdd(&v_sum[d], vs);

@@ -88,27 +88,31 @@ __device__ inline int32_t silu_mul(int16_t g, int16_t u, const int16_t* __restri
 }
 
 // The gate/up product fused with the SiLU gate and the byte-plane split of
-// its output: weight rows 2i (gate) and 2i+1 (up) land in lanes l and l ^ 1
-// of the accumulator layout, so a DPP swap hands the even lane both values,
-// and h_i of row m goes straight to planes[2m][i] (hi) and
-// planes[2m+1][i] (lo'), the down product's operand [2M x I].  pair() must
-// be called by every lane of the wave together; `valid` marks lanes whose
-// (n, m) lies inside the product.
+// its output (mm2_staged_kernel): weight rows 2i (gate) and 2i+1 (up) are
+// requantized to their own fracs, staged, and each 8-element chunk of
+// h = silu(g) * u leaves as one 8-byte hi row piece (planes[2m][i0..]) and one
+// lo' piece (planes[2m+1][i0..]) of the down product's operand [2M x I]
+// (I % 8 == 0).
 struct EpiGUSiluPlanes {
     const uint8_t* shifts;
     uint8_t act_frac, gate_frac, up_frac, down_in_frac;
     const int16_t* silu; uint32_t silu_len;
     int8_t* planes; int I;
-    __device__ inline void pair(int n, int m, int64_t acc, bool valid) const {
-        int32_t v = 0;
-        if (valid) v = clamp_i16_i64(rescale64(acc, (uint8_t)(shifts[n] + act_frac), (n & 1) ? up_frac : gate_frac));
-        const int32_t o = dpp_mov<dpp::kXor1>(v);
-        if (valid && (n & 1) == 0) {
-            const int32_t h = silu_mul((int16_t)v, (int16_t)o, silu, silu_len, gate_frac, up_frac, down_in_frac);
-            const int i = n >> 1;
-            planes[(size_t)(2 * m) * I + i] = (int8_t)(h >> 8);
-            planes[(size_t)(2 * m + 1) * I + i] = (int8_t)((h & 255) - 128);
+    __device__ inline int16_t stage(int n, int64_t acc) const {
+        return clamp_i16_i64(rescale64(acc, (uint8_t)(shifts[n] + act_frac), (n & 1) ? up_frac : gate_frac));
+    }
+    __device__ inline void emit(int m, int i0, const uint4& a, const uint4& b) const {
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};  // (g, u) pairs
+        uint32_t hi[2] = {0, 0}, lo[2] = {0, 0};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int32_t h = silu_mul((int16_t)(w[k] & 0xFFFFu), (int16_t)(w[k] >> 16), silu, silu_len, gate_frac,
+                                       up_frac, down_in_frac);
+            hi[k >> 2] |= ((uint32_t)(h >> 8) & 0xFFu) << (8 * (k & 3));
+            lo[k >> 2] |= ((uint32_t)((h & 255) - 128) & 0xFFu) << (8 * (k & 3));
         }
+        *reinterpret_cast<uint2*>(planes + (size_t)(2 * m) * I + i0) = make_uint2(hi[0], hi[1]);
+        *reinterpret_cast<uint2*>(planes + (size_t)(2 * m + 1) * I + i0) = make_uint2(lo[0], lo[1]);
     }
 };
 

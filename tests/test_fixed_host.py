@@ -1,0 +1,73 @@
+"""The device fixed-point helpers of csrc/fixed.h, compiled for the host with
+hipcc and checked against their general forms (no GPU needed).
+
+softmax_div_round_pos (the probability division of the matrix-core
+attention, softmax.rs:50-63 for a non-negative numerator and a positive sum,
+with a 32-bit reciprocal) must equal softmax_div_round (the general signed
+form, itself pinned against exact rational rounding in test_oracle_pins.py)
+on edge cases -- s = 1, 2, near 2^31, ties, remainders whose doubling wraps
+in i32 -- and on a million seeded pairs."""
+from __future__ import annotations
+
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+SRC = r"""
+#include <hip/hip_runtime.h>
+#include <cstdio>
+#include <cstdint>
+#include "fixed.h"
+static uint64_t sm = 0x9E3779B97F4A7C15ull;
+static uint64_t next() {
+    uint64_t z = (sm += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+static long bad = 0, n = 0;
+static void check(int32_t num, int32_t s) {
+    const int32_t a = softmax_div_round_pos(num, s, recip32_u32((uint32_t)s));
+    const int32_t b = softmax_div_round(num, s, recip32((uint32_t)s));
+    ++n;
+    if (a != b && bad++ < 10) printf("num=%d s=%d fast=%d general=%d\n", num, s, a, b);
+}
+int main() {
+    const int32_t ss[] = {1, 2, 3, 7, 16384, 32767, 65536, 1 << 30, (1 << 30) + 1, 2147483646, 2147483647};
+    for (int32_t s : ss) {
+        const int64_t S = s;
+        const int64_t nums[] = {0, 1, 2, S / 2, S / 2 + 1, S - 1, S, S + 1, 3 * (S / 2), 1 << 29, (1 << 29) - 1,
+                                2147483647, 2147483646, 1 << 30, (1 << 30) + 7};
+        for (int64_t num : nums)
+            if (num >= 0 && num <= 2147483647) check((int32_t)num, s);
+    }
+    for (int i = 0; i < 1000000; ++i) {
+        const uint64_t z = next();
+        const int32_t s = 1 + (int32_t)((z >> 1) % (i & 1 ? 2147483647u : 1u << (1 + (z & 30))));
+        const int32_t num = (int32_t)((next() >> 33) % (i & 2 ? 2147483648ull : (1ull << 29) + 1));
+        check(num, s);
+        // ties: num = q * s + s / 2 for even s
+        if ((s & 1) == 0 && s < (1 << 29)) check((int32_t)((uint32_t)((next() >> 40) % ((1u << 29) / (uint32_t)s + 1)) * (uint32_t)s + (uint32_t)s / 2), s);
+    }
+    printf("checked %ld, mismatches %ld\n", n, bad);
+    return bad != 0;
+}
+"""
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not Path("/opt/rocm/bin/hipcc").exists(), reason="hipcc absent")
+def test_softmax_div_round_pos_matches_general(tmp_path):
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    src = tmp_path / "t.hip"
+    src.write_text(SRC)
+    exe = tmp_path / "t"
+    subprocess.run([hipcc, "-O2", "-std=c++17", "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang",
+                    "-packed-fp32-ops", "-I", str(ROOT / "myelith_amd" / "csrc"), str(src), "-o", str(exe)],
+                   check=True, capture_output=True, timeout=300)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout
+    assert "mismatches 0" in r.stdout
