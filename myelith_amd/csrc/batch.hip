@@ -183,6 +183,74 @@ __global__ __launch_bounds__(256) void silu_planes_kernel(const int16_t* __restr
     planes[(size_t)(2 * r + 1) * I + i] = (int8_t)((h & 255) - 128);
 }
 
+// The finish of a split residual product fused with the next RMSNorm
+// (rmsnorm.rs:61-161): one block per row m takes the row's exact sums out of
+// the split-K accumulator (clearing them), applies the residual epilogue
+// (storing the new residual row) and normalises that row into the next
+// product's byte planes [2M x N].  1024 threads, PER = ceil(N / 1024).
+constexpr int kFinNormThreads = 1024;
+template <int PER>
+__global__ __launch_bounds__(kFinNormThreads) void finish_resid_norm_kernel(unsigned long long* __restrict__ acc, int N,
+                                                                EpiResidRows epi, const uint8_t* __restrict__ xs,
+                                                                const int8_t* __restrict__ g,
+                                                                const uint8_t* __restrict__ gs, RmsParams p,
+                                                                uint8_t out_frac, int8_t* __restrict__ planes) {
+    __shared__ myl_i128 red128[kFinNormThreads / 64];
+    __shared__ int32_t red32[kFinNormThreads / 64];
+    const int m = blockIdx.x;
+    int16_t xv[PER];
+    uint8_t sv[PER], gsv[PER];
+    int8_t gv[PER];
+#pragma unroll
+    for (int t = 0; t < PER; ++t) {
+        const int n = threadIdx.x + t * kFinNormThreads;
+        xv[t] = 0;
+        sv[t] = gsv[t] = 0;
+        gv[t] = 0;
+        if (n < N) {
+            unsigned long long* a = acc + (size_t)m * N + n;
+            const int64_t v = (int64_t)*a;
+            *a = 0;
+            xv[t] = epi.value(n, m, v);
+            sv[t] = xs[n];
+            gv[t] = g[n];
+            gsv[t] = gs[n];
+        }
+    }
+    const RmsFactor f = rms_factor_regs<PER>(xv, sv, p, red128, red32);
+    int8_t* ph = planes + (size_t)(2 * m) * N;
+#pragma unroll
+    for (int t = 0; t < PER; ++t) {
+        const int n = threadIdx.x + t * kFinNormThreads;
+        if (n < N) {
+            const int32_t y = rms_out(xv[t], sv[t], gv[t], gsv[t], f, out_frac);
+            ph[n] = (int8_t)(y >> 8);
+            ph[N + n] = (int8_t)((y & 255) - 128);
+        }
+    }
+}
+
+// A residual product (o_proj, down) of R rows followed by the RMSNorm of its
+// output rows into planes: fused into the finish of a split product,
+// otherwise the product then rmsnorm_planes.
+hipError_t resid_then_norm(const int8_t* Ap, int R, const int8_t* W, int N, int K, const EpiResidRows& epi,
+                           const MmCtx* mm, const uint8_t* xs, const int8_t* g, const uint8_t* gs, const myl_model* m,
+                           uint8_t out_frac, int8_t* planes, hipStream_t st) {
+    const RmsParams p{m->rsqrt, m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20};
+    auto fin = [&](unsigned long long* acc, hipStream_t s) -> hipError_t {
+        if (N <= kFinNormThreads)
+            finish_resid_norm_kernel<1><<<R, kFinNormThreads, 0, s>>>(acc, N, epi, xs, g, gs, p, out_frac, planes);
+        else
+            finish_resid_norm_kernel<4><<<R, kFinNormThreads, 0, s>>>(acc, N, epi, xs, g, gs, p, out_frac, planes);
+        return hipGetLastError();
+    };
+    bool split = false;
+    hipError_t e = N <= 4096 ? mm_planes_fin(Ap, R, W, N, K, epi, mm, st, fin, &split) : mm_planes(Ap, R, W, N, K, epi, mm, st);
+    if (e != hipSuccess || split) return e;
+    return rmsnorm_planes(epi.out, R, epi.ldo, xs, g, gs, N, m->rsqrt, m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT,
+                          MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, out_frac, planes, st);
+}
+
 // Greedy continuation: row r's next token is its argmax; positions advance.
 __global__ void rows_advance_kernel(int32_t* __restrict__ rows, int rows_cap, int R, const int64_t* __restrict__ am,
                                     uint32_t rope_rows, int64_t* __restrict__ tokens_out) {
@@ -283,6 +351,10 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
     hipError_t e;
     embed_rows_kernel<<<R, 256, 0, st>>>(b->rows + 3 * b->rows_cap, m->emb, m->emb_shifts, m->layers[0].res_in, H, b->X);
     if ((e = hipGetLastError()) != hipSuccess) return e;
+    // Without the fused gate/up (few rows), each residual product's split-K
+    // finish also normalises its rows into the next product's planes.
+    const bool norm_in_finish = planes && !fuse_silu;
+    bool in_normed = false;  // this layer's input planes were written by the previous down product
     for (int l = 0; l < (int)m->spec.layers; ++l) {
         const LayerDev& Ld = m->layers[l];
         const myl_layer_fracs& f = Ld.f;
@@ -291,11 +363,12 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         eq.act_frac = f.norm_attn_frac; eq.q_frac = f.q_frac; eq.k_frac = f.k_frac; eq.v_frac = f.v_frac;
         eq.nq = nq; eq.nkv = nkv; eq.out = b->QKV; eq.ldo = nqkv;
         if (planes) {
-            if ((e = rmsnorm_planes(b->X, R, H, Ld.res_in, Ld.in_gamma, Ld.in_gamma_s, H, m->rsqrt, m->rsqrt_len,
+            if (!in_normed &&
+                (e = rmsnorm_planes(b->X, R, H, Ld.res_in, Ld.in_gamma, Ld.in_gamma_s, H, m->rsqrt, m->rsqrt_len,
                                     MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, f.norm_attn_frac,
-                                    mm->planes, st)) != hipSuccess ||
-                (e = mm_planes(mm->planes, R, Ld.wqkv, nqkv, H, eq, mm, st)) != hipSuccess)
+                                    mm->planes, st)) != hipSuccess)
                 return e;
+            if ((e = mm_planes(mm->planes, R, Ld.wqkv, nqkv, H, eq, mm, st)) != hipSuccess) return e;
         } else {
             if ((e = rmsnorm(b->X, R, H, Ld.res_in, Ld.in_gamma, Ld.in_gamma_s, H, m->rsqrt, m->rsqrt_len,
                              MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, f.norm_attn_frac, b->Xn,
@@ -325,23 +398,38 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         rows_stats_kernel<<<dim3(heads, R), 256, 0, st>>>(b->rows, b->rows_cap, b->scores, heads, b->lmax_cap,
                                                           m->exp_lut, (uint32_t)m->exp_len, lut_shift, b->stats);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        if (hd == 128)
-            rows_pv_kernel<128><<<ag, kAttnThreads, attn_pv_lds<128>(), st>>>(b->tiles, b->rows, b->rows_cap, b->scores, b->stats, heads,
-                                                             b->lmax_cap, vc, sstride, m->max_pos, G, m->exp_lut,
-                                                             (uint32_t)m->exp_len, lut_shift, b->part, pst, nq);
-        else
-            rows_pv_kernel<64><<<ag, kAttnThreads, attn_pv_lds<64>(), st>>>(b->tiles, b->rows, b->rows_cap, b->scores, b->stats, heads,
-                                                            b->lmax_cap, vc, sstride, m->max_pos, G, m->exp_lut,
-                                                            (uint32_t)m->exp_len, lut_shift, b->part, pst, nq);
+        // Big grids (prefill) loop each block over its tile's ranges and
+        // finish the attention output in place; small ones (decode batches)
+        // keep a block per range and sum the ranges afterwards.
+        const bool loop = (int64_t)b->ntiles * kvh >= 2 * (int64_t)c->prop.multiProcessorCount;
+        const dim3 pg(b->ntiles, kvh, loop ? 1 : ranges);
+        int8_t* pplanes = planes ? mm->planes : nullptr;
+#define MYL_PV_LAUNCH(HDV, LOOPV)                                                                                  \
+    rows_pv_kernel<HDV, LOOPV><<<pg, kAttnThreads, attn_pv_lds<HDV>(), st>>>(                                      \
+        b->tiles, b->rows, b->rows_cap, b->scores, b->stats, heads, b->lmax_cap, vc, sstride, m->max_pos, G,         \
+        m->exp_lut, (uint32_t)m->exp_len, lut_shift, b->part, pst, nq, f.v_frac, f.attn_out_frac, b->A, pplanes)
+        if (hd == 128) {
+            if (loop) MYL_PV_LAUNCH(128, true);
+            else MYL_PV_LAUNCH(128, false);
+        } else {
+            if (loop) MYL_PV_LAUNCH(64, true);
+            else MYL_PV_LAUNCH(64, false);
+        }
+#undef MYL_PV_LAUNCH
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        rows_attn_out_kernel<<<dim3((nq + 255) / 256, R), 256, 0, st>>>(b->part, pst, b->rows, b->rows_cap, nq, f.v_frac,
-                                                                        f.attn_out_frac, b->A,
-                                                                        planes ? mm->planes : nullptr);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (!loop) {
+            rows_attn_out_kernel<<<dim3((nq + 255) / 256, R), 256, 0, st>>>(b->part, pst, b->rows, b->rows_cap, nq,
+                                                                            f.v_frac, f.attn_out_frac, b->A, pplanes);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
         EpiResidRows eo{};
         eo.shifts = Ld.so; eo.act_frac = f.attn_out_frac; eo.acc_frac = Ld.acc_attn; eo.res_frac = Ld.res_in;
         eo.out_frac = Ld.res_mid; eo.res = b->X; eo.ldr = H; eo.out = b->X2; eo.ldo = H;
-        e = planes ? mm_planes(mm->planes, R, Ld.wo, H, nq, eo, mm, st) : gemv_i8(b->A, R, nq, Ld.wo, H, nq, eo, st, mm);
+        if (norm_in_finish)
+            e = resid_then_norm(mm->planes, R, Ld.wo, H, nq, eo, mm, Ld.res_mid, Ld.post_gamma, Ld.post_gamma_s, m,
+                                f.norm_mlp_frac, mm->planes, st);
+        else
+            e = planes ? mm_planes(mm->planes, R, Ld.wo, H, nq, eo, mm, st) : gemv_i8(b->A, R, nq, Ld.wo, H, nq, eo, st, mm);
         if (e != hipSuccess) return e;
         EpiGURows eg{};
         eg.shifts = Ld.sgu; eg.act_frac = f.norm_mlp_frac; eg.gate_frac = f.gate_frac; eg.up_frac = f.up_frac;
@@ -356,11 +444,8 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
                 (e = mm_planes_staged(xin, R, Ld.wgu, 2 * I, H, es, mm, st)) != hipSuccess)
                 return e;
         } else if (planes) {
-            if ((e = rmsnorm_planes(b->X2, R, H, Ld.res_mid, Ld.post_gamma, Ld.post_gamma_s, H, m->rsqrt,
-                                    m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20,
-                                    f.norm_mlp_frac, mm->planes, st)) != hipSuccess ||
-                (e = mm_planes(mm->planes, R, Ld.wgu, 2 * I, H, eg, mm, st)) != hipSuccess)
-                return e;
+            // the post-attention norm's planes come from the o_proj finish
+            if ((e = mm_planes(mm->planes, R, Ld.wgu, 2 * I, H, eg, mm, st)) != hipSuccess) return e;
             silu_planes_kernel<<<dim3((I + 255) / 256, R), 256, 0, st>>>(b->GU, I, m->silu, (uint32_t)m->silu_len,
                                                                          f.gate_frac, f.up_frac, f.down_in_frac,
                                                                          mm->planes);
@@ -377,7 +462,14 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         EpiResidRows ed{};
         ed.shifts = Ld.sd; ed.act_frac = f.down_in_frac; ed.acc_frac = Ld.acc_mlp; ed.res_frac = Ld.res_mid;
         ed.out_frac = Ld.res_out; ed.res = b->X2; ed.ldr = H; ed.out = b->X; ed.ldo = H;
-        e = planes ? mm_planes(mm->planes, R, Ld.wd, H, I, ed, mm, st) : gemv_i8(b->Hh, R, I, Ld.wd, H, I, ed, st, mm);
+        in_normed = norm_in_finish && l + 1 < (int)m->spec.layers;
+        if (in_normed) {
+            const LayerDev& Ln = m->layers[l + 1];
+            e = resid_then_norm(mm->planes, R, Ld.wd, H, I, ed, mm, Ln.res_in, Ln.in_gamma, Ln.in_gamma_s, m,
+                                Ln.f.norm_attn_frac, mm->planes, st);
+        } else {
+            e = planes ? mm_planes(mm->planes, R, Ld.wd, H, I, ed, mm, st) : gemv_i8(b->Hh, R, I, Ld.wd, H, I, ed, st, mm);
+        }
         if (e != hipSuccess) return e;
     }
     // final norm and head over rows [h0, R)
@@ -389,8 +481,8 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         return e;
     if (m->spec.lm_head_int16) {
         EpiLogits el{m->lm16_shifts, m->final_norm_frac, MYL_TV_LOGIT_FRAC_BITS, logits_out, V};
-        if (HR >= 256 && H % 64 == 0 && mm && mm->planes && (size_t)2 * HR * H <= mm->planes_bytes) {
-            // many rows: byte planes of both operands, one int8 product
+        if (HR >= 2 && H % 64 == 0 && mm && mm->planes && (size_t)2 * HR * H <= mm->planes_bytes) {
+            // byte planes of both operands, one int8 product
             if (!m->lm16_planes_ok) {
                 if (!m->lm16_planes) {
                     m->lm16_planes = m->dalloc<int8_t>((size_t)2 * V * H);
@@ -457,6 +549,20 @@ int upload_rows(myl_model* m, BatchState* b, uint32_t R, const uint32_t* seq, co
         while (i < R && t.n < tr && (int32_t)(order[i].first >> 32) == t.seq) t.row[t.n++] = (int32_t)order[i++].second;
         tiles.push_back(t);
     }
+    // tiles reaching furthest into their caches (the most attention work)
+    // first: the row attention kernels schedule them earliest
+    {
+        std::vector<std::pair<uint32_t, size_t>> key(tiles.size());
+        for (size_t i = 0; i < tiles.size(); ++i) {
+            uint32_t pm = 0;
+            for (int k = 0; k < tiles[i].n; ++k) pm = std::max(pm, pos[tiles[i].row[k]]);
+            key[i] = {pm, i};
+        }
+        std::stable_sort(key.begin(), key.end(), [](const auto& x, const auto& y) { return x.first > y.first; });
+        std::vector<AttnTile> sorted(tiles.size());
+        for (size_t i = 0; i < tiles.size(); ++i) sorted[i] = tiles[key[i].second];
+        tiles.swap(sorted);
+    }
     if ((int)tiles.size() > b->tiles_cap) {
         (void)hipStreamSynchronize(c->stream);
         if (b->tiles) (void)hipFree(b->tiles);
@@ -498,10 +604,12 @@ int row_path_setup(myl_model* m) {
     if (rc) return rc;
     for (int16_t v : lut)
         if (v < 0) return c->fail(MYL_E_UNSUPPORTED, "batch: the exp table has negative entries");
-    const std::pair<const void*, size_t> big[4] = {{(const void*)rows_qk_kernel<128>, attn_qk_lds<128>()},
+    const std::pair<const void*, size_t> big[6] = {{(const void*)rows_qk_kernel<128>, attn_qk_lds<128>()},
                                                    {(const void*)rows_qk_kernel<64>, attn_qk_lds<64>()},
-                                                   {(const void*)rows_pv_kernel<128>, attn_pv_lds<128>()},
-                                                   {(const void*)rows_pv_kernel<64>, attn_pv_lds<64>()}};
+                                                   {(const void*)rows_pv_kernel<128, false>, attn_pv_lds<128>()},
+                                                   {(const void*)rows_pv_kernel<128, true>, attn_pv_lds<128>()},
+                                                   {(const void*)rows_pv_kernel<64, false>, attn_pv_lds<64>()},
+                                                   {(const void*)rows_pv_kernel<64, true>, attn_pv_lds<64>()}};
     for (const auto& k : big)
         if (hipFuncSetAttribute(k.first, hipFuncAttributeMaxDynamicSharedMemorySize, (int)k.second) != hipSuccess)
             return c->fail(MYL_E_HIP, "batch: attention LDS size");

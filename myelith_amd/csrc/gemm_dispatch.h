@@ -126,6 +126,20 @@ inline hipError_t mm_planes(const int8_t* Ap, int M, const int8_t* W, int N, int
     return mm2_launch_splitk<2, 1, 2, 4, 4>(Ap, M, W, N, K, epi, mm, cus / 2, st);
 }
 
+// mm_planes with a custom finish of split products (mm2_launch_splitk_fin):
+// for up to 64 rows the same tiles and splits, and *split tells whether fin
+// ran; more rows take mm_planes (no split, *split = false).
+template <class Epi, class Fin>
+inline hipError_t mm_planes_fin(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, const MmCtx* mm,
+                                hipStream_t st, const Fin& fin, bool* split) {
+    const int cus = mm->cus;
+    *split = false;
+    if (M <= 16) return mm2_launch_splitk_fin<1, 1, 1, 4, 4>(Ap, M, W, N, K, epi, mm, 2 * cus, st, fin, split);
+    if (M <= 32) return mm2_launch_splitk_fin<2, 1, 1, 4, 4>(Ap, M, W, N, K, epi, mm, cus, st, fin, split);
+    if (M <= 64) return mm2_launch_splitk_fin<2, 1, 2, 4, 4>(Ap, M, W, N, K, epi, mm, cus / 2, st, fin, split);
+    return mm_planes(Ap, M, W, N, K, epi, mm, st);
+}
+
 // The gate/up product with the staged epilogue (EpiGUSiluPlanes), for more
 // than 64 rows and N % 16 == 0: the tiles of mm_planes without a K split.
 template <class Epi>

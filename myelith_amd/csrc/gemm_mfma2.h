@@ -347,10 +347,11 @@ inline hipError_t split_planes_sum(const int16_t* x, int M, int ldx, int K, int8
     return hipGetLastError();
 }
 
-// The int16-weight product for many rows: A' and xsum from split_planes_sum,
-// Wp and wsum prepared once the same way.  Tiles of 256 A' rows x 256 W' rows
-// with 128-byte stages when the grid holds at least four tiles per CU (and
-// K % 128 == 0), else 256 x 128 tiles with 64-byte stages.
+// The int16-weight product for two rows or more: A' and xsum from
+// split_planes_sum, Wp and wsum prepared once the same way.  Up to 64 rows:
+// 32- or 64-row plane tiles x 128 W' rows (the weight planes stream once);
+// more: 256 A' rows x 256 W' rows with 128-byte stages when the grid holds
+// at least four tiles per CU (and K % 128 == 0), else 256 x 128 tiles.
 template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class Epi>
 hipError_t mm2w16_launch_cfg(const int8_t* Ap, const int32_t* xsum, int M, const int8_t* Wp, const int32_t* wsum,
                              int N, int K, const Epi& epi, hipStream_t st) {
@@ -368,6 +369,10 @@ hipError_t mm2w16_launch_cfg(const int8_t* Ap, const int32_t* xsum, int M, const
 template <class Epi>
 hipError_t mm2w16_launch(const int8_t* Ap, const int32_t* xsum, int M, const int8_t* Wp, const int32_t* wsum, int N,
                          int K, const Epi& epi, int cus, hipStream_t st) {
+    // few rows: one plane-row tile streams the weight planes once
+    if (M <= 16) return mm2w16_launch_cfg<1, 1, 1, 4, 4, 64>(Ap, xsum, M, Wp, wsum, N, K, epi, st);
+    if (M <= 32) return mm2w16_launch_cfg<2, 1, 1, 4, 4, 64>(Ap, xsum, M, Wp, wsum, N, K, epi, st);
+    if (M <= 64) return mm2w16_launch_cfg<2, 1, 2, 4, 4, 64>(Ap, xsum, M, Wp, wsum, N, K, epi, st);
     using W = Mm2<2, 2, 4, 4, 2, 128>;
     const int wide_tiles = ((2 * M + W::BR - 1) / W::BR) * ((2 * N + W::BN - 1) / W::BN);
     if (K % 128 == 0 && wide_tiles >= 4 * cus)
@@ -413,10 +418,12 @@ hipError_t mm2_launch(const int8_t* Ap, int M, const int8_t* W, int N, int K, co
 
 // Weights stream once per row tile; K split across blocks when there are
 // fewer tiles than `fill` (slices of at least 8 stages of 64 bytes), partial
-// sums through the i64 accumulator.
-template <int MB, int NB, int WM_, int WN_, int STAGES, class Epi>
-hipError_t mm2_launch_splitk(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, const MmCtx* mm,
-                             int fill, hipStream_t st) {
+// sums through the i64 accumulator.  A split product ends with fin(acc, st)
+// (the finish kernel that applies the epilogue and clears acc) and sets
+// *split; otherwise the tiles apply epi themselves.
+template <int MB, int NB, int WM_, int WN_, int STAGES, class Epi, class Fin>
+hipError_t mm2_launch_splitk_fin(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi,
+                                 const MmCtx* mm, int fill, hipStream_t st, const Fin& fin, bool* split) {
     using S = Mm2<MB, NB, WM_, WN_, STAGES>;
     const int R2 = 2 * M;
     const int tiles_r = (R2 + S::BR - 1) / S::BR, ntiles = tiles_r * ((N + S::BN - 1) / S::BN);
@@ -424,6 +431,7 @@ hipError_t mm2_launch_splitk(const int8_t* Ap, int M, const int8_t* W, int N, in
     int ks = 1;
     if (ntiles < fill && (size_t)M * N <= mm->acc_elems)
         ks = std::max(1, std::min((2 * mm->cus + ntiles - 1) / ntiles, nkb / 8));
+    *split = ks > 1;
     if (ks <= 1) return mm2_launch<MB, NB, WM_, WN_, STAGES>(Ap, M, W, N, K, epi, st);
     const int kslice = ((nkb + ks - 1) / ks) * 64;
     const int ns = (K + kslice - 1) / kslice, nitems = ntiles * ns;
@@ -436,10 +444,20 @@ hipError_t mm2_launch_splitk(const int8_t* Ap, int M, const int8_t* W, int N, in
                                                               Divider::of((uint32_t)ntiles), nitems, kslice, mm->acc);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int colb = (N + 255) / 256;
-    const int rows = std::max(1, std::min(M, (mm->cus * 8 + colb - 1) / colb));
-    mm_splitk_finish_kernel<Epi><<<dim3(colb, rows), 256, 0, st>>>(mm->acc, M, N, epi);
-    return hipGetLastError();
+    return fin(mm->acc, st);
+}
+
+template <int MB, int NB, int WM_, int WN_, int STAGES, class Epi>
+hipError_t mm2_launch_splitk(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, const MmCtx* mm,
+                             int fill, hipStream_t st) {
+    bool split = false;
+    auto fin = [&](unsigned long long* acc, hipStream_t s) {
+        const int colb = (N + 255) / 256;
+        const int rows = std::max(1, std::min(M, (mm->cus * 8 + colb - 1) / colb));
+        mm_splitk_finish_kernel<Epi><<<dim3(colb, rows), 256, 0, s>>>(acc, M, N, epi);
+        return hipGetLastError();
+    };
+    return mm2_launch_splitk_fin<MB, NB, WM_, WN_, STAGES>(Ap, M, W, N, K, epi, mm, fill, st, fin, &split);
 }
 
 // Block tiles of a launch shape (for the dispatch's tile count).

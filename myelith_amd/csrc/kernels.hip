@@ -128,20 +128,24 @@ __global__ __launch_bounds__(kRowsThreads) void rmsnorm_rows_kernel(const int16_
     const int16_t* xr = x + (size_t)blockIdx.x * ldx;
     const int nc = n >> 3;
     uint4 xv[PER];
-    uint2 sv[PER];
+    uint2 sv[PER], gv[PER], gsv[PER];  // gamma and its shifts load with x
     int32_t mx = 0;
 #pragma unroll
     for (int t = 0; t < PER; ++t) {
         const int c = threadIdx.x + t * kRowsThreads;
         xv[t] = make_uint4(0, 0, 0, 0);
-        sv[t] = make_uint2(0, 0);
+        sv[t] = gv[t] = gsv[t] = make_uint2(0, 0);
         if (c < nc) {
             xv[t] = *reinterpret_cast<const uint4*>(xr + 8 * c);
             sv[t] = *reinterpret_cast<const uint2*>(xs + 8 * c);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) mx = max(mx, (int32_t)byte_of(sv[t], q));
+            gv[t] = *reinterpret_cast<const uint2*>(g + 8 * c);
+            gsv[t] = *reinterpret_cast<const uint2*>(gs + 8 * c);
         }
     }
+#pragma unroll
+    for (int t = 0; t < PER; ++t)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) mx = max(mx, (int32_t)byte_of(sv[t], q));
     const uint8_t ref = (uint8_t)block_max_i32(mx, red32);
     uint64_t acc64 = 0;
     myl_i128 acc = 0;
@@ -157,8 +161,10 @@ __global__ __launch_bounds__(kRowsThreads) void rmsnorm_rows_kernel(const int16_
             else acc = (myl_i128)((myl_u128)acc + (myl_u128)shl128((myl_i128)sq, align));
         }
     }
-    acc = (myl_i128)((myl_u128)acc + (myl_u128)acc64);
-    acc = wave_sum_i128(acc);
+    // all lanes at the largest shift (the usual case): a 64-bit DPP sum
+    // (each lane < 2^34, so the wave total < 2^40); else the 128-bit one
+    if (__any(acc != 0)) acc = wave_sum_i128((myl_i128)((myl_u128)acc + (myl_u128)acc64));
+    else acc = (myl_i128)wave_sum_u64(acc64);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red128[threadIdx.x >> 6] = acc;
     __syncthreads();
@@ -170,14 +176,12 @@ __global__ __launch_bounds__(kRowsThreads) void rmsnorm_rows_kernel(const int16_
     for (int t = 0; t < PER; ++t) {
         const int c = threadIdx.x + t * kRowsThreads;
         if (c >= nc) continue;
-        const uint2 gv = *reinterpret_cast<const uint2*>(g + 8 * c);
-        const uint2 gsv = *reinterpret_cast<const uint2*>(gs + 8 * c);
         const uint32_t w[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
         int32_t y[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q)
             y[q] = rms_out((int16_t)((w[q >> 1] >> (16 * (q & 1))) & 0xFFFFu), byte_of(sv[t], q),
-                           (int8_t)byte_of(gv, q), byte_of(gsv, q), f, out_frac);
+                           (int8_t)byte_of(gv[t], q), byte_of(gsv[t], q), f, out_frac);
         if (planes) {
             uint32_t h[2] = {0, 0}, l[2] = {0, 0};
 #pragma unroll

@@ -217,12 +217,13 @@ __global__ __launch_bounds__(kAttnThreads) void rows_qk_kernel(
     }
 }
 
-template <int HD>
+template <int HD, bool LOOP>
 __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
     const AttnTile* __restrict__ tiles, const int32_t* __restrict__ rows, int rows_cap,
     const int32_t* __restrict__ scores, const int32_t* __restrict__ stats, int heads, int lcap,
     const int16_t* __restrict__ vc, size_t seq_stride, int max_pos, int G, const int16_t* __restrict__ lut,
-    uint32_t lut_len, uint8_t lut_shift, int64_t* __restrict__ part, size_t part_stride, int nq) {
+    uint32_t lut_len, uint8_t lut_shift, int64_t* __restrict__ part, size_t part_stride, int nq,
+    uint8_t v_frac, uint8_t out_frac, int16_t* __restrict__ A, int8_t* __restrict__ planes) {
     constexpr int RS = kAttnRange + 16;  // LDS row stride: the range's positions of one vector / dimension
     constexpr int NT = HD / 32;
     constexpr int CH = HD / 8, CH_LOG = HD == 128 ? 4 : 3;
@@ -237,12 +238,14 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
     __shared__ uint32_t q_r32[kAttnQV];
     __shared__ int32_t p_sum[kAttnQV], v_sum[HD];
     __shared__ int s_pmax;
-    const int g = blockIdx.y, range = blockIdx.z, j0 = range * kAttnRange;
+    const int g = blockIdx.y;
     int QV;
     const int seq = attn_setup(tiles, rows, rows_cap, G, g, qv, &s_pmax, QV);
     const int pmax = s_pmax;
-    if (j0 > pmax) return;
-    const int nk = (min(j0 + kAttnRange, pmax + 1) - j0 + 31) / 32;  // 32-position steps
+    // one range (blockIdx.z), or every range of the tile in turn (LOOP)
+    const int r_first = LOOP ? 0 : (int)blockIdx.z;
+    const int r_last = LOOP ? pmax / kAttnRange : (int)blockIdx.z;
+    if (r_first * kAttnRange > pmax) return;
     const int MT = (QV + 31) / 32;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -264,151 +267,186 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
             q_ur[tid] = wsub32(one, wmul32((int32_t)qq, (int32_t)L));
         }
     }
-    if (tid < HD) v_sum[tid] = 0;
-    __syncthreads();
-    // Every score load of the wave and every V load of the thread is issued
-    // before any of them is used (one memory latency instead of one per
-    // vector and per item).
-    constexpr int kVpw = kAttnQV / (kAttnThreads / 64);      // vectors per wave
-    constexpr int kVit = (CH * 64 + kAttnThreads - 1) / kAttnThreads;  // V items per thread
-    const int q4 = lane, jb = j0 + 4 * q4;
-    int4 zv[kVpw];
-#pragma unroll
-    for (int i = 0; i < kVpw; ++i) {
-        const int v = wave + i * (kAttnThreads / 64);
-        zv[i] = make_int4(0, 0, 0, 0);
-        if (q4 < 8 * nk && v < QV && jb <= qv.pos[v])
-            zv[i] = *reinterpret_cast<const int4*>(scores + ((size_t)qv.row[v] * heads + qv.head[v]) * lcap + jb);
-    }
-    const int16_t* vg = vc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD;
-    uint4 vw[kVit][4];
-#pragma unroll
-    for (int i = 0; i < kVit; ++i) {
-        const int t = tid + i * kAttnThreads;
-        const int c = t & (CH - 1), vq4 = t >> CH_LOG;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int j = j0 + 4 * vq4 + k;
-            vw[i][k] = t < CH * 8 * nk && j < max_pos ? *reinterpret_cast<const uint4*>(vg + (size_t)j * HD + c * 8)
-                                                      : make_uint4(0, 0, 0, 0);
-        }
-    }
-    // P planes [vector][position]: a wave per vector, its lanes over the
-    // range's 4-position groups (8 * nk <= 64 of them)
-#pragma unroll
-    for (int i = 0; i < kVpw; ++i) {
-        const int v = wave + i * (kAttnThreads / 64);
-        if (v >= MT * 32) break;  // wave-uniform
-        uint32_t hw = 0, lw = 0x80808080u;  // p = 0: hi 0, lo' -128
-        int32_t ps = 0;
-        if (q4 < 8 * nk && v < QV && jb <= qv.pos[v]) {
-            const int pos = qv.pos[v];
-            const int32_t zz[4] = {zv[i].x, zv[i].y, zv[i].z, zv[i].w};
-            lw = 0;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int j = jb + k;
-                int32_t p = 0;
-                if (j <= pos) {
-                    if (q_s[v] == 0) {
-                        p = q_ub[v] + (((uint64_t)j < (uint64_t)(int64_t)q_ur[v]) ? 1 : 0);
-                    } else {
-                        const int32_t e = exp_lookup(sat_sub32(q_m[v], zz[k]), lut, lut_len, lut_shift, lut_one);
-                        // e * 2^14 >= 0 (a non-negative exp table); the
-                        // sum is positive unless it wrapped
-                        p = q_s[v] > 0 ? softmax_div_round_pos(wmul32(e, one), q_s[v], q_r32[v])
-                                       : softmax_div_round(wmul32(e, one), q_s[v], q_rs[v]);
-                    }
-                }
-                ps += p;
-                hw |= ((uint32_t)(p >> 8) & 0xFFu) << (8 * k);
-                lw |= ((uint32_t)((p & 255) - 128) & 0xFFu) << (8 * k);
-            }
-        }
-        if (q4 < 8 * nk) {
-            *reinterpret_cast<uint32_t*>(ph + v * RS + 4 * q4) = hw;
-            *reinterpret_cast<uint32_t*>(pl + v * RS + 4 * q4) = lw;
-        }
-        ps = wave_sum_i32(ps);
-        if (lane == 0) p_sum[v] = ps;
-    }
-    // V planes transposed to [dimension][position]: 8 dimensions x 4 positions per item
-#pragma unroll
-    for (int i = 0; i < kVit; ++i) {
-        const int t = tid + i * kAttnThreads;
-        if (t >= CH * 8 * nk) break;
-        const int c = t & (CH - 1), vq4 = t >> CH_LOG;
-        const uint4 (&w)[4] = vw[i];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            uint32_t hw = 0, lw = 0;
-            int32_t vs = 0;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t word = (e >> 1) == 0 ? w[k].x : ((e >> 1) == 1 ? w[k].y : ((e >> 1) == 2 ? w[k].z : w[k].w));
-                const int32_t x = (int16_t)((e & 1) ? (word >> 16) : (word & 0xFFFFu));
-                vs += x;
-                hw |= ((uint32_t)(x >> 8) & 0xFFu) << (8 * k);
-                lw |= ((uint32_t)((x & 255) - 128) & 0xFFu) << (8 * k);
-            }
-            const int d = c * 8 + e;
-            // 16-byte position chunk (vq4 >> 2) at slot chunk ^ (d >> 3): rows
-            // eight apart no longer share banks
-            const int off = (((vq4 >> 2) ^ (c & 15)) << 4) + 4 * (vq4 & 3);
-            *reinterpret_cast<uint32_t*>(vh + d * RS + off) = hw;
-            *reinterpret_cast<uint32_t*>(vl + d * RS + off) = lw;
-            atomicAdd(&v_sum[d], vs);
-        }
-    }
-    __syncthreads();
-    // wave tasks: (query tile, dimension tile) pairs, at most two per wave
     const int ntask = MT * NT;
-    v16i32_t acc[2][3];
+    // exact P.V sums of the block's (vector, dimension) outputs over its ranges
+    int64_t tot[2][16];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int b = 0; b < 3; ++b)
+        for (int r = 0; r < 16; ++r) tot[a][r] = 0;
+    for (int range = r_first; range <= r_last; ++range) {
+        const int j0 = range * kAttnRange;
+        const int nk = (min(j0 + kAttnRange, pmax + 1) - j0 + 31) / 32;  // 32-position steps
+        if (tid < HD) v_sum[tid] = 0;
+        __syncthreads();
+        // Every score load of the wave and every V load of the thread is issued
+        // before any of them is used (one memory latency instead of one per
+        // vector and per item).
+        constexpr int kVpw = kAttnQV / (kAttnThreads / 64);      // vectors per wave
+        constexpr int kVit = (CH * 64 + kAttnThreads - 1) / kAttnThreads;  // V items per thread
+        const int q4 = lane, jb = j0 + 4 * q4;
+        int4 zv[kVpw];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0;
-#pragma unroll
-    for (int a = 0; a < 2; ++a) {
-        const int task = wave + a * (kAttnThreads / 64);
-        if (task >= ntask) continue;
-        const int mt = task / NT, nt = task - mt * NT;
-        const int8_t* ah_row = ph + (mt * 32 + (lane & 31)) * RS + 16 * (lane >> 5);
-        const int8_t* al_row = pl + (mt * 32 + (lane & 31)) * RS + 16 * (lane >> 5);
-        const int dr = nt * 32 + (lane & 31);
-        const int8_t* bh_row = vh + dr * RS;
-        const int8_t* bl_row = vl + dr * RS;
-        const int sw = (dr >> 3) & 15;
-        for (int kk = 0; kk < nk; ++kk) {
-            const int slot = ((2 * kk + (lane >> 5)) ^ sw) << 4;
-            const v4i32_t ah = *reinterpret_cast<const v4i32_t*>(ah_row + 32 * kk);
-            const v4i32_t al = *reinterpret_cast<const v4i32_t*>(al_row + 32 * kk);
-            const v4i32_t bh = *reinterpret_cast<const v4i32_t*>(bh_row + slot);
-            const v4i32_t bl = *reinterpret_cast<const v4i32_t*>(bl_row + slot);
-            acc[a][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bh, acc[a][0], 0, 0, 0);
-            acc[a][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bl, acc[a][1], 0, 0, 0);
-            acc[a][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bh, acc[a][1], 0, 0, 0);
-            acc[a][2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bl, acc[a][2], 0, 0, 0);
+        for (int i = 0; i < kVpw; ++i) {
+            const int v = wave + i * (kAttnThreads / 64);
+            zv[i] = make_int4(0, 0, 0, 0);
+            if (q4 < 8 * nk && v < QV && jb <= qv.pos[v])
+                zv[i] = *reinterpret_cast<const int4*>(scores + ((size_t)qv.row[v] * heads + qv.head[v]) * lcap + jb);
         }
+        const int16_t* vg = vc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD;
+        uint4 vw[kVit][4];
+#pragma unroll
+        for (int i = 0; i < kVit; ++i) {
+            const int t = tid + i * kAttnThreads;
+            const int c = t & (CH - 1), vq4 = t >> CH_LOG;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int j = j0 + 4 * vq4 + k;
+                vw[i][k] = t < CH * 8 * nk && j < max_pos ? *reinterpret_cast<const uint4*>(vg + (size_t)j * HD + c * 8)
+                                                          : make_uint4(0, 0, 0, 0);
+            }
+        }
+        // P planes [vector][position]: a wave per vector, its lanes over the
+        // range's 4-position groups (8 * nk <= 64 of them)
+#pragma unroll
+        for (int i = 0; i < kVpw; ++i) {
+            const int v = wave + i * (kAttnThreads / 64);
+            if (v >= MT * 32) break;  // wave-uniform
+            uint32_t hw = 0, lw = 0x80808080u;  // p = 0: hi 0, lo' -128
+            int32_t ps = 0;
+            if (q4 < 8 * nk && v < QV && jb <= qv.pos[v]) {
+                const int pos = qv.pos[v];
+                const int32_t zz[4] = {zv[i].x, zv[i].y, zv[i].z, zv[i].w};
+                lw = 0;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int j = jb + k;
+                    int32_t p = 0;
+                    if (j <= pos) {
+                        if (q_s[v] == 0) {
+                            p = q_ub[v] + (((uint64_t)j < (uint64_t)(int64_t)q_ur[v]) ? 1 : 0);
+                        } else {
+                            const int32_t e = exp_lookup(sat_sub32(q_m[v], zz[k]), lut, lut_len, lut_shift, lut_one);
+                            // e * 2^14 >= 0 (a non-negative exp table); the
+                            // sum is positive unless it wrapped
+                            p = q_s[v] > 0 ? softmax_div_round_pos(wmul32(e, one), q_s[v], q_r32[v])
+                                           : softmax_div_round(wmul32(e, one), q_s[v], q_rs[v]);
+                        }
+                    }
+                    ps += p;
+                    hw |= ((uint32_t)(p >> 8) & 0xFFu) << (8 * k);
+                    lw |= ((uint32_t)((p & 255) - 128) & 0xFFu) << (8 * k);
+                }
+            }
+            if (q4 < 8 * nk) {
+                *reinterpret_cast<uint32_t*>(ph + v * RS + 4 * q4) = hw;
+                *reinterpret_cast<uint32_t*>(pl + v * RS + 4 * q4) = lw;
+            }
+            ps = wave_sum_i32(ps);
+            if (lane == 0) p_sum[v] = ps;
+        }
+        // V planes transposed to [dimension][position]: 8 dimensions x 4 positions per item
+#pragma unroll
+        for (int i = 0; i < kVit; ++i) {
+            const int t = tid + i * kAttnThreads;
+            if (t >= CH * 8 * nk) break;
+            const int c = t & (CH - 1), vq4 = t >> CH_LOG;
+            const uint4 (&w)[4] = vw[i];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                uint32_t hw = 0, lw = 0;
+                int32_t vs = 0;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t word = (e >> 1) == 0 ? w[k].x : ((e >> 1) == 1 ? w[k].y : ((e >> 1) == 2 ? w[k].z : w[k].w));
+                    const int32_t x = (int16_t)((e & 1) ? (word >> 16) : (word & 0xFFFFu));
+                    vs += x;
+                    hw |= ((uint32_t)(x >> 8) & 0xFFu) << (8 * k);
+                    lw |= ((uint32_t)((x & 255) - 128) & 0xFFu) << (8 * k);
+                }
+                const int d = c * 8 + e;
+                // 16-byte position chunk (vq4 >> 2) at slot chunk ^ (d >> 3): rows
+                // eight apart no longer share banks
+                const int off = (((vq4 >> 2) ^ (c & 15)) << 4) + 4 * (vq4 & 3);
+                *reinterpret_cast<uint32_t*>(vh + d * RS + off) = hw;
+                *reinterpret_cast<uint32_t*>(vl + d * RS + off) = lw;
+                atomicAdd(&v_sum[d], vs);
+            }
+        }
+        __syncthreads();
+        // wave tasks: (query tile, dimension tile) pairs, at most two per wave
+        v16i32_t acc[2][3];
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 3; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[a][b][r] = 0;
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            const int task = wave + a * (kAttnThreads / 64);
+            if (task >= ntask) continue;
+            const int mt = task / NT, nt = task - mt * NT;
+            const int8_t* ah_row = ph + (mt * 32 + (lane & 31)) * RS + 16 * (lane >> 5);
+            const int8_t* al_row = pl + (mt * 32 + (lane & 31)) * RS + 16 * (lane >> 5);
+            const int dr = nt * 32 + (lane & 31);
+            const int8_t* bh_row = vh + dr * RS;
+            const int8_t* bl_row = vl + dr * RS;
+            const int sw = (dr >> 3) & 15;
+            for (int kk = 0; kk < nk; ++kk) {
+                const int slot = ((2 * kk + (lane >> 5)) ^ sw) << 4;
+                const v4i32_t ah = *reinterpret_cast<const v4i32_t*>(ah_row + 32 * kk);
+                const v4i32_t al = *reinterpret_cast<const v4i32_t*>(al_row + 32 * kk);
+                const v4i32_t bh = *reinterpret_cast<const v4i32_t*>(bh_row + slot);
+                const v4i32_t bl = *reinterpret_cast<const v4i32_t*>(bl_row + slot);
+                acc[a][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bh, acc[a][0], 0, 0, 0);
+                acc[a][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bl, acc[a][1], 0, 0, 0);
+                acc[a][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bh, acc[a][1], 0, 0, 0);
+                acc[a][2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bl, acc[a][2], 0, 0, 0);
+            }
+        }
+        const int64_t cterm = 16384 * 32 * (int64_t)nk;
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            const int task = wave + a * (kAttnThreads / 64);
+            if (task >= ntask) continue;
+            const int mt = task / NT, nt = task - mt * NT;
+            const int d = nt * 32 + (lane & 31);
+            const int64_t dterm = 128 * (int64_t)v_sum[d] - cterm;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int v = mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                tot[a][r] = wadd64(tot[a][r], 65536 * (int64_t)acc[a][0][r] + 256 * (int64_t)acc[a][1][r] +
+                                                  (int64_t)acc[a][2][r] + 128 * (int64_t)p_sum[v] + dterm);
+            }
+        }
+        __syncthreads();  // the next range overwrites the planes, p_sum and v_sum
     }
-    const int64_t cterm = 16384 * 32 * (int64_t)nk;
-    int64_t* out = part + (size_t)range * part_stride;
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
         const int task = wave + a * (kAttnThreads / 64);
         if (task >= ntask) continue;
         const int mt = task / NT, nt = task - mt * NT;
         const int d = nt * 32 + (lane & 31);
-        const int64_t dterm = 128 * (int64_t)v_sum[d] - cterm;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int v = mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (v < QV)
-                out[(size_t)qv.row[v] * nq + (size_t)qv.head[v] * HD + d] =
-                    65536 * (int64_t)acc[a][0][r] + 256 * (int64_t)acc[a][1][r] + (int64_t)acc[a][2][r] +
-                    128 * (int64_t)p_sum[v] + dterm;
+            if (v >= QV) continue;
+            const size_t o = (size_t)qv.row[v] * nq + (size_t)qv.head[v] * HD + d;
+            if (!LOOP) {
+                part[(size_t)r_first * part_stride + o] = tot[a][r];
+                continue;
+            }
+            // attention.rs:84-86 then model.rs:563-567 (as rows_attn_out_kernel)
+            const int16_t vv = clamp_i16_i64(rshift_round64(tot[a][r], MYL_TV_PROB_FRAC_BITS));
+            const int16_t av = clamp_i16(rescale32((int32_t)vv, v_frac, out_frac));
+            if (planes) {
+                const size_t ro = (size_t)qv.row[v] * 2 * nq + (size_t)qv.head[v] * HD + d;
+                planes[ro] = (int8_t)(av >> 8);
+                planes[ro + nq] = (int8_t)((av & 255) - 128);
+            } else {
+                A[o] = av;
+            }
         }
     }
 }

@@ -57,12 +57,16 @@ struct EpiResidRows : EpiApply<EpiResidRows> {
         e.out += (size_t)m0 * ldo;
         return e;
     }
-    __device__ inline void one(int n, int m, int64_t acc) const {
+    // the output element, also stored
+    __device__ inline int16_t value(int n, int m, int64_t acc) const {
         const uint8_t af = acc_frac[n];
         const int16_t o = clamp_i16_i64(rescale64(acc, (uint8_t)(shifts[n] + act_frac), af));
         const int64_t h = rescale64((int64_t)res[(size_t)m * ldr + n], res_frac[n], af);
-        out[(size_t)m * ldo + n] = clamp_i16_i64(rescale64(wadd64(h, (int64_t)o), af, out_frac[n]));
+        const int16_t y = clamp_i16_i64(rescale64(wadd64(h, (int64_t)o), af, out_frac[n]));
+        out[(size_t)m * ldo + n] = y;
+        return y;
     }
+    __device__ inline void one(int n, int m, int64_t acc) const { (void)value(n, m, acc); }
 };
 
 // gate (even rows) and up (odd rows) requantized to their own fracs (mlp.rs:46-53).
