@@ -117,8 +117,14 @@ inline hipError_t mm_planes(const int8_t* Ap, int M, const int8_t* W, int N, int
                             hipStream_t st) {
     const int cus = mm->cus;
     // few rows: partial sums cost little, so K is split until every CU has
-    // work (up to 16 tokens: one 32-row plane tile, and K split for up to two
-    // items per CU, 5-10% faster on MI355X than 64-row tiles)
+    // work (up to 16 tokens: one 32-row plane tile with 128-byte K stages, 64
+    // weight rows per tile, or 128 when that alone gives two tiles per CU;
+    // K split for up to two items per CU: 20-25% faster on MI355X than
+    // 64-byte stages for the 7B gate/up and LM head shapes at 8 rows)
+    if (M <= 16 && K % 128 == 0) {
+        if (N >= 256 * cus) return mm2_launch_splitk<1, 1, 1, 4, 3, 128>(Ap, M, W, N, K, epi, mm, 2 * cus, st);
+        return mm2_launch_splitk<1, 1, 1, 2, 4, 128>(Ap, M, W, N, K, epi, mm, 2 * cus, st);
+    }
     if (M <= 16) return mm2_launch_splitk<1, 1, 1, 4, 4>(Ap, M, W, N, K, epi, mm, 2 * cus, st);
     if (M <= 32) return mm2_launch_splitk<2, 1, 1, 4, 4>(Ap, M, W, N, K, epi, mm, cus, st);
     if (M > 64 && mm_wide_tiles(M, N, K, cus)) return mm2_launch<2, 2, 4, 4, 2, 128>(Ap, M, W, N, K, epi, st);
@@ -134,6 +140,11 @@ inline hipError_t mm_planes_fin(const int8_t* Ap, int M, const int8_t* W, int N,
                                 hipStream_t st, const Fin& fin, bool* split) {
     const int cus = mm->cus;
     *split = false;
+    if (M <= 16 && K % 128 == 0) {
+        if (N >= 256 * cus)
+            return mm2_launch_splitk_fin<1, 1, 1, 4, 3, 128>(Ap, M, W, N, K, epi, mm, 2 * cus, st, fin, split);
+        return mm2_launch_splitk_fin<1, 1, 1, 2, 4, 128>(Ap, M, W, N, K, epi, mm, 2 * cus, st, fin, split);
+    }
     if (M <= 16) return mm2_launch_splitk_fin<1, 1, 1, 4, 4>(Ap, M, W, N, K, epi, mm, 2 * cus, st, fin, split);
     if (M <= 32) return mm2_launch_splitk_fin<2, 1, 1, 4, 4>(Ap, M, W, N, K, epi, mm, cus, st, fin, split);
     if (M <= 64) return mm2_launch_splitk_fin<2, 1, 2, 4, 4>(Ap, M, W, N, K, epi, mm, cus / 2, st, fin, split);

@@ -370,6 +370,7 @@ template <class Epi>
 hipError_t mm2w16_launch(const int8_t* Ap, const int32_t* xsum, int M, const int8_t* Wp, const int32_t* wsum, int N,
                          int K, const Epi& epi, int cus, hipStream_t st) {
     // few rows: one plane-row tile streams the weight planes once
+    if (M <= 16 && K % 128 == 0) return mm2w16_launch_cfg<1, 1, 1, 4, 3, 128>(Ap, xsum, M, Wp, wsum, N, K, epi, st);
     if (M <= 16) return mm2w16_launch_cfg<1, 1, 1, 4, 4, 64>(Ap, xsum, M, Wp, wsum, N, K, epi, st);
     if (M <= 32) return mm2w16_launch_cfg<2, 1, 1, 4, 4, 64>(Ap, xsum, M, Wp, wsum, N, K, epi, st);
     if (M <= 64) return mm2w16_launch_cfg<2, 1, 2, 4, 4, 64>(Ap, xsum, M, Wp, wsum, N, K, epi, st);
@@ -383,12 +384,12 @@ hipError_t mm2w16_launch(const int8_t* Ap, const int32_t* xsum, int M, const int
 // Split-K form: item t -> (slice t / ntiles, tile t % ntiles); the exact
 // partial sums of each slice are added into acc [M x N] (i64, zero-kept; the
 // finish kernel applies the epilogue and clears it).
-template <int MB, int NB, int WM_, int WN_, int STAGES>
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS = 64>
 __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_splitk_kernel(const int8_t* __restrict__ Ap, int R2,
                                                                     const int8_t* __restrict__ W, int N, int K,
                                                                     Divider tiles_r, Divider ntiles, int nitems,
                                                                     int kslice, unsigned long long* __restrict__ acc) {
-    using S = Mm2<MB, NB, WM_, WN_, STAGES>;
+    using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     extern __shared__ __align__(16) int8_t lds[];
     const int t = mm_tile_index(nitems);
     if (t < 0) return;
@@ -397,7 +398,7 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_splitk_kernel(const int8_t
     tiles_r.divmod(tile, tn, tr);
     const int kb = (int)ks * kslice, ke = min(K, kb + kslice);
     if (kb >= ke) return;
-    mm2_tile<MB, NB, WM_, WN_, STAGES, 64>(Ap, R2, W, N, K, kb, ke, (int)tr * S::BR, (int)tn * S::BN, lds,
+    mm2_tile<MB, NB, WM_, WN_, STAGES, KS>(Ap, R2, W, N, K, kb, ke, (int)tr * S::BR, (int)tn * S::BN, lds,
                                            SinkAtomic{acc, N});
 }
 
@@ -417,25 +418,25 @@ hipError_t mm2_launch(const int8_t* Ap, int M, const int8_t* W, int N, int K, co
 }
 
 // Weights stream once per row tile; K split across blocks when there are
-// fewer tiles than `fill` (slices of at least 8 stages of 64 bytes), partial
-// sums through the i64 accumulator.  A split product ends with fin(acc, st)
-// (the finish kernel that applies the epilogue and clears acc) and sets
-// *split; otherwise the tiles apply epi themselves.
-template <int MB, int NB, int WM_, int WN_, int STAGES, class Epi, class Fin>
+// fewer tiles than `fill` (slices of at least 512 bytes), partial sums
+// through the i64 accumulator.  A split product ends with fin(acc, st) (the
+// finish kernel that applies the epilogue and clears acc) and sets *split;
+// otherwise the tiles apply epi themselves.  K % KS == 0.
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS = 64, class Epi, class Fin>
 hipError_t mm2_launch_splitk_fin(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi,
                                  const MmCtx* mm, int fill, hipStream_t st, const Fin& fin, bool* split) {
-    using S = Mm2<MB, NB, WM_, WN_, STAGES>;
+    using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     const int R2 = 2 * M;
     const int tiles_r = (R2 + S::BR - 1) / S::BR, ntiles = tiles_r * ((N + S::BN - 1) / S::BN);
-    const int nkb = K / 64;
+    const int nkb = K / KS;
     int ks = 1;
     if (ntiles < fill && (size_t)M * N <= mm->acc_elems)
-        ks = std::max(1, std::min((2 * mm->cus + ntiles - 1) / ntiles, nkb / 8));
+        ks = std::max(1, std::min((2 * mm->cus + ntiles - 1) / ntiles, nkb / (512 / KS)));
     *split = ks > 1;
-    if (ks <= 1) return mm2_launch<MB, NB, WM_, WN_, STAGES>(Ap, M, W, N, K, epi, st);
-    const int kslice = ((nkb + ks - 1) / ks) * 64;
+    if (ks <= 1) return mm2_launch<MB, NB, WM_, WN_, STAGES, KS>(Ap, M, W, N, K, epi, st);
+    const int kslice = ((nkb + ks - 1) / ks) * KS;
     const int ns = (K + kslice - 1) / kslice, nitems = ntiles * ns;
-    auto kern = mm2_splitk_kernel<MB, NB, WM_, WN_, STAGES>;
+    auto kern = mm2_splitk_kernel<MB, NB, WM_, WN_, STAGES, KS>;
     if (S::kLds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
         if (e != hipSuccess) return e;
@@ -447,7 +448,7 @@ hipError_t mm2_launch_splitk_fin(const int8_t* Ap, int M, const int8_t* W, int N
     return fin(mm->acc, st);
 }
 
-template <int MB, int NB, int WM_, int WN_, int STAGES, class Epi>
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS = 64, class Epi>
 hipError_t mm2_launch_splitk(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, const MmCtx* mm,
                              int fill, hipStream_t st) {
     bool split = false;
@@ -457,7 +458,7 @@ hipError_t mm2_launch_splitk(const int8_t* Ap, int M, const int8_t* W, int N, in
         mm_splitk_finish_kernel<Epi><<<dim3(colb, rows), 256, 0, s>>>(acc, M, N, epi);
         return hipGetLastError();
     };
-    return mm2_launch_splitk_fin<MB, NB, WM_, WN_, STAGES>(Ap, M, W, N, K, epi, mm, fill, st, fin, &split);
+    return mm2_launch_splitk_fin<MB, NB, WM_, WN_, STAGES, KS>(Ap, M, W, N, K, epi, mm, fill, st, fin, &split);
 }
 
 // Block tiles of a launch shape (for the dispatch's tile count).
