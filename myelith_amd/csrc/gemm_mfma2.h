@@ -372,7 +372,9 @@ hipError_t mm2w16_launch(const int8_t* Ap, const int32_t* xsum, int M, const int
     // few rows: one plane-row tile streams the weight planes once
     if (M <= 16 && K % 128 == 0) return mm2w16_launch_cfg<1, 1, 1, 4, 3, 128>(Ap, xsum, M, Wp, wsum, N, K, epi, st);
     if (M <= 16) return mm2w16_launch_cfg<1, 1, 1, 4, 4, 64>(Ap, xsum, M, Wp, wsum, N, K, epi, st);
+    if (M <= 32 && K % 128 == 0) return mm2w16_launch_cfg<2, 1, 1, 4, 2, 128>(Ap, xsum, M, Wp, wsum, N, K, epi, st);
     if (M <= 32) return mm2w16_launch_cfg<2, 1, 1, 4, 4, 64>(Ap, xsum, M, Wp, wsum, N, K, epi, st);
+    if (M <= 64 && K % 128 == 0) return mm2w16_launch_cfg<2, 1, 2, 2, 3, 128>(Ap, xsum, M, Wp, wsum, N, K, epi, st);
     if (M <= 64) return mm2w16_launch_cfg<2, 1, 2, 4, 4, 64>(Ap, xsum, M, Wp, wsum, N, K, epi, st);
     using W = Mm2<2, 2, 4, 4, 2, 128>;
     const int wide_tiles = ((2 * M + W::BR - 1) / W::BR) * ((2 * N + W::BN - 1) / W::BN);
