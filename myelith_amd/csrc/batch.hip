@@ -132,7 +132,9 @@ __global__ __launch_bounds__(256) void rope_scatter_kernel(const int16_t* __rest
 }
 
 // Softmax statistics of one (row, head) over its L scores (softmax.rs:32-41):
-// m = max, S = wrapping i32 sum of the exp LUT values.  Grid (heads, R).
+// m = max, S = wrapping i32 sum of the exp LUT values, and the 32-bit
+// reciprocal of a positive S, as stats[(row, head)] = {m, S, recip, 0}.
+// Grid (heads, R).
 __global__ __launch_bounds__(256) void rows_stats_kernel(const int32_t* __restrict__ rows, int rows_cap,
                                                          const int32_t* __restrict__ scores, int heads, int lcap,
                                                          const int16_t* __restrict__ lut, uint32_t lut_len,
@@ -150,8 +152,10 @@ __global__ __launch_bounds__(256) void rows_stats_kernel(const int32_t* __restri
     for (int j = threadIdx.x; j < L; j += 256) s += (uint32_t)exp_lookup(sat_sub32(mx, z[j]), lut, lut_len, lut_shift, lut_one);
     const uint32_t S = block_sum_u32_dpp(s, reds);
     if (threadIdx.x == 0) {
-        stats[((size_t)r * heads + h) * 2] = mx;
-        stats[((size_t)r * heads + h) * 2 + 1] = (int32_t)S;
+        int32_t* o = stats + ((size_t)r * heads + h) * 4;
+        o[0] = mx;
+        o[1] = (int32_t)S;
+        o[2] = (int32_t)((int32_t)S > 0 ? recip32_u32(S) : 0u);  // for softmax_div_round_pos
     }
 }
 
@@ -302,7 +306,7 @@ int ensure_rows(myl_model* m, BatchState* b, int R) {
     b->argmax = balloc<int64_t>(L, R);
     b->xsum = balloc<int32_t>(L, R);
     b->argmax_part = balloc<uint64_t>(L, (size_t)R * ((V + kArgChunk - 1) / kArgChunk));
-    b->stats = balloc<int32_t>(L, (size_t)R * m->spec.heads * 2);
+    b->stats = balloc<int32_t>(L, (size_t)R * m->spec.heads * 4);
     for (void* p : L)
         if (!p) return c->fail(MYL_E_NOMEM, "batch: row buffer allocation");
     b->rows_cap = R;

@@ -220,7 +220,7 @@ __global__ __launch_bounds__(kAttnThreads) void rows_qk_kernel(
 template <int HD, bool LOOP>
 __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
     const AttnTile* __restrict__ tiles, const int32_t* __restrict__ rows, int rows_cap,
-    const int32_t* __restrict__ scores, const int32_t* __restrict__ stats, int heads, int lcap,
+    const int32_t* __restrict__ scores, const int32_t* __restrict__ stats /* [row][head][4] */, int heads, int lcap,
     const int16_t* __restrict__ vc, size_t seq_stride, int max_pos, int G, const int16_t* __restrict__ lut,
     uint32_t lut_len, uint8_t lut_shift, int64_t* __restrict__ part, size_t part_stride, int nq,
     uint8_t v_frac, uint8_t out_frac, int16_t* __restrict__ A, int8_t* __restrict__ planes) {
@@ -254,17 +254,21 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
     if (tid < kAttnQV) {
         p_sum[tid] = 0;
         if (tid < QV) {
-            const size_t si = ((size_t)qv.row[tid] * heads + qv.head[tid]) * 2;
+            const size_t si = ((size_t)qv.row[tid] * heads + qv.head[tid]) * 4;
             const int32_t S = stats[si + 1];
             q_m[tid] = stats[si];
             q_s[tid] = S;
-            q_rs[tid] = recip32(S < 0 ? 0u - (uint32_t)S : (uint32_t)S);
-            q_r32[tid] = S > 0 ? recip32_u32((uint32_t)S) : 0u;
-            const uint32_t L = (uint32_t)qv.pos[tid] + 1u;
-            uint32_t qq, rr;
-            udivmod32((uint32_t)one, L, recip32(L), &qq, &rr);
-            q_ub[tid] = (int32_t)qq;
-            q_ur[tid] = wsub32(one, wmul32((int32_t)qq, (int32_t)L));
+            q_r32[tid] = (uint32_t)stats[si + 2];
+            q_rs[tid] = 0;
+            q_ub[tid] = q_ur[tid] = 0;
+            if (S < 0) q_rs[tid] = recip32(0u - (uint32_t)S);  // a wrapped sum
+            if (S == 0) {  // the uniform split (softmax.rs:42-48)
+                const uint32_t L = (uint32_t)qv.pos[tid] + 1u;
+                uint32_t qq, rr;
+                udivmod32((uint32_t)one, L, recip32(L), &qq, &rr);
+                q_ub[tid] = (int32_t)qq;
+                q_ur[tid] = wsub32(one, wmul32((int32_t)qq, (int32_t)L));
+            }
         }
     }
     const int ntask = MT * NT;
