@@ -60,6 +60,7 @@ struct BatchState {
     int64_t* part = nullptr;             // [lmax_cap / 256][rows_cap][nq]: exact P.V per position range
     AttnTile* tiles = nullptr;           // rows grouped by sequence for the attention kernels
     int ntiles = 0, tiles_cap = 0;
+    int max_qv = 0;                      // largest query-vector count of a tile (rows x G)
     std::vector<void*> allocs_rows;      // row buffers (regrown together)
     std::vector<void*> allocs_scores;
 };
@@ -408,16 +409,29 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         const bool loop = (int64_t)b->ntiles * kvh >= 2 * (int64_t)c->prop.multiProcessorCount;
         const dim3 pg(b->ntiles, kvh, loop ? 1 : ranges);
         int8_t* pplanes = planes ? mm->planes : nullptr;
-#define MYL_PV_LAUNCH(HDV, LOOPV)                                                                                  \
-    rows_pv_kernel<HDV, LOOPV><<<pg, kAttnThreads, attn_pv_lds<HDV>(), st>>>(                                      \
+#define MYL_PV_LAUNCH(HDV, LOOPV, QVMV)                                                                            \
+    rows_pv_kernel<HDV, LOOPV, QVMV><<<pg, kAttnThreads, attn_pv_lds<HDV, QVMV>(), st>>>(                          \
         b->tiles, b->rows, b->rows_cap, b->scores, b->stats, heads, b->lmax_cap, vc, sstride, m->max_pos, G,         \
         m->exp_lut, (uint32_t)m->exp_len, lut_shift, b->part, pst, nq, f.v_frac, f.attn_out_frac, b->A, pplanes)
+        // tiles of at most 32 query vectors (decode batches) take the
+        // narrow variant: 60 KB of LDS, two blocks per CU
+        const bool narrow = b->max_qv <= 32;
         if (hd == 128) {
-            if (loop) MYL_PV_LAUNCH(128, true);
-            else MYL_PV_LAUNCH(128, false);
+            if (narrow) {
+                if (loop) MYL_PV_LAUNCH(128, true, 32);
+                else MYL_PV_LAUNCH(128, false, 32);
+            } else {
+                if (loop) MYL_PV_LAUNCH(128, true, kAttnQV);
+                else MYL_PV_LAUNCH(128, false, kAttnQV);
+            }
         } else {
-            if (loop) MYL_PV_LAUNCH(64, true);
-            else MYL_PV_LAUNCH(64, false);
+            if (narrow) {
+                if (loop) MYL_PV_LAUNCH(64, true, 32);
+                else MYL_PV_LAUNCH(64, false, 32);
+            } else {
+                if (loop) MYL_PV_LAUNCH(64, true, kAttnQV);
+                else MYL_PV_LAUNCH(64, false, kAttnQV);
+            }
         }
 #undef MYL_PV_LAUNCH
         if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -577,6 +591,8 @@ int upload_rows(myl_model* m, BatchState* b, uint32_t R, const uint32_t* seq, co
         b->tiles_cap = (int)tiles.size();
     }
     b->ntiles = (int)tiles.size();
+    b->max_qv = 0;
+    for (const AttnTile& t : tiles) b->max_qv = std::max(b->max_qv, t.n * m->G);
     rc = c->hip(hipMemcpyAsync(b->tiles, tiles.data(), tiles.size() * sizeof(AttnTile), hipMemcpyHostToDevice,
                                c->stream), "batch tiles");
     if (rc) return rc;
@@ -608,12 +624,17 @@ int row_path_setup(myl_model* m) {
     if (rc) return rc;
     for (int16_t v : lut)
         if (v < 0) return c->fail(MYL_E_UNSUPPORTED, "batch: the exp table has negative entries");
-    const std::pair<const void*, size_t> big[6] = {{(const void*)rows_qk_kernel<128>, attn_qk_lds<128>()},
-                                                   {(const void*)rows_qk_kernel<64>, attn_qk_lds<64>()},
-                                                   {(const void*)rows_pv_kernel<128, false>, attn_pv_lds<128>()},
-                                                   {(const void*)rows_pv_kernel<128, true>, attn_pv_lds<128>()},
-                                                   {(const void*)rows_pv_kernel<64, false>, attn_pv_lds<64>()},
-                                                   {(const void*)rows_pv_kernel<64, true>, attn_pv_lds<64>()}};
+    const std::pair<const void*, size_t> big[10] = {
+        {(const void*)rows_qk_kernel<128>, attn_qk_lds<128>()},
+        {(const void*)rows_qk_kernel<64>, attn_qk_lds<64>()},
+        {(const void*)rows_pv_kernel<128, false, kAttnQV>, attn_pv_lds<128, kAttnQV>()},
+        {(const void*)rows_pv_kernel<128, true, kAttnQV>, attn_pv_lds<128, kAttnQV>()},
+        {(const void*)rows_pv_kernel<64, false, kAttnQV>, attn_pv_lds<64, kAttnQV>()},
+        {(const void*)rows_pv_kernel<64, true, kAttnQV>, attn_pv_lds<64, kAttnQV>()},
+        {(const void*)rows_pv_kernel<128, false, 32>, attn_pv_lds<128, 32>()},
+        {(const void*)rows_pv_kernel<128, true, 32>, attn_pv_lds<128, 32>()},
+        {(const void*)rows_pv_kernel<64, false, 32>, attn_pv_lds<64, 32>()},
+        {(const void*)rows_pv_kernel<64, true, 32>, attn_pv_lds<64, 32>()}};
     for (const auto& k : big)
         if (hipFuncSetAttribute(k.first, hipFuncAttributeMaxDynamicSharedMemorySize, (int)k.second) != hipSuccess)
             return c->fail(MYL_E_HIP, "batch: attention LDS size");

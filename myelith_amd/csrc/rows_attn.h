@@ -50,10 +50,15 @@ struct AttnTile {
 template <int HD>
 constexpr size_t attn_qk_lds() { return (size_t)2 * 192 * (HD + 16); }
 
-// LDS bytes of rows_pv_kernel: P planes for kAttnQV vectors and V planes for
-// HD dimensions, each a row of the range's positions (+16 bytes of padding).
-template <int HD>
-constexpr size_t attn_pv_lds() { return (size_t)2 * (kAttnQV + HD) * (kAttnRange + 16); }
+// LDS bytes of rows_pv_kernel: P planes for QVM vectors, each a row of the
+// range's positions (+16 bytes of padding), and V planes for HD dimensions,
+// each a row of one pass's positions (a range in one pass for QVM = 128, in
+// two passes of 128 positions for QVM = 32: 60 KB, two blocks per CU).
+constexpr int attn_pv_passes(int QVM) { return QVM == kAttnQV ? 1 : 2; }
+template <int HD, int QVM = kAttnQV>
+constexpr size_t attn_pv_lds() {
+    return (size_t)2 * QVM * (kAttnRange + 16) + (size_t)2 * HD * (kAttnRange / attn_pv_passes(QVM) + 16);
+}
 
 // Sum of the eight int16 values of a 16-byte chunk.
 __device__ inline int32_t sum8_i16(const uint4 x) {
@@ -217,26 +222,31 @@ __global__ __launch_bounds__(kAttnThreads) void rows_qk_kernel(
     }
 }
 
-template <int HD, bool LOOP>
+template <int HD, bool LOOP, int QVM = kAttnQV>
 __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
     const AttnTile* __restrict__ tiles, const int32_t* __restrict__ rows, int rows_cap,
     const int32_t* __restrict__ scores, const int32_t* __restrict__ stats /* [row][head][4] */, int heads, int lcap,
     const int16_t* __restrict__ vc, size_t seq_stride, int max_pos, int G, const int16_t* __restrict__ lut,
     uint32_t lut_len, uint8_t lut_shift, int64_t* __restrict__ part, size_t part_stride, int nq,
     uint8_t v_frac, uint8_t out_frac, int16_t* __restrict__ A, int8_t* __restrict__ planes) {
-    constexpr int RS = kAttnRange + 16;  // LDS row stride: the range's positions of one vector / dimension
+    static_assert(QVM == kAttnQV || QVM == 32, "tile widths");
+    constexpr int RS = kAttnRange + 16;  // LDS row stride of a P plane: the range's positions of one vector
+    constexpr int VP = attn_pv_passes(QVM);
+    constexpr int PW = kAttnRange / VP;   // positions per V pass
+    constexpr int RSV = PW + 16;          // LDS row stride of a V plane: one pass's positions of a dimension
+    constexpr int SLOTS = PW / 16;        // 16-byte position chunks per V row (the swizzle's range)
     constexpr int NT = HD / 32;
     constexpr int CH = HD / 8, CH_LOG = HD == 128 ? 4 : 3;
     extern __shared__ __align__(16) int8_t lds[];
     int8_t* ph = lds;
-    int8_t* pl = ph + kAttnQV * RS;
-    int8_t* vh = pl + kAttnQV * RS;
-    int8_t* vl = vh + HD * RS;
+    int8_t* pl = ph + QVM * RS;
+    int8_t* vh = pl + QVM * RS;
+    int8_t* vl = vh + HD * RSV;
     __shared__ AttnQv qv;
-    __shared__ int32_t q_m[kAttnQV], q_s[kAttnQV], q_ub[kAttnQV], q_ur[kAttnQV];
-    __shared__ uint64_t q_rs[kAttnQV];
-    __shared__ uint32_t q_r32[kAttnQV];
-    __shared__ int32_t p_sum[kAttnQV], v_sum[HD];
+    __shared__ int32_t q_m[QVM], q_s[QVM], q_ub[QVM], q_ur[QVM];
+    __shared__ uint64_t q_rs[QVM];
+    __shared__ uint32_t q_r32[QVM];
+    __shared__ int32_t p_sum[QVM], v_sum[HD];
     __shared__ int s_pmax;
     const int g = blockIdx.y;
     int QV;
@@ -245,13 +255,13 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
     // one range (blockIdx.z), or every range of the tile in turn (LOOP)
     const int r_first = LOOP ? 0 : (int)blockIdx.z;
     const int r_last = LOOP ? pmax / kAttnRange : (int)blockIdx.z;
-    if (r_first * kAttnRange > pmax) return;
+    if (r_first * kAttnRange > pmax || QV > QVM) return;  // the launcher picks QVM >= every tile's QV
     const int MT = (QV + 31) / 32;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
     const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
-    if (tid < kAttnQV) {
+    if (tid < QVM) {
         p_sum[tid] = 0;
         if (tid < QV) {
             const size_t si = ((size_t)qv.row[tid] * heads + qv.head[tid]) * 4;
@@ -286,8 +296,9 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
         // Every score load of the wave and every V load of the thread is issued
         // before any of them is used (one memory latency instead of one per
         // vector and per item).
-        constexpr int kVpw = kAttnQV / (kAttnThreads / 64);      // vectors per wave
-        constexpr int kVit = (CH * 64 + kAttnThreads - 1) / kAttnThreads;  // V items per thread
+        constexpr int kVpw = QVM / (kAttnThreads / 64);               // vectors per wave
+        constexpr int kGroups = PW / 4;                                // 4-position groups per V pass
+        constexpr int kVit = (CH * kGroups + kAttnThreads - 1) / kAttnThreads;  // V items per thread
         const int q4 = lane, jb = j0 + 4 * q4;
         int4 zv[kVpw];
 #pragma unroll
@@ -299,17 +310,22 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
         }
         const int16_t* vg = vc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD;
         uint4 vw[kVit][4];
+        // V of pass vp: item t = (8-dimension chunk c, 4-position group vq4)
+        auto load_v = [&](int vp) {
 #pragma unroll
-        for (int i = 0; i < kVit; ++i) {
-            const int t = tid + i * kAttnThreads;
-            const int c = t & (CH - 1), vq4 = t >> CH_LOG;
+            for (int i = 0; i < kVit; ++i) {
+                const int t = tid + i * kAttnThreads;
+                const int c = t & (CH - 1), vq4 = t >> CH_LOG;
+                const bool ok = t < CH * kGroups && vp * kGroups + vq4 < 8 * nk;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int j = j0 + 4 * vq4 + k;
-                vw[i][k] = t < CH * 8 * nk && j < max_pos ? *reinterpret_cast<const uint4*>(vg + (size_t)j * HD + c * 8)
-                                                          : make_uint4(0, 0, 0, 0);
+                for (int k = 0; k < 4; ++k) {
+                    const int j = j0 + vp * PW + 4 * vq4 + k;
+                    vw[i][k] = ok && j < max_pos ? *reinterpret_cast<const uint4*>(vg + (size_t)j * HD + c * 8)
+                                                 : make_uint4(0, 0, 0, 0);
+                }
             }
-        }
+        };
+        load_v(0);
         // P planes [vector][position]: a wave per vector, its lanes over the
         // range's 4-position groups (8 * nk <= 64 of them)
 #pragma unroll
@@ -349,35 +365,6 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
             ps = wave_sum_i32(ps);
             if (lane == 0) p_sum[v] = ps;
         }
-        // V planes transposed to [dimension][position]: 8 dimensions x 4 positions per item
-#pragma unroll
-        for (int i = 0; i < kVit; ++i) {
-            const int t = tid + i * kAttnThreads;
-            if (t >= CH * 8 * nk) break;
-            const int c = t & (CH - 1), vq4 = t >> CH_LOG;
-            const uint4 (&w)[4] = vw[i];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                uint32_t hw = 0, lw = 0;
-                int32_t vs = 0;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const uint32_t word = (e >> 1) == 0 ? w[k].x : ((e >> 1) == 1 ? w[k].y : ((e >> 1) == 2 ? w[k].z : w[k].w));
-                    const int32_t x = (int16_t)((e & 1) ? (word >> 16) : (word & 0xFFFFu));
-                    vs += x;
-                    hw |= ((uint32_t)(x >> 8) & 0xFFu) << (8 * k);
-                    lw |= ((uint32_t)((x & 255) - 128) & 0xFFu) << (8 * k);
-                }
-                const int d = c * 8 + e;
-                // 16-byte position chunk (vq4 >> 2) at slot chunk ^ (d >> 3): rows
-                // eight apart no longer share banks
-                const int off = (((vq4 >> 2) ^ (c & 15)) << 4) + 4 * (vq4 & 3);
-                *reinterpret_cast<uint32_t*>(vh + d * RS + off) = hw;
-                *reinterpret_cast<uint32_t*>(vl + d * RS + off) = lw;
-                atomicAdd(&v_sum[d], vs);
-            }
-        }
-        __syncthreads();
         // wave tasks: (query tile, dimension tile) pairs, at most two per wave
         v16i32_t acc[2][3];
 #pragma unroll
@@ -387,26 +374,64 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[a][b][r] = 0;
 #pragma unroll
-        for (int a = 0; a < 2; ++a) {
-            const int task = wave + a * (kAttnThreads / 64);
-            if (task >= ntask) continue;
-            const int mt = task / NT, nt = task - mt * NT;
-            const int8_t* ah_row = ph + (mt * 32 + (lane & 31)) * RS + 16 * (lane >> 5);
-            const int8_t* al_row = pl + (mt * 32 + (lane & 31)) * RS + 16 * (lane >> 5);
-            const int dr = nt * 32 + (lane & 31);
-            const int8_t* bh_row = vh + dr * RS;
-            const int8_t* bl_row = vl + dr * RS;
-            const int sw = (dr >> 3) & 15;
-            for (int kk = 0; kk < nk; ++kk) {
-                const int slot = ((2 * kk + (lane >> 5)) ^ sw) << 4;
-                const v4i32_t ah = *reinterpret_cast<const v4i32_t*>(ah_row + 32 * kk);
-                const v4i32_t al = *reinterpret_cast<const v4i32_t*>(al_row + 32 * kk);
-                const v4i32_t bh = *reinterpret_cast<const v4i32_t*>(bh_row + slot);
-                const v4i32_t bl = *reinterpret_cast<const v4i32_t*>(bl_row + slot);
-                acc[a][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bh, acc[a][0], 0, 0, 0);
-                acc[a][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bl, acc[a][1], 0, 0, 0);
-                acc[a][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bh, acc[a][1], 0, 0, 0);
-                acc[a][2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bl, acc[a][2], 0, 0, 0);
+        for (int vp = 0; vp < VP; ++vp) {
+            if (vp > 0) {
+                __syncthreads();  // the previous pass's V planes are consumed
+                load_v(vp);
+            }
+            // V planes transposed to [dimension][position]: 8 dimensions x 4
+            // positions per item; 16-byte position chunk (vq4 >> 2) at slot
+            // chunk ^ ((d >> 3) % SLOTS), so rows eight apart do not share banks
+#pragma unroll
+            for (int i = 0; i < kVit; ++i) {
+                const int t = tid + i * kAttnThreads;
+                const int c = t & (CH - 1), vq4 = t >> CH_LOG;
+                if (t >= CH * kGroups || vp * kGroups + vq4 >= 8 * nk) continue;
+                const uint4 (&w)[4] = vw[i];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    uint32_t hw = 0, lw = 0;
+                    int32_t vs = 0;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const uint32_t word =
+                            (e >> 1) == 0 ? w[k].x : ((e >> 1) == 1 ? w[k].y : ((e >> 1) == 2 ? w[k].z : w[k].w));
+                        const int32_t x = (int16_t)((e & 1) ? (word >> 16) : (word & 0xFFFFu));
+                        vs += x;
+                        hw |= ((uint32_t)(x >> 8) & 0xFFu) << (8 * k);
+                        lw |= ((uint32_t)((x & 255) - 128) & 0xFFu) << (8 * k);
+                    }
+                    const int d = c * 8 + e;
+                    const int off = (((vq4 >> 2) ^ (c & (SLOTS - 1))) << 4) + 4 * (vq4 & 3);
+                    *reinterpret_cast<uint32_t*>(vh + d * RSV + off) = hw;
+                    *reinterpret_cast<uint32_t*>(vl + d * RSV + off) = lw;
+                    atomicAdd(&v_sum[d], vs);
+                }
+            }
+            __syncthreads();
+            const int k0 = vp * (PW / 32), k1 = min(nk, k0 + PW / 32);  // this pass's 32-position steps
+#pragma unroll
+            for (int a = 0; a < 2; ++a) {
+                const int task = wave + a * (kAttnThreads / 64);
+                if (task >= ntask) continue;
+                const int mt = task / NT, nt = task - mt * NT;
+                const int8_t* ah_row = ph + (mt * 32 + (lane & 31)) * RS + 16 * (lane >> 5);
+                const int8_t* al_row = pl + (mt * 32 + (lane & 31)) * RS + 16 * (lane >> 5);
+                const int dr = nt * 32 + (lane & 31);
+                const int8_t* bh_row = vh + dr * RSV;
+                const int8_t* bl_row = vl + dr * RSV;
+                const int sw = (dr >> 3) & (SLOTS - 1);
+                for (int kk = k0; kk < k1; ++kk) {
+                    const int slot = ((2 * (kk - k0) + (lane >> 5)) ^ sw) << 4;
+                    const v4i32_t ah = *reinterpret_cast<const v4i32_t*>(ah_row + 32 * kk);
+                    const v4i32_t al = *reinterpret_cast<const v4i32_t*>(al_row + 32 * kk);
+                    const v4i32_t bh = *reinterpret_cast<const v4i32_t*>(bh_row + slot);
+                    const v4i32_t bl = *reinterpret_cast<const v4i32_t*>(bl_row + slot);
+                    acc[a][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bh, acc[a][0], 0, 0, 0);
+                    acc[a][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah, bl, acc[a][1], 0, 0, 0);
+                    acc[a][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bh, acc[a][1], 0, 0, 0);
+                    acc[a][2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(al, bl, acc[a][2], 0, 0, 0);
+                }
             }
         }
         const int64_t cterm = 16384 * 32 * (int64_t)nk;

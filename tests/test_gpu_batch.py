@@ -99,6 +99,51 @@ def test_batch_many_rows(backend, hd, lm16):
     compare_batch_kv(gm, om, spec, 1, toks[1])
 
 
+@pytest.mark.parametrize("hd", [128, 64])
+def test_batch_many_sequences(backend, hd):
+    """300 sequences: their 4-token prompts in one batch of 1200 rows, then
+    one row per sequence twice (decode batches).  With this many tiles the
+    attention blocks loop over their ranges and finish the output in place,
+    and the one-row tiles take the narrow P.V variant; every row's logits
+    equal the oracle's."""
+    spec = tiny(hd, 0, 1, 2)
+    case(f"batch many sequences hd={hd}")
+    gm, om = build(backend, spec)
+    r = np.random.default_rng(hd + 11)
+    S, P = 300, 4
+    toks = [r.integers(0, spec["vocab"], P + 2) for _ in range(S)]
+    ref = oracle_rows(om, toks)
+    gm.batch_begin(S)
+    rows = [(s, p) for s in range(S) for p in range(P)]
+    logits, _ = gm.forward_batch([s for s, _ in rows], [p for _, p in rows], [int(toks[s][p]) for s, p in rows])
+    for i, (s, p) in enumerate(rows):
+        assert np.array_equal(logits[i], ref[s][p]), ("prompt row", s, p)
+    for p in (P, P + 1):
+        logits, am = gm.forward_batch(list(range(S)), [p] * S, [int(toks[s][p]) for s in range(S)])
+        for s in range(S):
+            assert np.array_equal(logits[s], ref[s][p]), ("decode row", s, p)
+            assert am[s] == int(np.argmax(ref[s][p]))
+
+
+def test_batch_many_tiles_loop_ranges(backend):
+    """32 sequences x 300 rows (320 attention tiles of 32 rows): the blocks
+    loop over two 256-position ranges each and finish the attention output in
+    place; every row's logits equal the oracle's."""
+    spec = tiny(128, 1, 1, 2)
+    case("batch 32 x 300 rows")
+    gm, om = build(backend, spec)
+    r = np.random.default_rng(5)
+    S, T = 32, 300
+    toks = [r.integers(0, spec["vocab"], T) for _ in range(S)]
+    ref = oracle_rows(om, toks)
+    gm.batch_begin(S)
+    rows = [(s, p) for s in range(S) for p in range(T)]
+    rows = [rows[i] for i in r.permutation(len(rows))]
+    logits, _ = gm.forward_batch([s for s, _ in rows], [p for _, p in rows], [int(toks[s][p]) for s, p in rows])
+    for i, (s, p) in enumerate(rows):
+        assert np.array_equal(logits[i], ref[s][p]), ("row", s, p)
+
+
 def test_batch_decode_greedy_lock_step(backend):
     """Four sequences prefilled to different lengths, then 12 lock-step greedy
     steps on the device: each sequence's tokens equal its own greedy run."""
