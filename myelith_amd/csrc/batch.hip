@@ -341,7 +341,7 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
     const int nqkv = nq + 2 * nkv, heads = (int)m->spec.heads, kvh = (int)m->spec.kv_heads;
     // planes: [2R x max(I, H)] for every product, plus [2R x H] after the
     // first 2R x I bytes for the gate/up input when the SiLU is fused
-    const size_t plane_req = R < 2 ? 0 : (size_t)2 * R * (R > 64 ? (size_t)I + H : (size_t)std::max(I, H));
+    const size_t plane_req = R < 2 ? 0 : (size_t)2 * R * ((size_t)I + H);
     const MmCtx* mm = c->mm_ctx((size_t)R * std::max(2 * I, nqkv), plane_req);
     const size_t sstride = seq_stride(m);
     const int ranges = (lmax + kAttnRange - 1) / kAttnRange;
@@ -351,14 +351,19 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
                         rmsnorm_planes_ok(H) && xvec_ok(b->X, H);
     // the gate/up product applies the SiLU and writes the down product's
     // planes itself (staged epilogue) when its tiles need no K split
-    const bool fuse_silu = planes && R > 64 && I % 8 == 0 && (size_t)2 * R * ((size_t)I + H) <= mm->planes_bytes;
+    // (17-64 rows: the split gate/up product with its own finish and SiLU
+    // measured faster on MI355X than the unsplit fused one)
+    const bool fuse_silu = planes && I % 8 == 0 && (R > 64 || (R <= 16 && H % 128 == 0)) &&
+                           (size_t)2 * R * ((size_t)I + H) <= mm->planes_bytes;
+    int8_t* const xin = mm && mm->planes ? mm->planes + (size_t)2 * R * I : nullptr;  // gate/up input planes
     const uint8_t lut_shift = MYL_TV_SCORE_FRAC_BITS - MYL_TV_EXP_INPUT_FRAC;
     hipError_t e;
     embed_rows_kernel<<<R, 256, 0, st>>>(b->rows + 3 * b->rows_cap, m->emb, m->emb_shifts, m->layers[0].res_in, H, b->X);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    // Without the fused gate/up (few rows), each residual product's split-K
-    // finish also normalises its rows into the next product's planes.
-    const bool norm_in_finish = planes && !fuse_silu;
+    // Each residual product's split-K finish also normalises its rows into
+    // the next product's planes (resid_then_norm; without a split, the
+    // product then rmsnorm_planes).
+    const bool norm_in_finish = planes;
     bool in_normed = false;  // this layer's input planes were written by the previous down product
     for (int l = 0; l < (int)m->spec.layers; ++l) {
         const LayerDev& Ld = m->layers[l];
@@ -445,7 +450,7 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         eo.out_frac = Ld.res_mid; eo.res = b->X; eo.ldr = H; eo.out = b->X2; eo.ldo = H;
         if (norm_in_finish)
             e = resid_then_norm(mm->planes, R, Ld.wo, H, nq, eo, mm, Ld.res_mid, Ld.post_gamma, Ld.post_gamma_s, m,
-                                f.norm_mlp_frac, mm->planes, st);
+                                f.norm_mlp_frac, fuse_silu ? xin : mm->planes, st);
         else
             e = planes ? mm_planes(mm->planes, R, Ld.wo, H, nq, eo, mm, st) : gemv_i8(b->A, R, nq, Ld.wo, H, nq, eo, st, mm);
         if (e != hipSuccess) return e;
@@ -453,14 +458,10 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         eg.shifts = Ld.sgu; eg.act_frac = f.norm_mlp_frac; eg.gate_frac = f.gate_frac; eg.up_frac = f.up_frac;
         eg.out = b->GU; eg.ldo = 2 * I;
         if (fuse_silu) {
-            int8_t* xin = mm->planes + (size_t)2 * R * I;
+            // the post-attention norm's planes (xin) come from the o_proj finish
             EpiGUSiluPlanes es{Ld.sgu, f.norm_mlp_frac, f.gate_frac, f.up_frac, f.down_in_frac,
                                m->silu, (uint32_t)m->silu_len, mm->planes, I};
-            if ((e = rmsnorm_planes(b->X2, R, H, Ld.res_mid, Ld.post_gamma, Ld.post_gamma_s, H, m->rsqrt,
-                                    m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20,
-                                    f.norm_mlp_frac, xin, st)) != hipSuccess ||
-                (e = mm_planes_staged(xin, R, Ld.wgu, 2 * I, H, es, mm, st)) != hipSuccess)
-                return e;
+            if ((e = mm_planes_staged(xin, R, Ld.wgu, 2 * I, H, es, mm, st)) != hipSuccess) return e;
         } else if (planes) {
             // the post-attention norm's planes come from the o_proj finish
             if ((e = mm_planes(mm->planes, R, Ld.wgu, 2 * I, H, eg, mm, st)) != hipSuccess) return e;

@@ -159,12 +159,19 @@ inline hipError_t mm_planes_fin(const int8_t* Ap, int M, const int8_t* W, int N,
     return mm_planes(Ap, M, W, N, K, epi, mm, st);
 }
 
-// The gate/up product with the staged epilogue (EpiGUSiluPlanes), for more
-// than 64 rows and N % 16 == 0: the tiles of mm_planes without a K split.
+// The gate/up product with the staged epilogue (EpiGUSiluPlanes), N % 16 ==
+// 0, without a K split: up to 64 rows, 32/64/128-row plane tiles x 64 weight
+// rows with 128-byte stages (K % 128 == 0: enough tiles without a split for
+// the 7B gate/up; the batched forward uses it up to 16 rows); more rows, the
+// tiles of mm_planes.
 template <class Epi>
 inline hipError_t mm_planes_staged(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi,
                                    const MmCtx* mm, hipStream_t st) {
-    if (M <= 64 || N % 16 != 0 || K % 64 != 0) return hipErrorInvalidValue;
+    if (M < 2 || N % 16 != 0 || K % 64 != 0) return hipErrorInvalidValue;
+    if (M <= 64 && K % 128 != 0) return hipErrorInvalidValue;
+    if (M <= 16) return mm2_staged_launch<1, 1, 1, 2, 4, 128>(Ap, M, W, N, K, epi, st);
+    if (M <= 32) return mm2_staged_launch<2, 1, 1, 2, 4, 128>(Ap, M, W, N, K, epi, st);
+    if (M <= 64) return mm2_staged_launch<2, 1, 2, 2, 4, 128>(Ap, M, W, N, K, epi, st);
     if (mm_wide_tiles(M, N, K, mm->cus)) return mm2_staged_launch<2, 2, 4, 4, 2, 128>(Ap, M, W, N, K, epi, st);
     return mm2_staged_launch<2, 2, 4, 2, 3, 64>(Ap, M, W, N, K, epi, st);
 }
