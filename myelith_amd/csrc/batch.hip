@@ -56,7 +56,7 @@ struct BatchState {
     int64_t* tokens_out = nullptr;       // greedy chains: [steps][rows]
     size_t tokens_out_cap = 0;
     int32_t* scores = nullptr;           // [rows_cap][heads][lmax_cap]
-    int32_t* stats = nullptr;            // [rows_cap][heads][2]: max, wrapping exp sum
+    int16_t* probs = nullptr;            // [rows_cap][heads][lmax_cap] softmax probabilities (Q14)
     int64_t* part = nullptr;             // [lmax_cap / 256][rows_cap][nq]: exact P.V per position range
     AttnTile* tiles = nullptr;           // rows grouped by sequence for the attention kernels
     int ntiles = 0, tiles_cap = 0;
@@ -132,31 +132,57 @@ __global__ __launch_bounds__(256) void rope_scatter_kernel(const int16_t* __rest
     dst[p + half] = y1;
 }
 
-// Softmax statistics of one (row, head) over its L scores (softmax.rs:32-41):
-// m = max, S = wrapping i32 sum of the exp LUT values, and the 32-bit
-// reciprocal of a positive S, as stats[(row, head)] = {m, S, recip, 0}.
-// Grid (heads, R).
-__global__ __launch_bounds__(256) void rows_stats_kernel(const int32_t* __restrict__ rows, int rows_cap,
+// softmax.rs:12-64 for one (row, head) over its L scores: m = max, S =
+// wrapping i32 sum of the exp LUT values, then every probability
+// p_j = RNE(e_j 2^14 / S) (or the uniform split when S == 0) as an int16
+// (0 <= p <= 2^14 for a non-negative exp table) into probs[row][head][j],
+// j < L.  Grid (heads, R), 256 threads.
+__global__ __launch_bounds__(256) void rows_probs_kernel(const int32_t* __restrict__ rows, int rows_cap,
                                                          const int32_t* __restrict__ scores, int heads, int lcap,
                                                          const int16_t* __restrict__ lut, uint32_t lut_len,
-                                                         uint8_t lut_shift, int32_t* __restrict__ stats) {
+                                                         uint8_t lut_shift, int16_t* __restrict__ probs) {
     __shared__ int32_t redm[4];
     __shared__ uint32_t reds[4];
+    __shared__ uint64_t s_recip;
+    __shared__ uint32_t s_r32;
+    __shared__ int32_t s_ub, s_ur;
     const int h = blockIdx.x, r = blockIdx.y;
     const int L = rows[rows_cap + r] + 1;
-    const int32_t* z = scores + ((size_t)r * heads + h) * lcap;
+    const size_t o = ((size_t)r * heads + h) * lcap;
+    const int32_t* z = scores + o;
     const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
+    const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
     int32_t mx = INT32_MIN;
     for (int j = threadIdx.x; j < L; j += 256) mx = max(mx, z[j]);
     mx = block_max_i32_dpp(mx, redm);
     uint32_t s = 0;
     for (int j = threadIdx.x; j < L; j += 256) s += (uint32_t)exp_lookup(sat_sub32(mx, z[j]), lut, lut_len, lut_shift, lut_one);
-    const uint32_t S = block_sum_u32_dpp(s, reds);
+    const int32_t S = (int32_t)block_sum_u32_dpp(s, reds);
     if (threadIdx.x == 0) {
-        int32_t* o = stats + ((size_t)r * heads + h) * 4;
-        o[0] = mx;
-        o[1] = (int32_t)S;
-        o[2] = (int32_t)((int32_t)S > 0 ? recip32_u32(S) : 0u);  // for softmax_div_round_pos
+        s_r32 = S > 0 ? recip32_u32((uint32_t)S) : 0u;
+        s_recip = S < 0 ? recip32(0u - (uint32_t)S) : 0u;  // a wrapped sum
+        s_ub = s_ur = 0;
+        if (S == 0) {
+            uint32_t qq, rr;
+            udivmod32((uint32_t)one, (uint32_t)L, recip32((uint32_t)L), &qq, &rr);
+            s_ub = (int32_t)qq;
+            s_ur = wsub32(one, wmul32((int32_t)qq, L));
+        }
+    }
+    __syncthreads();
+    const uint32_t r32 = s_r32;
+    const uint64_t recip = s_recip;
+    const int32_t ub = s_ub, ur = s_ur;
+    int16_t* pr = probs + o;
+    for (int j = threadIdx.x; j < L; j += 256) {
+        int32_t p;
+        if (S == 0) {
+            p = ub + (((uint64_t)j < (uint64_t)(int64_t)ur) ? 1 : 0);
+        } else {
+            const int32_t e = exp_lookup(sat_sub32(mx, z[j]), lut, lut_len, lut_shift, lut_one);
+            p = S > 0 ? softmax_div_round_pos(wmul32(e, one), S, r32) : softmax_div_round(wmul32(e, one), S, recip);
+        }
+        pr[j] = (int16_t)p;
     }
 }
 
@@ -307,7 +333,6 @@ int ensure_rows(myl_model* m, BatchState* b, int R) {
     b->argmax = balloc<int64_t>(L, R);
     b->xsum = balloc<int32_t>(L, R);
     b->argmax_part = balloc<uint64_t>(L, (size_t)R * ((V + kArgChunk - 1) / kArgChunk));
-    b->stats = balloc<int32_t>(L, (size_t)R * m->spec.heads * 4);
     for (void* p : L)
         if (!p) return c->fail(MYL_E_NOMEM, "batch: row buffer allocation");
     b->rows_cap = R;
@@ -324,8 +349,9 @@ int ensure_scores(myl_model* m, BatchState* b, int lmax) {
     b->lmax_cap = 0;
     const int cap = ((lmax + kAttnRange - 1) / kAttnRange) * kAttnRange;
     b->scores = balloc<int32_t>(b->allocs_scores, (size_t)b->rows_cap * m->spec.heads * cap);
+    b->probs = balloc<int16_t>(b->allocs_scores, (size_t)b->rows_cap * m->spec.heads * cap);
     b->part = balloc<int64_t>(b->allocs_scores, (size_t)(cap / kAttnRange) * b->rows_cap * m->nq);
-    if (!b->scores || !b->part) return c->fail(MYL_E_NOMEM, "batch: score buffer allocation");
+    if (!b->scores || !b->probs || !b->part) return c->fail(MYL_E_NOMEM, "batch: score buffer allocation");
     b->lmax_cap = cap;
     return MYL_OK;
 }
@@ -405,8 +431,8 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
                 b->tiles, b->rows, b->rows_cap, b->Q, nq, kc, sstride, m->max_pos, G, m->score_mult, score_shift,
                 b->scores, heads, b->lmax_cap);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        rows_stats_kernel<<<dim3(heads, R), 256, 0, st>>>(b->rows, b->rows_cap, b->scores, heads, b->lmax_cap,
-                                                          m->exp_lut, (uint32_t)m->exp_len, lut_shift, b->stats);
+        rows_probs_kernel<<<dim3(heads, R), 256, 0, st>>>(b->rows, b->rows_cap, b->scores, heads, b->lmax_cap,
+                                                          m->exp_lut, (uint32_t)m->exp_len, lut_shift, b->probs);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // Big grids (prefill) loop each block over its tile's ranges and
         // finish the attention output in place; small ones (decode batches)
@@ -416,8 +442,8 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         int8_t* pplanes = planes ? mm->planes : nullptr;
 #define MYL_PV_LAUNCH(HDV, LOOPV, QVMV)                                                                            \
     rows_pv_kernel<HDV, LOOPV, QVMV><<<pg, kAttnThreads, attn_pv_lds<HDV, QVMV>(), st>>>(                          \
-        b->tiles, b->rows, b->rows_cap, b->scores, b->stats, heads, b->lmax_cap, vc, sstride, m->max_pos, G,         \
-        m->exp_lut, (uint32_t)m->exp_len, lut_shift, b->part, pst, nq, f.v_frac, f.attn_out_frac, b->A, pplanes)
+        b->tiles, b->rows, b->rows_cap, b->probs, heads, b->lmax_cap, vc, sstride, m->max_pos, G, b->part, pst, nq,  \
+        f.v_frac, f.attn_out_frac, b->A, pplanes)
         // tiles of at most 32 query vectors (decode batches) take the
         // narrow variant: 60 KB of LDS, two blocks per CU
         const bool narrow = b->max_qv <= 32;
@@ -619,12 +645,18 @@ int row_path_setup(myl_model* m) {
     myl_ctx* c = m->ctx;
     if (m->G > 16) return c->fail(MYL_E_UNSUPPORTED, "batch: at most 16 query heads per KV head");
     // The matrix-core P.V splits probabilities into bytes; they stay within
-    // [0, 2^14] when every exp-table entry is non-negative (S >= e_j).
+    // [0, 2^14] when every exp-table entry is non-negative and no exp sum
+    // over max_pos positions wraps (then S >= e_j).
     std::vector<int16_t> lut(m->exp_len);
     int rc = c->hip(hipMemcpy(lut.data(), m->exp_lut, lut.size() * 2, hipMemcpyDeviceToHost), "batch: exp table");
     if (rc) return rc;
-    for (int16_t v : lut)
+    int64_t lut_max = 1;  // an empty table reads as 1 (exp_lookup)
+    for (int16_t v : lut) {
         if (v < 0) return c->fail(MYL_E_UNSUPPORTED, "batch: the exp table has negative entries");
+        lut_max = std::max<int64_t>(lut_max, v);
+    }
+    if (lut_max * (int64_t)m->max_pos > (int64_t)INT32_MAX)
+        return c->fail(MYL_E_UNSUPPORTED, "batch: exp sums over max_pos positions could wrap");
     const std::pair<const void*, size_t> big[10] = {
         {(const void*)rows_qk_kernel<128>, attn_qk_lds<128>()},
         {(const void*)rows_qk_kernel<64>, attn_qk_lds<64>()},

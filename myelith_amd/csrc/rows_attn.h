@@ -13,14 +13,16 @@
 //
 //   rows_qk_kernel   s_j = (i32)RNE(q . k_j * mult, shift) for j <= pos, written
 //                    to scores[row][head][j]                  (attention.rs:66-67)
-//   rows_stats_kernel (batch.hip) max and wrapping exp-LUT sum per (row, head)
-//   rows_pv_kernel   p_j = RNE(e_j 2^14 / S) (or the uniform split when S = 0,
-//                    softmax.rs:42-63), then sum_j p_j v_j exactly as int64 per
-//                    256-position range, written to part[range][row][q dim];
-//                    p in [0, 2^14] (a non-negative exp table) so p >> 8 <= 64.
-//                    The range's P planes and transposed V planes are built in
-//                    LDS in one phase (every load in flight at once), then the
-//                    products run over its 32-position steps
+//   rows_probs_kernel (batch.hip) per (row, head): max, wrapping exp-LUT sum
+//                    S, then p_j = RNE(e_j 2^14 / S) (or the uniform split when
+//                    S = 0, softmax.rs:42-63) as int16 into probs[row][head][j];
+//                    p in [0, 2^14] (a non-negative exp table whose sums do not
+//                    wrap) so p >> 8 <= 64
+//   rows_pv_kernel   sum_j p_j v_j exactly as int64 per 256-position range,
+//                    written to part[range][row][q dim].  The range's P planes
+//                    and transposed V planes are built in LDS in one phase
+//                    (every load in flight at once), then the products run over
+//                    its 32-position steps
 //   rows_attn_out    sums the ranges, RNE by 14, clamps (attention.rs:84-86),
 //                    then the attn_out rescale (model.rs:563-567)
 // Each kernel's grid is (tiles, KV heads, 256-position ranges); a block whose
@@ -225,9 +227,8 @@ __global__ __launch_bounds__(kAttnThreads) void rows_qk_kernel(
 template <int HD, bool LOOP, int QVM = kAttnQV>
 __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
     const AttnTile* __restrict__ tiles, const int32_t* __restrict__ rows, int rows_cap,
-    const int32_t* __restrict__ scores, const int32_t* __restrict__ stats /* [row][head][4] */, int heads, int lcap,
-    const int16_t* __restrict__ vc, size_t seq_stride, int max_pos, int G, const int16_t* __restrict__ lut,
-    uint32_t lut_len, uint8_t lut_shift, int64_t* __restrict__ part, size_t part_stride, int nq,
+    const int16_t* __restrict__ probs /* [row][head][lcap] */, int heads, int lcap, const int16_t* __restrict__ vc,
+    size_t seq_stride, int max_pos, int G, int64_t* __restrict__ part, size_t part_stride, int nq,
     uint8_t v_frac, uint8_t out_frac, int16_t* __restrict__ A, int8_t* __restrict__ planes) {
     static_assert(QVM == kAttnQV || QVM == 32, "tile widths");
     constexpr int RS = kAttnRange + 16;  // LDS row stride of a P plane: the range's positions of one vector
@@ -243,9 +244,6 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
     int8_t* vh = pl + QVM * RS;
     int8_t* vl = vh + HD * RSV;
     __shared__ AttnQv qv;
-    __shared__ int32_t q_m[QVM], q_s[QVM], q_ub[QVM], q_ur[QVM];
-    __shared__ uint64_t q_rs[QVM];
-    __shared__ uint32_t q_r32[QVM];
     __shared__ int32_t p_sum[QVM], v_sum[HD];
     __shared__ int s_pmax;
     const int g = blockIdx.y;
@@ -259,28 +257,6 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
     const int MT = (QV + 31) / 32;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
-    const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
-    if (tid < QVM) {
-        p_sum[tid] = 0;
-        if (tid < QV) {
-            const size_t si = ((size_t)qv.row[tid] * heads + qv.head[tid]) * 4;
-            const int32_t S = stats[si + 1];
-            q_m[tid] = stats[si];
-            q_s[tid] = S;
-            q_r32[tid] = (uint32_t)stats[si + 2];
-            q_rs[tid] = 0;
-            q_ub[tid] = q_ur[tid] = 0;
-            if (S < 0) q_rs[tid] = recip32(0u - (uint32_t)S);  // a wrapped sum
-            if (S == 0) {  // the uniform split (softmax.rs:42-48)
-                const uint32_t L = (uint32_t)qv.pos[tid] + 1u;
-                uint32_t qq, rr;
-                udivmod32((uint32_t)one, L, recip32(L), &qq, &rr);
-                q_ub[tid] = (int32_t)qq;
-                q_ur[tid] = wsub32(one, wmul32((int32_t)qq, (int32_t)L));
-            }
-        }
-    }
     const int ntask = MT * NT;
     // exact P.V sums of the block's (vector, dimension) outputs over its ranges
     int64_t tot[2][16];
@@ -293,20 +269,20 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
         const int nk = (min(j0 + kAttnRange, pmax + 1) - j0 + 31) / 32;  // 32-position steps
         if (tid < HD) v_sum[tid] = 0;
         __syncthreads();
-        // Every score load of the wave and every V load of the thread is issued
-        // before any of them is used (one memory latency instead of one per
-        // vector and per item).
+        // Every probability load of the wave and every V load of the thread is
+        // issued before any of them is used (one memory latency instead of one
+        // per vector and per item).
         constexpr int kVpw = QVM / (kAttnThreads / 64);               // vectors per wave
         constexpr int kGroups = PW / 4;                                // 4-position groups per V pass
         constexpr int kVit = (CH * kGroups + kAttnThreads - 1) / kAttnThreads;  // V items per thread
         const int q4 = lane, jb = j0 + 4 * q4;
-        int4 zv[kVpw];
+        uint2 pv4[kVpw];
 #pragma unroll
         for (int i = 0; i < kVpw; ++i) {
             const int v = wave + i * (kAttnThreads / 64);
-            zv[i] = make_int4(0, 0, 0, 0);
+            pv4[i] = make_uint2(0, 0);
             if (q4 < 8 * nk && v < QV && jb <= qv.pos[v])
-                zv[i] = *reinterpret_cast<const int4*>(scores + ((size_t)qv.row[v] * heads + qv.head[v]) * lcap + jb);
+                pv4[i] = *reinterpret_cast<const uint2*>(probs + ((size_t)qv.row[v] * heads + qv.head[v]) * lcap + jb);
         }
         const int16_t* vg = vc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD;
         uint4 vw[kVit][4];
@@ -336,23 +312,13 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
             int32_t ps = 0;
             if (q4 < 8 * nk && v < QV && jb <= qv.pos[v]) {
                 const int pos = qv.pos[v];
-                const int32_t zz[4] = {zv[i].x, zv[i].y, zv[i].z, zv[i].w};
+                const uint32_t pw[2] = {pv4[i].x, pv4[i].y};
                 lw = 0;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const int j = jb + k;
-                    int32_t p = 0;
-                    if (j <= pos) {
-                        if (q_s[v] == 0) {
-                            p = q_ub[v] + (((uint64_t)j < (uint64_t)(int64_t)q_ur[v]) ? 1 : 0);
-                        } else {
-                            const int32_t e = exp_lookup(sat_sub32(q_m[v], zz[k]), lut, lut_len, lut_shift, lut_one);
-                            // e * 2^14 >= 0 (a non-negative exp table); the
-                            // sum is positive unless it wrapped
-                            p = q_s[v] > 0 ? softmax_div_round_pos(wmul32(e, one), q_s[v], q_r32[v])
-                                           : softmax_div_round(wmul32(e, one), q_s[v], q_rs[v]);
-                        }
-                    }
+                    // positions past the row's own are not its probabilities
+                    const int32_t p =
+                        jb + k <= pos ? (int32_t)(int16_t)((k & 1) ? (pw[k >> 1] >> 16) : (pw[k >> 1] & 0xFFFFu)) : 0;
                     ps += p;
                     hw |= ((uint32_t)(p >> 8) & 0xFFu) << (8 * k);
                     lw |= ((uint32_t)((p & 255) - 128) & 0xFFu) << (8 * k);
