@@ -14,6 +14,7 @@ current stream (plumbing only: the arithmetic is in the HIP kernels).
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 
 import numpy as np
 
@@ -42,6 +43,9 @@ class RocmBackend:
             raise MylError(f"RocmBackend::init({device_id}) failed with status {rc}")
         self._h = h
         self._device_id = device_id
+        # models and MoE layers on this context: closed before it is destroyed,
+        # whatever order the interpreter finalises them in
+        self._owned = weakref.WeakSet()
         arch = C.create_string_buffer(128)
         cus = C.c_int()
         hbm = C.c_uint64()
@@ -74,8 +78,15 @@ class RocmBackend:
     def handle(self):
         return self._h
 
+    def adopt(self, obj) -> None:
+        """Registers an object holding device state of this context; close()
+        closes it first."""
+        self._owned.add(obj)
+
     def close(self) -> None:
         if self._h:
+            for obj in list(self._owned):
+                obj.close()
             lib().myl_destroy(self._h)
             self._h = None
 

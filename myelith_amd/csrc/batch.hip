@@ -135,54 +135,121 @@ __global__ __launch_bounds__(256) void rope_scatter_kernel(const int16_t* __rest
 // softmax.rs:12-64 for one (row, head) over its L scores: m = max, S =
 // wrapping i32 sum of the exp LUT values, then every probability
 // p_j = RNE(e_j 2^14 / S) (or the uniform split when S == 0) as an int16
-// (0 <= p <= 2^14 for a non-negative exp table) into probs[row][head][j],
-// j < L.  Grid (heads, R), 256 threads.
+// into probs[row][head][j], j < L (the rest of the last 4-position group gets
+// 0; later positions are not written, and their readers mask them).
+// W waves per (row, head) (pair = row * heads + head), 4 / W pairs per
+// 256-thread block; a thread takes 4 positions of each chunk of 256 W.
+// Rows of up to 2048 (W = 1) or 4096 (W = 4) positions keep their scores,
+// then their exp values, in registers; longer ones read the scores three times.
+template <int W>
 __global__ __launch_bounds__(256) void rows_probs_kernel(const int32_t* __restrict__ rows, int rows_cap,
                                                          const int32_t* __restrict__ scores, int heads, int lcap,
-                                                         const int16_t* __restrict__ lut, uint32_t lut_len,
+                                                         int npairs, const int16_t* __restrict__ lut, uint32_t lut_len,
                                                          uint8_t lut_shift, int16_t* __restrict__ probs) {
+    static_assert(W == 1 || W == 4, "waves per pair");
+    constexpr int CW = 256 * W;      // positions per chunk
+    constexpr int KPER = W == 1 ? 8 : 4;  // register-resident chunks (2048 / 4096 positions)
     __shared__ int32_t redm[4];
     __shared__ uint32_t reds[4];
-    __shared__ uint64_t s_recip;
-    __shared__ uint32_t s_r32;
-    __shared__ int32_t s_ub, s_ur;
-    const int h = blockIdx.x, r = blockIdx.y;
-    const int L = rows[rows_cap + r] + 1;
-    const size_t o = ((size_t)r * heads + h) * lcap;
+    const int t = W == 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
+    const int pair = W == 1 ? (int)(blockIdx.x * 4 + (threadIdx.x >> 6)) : (int)blockIdx.x;
+    if (pair >= npairs) return;  // uniform over the pair's waves: every reduction sees all of them
+    const int L = rows[rows_cap + pair / heads] + 1;
+    const size_t o = (size_t)pair * lcap;
     const int32_t* z = scores + o;
+    int16_t* pr = probs + o;
     const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
     const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
+    const int nc = (L + CW - 1) / CW;
+    const bool regs = nc <= KPER;
+    int32_t e[KPER][4];
     int32_t mx = INT32_MIN;
-    for (int j = threadIdx.x; j < L; j += 256) mx = max(mx, z[j]);
-    mx = block_max_i32_dpp(mx, redm);
-    uint32_t s = 0;
-    for (int j = threadIdx.x; j < L; j += 256) s += (uint32_t)exp_lookup(sat_sub32(mx, z[j]), lut, lut_len, lut_shift, lut_one);
-    const int32_t S = (int32_t)block_sum_u32_dpp(s, reds);
-    if (threadIdx.x == 0) {
-        s_r32 = S > 0 ? recip32_u32((uint32_t)S) : 0u;
-        s_recip = S < 0 ? recip32(0u - (uint32_t)S) : 0u;  // a wrapped sum
-        s_ub = s_ur = 0;
-        if (S == 0) {
-            uint32_t qq, rr;
-            udivmod32((uint32_t)one, (uint32_t)L, recip32((uint32_t)L), &qq, &rr);
-            s_ub = (int32_t)qq;
-            s_ur = wsub32(one, wmul32((int32_t)qq, L));
+    if (regs) {
+#pragma unroll
+        for (int c = 0; c < KPER; ++c) {
+            const int jb = c * CW + 4 * t;
+            int4 v = make_int4(INT32_MIN, INT32_MIN, INT32_MIN, INT32_MIN);
+            if (c < nc && jb < L) v = *reinterpret_cast<const int4*>(z + jb);  // jb + 3 < lcap
+            e[c][0] = jb < L ? v.x : INT32_MIN;
+            e[c][1] = jb + 1 < L ? v.y : INT32_MIN;
+            e[c][2] = jb + 2 < L ? v.z : INT32_MIN;
+            e[c][3] = jb + 3 < L ? v.w : INT32_MIN;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) mx = max(mx, e[c][k]);
+        }
+    } else {
+        for (int jb = 4 * t; jb < L; jb += CW) {
+            const int4 v = *reinterpret_cast<const int4*>(z + jb);
+            const int32_t zz[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (jb + k < L) mx = max(mx, zz[k]);
         }
     }
-    __syncthreads();
-    const uint32_t r32 = s_r32;
-    const uint64_t recip = s_recip;
-    const int32_t ub = s_ub, ur = s_ur;
-    int16_t* pr = probs + o;
-    for (int j = threadIdx.x; j < L; j += 256) {
-        int32_t p;
-        if (S == 0) {
-            p = ub + (((uint64_t)j < (uint64_t)(int64_t)ur) ? 1 : 0);
-        } else {
-            const int32_t e = exp_lookup(sat_sub32(mx, z[j]), lut, lut_len, lut_shift, lut_one);
-            p = S > 0 ? softmax_div_round_pos(wmul32(e, one), S, r32) : softmax_div_round(wmul32(e, one), S, recip);
+    mx = W == 1 ? wave_max_i32(mx) : block_max_i32_dpp(mx, redm);
+    uint32_t s = 0;
+    if (regs) {
+#pragma unroll
+        for (int c = 0; c < KPER; ++c) {
+            const int jb = c * CW + 4 * t;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                e[c][k] = jb + k < L ? exp_lookup(sat_sub32(mx, e[c][k]), lut, lut_len, lut_shift, lut_one) : 0;
+                s += (uint32_t)e[c][k];
+            }
         }
-        pr[j] = (int16_t)p;
+    } else {
+        for (int jb = 4 * t; jb < L; jb += CW) {
+            const int4 v = *reinterpret_cast<const int4*>(z + jb);
+            const int32_t zz[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (jb + k < L) s += (uint32_t)exp_lookup(sat_sub32(mx, zz[k]), lut, lut_len, lut_shift, lut_one);
+        }
+    }
+    const int32_t S = W == 1 ? wave_sum_i32((int32_t)s) : (int32_t)block_sum_u32_dpp(s, reds);
+    int32_t ub = 0, ur = 0;
+    uint32_t r32 = 0;
+    uint64_t recip = 0;
+    if (S > 0) {
+        r32 = recip32_u32((uint32_t)S);
+    } else if (S < 0) {
+        recip = recip32(0u - (uint32_t)S);  // a wrapped sum
+    } else {  // the uniform split (softmax.rs:42-48)
+        uint32_t qq, rr;
+        udivmod32((uint32_t)one, (uint32_t)L, recip32((uint32_t)L), &qq, &rr);
+        ub = (int32_t)qq;
+        ur = wsub32(one, wmul32((int32_t)qq, L));
+    }
+    auto emit = [&](int jb, const int32_t (&ev)[4]) {
+        uint32_t pw[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int j = jb + k;
+            int32_t p = 0;
+            if (j < L) {
+                if (S == 0) p = ub + (((uint64_t)j < (uint64_t)(int64_t)ur) ? 1 : 0);
+                else if (S > 0) p = softmax_div_round_pos(wmul32(ev[k], one), S, r32);
+                else p = softmax_div_round(wmul32(ev[k], one), S, recip);
+            }
+            pw[k] = (uint32_t)p & 0xFFFFu;
+        }
+        *reinterpret_cast<uint2*>(pr + jb) = make_uint2(pw[0] | (pw[1] << 16), pw[2] | (pw[3] << 16));
+    };
+    if (regs) {
+#pragma unroll
+        for (int c = 0; c < KPER; ++c)
+            if (c < nc && c * CW + 4 * t < L) emit(c * CW + 4 * t, e[c]);
+        return;
+    }
+    for (int jb = 4 * t; jb < L; jb += CW) {
+        const int4 v = *reinterpret_cast<const int4*>(z + jb);
+        const int32_t zz[4] = {v.x, v.y, v.z, v.w};
+        int32_t ev[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            ev[k] = jb + k < L ? exp_lookup(sat_sub32(mx, zz[k]), lut, lut_len, lut_shift, lut_one) : 0;
+        emit(jb, ev);
     }
 }
 
@@ -431,8 +498,16 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
                 b->tiles, b->rows, b->rows_cap, b->Q, nq, kc, sstride, m->max_pos, G, m->score_mult, score_shift,
                 b->scores, heads, b->lmax_cap);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        rows_probs_kernel<<<dim3(heads, R), 256, 0, st>>>(b->rows, b->rows_cap, b->scores, heads, b->lmax_cap,
-                                                          m->exp_lut, (uint32_t)m->exp_len, lut_shift, b->probs);
+        // a wave per (row, head) when there are enough of them to fill the
+        // chip, else a block of four waves each
+        const int npairs = R * heads;
+        if (npairs >= 16 * c->prop.multiProcessorCount)
+            rows_probs_kernel<1><<<(npairs + 3) / 4, 256, 0, st>>>(b->rows, b->rows_cap, b->scores, heads, b->lmax_cap,
+                                                                   npairs, m->exp_lut, (uint32_t)m->exp_len, lut_shift,
+                                                                   b->probs);
+        else
+            rows_probs_kernel<4><<<npairs, 256, 0, st>>>(b->rows, b->rows_cap, b->scores, heads, b->lmax_cap, npairs,
+                                                         m->exp_lut, (uint32_t)m->exp_len, lut_shift, b->probs);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // Big grids (prefill) loop each block over its tile's ranges and
         // finish the attention output in place; small ones (decode batches)

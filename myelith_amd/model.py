@@ -58,6 +58,7 @@ class IntegerModel:
             backend.check(lib().myl_model_create_synthetic(backend.handle, C.byref(cspec), C.byref(cl),
                                                            C.byref(_handle)), "model_create_synthetic")
         self._h = _handle
+        backend.adopt(self)
         self.vocab_size = spec["vocab"]
         self.hidden_size = spec["hidden"]
         self.num_layers = spec["layers"]

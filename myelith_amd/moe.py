@@ -67,6 +67,7 @@ class MoeLayer:
         backend.check(lib().myl_moe_create_synthetic(backend.handle, C.byref(cs), self.bias.ctypes.data, C.byref(cl),
                                                      C.byref(h)), "moe_create_synthetic")
         self._h = h
+        backend.adopt(self)
 
     def close(self) -> None:
         if getattr(self, "_h", None):

@@ -191,3 +191,18 @@ def test_prefill_rows_match_the_token_loop(backend, hd, lm16, kvh):
     for i, t in enumerate(p2[:5]):
         o = om.forward_token(t, 338 + i)
     assert np.array_equal(g, o)
+
+
+@pytest.mark.gpu
+def test_backend_close_closes_its_models():
+    """A model still referenced when its backend closes (as a failed test's
+    frames keep it) is closed first, so its later finalisation does nothing."""
+    from myelith_amd.backend import RocmBackend
+    from myelith_amd.model import IntegerModel
+    case("backend close order")
+    b = RocmBackend(0)
+    m = IntegerModel(b, tiny())
+    b.close()
+    assert m._h is None
+    m.close()
+    del m
