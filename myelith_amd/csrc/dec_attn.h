@@ -75,44 +75,11 @@ __device__ inline void dec_scores(int L, int base, const int16_t* __restrict__ q
     }
 }
 
-// Softmax statistics of one query head over its L scores (softmax.rs:32-41):
-// m = max, S = wrapping i32 sum of the exp LUT.  Whole block (256 threads).
-__device__ inline void dec_stats(int L, const int32_t* __restrict__ z, const int16_t* __restrict__ lut,
-                                 uint32_t lut_len, uint8_t lut_shift, int32_t& m, int32_t& S) {
-    constexpr int ZPER = 16;  // scores held in registers per thread
-    __shared__ int32_t redm[4];
-    __shared__ uint32_t reds[4];
-    const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
-    int32_t mx = INT32_MIN;
-    uint32_t s = 0;
-    if (L <= 256 * ZPER) {
-        int32_t zz[ZPER];
-#pragma unroll
-        for (int t = 0; t < ZPER; ++t) {
-            const int j = threadIdx.x + t * 256;
-            zz[t] = j < L ? z[j] : INT32_MIN;
-        }
-#pragma unroll
-        for (int t = 0; t < ZPER; ++t) mx = max(mx, zz[t]);
-        mx = block_max_i32_dpp(mx, redm);
-#pragma unroll
-        for (int t = 0; t < ZPER; ++t)
-            if (threadIdx.x + t * 256 < L) s += (uint32_t)exp_lookup(sat_sub32(mx, zz[t]), lut, lut_len, lut_shift, lut_one);
-    } else {
-        for (int j = threadIdx.x; j < L; j += 256) mx = max(mx, z[j]);
-        mx = block_max_i32_dpp(mx, redm);
-        for (int j = threadIdx.x; j < L; j += 256)
-            s += (uint32_t)exp_lookup(sat_sub32(mx, z[j]), lut, lut_len, lut_shift, lut_one);
-    }
-    m = mx;
-    S = (int32_t)block_sum_u32_dpp(s, reds);
-}
+// Exp-table entries a P.V block can hold in LDS (8 KB).
+constexpr int kDecExpLds = 4096;
 
-// The exact partial P.V of one chunk (attention.rs:75-81) given the head's
-// statistics: p_j = RNE(e_j * 2^14 / S) (or the uniform split when S == 0,
-// softmax.rs:42-63), then sum_j p_j v_j per dimension in i64, added to
-// acc[0 .. HD) with 64-bit atomics (exact, order-free).  vv holds the chunk's
-// V pairs (dec_load_v).  Whole block (256 threads).
+// V pairs of one chunk: threads TPR per V row (one dimension pair each), the
+// rows of the chunk dealt over STREAMS position streams.
 template <int HD>
 struct DecV {
     static constexpr int TPR = HD / 2;           // threads per V row (one dim pair each)
@@ -132,35 +99,110 @@ __device__ inline void dec_load_v(int L, int base, const int16_t* __restrict__ v
     }
 }
 
+// The exact partial P.V of one chunk (attention.rs:75-81 with
+// softmax.rs:12-64): the head's max m and wrapping exp-LUT sum S over all L
+// scores (every block of a head recomputes them; cheap for one row), then
+// p_j = RNE(e_j * 2^14 / S) (or the uniform split when S == 0) for the
+// chunk's positions and sum_j p_j v_j per dimension in i64, added to
+// acc[0 .. HD) with 64-bit atomics (exact, order-free).  exp_lds >= 0: every
+// exp-table entry from exp_lds on is zero and entries [0, exp_lds) are read
+// from an LDS copy (exp_lds <= kDecExpLds); -1: the table is read in place.
+// Every global load of the block (table, V, scores) is issued before any is
+// used.  Whole block (256 threads).
 template <int HD>
-__device__ inline void dec_pv_chunk(int L, int base, const int32_t* __restrict__ z, const DecV<HD>& v,
-                                    const int16_t* __restrict__ lut, uint32_t lut_len, uint8_t lut_shift, int32_t mx,
-                                    int32_t S, unsigned long long* __restrict__ acc) {
+__device__ inline void dec_pv(int L, int base, const int32_t* __restrict__ z, const int16_t* __restrict__ vg,
+                              const int16_t* __restrict__ lut, uint32_t lut_len, uint8_t lut_shift, int exp_lds,
+                              unsigned long long* __restrict__ acc) {
+    constexpr int ZPER = 16;  // scores held in registers per thread (L <= 4096)
+    constexpr int LPT = kDecExpLds / 8 / 256;  // 8-entry table pieces per thread
     constexpr int STREAMS = DecV<HD>::STREAMS, PER = DecV<HD>::PER;
-    const int n = min(kChunk, L - base);
+    __shared__ int16_t elut[kDecExpLds];
+    __shared__ int32_t redm[4];
+    __shared__ uint32_t reds[4];
     __shared__ int32_t p[kChunk];
     __shared__ int64_t red[STREAMS][HD];
-    const int dp = threadIdx.x % DecV<HD>::TPR, stream = threadIdx.x / DecV<HD>::TPR;
-    const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
+    const int tid = threadIdx.x;
+    const bool lds = exp_lds >= 0;
+    uint4 lv[LPT];
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+        const int e0 = (tid + i * 256) * 8;
+        lv[i] = make_uint4(0, 0, 0, 0);
+        if (lds && e0 < exp_lds) {
+            if ((uint32_t)e0 + 8u <= lut_len) {
+                lv[i] = *reinterpret_cast<const uint4*>(lut + e0);
+            } else {
+                uint32_t w[4] = {0, 0, 0, 0};
+                for (int k = 0; k < 8 && (uint32_t)(e0 + k) < lut_len; ++k)
+                    w[k >> 1] |= (uint32_t)(uint16_t)lut[e0 + k] << (16 * (k & 1));
+                lv[i] = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        }
+    }
     const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
-    if (threadIdx.x < kChunk) {
-        const int t = threadIdx.x;
+    DecV<HD> v;
+    dec_load_v<HD>(L, base, vg, v);
+    const bool regs = L <= 256 * ZPER;
+    int32_t zz[ZPER];
+    if (regs) {
+#pragma unroll
+        for (int t = 0; t < ZPER; ++t) {
+            const int j = tid + t * 256;
+            zz[t] = j < L ? z[j] : INT32_MIN;
+        }
+    }
+    const int n = min(kChunk, L - base);
+    const int32_t zown = tid < n ? z[base + tid] : 0;
+    if (lds) {
+#pragma unroll
+        for (int i = 0; i < LPT; ++i) {
+            const int e0 = (tid + i * 256) * 8;
+            if (e0 < exp_lds) *reinterpret_cast<uint4*>(elut + e0) = lv[i];  // visible after the max's barrier
+        }
+    }
+    int32_t mx = INT32_MIN;
+    if (regs) {
+#pragma unroll
+        for (int t = 0; t < ZPER; ++t) mx = max(mx, zz[t]);
+    } else {
+        for (int j = tid; j < L; j += 256) mx = max(mx, z[j]);
+    }
+    mx = block_max_i32_dpp(mx, redm);
+    // exp_lookup (softmax.rs:12-20) of the score zj
+    auto ex = [&](int32_t zj) -> int32_t {
+        const int32_t x = sat_sub32(mx, zj);
+        if (x <= 0) return lut_one;
+        const uint32_t idx = (uint32_t)x >> (lut_shift & 31u);
+        if (lds) return idx < (uint32_t)exp_lds ? (int32_t)elut[idx] : 0;
+        return idx < lut_len ? (int32_t)lut[idx] : 0;
+    };
+    uint32_t s = 0;
+    if (regs) {
+#pragma unroll
+        for (int t = 0; t < ZPER; ++t)
+            if (tid + t * 256 < L) s += (uint32_t)ex(zz[t]);
+    } else {
+        for (int j = tid; j < L; j += 256) s += (uint32_t)ex(z[j]);
+    }
+    const int32_t S = (int32_t)block_sum_u32_dpp(s, reds);
+    const int dp = tid % DecV<HD>::TPR, stream = tid / DecV<HD>::TPR;
+    const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
+    if (tid < kChunk) {
         int32_t pv = 0;
-        if (t < n) {
+        if (tid < n) {
             if (S == 0) {
                 const uint64_t rl = recip32((uint32_t)L);
                 uint32_t qq, rr;
                 udivmod32((uint32_t)one, (uint32_t)L, rl, &qq, &rr);
                 const int32_t ubase = (int32_t)qq;
                 const int32_t urem = wsub32(one, wmul32(ubase, L));
-                pv = ubase + (((uint64_t)(base + t) < (uint64_t)(int64_t)urem) ? 1 : 0);
+                pv = ubase + (((uint64_t)(base + tid) < (uint64_t)(int64_t)urem) ? 1 : 0);
             } else {
                 const uint64_t rs = recip32(S < 0 ? 0u - (uint32_t)S : (uint32_t)S);
-                const int32_t e = exp_lookup(sat_sub32(mx, z[base + t]), lut, lut_len, lut_shift, lut_one);
-                pv = softmax_div_round(wmul32(e, one), S, rs);
+                pv = softmax_div_round(wmul32(ex(zown), one), S, rs);
             }
         }
-        p[t] = pv;
+        p[tid] = pv;
     }
     __syncthreads();
     int64_t a0 = 0, a1 = 0;
@@ -173,26 +215,12 @@ __device__ inline void dec_pv_chunk(int L, int base, const int32_t* __restrict__
     red[stream][2 * dp] = a0;
     red[stream][2 * dp + 1] = a1;
     __syncthreads();
-    if (threadIdx.x < HD) {
+    if (tid < HD) {
         int64_t sum = 0;
 #pragma unroll
-        for (int k = 0; k < STREAMS; ++k) sum = wadd64(sum, red[k][threadIdx.x]);
-        atomicAdd(acc + threadIdx.x, (unsigned long long)sum);
+        for (int k = 0; k < STREAMS; ++k) sum = wadd64(sum, red[k][tid]);
+        atomicAdd(acc + tid, (unsigned long long)sum);
     }
-}
-
-// Statistics and P.V of one chunk in one block: every block of a head
-// recomputes the head's statistics over all L scores (cheap for one row;
-// the V loads are in flight meanwhile).
-template <int HD>
-__device__ inline void dec_pv(int L, int base, const int32_t* __restrict__ z, const int16_t* __restrict__ vg,
-                              const int16_t* __restrict__ lut, uint32_t lut_len, uint8_t lut_shift,
-                              unsigned long long* __restrict__ acc) {
-    DecV<HD> v;
-    dec_load_v<HD>(L, base, vg, v);
-    int32_t mx, S;
-    dec_stats(L, z, lut, lut_len, lut_shift, mx, S);
-    dec_pv_chunk<HD>(L, base, z, v, lut, lut_len, lut_shift, mx, S, acc);
 }
 
 }  // namespace myl

@@ -535,7 +535,8 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(const DecodeState* __restr
                                                      const int32_t* __restrict__ scores,
                                                      const int16_t* __restrict__ vc, int max_pos, int G, int chunks,
                                                      const int16_t* __restrict__ lut, uint32_t lut_len,
-                                                     uint8_t lut_shift, unsigned long long* __restrict__ acc) {
+                                                     uint8_t lut_shift, int exp_lds,
+                                                     unsigned long long* __restrict__ acc) {
     const AttnBlock b;
     if (b.c >= chunks) return;
     const int L = st->pos + 1;
@@ -543,7 +544,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(const DecodeState* __restr
     if (base >= L) return;
     const int head = b.g * G + b.h;
     dec_pv<HD>(L, base, scores + (size_t)head * max_pos, vc + (size_t)b.g * max_pos * HD, lut, lut_len, lut_shift,
-               acc + (size_t)head * HD);
+               exp_lds, acc + (size_t)head * HD);
 }
 
 // ---------------------------------------------------------------------------
@@ -650,6 +651,12 @@ int alloc_impl(myl_model* m, const myl_luts* luts) {
     m->rsqrt_len = (int)luts->rsqrt_len;
     m->silu_len = (int)luts->silu_len;
     m->exp_len = (int)luts->exp_len;
+    m->exp_nz = 0;
+    for (int i = m->exp_len - 1; i >= 0; --i)
+        if (luts->exp[i] != 0) {
+            m->exp_nz = i + 1;
+            break;
+        }
     m->rope_rows = (uint32_t)(luts->rope_len / (size_t)(hd / 2));
     m->rsqrt = m->dalloc<int16_t>(luts->rsqrt_len);
     m->silu = m->dalloc<int16_t>(luts->silu_len);
@@ -947,16 +954,17 @@ hipError_t layer_step(myl_model* m, int l) {
         const int16_t* kc = m->kcache + layer_kv;
         const int16_t* vc = m->vcache + layer_kv;
         const dim3 agrid(8 * G, (chunks + 7) / 8, kvh);
+        const int exp_lds = m->exp_nz <= kDecExpLds ? m->exp_nz : -1;
         if (hd == 128) {
             attn_scores_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, chunks, m->score_mult,
                                                           score_shift, m->scores);
             attn_pv_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, G, chunks, m->exp_lut,
-                                                      (uint32_t)m->exp_len, lut_shift, m->attn_acc);
+                                                      (uint32_t)m->exp_len, lut_shift, exp_lds, m->attn_acc);
         } else {
             attn_scores_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, chunks, m->score_mult,
                                                          score_shift, m->scores);
             attn_pv_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, G, chunks, m->exp_lut,
-                                                     (uint32_t)m->exp_len, lut_shift, m->attn_acc);
+                                                     (uint32_t)m->exp_len, lut_shift, exp_lds, m->attn_acc);
         }
         e = hipGetLastError();
         if (e != hipSuccess) return e;

@@ -101,6 +101,7 @@ struct myl_model {
     void (*io_free)(void*) = nullptr;
     int16_t *rsqrt = nullptr, *silu = nullptr, *exp_lut = nullptr, *cos_lut = nullptr, *sin_lut = nullptr;
     int rsqrt_len = 0, silu_len = 0, exp_len = 0;
+    int exp_nz = 0;  // exp-table entries up to its last nonzero one
     int64_t inv_n_q20 = 0;
     int64_t score_mult = 0;
     // caches and activations

@@ -206,3 +206,21 @@ def test_backend_close_closes_its_models():
     assert m._h is None
     m.close()
     del m
+
+
+def test_decode_with_a_long_exp_table_tail(backend):
+    """An exp table whose nonzero entries run past what the decode P.V kernel
+    copies into LDS (4096) is read in place; logits still match the oracle."""
+    from myelith_amd.luts import LutSet
+    from myelith_amd.model import IntegerModel
+    from oracle.binding import OracleModel
+    spec = tiny(128, 0, 1, 2)
+    case(f"long exp tail {spec}")
+    base = LutSet.for_head_dim(128)
+    exp = np.asarray(base.exp, dtype=np.int16).copy()
+    exp[2600:6000] = np.maximum(exp[2600:6000], 1)
+    luts = LutSet.from_tables(128, base.rsqrt, base.silu, exp, base.cos, base.sin)
+    gm, om = IntegerModel(backend, spec, luts), OracleModel(spec, luts, threads=16)
+    r = np.random.default_rng(5)
+    for pos, t in enumerate(r.integers(0, spec["vocab"], 160)):
+        assert np.array_equal(gm.forward_token(int(t), pos), om.forward_token(int(t), pos)), pos
