@@ -143,7 +143,7 @@ __global__ __launch_bounds__(256) void rope_scatter_kernel(const int16_t* __rest
 // then their exp values, in registers; longer ones read the scores three times.
 template <int W>
 __global__ __launch_bounds__(256) void rows_probs_kernel(const int32_t* __restrict__ rows, int rows_cap,
-                                                         const int32_t* __restrict__ scores, int heads, int lcap,
+                                                         const int32_t* __restrict__ scores, Divider heads, int lcap,
                                                          int npairs, const int16_t* __restrict__ lut, uint32_t lut_len,
                                                          uint8_t lut_shift, int16_t* __restrict__ probs) {
     static_assert(W == 1 || W == 4, "waves per pair");
@@ -154,7 +154,9 @@ __global__ __launch_bounds__(256) void rows_probs_kernel(const int32_t* __restri
     const int t = W == 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
     const int pair = W == 1 ? (int)(blockIdx.x * 4 + (threadIdx.x >> 6)) : (int)blockIdx.x;
     if (pair >= npairs) return;  // uniform over the pair's waves: every reduction sees all of them
-    const int L = rows[rows_cap + pair / heads] + 1;
+    uint32_t row, head;
+    heads.divmod((uint32_t)pair, row, head);
+    const int L = rows[rows_cap + (int)row] + 1;
     const size_t o = (size_t)pair * lcap;
     const int32_t* z = scores + o;
     int16_t* pr = probs + o;
@@ -501,12 +503,13 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         // a wave per (row, head) when there are enough of them to fill the
         // chip, else a block of four waves each
         const int npairs = R * heads;
+        const Divider hdiv = Divider::of((uint32_t)heads);
         if (npairs >= 16 * c->prop.multiProcessorCount)
-            rows_probs_kernel<1><<<(npairs + 3) / 4, 256, 0, st>>>(b->rows, b->rows_cap, b->scores, heads, b->lmax_cap,
+            rows_probs_kernel<1><<<(npairs + 3) / 4, 256, 0, st>>>(b->rows, b->rows_cap, b->scores, hdiv, b->lmax_cap,
                                                                    npairs, m->exp_lut, (uint32_t)m->exp_len, lut_shift,
                                                                    b->probs);
         else
-            rows_probs_kernel<4><<<npairs, 256, 0, st>>>(b->rows, b->rows_cap, b->scores, heads, b->lmax_cap, npairs,
+            rows_probs_kernel<4><<<npairs, 256, 0, st>>>(b->rows, b->rows_cap, b->scores, hdiv, b->lmax_cap, npairs,
                                                          m->exp_lut, (uint32_t)m->exp_len, lut_shift, b->probs);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // Big grids (prefill) loop each block over its tile's ranges and
