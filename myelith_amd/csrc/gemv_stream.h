@@ -18,6 +18,13 @@
 // in a per-wave LDS record; after the stream every lane applies the epilogue
 // to one recorded group, so all epilogue loads and stores of a wave overlap.
 //
+// Staging interface (Src):
+//   Pre; pre(K, kpad)                            per thread, first thing in the kernel
+//   stage_i8(pre, hi, lo, K, kpad)               whole block, after the first weight loads
+// pre() issues the source's own loads (activations, scales, norm sums) ahead of
+// every weight load: loads complete in issue order, so staging then waits for
+// its operands without waiting for a weight batch.
+//
 // Epilogue interface:
 //   State; begin(State&)                        per thread, before the stream
 //   group(State&, row0, N, const int64_t (&)[R]) per lane, one group each
@@ -44,11 +51,50 @@ __device__ inline uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 
 // ---- staging sources ----------------------------------------------------------
 
-// Plain int16 activations, converted to the two signed byte planes.
+// 8-element chunks of the staged vector a thread loads in pre(): chunks
+// threadIdx.x + j * blockDim.x, j < kPreChunks; the rest load during staging.
+constexpr int kPreChunks = 3;
+
+// Eight int16 values -> their signed byte planes (hi = x >> 8, lo' = (x & 255) - 128).
+__device__ inline void put_x8_planes(const uint4 v, int8_t* hi, int8_t* lo) {
+    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+    uint32_t h[2], l[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint32_t d0 = d[2 * t], d1 = d[2 * t + 1];
+        h[t] = ((d0 >> 8) & 0xFFu) | ((d0 >> 16) & 0xFF00u) | ((d1 << 8) & 0xFF0000u) | (d1 & 0xFF000000u);
+        l[t] = ((d0 & 0xFFu) | ((d0 >> 8) & 0xFF00u) | ((d1 << 16) & 0xFF0000u) | ((d1 << 8) & 0xFF000000u)) ^ 0x80808080u;
+    }
+    *reinterpret_cast<uint2*>(hi) = make_uint2(h[0], h[1]);
+    *reinterpret_cast<uint2*>(lo) = make_uint2(l[0], l[1]);
+}
+
+// Plain int16 activations (K % 8 == 0), converted to the two signed byte planes.
 struct SrcPlain {
     const int16_t* x;
-    __device__ inline void stage_i8(int8_t* hi, int8_t* lo, int K, int kpad) const {
-        stage_x_planes(x, 1, K, K, 0, kpad, hi, lo, true);
+    struct Pre {
+        uint4 x[kPreChunks];
+    };
+    __device__ inline Pre pre(int K, int kpad) const {
+        Pre p;
+#pragma unroll
+        for (int j = 0; j < kPreChunks; ++j) {
+            const int k = (threadIdx.x + j * blockDim.x) * 8;
+            p.x[j] = k < K ? *reinterpret_cast<const uint4*>(x + k) : make_uint4(0, 0, 0, 0);
+        }
+        return p;
+    }
+    __device__ inline void stage_i8(const Pre& p, int8_t* hi, int8_t* lo, int K, int kpad) const {
+        const int n8 = kpad >> 3;
+#pragma unroll
+        for (int j = 0; j < kPreChunks; ++j) {
+            const int i = threadIdx.x + j * blockDim.x;
+            if (i < n8) put_x8_planes(p.x[j], hi + i * 8, lo + i * 8);
+        }
+        for (int i = threadIdx.x + kPreChunks * blockDim.x; i < n8; i += blockDim.x) {
+            const uint4 v = i * 8 < K ? *reinterpret_cast<const uint4*>(x + i * 8) : make_uint4(0, 0, 0, 0);
+            put_x8_planes(v, hi + i * 8, lo + i * 8);
+        }
     }
 };
 
@@ -91,6 +137,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i8_stream(Src src, const int8
     const int ngroups = (N + R - 1) / R;
     const int nit = (K + kWave * 16 - 1) / (kWave * 16);  // 1 KiB steps per row
     const int nb = (nit + U - 1) / U;                      // batches per group
+    const typename Src::Pre pre = src.pre(K, kpad);
     typename Epi::State es;
     epi.begin(es);
 
@@ -169,7 +216,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i8_stream(Src src, const int8
         advance(g1, kb1);
         load(A, g, 0);
         load(B, g1, kb1);
-        src.stage_i8(hi_plane, lo_plane, K, kpad);
+        src.stage_i8(pre, hi_plane, lo_plane, K, kpad);
         __syncthreads();
         reset();
         while (g < ngroups) {
@@ -192,7 +239,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i8_stream(Src src, const int8
         }
     } else {
         load(A, g, 0);
-        src.stage_i8(hi_plane, lo_plane, K, kpad);
+        src.stage_i8(pre, hi_plane, lo_plane, K, kpad);
         __syncthreads();
         reset();
         while (g < ngroups) {
@@ -235,6 +282,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i16_stream(Src16 src, const i
     const int nit = (K + kWave * 8 - 1) / (kWave * 8);
     const int nb = (nit + U - 1) / U;
     typedef short __attribute__((ext_vector_type(2))) s2;
+    const typename Src16::Pre pre = src.pre(K, kpad);
     typename Epi::State es;
     epi.begin(es);
 
@@ -303,7 +351,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i16_stream(Src16 src, const i
         if (++kk == nb) { kk = 0; gg += nw; }
     };
     load(A, g, 0);
-    src.stage_i16(hi_plane, lo_plane, K, kpad);
+    src.stage_i16(pre, hi_plane, lo_plane, K, kpad);
     __syncthreads();
     reset();
     while (g < ngroups) {

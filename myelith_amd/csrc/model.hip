@@ -150,6 +150,8 @@ __device__ inline void put_planes_i16(const int16_t (&v)[8], int16_t* hi, int16_
 }
 
 // Staging source: RMSNorm of x (x_shifts xs, gamma g/gs) from a NormAcc.
+constexpr int kNormPre = 1;
+
 struct SrcNorm {
     const int16_t* x;
     const uint8_t* xs;
@@ -159,12 +161,38 @@ struct SrcNorm {
     uint8_t ref, out_frac;
     const NormAcc* acc;
 
-    __device__ inline RmsFactor factor() const {
+    // the norm-sum words (threads < 64) and the first kNormPre chunks of x,
+    // its shifts, gamma and gamma's shifts (one: every launch has K <= 8 x
+    // its threads)
+    struct Pre {
+        uint64_t a[3];
+        uint4 xv[kNormPre];
+        uint2 sv[kNormPre], gv[kNormPre], gsv[kNormPre];
+    };
+    __device__ inline Pre pre(int K, int kpad) const {
+        Pre q;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) q.a[j] = threadIdx.x < 64 ? acc->v[threadIdx.x][j] : 0;
+#pragma unroll
+        for (int j = 0; j < kNormPre; ++j) {
+            const int k0 = (threadIdx.x + j * blockDim.x) * 8;
+            q.xv[j] = make_uint4(0, 0, 0, 0);
+            q.sv[j] = q.gv[j] = q.gsv[j] = make_uint2(0, 0);
+            if (k0 < K) {
+                q.xv[j] = *reinterpret_cast<const uint4*>(x + k0);
+                q.sv[j] = *reinterpret_cast<const uint2*>(xs + k0);
+                q.gv[j] = *reinterpret_cast<const uint2*>(g + k0);
+                q.gsv[j] = *reinterpret_cast<const uint2*>(gs + k0);
+            }
+        }
+        return q;
+    }
+    __device__ inline RmsFactor factor(const Pre& q) const {
         __shared__ RmsFactor sf;
         if (threadIdx.x < 64) {
             uint64_t l[3];
 #pragma unroll
-            for (int j = 0; j < 3; ++j) l[j] = wave_sum_u64(acc->v[threadIdx.x][j]);
+            for (int j = 0; j < 3; ++j) l[j] = wave_sum_u64(q.a[j]);
             if (threadIdx.x == 0) {
                 const myl_i128 a = (myl_i128)((myl_u128)l[0] + ((myl_u128)l[1] << 42) + ((myl_u128)l[2] << 84));
                 sf = rms_factor_of(a, ref, p);
@@ -173,16 +201,8 @@ struct SrcNorm {
         __syncthreads();
         return sf;
     }
-    __device__ inline void values8(const RmsFactor& f, int k0, int K, int16_t (&v)[8]) const {
-        if (k0 >= K) {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) v[t] = 0;
-            return;
-        }
-        const uint4 xv = *reinterpret_cast<const uint4*>(x + k0);
-        const uint2 sv = *reinterpret_cast<const uint2*>(xs + k0);
-        const uint2 gv = *reinterpret_cast<const uint2*>(g + k0);
-        const uint2 gsv = *reinterpret_cast<const uint2*>(gs + k0);
+    __device__ inline void values8(const RmsFactor& f, uint4 xv, uint2 sv, uint2 gv, uint2 gsv,
+                                   int16_t (&v)[8]) const {
         const int16_t* xe = reinterpret_cast<const int16_t*>(&xv);
         const uint8_t* se = reinterpret_cast<const uint8_t*>(&sv);
         const int8_t* ge = reinterpret_cast<const int8_t*>(&gv);
@@ -190,21 +210,42 @@ struct SrcNorm {
 #pragma unroll
         for (int t = 0; t < 8; ++t) v[t] = rms_out(xe[t], se[t], ge[t], gse[t], f, out_frac);
     }
-    __device__ inline void stage_i8(int8_t* hi, int8_t* lo, int K, int kpad) const {
-        const RmsFactor f = factor();
-        for (int i = threadIdx.x; i < (kpad >> 3); i += blockDim.x) {
+    // chunk i (k0 = 8 i) of the normalised vector; zeros past K
+    template <class Put>
+    __device__ inline void stage(const Pre& q, int K, int kpad, const Put& put) const {
+        const RmsFactor f = factor(q);
+        const int n8 = kpad >> 3;
+#pragma unroll
+        for (int j = 0; j < kNormPre; ++j) {
+            const int i = threadIdx.x + j * blockDim.x;
+            if (i >= n8) break;
             int16_t v[8];
-            values8(f, i * 8, K, v);
-            put_planes_i8(v, hi + i * 8, lo + i * 8);
+            if (i * 8 < K) {
+                values8(f, q.xv[j], q.sv[j], q.gv[j], q.gsv[j], v);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) v[t] = 0;
+            }
+            put(i, v);
+        }
+        for (int i = threadIdx.x + kNormPre * blockDim.x; i < n8; i += blockDim.x) {
+            int16_t v[8];
+            const int k0 = i * 8;
+            if (k0 < K) {
+                values8(f, *reinterpret_cast<const uint4*>(x + k0), *reinterpret_cast<const uint2*>(xs + k0),
+                        *reinterpret_cast<const uint2*>(g + k0), *reinterpret_cast<const uint2*>(gs + k0), v);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) v[t] = 0;
+            }
+            put(i, v);
         }
     }
-    __device__ inline void stage_i16(int16_t* hi, int16_t* lo, int K, int kpad) const {
-        const RmsFactor f = factor();
-        for (int i = threadIdx.x; i < (kpad >> 3); i += blockDim.x) {
-            int16_t v[8];
-            values8(f, i * 8, K, v);
-            put_planes_i16(v, hi + i * 8, lo + i * 8);
-        }
+    __device__ inline void stage_i8(const Pre& q, int8_t* hi, int8_t* lo, int K, int kpad) const {
+        stage(q, K, kpad, [&](int i, const int16_t (&v)[8]) { put_planes_i8(v, hi + i * 8, lo + i * 8); });
+    }
+    __device__ inline void stage_i16(const Pre& q, int16_t* hi, int16_t* lo, int K, int kpad) const {
+        stage(q, K, kpad, [&](int i, const int16_t (&v)[8]) { put_planes_i16(v, hi + i * 8, lo + i * 8); });
     }
 };
 
@@ -213,23 +254,42 @@ struct SrcNorm {
 struct SrcAttn {
     const unsigned long long* acc;
     uint8_t v_frac, out_frac;
-    __device__ inline void stage_i8(int8_t* hi, int8_t* lo, int K, int kpad) const {
+    // the first chunk of each thread: 8 accumulators as four 16-byte pieces
+    struct Pre {
+        uint4 a[4];
+    };
+    __device__ inline Pre pre(int K, int kpad) const {
+        Pre q;
+        const int k0 = threadIdx.x * 8;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            q.a[t] = k0 < K ? reinterpret_cast<const uint4*>(acc + k0)[t] : make_uint4(0, 0, 0, 0);
+        return q;
+    }
+    __device__ inline void values8(const uint4 (&a4)[4], int16_t (&v)[8]) const {
+        uint64_t a[8];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            a[2 * t] = ((uint64_t)a4[t].y << 32) | a4[t].x;
+            a[2 * t + 1] = ((uint64_t)a4[t].w << 32) | a4[t].z;
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int16_t r = clamp_i16_i64(rshift_round64((int64_t)a[t], MYL_TV_PROB_FRAC_BITS));
+            v[t] = clamp_i16(rescale32((int32_t)r, v_frac, out_frac));
+        }
+    }
+    __device__ inline void stage_i8(const Pre& q, int8_t* hi, int8_t* lo, int K, int kpad) const {
         for (int i = threadIdx.x; i < (kpad >> 3); i += blockDim.x) {
             int16_t v[8];
             const int k0 = i * 8;
             if (k0 < K) {
-                const uint4* a4 = reinterpret_cast<const uint4*>(acc + k0);
-                uint64_t a[8];
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const uint4 q = a4[t];
-                    a[2 * t] = ((uint64_t)q.y << 32) | q.x;
-                    a[2 * t + 1] = ((uint64_t)q.w << 32) | q.z;
-                }
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const int16_t r = clamp_i16_i64(rshift_round64((int64_t)a[t], MYL_TV_PROB_FRAC_BITS));
-                    v[t] = clamp_i16(rescale32((int32_t)r, v_frac, out_frac));
+                if (i == (int)threadIdx.x) {
+                    values8(q.a, v);
+                } else {
+                    const uint4* a4 = reinterpret_cast<const uint4*>(acc + k0);
+                    const uint4 w[4] = {a4[0], a4[1], a4[2], a4[3]};
+                    values8(w, v);
                 }
             } else {
 #pragma unroll
