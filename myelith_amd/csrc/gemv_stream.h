@@ -27,6 +27,10 @@
 //
 // Epilogue interface:
 //   State; begin(State&)                        per thread, before the stream
+//   prefetch(State&, row0, N)                    per lane, right after the first
+//                                                weight batch: the per-row operands
+//                                                of the lane's first group (rows
+//                                                row0 ..), in registers by the end
 //   group(State&, row0, N, const int64_t (&)[R]) per lane, one group each
 //   finish(State&)                               whole block, after the stream
 //                                                (may synchronise the block)
@@ -215,6 +219,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i8_stream(Src src, const int8
         int g1 = g, kb1 = kb;
         advance(g1, kb1);
         load(A, g, 0);
+        epi.prefetch(es, (g0 + lane * nw) * R, N);
         load(B, g1, kb1);
         src.stage_i8(pre, hi_plane, lo_plane, K, kpad);
         __syncthreads();
@@ -239,6 +244,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i8_stream(Src src, const int8
         }
     } else {
         load(A, g, 0);
+        epi.prefetch(es, (g0 + lane * nw) * R, N);
         src.stage_i8(pre, hi_plane, lo_plane, K, kpad);
         __syncthreads();
         reset();
@@ -351,6 +357,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i16_stream(Src16 src, const i
         if (++kk == nb) { kk = 0; gg += nw; }
     };
     load(A, g, 0);
+    epi.prefetch(es, (g0 + lane * nw) * R, N);
     src.stage_i16(pre, hi_plane, lo_plane, K, kpad);
     __syncthreads();
     reset();

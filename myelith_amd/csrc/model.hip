@@ -372,6 +372,9 @@ struct EpiQKV {
     int16_t* vc;
     using State = NoState;
     __device__ inline void begin(State&) const {}
+    // the per-row operands load in group(): loading them early measured
+    // slower (the RoPE entries depend on the step's row)
+    __device__ inline void prefetch(State&, int, int) const {}
     __device__ inline void finish(State&) const {}
     template <int R>
     __device__ inline void group(State&, int row0, int N, const int64_t (&tot)[R]) const {
@@ -423,18 +426,46 @@ struct EpiResid {
     NormAcc* sum_out;
     uint8_t ref_out;           // max over out_frac
     NormAcc* clear;            // may be null
-    struct State { uint64_t l[3]; };
-    __device__ inline void begin(State& s) const { s.l[0] = s.l[1] = s.l[2] = 0; }
+    // the norm partial sums, and the per-row operands of the lane's first
+    // group (up to two rows)
+    struct State {
+        uint64_t l[3];
+        int row0;
+        uint8_t sh[2], af[2], rf[2], of[2];
+        int16_t res[2];
+    };
+    __device__ inline void begin(State& s) const {
+        s.l[0] = s.l[1] = s.l[2] = 0;
+        s.row0 = -1;
+    }
+    __device__ inline void prefetch(State& s, int row0, int N) const {
+        if (row0 >= N) return;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int i = min(row0 + r, N - 1);
+            s.sh[r] = shifts[i];
+            s.af[r] = acc_frac[i];
+            s.rf[r] = res_frac[i];
+            s.of[r] = out_frac[i];
+            s.res[r] = res_in[i];
+        }
+        s.row0 = row0;
+    }
     template <int R>
     __device__ inline void group(State& s, int row0, int N, const int64_t (&tot)[R]) const {
+        static_assert(R <= 2, "two prefetched rows per group");
+        const bool pre = s.row0 == row0;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             if (row0 + r < N) {
                 const int i = row0 + r;
-                const uint8_t af = acc_frac[i];
-                const int16_t o = clamp_i16_i64(rescale64(tot[r], (uint8_t)(shifts[i] + act_frac), af));
-                const int64_t h = rescale64((int64_t)res_in[i], res_frac[i], af);
-                const uint8_t of = out_frac[i];
+                const uint8_t af = pre ? s.af[r] : acc_frac[i];
+                const uint8_t sh = pre ? s.sh[r] : shifts[i];
+                const int16_t ri = pre ? s.res[r] : res_in[i];
+                const uint8_t rf = pre ? s.rf[r] : res_frac[i];
+                const int16_t o = clamp_i16_i64(rescale64(tot[r], (uint8_t)(sh + act_frac), af));
+                const int64_t h = rescale64((int64_t)ri, rf, af);
+                const uint8_t of = pre ? s.of[r] : out_frac[i];
                 const int16_t v = clamp_i16_i64(rescale64(wadd64(h, (int64_t)o), af, of));
                 out[i] = v;
                 add_sq_limbs(v, of, ref_out, s.l);
@@ -464,6 +495,8 @@ struct EpiSilu {
     unsigned long long* clear; int clear_n;
     using State = NoState;
     __device__ inline void begin(State&) const {}
+    // two shift bytes: loading them early measured slower
+    __device__ inline void prefetch(State&, int, int) const {}
     __device__ inline void finish(State&) const {
         for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < clear_n; i += gridDim.x * blockDim.x) clear[i] = 0;
     }
@@ -488,14 +521,30 @@ struct EpiHead {
     uint8_t norm_frac;
     int32_t* logits;
     DecodeState* st;
-    struct State { uint64_t best; };
-    __device__ inline void begin(State& s) const { s.best = 0; }
+    struct State {
+        uint64_t best;
+        int row0;
+        uint8_t sh[2];
+    };
+    __device__ inline void begin(State& s) const {
+        s.best = 0;
+        s.row0 = -1;
+    }
+    __device__ inline void prefetch(State& s, int row0, int N) const {
+        if (row0 >= N) return;
+        s.sh[0] = shifts[row0];
+        s.sh[1] = shifts[min(row0 + 1, N - 1)];
+        s.row0 = row0;
+    }
     template <int R>
     __device__ inline void group(State& s, int row0, int N, const int64_t (&tot)[R]) const {
+        static_assert(R <= 2, "two prefetched rows per group");
+        const bool pre = s.row0 == row0;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             if (row0 + r < N) {
-                const int32_t v = clamp_i32_i64(rescale64(tot[r], (uint8_t)(shifts[row0 + r] + norm_frac),
+                const uint8_t sh = pre ? s.sh[r] : shifts[row0 + r];
+                const int32_t v = clamp_i32_i64(rescale64(tot[r], (uint8_t)(sh + norm_frac),
                                                           MYL_TV_LOGIT_FRAC_BITS));
                 logits[row0 + r] = v;
                 const uint64_t k = argmax_key(v, (uint32_t)(row0 + r));
