@@ -224,3 +224,22 @@ def test_decode_with_a_long_exp_table_tail(backend):
     r = np.random.default_rng(5)
     for pos, t in enumerate(r.integers(0, spec["vocab"], 160)):
         assert np.array_equal(gm.forward_token(int(t), pos), om.forward_token(int(t), pos)), pos
+
+
+def test_long_prompt_rows_match_the_oracle(backend):
+    """A 4200-token prompt runs as three chunks of rows (2048, 2048, 104):
+    the softmax kernel's register path (a wave per (row, head), rows up to
+    2048 positions), its re-reading path for longer rows, and the four-wave
+    path for few rows past 4096 positions.  Layer 1's K/V at every position
+    depend on layer 0's attention for that row."""
+    spec = tiny(64, 0, 1, 2, layers=2, max_pos=4300)
+    case(f"long prompt rows {spec}")
+    gm, om = build(backend, spec)
+    r = np.random.default_rng(17)
+    p = [int(t) for t in r.integers(0, spec["vocab"], 4200)]
+    g = gm.prefill(p, 0)
+    o = None
+    for pos, t in enumerate(p):
+        o = om.forward_token(t, pos)
+    assert np.array_equal(g, o)
+    compare_kv(gm, om, spec, 4200)
