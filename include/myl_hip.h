@@ -229,7 +229,11 @@ int myl_model_read_tensor(myl_model* m, const char* name, uint32_t layer, void* 
 /* ---- batched forward: rows of (sequence, position, token) -------------------
  * Generalises the prompt loop of generate.rs:28-32 to many sequences with
  * their own KV caches; row r computes what IntegerModel::forward_token
- * (model.rs:229-311) computes for token[r] at pos[r] on sequence seq[r]. */
+ * (model.rs:229-311) computes for token[r] at pos[r] on sequence seq[r].
+ * The row path splits attention probabilities into bytes, so it returns
+ * MYL_E_UNSUPPORTED for models with more than 16 query heads per KV head, an
+ * exp table with negative entries, or one whose sum over max_pos positions
+ * could pass 2^31 - 1 (myl_model_prefill then runs the token loop). */
 
 /* Allocates KV caches for n_seqs sequences (max_pos positions each, separate
  * from the single-sequence cache) and empties them. */
