@@ -91,6 +91,7 @@ SIGNATURES: dict[str, tuple] = {
     "myl_model_decode_greedy": (INT, [P, u32, u32, u32, P, P]),
     "myl_model_prefill": (INT, [P, P, u32, u32, P]),
     "myl_model_set_graphs": (INT, [P, INT]),
+    "myl_model_set_kernel_repeat": (INT, [P, INT, INT]),
     "myl_model_timing": (INT, [P, INT, P, P]),
     "myl_model_embed_token": (INT, [P, u32, P]),
     "myl_model_run_layers": (INT, [P, P, u32, u32, u32]),

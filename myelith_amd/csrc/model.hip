@@ -1095,6 +1095,16 @@ hipError_t layer_step(myl_model* m, int l) {
         // flight during staging is enough (1.5-2 % faster per decode step on
         // MI355X than two)
         e = stream_i8<2, 4, 8>(src, L.wgu, 2 * I, H, s, st, cus);
+        // measurement repeats (myl_model_set_kernel_repeat): the same launch
+        // over the next layers' gate/up weights, which the step last read one
+        // step ago (out of the caches, as this layer's), into scratch rows
+        for (int rep = 1; rep < m->gu_repeat && e == hipSuccess; ++rep) {
+            const LayerDev& Lr = m->layers[(l + rep) % (int)m->spec.layers];
+            EpiSilu sr = s;
+            sr.shifts = Lr.sgu;
+            sr.h = m->h_scratch;
+            e = stream_i8<2, 4, 8>(src, Lr.wgu, 2 * I, H, sr, st, cus);
+        }
     }
     if (e != hipSuccess) return e;
     {
@@ -1215,6 +1225,18 @@ int model_finalize(myl_model* m) { return finalize_impl(m); }
 }  // namespace myl
 
 extern "C" {
+
+int myl_model_set_kernel_repeat(myl_model* m, int kclass, int times) {
+    if (!m || kclass != K_GU || times < 1 || times > 4) return MYL_E_INVALID;
+    (void)hipStreamSynchronize(m->ctx->stream);
+    if (times > 1 && !m->h_scratch && !(m->h_scratch = m->dalloc<int16_t>(m->I)))
+        return m->ctx->fail(MYL_E_NOMEM, "kernel repeat scratch");
+    m->gu_repeat = times;
+    // the captured step holds the launch sequence
+    if (m->step_exec) { (void)hipGraphExecDestroy(m->step_exec); m->step_exec = nullptr; }
+    if (m->step_graph) { (void)hipGraphDestroy(m->step_graph); m->step_graph = nullptr; }
+    return MYL_OK;
+}
 
 int myl_model_set_graphs(myl_model* m, int enable) {
     if (!m) return MYL_E_INVALID;

@@ -198,6 +198,14 @@ class IntegerModel:
 
     KERNEL_CLASSES = ("embed", "rmsnorm", "qkv", "attention", "o_proj", "gate_up", "down", "lm_head")
 
+    def set_kernel_repeat(self, kclass: str, times: int) -> None:
+        """Launches the kernel class `times` times per layer and decode step
+        (a measurement hook; only "gate_up": each repeat streams the next
+        layers' weights into scratch rows, so every output is unchanged).  The
+        next greedy decode recaptures its step graph."""
+        self._check(lib().myl_model_set_kernel_repeat(self._h, self.KERNEL_CLASSES.index(kclass), int(times)),
+                    "set_kernel_repeat")
+
     def timing(self, enable: bool):
         """Starts (True) or stops (False) per-kernel-class HIP event timing.
         Stopping returns {class: (total_ms, launches)}."""

@@ -243,3 +243,29 @@ def test_long_prompt_rows_match_the_oracle(backend):
         o = om.forward_token(t, pos)
     assert np.array_equal(g, o)
     compare_kv(gm, om, spec, 4200)
+
+
+def test_repeated_gate_up_leaves_the_decode_unchanged(backend):
+    """The measurement hook that launches each layer's gate/up GEMV twice per
+    step (captured graph and eager launches) gives the oracle's tokens and
+    logits."""
+    spec = tiny(128, 1, 1, 2, layers=3)
+    case("gate/up repeated twice")
+    gm, om = build(backend, spec)
+    prompt = [17, 3, 999, 42, 7]
+    for pos, t in enumerate(prompt):
+        o = om.forward_token(t, pos)
+    gm.set_kernel_repeat("gate_up", 2)
+    g = gm.prefill(prompt, 0)
+    assert np.array_equal(g, o)
+    first = int(np.argmax(o))
+    toks, logits = gm.decode_greedy(first, len(prompt), 10, want_logits=True)
+    t = first
+    for i in range(10):
+        ref = om.forward_token(t, len(prompt) + i)
+        assert np.array_equal(logits[i], ref), i
+        t = int(np.argmax(ref))
+        assert int(toks[i]) == t, i
+    gm.set_kernel_repeat("gate_up", 1)
+    with pytest.raises(ValueError):
+        gm.set_kernel_repeat("down", 2)
