@@ -2,7 +2,7 @@
 """Benchmark: Qwen2.5-7B-shape integer decode at batch 1 on one MI355X, plus
 the W8A16 GEMV sweep's HBM bandwidth, both bit-exact with the CPU reference.
 
-Workload (the BASELINE 7B decode configuration at batch 1): a Qwen2.5-7B
+Workload (7B-shape integer decode at batch 1, 2048-token context): a Qwen2.5-7B
 architecture integer model (28 layers, hidden 3584, 28/4 heads, head_dim 128,
 intermediate 18944, vocab 152064, int16 LM head) with seeded synthetic int8
 weights and per-channel power-of-two scales; a 2048-token seeded prompt is

@@ -68,7 +68,7 @@ enum myl_role {
     MYL_R_ROUTER, MYL_R_ROUTER_SHIFT, MYL_R_MOE_OUT_FRAC
 };
 
-/* int8 weight element, uniform in [-127, 127] (BASELINE weight distribution). */
+/* int8 weight element, uniform in [-127, 127] (the benchmark models' weight distribution). */
 MYL_HD int8_t myl_synth_w8(uint64_t tseed, uint64_t i) {
     return (int8_t)myl_draw_range(myl_splitmix_at(tseed, i), -127, 127);
 }
@@ -81,7 +81,7 @@ MYL_HD int16_t myl_synth_w16(uint64_t tseed, uint64_t i) {
 /* Approximately Gaussian int16 activation with standard deviation sigma: an
  * integer Irwin-Hall draw.  Each of the 12 uniforms lies in [-4096, 4095]
  * (sd 8192/sqrt(12)), so their sum has sd 8192; it is scaled by sigma/8192
- * and clipped to +-32767 (the BASELINE activation distribution). */
+ * and clipped to +-32767 (the benchmark sweep's activation distribution). */
 MYL_HD int16_t myl_synth_gauss16(uint64_t tseed, uint64_t i, int32_t sigma) {
     int64_t s = 0;
     for (int t = 0; t < 12; ++t)

@@ -21,7 +21,7 @@ from ._lib import LayerFracs, Luts, ModelDims, SynthSpec, lib
 from .backend import RocmBackend
 from .luts import LutSet
 
-# Architectures of the workloads (Qwen2.5 layout).
+# Architectures of the benchmark workloads (the Qwen2.5-0.5B and Qwen2.5-7B layouts).
 QWEN25_05B = dict(vocab=151936, hidden=896, layers=24, heads=14, kv_heads=2, head_dim=64, inter=4864,
                   lm_head_int16=0, attention_bias=1)
 QWEN25_7B = dict(vocab=152064, hidden=3584, layers=28, heads=28, kv_heads=4, head_dim=128, inter=18944,
