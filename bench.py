@@ -325,6 +325,8 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=2048)
     ap.add_argument("--seed", type=int, default=7)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-repeat-probe", action="store_true",
+                    help="skip the in-graph gate/up repeat measurement (profiler runs: only the step's own launches)")
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--no-batch", action="store_true",
                     help="skip the batched decode, teacher-forced prefill and MoE sections")
@@ -421,16 +423,18 @@ def main() -> int:
         tok, pos = int(t[-1]), pos + n
         return e0.elapsed_time(e1)
 
-    t_plain0 = graph_run(MARG_STEPS)
-    model.set_kernel_repeat("gate_up", 2)
-    graph_run(4)  # recaptures the step
-    t_double = graph_run(MARG_STEPS)
-    model.set_kernel_repeat("gate_up", 1)
-    graph_run(4)
-    t_plain1 = graph_run(MARG_STEPS)
-    gu_graph_us = (t_double - 0.5 * (t_plain0 + t_plain1)) * 1e3 / (MARG_STEPS * spec["layers"])
-    log(f"gate/up in the step graph: {gu_graph_us:.2f} us per launch "
-        f"(plain {t_plain0 / MARG_STEPS:.3f} / {t_plain1 / MARG_STEPS:.3f} ms, doubled {t_double / MARG_STEPS:.3f} ms per step)")
+    gu_graph_us = None
+    if not (args.no_repeat_probe or args.traffic_probe):
+        t_plain0 = graph_run(MARG_STEPS)
+        model.set_kernel_repeat("gate_up", 2)
+        graph_run(4)  # recaptures the step
+        t_double = graph_run(MARG_STEPS)
+        model.set_kernel_repeat("gate_up", 1)
+        graph_run(4)
+        t_plain1 = graph_run(MARG_STEPS)
+        gu_graph_us = (t_double - 0.5 * (t_plain0 + t_plain1)) * 1e3 / (MARG_STEPS * spec["layers"])
+        log(f"gate/up in the step graph: {gu_graph_us:.2f} us per launch (plain {t_plain0 / MARG_STEPS:.3f} / "
+            f"{t_plain1 / MARG_STEPS:.3f} ms, doubled {t_double / MARG_STEPS:.3f} ms per step)")
 
     # per-kernel-class timing of 8 more steps of the same decode (HIP events
     # around each eager launch on the decode stream: each bracket also holds
@@ -451,9 +455,11 @@ def main() -> int:
     achieved = per_class[dom]["GBps"]
     # the repeat starts with its staging operands in L2 (no cold start after a
     # kernel boundary): how fast the stream itself runs, not the roofline figure
-    repeat = {"avg_us": round(gu_graph_us, 2), "GBps": round(cb["gate_up"] / (gu_graph_us * 1e-6) / 1e9, 1),
-              "method": "step replays with a second gate/up launch per layer (next layer's weights, scratch "
-                        "rows) minus plain replays; the second launch follows the first, so it starts warm"}
+    repeat = None
+    if gu_graph_us is not None:
+        repeat = {"avg_us": round(gu_graph_us, 2), "GBps": round(cb["gate_up"] / (gu_graph_us * 1e-6) / 1e9, 1),
+                  "method": "step replays with a second gate/up launch per layer (next layer's weights, scratch "
+                            "rows) minus plain replays; the second launch follows the first, so it starts warm"}
     log("kernel classes: " + ", ".join(f"{k} {v['avg_us']}us" for k, v in per_class.items()))
 
     gemv = {}
