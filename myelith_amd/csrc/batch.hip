@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256) void rope_scatter_kernel(const int16_t* __rest
 // 0; later positions are not written, and their readers mask them).
 // W waves per (row, head) (pair = row * heads + head), 4 / W pairs per
 // 256-thread block; a thread takes 4 positions of each chunk of 256 W.
-// Rows of up to 2048 (W = 1) or 4096 (W = 4) positions keep their scores,
+// Rows of up to 1024 (W = 1) or 4096 (W = 4) positions keep their scores,
 // then their exp values, in registers; longer ones read the scores three times.
 template <int W>
 __global__ __launch_bounds__(256) void rows_probs_kernel(const int32_t* __restrict__ rows, int rows_cap,
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void rows_probs_kernel(const int32_t* __restri
                                                          uint8_t lut_shift, int16_t* __restrict__ probs) {
     static_assert(W == 1 || W == 4, "waves per pair");
     constexpr int CW = 256 * W;      // positions per chunk
-    constexpr int KPER = W == 1 ? 8 : 4;  // register-resident chunks (2048 / 4096 positions)
+    constexpr int KPER = 4;  // register-resident chunks (1024 / 4096 positions; 38 VGPRs, 8 waves per SIMD at W = 1)
     __shared__ int32_t redm[4];
     __shared__ uint32_t reds[4];
     const int t = W == 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x;

@@ -229,7 +229,7 @@ def test_decode_with_a_long_exp_table_tail(backend):
 def test_long_prompt_rows_match_the_oracle(backend):
     """A 4200-token prompt runs as three chunks of rows (2048, 2048, 104):
     the softmax kernel's register path (a wave per (row, head), rows up to
-    2048 positions), its re-reading path for longer rows, and the four-wave
+    1024 positions), its re-reading path for longer rows, and the four-wave
     path for few rows past 4096 positions.  Layer 1's K/V at every position
     depend on layer 0's attention for that row."""
     spec = tiny(64, 0, 1, 2, layers=2, max_pos=4300)
