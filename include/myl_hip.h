@@ -210,10 +210,12 @@ int myl_model_prefill(myl_model* m, const uint32_t* tokens, uint32_t n, uint32_t
 int myl_model_set_graphs(myl_model* m, int enable);
 /* No counterpart in the reference: a measurement hook for callers that time a
  * kernel class inside the captured decode step.  Launches the class's kernel
- * `times` (1-4) times per layer and step: the first as usual, each repeat over
- * the next layers' weights into scratch output rows, so every output of the
- * step is unchanged.  Only the gate/up class (kclass 5 of the timing order
- * below) is accepted.  The next greedy decode recaptures its step graph. */
+ * `times` (1-4, at most the number of layers) times per layer and step: the
+ * first as usual, each repeat over the next layers' weights (never weights the
+ * step has already read) into scratch output rows, so every output of the step
+ * is unchanged.  Only the gate/up class (kclass 5 of the timing order below)
+ * is accepted; myl_model_timing does not count the repeats.  The next greedy
+ * decode recaptures its step graph. */
 int myl_model_set_kernel_repeat(myl_model* m, int kclass, int times);
 /* Per-kernel-class timing with HIP events around each launch (eager launches,
  * no graphs while enabled).  enable = 1 starts; enable = 0 stops and returns

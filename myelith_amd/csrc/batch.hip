@@ -632,9 +632,11 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
 // Checks the rows against the sequences' cached lengths and uploads them.
 // Per sequence the batch's positions must be distinct and fill [p0, p0 + n)
 // with p0 <= cached length (a re-run position overwrites, as KVCache::write
-// does); the cached length becomes max(len, p0 + n).
+// does).  end[s] receives p0 + n (0 for sequences without rows); the caller
+// raises the cached lengths to it (commit_len) once the rows have run, so a
+// failure leaves no length counting positions whose K/V were never written.
 int upload_rows(myl_model* m, BatchState* b, uint32_t R, const uint32_t* seq, const uint32_t* pos, const uint32_t* tok,
-                int* lmax) {
+                int* lmax, std::vector<uint32_t>* end_out) {
     myl_ctx* c = m->ctx;
     std::vector<std::vector<uint32_t>> per(b->n_seqs);
     int lm = 0;
@@ -713,9 +715,13 @@ int upload_rows(myl_model* m, BatchState* b, uint32_t R, const uint32_t* seq, co
     // the pageable source must stay alive until the copy has been consumed
     rc = c->hip(hipStreamSynchronize(c->stream), "batch rows");
     if (rc) return rc;
-    for (int s = 0; s < b->n_seqs; ++s) b->len[s] = std::max(b->len[s], end[s]);
     *lmax = lm;
+    end_out->swap(end);
     return MYL_OK;
+}
+
+void commit_len(BatchState* b, const std::vector<uint32_t>& end) {
+    for (int s = 0; s < b->n_seqs; ++s) b->len[s] = std::max(b->len[s], end[s]);
 }
 
 // Whether the row path can run this model, and its kernels' LDS limits.
@@ -787,12 +793,14 @@ int prompt_rows(myl_model* m, const uint32_t* tokens, uint32_t n, uint32_t pos0)
         pos.resize(k);
         for (uint32_t i = 0; i < k; ++i) pos[i] = pos0 + i0 + i;
         int lmax = 0;
-        int rc = upload_rows(m, b, k, seq.data(), pos.data(), tokens + i0, &lmax);
+        std::vector<uint32_t> end;
+        int rc = upload_rows(m, b, k, seq.data(), pos.data(), tokens + i0, &lmax, &end);
         if (rc) return rc;
         // only the chunk that ends the prompt needs its last row's logits
         const int h0 = i0 + k == n ? (int)k - 1 : (int)k;
         rc = c->hip(forward_rows(m, b, (int)k, lmax, h0, m->logits, b->argmax), "prefill rows");
         if (rc) return rc;
+        commit_len(b, end);
     }
     return MYL_OK;
 }
@@ -837,10 +845,12 @@ int myl_model_forward_batch(myl_model* m, uint32_t n_rows, const uint32_t* seq, 
     if (n_rows == 0) return MYL_OK;
     int lmax = 0;
     BatchState* b = m->batch;
-    int rc = upload_rows(m, b, n_rows, seq, pos, tokens, &lmax);
+    std::vector<uint32_t> end;
+    int rc = upload_rows(m, b, n_rows, seq, pos, tokens, &lmax, &end);
     if (rc) return rc;
     rc = c->hip(forward_rows(m, b, (int)n_rows, lmax, 0, b->logits, b->argmax), "forward_batch");
     if (rc) return rc;
+    commit_len(b, end);
     if (logits) {
         rc = c->hip(hipMemcpyAsync(logits, b->logits, (size_t)n_rows * m->V * 4, hipMemcpyDeviceToHost, c->stream),
                     "logits");
@@ -877,7 +887,8 @@ int myl_model_batch_decode_greedy(myl_model* m, uint32_t n_rows, const uint32_t*
     }
     int lmax = 0;
     BatchState* b = m->batch;
-    int rc = upload_rows(m, b, n_rows, seq, pos, tokens, &lmax);
+    std::vector<uint32_t> end;
+    int rc = upload_rows(m, b, n_rows, seq, pos, tokens, &lmax, &end);
     if (rc) return rc;
     const size_t need = (size_t)n_steps * n_rows;
     if (need > b->tokens_out_cap) {

@@ -12,6 +12,7 @@
 #include "gemm_mfma.h"
 #include "gemm_mfma2.h"
 #include "gemv.h"
+#include "gemv_stream.h"
 #include "internal.h"
 
 #include <algorithm>
@@ -224,6 +225,11 @@ inline hipError_t gemv_i8(const int16_t* x, int M, int ldx, const int8_t* W, int
     // rows).  Up to 64 rows are one tile row, so the weights stream once; the
     // multi-row GEMV below reached only ~0.6 TB/s at 8 rows on MI355X.
     if (M > 1 && xvec_ok(x, ldx)) return mm_i8(x, M, ldx, W, N, K, epi, mm, st);
+    // One row: the persistent streaming kernel of the decode step.
+    if (M == 1 && xvec_ok(x, ldx)) {
+        const int cus = mm ? mm->cus : 256;
+        if (const int shape = stream_rows_shape(N, K, cus)) return stream_rows_i8(shape, x, W, N, K, epi, st, cus);
+    }
     // Activation rows in groups of at most 8.
     for (int m0 = 0; m0 < M; m0 += 8) {
         const int mm_rows = min(8, M - m0);

@@ -381,4 +381,128 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i16_stream(Src16 src, const i
     epi.finish(es);
 }
 
+// ---- launchers ------------------------------------------------------------------
+
+// Blocks of a kernel that fit on one CU at `lds` bytes of dynamic LDS.  The
+// answer is cached per kernel instantiation (the last LDS size asked), so a
+// launch of a few microseconds does not wait for the runtime query.
+template <class Kern>
+int stream_occupancy(Kern kern, int threads, size_t lds) {
+    static thread_local size_t last_lds = ~(size_t)0;
+    static thread_local int last_occ = 1;
+    if (lds != last_lds) {
+        int occ = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, threads, lds) != hipSuccess || occ < 1) occ = 1;
+        last_lds = lds;
+        last_occ = occ;
+    }
+    return last_occ;
+}
+
+// Persistent grid: as many blocks as fit on the device, shrunk so that every
+// wave gets the same number of row groups (no tail of half-filled rounds).
+// Returns the grid and, in gpw, the most groups one wave handles.
+template <class Kern>
+int stream_grid(Kern kern, int waves_per_block, size_t lds, int ngroups, int cus, int* gpw) {
+    const int occ = stream_occupancy(kern, waves_per_block * 64, lds);
+    const int waves_cap = occ * cus * waves_per_block;
+    const int per_wave = (ngroups + waves_cap - 1) / waves_cap;
+    const int waves = (ngroups + per_wave - 1) / per_wave;
+    const int grid = (waves + waves_per_block - 1) / waves_per_block;
+    const int nw = grid * waves_per_block;
+    *gpw = (ngroups + nw - 1) / nw;
+    return grid;
+}
+
+// Records are sized for up to kGpwReserve groups per wave when the occupancy
+// is computed; larger counts still run correctly (the LDS grows to fit).
+constexpr int kGpwReserve = 16;
+constexpr size_t kStreamLdsMax = 64 * 1024;
+
+template <int R, int U, int WAVES, bool PF2 = false, class Src, class Epi>
+hipError_t stream_i8(const Src& src, const int8_t* W, int N, int K, const Epi& e, hipStream_t s, int cus) {
+    // one buffer descriptor; i32 partial sums exact for K < 131072
+    if ((uint64_t)N * (uint64_t)K > 0xFFFFFF00ull || K >= 131072 || N < 1 || K < 1) return hipErrorInvalidValue;
+    auto kern = gemv_i8_stream<R, U, WAVES, Src, Epi, PF2>;
+    int gpw = 0;
+    const int grid = stream_grid(kern, WAVES, stream_lds_bytes(K, 1, WAVES, kGpwReserve, R), (N + R - 1) / R, cus, &gpw);
+    const size_t lds = stream_lds_bytes(K, 1, WAVES, gpw, R);
+    if (lds > kStreamLdsMax) return hipErrorInvalidValue;
+    kern<<<grid, WAVES * 64, lds, s>>>(src, W, N, K, gpw, e);
+    return hipGetLastError();
+}
+
+template <int R, int U, int WAVES, class Src, class Epi>
+hipError_t stream_i16(const Src& src, const int16_t* W, int N, int K, const Epi& e, hipStream_t s, int cus) {
+    // one buffer descriptor; per-lane i32 partials exact for K <= 8192
+    if (2ull * (uint64_t)N * (uint64_t)K > 0xFFFFFF00ull || K > 8192 || N < 1 || K < 1) return hipErrorInvalidValue;
+    auto kern = gemv_i16_stream<R, U, WAVES, Src, Epi>;
+    int gpw = 0;
+    const int grid = stream_grid(kern, WAVES, stream_lds_bytes(K, 2, WAVES, kGpwReserve, R), (N + R - 1) / R, cus, &gpw);
+    const size_t lds = stream_lds_bytes(K, 2, WAVES, gpw, R);
+    if (lds > kStreamLdsMax) return hipErrorInvalidValue;
+    kern<<<grid, WAVES * 64, lds, s>>>(src, W, N, K, gpw, e);
+    return hipGetLastError();
+}
+
+// ---- row-wise epilogues in the streaming interface ------------------------------
+
+struct NoState {};
+
+// Drives an epilogue of the row-wise form one(n, m, acc) (gemv.h, rows_epi.h)
+// for one activation row.
+template <class Epi>
+struct StreamOne {
+    Epi e;
+    using State = NoState;
+    __device__ inline void begin(State&) const {}
+    __device__ inline void prefetch(State&, int, int) const {}
+    __device__ inline void finish(State&) const {}
+    template <int R>
+    __device__ inline void group(State&, int row0, int N, const int64_t (&tot)[R]) const {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (row0 + r < N) e.one(row0 + r, 0, tot[r]);
+    }
+};
+
+// Whether stream_i8<R, U, WAVES> takes N rows of K int8 weights: one buffer
+// descriptor, exact i32 partials, and the LDS of the widest grid stream_grid
+// can choose (at least one block per CU, so at most
+// ceil(ceil(N / R) / (cus * WAVES)) groups per wave).
+template <int R, int WAVES>
+inline bool stream_fits(int N, int K, int cus) {
+    if (N < 1 || K < 1 || K % 16 != 0 || K >= 131072 || (uint64_t)N * (uint64_t)K > 0xFFFFFF00ull || cus < 1)
+        return false;
+    const int ngroups = (N + R - 1) / R;
+    const int gpw = (ngroups + cus * WAVES - 1) / (cus * WAVES);
+    return stream_lds_bytes(K, 1, WAVES, gpw, R) <= kStreamLdsMax;
+}
+
+// Launch shape of one activation row through the streaming kernel, the
+// decode step's shape for a product of the same kind: many rows (gate/up,
+// LM head) two rows per wave and 8-wave blocks; a long K (down) one row per
+// wave; short K and few rows (o_proj) 16-wave blocks.  0: the stream does
+// not take the shape.
+inline int stream_rows_shape(int N, int K, int cus) {
+    if (N >= 8192) return stream_fits<2, 8>(N, K, cus) ? 1 : 0;
+    if (K >= 8192) return stream_fits<1, 8>(N, K, cus) ? 2 : 0;
+    return stream_fits<1, 16>(N, K, cus) ? 3 : 0;
+}
+
+// One activation row x (16-byte aligned) of a W8A16 product with a row-wise
+// epilogue, in the shape stream_rows_shape chose (nonzero).
+template <class Epi>
+hipError_t stream_rows_i8(int shape, const int16_t* x, const int8_t* W, int N, int K, const Epi& epi, hipStream_t st,
+                          int cus) {
+    const SrcPlain src{x};
+    const StreamOne<Epi> e{epi};
+    switch (shape) {
+        case 1: return stream_i8<2, 4, 8>(src, W, N, K, e, st, cus);
+        case 2: return stream_i8<1, 4, 8>(src, W, N, K, e, st, cus);
+        case 3: return stream_i8<1, 2, 16>(src, W, N, K, e, st, cus);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 }  // namespace myl

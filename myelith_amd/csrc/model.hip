@@ -355,8 +355,6 @@ __global__ __launch_bounds__(1024) void embed_kernel(DecodeState* st, int mode, 
 // fused GEMV epilogues (streaming interface: begin / group per lane / finish)
 // ---------------------------------------------------------------------------
 
-struct NoState {};
-
 // q/k/v projection rows (pair-ordered) -> bias -> RoPE -> q buffer / KV cache.
 struct EpiQKV {
     const uint8_t* shifts;    // per device row
@@ -560,54 +558,6 @@ struct EpiHead {
         }
     }
 };
-
-// Persistent grid: as many blocks as fit on the device, shrunk so that every
-// wave gets the same number of row groups (no tail of half-filled rounds).
-// Returns the grid and, in gpw, the most groups one wave handles.
-template <class Kern>
-int stream_grid(Kern kern, int waves_per_block, size_t lds, int ngroups, int cus, int* gpw) {
-    int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, waves_per_block * 64, lds) != hipSuccess || occ < 1)
-        occ = 1;
-    const int waves_cap = occ * cus * waves_per_block;
-    const int per_wave = (ngroups + waves_cap - 1) / waves_cap;
-    const int waves = (ngroups + per_wave - 1) / per_wave;
-    const int grid = (waves + waves_per_block - 1) / waves_per_block;
-    const int nw = grid * waves_per_block;
-    *gpw = (ngroups + nw - 1) / nw;
-    return grid;
-}
-
-// Records are sized for up to kGpwReserve groups per wave when the occupancy
-// is computed; larger counts still run correctly (the LDS grows to fit).
-constexpr int kGpwReserve = 16;
-constexpr size_t kStreamLdsMax = 64 * 1024;
-
-template <int R, int U, int WAVES, bool PF2 = false, class Src, class Epi>
-hipError_t stream_i8(const Src& src, const int8_t* W, int N, int K, const Epi& e, hipStream_t s, int cus) {
-    // one buffer descriptor; i32 partial sums exact for K < 131072
-    if ((uint64_t)N * (uint64_t)K > 0xFFFFFF00ull || K >= 131072 || N < 1 || K < 1) return hipErrorInvalidValue;
-    auto kern = gemv_i8_stream<R, U, WAVES, Src, Epi, PF2>;
-    int gpw = 0;
-    const int grid = stream_grid(kern, WAVES, stream_lds_bytes(K, 1, WAVES, kGpwReserve, R), (N + R - 1) / R, cus, &gpw);
-    const size_t lds = stream_lds_bytes(K, 1, WAVES, gpw, R);
-    if (lds > kStreamLdsMax) return hipErrorInvalidValue;
-    kern<<<grid, WAVES * 64, lds, s>>>(src, W, N, K, gpw, e);
-    return hipGetLastError();
-}
-
-template <int R, int U, int WAVES, class Src, class Epi>
-hipError_t stream_i16(const Src& src, const int16_t* W, int N, int K, const Epi& e, hipStream_t s, int cus) {
-    // one buffer descriptor; per-lane i32 partials exact for K <= 8192
-    if (2ull * (uint64_t)N * (uint64_t)K > 0xFFFFFF00ull || K > 8192 || N < 1 || K < 1) return hipErrorInvalidValue;
-    auto kern = gemv_i16_stream<R, U, WAVES, Src, Epi>;
-    int gpw = 0;
-    const int grid = stream_grid(kern, WAVES, stream_lds_bytes(K, 2, WAVES, kGpwReserve, R), (N + R - 1) / R, cus, &gpw);
-    const size_t lds = stream_lds_bytes(K, 2, WAVES, gpw, R);
-    if (lds > kStreamLdsMax) return hipErrorInvalidValue;
-    kern<<<grid, WAVES * 64, lds, s>>>(src, W, N, K, gpw, e);
-    return hipGetLastError();
-}
 
 // ---------------------------------------------------------------------------
 // decode attention over the KV cache (attention.rs:42-90), GQA (model.rs:508-511)
@@ -1087,17 +1037,20 @@ hipError_t layer_step(myl_model* m, int l) {
         if (e != hipSuccess) return e;
     }
     {
-        TimedScope t(m, K_GU);
         SrcNorm src{m->resid, L.res_mid, L.post_gamma, L.post_gamma_s, rp, L.ref_mid, f.norm_mlp_frac, m->norm_b};
         EpiSilu s{L.sgu, f.norm_mlp_frac, f.gate_frac, f.up_frac, f.down_in_frac, m->silu, (uint32_t)m->silu_len, m->h,
                   m->attn_acc, nq};
-        // staging loads go out before the weights, so one register buffer in
-        // flight during staging is enough (1.5-2 % faster per decode step on
-        // MI355X than two)
-        e = stream_i8<2, 4, 8>(src, L.wgu, 2 * I, H, s, st, cus);
-        // measurement repeats (myl_model_set_kernel_repeat): the same launch
-        // over the next layers' gate/up weights, which the step last read one
-        // step ago (out of the caches, as this layer's), into scratch rows
+        {
+            TimedScope t(m, K_GU);
+            // staging loads go out before the weights, so one register buffer in
+            // flight during staging is enough (1.5-2 % faster per decode step on
+            // MI355X than two)
+            e = stream_i8<2, 4, 8>(src, L.wgu, 2 * I, H, s, st, cus);
+        }
+        // measurement repeats (myl_model_set_kernel_repeat), outside the timed
+        // class: the same launch over the next layers' gate/up weights, which
+        // the step last read one step ago (out of the caches, as this
+        // layer's), into scratch rows
         for (int rep = 1; rep < m->gu_repeat && e == hipSuccess; ++rep) {
             const LayerDev& Lr = m->layers[(l + rep) % (int)m->spec.layers];
             EpiSilu sr = s;
@@ -1228,6 +1181,10 @@ extern "C" {
 
 int myl_model_set_kernel_repeat(myl_model* m, int kclass, int times) {
     if (!m || kclass != K_GU || times < 1 || times > 4) return MYL_E_INVALID;
+    // each repeat streams another layer's weights; more repeats than layers
+    // would re-read weights this step already brought into the caches
+    if (times > (int)m->spec.layers)
+        return m->ctx->fail(MYL_E_INVALID, "kernel repeat: more repeats than layers");
     (void)hipStreamSynchronize(m->ctx->stream);
     if (times > 1 && !m->h_scratch && !(m->h_scratch = m->dalloc<int16_t>(m->I)))
         return m->ctx->fail(MYL_E_NOMEM, "kernel repeat scratch");

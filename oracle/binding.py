@@ -26,11 +26,16 @@ def build() -> Path:
 
 
 def lib():
+    """The oracle library; MYL_ORACLE_LIB names another build of oracle.c
+    (the mutation test runs the pins against deliberately broken copies)."""
     global _lib
     if _lib is None:
-        if not LIB_PATH.exists():
-            build()
-        _lib = C.CDLL(str(LIB_PATH))
+        path = os.environ.get("MYL_ORACLE_LIB")
+        if not path:
+            if not LIB_PATH.exists():
+                build()
+            path = str(LIB_PATH)
+        _lib = C.CDLL(path)
         _declare(_lib)
     return _lib
 
@@ -70,6 +75,8 @@ def _declare(L) -> None:
         "or_add_bias_i16": (C.c_int, [P, P, P, sz, u8]),
         "or_linear_w8a16_batch": (C.c_int, [P, sz, P, sz, sz, P, u8, u8, P, P]),
         "or_linear_w8a16_mult": (C.c_int, [P, sz, P, sz, sz, P, P, P]),
+        "or_requant_shift": (C.c_int, [P, sz, sz, P, u8, u8, P]),
+        "or_requant_mult": (C.c_int, [P, sz, sz, P, P, P]),
         "or_inv_n_q20": (i64, [sz]),
         "or_rmsnorm_i16": (C.c_int, [P, P, P, P, sz, P, sz, u8, u8, i64, u8, P]),
         "or_rotate_half_split_i16": (C.c_int, [P, sz, P, P, u8, P]),
@@ -94,7 +101,7 @@ def _declare(L) -> None:
         "or_moe_expert": (C.c_int, [P, P, u32, P]),
         "or_moe_router_logits": (None, [P, P, P]),
         "or_model_destroy": (None, [P]), "or_model_reset": (None, [P]),
-        "or_set_threads": (None, [C.c_int]),
+        "or_set_threads": (None, [C.c_int]), "or_set_simd": (None, [C.c_int]),
         "or_model_forward_token": (C.c_int, [P, u32, u32, P]),
         "or_model_embed_token": (C.c_int, [P, u32, P]),
         "or_model_run_layers": (C.c_int, [P, P, u32, u32, u32]),
@@ -186,6 +193,24 @@ def linear_mult(x, W, mult, shift) -> np.ndarray:
     N = W.shape[0]
     out = np.zeros((M, N), np.int16)
     _check(lib().or_linear_w8a16_mult(ptr(x), M, ptr(W), N, K, ptr(mult), ptr(shift), ptr(out)), "linear_mult")
+    return out
+
+
+def requant_shift(acc, w_shifts, act_frac, out_frac) -> np.ndarray:
+    """linear_w8a16's requant (linear.rs:61-68) of exact sums acc [M x N]."""
+    acc, ws = _arr(acc, np.int64), _arr(w_shifts, np.uint8)
+    M, N = acc.shape
+    out = np.zeros((M, N), np.int16)
+    _check(lib().or_requant_shift(ptr(acc), M, N, ptr(ws), act_frac, out_frac, ptr(out)), "requant_shift")
+    return out
+
+
+def requant_mult(acc, mult, shift) -> np.ndarray:
+    """The multiplier requant of exact sums acc [M x N]."""
+    acc, mult, shift = _arr(acc, np.int64), _arr(mult, np.int32), _arr(shift, np.uint8)
+    M, N = acc.shape
+    out = np.zeros((M, N), np.int16)
+    _check(lib().or_requant_mult(ptr(acc), M, N, ptr(mult), ptr(shift), ptr(out)), "requant_mult")
     return out
 
 
@@ -343,12 +368,19 @@ class OracleModel:
         return k, v
 
     def tensor(self, name: str, layer: int = 0, dtype=np.int8) -> np.ndarray:
+        """A copy of one of the model's tensors (or_model_tensor names)."""
+        return self.tensor_view(name, layer, dtype).copy()
+
+    def tensor_view(self, name: str, layer: int = 0, dtype=np.int8) -> np.ndarray:
+        """The model's own memory for tensor `name`: writes change the model
+        (tests build special-case layers this way).  "layer_fracs" is the
+        nine bytes norm_attn, q, k, v, attn_out, norm_mlp, gate, up, down_in."""
         n = sz()
         p = lib().or_model_tensor(self._h, name.encode(), layer, C.byref(n))
         if not p:
             raise KeyError(name)
         buf = (C.c_char * n.value).from_address(p)
-        return np.frombuffer(bytes(buf), dtype=dtype)
+        return np.frombuffer(buf, dtype=dtype)
 
 
 class OracleMoe:

@@ -20,6 +20,12 @@ typedef unsigned __int128 u128;
 static int g_threads = 1;
 void or_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
 
+/* Dot-product form: 0 = the scalar i64 loop of dot.rs:141-147 (the reference
+ * backend), 1 = i32 blocks drained to i64 (the cpu-simd backend's scheme,
+ * dot.rs:175-221).  Both are exact, so every result is the same. */
+static int g_simd = 1;
+void or_set_simd(int on) { g_simd = on != 0; }
+
 /* ---- release-mode shift helpers ---------------------------------------- */
 static inline int32_t shl32(int32_t v, uint32_t s) { return (int32_t)((uint32_t)v << (s & 31u)); }
 static inline int32_t shr32(int32_t v, uint32_t s) { return v >> (s & 31u); }
@@ -122,8 +128,23 @@ int64_t or_inv_sqrt_q15(size_t head_dim) {
 
 /* ---- dot.rs / linear.rs ------------------------------------------------- */
 
+/* dot.rs:175-221: products summed in i32 over blocks of 256 elements, then
+ * widened.  |w| <= 128 and |x| <= 32768 bound a block by 2^30 < 2^31, so no
+ * i32 sum wraps and the total equals the scalar loop's (dot.rs:266-296). */
+static int64_t dot_i8_i16_blocks(const int8_t* w, const int16_t* x, size_t n) {
+    int64_t acc = 0;
+    for (size_t i = 0; i < n; i += 256) {
+        size_t e = n - i < 256 ? n : i + 256;
+        int32_t s = 0;
+        for (size_t j = i; j < e; ++j) s += (int32_t)w[j] * (int32_t)x[j];
+        acc += s;
+    }
+    return acc;
+}
+
 /* dot.rs:141-147 (the numeric contract; any summation order is equal). */
 int64_t or_dot_i8_i16(const int8_t* w, const int16_t* x, size_t n) {
+    if (g_simd) return dot_i8_i16_blocks(w, x, n);
     uint64_t acc = 0;
     for (size_t i = 0; i < n; ++i) acc += (uint64_t)((int64_t)w[i] * (int64_t)x[i]);
     return (int64_t)acc;
@@ -181,22 +202,46 @@ int or_linear_w8a16_batch(const int16_t* x, size_t M, const int8_t* W, size_t N,
     return 0;
 }
 
-/* Build-defined multiplier requant.  With mult = 2^k and shift = k + s_ref it
- * equals linear_w8a16's rescale by s_ref >= 0 (the identity proved by
+/* Build-defined multiplier requant of one sum: clamp16(RNE(acc * mult, shift))
+ * in 128 bits.  With mult = 2^k and shift = k + s_ref it equals
+ * linear_w8a16's rescale by s_ref >= 0 (the identity proved by
  * fixed_point.rs:364-379). */
+static int16_t requant_mult(int64_t acc, int32_t mult, uint8_t shift) {
+    i128 y = rshift_round_i128((i128)acc * (i128)mult, shift);
+    return y < -32768 ? -32768 : (y > 32767 ? 32767 : (int16_t)y);
+}
+
 int or_linear_w8a16_mult(const int16_t* x, size_t M, const int8_t* W, size_t N, size_t K,
                          const int32_t* mult, const uint8_t* shift, int16_t* out) {
     if (K == 0) return -1;
     for (size_t m = 0; m < M; ++m) {
         long long NN = (long long)N;
 #pragma omp parallel for if (g_threads > 1 && NN > 64) num_threads(g_threads) schedule(static)
-        for (long long r = 0; r < NN; ++r) {
-            int64_t acc = or_dot_i8_i16(W + (size_t)r * K, x + m * K, K);
-            i128 p = (i128)acc * (i128)mult[r];
-            i128 y = rshift_round_i128(p, shift[r]);
-            int16_t o = y < -32768 ? -32768 : (y > 32767 ? 32767 : (int16_t)y);
-            out[m * N + (size_t)r] = o;
-        }
+        for (long long r = 0; r < NN; ++r)
+            out[m * N + (size_t)r] = requant_mult(or_dot_i8_i16(W + (size_t)r * K, x + m * K, K), mult[r], shift[r]);
+    }
+    return 0;
+}
+
+/* The requant step of linear_w8a16 (linear.rs:61-68) and of the multiplier
+ * form on sums computed elsewhere: acc [M x N] exact i64 dot products. */
+int or_requant_shift(const int64_t* acc, size_t M, size_t N, const uint8_t* w_shifts, uint8_t act_frac,
+                     uint8_t out_frac, int16_t* out) {
+    long long n = (long long)(M * N);
+#pragma omp parallel for if (g_threads > 1 && n > 4096) num_threads(g_threads) schedule(static)
+    for (long long i = 0; i < n; ++i) {
+        size_t r = (size_t)i % N;
+        out[i] = or_clamp_i16_from_i64(or_rescale_i64(acc[i], (uint8_t)(w_shifts[r] + act_frac), out_frac));
+    }
+    return 0;
+}
+
+int or_requant_mult(const int64_t* acc, size_t M, size_t N, const int32_t* mult, const uint8_t* shift, int16_t* out) {
+    long long n = (long long)(M * N);
+#pragma omp parallel for if (g_threads > 1 && n > 4096) num_threads(g_threads) schedule(static)
+    for (long long i = 0; i < n; ++i) {
+        size_t r = (size_t)i % N;
+        out[i] = requant_mult(acc[i], mult[r], shift[r]);
     }
     return 0;
 }
@@ -711,13 +756,17 @@ static int forward_layer(or_model* m, uint32_t l, const int16_t* hidden, uint32_
         uint32_t ss = (uint32_t)sc->q_frac + sc->k_frac + 15u;
         uint8_t score_shift = (uint8_t)(ss > MYL_TV_SCORE_FRAC_BITS ? ss - MYL_TV_SCORE_FRAC_BITS : 0);
         uint8_t lut_shift = MYL_TV_SCORE_FRAC_BITS > MYL_TV_EXP_INPUT_FRAC ? MYL_TV_SCORE_FRAC_BITS - MYL_TV_EXP_INPUT_FRAC : 0;
-        for (uint32_t h = 0; h < s->heads && !rc; ++h) {
-            uint32_t kvh = h / group;
-            rc = or_attention_int(qr + h * hd, kv_at(m->kcache, s, l, kvh, 0), kv_at(m->vcache, s, l, kvh, 0),
-                                  NULL, 1, (size_t)pos + 1, hd, score_mult, score_shift, m->exp_lut, m->exp_len,
-                                  lut_shift, MYL_TV_PROB_FRAC_BITS, attn + h * hd);
+        /* heads are independent: each writes its own slice of attn */
+        int bad = 0;
+        long long nh = (long long)s->heads;
+#pragma omp parallel for if (g_threads > 1 && pos >= 64) num_threads(g_threads) schedule(static) reduction(| : bad)
+        for (long long h = 0; h < nh; ++h) {
+            uint32_t kvh = (uint32_t)h / group;
+            bad |= or_attention_int(qr + h * hd, kv_at(m->kcache, s, l, kvh, 0), kv_at(m->vcache, s, l, kvh, 0),
+                                    NULL, 1, (size_t)pos + 1, hd, score_mult, score_shift, m->exp_lut, m->exp_len,
+                                    lut_shift, MYL_TV_PROB_FRAC_BITS, attn + h * hd) != 0;
         }
-        if (rc) goto done;
+        if (bad) { rc = -3; goto done; }
     }
     /* v_frac -> attn_out_frac (:563-567) */
     if (sc->attn_out_frac != sc->v_frac)

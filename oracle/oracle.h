@@ -58,6 +58,12 @@ int or_linear_w8a16_batch(const int16_t* x, size_t M, const int8_t* W, size_t N,
  * y[m][r] = clamp_i16(rshift_round_i128(dot(W[r], x[m]) * mult[r], shift[r])). */
 int or_linear_w8a16_mult(const int16_t* x, size_t M, const int8_t* W, size_t N, size_t K,
                          const int32_t* mult, const uint8_t* shift, int16_t* out);
+/* The two requant steps on precomputed exact sums acc [M x N]:
+ * clamp_i16(rescale_i64(acc, w_shifts[r] + act_frac, out_frac)) (linear.rs:61-68)
+ * and the multiplier form above. */
+int or_requant_shift(const int64_t* acc, size_t M, size_t N, const uint8_t* w_shifts, uint8_t act_frac,
+                     uint8_t out_frac, int16_t* out);
+int or_requant_mult(const int64_t* acc, size_t M, size_t N, const int32_t* mult, const uint8_t* shift, int16_t* out);
 
 /* ---- rmsnorm.rs -------------------------------------------------------- */
 int64_t or_inv_n_q20(size_t n);                                          /* rmsnorm.rs:20-23 */
@@ -115,6 +121,7 @@ or_model* or_model_create_synthetic(const myl_synth_spec* spec, const myl_luts* 
 void or_model_destroy(or_model* m);
 void or_model_reset(or_model* m);                   /* empty KV cache */
 void or_set_threads(int n);                          /* rows of a GEMV split over n threads (results unchanged) */
+void or_set_simd(int on);                            /* 1: i32-block dot (dot.rs:175-221), 0: scalar i64 loop; results unchanged */
 /* model.rs:229-311; logits has vocab entries. */
 int or_model_forward_token(or_model* m, uint32_t token, uint32_t pos, int32_t* logits);
 /* model.rs:323-331 */

@@ -269,3 +269,5 @@ def test_repeated_gate_up_leaves_the_decode_unchanged(backend):
     gm.set_kernel_repeat("gate_up", 1)
     with pytest.raises(ValueError):
         gm.set_kernel_repeat("down", 2)
+    with pytest.raises(ValueError):  # more repeats than the model's 3 layers
+        gm.set_kernel_repeat("gate_up", 4)

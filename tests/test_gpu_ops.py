@@ -99,32 +99,51 @@ def test_linear_rejects_what_the_reference_panics_on(backend):
 SWEEP = [(3584, 3584), (18944, 3584), (3584, 18944), (152064, 3584)]
 
 
+def exact_sums(x, W, chunk=16384):
+    """x [M x K] int16 times W [N x K] int8 as exact i64 sums: every product
+    and partial sum is an integer below 2^53, so float64 arithmetic is exact
+    in any summation order."""
+    xf = x.astype(np.float64)
+    out = np.empty((x.shape[0], W.shape[0]), np.int64)
+    for n0 in range(0, W.shape[0], chunk):
+        out[:, n0:n0 + chunk] = (xf @ W[n0:n0 + chunk].astype(np.float64).T).astype(np.int64)
+    return out
+
+
 @pytest.mark.parametrize("N,K", SWEEP)
 @pytest.mark.parametrize("M", [1, 8, 64, 512])
 def test_w8a16_sweep_shapes_dev(backend, oracle, M, N, K):
-    """The W8A16 sweep shapes (M x N x K), shift requant and multiplier requant."""
+    """The W8A16 sweep cells (M x N x K) at their full size, so each takes
+    the tile it runs in the benchmark (e.g. M = 8 x N = 152064 the K-split
+    32-row plane tiles of 128 weight rows): shift requant and multiplier
+    requant against the oracle's requant of the exact sums, and a row
+    subset against the oracle's own linear_w8a16."""
     import torch
     case(f"sweep M={M} N={N} K={K}")
     r = rng(M * 7 + N * 3 + K)
-    # Full N up to ~1 G multiply-adds of oracle work; beyond that a row subset of the same K.
-    Nt = N if M * N * K <= (1 << 30) else max(256, ((1 << 30) // (M * K)) // 16 * 16)
     x = gauss16(r, M * K).reshape(M, K)
-    W = r.integers(-127, 128, (Nt, K)).astype(np.int8)
-    ws = r.integers(8, 14, Nt).astype(np.uint8)
-    mult = r.integers(1 << 29, (1 << 30) + 1, Nt).astype(np.int32)
-    sh = r.integers(20, 41, Nt).astype(np.uint8)
+    W = r.integers(-127, 128, (N, K)).astype(np.int8)
+    ws = r.integers(8, 14, N).astype(np.uint8)
+    mult = r.integers(1 << 29, (1 << 30) + 1, N).astype(np.int32)
+    sh = r.integers(20, 41, N).astype(np.uint8)
     oracle.lib().or_set_threads(16)
     xd, Wd = torch.from_numpy(x).cuda(), torch.from_numpy(W).cuda()
-    got = backend.linear_w8a16_dev(xd, Wd, torch.from_numpy(ws).cuda(), 11, 10).cpu().numpy()
-    assert np.array_equal(got, oracle.linear_batch(x, W, ws, 11, 10))
-    got = backend.linear_w8a16_mult_dev(xd, Wd, torch.from_numpy(mult).cuda(), torch.from_numpy(sh).cuda())
-    assert np.array_equal(got.cpu().numpy(), oracle.linear_mult(x, W, mult, sh))
+    got_s = backend.linear_w8a16_dev(xd, Wd, torch.from_numpy(ws).cuda(), 11, 10).cpu().numpy()
+    got_m = backend.linear_w8a16_mult_dev(xd, Wd, torch.from_numpy(mult).cuda(), torch.from_numpy(sh).cuda())
+    got_m = got_m.cpu().numpy()
     # multiplier = 2^k with shift = k + reference shift reproduces the reference rescale
     k = 29
-    m2 = np.full(Nt, 1 << k, np.int32)
+    m2 = np.full(N, 1 << k, np.int32)
     s2 = (ws.astype(np.int32) + 11 - 10 + k).astype(np.uint8)
-    got = backend.linear_w8a16_mult_dev(xd, Wd, torch.from_numpy(m2).cuda(), torch.from_numpy(s2).cuda())
-    assert np.array_equal(got.cpu().numpy(), oracle.linear_batch(x, W, ws, 11, 10))
+    got_2 = backend.linear_w8a16_mult_dev(xd, Wd, torch.from_numpy(m2).cuda(), torch.from_numpy(s2).cuda())
+    got_2 = got_2.cpu().numpy()
+    acc = exact_sums(x, W)
+    want_s = oracle.requant_shift(acc, ws, 11, 10)
+    assert np.array_equal(got_s, want_s)
+    assert np.array_equal(got_m, oracle.requant_mult(acc, mult, sh))
+    assert np.array_equal(got_2, want_s)
+    rows = np.unique(np.concatenate([np.arange(min(N, 64)), r.integers(0, N, 192)]))
+    assert np.array_equal(got_s[:, rows], oracle.linear_batch(x, W[rows], ws[rows], 11, 10))
 
 
 # ---- matrix-core path (M > 8): every tile shape, with and without K splits ----------

@@ -101,17 +101,44 @@ def test_rescale_negative_shift_is_plain_left_shift(oracle):
 
 # ---- dot.rs / linear.rs ---------------------------------------------------------
 
-def test_dot_extremes_and_order(oracle):
+@pytest.mark.parametrize("simd", [0, 1])
+def test_dot_extremes_and_order(oracle, simd):
     # dot.rs:306-327: extremes beyond i32; any order gives the same exact sum.
+    # Both dot forms: the scalar i64 loop and the i32 blocks of 256 products,
+    # whose worst block (-128 * -32768 * 256 = 2^30) must not wrap.
     rng = np.random.default_rng(0)
     w = rng.integers(-128, 128, 4096).astype(np.int8)
     x = rng.integers(-32768, 32768, 4096).astype(np.int16)
     L = oracle.lib()
-    exact = int(np.dot(w.astype(np.int64), x.astype(np.int64)))
-    assert L.or_dot_i8_i16(w.ctypes.data, x.ctypes.data, 4096) == exact
-    w2 = np.full(20000, -128, np.int8)
-    x2 = np.full(20000, -32768, np.int16)
-    assert L.or_dot_i8_i16(w2.ctypes.data, x2.ctypes.data, 20000) == 20000 * 128 * 32768
+    L.or_set_simd(simd)
+    try:
+        exact = int(np.dot(w.astype(np.int64), x.astype(np.int64)))
+        assert L.or_dot_i8_i16(w.ctypes.data, x.ctypes.data, 4096) == exact
+        for n in (20000, 256, 257, 255, 1):
+            w2 = np.full(n, -128, np.int8)
+            x2 = np.full(n, -32768, np.int16)
+            assert L.or_dot_i8_i16(w2.ctypes.data, x2.ctypes.data, n) == n * 128 * 32768
+            x2[:] = 32767
+            assert L.or_dot_i8_i16(w2.ctypes.data, x2.ctypes.data, n) == -n * 128 * 32767
+    finally:
+        L.or_set_simd(1)
+
+
+def test_requant_of_exact_sums_equals_the_linear_forms(oracle):
+    # The requant steps on precomputed sums give what linear_w8a16 and the
+    # multiplier form give on the same operands.
+    rng = np.random.default_rng(12)
+    M, N, K = 3, 70, 300
+    W = rng.integers(-128, 128, (N, K)).astype(np.int8)
+    x = rng.integers(-32768, 32768, (M, K)).astype(np.int16)
+    x[0, :3] = (-32768, 32767, 0)
+    acc = x.astype(np.int64) @ W.astype(np.int64).T
+    ws = rng.integers(0, 14, N).astype(np.uint8)
+    assert np.array_equal(oracle.requant_shift(acc, ws, 11, 4), oracle.linear_batch(x, W, ws, 11, 4))
+    assert np.array_equal(oracle.requant_shift(acc, ws, 2, 9), oracle.linear_batch(x, W, ws, 2, 9))
+    mult = rng.integers(1 << 29, (1 << 30) + 1, N).astype(np.int32)
+    sh = rng.integers(20, 41, N).astype(np.uint8)
+    assert np.array_equal(oracle.requant_mult(acc, mult, sh), oracle.linear_mult(x, W, mult, sh))
 
 
 def test_linear_kats(oracle):
