@@ -144,6 +144,21 @@ int myl_linear_w8a16_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, c
 int myl_linear_w8a16_mult_dev(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, const int8_t* W, size_t N,
                               size_t K, const int32_t* mult, const uint8_t* shift, int16_t* out, size_t ldo);
 
+/* No counterpart in the reference: myl_linear_w8a16_dev for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments and results; it
+ * calls no hipMalloc / hipFree.  Its scratch (activation byte planes and
+ * split-K partial sums) is one fixed device array per GPU of
+ * myl_noalloc_scratch_bytes() bytes, held until the process ends: 2 * M * K
+ * must not exceed 4 MiB when M >= 2 (MYL_E_INVALID otherwise; one row needs
+ * no scratch).  Calls that overlap on one GPU share that array and race; the
+ * caller orders them. */
+int myl_linear_w8a16_dev_noalloc(myl_ctx* ctx, const int16_t* x, size_t M, size_t ldx, const int8_t* W, size_t N,
+                                 size_t K, const uint8_t* w_shifts, uint8_t act_frac, uint8_t out_frac,
+                                 const uint8_t* out_frac_pc, int16_t* out, size_t ldo);
+/* Bytes of the per-GPU scratch array of myl_linear_w8a16_dev_noalloc. */
+size_t myl_noalloc_scratch_bytes(void);
+
 /* LM head (model.rs:284-308): logits[m][r] = clamp_i32(rescale_i64(W[r].x[m],
  * row_shifts[r] + norm_frac, logit_frac)); w_bits = 16 for the int16 head
  * (path A), 8 for the tied int8 embedding (path B). */

@@ -77,6 +77,8 @@ SIGNATURES: dict[str, tuple] = {
     "myl_mlp": (INT, [P, P, P, P, P, P, sz, sz, P, P, P, P, sz, u8, u8, u8, u8, u8, i16, u8, P]),
     "myl_argmax_int": (INT, [P, P, sz, C.POINTER(i64)]),
     "myl_linear_w8a16_dev": (INT, [P, P, sz, sz, P, sz, sz, P, u8, u8, P, P, sz]),
+    "myl_linear_w8a16_dev_noalloc": (INT, [P, P, sz, sz, P, sz, sz, P, u8, u8, P, P, sz]),
+    "myl_noalloc_scratch_bytes": (sz, []),
     "myl_linear_w8a16_mult_dev": (INT, [P, P, sz, sz, P, sz, sz, P, P, P, sz]),
     "myl_logits_dev": (INT, [P, P, sz, sz, P, INT, sz, sz, P, u8, u8, P, sz]),
     "myl_dot_i8_i16_dev": (INT, [P, P, sz, sz, P, sz, sz, P, sz]),

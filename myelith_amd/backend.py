@@ -219,6 +219,18 @@ class RocmBackend:
                                               out.data_ptr(), out.stride(0)), "linear_w8a16_dev")
         return out
 
+    def linear_w8a16_dev_noalloc(self, x, W, w_shifts, act_frac: int, out_frac: int = 0, out_frac_pc=None, out=None):
+        """linear_w8a16_dev without device allocation: `out` must be given
+        (the library allocates nothing; include/myl_hip.h states the limit)."""
+        M, K = x.shape
+        N = W.shape[0]
+        assert out is not None and tuple(out.shape) == (M, N), "out [M x N] is the caller's"
+        self.check(lib().myl_linear_w8a16_dev_noalloc(self._h, x.data_ptr(), M, x.stride(0), W.data_ptr(), N, K,
+                                                      w_shifts.data_ptr(), act_frac, out_frac,
+                                                      None if out_frac_pc is None else out_frac_pc.data_ptr(),
+                                                      out.data_ptr(), out.stride(0)), "linear_w8a16_dev_noalloc")
+        return out
+
     def linear_w8a16_mult_dev(self, x, W, mult, shift, out=None):
         import torch
         M, K = x.shape

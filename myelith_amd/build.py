@@ -30,6 +30,7 @@ SOURCES = {  # source -> is HIP device code
     "batch.hip": True,
     "moe.hip": True,
     "model_io.hip": True,
+    "noalloc.hip": True,
     "abi.cpp": False,
     "artifact.cpp": False,
 }

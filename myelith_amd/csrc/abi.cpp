@@ -102,6 +102,12 @@ int myl_init(int device_id, myl_ctx** out) {
         return MYL_E_HIP;
     }
     c->stream = c->own_stream;
+    // the allocation-free product's scratch address on this device (current)
+    if (noalloc_setup(device_id) != MYL_OK) {
+        (void)hipStreamDestroy(c->own_stream);
+        delete c;
+        return MYL_E_HIP;
+    }
     *out = c;
     return MYL_OK;
 }
@@ -227,8 +233,6 @@ struct Stage {
         return ctx->hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     }
 };
-
-inline bool fits_int(size_t v) { return v <= (size_t)INT32_MAX; }
 
 }  // namespace
 

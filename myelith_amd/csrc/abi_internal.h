@@ -27,3 +27,13 @@ struct myl_ctx {
     // (both grown on demand within caps; nullptr only when allocation fails).
     const myl::MmCtx* mm_ctx(size_t elems, size_t plane_bytes = 0);
 };
+
+namespace myl {
+
+inline bool fits_int(size_t v) { return v <= (size_t)INT32_MAX; }
+
+// Looks up, with `device` current, the device address of the scratch array of
+// the allocation-free product (noalloc.hip) once per device.
+int noalloc_setup(int device);
+
+}  // namespace myl
