@@ -107,6 +107,8 @@ def _declare(L) -> None:
         "or_model_run_layers": (C.c_int, [P, P, u32, u32, u32]),
         "or_model_head_logits": (C.c_int, [P, P, P]),
         "or_model_read_kv": (C.c_int, [P, u32, u32, u32, P, P]),
+        "or_model_write_kv": (C.c_int, [P, u32, u32, u32, P, P]),
+        "or_model_set_cached": (C.c_int, [P, u32]),
         "or_model_tensor": (P, [P, C.c_char_p, u32, C.POINTER(sz)]),
     }
     for name, (res, args) in sigs.items():
@@ -366,6 +368,16 @@ class OracleModel:
         v = np.zeros((n_pos, hd), np.int16)
         _check(lib().or_model_read_kv(self._h, layer, kv_head, n_pos, ptr(k), ptr(v)), "read_kv")
         return k, v
+
+    def write_kv(self, layer: int, kv_head: int, k, v) -> None:
+        """Overwrites cache positions [0, len(k)) of (layer, kv_head)."""
+        k, v = _arr(k, np.int16), _arr(v, np.int16)
+        assert k.shape == v.shape and k.shape[1] == self.spec["head_dim"]
+        _check(lib().or_model_write_kv(self._h, layer, kv_head, k.shape[0], ptr(k), ptr(v)), "write_kv")
+
+    def set_cached(self, n_pos: int) -> None:
+        """The cached length: the next forward_token may run at any position <= n_pos."""
+        _check(lib().or_model_set_cached(self._h, n_pos), "set_cached")
 
     def tensor(self, name: str, layer: int = 0, dtype=np.int8) -> np.ndarray:
         """A copy of one of the model's tensors (or_model_tensor names)."""

@@ -871,6 +871,25 @@ int or_model_forward_token(or_model* m, uint32_t token, uint32_t pos, int32_t* l
     return rc;
 }
 
+/* KVCache::write for positions [0, n_pos) of one (layer, KV head), and the
+ * cached length: continues a run whose cache another implementation built
+ * (kv_cache.rs:38-52). */
+int or_model_write_kv(or_model* m, uint32_t layer, uint32_t kv_head, uint32_t n_pos, const int16_t* k,
+                      const int16_t* v) {
+    const myl_synth_spec* s = &m->spec;
+    if (layer >= s->layers || kv_head >= s->kv_heads || n_pos > s->max_pos) return -1;
+    size_t n = (size_t)n_pos * s->head_dim * 2;
+    memcpy(kv_at(m->kcache, s, layer, kv_head, 0), k, n);
+    memcpy(kv_at(m->vcache, s, layer, kv_head, 0), v, n);
+    return 0;
+}
+
+int or_model_set_cached(or_model* m, uint32_t n_pos) {
+    if (n_pos > m->spec.max_pos) return -1;
+    m->n_cached = n_pos;
+    return 0;
+}
+
 int or_model_read_kv(const or_model* m, uint32_t layer, uint32_t kv_head, uint32_t n_pos,
                      int16_t* k_out, int16_t* v_out) {
     const myl_synth_spec* s = &m->spec;

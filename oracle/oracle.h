@@ -133,6 +133,11 @@ int or_model_head_logits(const or_model* m, const int16_t* hidden, int32_t* logi
 /* kv_cache.rs:43-52 for one (layer, kv head): positions [0, n_pos). */
 int or_model_read_kv(const or_model* m, uint32_t layer, uint32_t kv_head, uint32_t n_pos,
                      int16_t* k_out, int16_t* v_out);
+/* kv_cache.rs:38-52 writes of positions [0, n_pos) of one (layer, kv head), and
+ * the cached length: a run continues from a cache another implementation built. */
+int or_model_write_kv(or_model* m, uint32_t layer, uint32_t kv_head, uint32_t n_pos, const int16_t* k,
+                      const int16_t* v);
+int or_model_set_cached(or_model* m, uint32_t n_pos);
 /* Raw tensor access for tests (NULL if the name is unknown). */
 const void* or_model_tensor(const or_model* m, const char* name, uint32_t layer, size_t* bytes);
 
