@@ -321,10 +321,15 @@ struct EpiShift {
     uint8_t act_frac, out_frac;
     int16_t* out; int ldo;
     EpiShift offset_m(int m0) const { EpiShift e = *this; e.out += (size_t)m0 * ldo; return e; }
-    __device__ inline void one(int r, int m, int64_t acc) const {
-        const uint8_t of = out_frac_pc ? out_frac_pc[r] : out_frac;
-        out[(size_t)m * ldo + r] = clamp_i16_i64(rescale64(acc, (uint8_t)(w_shifts[r] + act_frac), of));
+    // the per-row operands, loadable ahead of the sums
+    struct Ops {
+        uint8_t ws, of;
+    };
+    __device__ inline Ops ops(int r) const { return Ops{w_shifts[r], out_frac_pc ? out_frac_pc[r] : out_frac}; }
+    __device__ inline void one_ops(int r, int m, int64_t acc, const Ops& o) const {
+        out[(size_t)m * ldo + r] = clamp_i16_i64(rescale64(acc, (uint8_t)(o.ws + act_frac), o.of));
     }
+    __device__ inline void one(int r, int m, int64_t acc) const { one_ops(r, m, acc, ops(r)); }
     template <int R, int MT>
     __device__ inline void apply(int row0, int N, int M, int lane, const int64_t (&tot)[R][MT]) const {
 #pragma unroll
@@ -341,11 +346,17 @@ struct EpiMult {
     const uint8_t* shift;
     int16_t* out; int ldo;
     EpiMult offset_m(int m0) const { EpiMult e = *this; e.out += (size_t)m0 * ldo; return e; }
-    __device__ inline void one(int r, int m, int64_t acc) const {
-        myl_i128 p = (myl_i128)acc * (myl_i128)mult[r];
-        myl_i128 y = rshift_round128(p, shift[r]);
+    struct Ops {
+        int32_t mult;
+        uint8_t shift;
+    };
+    __device__ inline Ops ops(int r) const { return Ops{mult[r], shift[r]}; }
+    __device__ inline void one_ops(int r, int m, int64_t acc, const Ops& o) const {
+        myl_i128 p = (myl_i128)acc * (myl_i128)o.mult;
+        myl_i128 y = rshift_round128(p, o.shift);
         out[(size_t)m * ldo + r] = y < -32768 ? (int16_t)-32768 : (y > 32767 ? (int16_t)32767 : (int16_t)y);
     }
+    __device__ inline void one(int r, int m, int64_t acc) const { one_ops(r, m, acc, ops(r)); }
     template <int R, int MT>
     __device__ inline void apply(int row0, int N, int M, int lane, const int64_t (&tot)[R][MT]) const {
 #pragma unroll

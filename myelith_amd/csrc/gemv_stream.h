@@ -38,6 +38,10 @@
 
 #include "gemv.h"
 
+#include <algorithm>
+#include <cstdlib>
+#include <type_traits>
+
 namespace myl {
 
 // A raw buffer descriptor over a whole weight matrix (gfx9-family dword 3).
@@ -48,8 +52,12 @@ namespace myl {
 __device__ inline __amdgpu_buffer_rsrc_t weight_rsrc(const void* p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
+// Weight loads are non-temporal (cache-policy bit nt): each weight byte is
+// read once per step, and on MI355X the streaming kernels ran 5-12 % faster
+// with them (decode step 2.29 -> 2.13 ms, int16 LM head 188 -> 165 us).
+constexpr int kWeightCpol = 2;
 __device__ inline uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kWeightCpol);
     return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
 }
 
@@ -384,27 +392,31 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i16_stream(Src16 src, const i
 // ---- launchers ------------------------------------------------------------------
 
 // Blocks of a kernel that fit on one CU at `lds` bytes of dynamic LDS.  The
-// answer is cached per kernel instantiation (the last LDS size asked), so a
-// launch of a few microseconds does not wait for the runtime query.
+// answer is cached per kernel (the last LDS size asked), so a launch of a few
+// microseconds does not wait for the runtime query.
 template <class Kern>
 int stream_occupancy(Kern kern, int threads, size_t lds) {
+    static thread_local Kern last_kern = nullptr;
     static thread_local size_t last_lds = ~(size_t)0;
     static thread_local int last_occ = 1;
-    if (lds != last_lds) {
+    if (kern != last_kern || lds != last_lds) {
         int occ = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, threads, lds) != hipSuccess || occ < 1) occ = 1;
+        last_kern = kern;
         last_lds = lds;
         last_occ = occ;
     }
     return last_occ;
 }
 
-// Persistent grid: as many blocks as fit on the device, shrunk so that every
-// wave gets the same number of row groups (no tail of half-filled rounds).
-// Returns the grid and, in gpw, the most groups one wave handles.
+// Persistent grid: as many blocks as fit on the device (at most occ_cap per
+// CU when occ_cap > 0), shrunk so that every wave gets the same number of row
+// groups (no tail of half-filled rounds).  Returns the grid and, in gpw, the
+// most groups one wave handles.
 template <class Kern>
-int stream_grid(Kern kern, int waves_per_block, size_t lds, int ngroups, int cus, int* gpw) {
-    const int occ = stream_occupancy(kern, waves_per_block * 64, lds);
+int stream_grid(Kern kern, int waves_per_block, size_t lds, int ngroups, int cus, int* gpw, int occ_cap = 0) {
+    int occ = stream_occupancy(kern, waves_per_block * 64, lds);
+    if (occ_cap > 0) occ = std::min(occ, occ_cap);
     const int waves_cap = occ * cus * waves_per_block;
     const int per_wave = (ngroups + waves_cap - 1) / waves_cap;
     const int waves = (ngroups + per_wave - 1) / per_wave;
@@ -419,13 +431,18 @@ int stream_grid(Kern kern, int waves_per_block, size_t lds, int ngroups, int cus
 constexpr int kGpwReserve = 16;
 constexpr size_t kStreamLdsMax = 64 * 1024;
 
+// occ_cap: at most this many blocks per CU (0: as many as fit).  Fewer waves
+// in flight streamed matrices of about 70 MB faster on MI355X (the N = 18944
+// x K = 3584 product at one block per CU: 16.9 -> 14.6 us).
 template <int R, int U, int WAVES, bool PF2 = false, class Src, class Epi>
-hipError_t stream_i8(const Src& src, const int8_t* W, int N, int K, const Epi& e, hipStream_t s, int cus) {
+hipError_t stream_i8(const Src& src, const int8_t* W, int N, int K, const Epi& e, hipStream_t s, int cus,
+                     int occ_cap = 0) {
     // one buffer descriptor; i32 partial sums exact for K < 131072
     if ((uint64_t)N * (uint64_t)K > 0xFFFFFF00ull || K >= 131072 || N < 1 || K < 1) return hipErrorInvalidValue;
     auto kern = gemv_i8_stream<R, U, WAVES, Src, Epi, PF2>;
     int gpw = 0;
-    const int grid = stream_grid(kern, WAVES, stream_lds_bytes(K, 1, WAVES, kGpwReserve, R), (N + R - 1) / R, cus, &gpw);
+    const int grid = stream_grid(kern, WAVES, stream_lds_bytes(K, 1, WAVES, kGpwReserve, R), (N + R - 1) / R, cus, &gpw,
+                                 occ_cap);
     const size_t lds = stream_lds_bytes(K, 1, WAVES, gpw, R);
     if (lds > kStreamLdsMax) return hipErrorInvalidValue;
     kern<<<grid, WAVES * 64, lds, s>>>(src, W, N, K, gpw, e);
@@ -466,6 +483,43 @@ struct StreamOne {
     }
 };
 
+// The same for epilogues whose per-row operands are tables (Epi::Ops,
+// ops(n), one_ops): the lane's first group's operands load right after the
+// first weight batch, so they are in registers when the stream ends.
+template <class Epi>
+struct StreamOneOps {
+    Epi e;
+    struct State {
+        typename Epi::Ops o[2];
+        int row0;
+    };
+    __device__ inline void begin(State& s) const { s.row0 = -1; }
+    __device__ inline void prefetch(State& s, int row0, int N) const {
+        if (row0 >= N) return;
+        s.o[0] = e.ops(row0);
+        s.o[1] = e.ops(min(row0 + 1, N - 1));
+        s.row0 = row0;
+    }
+    __device__ inline void finish(State&) const {}
+    template <int R>
+    __device__ inline void group(State& s, int row0, int N, const int64_t (&tot)[R]) const {
+        static_assert(R <= 2, "two prefetched rows per group");
+        const bool pre = s.row0 == row0;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (row0 + r < N) e.one_ops(row0 + r, 0, tot[r], pre ? s.o[r] : e.ops(row0 + r));
+    }
+};
+
+template <class Epi, class = void>
+struct StreamEpiOf {
+    using type = StreamOne<Epi>;
+};
+template <class Epi>
+struct StreamEpiOf<Epi, std::void_t<typename Epi::Ops>> {
+    using type = StreamOneOps<Epi>;
+};
+
 // Whether stream_i8<R, U, WAVES> takes N rows of K int8 weights: one buffer
 // descriptor, exact i32 partials, and the LDS of the widest grid stream_grid
 // can choose (at least one block per CU, so at most
@@ -496,11 +550,16 @@ template <class Epi>
 hipError_t stream_rows_i8(int shape, const int16_t* x, const int8_t* W, int N, int K, const Epi& epi, hipStream_t st,
                           int cus) {
     const SrcPlain src{x};
-    const StreamOne<Epi> e{epi};
+    const typename StreamEpiOf<Epi>::type e{epi};
+    // one block per CU for 32-100 MB of weights (measured faster for the
+    // 68 MB shapes), as many as fit otherwise (12.8 MB: 5.5 against 6.0 us;
+    // the 545 MB LM-head shape)
+    const uint64_t wb = (uint64_t)N * (uint64_t)K;
+    const int occ = wb >= (32ull << 20) && wb <= (100ull << 20) ? 1 : 0;
     switch (shape) {
-        case 1: return stream_i8<2, 4, 8>(src, W, N, K, e, st, cus);
-        case 2: return stream_i8<1, 4, 8>(src, W, N, K, e, st, cus);
-        case 3: return stream_i8<1, 2, 16>(src, W, N, K, e, st, cus);
+        case 1: return stream_i8<2, 4, 8>(src, W, N, K, e, st, cus, occ);
+        case 2: return stream_i8<1, 4, 8>(src, W, N, K, e, st, cus, occ);
+        case 3: return stream_i8<1, 2, 16>(src, W, N, K, e, st, cus, occ);
         default: return hipErrorInvalidValue;
     }
 }
