@@ -1033,7 +1033,10 @@ hipError_t layer_step(myl_model* m, int l) {
         SrcAttn src{m->attn_acc, f.v_frac, f.attn_out_frac};
         EpiResid o{L.so, f.attn_out_frac, L.acc_attn, L.res_in, L.res_mid, m->hidden, m->resid, m->norm_b, L.ref_mid,
                    m->norm_a};
-        e = stream_i8<1, 2, 16>(src, L.wo, H, nq, o, st, cus);
+        // 8-wave blocks streaming 4 KiB per row per batch, one block per CU:
+        // 10.8 -> 9.7 us per launch on MI355X at 7B widths (16-wave blocks,
+        // two-step batches, as many blocks as fit: the previous shape)
+        e = stream_i8<1, 4, 8>(src, L.wo, H, nq, o, st, cus, 1);
         if (e != hipSuccess) return e;
     }
     {
