@@ -292,11 +292,11 @@ constexpr int kFinNormThreads = 1024;
 template <int PER>
 __global__ __launch_bounds__(kFinNormThreads) void finish_resid_norm_kernel(unsigned long long* __restrict__ acc, int N,
                                                                 EpiResidRows epi, const uint8_t* __restrict__ xs,
-                                                                const int8_t* __restrict__ g,
+                                                                uint8_t ref, const int8_t* __restrict__ g,
                                                                 const uint8_t* __restrict__ gs, RmsParams p,
                                                                 uint8_t out_frac, int8_t* __restrict__ planes) {
-    __shared__ myl_i128 red128[kFinNormThreads / 64];
-    __shared__ int32_t red32[kFinNormThreads / 64];
+    __shared__ uint64_t red[kFinNormThreads / 64][3];
+    __shared__ RmsFactor sf;
     const int m = blockIdx.x;
     int16_t xv[PER];
     uint8_t sv[PER], gsv[PER];
@@ -317,7 +317,7 @@ __global__ __launch_bounds__(kFinNormThreads) void finish_resid_norm_kernel(unsi
             gsv[t] = gs[n];
         }
     }
-    const RmsFactor f = rms_factor_regs<PER>(xv, sv, p, red128, red32);
+    const RmsFactor f = rms_factor_limbs<PER>(xv, sv, ref, p, red, &sf);
     int8_t* ph = planes + (size_t)(2 * m) * N;
 #pragma unroll
     for (int t = 0; t < PER; ++t) {
@@ -332,16 +332,17 @@ __global__ __launch_bounds__(kFinNormThreads) void finish_resid_norm_kernel(unsi
 
 // A residual product (o_proj, down) of R rows followed by the RMSNorm of its
 // output rows into planes: fused into the finish of a split product,
-// otherwise the product then rmsnorm_planes.
+// otherwise the product then rmsnorm_planes.  ref is the largest entry of
+// the norm's input scales xs (rmsnorm.rs:96).
 hipError_t resid_then_norm(const int8_t* Ap, int R, const int8_t* W, int N, int K, const EpiResidRows& epi,
-                           const MmCtx* mm, const uint8_t* xs, const int8_t* g, const uint8_t* gs, const myl_model* m,
-                           uint8_t out_frac, int8_t* planes, hipStream_t st) {
+                           const MmCtx* mm, const uint8_t* xs, uint8_t ref, const int8_t* g, const uint8_t* gs,
+                           const myl_model* m, uint8_t out_frac, int8_t* planes, hipStream_t st) {
     const RmsParams p{m->rsqrt, m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20};
     auto fin = [&](unsigned long long* acc, hipStream_t s) -> hipError_t {
         if (N <= kFinNormThreads)
-            finish_resid_norm_kernel<1><<<R, kFinNormThreads, 0, s>>>(acc, N, epi, xs, g, gs, p, out_frac, planes);
+            finish_resid_norm_kernel<1><<<R, kFinNormThreads, 0, s>>>(acc, N, epi, xs, ref, g, gs, p, out_frac, planes);
         else
-            finish_resid_norm_kernel<4><<<R, kFinNormThreads, 0, s>>>(acc, N, epi, xs, g, gs, p, out_frac, planes);
+            finish_resid_norm_kernel<4><<<R, kFinNormThreads, 0, s>>>(acc, N, epi, xs, ref, g, gs, p, out_frac, planes);
         return hipGetLastError();
     };
     bool split = false;
@@ -553,8 +554,8 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         eo.shifts = Ld.so; eo.act_frac = f.attn_out_frac; eo.acc_frac = Ld.acc_attn; eo.res_frac = Ld.res_in;
         eo.out_frac = Ld.res_mid; eo.res = b->X; eo.ldr = H; eo.out = b->X2; eo.ldo = H;
         if (norm_in_finish)
-            e = resid_then_norm(mm->planes, R, Ld.wo, H, nq, eo, mm, Ld.res_mid, Ld.post_gamma, Ld.post_gamma_s, m,
-                                f.norm_mlp_frac, fuse_silu ? xin : mm->planes, st);
+            e = resid_then_norm(mm->planes, R, Ld.wo, H, nq, eo, mm, Ld.res_mid, Ld.ref_mid, Ld.post_gamma,
+                                Ld.post_gamma_s, m, f.norm_mlp_frac, fuse_silu ? xin : mm->planes, st);
         else
             e = planes ? mm_planes(mm->planes, R, Ld.wo, H, nq, eo, mm, st) : gemv_i8(b->A, R, nq, Ld.wo, H, nq, eo, st, mm);
         if (e != hipSuccess) return e;
@@ -588,7 +589,7 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         in_normed = norm_in_finish && l + 1 < (int)m->spec.layers;
         if (in_normed) {
             const LayerDev& Ln = m->layers[l + 1];
-            e = resid_then_norm(mm->planes, R, Ld.wd, H, I, ed, mm, Ln.res_in, Ln.in_gamma, Ln.in_gamma_s, m,
+            e = resid_then_norm(mm->planes, R, Ld.wd, H, I, ed, mm, Ln.res_in, Ln.ref_in, Ln.in_gamma, Ln.in_gamma_s, m,
                                 Ln.f.norm_attn_frac, mm->planes, st);
         } else {
             e = planes ? mm_planes(mm->planes, R, Ld.wd, H, I, ed, mm, st) : gemv_i8(b->Hh, R, I, Ld.wd, H, I, ed, st, mm);

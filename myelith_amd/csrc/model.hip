@@ -83,13 +83,6 @@ __global__ void gen_w16_kernel(int16_t* __restrict__ dst, int row0, int K, uint6
 // ---------------------------------------------------------------------------
 
 
-__device__ inline void add_sq_limbs(int16_t x, uint8_t xs, uint8_t ref, uint64_t (&l)[3]) {
-    const uint32_t align = 2u * (uint32_t)(uint8_t)(ref - xs);
-    const myl_u128 t = (myl_u128)shl128((myl_i128)((int64_t)x * (int64_t)x), align);
-    l[0] += (uint64_t)t & kLimbMask;
-    l[1] += (uint64_t)(t >> 42) & kLimbMask;
-    l[2] += (uint64_t)(t >> 84);
-}
 
 // Block-level sum of per-thread limbs; thread 0 gets the totals.
 __device__ inline void block_sum_limbs(uint64_t (&l)[3], uint64_t* red /* [16][3] */) {
