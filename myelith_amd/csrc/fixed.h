@@ -74,11 +74,16 @@ MYL_FN int64_t rescale64(int64_t acc, uint8_t in_frac, uint8_t out_frac) {
     return sh >= 0 ? rshift_round64(acc, (uint8_t)sh) : shl64(acc, (uint8_t)(-(int32_t)sh));
 }
 
-// floor(2^32 / d) for d >= 1, by restoring long division (33 steps, integer only).
+// floor(2^32 / d) for d >= 1 (2^33 - 1 for d = 0), by restoring long
+// division (integer only).  The dividend 2^32 has its only set bit at
+// position 32, so the quotient bits above position 32 - ceil(log2 d) are zero
+// and the remainder entering that position is 2^(ceil(log2 d) - 1): the loop
+// starts there (33 - ceil(log2 d) steps instead of 33).
 MYL_FN uint64_t recip32(uint32_t d) {
-    uint64_t q = 0, r = 0;
-    // dividend 2^32 has its only set bit at position 32
-    for (int bit = 32; bit >= 0; --bit) {
+    if (d == 0) return 0x1FFFFFFFFull;
+    const int c = d > 1 ? 32 - __builtin_clz(d - 1u) : 0;  // ceil(log2 d)
+    uint64_t q = 0, r = c > 0 ? (1ull << (c - 1)) : 0;
+    for (int bit = 32 - c; bit >= 0; --bit) {
         r = (r << 1) | (bit == 32 ? 1u : 0u);
         q <<= 1;
         if (r >= d) { r -= d; q |= 1; }
@@ -132,6 +137,24 @@ MYL_FN int32_t softmax_div_round_pos(int32_t num, int32_t s, uint32_t m) {
         r -= us;
     }
     const int32_t twice = wmul32((int32_t)r, 2);
+    if (twice > s || (twice == s && (q & 1u))) return wadd32((int32_t)q, 1);
+    return (int32_t)q;
+}
+
+// softmax.rs:50-63 for num = e * 2^14 with 0 <= e <= s and s > 0: the
+// quotient is at most 2^14, so fifteen restoring-division steps give it and
+// the remainder exactly (no reciprocal); then the same half-even step with
+// the wrapping i32 doubling of the remainder.
+MYL_FN int32_t softmax_div_round_q15(int32_t e, int32_t s) {
+    uint32_t rem = (uint32_t)e << 14, q = 0;
+    const uint32_t us = (uint32_t)s;
+    for (int b = 14; b >= 0; --b) {
+        if ((rem >> b) >= us) {
+            rem -= us << b;
+            q |= 1u << b;
+        }
+    }
+    const int32_t twice = wmul32((int32_t)rem, 2);
     if (twice > s || (twice == s && (q & 1u))) return wadd32((int32_t)q, 1);
     return (int32_t)q;
 }

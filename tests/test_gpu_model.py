@@ -226,6 +226,54 @@ def test_decode_with_a_long_exp_table_tail(backend):
         assert np.array_equal(gm.forward_token(int(t), pos), om.forward_token(int(t), pos)), pos
 
 
+@pytest.mark.parametrize("hd,variant", [(64, "negative"), (128, "negative"), (128, "zero")])
+def test_decode_attention_exp_table_variants(backend, hd, variant):
+    """Exp tables outside the decode attention's int16-probability path:
+    negative entries (probabilities need not lie in [0, 2^14]: P.V runs in
+    i64) and an all-zero table (every head sum is 0: softmax.rs:37-44 splits
+    one / L uniformly)."""
+    from myelith_amd.luts import LutSet
+    from myelith_amd.model import IntegerModel
+    from oracle.binding import OracleModel
+    spec = tiny(hd, 0, 1, 2)
+    case(f"exp table {variant} {spec}")
+    base = LutSet.for_head_dim(hd)
+    exp = np.asarray(base.exp, dtype=np.int16).copy()
+    if variant == "negative":
+        exp[1:600:3] = -exp[1:600:3]
+    else:
+        exp[:] = 0
+    luts = LutSet.from_tables(hd, base.rsqrt, base.silu, exp, base.cos, base.sin)
+    gm, om = IntegerModel(backend, spec, luts), OracleModel(spec, luts, threads=16)
+    r = np.random.default_rng(hd + len(variant))
+    for pos, t in enumerate(r.integers(0, spec["vocab"], 200)):
+        assert np.array_equal(gm.forward_token(int(t), pos), om.forward_token(int(t), pos)), pos
+    compare_kv(gm, om, spec, 200)
+
+
+def test_decode_attention_blocks_of_several_chunks(backend):
+    """Four KV heads x 4300 positions are more 64-position chunks than CUs, so
+    each decode attention block takes a run of chunks (the blocks of a KV head
+    wait for each other and must all be resident).  A 4130-token prompt, then
+    decode steps past 4096 positions."""
+    spec = tiny(128, 0, 1, 4, layers=1, max_pos=4300)
+    case(f"decode blocks of several chunks {spec}")
+    gm, om = build(backend, spec)
+    r = np.random.default_rng(23)
+    p = [int(t) for t in r.integers(0, spec["vocab"], 4130)]
+    gm.prefill(p, 0)
+    # the prompt's rows are checked elsewhere; the oracle continues from the
+    # device's cache
+    for l in range(spec["layers"]):
+        for h in range(spec["kv_heads"]):
+            om.write_kv(l, h, *gm.read_kv(l, h, 4130))
+    om.set_cached(4130)
+    for i, t in enumerate(r.integers(0, spec["vocab"], 6)):
+        pos = 4130 + i
+        assert np.array_equal(gm.forward_token(int(t), pos), om.forward_token(int(t), pos)), pos
+    compare_kv(gm, om, spec, 4136)
+
+
 def test_long_prompt_rows_match_the_oracle(backend):
     """A 4200-token prompt runs as three chunks of rows (2048, 2048, 104):
     the softmax kernel's register path (a wave per (row, head), rows up to
