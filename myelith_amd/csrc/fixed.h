@@ -141,24 +141,6 @@ MYL_FN int32_t softmax_div_round_pos(int32_t num, int32_t s, uint32_t m) {
     return (int32_t)q;
 }
 
-// softmax.rs:50-63 for num = e * 2^14 with 0 <= e <= s and s > 0: the
-// quotient is at most 2^14, so fifteen restoring-division steps give it and
-// the remainder exactly (no reciprocal); then the same half-even step with
-// the wrapping i32 doubling of the remainder.
-MYL_FN int32_t softmax_div_round_q15(int32_t e, int32_t s) {
-    uint32_t rem = (uint32_t)e << 14, q = 0;
-    const uint32_t us = (uint32_t)s;
-    for (int b = 14; b >= 0; --b) {
-        if ((rem >> b) >= us) {
-            rem -= us << b;
-            q |= 1u << b;
-        }
-    }
-    const int32_t twice = wmul32((int32_t)rem, 2);
-    if (twice > s || (twice == s && (q & 1u))) return wadd32((int32_t)q, 1);
-    return (int32_t)q;
-}
-
 // Unsigned 32-bit n % d without a hardware divide (small loops only: LUT row
 // selection pos % n_pos, done once per launch).
 MYL_FN uint32_t umod32_slow(uint32_t n, uint32_t d) {

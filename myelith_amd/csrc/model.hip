@@ -10,11 +10,11 @@
 //   per layer:
 //     rmsnorm      input_layernorm                                 (:416-426)
 //     gemv qkv     q/k/v rows + bias + RoPE, K/V appended to cache (:438-503)
-//     attention    s_j = (i32)RNE(q.k_j * mult, shift)             (attention.rs:66-67)
-//                  max, sum of exp-LUT over the KV head's blocks   (softmax.rs:32-48)
+//     attn_scores  s_j = (i32)RNE(q.k_j * mult, shift)             (attention.rs:66-67)
+//     attn_pv      max, sum of exp-LUT, reciprocal of the sum      (softmax.rs:32-48)
 //                  p_j = RNE(e_j * 2^14 / S), partial sum p_j v_j  (softmax.rs:50-63, attention.rs:75-81)
-//     gemv o       RNE(., 14), clamp, rescale v -> attn_out staged (attention.rs:84-86, model.rs:563-567)
-//                  o_proj + residual add 1                         (:576-593)
+//     attn_reduce  RNE(., 14), clamp, rescale v -> attn_out        (attention.rs:84-86, model.rs:563-567)
+//     gemv o       o_proj + residual add 1                         (:576-593)
 //     rmsnorm      post_attention_layernorm                        (:596-606)
 //     gemv gate/up gate, up interleaved, SiLU-LUT product           (mlp.rs:55-65)
 //     gemv down    down_proj + residual add 2                      (:612-671)
@@ -31,9 +31,9 @@
 #include "gemv.h"
 #include "gemv_stream.h"
 #include "ops.h"
+#include "dec_attn.h"
 #include "../../include/myl_synth.h"
 #include "model_internal.h"
-#include "dec_attn.h"
 
 #include <cstring>
 #include <new>
@@ -557,16 +557,46 @@ struct EpiHead {
 // ---------------------------------------------------------------------------
 
 // Launch shape shared by the two attention kernels: grid
-template <int HD, bool PV16>
-__global__ __launch_bounds__(256) void attn_decode_kernel(DecodeState* __restrict__ st, const int16_t* __restrict__ q,
-                                                         const int16_t* __restrict__ kc,
-                                                         const int16_t* __restrict__ vc, int max_pos, int G, int sub,
-                                                         int64_t score_mult, uint8_t score_shift,
-                                                         const int16_t* __restrict__ lut, uint32_t lut_len,
-                                                         uint8_t lut_shift, int exp_lds, uint32_t* __restrict__ sync,
-                                                         unsigned long long* __restrict__ acc) {
-    dec_attention<HD, PV16>(st, q, kc, vc, max_pos, G, sub, score_mult, score_shift, lut, lut_len, lut_shift, exp_lds,
-                            sync, acc);
+// dim3(8 * G, ceil(chunks / 8), kv_heads), 256 threads; block (x, y, z) works
+// on query head x >> 3 of KV head z and on position chunk y * 8 + (x & 7).
+// Workgroups are dispatched to the 8 XCDs round robin in linear-id order (x
+// fastest, and gridDim.x is a multiple of 8), so the G head blocks of one
+// chunk run on one XCD and share its L2 copy of the K or V rows.
+struct AttnBlock {
+    int h, c, g;
+    __device__ AttnBlock() : h((int)blockIdx.x >> 3), c((int)blockIdx.y * 8 + ((int)blockIdx.x & 7)), g((int)blockIdx.z) {}
+};
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_scores_kernel(const DecodeState* __restrict__ st,
+                                                         const int16_t* __restrict__ q, const int16_t* __restrict__ kc,
+                                                         int max_pos, int G, int chunks, int64_t score_mult,
+                                                         uint8_t score_shift, int32_t* __restrict__ scores) {
+    const AttnBlock b;
+    if (b.c >= chunks) return;
+    const int L = st->pos + 1;
+    const int base = b.c * kChunk;
+    if (base >= L) return;
+    const int head = b.g * G + b.h;
+    dec_scores<HD>(L, base, q + (size_t)head * HD, kc + (size_t)b.g * max_pos * HD, score_mult, score_shift,
+                   scores + (size_t)head * max_pos);
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_pv_kernel(const DecodeState* __restrict__ st,
+                                                     const int32_t* __restrict__ scores,
+                                                     const int16_t* __restrict__ vc, int max_pos, int G, int chunks,
+                                                     const int16_t* __restrict__ lut, uint32_t lut_len,
+                                                     uint8_t lut_shift, int exp_lds,
+                                                     unsigned long long* __restrict__ acc) {
+    const AttnBlock b;
+    if (b.c >= chunks) return;
+    const int L = st->pos + 1;
+    const int base = b.c * kChunk;
+    if (base >= L) return;
+    const int head = b.g * G + b.h;
+    dec_pv<HD>(L, base, scores + (size_t)head * max_pos, vc + (size_t)b.g * max_pos * HD, lut, lut_len, lut_shift,
+               exp_lds, acc + (size_t)head * HD);
 }
 
 // ---------------------------------------------------------------------------
@@ -682,21 +712,14 @@ int alloc_impl(myl_model* m, const myl_luts* luts) {
     m->rope_rows = (uint32_t)(luts->rope_len / (size_t)(hd / 2));
     m->rsqrt = m->dalloc<int16_t>(luts->rsqrt_len);
     m->silu = m->dalloc<int16_t>(luts->silu_len);
-    // the exp table is zero-padded to at least kDecExpLds entries: the decode
-    // attention copies that many into LDS without a bounds check
-    const size_t exp_alloc = std::max<size_t>(luts->exp_len, (size_t)kDecExpLds);
-    m->exp_lut = m->dalloc<int16_t>(exp_alloc);
+    m->exp_lut = m->dalloc<int16_t>(luts->exp_len);
     m->cos_lut = m->dalloc<int16_t>(luts->rope_len);
     m->sin_lut = m->dalloc<int16_t>(luts->rope_len);
     if (!m->rsqrt || !m->silu || !m->exp_lut || !m->cos_lut || !m->sin_lut) return c->fail(MYL_E_NOMEM, "LUT allocation");
     int rc = 0;
     rc |= upload(m, m->rsqrt, std::vector<int16_t>(luts->rsqrt, luts->rsqrt + luts->rsqrt_len));
     rc |= upload(m, m->silu, std::vector<int16_t>(luts->silu, luts->silu + luts->silu_len));
-    {
-        std::vector<int16_t> e(exp_alloc, 0);
-        std::copy(luts->exp, luts->exp + luts->exp_len, e.begin());
-        rc |= upload(m, m->exp_lut, e);
-    }
+    rc |= upload(m, m->exp_lut, std::vector<int16_t>(luts->exp, luts->exp + luts->exp_len));
     rc |= upload(m, m->cos_lut, std::vector<int16_t>(luts->cos, luts->cos + luts->rope_len));
     rc |= upload(m, m->sin_lut, std::vector<int16_t>(luts->sin, luts->sin + luts->rope_len));
     if (rc) return MYL_E_HIP;
@@ -793,33 +816,18 @@ int alloc_impl(myl_model* m, const myl_luts* luts) {
     m->resid = m->dalloc<int16_t>(H);
     m->h = m->dalloc<int16_t>(I);
     m->logits = m->dalloc<int32_t>(V);
-    // the P.V accumulators, then the decode attention's sync words: one
-    // allocation that the gate/up kernel clears after each layer
-    const int sync_words = AttnSyncWords::count((int)s.kv_heads, (int)s.heads);
-    m->attn_clear_n = nq + (sync_words + 1) / 2;
-    m->attn_acc = m->dalloc<unsigned long long>((size_t)m->attn_clear_n);
-    m->attn_sync = reinterpret_cast<uint32_t*>(m->attn_acc + nq);
-    {
-        // P.V on int16 probabilities needs every exp value in [0, S] with the
-        // head sum S exact in i32
-        int64_t emax = 0;
-        bool nonneg = luts->exp_len > 0;
-        for (size_t i = 0; i < luts->exp_len; ++i) {
-            nonneg = nonneg && luts->exp[i] >= 0;
-            emax = std::max<int64_t>(emax, luts->exp[i]);
-        }
-        m->attn_pv16 = nonneg && (int64_t)m->max_pos * emax < (1LL << 31);
-    }
+    m->scores = m->dalloc<int32_t>((size_t)s.heads * m->max_pos);
+    m->attn_acc = m->dalloc<unsigned long long>((size_t)nq);
     m->norm_a = m->dalloc<NormAcc>(1);
     m->norm_b = m->dalloc<NormAcc>(1);
     m->state = m->dalloc<DecodeState>(1);
     if (!m->kcache || !m->vcache || !m->hidden || !m->norm || !m->q || !m->attn || !m->resid || !m->h ||
-        !m->logits || !m->attn_acc || !m->state || !m->norm_a || !m->norm_b)
+        !m->logits || !m->scores || !m->attn_acc || !m->state || !m->norm_a || !m->norm_b)
         return c->fail(MYL_E_NOMEM, "activation allocation");
     if (hipMemsetAsync(m->kcache, 0, kv * 2, c->stream) != hipSuccess ||
         hipMemsetAsync(m->vcache, 0, kv * 2, c->stream) != hipSuccess ||
         hipMemsetAsync(m->state, 0, sizeof(DecodeState), c->stream) != hipSuccess ||
-        hipMemsetAsync(m->attn_acc, 0, (size_t)m->attn_clear_n * 8, c->stream) != hipSuccess ||
+        hipMemsetAsync(m->attn_acc, 0, (size_t)nq * 8, c->stream) != hipSuccess ||
         hipMemsetAsync(m->norm_a, 0, sizeof(NormAcc), c->stream) != hipSuccess ||
         hipMemsetAsync(m->norm_b, 0, sizeof(NormAcc), c->stream) != hipSuccess)
         return MYL_E_HIP;
@@ -968,9 +976,9 @@ RmsParams rms_params(const myl_model* m) {
 // One transformer layer on m->hidden (model.rs:401-674); the result replaces
 // m->hidden and its input-norm sum is left in norm_a for the next consumer.
 //   qkv   : RMSNorm(hidden) staged from norm_a            -> q, KV cache
-//   attn  : scores, softmax, P.V into attn_acc (one kernel, blocks of a KV head exchange max and sum)
+//   attn  : scores, then softmax + P.V into attn_acc
 //   o     : attn_acc staged, residual 1 -> resid; sum -> norm_b; clears norm_a
-//   gu    : RMSNorm(resid) staged from norm_b             -> h; clears attn_acc and the sync words
+//   gu    : RMSNorm(resid) staged from norm_b             -> h; clears attn_acc
 //   down  : h, residual 2 -> hidden; sum -> norm_a; clears norm_b
 hipError_t layer_step(myl_model* m, int l) {
     const LayerDev& L = m->layers[l];
@@ -994,20 +1002,22 @@ hipError_t layer_step(myl_model* m, int l) {
         const uint32_t ss = (uint32_t)f.q_frac + f.k_frac + 15u;
         const uint8_t score_shift = (uint8_t)(ss > MYL_TV_SCORE_FRAC_BITS ? ss - MYL_TV_SCORE_FRAC_BITS : 0);
         const uint8_t lut_shift = MYL_TV_SCORE_FRAC_BITS - MYL_TV_EXP_INPUT_FRAC;
+        const int chunks = (m->max_pos + kChunk - 1) / kChunk;
         const int16_t* kc = m->kcache + layer_kv;
         const int16_t* vc = m->vcache + layer_kv;
-        const dim3 agrid(m->attn_grid_x, kvh);
-        const size_t dyn = attn_dyn_lds(G, m->attn_sub, hd);
+        const dim3 agrid(8 * G, (chunks + 7) / 8, kvh);
         const int exp_lds = m->exp_nz <= kDecExpLds ? m->exp_nz : -1;
-        auto launch = [&](auto kern) {
-            kern<<<agrid, 256, dyn, st>>>(m->state, m->q, kc, vc, m->max_pos, G, m->attn_sub, m->score_mult,
-                                          score_shift, m->exp_lut, (uint32_t)m->exp_len, lut_shift, exp_lds,
-                                          m->attn_sync, m->attn_acc);
-        };
-        if (hd == 128)
-            m->attn_pv16 ? launch(attn_decode_kernel<128, true>) : launch(attn_decode_kernel<128, false>);
-        else
-            m->attn_pv16 ? launch(attn_decode_kernel<64, true>) : launch(attn_decode_kernel<64, false>);
+        if (hd == 128) {
+            attn_scores_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, chunks, m->score_mult,
+                                                          score_shift, m->scores);
+            attn_pv_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, G, chunks, m->exp_lut,
+                                                      (uint32_t)m->exp_len, lut_shift, exp_lds, m->attn_acc);
+        } else {
+            attn_scores_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, chunks, m->score_mult,
+                                                         score_shift, m->scores);
+            attn_pv_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, G, chunks, m->exp_lut,
+                                                     (uint32_t)m->exp_len, lut_shift, exp_lds, m->attn_acc);
+        }
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -1025,7 +1035,7 @@ hipError_t layer_step(myl_model* m, int l) {
     {
         SrcNorm src{m->resid, L.res_mid, L.post_gamma, L.post_gamma_s, rp, L.ref_mid, f.norm_mlp_frac, m->norm_b};
         EpiSilu s{L.sgu, f.norm_mlp_frac, f.gate_frac, f.up_frac, f.down_in_frac, m->silu, (uint32_t)m->silu_len, m->h,
-                  m->attn_acc, m->attn_clear_n};
+                  m->attn_acc, nq};
         {
             TimedScope t(m, K_GU);
             // staging loads go out before the weights, so one register buffer in
@@ -1116,27 +1126,6 @@ hipError_t capture_step(myl_model* m) {
     return e;
 }
 
-// A timed-out wait of the decode attention (its blocks were not all
-// resident) leaves a mark in the step state; the call then fails, since the
-// step's outputs are invalid.
-int check_stalls(myl_model* m, const DecodeState& s) {
-    if (!s.stalls) return MYL_OK;
-    (void)hipMemsetAsync(&m->state->stalls, 0, sizeof(uint32_t), m->ctx->stream);
-    (void)hipStreamSynchronize(m->ctx->stream);
-    return m->ctx->fail(MYL_E_HIP, "decode attention: a cross-block wait timed out; the step's results are invalid");
-}
-
-// Waits for the stream, then checks the step state for stalls.
-int sync_checked(myl_model* m, const char* what) {
-    DecodeState s;
-    myl_ctx* c = m->ctx;
-    int rc = c->hip(hipMemcpyAsync(&s, m->state, sizeof(s), hipMemcpyDeviceToHost, c->stream), what);
-    if (rc) return rc;
-    rc = c->hip(hipStreamSynchronize(c->stream), what);
-    if (rc) return rc;
-    return check_stalls(m, s);
-}
-
 }  // namespace
 
 namespace myl {
@@ -1171,21 +1160,6 @@ int model_setup(myl_ctx* ctx, const myl_synth_spec& s, bool tied, const myl_luts
     m->nkv = (int)(s.kv_heads * s.head_dim);
     m->max_pos = (int)s.max_pos;
     m->cus = ctx->prop.multiProcessorCount > 0 ? ctx->prop.multiProcessorCount : 1;
-    {
-        // decode attention: every block of a KV head must be resident at once,
-        // so at most one block per CU (sub chunks of 64 positions per block, a
-        // power of two)
-        const int nch = (m->max_pos + kChunk - 1) / kChunk;
-        int sub = 1;
-        while (sub < kAttnMaxSub && (int64_t)s.kv_heads * ((nch + sub - 1) / sub) > m->cus) sub *= 2;
-        const size_t lds = attn_dyn_lds(m->G, sub, m->hd) + 2 * kDecExpLds + (size_t)kChunk * m->hd * 2 + 16;
-        if ((int64_t)s.kv_heads * ((nch + sub - 1) / sub) > m->cus || lds > 65536 || m->G > kAttnMaxG) {
-            delete m;
-            return ctx->fail(MYL_E_UNSUPPORTED, "model: KV heads x positions beyond the decode attention's one block per CU");
-        }
-        m->attn_sub = sub;
-        m->attn_grid_x = (nch + sub - 1) / sub;
-    }
     int rc = alloc_impl(m, luts);
     if (rc) {
         delete m;
@@ -1296,12 +1270,10 @@ int myl_model_forward_token(myl_model* m, uint32_t token, uint32_t pos, int32_t*
         if (rc) return rc;
         rc = c->hip(hipStreamSynchronize(c->stream), "forward_token");
         if (rc) return rc;
-        rc = check_stalls(m, s);
-        if (rc) return rc;
         *argmax_out = key_index(s.argmax_key);
         return MYL_OK;
     }
-    return sync_checked(m, "forward_token");
+    return c->hip(hipStreamSynchronize(c->stream), "forward_token");
 }
 
 int myl_model_decode_greedy(myl_model* m, uint32_t token, uint32_t pos, uint32_t n_steps, int64_t* tokens_out,
@@ -1347,8 +1319,6 @@ int myl_model_decode_greedy(myl_model* m, uint32_t token, uint32_t pos, uint32_t
     if (rc) return rc;
     rc = c->hip(hipStreamSynchronize(c->stream), "decode");
     if (rc) return rc;
-    rc = check_stalls(m, s);
-    if (rc) return rc;
     toks[n_steps - 1] = key_index(s.argmax_key);
     if (tokens_out) std::memcpy(tokens_out, toks.data(), (size_t)n_steps * 8);
     return MYL_OK;
@@ -1386,7 +1356,7 @@ int myl_model_prefill(myl_model* m, const uint32_t* tokens, uint32_t n, uint32_t
         rc = c->hip(hipMemcpyAsync(last_logits, m->logits, (size_t)m->V * 4, hipMemcpyDeviceToHost, c->stream), "logits");
         if (rc) return rc;
     }
-    return sync_checked(m, "prefill");
+    return c->hip(hipStreamSynchronize(c->stream), "prefill");
 }
 
 int myl_model_embed_token(myl_model* m, uint32_t token, int16_t* hidden) {
@@ -1420,7 +1390,7 @@ int myl_model_run_layers(myl_model* m, int16_t* hidden, uint32_t pos, uint32_t l
     if (rc) return rc;
     rc = c->hip(hipMemcpyAsync(hidden, m->hidden, (size_t)m->H * 2, hipMemcpyDeviceToHost, c->stream), "hidden");
     if (rc) return rc;
-    return sync_checked(m, "run_layers");
+    return c->hip(hipStreamSynchronize(c->stream), "run_layers");
 }
 
 int myl_model_head_logits(myl_model* m, const int16_t* hidden, int32_t* logits) {

@@ -18,7 +18,6 @@ struct DecodeState {
     int32_t pos;
     int32_t rope_row;     // pos % rope rows
     int32_t step;         // decode steps taken since the last set
-    uint32_t stalls;      // nonzero: a decode attention wait timed out (the step's results are invalid)
 };
 
 // Exact sum of squares of a residual-stream vector for the next RMSNorm,
@@ -111,12 +110,8 @@ struct myl_model {
     int16_t *kcache = nullptr, *vcache = nullptr;
     int16_t *hidden = nullptr, *norm = nullptr, *q = nullptr, *attn = nullptr, *resid = nullptr, *h = nullptr;
     int32_t* logits = nullptr;
-    unsigned long long* attn_acc = nullptr;  // [nq] exact P.V sums, then the attention sync words; cleared after each use
-    uint32_t* attn_sync = nullptr;           // decode attention arrival counters (inside the attn_acc allocation)
-    bool attn_pv16 = false;                  // decode attention P.V on int16 probabilities (exp table >= 0)
-    int attn_clear_n = 0;                    // u64 words the gate/up kernel clears from attn_acc on
-    int attn_sub = 1;                        // 64-position chunks per decode attention block
-    int attn_grid_x = 1;                     // decode attention blocks per KV head at max_pos
+    int32_t* scores = nullptr;
+    unsigned long long* attn_acc = nullptr;  // [nq] exact P.V sums, cleared after each use
     NormAcc* norm_a = nullptr;               // input-norm / final-norm sums of squares
     NormAcc* norm_b = nullptr;               // post-attention-norm sums of squares
     uint8_t ref_final = 0;

@@ -228,10 +228,9 @@ def test_decode_with_a_long_exp_table_tail(backend):
 
 @pytest.mark.parametrize("hd,variant", [(64, "negative"), (128, "negative"), (128, "zero")])
 def test_decode_attention_exp_table_variants(backend, hd, variant):
-    """Exp tables outside the decode attention's int16-probability path:
-    negative entries (probabilities need not lie in [0, 2^14]: P.V runs in
-    i64) and an all-zero table (every head sum is 0: softmax.rs:37-44 splits
-    one / L uniformly)."""
+    """Exp tables unlike the calibrated one: negative entries (probabilities
+    outside [0, 2^14], negative and wrapping sums) and an all-zero table
+    (every head sum is 0: softmax.rs:37-44 splits one / L uniformly)."""
     from myelith_amd.luts import LutSet
     from myelith_amd.model import IntegerModel
     from oracle.binding import OracleModel
@@ -251,13 +250,12 @@ def test_decode_attention_exp_table_variants(backend, hd, variant):
     compare_kv(gm, om, spec, 200)
 
 
-def test_decode_attention_blocks_of_several_chunks(backend):
-    """Four KV heads x 4300 positions are more 64-position chunks than CUs, so
-    each decode attention block takes a run of chunks (the blocks of a KV head
-    wait for each other and must all be resident).  A 4130-token prompt, then
-    decode steps past 4096 positions."""
+def test_decode_past_4096_positions(backend):
+    """Decode attention over more than 4096 cached positions with four KV
+    heads (the P.V kernel's scores no longer fit its registers and are read
+    in place): a 4130-token prompt, then decode steps past 4096."""
     spec = tiny(128, 0, 1, 4, layers=1, max_pos=4300)
-    case(f"decode blocks of several chunks {spec}")
+    case(f"decode past 4096 positions {spec}")
     gm, om = build(backend, spec)
     r = np.random.default_rng(23)
     p = [int(t) for t in r.integers(0, spec["vocab"], 4130)]
