@@ -337,7 +337,8 @@ __global__ __launch_bounds__(kFinNormThreads) void finish_resid_norm_kernel(unsi
 hipError_t resid_then_norm(const int8_t* Ap, int R, const int8_t* W, int N, int K, const EpiResidRows& epi,
                            const MmCtx* mm, const uint8_t* xs, uint8_t ref, const int8_t* g, const uint8_t* gs,
                            const myl_model* m, uint8_t out_frac, int8_t* planes, hipStream_t st) {
-    const RmsParams p{m->rsqrt, m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20};
+    const RmsParams p{m->rsqrt, m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20,
+                      m->rsqrt_closed};
     auto fin = [&](unsigned long long* acc, hipStream_t s) -> hipError_t {
         if (N <= kFinNormThreads)
             finish_resid_norm_kernel<1><<<R, kFinNormThreads, 0, s>>>(acc, N, epi, xs, ref, g, gs, p, out_frac, planes);

@@ -19,8 +19,11 @@
 // to one recorded group, so all epilogue loads and stores of a wave overlap.
 //
 // Staging interface (Src):
-//   Pre; pre(K, kpad)                            per thread, first thing in the kernel
-//   stage_i8(pre, hi, lo, K, kpad)               whole block, after the first weight loads
+//   Pre; pre(K, kpad, nthr)                      per thread, first thing in the kernel
+//   stage_i8(pre, hi, lo, K, kpad, nthr)         whole block, after the first weight loads
+// nthr is the block size as a compile-time constant of the kernel: blockDim
+// is read from the dispatch packet, a load that would delay the first loads
+// and (issued behind the weights) make the staging wait for them.
 // pre() issues the source's own loads (activations, scales, norm sums) ahead of
 // every weight load: loads complete in issue order, so staging then waits for
 // its operands without waiting for a weight batch.
@@ -61,11 +64,31 @@ __device__ inline uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
 }
 
+// Loads of the staging operands, issued ahead of the first weight batch,
+// through a buffer descriptor over the operand: past num_records a load
+// returns zero, so no branch guards it.
+constexpr int kPreCpol = 0;
+__device__ inline uint4 cload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kPreCpol);
+    return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+}
+__device__ inline uint2 cload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kPreCpol);
+    return make_uint2((uint32_t)v[0], (uint32_t)v[1]);
+}
+
 // ---- staging sources ----------------------------------------------------------
 
 // 8-element chunks of the staged vector a thread loads in pre(): chunks
-// threadIdx.x + j * blockDim.x, j < kPreChunks; the rest load during staging.
-constexpr int kPreChunks = 3;
+// threadIdx.x + j * nthr, j < kPreChunks; the rest load during staging.
+constexpr int kPreChunks = 5;
+
+// Each staged plane is followed by kStageSlack spare elements: chunk index
+// n8 = kpad / 8 is a dump slot, so the chunks loaded ahead of the weights are
+// staged without a branch (a thread past the end writes its zeros there).
+// A branch would let the compiler sink those loads behind the weight batch.
+constexpr int kStageSlack = 16;
+__device__ inline int stage_slot(int i, int n8) { return i < n8 ? i : n8; }
 
 // Eight int16 values -> their signed byte planes (hi = x >> 8, lo' = (x & 255) - 128).
 __device__ inline void put_x8_planes(const uint4 v, int8_t* hi, int8_t* lo) {
@@ -87,23 +110,21 @@ struct SrcPlain {
     struct Pre {
         uint4 x[kPreChunks];
     };
-    __device__ inline Pre pre(int K, int kpad) const {
+    __device__ inline Pre pre(int K, int kpad, int nthr) const {
         Pre p;
+        const __amdgpu_buffer_rsrc_t r = weight_rsrc(x, 2u * (uint32_t)K);
 #pragma unroll
-        for (int j = 0; j < kPreChunks; ++j) {
-            const int k = (threadIdx.x + j * blockDim.x) * 8;
-            p.x[j] = k < K ? *reinterpret_cast<const uint4*>(x + k) : make_uint4(0, 0, 0, 0);
-        }
+        for (int j = 0; j < kPreChunks; ++j) p.x[j] = cload16(r, (threadIdx.x + j * nthr) * 16u);
         return p;
     }
-    __device__ inline void stage_i8(const Pre& p, int8_t* hi, int8_t* lo, int K, int kpad) const {
+    __device__ inline void stage_i8(const Pre& p, int8_t* hi, int8_t* lo, int K, int kpad, int nthr) const {
         const int n8 = kpad >> 3;
 #pragma unroll
         for (int j = 0; j < kPreChunks; ++j) {
-            const int i = threadIdx.x + j * blockDim.x;
-            if (i < n8) put_x8_planes(p.x[j], hi + i * 8, lo + i * 8);
+            const int i = stage_slot(threadIdx.x + j * nthr, n8);
+            put_x8_planes(p.x[j], hi + i * 8, lo + i * 8);
         }
-        for (int i = threadIdx.x + kPreChunks * blockDim.x; i < n8; i += blockDim.x) {
+        for (int i = threadIdx.x + kPreChunks * nthr; i < n8; i += nthr) {
             const uint4 v = i * 8 < K ? *reinterpret_cast<const uint4*>(x + i * 8) : make_uint4(0, 0, 0, 0);
             put_x8_planes(v, hi + i * 8, lo + i * 8);
         }
@@ -114,7 +135,7 @@ struct SrcPlain {
 __host__ __device__ inline size_t stream_lds_bytes(int K, int elem, int waves, int gpw, int R) {
     const size_t step = elem == 1 ? 16 : 8;
     const size_t kpad = (((size_t)K + step - 1) / step) * step;
-    return 2 * kpad * (size_t)elem + (size_t)waves * gpw * R * 8;
+    return 2 * (kpad + kStageSlack) * (size_t)elem + (size_t)waves * gpw * R * 8;
 }
 
 template <int R, class Epi>
@@ -138,18 +159,19 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i8_stream(Src src, const int8
     extern __shared__ __align__(16) int8_t lds[];
     const int kpad = ((K + 15) >> 4) << 4;
     int8_t* hi_plane = lds;
-    int8_t* lo_plane = lds + kpad;
+    int8_t* lo_plane = lds + kpad + kStageSlack;
     const int lane = threadIdx.x & (kWave - 1);
     // wave-uniform by construction; readfirstlane lets the compiler keep the
     // loop control in scalar registers (a vector loop would end every
     // iteration with a full vmcnt drain)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    int64_t* rec = reinterpret_cast<int64_t*>(lds + 2 * kpad) + (size_t)wave * gpw * R;
+    int64_t* rec = reinterpret_cast<int64_t*>(lds + 2 * (kpad + kStageSlack)) + (size_t)wave * gpw * R;
     const int nw = gridDim.x * WAVES;
     const int ngroups = (N + R - 1) / R;
     const int nit = (K + kWave * 16 - 1) / (kWave * 16);  // 1 KiB steps per row
     const int nb = (nit + U - 1) / U;                      // batches per group
-    const typename Src::Pre pre = src.pre(K, kpad);
+    constexpr int kThreads = WAVES * kWave;
+    const typename Src::Pre pre = src.pre(K, kpad, kThreads);
     typename Epi::State es;
     epi.begin(es);
 
@@ -229,7 +251,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i8_stream(Src src, const int8
         load(A, g, 0);
         epi.prefetch(es, (g0 + lane * nw) * R, N);
         load(B, g1, kb1);
-        src.stage_i8(pre, hi_plane, lo_plane, K, kpad);
+        src.stage_i8(pre, hi_plane, lo_plane, K, kpad, kThreads);
         __syncthreads();
         reset();
         while (g < ngroups) {
@@ -253,7 +275,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i8_stream(Src src, const int8
     } else {
         load(A, g, 0);
         epi.prefetch(es, (g0 + lane * nw) * R, N);
-        src.stage_i8(pre, hi_plane, lo_plane, K, kpad);
+        src.stage_i8(pre, hi_plane, lo_plane, K, kpad, kThreads);
         __syncthreads();
         reset();
         while (g < ngroups) {
@@ -284,19 +306,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i16_stream(Src16 src, const i
     extern __shared__ __align__(16) int8_t lds_raw[];
     const int kpad = ((K + 7) >> 3) << 3;
     int16_t* hi_plane = reinterpret_cast<int16_t*>(lds_raw);
-    int16_t* lo_plane = hi_plane + kpad;
+    int16_t* lo_plane = hi_plane + kpad + kStageSlack;
     const int lane = threadIdx.x & (kWave - 1);
     // wave-uniform by construction; readfirstlane lets the compiler keep the
     // loop control in scalar registers (a vector loop would end every
     // iteration with a full vmcnt drain)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    int64_t* rec = reinterpret_cast<int64_t*>(lds_raw + 4 * kpad) + (size_t)wave * gpw * R;
+    int64_t* rec = reinterpret_cast<int64_t*>(lds_raw + 4 * (kpad + kStageSlack)) + (size_t)wave * gpw * R;
     const int nw = gridDim.x * WAVES;
     const int ngroups = (N + R - 1) / R;
     const int nit = (K + kWave * 8 - 1) / (kWave * 8);
     const int nb = (nit + U - 1) / U;
     typedef short __attribute__((ext_vector_type(2))) s2;
-    const typename Src16::Pre pre = src.pre(K, kpad);
+    constexpr int kThreads = WAVES * kWave;
+    const typename Src16::Pre pre = src.pre(K, kpad, kThreads);
     typename Epi::State es;
     epi.begin(es);
 
@@ -366,7 +389,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i16_stream(Src16 src, const i
     };
     load(A, g, 0);
     epi.prefetch(es, (g0 + lane * nw) * R, N);
-    src.stage_i16(pre, hi_plane, lo_plane, K, kpad);
+    src.stage_i16(pre, hi_plane, lo_plane, K, kpad, kThreads);
     __syncthreads();
     reset();
     while (g < ngroups) {
@@ -495,8 +518,7 @@ struct StreamOneOps {
     };
     __device__ inline void begin(State& s) const { s.row0 = -1; }
     __device__ inline void prefetch(State& s, int row0, int N) const {
-        if (row0 >= N) return;
-        s.o[0] = e.ops(row0);
+        s.o[0] = e.ops(min(row0, N - 1));
         s.o[1] = e.ops(min(row0 + 1, N - 1));
         s.row0 = row0;
     }

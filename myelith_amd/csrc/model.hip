@@ -162,34 +162,36 @@ struct SrcNorm {
         uint4 xv[kNormPre];
         uint2 sv[kNormPre], gv[kNormPre], gsv[kNormPre];
     };
-    __device__ inline Pre pre(int K, int kpad) const {
+    __device__ inline Pre pre(int K, int kpad, int nthr) const {
         Pre q;
-#pragma unroll
-        for (int j = 0; j < 3; ++j) q.a[j] = threadIdx.x < 64 ? acc->v[threadIdx.x][j] : 0;
+        const __amdgpu_buffer_rsrc_t ra = weight_rsrc(acc, sizeof(NormAcc));
+        const uint2 a01 = cload8(ra, threadIdx.x * 24u), a2 = cload8(ra, threadIdx.x * 24u + 8u);
+        q.a[0] = ((uint64_t)a01.y << 32) | a01.x;
+        q.a[1] = ((uint64_t)a2.y << 32) | a2.x;
+        const uint2 a3 = cload8(ra, threadIdx.x * 24u + 16u);
+        q.a[2] = ((uint64_t)a3.y << 32) | a3.x;
+        const __amdgpu_buffer_rsrc_t rx = weight_rsrc(x, 2u * (uint32_t)K), rs = weight_rsrc(xs, (uint32_t)K),
+                                     rg = weight_rsrc(g, (uint32_t)K), rgs = weight_rsrc(gs, (uint32_t)K);
 #pragma unroll
         for (int j = 0; j < kNormPre; ++j) {
-            const int k0 = (threadIdx.x + j * blockDim.x) * 8;
-            q.xv[j] = make_uint4(0, 0, 0, 0);
-            q.sv[j] = q.gv[j] = q.gsv[j] = make_uint2(0, 0);
-            if (k0 < K) {
-                q.xv[j] = *reinterpret_cast<const uint4*>(x + k0);
-                q.sv[j] = *reinterpret_cast<const uint2*>(xs + k0);
-                q.gv[j] = *reinterpret_cast<const uint2*>(g + k0);
-                q.gsv[j] = *reinterpret_cast<const uint2*>(gs + k0);
-            }
+            const uint32_t k0 = (threadIdx.x + j * nthr) * 8u;
+            q.xv[j] = cload16(rx, 2u * k0);
+            q.sv[j] = cload8(rs, k0);
+            q.gv[j] = cload8(rg, k0);
+            q.gsv[j] = cload8(rgs, k0);
         }
         return q;
     }
     __device__ inline RmsFactor factor(const Pre& q) const {
         __shared__ RmsFactor sf;
-        if (threadIdx.x < 64) {
-            uint64_t l[3];
+        // every wave reduces (the words past thread 63 are zero): the
+        // reduction has no branch to sink the norm-sum loads into
+        uint64_t l[3];
 #pragma unroll
-            for (int j = 0; j < 3; ++j) l[j] = wave_sum_u64(q.a[j]);
-            if (threadIdx.x == 0) {
-                const myl_i128 a = (myl_i128)((myl_u128)l[0] + ((myl_u128)l[1] << 42) + ((myl_u128)l[2] << 84));
-                sf = rms_factor_of(a, ref, p);
-            }
+        for (int j = 0; j < 3; ++j) l[j] = wave_sum_u64(q.a[j]);
+        if (threadIdx.x == 0) {
+            const myl_i128 a = (myl_i128)((myl_u128)l[0] + ((myl_u128)l[1] << 42) + ((myl_u128)l[2] << 84));
+            sf = rms_factor_of(a, ref, p);
         }
         __syncthreads();
         return sf;
@@ -205,23 +207,17 @@ struct SrcNorm {
     }
     // chunk i (k0 = 8 i) of the normalised vector; zeros past K
     template <class Put>
-    __device__ inline void stage(const Pre& q, int K, int kpad, const Put& put) const {
+    __device__ inline void stage(const Pre& q, int K, int kpad, int nthr, const Put& put) const {
         const RmsFactor f = factor(q);
         const int n8 = kpad >> 3;
 #pragma unroll
         for (int j = 0; j < kNormPre; ++j) {
-            const int i = threadIdx.x + j * blockDim.x;
-            if (i >= n8) break;
+            // zero operands past K give zero outputs
             int16_t v[8];
-            if (i * 8 < K) {
-                values8(f, q.xv[j], q.sv[j], q.gv[j], q.gsv[j], v);
-            } else {
-#pragma unroll
-                for (int t = 0; t < 8; ++t) v[t] = 0;
-            }
-            put(i, v);
+            values8(f, q.xv[j], q.sv[j], q.gv[j], q.gsv[j], v);
+            put(stage_slot(threadIdx.x + j * nthr, n8), v);
         }
-        for (int i = threadIdx.x + kNormPre * blockDim.x; i < n8; i += blockDim.x) {
+        for (int i = threadIdx.x + kNormPre * nthr; i < n8; i += nthr) {
             int16_t v[8];
             const int k0 = i * 8;
             if (k0 < K) {
@@ -234,11 +230,11 @@ struct SrcNorm {
             put(i, v);
         }
     }
-    __device__ inline void stage_i8(const Pre& q, int8_t* hi, int8_t* lo, int K, int kpad) const {
-        stage(q, K, kpad, [&](int i, const int16_t (&v)[8]) { put_planes_i8(v, hi + i * 8, lo + i * 8); });
+    __device__ inline void stage_i8(const Pre& q, int8_t* hi, int8_t* lo, int K, int kpad, int nthr) const {
+        stage(q, K, kpad, nthr, [&](int i, const int16_t (&v)[8]) { put_planes_i8(v, hi + i * 8, lo + i * 8); });
     }
-    __device__ inline void stage_i16(const Pre& q, int16_t* hi, int16_t* lo, int K, int kpad) const {
-        stage(q, K, kpad, [&](int i, const int16_t (&v)[8]) { put_planes_i16(v, hi + i * 8, lo + i * 8); });
+    __device__ inline void stage_i16(const Pre& q, int16_t* hi, int16_t* lo, int K, int kpad, int nthr) const {
+        stage(q, K, kpad, nthr, [&](int i, const int16_t (&v)[8]) { put_planes_i16(v, hi + i * 8, lo + i * 8); });
     }
 };
 
@@ -251,12 +247,11 @@ struct SrcAttn {
     struct Pre {
         uint4 a[4];
     };
-    __device__ inline Pre pre(int K, int kpad) const {
+    __device__ inline Pre pre(int K, int kpad, int nthr) const {
         Pre q;
-        const int k0 = threadIdx.x * 8;
+        const __amdgpu_buffer_rsrc_t r = weight_rsrc(acc, 8u * (uint32_t)K);
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-            q.a[t] = k0 < K ? reinterpret_cast<const uint4*>(acc + k0)[t] : make_uint4(0, 0, 0, 0);
+        for (int t = 0; t < 4; ++t) q.a[t] = cload16(r, threadIdx.x * 64u + 16u * t);
         return q;
     }
     __device__ inline void values8(const uint4 (&a4)[4], int16_t (&v)[8]) const {
@@ -272,18 +267,22 @@ struct SrcAttn {
             v[t] = clamp_i16(rescale32((int32_t)r, v_frac, out_frac));
         }
     }
-    __device__ inline void stage_i8(const Pre& q, int8_t* hi, int8_t* lo, int K, int kpad) const {
-        for (int i = threadIdx.x; i < (kpad >> 3); i += blockDim.x) {
+    __device__ inline void stage_i8(const Pre& q, int8_t* hi, int8_t* lo, int K, int kpad, int nthr) const {
+        const int n8 = kpad >> 3;
+        {
+            // zero accumulators past K give zero outputs
+            int16_t v[8];
+            values8(q.a, v);
+            const int i = stage_slot(threadIdx.x, n8);
+            put_planes_i8(v, hi + i * 8, lo + i * 8);
+        }
+        for (int i = threadIdx.x + nthr; i < n8; i += nthr) {
             int16_t v[8];
             const int k0 = i * 8;
             if (k0 < K) {
-                if (i == (int)threadIdx.x) {
-                    values8(q.a, v);
-                } else {
-                    const uint4* a4 = reinterpret_cast<const uint4*>(acc + k0);
-                    const uint4 w[4] = {a4[0], a4[1], a4[2], a4[3]};
-                    values8(w, v);
-                }
+                const uint4* a4 = reinterpret_cast<const uint4*>(acc + k0);
+                const uint4 w[4] = {a4[0], a4[1], a4[2], a4[3]};
+                values8(w, v);
             } else {
 #pragma unroll
                 for (int t = 0; t < 8; ++t) v[t] = 0;
@@ -430,7 +429,6 @@ struct EpiResid {
         s.row0 = -1;
     }
     __device__ inline void prefetch(State& s, int row0, int N) const {
-        if (row0 >= N) return;
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
             const int i = min(row0 + r, N - 1);
@@ -522,8 +520,7 @@ struct EpiHead {
         s.row0 = -1;
     }
     __device__ inline void prefetch(State& s, int row0, int N) const {
-        if (row0 >= N) return;
-        s.sh[0] = shifts[row0];
+        s.sh[0] = shifts[min(row0, N - 1)];
         s.sh[1] = shifts[min(row0 + 1, N - 1)];
         s.row0 = row0;
     }
@@ -709,6 +706,13 @@ int alloc_impl(myl_model* m, const myl_luts* luts) {
             m->exp_nz = i + 1;
             break;
         }
+    // a table equal to its closed form at every entry is computed in the
+    // norm setup instead of read: the read is a dependent load that waits
+    // behind the weight stream the kernel has already issued
+    m->rsqrt_closed = MYL_TV_RSQRT_OUTPUT_FRAC + (MYL_TV_RSQRT_INPUT_SHIFT + 1) / 2 <= 20;
+    for (size_t i = 0; i < luts->rsqrt_len && m->rsqrt_closed; ++i)
+        if (luts->rsqrt[i] != rsqrt_closed((uint32_t)i, MYL_TV_RSQRT_OUTPUT_FRAC, MYL_TV_RSQRT_INPUT_SHIFT))
+            m->rsqrt_closed = 0;
     m->rope_rows = (uint32_t)(luts->rope_len / (size_t)(hd / 2));
     m->rsqrt = m->dalloc<int16_t>(luts->rsqrt_len);
     m->silu = m->dalloc<int16_t>(luts->silu_len);
@@ -970,7 +974,8 @@ int synth_fill(myl_model* m) {
 }
 
 RmsParams rms_params(const myl_model* m) {
-    return RmsParams{m->rsqrt, m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20};
+    return RmsParams{m->rsqrt, m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20,
+                     m->rsqrt_closed};
 }
 
 // One transformer layer on m->hidden (model.rs:401-674); the result replaces

@@ -101,6 +101,7 @@ struct myl_model {
     void (*io_free)(void*) = nullptr;
     int16_t *rsqrt = nullptr, *silu = nullptr, *exp_lut = nullptr, *cos_lut = nullptr, *sin_lut = nullptr;
     int rsqrt_len = 0, silu_len = 0, exp_len = 0;
+    uint8_t rsqrt_closed = 0;  // the rsqrt table equals its closed form (RmsParams::closed)
     int exp_nz = 0;  // exp-table entries up to its last nonzero one
     int gu_repeat = 1;  // launches of each layer's gate/up GEMV per step (myl_model_set_kernel_repeat)
     int16_t* h_scratch = nullptr;  // output rows of the repeated launches

@@ -55,7 +55,33 @@ struct RmsParams {
     const int16_t* lut; int lut_len;
     uint8_t lut_input_shift, lut_output_frac;
     int64_t inv_n_q20;
+    // nonzero: every table entry equals rsqrt_closed(x, lut_output_frac,
+    // lut_input_shift) (checked on the host when the table is set), so the
+    // entry is computed instead of loaded
+    uint8_t closed = 0;
 };
+
+// The closed form of the rsqrt table, round(2^f / sqrt(x / 2^s)) for x >= 1
+// and 2^f at x = 0 (luts.py:32-49), in integer arithmetic: the result is the
+// largest v >= 0 with v - 1/2 <= 2^f sqrt(2^s / x), i.e. with
+// (2v - 1)^2 x <= 2^(2f + s + 2), found by bisection.  Exact ties (where the
+// reference's half-even rounding would decide) need x = 2^(2f + s + 2) with
+// v = 1; the host check against the table covers them.  f + s / 2 <= 20.
+MYL_FN int32_t rsqrt_closed(uint32_t x, uint32_t f, uint32_t s) {
+    if (x == 0) return (int32_t)(1u << f);
+    const uint32_t e = 2u * f + s + 2u;
+    uint32_t lo = 0, hi = (1u << (f + (s + 1u) / 2u)) + 1u;  // v(lo) holds, v(hi) fails
+    while (hi - lo > 1u) {
+        const uint32_t mid = (lo + hi) >> 1;
+        const uint64_t t = 2ull * mid - 1ull;
+        if (t * t * (uint64_t)x <= (1ull << e)) lo = mid; else hi = mid;
+    }
+    return (int32_t)lo;
+}
+
+__device__ inline int64_t rms_lut_value(const RmsParams& p, int idx) {
+    return p.closed ? (int64_t)rsqrt_closed((uint32_t)idx, p.lut_output_frac, p.lut_input_shift) : (int64_t)p.lut[idx];
+}
 
 // Norm factor of one row: everything except the per-channel output.
 struct RmsFactor { bool zero; uint8_t ref_shift; int64_t lut_val; uint32_t norm_frac; };
@@ -88,7 +114,7 @@ __device__ inline bool rms_factor_u64(myl_i128 acc, uint8_t ref, const RmsParams
         while ((m >> q) > max_idx) q += 2;
         int64_t idx = rshift_round64((int64_t)m, (uint8_t)q);
         if (idx > (int64_t)max_idx) idx = (int64_t)max_idx;
-        f.lut_val = (int64_t)p.lut[(int)idx];
+        f.lut_val = rms_lut_value(p, (int)idx);
         f.norm_frac = (uint32_t)p.lut_output_frac + (uint32_t)p.lut_input_shift / 2u + q / 2u;
     }
     return true;
@@ -119,7 +145,7 @@ __device__ inline RmsFactor rms_factor_of(myl_i128 acc, uint8_t ref, const RmsPa
         myl_i128 idx = rshift_round128(m, q);
         if (idx > max_idx) idx = max_idx;
         if (idx < 0) idx = 0;
-        f.lut_val = (int64_t)p.lut[(int)idx];
+        f.lut_val = rms_lut_value(p, (int)idx);
         f.norm_frac = (uint32_t)p.lut_output_frac + (uint32_t)p.lut_input_shift / 2u + q / 2u;
     }
     return f;

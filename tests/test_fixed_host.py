@@ -13,6 +13,7 @@ import shutil
 import subprocess
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -127,3 +128,39 @@ def test_recip32_matches_long_division(tmp_path):
     assert r.returncode == 0, r.stdout
     assert "mismatches 0" in r.stdout
 
+
+
+RSQRT_SRC = r"""
+#include <hip/hip_runtime.h>
+#include <cstdio>
+#include <cstdint>
+#include "ops.h"
+int main(int argc, char** argv) {
+    const uint32_t f = (uint32_t)atoi(argv[1]), sh = (uint32_t)atoi(argv[2]), n = (uint32_t)atoi(argv[3]);
+    for (uint32_t x = 0; x < n; ++x) printf("%d\n", myl::rsqrt_closed(x, f, sh));
+    return 0;
+}
+"""
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not Path("/opt/rocm/bin/hipcc").exists(), reason="hipcc absent")
+def test_rsqrt_closed_form_equals_the_table(tmp_path):
+    """rsqrt_closed (the norm setup's integer closed form) against the
+    reference's float64 table generator (luts.py:32-49) at every entry, for
+    the contract's parameters (input shift 8, 8 fraction bits) and for two
+    others, one with an odd input shift."""
+    from myelith_amd.luts import rsqrt_lut
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    src = tmp_path / "q.hip"
+    src.write_text(RSQRT_SRC)
+    exe = tmp_path / "q"
+    subprocess.run([hipcc, "-O2", "-std=c++17", "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang",
+                    "-packed-fp32-ops", "-I", str(ROOT / "myelith_amd" / "csrc"), "-I", str(ROOT / "include"),
+                    str(src), "-o", str(exe)], check=True, capture_output=True, timeout=300)
+    for frac, shift, n in ((8, 8, 32768), (6, 4, 20000), (10, 3, 9000)):
+        r = subprocess.run([str(exe), str(frac), str(shift), str(n)], capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0
+        got = np.array([int(v) for v in r.stdout.split()], dtype=np.int64)
+        want = rsqrt_lut(n - 1, shift, frac).astype(np.int64)
+        bad = np.nonzero(got != want)[0]
+        assert bad.size == 0, (frac, shift, bad[:10], got[bad[:10]], want[bad[:10]])

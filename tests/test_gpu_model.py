@@ -250,6 +250,32 @@ def test_decode_attention_exp_table_variants(backend, hd, variant):
     compare_kv(gm, om, spec, 200)
 
 
+def test_decode_rsqrt_table_unlike_its_closed_form(backend):
+    """An rsqrt table that differs from round(2^8 / sqrt(x / 2^8)) at every
+    odd index: the norm factor must come from the table (the closed form is
+    used only when every entry matches), for both decode and prompt rows."""
+    from myelith_amd.luts import LutSet
+    from myelith_amd.model import IntegerModel
+    from oracle.binding import OracleModel
+    spec = tiny(64, 0, 1, 2)
+    case(f"rsqrt table unlike its closed form {spec}")
+    base = LutSet.for_head_dim(64)
+    rsqrt = np.asarray(base.rsqrt, dtype=np.int16).copy()
+    rsqrt[1::2] += 3
+    luts = LutSet.from_tables(64, rsqrt, base.silu, base.exp, base.cos, base.sin)
+    gm, om = IntegerModel(backend, spec, luts), OracleModel(spec, luts, threads=16)
+    r = np.random.default_rng(5)
+    prompt = [int(t) for t in r.integers(0, spec["vocab"], 24)]
+    g = gm.prefill(prompt, 0)
+    for pos, t in enumerate(prompt):
+        o = om.forward_token(t, pos)
+    assert np.array_equal(g, o)
+    for i, t in enumerate(r.integers(0, spec["vocab"], 40)):
+        pos = len(prompt) + i
+        assert np.array_equal(gm.forward_token(int(t), pos), om.forward_token(int(t), pos)), pos
+    compare_kv(gm, om, spec, len(prompt) + 40)
+
+
 def test_decode_past_4096_positions(backend):
     """Decode attention over more than 4096 cached positions with four KV
     heads (the P.V kernel's scores no longer fit its registers and are read
