@@ -174,6 +174,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i8_stream(Src src, const int8
     const typename Src::Pre pre = src.pre(K, kpad, kThreads);
     typename Epi::State es;
     epi.begin(es);
+    // the staging loads above go out before the first weight batch below
+    // (the scheduler would otherwise interleave them, and loads complete in
+    // issue order)
+    __builtin_amdgcn_sched_barrier(0);
 
     const uint32_t wbytes = (uint32_t)N * (uint32_t)K;  // < 2^32 (checked by the launcher)
     const __amdgpu_buffer_rsrc_t wr = weight_rsrc(W, wbytes);
@@ -322,6 +326,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i16_stream(Src16 src, const i
     const typename Src16::Pre pre = src.pre(K, kpad, kThreads);
     typename Epi::State es;
     epi.begin(es);
+    __builtin_amdgcn_sched_barrier(0);  // staging loads before the first weight batch
 
     const uint32_t wbytes = 2u * (uint32_t)N * (uint32_t)K;  // < 2^32 (checked by the launcher)
     const __amdgpu_buffer_rsrc_t wr = weight_rsrc(W, wbytes);
