@@ -1,9 +1,9 @@
 // dec_attn.h -- integer attention of one query row per KV cache
-// (attention.rs:42-90 with softmax.rs:12-64): the decode step's attention,
-// shared by the single-sequence step and by decode batches (one row per
-// sequence).  A block covers one query head and kChunk positions.
+// (attention.rs:42-90 with softmax.rs:12-64): the decode step's attention.
+// A block covers one query head and kChunk positions.
 #pragma once
 
+#include "bufload.h"
 #include "ops.h"
 #include "wave.h"
 
@@ -88,15 +88,14 @@ struct DecV {
     uint32_t vv[PER];
 };
 
+// Rows at L and beyond (past the descriptor's range) read zero.
 template <int HD>
 __device__ inline void dec_load_v(int L, int base, const int16_t* __restrict__ vg, DecV<HD>& v) {
-    const int n = min(kChunk, L - base);
     const int dp = threadIdx.x % DecV<HD>::TPR, stream = threadIdx.x / DecV<HD>::TPR;
+    const __amdgpu_buffer_rsrc_t r = weight_rsrc(vg, (uint32_t)L * HD * 2u);
 #pragma unroll
-    for (int i = 0; i < DecV<HD>::PER; ++i) {
-        const int t = stream + i * DecV<HD>::STREAMS;
-        v.vv[i] = t < n ? *reinterpret_cast<const uint32_t*>(vg + (size_t)(base + t) * HD + 2 * dp) : 0u;
-    }
+    for (int i = 0; i < DecV<HD>::PER; ++i)
+        v.vv[i] = cload4(r, ((uint32_t)(base + stream + i * DecV<HD>::STREAMS) * HD + 2 * dp) * 2u);
 }
 
 // The exact partial P.V of one chunk (attention.rs:75-81 with
@@ -107,13 +106,17 @@ __device__ inline void dec_load_v(int L, int base, const int16_t* __restrict__ v
 // acc[0 .. HD) with 64-bit atomics (exact, order-free).  exp_lds >= 0: every
 // exp-table entry from exp_lds on is zero and entries [0, exp_lds) are read
 // from an LDS copy (exp_lds <= kDecExpLds); -1: the table is read in place.
-// Every global load of the block (table, V, scores) is issued before any is
-// used.  Whole block (256 threads).
+// The table is zero-padded to a multiple of 8 entries; z holds zlen >= L
+// entries (a multiple of 4, 16-byte aligned).  Every global load of the
+// block is issued before any is used, the table and the scores (needed
+// first) ahead of the chunk's V rows, all through buffer descriptors (no
+// branch, no clamp: past the range a load reads zero).  Whole block (256
+// threads).
 template <int HD>
-__device__ inline void dec_pv(int L, int base, const int32_t* __restrict__ z, const int16_t* __restrict__ vg,
-                              const int16_t* __restrict__ lut, uint32_t lut_len, uint8_t lut_shift, int exp_lds,
-                              unsigned long long* __restrict__ acc) {
-    constexpr int ZPER = 16;  // scores held in registers per thread (L <= 4096)
+__device__ inline void dec_pv(int L, int base, const int32_t* __restrict__ z, int zlen,
+                              const int16_t* __restrict__ vg, const int16_t* __restrict__ lut, uint32_t lut_len,
+                              uint8_t lut_shift, int exp_lds, unsigned long long* __restrict__ acc) {
+    constexpr int ZV = 4;  // 4-score vectors held in registers per thread (L <= 4096)
     constexpr int LPT = kDecExpLds / 8 / 256;  // 8-entry table pieces per thread
     constexpr int STREAMS = DecV<HD>::STREAMS, PER = DecV<HD>::PER;
     __shared__ int16_t elut[kDecExpLds];
@@ -123,47 +126,44 @@ __device__ inline void dec_pv(int L, int base, const int32_t* __restrict__ z, co
     __shared__ int64_t red[STREAMS][HD];
     const int tid = threadIdx.x;
     const bool lds = exp_lds >= 0;
+    // the table's nonzero prefix (pieces past it read zero without a fetch)
+    const __amdgpu_buffer_rsrc_t rl = weight_rsrc(lut, lds ? (uint32_t)((exp_lds + 7) & ~7) * 2u : 0u);
     uint4 lv[LPT];
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-        const int e0 = (tid + i * 256) * 8;
-        lv[i] = make_uint4(0, 0, 0, 0);
-        if (lds && e0 < exp_lds) {
-            if ((uint32_t)e0 + 8u <= lut_len) {
-                lv[i] = *reinterpret_cast<const uint4*>(lut + e0);
-            } else {
-                uint32_t w[4] = {0, 0, 0, 0};
-                for (int k = 0; k < 8 && (uint32_t)(e0 + k) < lut_len; ++k)
-                    w[k >> 1] |= (uint32_t)(uint16_t)lut[e0 + k] << (16 * (k & 1));
-                lv[i] = make_uint4(w[0], w[1], w[2], w[3]);
-            }
-        }
-    }
-    const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
-    DecV<HD> v;
-    dec_load_v<HD>(L, base, vg, v);
-    const bool regs = L <= 256 * ZPER;
-    int32_t zz[ZPER];
-    if (regs) {
+    for (int i = 0; i < LPT; ++i) lv[i] = cload16(rl, (uint32_t)(tid + i * 256) * 16u);
+    const int32_t lut0 = (int16_t)(cload4(weight_rsrc(lut, ((lut_len + 7u) & ~7u) * 2u), 0) & 0xFFFFu);
+    // thread t holds the score vectors t + 256 i (positions 4 (t + 256 i) ..
+    // + 3); entries at L and beyond are masked where used
+    const bool regs = L <= 1024 * ZV;
+    const int nzv = (L + 1023) >> 10;
+    const __amdgpu_buffer_rsrc_t rz = weight_rsrc(z, (uint32_t)zlen * 4u);
+    int4 zv[ZV];
 #pragma unroll
-        for (int t = 0; t < ZPER; ++t) {
-            const int j = tid + t * 256;
-            zz[t] = j < L ? z[j] : INT32_MIN;
-        }
+    for (int i = 0; i < ZV; ++i) {
+        const uint4 w = cload16(rz, (uint32_t)(tid + 256 * i) * 16u);
+        zv[i] = make_int4((int32_t)w.x, (int32_t)w.y, (int32_t)w.z, (int32_t)w.w);
     }
     const int n = min(kChunk, L - base);
-    const int32_t zown = tid < n ? z[base + tid] : 0;
-    if (lds) {
+    const int32_t zown = (int32_t)cload4(rz, (uint32_t)(base + tid) * 4u);  // used for tid < n
+    __builtin_amdgcn_sched_barrier(0);  // the V rows load after all of the above
+    DecV<HD> v;
+    dec_load_v<HD>(L, base, vg, v);
+    // the whole LDS table, unconditionally (a store under a branch would take
+    // its load in with it); entries from exp_lds on are never read
 #pragma unroll
-        for (int i = 0; i < LPT; ++i) {
-            const int e0 = (tid + i * 256) * 8;
-            if (e0 < exp_lds) *reinterpret_cast<uint4*>(elut + e0) = lv[i];  // visible after the max's barrier
-        }
-    }
+    for (int i = 0; i < LPT; ++i)
+        *reinterpret_cast<uint4*>(elut + (tid + i * 256) * 8) = lv[i];  // read after the max's barrier
+    const int32_t lut_one = lut_len > 0 ? lut0 : 1;
+    auto zat = [&](int i, int e) { return e == 0 ? zv[i].x : e == 1 ? zv[i].y : e == 2 ? zv[i].z : zv[i].w; };
     int32_t mx = INT32_MIN;
     if (regs) {
 #pragma unroll
-        for (int t = 0; t < ZPER; ++t) mx = max(mx, zz[t]);
+        for (int i = 0; i < ZV; ++i)
+            if (i < nzv) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (4 * (tid + 256 * i) + e < L) mx = max(mx, zat(i, e));
+            }
     } else {
         for (int j = tid; j < L; j += 256) mx = max(mx, z[j]);
     }
@@ -176,14 +176,48 @@ __device__ inline void dec_pv(int L, int base, const int32_t* __restrict__ z, co
         if (lds) return idx < (uint32_t)exp_lds ? (int32_t)elut[idx] : 0;
         return idx < lut_len ? (int32_t)lut[idx] : 0;
     };
+    // the same from the LDS copy, straight-line: the table read is issued
+    // whatever the entry, then selects (no branch, no wait per entry)
+    const uint32_t sh = lut_shift & 31u;
+    auto ex_lds = [&](int32_t zj) -> int32_t {
+        const int32_t x = sat_sub32(mx, zj);
+        const uint32_t idx = (uint32_t)x >> sh;
+        const bool in = idx < (uint32_t)exp_lds;
+        const int32_t t = elut[in ? idx : 0u];
+        return x <= 0 ? lut_one : (in ? t : 0);
+    };
     uint32_t s = 0;
-    if (regs) {
+    if (regs && lds) {
 #pragma unroll
-        for (int t = 0; t < ZPER; ++t)
-            if (tid + t * 256 < L) s += (uint32_t)ex(zz[t]);
+        for (int i = 0; i < ZV; ++i)
+            if (i < nzv) {
+                // a vector's four table reads issue together, then selects
+                int32_t x[4], t[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    x[e] = sat_sub32(mx, zat(i, e));
+                    const uint32_t idx = (uint32_t)x[e] >> sh;
+                    t[e] = elut[idx < (uint32_t)exp_lds ? idx : 0u];
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool in = ((uint32_t)x[e] >> sh) < (uint32_t)exp_lds;
+                    const int32_t v = x[e] <= 0 ? lut_one : (in ? t[e] : 0);
+                    s += 4 * (tid + 256 * i) + e < L ? (uint32_t)v : 0u;
+                }
+            }
+    } else if (regs) {
+#pragma unroll
+        for (int i = 0; i < ZV; ++i)
+            if (i < nzv) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (4 * (tid + 256 * i) + e < L) s += (uint32_t)ex(zat(i, e));
+            }
     } else {
         for (int j = tid; j < L; j += 256) s += (uint32_t)ex(z[j]);
     }
+    const int32_t eown = lds ? ex_lds(zown) : ex(zown);  // this entry's numerator, ahead of the sum's barrier
     const int32_t S = (int32_t)block_sum_u32_dpp(s, reds);
     const int dp = tid % DecV<HD>::TPR, stream = tid / DecV<HD>::TPR;
     const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
@@ -199,7 +233,7 @@ __device__ inline void dec_pv(int L, int base, const int32_t* __restrict__ z, co
                 pv = ubase + (((uint64_t)(base + tid) < (uint64_t)(int64_t)urem) ? 1 : 0);
             } else {
                 const uint64_t rs = recip32(S < 0 ? 0u - (uint32_t)S : (uint32_t)S);
-                pv = softmax_div_round(wmul32(ex(zown), one), S, rs);
+                pv = softmax_div_round(wmul32(eown, one), S, rs);
             }
         }
         p[tid] = pv;

@@ -78,15 +78,20 @@ MYL_FN int64_t rescale64(int64_t acc, uint8_t in_frac, uint8_t out_frac) {
 // division (integer only).  The dividend 2^32 has its only set bit at
 // position 32, so the quotient bits above position 32 - ceil(log2 d) are zero
 // and the remainder entering that position is 2^(ceil(log2 d) - 1): the loop
-// starts there (33 - ceil(log2 d) steps instead of 33).
+// starts there (33 - ceil(log2 d) steps instead of 33).  For d >= 2 the
+// quotient fits 32 bits and the remainder stays below d, so each step runs
+// on 32-bit words: the doubled remainder's 33rd bit is the old top bit, and
+// when it is set the difference 2r - d (below d) is exact modulo 2^32.
 MYL_FN uint64_t recip32(uint32_t d) {
-    if (d == 0) return 0x1FFFFFFFFull;
-    const int c = d > 1 ? 32 - __builtin_clz(d - 1u) : 0;  // ceil(log2 d)
-    uint64_t q = 0, r = c > 0 ? (1ull << (c - 1)) : 0;
+    if (d <= 1) return d == 0 ? 0x1FFFFFFFFull : 0x100000000ull;
+    const int c = 32 - __builtin_clz(d - 1u);  // ceil(log2 d), 1..32
+    uint32_t q = 0, r = 1u << (c - 1);
     for (int bit = 32 - c; bit >= 0; --bit) {
-        r = (r << 1) | (bit == 32 ? 1u : 0u);
-        q <<= 1;
-        if (r >= d) { r -= d; q |= 1; }
+        const bool carry = (int32_t)r < 0;
+        const uint32_t r2 = r << 1;
+        const bool take = carry || r2 >= d;
+        r = take ? r2 - d : r2;
+        q = (q << 1) | (take ? 1u : 0u);
     }
     return q;
 }

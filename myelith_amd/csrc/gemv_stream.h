@@ -39,6 +39,7 @@
 //                                                (may synchronise the block)
 #pragma once
 
+#include "bufload.h"
 #include "gemv.h"
 
 #include <algorithm>
@@ -47,14 +48,6 @@
 
 namespace myl {
 
-// A raw buffer descriptor over a whole weight matrix (gfx9-family dword 3).
-// Loads whose byte offset is at or past num_records return zero in hardware,
-// so out-of-range slots need no predicate: the loads stay straight-line code
-// and the compiler's in-order vmcnt accounting can keep a whole batch in
-// flight while the previous one is consumed.
-__device__ inline __amdgpu_buffer_rsrc_t weight_rsrc(const void* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
 // Weight loads are non-temporal (cache-policy bit nt): each weight byte is
 // read once per step, and on MI355X the streaming kernels ran 5-12 % faster
 // with them (decode step 2.29 -> 2.13 ms, int16 LM head 188 -> 165 us).
@@ -64,18 +57,9 @@ __device__ inline uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
 }
 
-// Loads of the staging operands, issued ahead of the first weight batch,
-// through a buffer descriptor over the operand: past num_records a load
-// returns zero, so no branch guards it.
-constexpr int kPreCpol = 0;
-__device__ inline uint4 cload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kPreCpol);
-    return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
-}
-__device__ inline uint2 cload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kPreCpol);
-    return make_uint2((uint32_t)v[0], (uint32_t)v[1]);
-}
+// The staging operands load through cload16 / cload8 (bufload.h), issued
+// ahead of the first weight batch: past num_records a load returns zero, so
+// no branch guards it.
 
 // ---- staging sources ----------------------------------------------------------
 

@@ -568,7 +568,8 @@ template <int HD>
 __global__ __launch_bounds__(256) void attn_scores_kernel(const DecodeState* __restrict__ st,
                                                          const int16_t* __restrict__ q, const int16_t* __restrict__ kc,
                                                          int max_pos, int G, int chunks, int64_t score_mult,
-                                                         uint8_t score_shift, int32_t* __restrict__ scores) {
+                                                         uint8_t score_shift, int32_t* __restrict__ scores,
+                                                         int score_ld) {
     const AttnBlock b;
     if (b.c >= chunks) return;
     const int L = st->pos + 1;
@@ -576,14 +577,14 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(const DecodeState* __r
     if (base >= L) return;
     const int head = b.g * G + b.h;
     dec_scores<HD>(L, base, q + (size_t)head * HD, kc + (size_t)b.g * max_pos * HD, score_mult, score_shift,
-                   scores + (size_t)head * max_pos);
+                   scores + (size_t)head * score_ld);
 }
 
 template <int HD>
 __global__ __launch_bounds__(256) void attn_pv_kernel(const DecodeState* __restrict__ st,
                                                      const int32_t* __restrict__ scores,
-                                                     const int16_t* __restrict__ vc, int max_pos, int G, int chunks,
-                                                     const int16_t* __restrict__ lut, uint32_t lut_len,
+                                                     const int16_t* __restrict__ vc, int max_pos, int score_ld, int G,
+                                                     int chunks, const int16_t* __restrict__ lut, uint32_t lut_len,
                                                      uint8_t lut_shift, int exp_lds,
                                                      unsigned long long* __restrict__ acc) {
     const AttnBlock b;
@@ -592,8 +593,8 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(const DecodeState* __restr
     const int base = b.c * kChunk;
     if (base >= L) return;
     const int head = b.g * G + b.h;
-    dec_pv<HD>(L, base, scores + (size_t)head * max_pos, vc + (size_t)b.g * max_pos * HD, lut, lut_len, lut_shift,
-               exp_lds, acc + (size_t)head * HD);
+    dec_pv<HD>(L, base, scores + (size_t)head * score_ld, score_ld, vc + (size_t)b.g * max_pos * HD, lut, lut_len,
+               lut_shift, exp_lds, acc + (size_t)head * HD);
 }
 
 // ---------------------------------------------------------------------------
@@ -716,14 +717,17 @@ int alloc_impl(myl_model* m, const myl_luts* luts) {
     m->rope_rows = (uint32_t)(luts->rope_len / (size_t)(hd / 2));
     m->rsqrt = m->dalloc<int16_t>(luts->rsqrt_len);
     m->silu = m->dalloc<int16_t>(luts->silu_len);
-    m->exp_lut = m->dalloc<int16_t>(luts->exp_len);
+    const size_t exp_pad = (luts->exp_len + 7) & ~(size_t)7;  // whole 16-byte pieces (dec_pv)
+    m->exp_lut = m->dalloc<int16_t>(exp_pad ? exp_pad : 8);
     m->cos_lut = m->dalloc<int16_t>(luts->rope_len);
     m->sin_lut = m->dalloc<int16_t>(luts->rope_len);
     if (!m->rsqrt || !m->silu || !m->exp_lut || !m->cos_lut || !m->sin_lut) return c->fail(MYL_E_NOMEM, "LUT allocation");
     int rc = 0;
     rc |= upload(m, m->rsqrt, std::vector<int16_t>(luts->rsqrt, luts->rsqrt + luts->rsqrt_len));
     rc |= upload(m, m->silu, std::vector<int16_t>(luts->silu, luts->silu + luts->silu_len));
-    rc |= upload(m, m->exp_lut, std::vector<int16_t>(luts->exp, luts->exp + luts->exp_len));
+    std::vector<int16_t> exp_host(luts->exp, luts->exp + luts->exp_len);
+    exp_host.resize(exp_pad, 0);
+    rc |= upload(m, m->exp_lut, exp_host);
     rc |= upload(m, m->cos_lut, std::vector<int16_t>(luts->cos, luts->cos + luts->rope_len));
     rc |= upload(m, m->sin_lut, std::vector<int16_t>(luts->sin, luts->sin + luts->rope_len));
     if (rc) return MYL_E_HIP;
@@ -820,7 +824,8 @@ int alloc_impl(myl_model* m, const myl_luts* luts) {
     m->resid = m->dalloc<int16_t>(H);
     m->h = m->dalloc<int16_t>(I);
     m->logits = m->dalloc<int32_t>(V);
-    m->scores = m->dalloc<int32_t>((size_t)s.heads * m->max_pos);
+    m->score_ld = (m->max_pos + 3) & ~3;
+    m->scores = m->dalloc<int32_t>((size_t)s.heads * m->score_ld);
     m->attn_acc = m->dalloc<unsigned long long>((size_t)nq);
     m->norm_a = m->dalloc<NormAcc>(1);
     m->norm_b = m->dalloc<NormAcc>(1);
@@ -1018,14 +1023,14 @@ hipError_t layer_step(myl_model* m, int l) {
         const int exp_lds = m->exp_nz <= kDecExpLds ? m->exp_nz : -1;
         if (hd == 128) {
             attn_scores_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, chunks, m->score_mult,
-                                                          score_shift, m->scores);
-            attn_pv_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, G, chunks, m->exp_lut,
-                                                      (uint32_t)m->exp_len, lut_shift, exp_lds, m->attn_acc);
+                                                          score_shift, m->scores, m->score_ld);
+            attn_pv_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G, chunks,
+                                                      m->exp_lut, (uint32_t)m->exp_len, lut_shift, exp_lds, m->attn_acc);
         } else {
             attn_scores_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, chunks, m->score_mult,
-                                                         score_shift, m->scores);
-            attn_pv_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, G, chunks, m->exp_lut,
-                                                     (uint32_t)m->exp_len, lut_shift, exp_lds, m->attn_acc);
+                                                         score_shift, m->scores, m->score_ld);
+            attn_pv_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G, chunks,
+                                                     m->exp_lut, (uint32_t)m->exp_len, lut_shift, exp_lds, m->attn_acc);
         }
         e = hipGetLastError();
         if (e != hipSuccess) return e;

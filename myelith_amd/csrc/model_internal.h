@@ -111,7 +111,8 @@ struct myl_model {
     int16_t *kcache = nullptr, *vcache = nullptr;
     int16_t *hidden = nullptr, *norm = nullptr, *q = nullptr, *attn = nullptr, *resid = nullptr, *h = nullptr;
     int32_t* logits = nullptr;
-    int32_t* scores = nullptr;
+    int32_t* scores = nullptr;  // [heads][score_ld] decode attention scores
+    int score_ld = 0;           // max_pos rounded up to 4 (16-byte aligned rows)
     unsigned long long* attn_acc = nullptr;  // [nq] exact P.V sums, cleared after each use
     NormAcc* norm_a = nullptr;               // input-norm / final-norm sums of squares
     NormAcc* norm_b = nullptr;               // post-attention-norm sums of squares
