@@ -26,6 +26,7 @@
 #include "model_internal.h"
 #include "ops.h"
 #include "rows_attn.h"
+#include "rows_dec.h"
 #include "rows_epi.h"
 #include "wave.h"
 
@@ -427,6 +428,44 @@ int ensure_scores(myl_model* m, BatchState* b, int lmax) {
     return MYL_OK;
 }
 
+// The decode-batch attention kernels (rows_dec.h) for the query-head group
+// sizes they are built for.
+constexpr bool rows_dec_ok(int hd, int G) { return (hd == 64 || hd == 128) && (G == 4 || G == 7 || G == 8); }
+
+template <int HD>
+hipError_t rows_dec_qk(int G, dim3 grid, hipStream_t st, const int32_t* rows, int rows_cap, const int16_t* Q, int nq,
+                       const int16_t* kc, size_t sstride, int max_pos, int64_t mult, uint8_t shift, int32_t* scores,
+                       int heads, int lcap) {
+#define MYL_DEC_QK(GV)                                                                                              \
+    rows_dec_qk_kernel<HD, GV><<<grid, 256, 0, st>>>(rows, rows_cap, Q, nq, kc, sstride, max_pos, mult, shift, scores, \
+                                                     heads, lcap)
+    switch (G) {
+        case 4: MYL_DEC_QK(4); break;
+        case 7: MYL_DEC_QK(7); break;
+        case 8: MYL_DEC_QK(8); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef MYL_DEC_QK
+    return hipGetLastError();
+}
+
+template <int HD>
+hipError_t rows_dec_pv(int G, dim3 grid, hipStream_t st, const int32_t* rows, int rows_cap, const int16_t* probs,
+                       int heads, int lcap, const int16_t* vc, size_t sstride, int max_pos, int64_t* part,
+                       size_t part_stride, int nq) {
+#define MYL_DEC_PV(GV)                                                                                              \
+    rows_dec_pv_kernel<HD, GV><<<grid, 256, 0, st>>>(rows, rows_cap, probs, heads, lcap, vc, sstride, max_pos, part, \
+                                                     part_stride, nq)
+    switch (G) {
+        case 4: MYL_DEC_PV(4); break;
+        case 7: MYL_DEC_PV(7); break;
+        case 8: MYL_DEC_PV(8); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef MYL_DEC_PV
+    return hipGetLastError();
+}
+
 // One batched forward over the rows already uploaded to b->rows; lmax is the
 // largest position + 1 among them.  The final norm and LM head run over rows
 // [h0, R) only, into logits_out [(R - h0) x V] and argmax_out [R - h0].
@@ -493,7 +532,16 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         const uint8_t score_shift = (uint8_t)(ss > MYL_TV_SCORE_FRAC_BITS ? ss - MYL_TV_SCORE_FRAC_BITS : 0);
         const dim3 ag(b->ntiles, kvh, ranges);
         const size_t pst = (size_t)b->rows_cap * nq;
-        if (hd == 128)
+        // one row per sequence (decode batches): a block per (row, KV head,
+        // range) instead of row tiles
+        const bool dec_rows = b->max_qv == G && rows_dec_ok(hd, G);
+        const dim3 dg((lmax + kChunk - 1) / kChunk, kvh, R), dpg(ranges, kvh, R);
+        if (dec_rows)
+            e = hd == 128 ? rows_dec_qk<128>(G, dg, st, b->rows, b->rows_cap, b->Q, nq, kc, sstride, m->max_pos,
+                                             m->score_mult, score_shift, b->scores, heads, b->lmax_cap)
+                          : rows_dec_qk<64>(G, dg, st, b->rows, b->rows_cap, b->Q, nq, kc, sstride, m->max_pos,
+                                            m->score_mult, score_shift, b->scores, heads, b->lmax_cap);
+        else if (hd == 128)
             rows_qk_kernel<128><<<ag, kAttnThreads, attn_qk_lds<128>(), st>>>(
                 b->tiles, b->rows, b->rows_cap, b->Q, nq, kc, sstride, m->max_pos, G, m->score_mult, score_shift,
                 b->scores, heads, b->lmax_cap);
@@ -501,7 +549,8 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
             rows_qk_kernel<64><<<ag, kAttnThreads, attn_qk_lds<64>(), st>>>(
                 b->tiles, b->rows, b->rows_cap, b->Q, nq, kc, sstride, m->max_pos, G, m->score_mult, score_shift,
                 b->scores, heads, b->lmax_cap);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (!dec_rows) e = hipGetLastError();
+        if (e != hipSuccess) return e;
         // a wave per (row, head) when there are enough of them to fill the
         // chip, else a block of four waves each
         const int npairs = R * heads;
@@ -517,7 +566,7 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         // Big grids (prefill) loop each block over its tile's ranges and
         // finish the attention output in place; small ones (decode batches)
         // keep a block per range and sum the ranges afterwards.
-        const bool loop = (int64_t)b->ntiles * kvh >= 2 * (int64_t)c->prop.multiProcessorCount;
+        const bool loop = !dec_rows && (int64_t)b->ntiles * kvh >= 2 * (int64_t)c->prop.multiProcessorCount;
         const dim3 pg(b->ntiles, kvh, loop ? 1 : ranges);
         int8_t* pplanes = planes ? mm->planes : nullptr;
 #define MYL_PV_LAUNCH(HDV, LOOPV, QVMV)                                                                            \
@@ -527,7 +576,13 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         // tiles of at most 32 query vectors (decode batches) take the
         // narrow variant: 60 KB of LDS, two blocks per CU
         const bool narrow = b->max_qv <= 32;
-        if (hd == 128) {
+        if (dec_rows) {
+            e = hd == 128 ? rows_dec_pv<128>(G, dpg, st, b->rows, b->rows_cap, b->probs, heads, b->lmax_cap, vc,
+                                             sstride, m->max_pos, b->part, pst, nq)
+                          : rows_dec_pv<64>(G, dpg, st, b->rows, b->rows_cap, b->probs, heads, b->lmax_cap, vc,
+                                            sstride, m->max_pos, b->part, pst, nq);
+            if (e != hipSuccess) return e;
+        } else if (hd == 128) {
             if (narrow) {
                 if (loop) MYL_PV_LAUNCH(128, true, 32);
                 else MYL_PV_LAUNCH(128, false, 32);

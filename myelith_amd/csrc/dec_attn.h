@@ -18,61 +18,79 @@ __device__ inline void split_pair(uint32_t v, uint32_t& hi, uint32_t& lo) {
     lo = (v & 0x00FF00FFu);
 }
 
+// The K rows of one chunk as dec_scores holds them: LPP = HD / 8 lanes hold
+// 16 bytes of a K row each (a wave reads whole rows, coalesced), the wave's
+// kChunk / 4 positions in STEPS steps of PPW rows.
+template <int HD>
+struct DecK {
+    static constexpr int LPP = HD / 8;
+    static constexpr int PPW = 64 / LPP;              // positions per wave per step
+    static constexpr int STEPS = kChunk / 4 / PPW;    // steps per wave
+    static_assert(LPP == 8 || LPP == 16, "row sums cover 8 or 16 lanes");
+    uint4 kv[STEPS];
+    __device__ static int sub() { return (threadIdx.x & 63) % LPP; }
+    __device__ static int pos(int base, int it) {
+        return base + (int)(threadIdx.x >> 6) * (kChunk / 4) + it * PPW + (int)(threadIdx.x & 63) / LPP;
+    }
+    __device__ inline void load(int L, int base, const int16_t* __restrict__ kg) {
+#pragma unroll
+        for (int it = 0; it < STEPS; ++it) {
+            const int j = pos(base, it);
+            kv[it] = j < L ? *reinterpret_cast<const uint4*>(kg + (size_t)j * HD + sub() * 8) : make_uint4(0, 0, 0, 0);
+        }
+    }
+    // z_j for the held rows j < L and one head's query piece qv (the lane's
+    // 16 bytes of q): q . k is exact as 256 * sum(k * q_hi) + sum(k * q_lo) on
+    // v_dot2_i32_i16 (|partials| < 2^31), the row sums over the LPP lanes are
+    // DPP moves
+    __device__ inline void scores(int L, int base, uint4 qv, int64_t score_mult, uint8_t score_shift,
+                                  int32_t* __restrict__ z) const {
+        uint4 qh, ql;
+        split_pair(qv.x, qh.x, ql.x);
+        split_pair(qv.y, qh.y, ql.y);
+        split_pair(qv.z, qh.z, ql.z);
+        split_pair(qv.w, qh.w, ql.w);
+        typedef short __attribute__((ext_vector_type(2))) s2;
+        auto d2 = [](uint32_t a, uint32_t c, int32_t acc) {
+            return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, a), __builtin_bit_cast(s2, c), acc, false);
+        };
+#pragma unroll
+        for (int it = 0; it < STEPS; ++it) {
+            const int j = pos(base, it);
+            int32_t ahi = 0, alo = 0;
+            ahi = d2(kv[it].x, qh.x, ahi);
+            ahi = d2(kv[it].y, qh.y, ahi);
+            ahi = d2(kv[it].z, qh.z, ahi);
+            ahi = d2(kv[it].w, qh.w, ahi);
+            alo = d2(kv[it].x, ql.x, alo);
+            alo = d2(kv[it].y, ql.y, alo);
+            alo = d2(kv[it].z, ql.z, alo);
+            alo = d2(kv[it].w, ql.w, alo);
+            if (LPP == 16) {
+                ahi = row_sum16_i32(ahi);
+                alo = row_sum16_i32(alo);
+            } else {
+                ahi = row_sum8_i32(ahi);
+                alo = row_sum8_i32(alo);
+            }
+            if (sub() == 0 && j < L) {
+                const int64_t dot = (int64_t)ahi * 256 + (int64_t)alo;
+                z[j] = (int32_t)rshift_round64(wmul64(dot, score_mult), score_shift);
+            }
+        }
+    }
+};
+
 // z_j = (i32)RNE(q . k_j * mult, shift) for j in [base, min(base + kChunk, L))
 // (attention.rs:66-67); q is one head's vector, kg the KV head's K rows, z
-// the head's score row.  LPP = HD / 8 lanes hold 16 bytes of a K row each
-// (a wave reads whole rows, coalesced); q . k is exact as
-// 256 * sum(k * q_hi) + sum(k * q_lo) on v_dot2_i32_i16 (|partials| < 2^31),
-// the row sums over the LPP lanes are DPP moves.  256 threads.
+// the head's score row.  256 threads.
 template <int HD>
 __device__ inline void dec_scores(int L, int base, const int16_t* __restrict__ q, const int16_t* __restrict__ kg,
                                   int64_t score_mult, uint8_t score_shift, int32_t* __restrict__ z) {
-    constexpr int LPP = HD / 8;
-    constexpr int PPW = 64 / LPP;                 // positions per wave per step
-    constexpr int STEPS = kChunk / 4 / PPW;       // steps per wave
-    static_assert(LPP == 8 || LPP == 16, "row sums cover 8 or 16 lanes");
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane % LPP, slot = lane / LPP;
-    uint4 kv[STEPS];
-#pragma unroll
-    for (int it = 0; it < STEPS; ++it) {
-        const int j = base + wave * (kChunk / 4) + it * PPW + slot;
-        kv[it] = j < L ? *reinterpret_cast<const uint4*>(kg + (size_t)j * HD + sub * 8) : make_uint4(0, 0, 0, 0);
-    }
-    const uint4 qv = *reinterpret_cast<const uint4*>(q + sub * 8);
-    uint4 qh, ql;
-    split_pair(qv.x, qh.x, ql.x);
-    split_pair(qv.y, qh.y, ql.y);
-    split_pair(qv.z, qh.z, ql.z);
-    split_pair(qv.w, qh.w, ql.w);
-    typedef short __attribute__((ext_vector_type(2))) s2;
-    auto d2 = [](uint32_t a, uint32_t c, int32_t acc) {
-        return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, a), __builtin_bit_cast(s2, c), acc, false);
-    };
-#pragma unroll
-    for (int it = 0; it < STEPS; ++it) {
-        const int j = base + wave * (kChunk / 4) + it * PPW + slot;
-        int32_t ahi = 0, alo = 0;
-        ahi = d2(kv[it].x, qh.x, ahi);
-        ahi = d2(kv[it].y, qh.y, ahi);
-        ahi = d2(kv[it].z, qh.z, ahi);
-        ahi = d2(kv[it].w, qh.w, ahi);
-        alo = d2(kv[it].x, ql.x, alo);
-        alo = d2(kv[it].y, ql.y, alo);
-        alo = d2(kv[it].z, ql.z, alo);
-        alo = d2(kv[it].w, ql.w, alo);
-        if (LPP == 16) {
-            ahi = row_sum16_i32(ahi);
-            alo = row_sum16_i32(alo);
-        } else {
-            ahi = row_sum8_i32(ahi);
-            alo = row_sum8_i32(alo);
-        }
-        if (sub == 0 && j < L) {
-            const int64_t dot = (int64_t)ahi * 256 + (int64_t)alo;
-            z[j] = (int32_t)rshift_round64(wmul64(dot, score_mult), score_shift);
-        }
-    }
+    DecK<HD> k;
+    k.load(L, base, kg);
+    const uint4 qv = *reinterpret_cast<const uint4*>(q + DecK<HD>::sub() * 8);
+    k.scores(L, base, qv, score_mult, score_shift, z);
 }
 
 // Exp-table entries a P.V block can hold in LDS (8 KB).

@@ -176,6 +176,49 @@ def test_batch_decode_greedy_lock_step(backend):
         assert [int(t) for t in toks[:, s]] == exp, s
 
 
+@pytest.mark.parametrize("hd,heads,bias", [(64, 8, 1), (128, 14, 0), (64, 16, 1)])
+def test_batch_decode_rows_grouped_heads(backend, hd, heads, bias):
+    """Decode batches (one row per sequence) take the per-row attention
+    kernels when 4, 7 or 8 query heads share a KV head: sequences of 1, 63,
+    64, 257 and 300 positions (chunk and range edges), one decode row each,
+    then lock-step greedy steps; logits, tokens and KV cache equal each
+    sequence's own forward_token run."""
+    spec = dict(seed=5, vocab=1000, hidden=heads * hd, layers=2, heads=heads, kv_heads=2, head_dim=hd, inter=320,
+                max_pos=640, lm_head_int16=0, attention_bias=bias)
+    case(f"batch decode rows {spec}")
+    gm, om = build(backend, spec)
+    r = np.random.default_rng(hd + heads)
+    lens = [1, 63, 64, 257, 300]
+    toks = [r.integers(0, spec["vocab"], n + 1) for n in lens]
+    S = len(lens)
+    gm.batch_begin(S)
+    rows = [(s, p) for s, n in enumerate(lens) for p in range(n)]
+    gm.forward_batch([s for s, _ in rows], [p for _, p in rows], [int(toks[s][p]) for s, p in rows],
+                     want_logits=False)
+    logits, am = gm.forward_batch(list(range(S)), lens, [int(toks[s][n]) for s, n in enumerate(lens)])
+    first = []
+    for s, n in enumerate(lens):
+        om.reset()
+        for p in range(n + 1):
+            ref = om.forward_token(int(toks[s][p]), p)
+        assert np.array_equal(logits[s], ref), ("decode row", s, n)
+        first.append(int(np.argmax(ref)))
+    assert [int(a) for a in am] == first
+    steps = 5
+    out = gm.batch_decode_greedy(range(S), [n + 1 for n in lens], first, steps)
+    for s, n in enumerate(lens):
+        om.reset()
+        for p in range(n + 1):
+            logits_o = om.forward_token(int(toks[s][p]), p)
+        nxt, exp = int(np.argmax(logits_o)), []
+        for i in range(steps):
+            logits_o = om.forward_token(nxt, n + 1 + i)
+            nxt = int(np.argmax(logits_o))
+            exp.append(nxt)
+        assert [int(t) for t in out[:, s]] == exp, s
+        compare_batch_kv(gm, om, spec, s, list(toks[s][:n + 1]) + [first[s]] + exp[:-1])
+
+
 def test_logsoftmax_dev(backend, oracle):
     import torch
     from myelith_amd.luts import exp_lut
