@@ -553,15 +553,33 @@ struct EpiHead {
 // decode attention over the KV cache (attention.rs:42-90), GQA (model.rs:508-511)
 // ---------------------------------------------------------------------------
 
-// Launch shape shared by the two attention kernels: grid
-// dim3(8 * G, ceil(chunks / 8), kv_heads), 256 threads; block (x, y, z) works
-// on query head x >> 3 of KV head z and on position chunk y * 8 + (x & 7).
-// Workgroups are dispatched to the 8 XCDs round robin in linear-id order (x
-// fastest, and gridDim.x is a multiple of 8), so the G head blocks of one
-// chunk run on one XCD and share its L2 copy of the K or V rows.
+// Launch shape shared by the two attention kernels, 256 threads.  Workgroups
+// are dispatched to the 8 XCDs round robin in linear-id order, and each XCD
+// has its own L2.  With kv_heads dividing 8 (xs_log = log2(8 / kv_heads)):
+// grid 8 * G * ceil(chunks / 2^xs_log); block x, with k = x >> 3 (the XCD's
+// k-th block), works on query head k % G of KV head (x & 7) >> xs_log and on
+// position chunk (k / G) 2^xs_log + (x & (2^xs_log - 1)), so each KV head's
+// chunks stay on its 2^xs_log XCDs and the G heads of a chunk run there
+// back to back: a chunk's K or V rows are read into one L2 for the heads that
+// share them, and a head's score row into 2^xs_log L2s rather than all 8.
+// Otherwise (xs_log < 0): grid dim3(8 * G, ceil(chunks / 8),
+// kv_heads); block (x, y, z) works on query head x >> 3 of KV head z and on
+// chunk y * 8 + (x & 7), the G head blocks of a chunk on one XCD.
 struct AttnBlock {
     int h, c, g;
-    __device__ AttnBlock() : h((int)blockIdx.x >> 3), c((int)blockIdx.y * 8 + ((int)blockIdx.x & 7)), g((int)blockIdx.z) {}
+    __device__ AttnBlock(int xs_log, int G, uint32_t ginv) {
+        if (xs_log >= 0) {
+            const int xcd = (int)blockIdx.x & 7, k = (int)blockIdx.x >> 3;
+            const int cc = (int)(((uint64_t)(uint32_t)k * ginv) >> 24);  // k / G: ginv = ceil(2^24 / G), k G < 2^24
+            h = k - cc * G;
+            g = xcd >> xs_log;
+            c = (cc << xs_log) + (xcd & ((1 << xs_log) - 1));
+        } else {
+            h = (int)blockIdx.x >> 3;
+            c = (int)blockIdx.y * 8 + ((int)blockIdx.x & 7);
+            g = (int)blockIdx.z;
+        }
+    }
 };
 
 template <int HD>
@@ -569,8 +587,8 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(const DecodeState* __r
                                                          const int16_t* __restrict__ q, const int16_t* __restrict__ kc,
                                                          int max_pos, int G, int chunks, int64_t score_mult,
                                                          uint8_t score_shift, int32_t* __restrict__ scores,
-                                                         int score_ld) {
-    const AttnBlock b;
+                                                         int score_ld, int xs_log, uint32_t ginv) {
+    const AttnBlock b(xs_log, G, ginv);
     if (b.c >= chunks) return;
     const int L = st->pos + 1;
     const int base = b.c * kChunk;
@@ -586,8 +604,9 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(const DecodeState* __restr
                                                      const int16_t* __restrict__ vc, int max_pos, int score_ld, int G,
                                                      int chunks, const int16_t* __restrict__ lut, uint32_t lut_len,
                                                      uint8_t lut_shift, int exp_lds,
-                                                     unsigned long long* __restrict__ acc) {
-    const AttnBlock b;
+                                                     unsigned long long* __restrict__ acc, int xs_log,
+                                                     uint32_t ginv) {
+    const AttnBlock b(xs_log, G, ginv);
     if (b.c >= chunks) return;
     const int L = st->pos + 1;
     const int base = b.c * kChunk;
@@ -1019,18 +1038,26 @@ hipError_t layer_step(myl_model* m, int l) {
         const int chunks = (m->max_pos + kChunk - 1) / kChunk;
         const int16_t* kc = m->kcache + layer_kv;
         const int16_t* vc = m->vcache + layer_kv;
-        const dim3 agrid(8 * G, (chunks + 7) / 8, kvh);
+        int xs_log = -1;  // AttnBlock
+        if (kvh <= 8 && 8 % kvh == 0)
+            for (xs_log = 0; (kvh << xs_log) < 8;) ++xs_log;
+        if (xs_log >= 0 && (int64_t)G * G * ((chunks + (1 << xs_log) - 1) >> xs_log) >= (1 << 24)) xs_log = -1;
+        const uint32_t ginv = ((1u << 24) + (uint32_t)G - 1) / (uint32_t)G;
+        const dim3 agrid = xs_log >= 0 ? dim3(8 * G * ((chunks + (1 << xs_log) - 1) >> xs_log))
+                                       : dim3(8 * G, (chunks + 7) / 8, kvh);
         const int exp_lds = m->exp_nz <= kDecExpLds ? m->exp_nz : -1;
         if (hd == 128) {
             attn_scores_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, chunks, m->score_mult,
-                                                          score_shift, m->scores, m->score_ld);
+                                                          score_shift, m->scores, m->score_ld, xs_log, ginv);
             attn_pv_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G, chunks,
-                                                      m->exp_lut, (uint32_t)m->exp_len, lut_shift, exp_lds, m->attn_acc);
+                                                      m->exp_lut, (uint32_t)m->exp_len, lut_shift, exp_lds, m->attn_acc,
+                                                      xs_log, ginv);
         } else {
             attn_scores_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, chunks, m->score_mult,
-                                                         score_shift, m->scores, m->score_ld);
+                                                         score_shift, m->scores, m->score_ld, xs_log, ginv);
             attn_pv_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G, chunks,
-                                                     m->exp_lut, (uint32_t)m->exp_len, lut_shift, exp_lds, m->attn_acc);
+                                                     m->exp_lut, (uint32_t)m->exp_len, lut_shift, exp_lds, m->attn_acc,
+                                                     xs_log, ginv);
         }
         e = hipGetLastError();
         if (e != hipSuccess) return e;

@@ -52,6 +52,21 @@ def test_tiny_forward_parity(backend, hd, lm16, bias, kvh):
     compare_kv(gm, om, spec, len(toks))
 
 
+@pytest.mark.parametrize("heads,kvh", [(6, 3), (16, 16)])
+def test_decode_kv_heads_not_dividing_eight(backend, heads, kvh):
+    """KV-head counts that do not divide the 8 XCDs take the attention's
+    three-dimensional launch shape (and 16 KV heads with one query head
+    each): 200 positions, logits and KV cache equal the oracle's."""
+    spec = dict(seed=9, vocab=1000, hidden=heads * 64, layers=2, heads=heads, kv_heads=kvh, head_dim=64, inter=320,
+                max_pos=256, lm_head_int16=0, attention_bias=1)
+    case(f"decode kv heads {spec}")
+    gm, om = build(backend, spec)
+    toks = np.random.default_rng(heads + kvh).integers(0, spec["vocab"], 200)
+    for pos, t in enumerate(toks):
+        assert np.array_equal(gm.forward_token(int(t), pos), om.forward_token(int(t), pos)), pos
+    compare_kv(gm, om, spec, len(toks))
+
+
 def test_device_weights_match_the_synthetic_definition(backend):
     spec = tiny(64, 1, 1, 2)
     case("device-generated weights")
