@@ -97,6 +97,17 @@ inline bool mm_planes_ok(int M, int K, const MmCtx* mm) {
            mm_env("MYL_MM_TILE") < 0;
 }
 
+// Row tiles per group of the tile order of 256 x 256 tiles (TileOrder): the
+// 32 blocks an XCD runs at one time cover 4 row tiles x 8 weight tiles.
+// MYL_MM_GROUP overrides it for sweeps (0: the plain order).
+inline int mm_group() {
+    static const int g = [] {
+        const int v = mm_env("MYL_MM_GROUP");
+        return v >= 0 ? v : 4;
+    }();
+    return g;
+}
+
 // Whether 256 x 256 tiles with 128-byte K stages fill the chip well enough
 // (mm_planes).
 inline bool mm_wide_tiles(int M, int N, int K, int cus) {
@@ -132,7 +143,7 @@ inline hipError_t mm_planes(const int8_t* Ap, int M, const int8_t* W, int N, int
     if (M <= 32 && K % 128 == 0) return mm2_launch_splitk<2, 1, 1, 4, 2, 128>(Ap, M, W, N, K, epi, mm, 2 * cus, st);
     if (M <= 32) return mm2_launch_splitk<2, 1, 1, 4, 4>(Ap, M, W, N, K, epi, mm, cus, st);
     if (M <= 64 && K % 128 == 0) return mm2_launch_splitk<1, 1, 4, 2, 3, 128>(Ap, M, W, N, K, epi, mm, cus, st);
-    if (M > 64 && mm_wide_tiles(M, N, K, cus)) return mm2_launch<2, 2, 4, 4, 2, 128>(Ap, M, W, N, K, epi, st);
+    if (M > 64 && mm_wide_tiles(M, N, K, cus)) return mm2_launch<2, 2, 4, 4, 2, 128>(Ap, M, W, N, K, epi, st, mm_group());
     if (M > 64 && mm2_tiles<2, 2, 4, 2, 3>(M, N) >= cus) return mm2_launch<2, 2, 4, 2, 3>(Ap, M, W, N, K, epi, st);
     return mm2_launch_splitk<2, 1, 2, 4, 4>(Ap, M, W, N, K, epi, mm, cus / 2, st);
 }
@@ -173,7 +184,7 @@ inline hipError_t mm_planes_staged(const int8_t* Ap, int M, const int8_t* W, int
     if (M <= 16) return mm2_staged_launch<1, 1, 1, 2, 4, 128>(Ap, M, W, N, K, epi, st);
     if (M <= 32) return mm2_staged_launch<2, 1, 1, 2, 4, 128>(Ap, M, W, N, K, epi, st);
     if (M <= 64) return mm2_staged_launch<2, 1, 2, 2, 4, 128>(Ap, M, W, N, K, epi, st);
-    if (mm_wide_tiles(M, N, K, mm->cus)) return mm2_staged_launch<2, 2, 4, 4, 2, 128>(Ap, M, W, N, K, epi, st);
+    if (mm_wide_tiles(M, N, K, mm->cus)) return mm2_staged_launch<2, 2, 4, 4, 2, 128>(Ap, M, W, N, K, epi, st, mm_group());
     return mm2_staged_launch<2, 2, 4, 2, 3, 64>(Ap, M, W, N, K, epi, st);
 }
 

@@ -70,6 +70,33 @@ struct Mm2 {
     __device__ static int slot(int row, int chunk) { return chunk ^ ((row / kSwzRows) & (kCpr - 1)); }
 };
 
+// Order of a product's output tiles over the grid.  mm_tile_index gives each
+// XCD a contiguous range of tile numbers; here tile numbers run over groups
+// of G row tiles (the row-tile count padded to a multiple of G, padding
+// tiles exit at once), the row tile fastest inside a group.  G = tiles_r is
+// the plain order (all row tiles of one weight tile, then the next weight
+// tile): the blocks an XCD runs at one time share one weight tile and read
+// as many distinct A' tiles.  A small G makes them cover G row tiles x
+// (blocks / G) weight tiles, so both operands are shared in the XCD's L2.
+struct TileOrder {
+    Divider span;  // G * tiles_n
+    Divider g;     // G
+    uint32_t tiles_r;
+    static TileOrder of(int tiles_r, int tiles_n, int G) {
+        if (G < 1 || G > tiles_r) G = tiles_r;
+        return TileOrder{Divider::of((uint32_t)(G * tiles_n)), Divider::of((uint32_t)G), (uint32_t)tiles_r};
+    }
+    // tile numbers the grid must cover
+    int count(int tiles_n) const { return (int)(((tiles_r + g.d - 1) / g.d) * g.d) * tiles_n; }
+    __device__ inline bool decode(uint32_t t, uint32_t& tn, uint32_t& tr) const {
+        uint32_t grp, in, r;
+        span.divmod(t, grp, in);
+        g.divmod(in, tn, r);
+        tr = grp * g.d + r;
+        return tr < tiles_r;
+    }
+};
+
 // LDS layout of a stage: BR A' rows then BN weight rows, KS bytes each, the
 // chunks of each row at Mm2::slot.
 // The pipelined main loop: acc[i][j] = A' tile i x W tile j over K in
@@ -185,13 +212,13 @@ __device__ inline void mm2_tile(const int8_t* __restrict__ Ap, int R2, const int
 
 template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class Epi>
 __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_kernel(const int8_t* __restrict__ Ap, int R2, const int8_t* __restrict__ W,
-                                                             int N, int K, Divider tiles_r, int ntiles, Epi epi) {
+                                                             int N, int K, TileOrder ord, int ntiles, Epi epi) {
     using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     extern __shared__ __align__(16) int8_t lds[];
     const int t = mm_tile_index(ntiles);
     if (t < 0) return;
     uint32_t tn, tr;
-    tiles_r.divmod((uint32_t)t, tn, tr);
+    if (!ord.decode((uint32_t)t, tn, tr)) return;
     mm2_tile<MB, NB, WM_, WN_, STAGES, KS>(Ap, R2, W, N, K, 0, K, (int)tr * S::BR, (int)tn * S::BN, lds, SinkEpi<Epi>{epi});
 }
 
@@ -205,14 +232,14 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_kernel(const int8_t* __res
 template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class Epi>
 __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_staged_kernel(const int8_t* __restrict__ Ap, int R2,
                                                                     const int8_t* __restrict__ W, int N, int K,
-                                                                    Divider tiles_r, int ntiles, Epi epi) {
+                                                                    TileOrder ord, int ntiles, Epi epi) {
     using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     static_assert((size_t)(S::BR / 2) * S::BN * 2 <= S::kLds, "staged tile fits the stage buffers");
     extern __shared__ __align__(16) int8_t lds[];
     const int t = mm_tile_index(ntiles);
     if (t < 0) return;
     uint32_t tn, tr;
-    tiles_r.divmod((uint32_t)t, tn, tr);
+    if (!ord.decode((uint32_t)t, tn, tr)) return;
     const int r0 = (int)tr * S::BR, n0 = (int)tn * S::BN;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -251,15 +278,19 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_staged_kernel(const int8_t
     }
 }
 
+// group: row tiles per group of the tile order (TileOrder; 0: the plain order).
 template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class Epi>
-hipError_t mm2_staged_launch(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, hipStream_t st) {
+hipError_t mm2_staged_launch(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, hipStream_t st,
+                             int group = 0) {
     using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     const int R2 = 2 * M;
-    const int tiles_r = (R2 + S::BR - 1) / S::BR, ntiles = tiles_r * ((N + S::BN - 1) / S::BN);
+    const int tiles_r = (R2 + S::BR - 1) / S::BR, tiles_n = (N + S::BN - 1) / S::BN;
+    const TileOrder ord = TileOrder::of(tiles_r, tiles_n, group);
+    const int ntiles = ord.count(tiles_n);
     auto kern = mm2_staged_kernel<MB, NB, WM_, WN_, STAGES, KS, Epi>;
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
     if (e != hipSuccess) return e;
-    kern<<<8 * ((ntiles + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, R2, W, N, K, Divider::of((uint32_t)tiles_r), ntiles, epi);
+    kern<<<8 * ((ntiles + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, R2, W, N, K, ord, ntiles, epi);
     return hipGetLastError();
 }
 
@@ -305,14 +336,14 @@ template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class Epi>
 __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2w16_kernel(const int8_t* __restrict__ Ap, int R2,
                                                                 const int8_t* __restrict__ Wp, int N2, int K,
                                                                 const int32_t* __restrict__ xsum,
-                                                                const int32_t* __restrict__ wsum, Divider tiles_r,
+                                                                const int32_t* __restrict__ wsum, TileOrder ord,
                                                                 int ntiles, Epi epi) {
     using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     extern __shared__ __align__(16) int8_t lds[];
     const int t = mm_tile_index(ntiles);
     if (t < 0) return;
     uint32_t tn, tr;
-    tiles_r.divmod((uint32_t)t, tn, tr);
+    if (!ord.decode((uint32_t)t, tn, tr)) return;
     mm2w16_tile<MB, NB, WM_, WN_, STAGES, KS>(Ap, R2, Wp, N2, K, xsum, wsum, (int)tr * S::BR, (int)tn * S::BN, lds,
                                           SinkEpi<Epi>{epi});
 }
@@ -354,15 +385,16 @@ inline hipError_t split_planes_sum(const int16_t* x, int M, int ldx, int K, int8
 // at least four tiles per CU (and K % 128 == 0), else 256 x 128 tiles.
 template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class Epi>
 hipError_t mm2w16_launch_cfg(const int8_t* Ap, const int32_t* xsum, int M, const int8_t* Wp, const int32_t* wsum,
-                             int N, int K, const Epi& epi, hipStream_t st) {
+                             int N, int K, const Epi& epi, hipStream_t st, int group = 0) {
     using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     const int R2 = 2 * M, N2 = 2 * N;
-    const int tiles_r = (R2 + S::BR - 1) / S::BR, ntiles = tiles_r * ((N2 + S::BN - 1) / S::BN);
+    const int tiles_r = (R2 + S::BR - 1) / S::BR, tiles_n = (N2 + S::BN - 1) / S::BN;
+    const TileOrder ord = TileOrder::of(tiles_r, tiles_n, group);
+    const int ntiles = ord.count(tiles_n);
     auto kern = mm2w16_kernel<MB, NB, WM_, WN_, STAGES, KS, Epi>;
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
     if (e != hipSuccess) return e;
-    kern<<<8 * ((ntiles + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, R2, Wp, N2, K, xsum, wsum,
-                                                              Divider::of((uint32_t)tiles_r), ntiles, epi);
+    kern<<<8 * ((ntiles + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, R2, Wp, N2, K, xsum, wsum, ord, ntiles, epi);
     return hipGetLastError();
 }
 
@@ -406,16 +438,19 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_splitk_kernel(const int8_t
 
 // K % KS == 0.
 template <int MB, int NB, int WM_, int WN_, int STAGES, int KS = 64, class Epi>
-hipError_t mm2_launch(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, hipStream_t st) {
+hipError_t mm2_launch(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, hipStream_t st,
+                      int group = 0) {
     using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     const int R2 = 2 * M;
-    const int tiles_r = (R2 + S::BR - 1) / S::BR, ntiles = tiles_r * ((N + S::BN - 1) / S::BN);
+    const int tiles_r = (R2 + S::BR - 1) / S::BR, tiles_n = (N + S::BN - 1) / S::BN;
+    const TileOrder ord = TileOrder::of(tiles_r, tiles_n, group);
+    const int ntiles = ord.count(tiles_n);
     auto kern = mm2_kernel<MB, NB, WM_, WN_, STAGES, KS, Epi>;
     if (S::kLds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
         if (e != hipSuccess) return e;
     }
-    kern<<<8 * ((ntiles + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, R2, W, N, K, Divider::of((uint32_t)tiles_r), ntiles, epi);
+    kern<<<8 * ((ntiles + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, R2, W, N, K, ord, ntiles, epi);
     return hipGetLastError();
 }
 
