@@ -80,6 +80,40 @@ def class_bytes(spec: dict) -> dict:
     }
 
 
+def _graph_time(backend, launch, replays):
+    """ms per replay of a HIP graph holding what launch() enqueues through the
+    library (captured on a side stream the library is pointed at), or None
+    when the capture is refused.  The library's stream is restored."""
+    import torch
+    prev = torch.cuda.current_stream()
+    cap = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    try:
+        torch.cuda.synchronize()
+        torch.cuda.set_stream(cap)
+        backend.use_torch_stream()
+        with torch.cuda.graph(g, stream=cap):
+            launch()
+        torch.cuda.set_stream(prev)
+        backend.use_torch_stream()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / replays
+    except RuntimeError as exc:
+        log(f"graph capture refused ({exc}); timing eager launches")
+        torch.cuda.set_stream(prev)
+        backend.use_torch_stream()
+        return None
+    finally:
+        del g
+
+
 def w8a16_sweep(backend, shapes, ms=(1, 8, 64, 512), target_bytes=6 << 30, target_ops=4e12):
     """The isolated W8A16 matmul sweep with multiplier requant: y = clamp16(RNE(W.x * mult, shift)).
     Algorithmic bytes N*K + 2MK + 2MN + 5N (i32 mult + u8 shift), ops 2MNK.
@@ -103,18 +137,32 @@ def w8a16_sweep(backend, shapes, ms=(1, 8, 64, 512), target_bytes=6 << 30, targe
             for W in Ws[:nc]:  # warm-up
                 backend.linear_w8a16_mult_dev(x, W, mult, sh, out=y)
             launches = max(nc, int(min(target_bytes // per, target_ops // (2 * M * per))) // nc * nc)
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for i in range(launches):
-                backend.linear_w8a16_mult_dev(x, Ws[i % nc], mult, sh, out=y)
-            e1.record()
-            torch.cuda.synchronize()
-            ms_ = e0.elapsed_time(e1) / launches
+            # The short products take about as long as a Python call through
+            # ctypes, so eagerly launched ones would be timed at the host's
+            # pace: at least 16 launches (whole passes over the weight copies)
+            # are captured as a HIP graph and replayed, events around the
+            # replays.  Eager launches if the capture is refused.
+            per_graph = nc * max(1, 16 // nc)
+            method = f"HIP graph of {per_graph} launches over the weight copies, replayed; events around the replays"
+            ms_ = _graph_time(backend, lambda: [backend.linear_w8a16_mult_dev(x, Ws[i % nc], mult, sh, out=y)
+                                                for i in range(per_graph)], max(1, launches // per_graph))
+            if ms_ is not None:
+                ms_ /= per_graph
+                launches = per_graph * max(1, launches // per_graph)
+            else:
+                method = "eager launches from Python, events around the loop"
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for i in range(launches):
+                    backend.linear_w8a16_mult_dev(x, Ws[i % nc], mult, sh, out=y)
+                e1.record()
+                torch.cuda.synchronize()
+                ms_ = e0.elapsed_time(e1) / launches
             nbytes = per + 2 * M * K + 2 * M * N + 5 * N
             rec = {"us": round(ms_ * 1e3, 2), "GBps": round(nbytes / (ms_ * 1e-3) / 1e9, 1),
                    "TOPs": round(2 * M * per / (ms_ * 1e-3) / 1e12, 1), "bytes": nbytes, "launches": launches,
-                   "distinct_weight_MB": round(nc * per / 2**20)}
+                   "distinct_weight_MB": round(nc * per / 2**20), "method": method}
             out[f"M{M}_N{N}_K{K}"] = rec
             log(f"w8a16 M={M} N={N} K={K}: {rec['us']} us, {rec['GBps']} GB/s, {rec['TOPs']} TOP/s")
             del x, y

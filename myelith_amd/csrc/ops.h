@@ -167,6 +167,18 @@ __device__ inline RmsFactor rms_factor(const int16_t* x, const uint8_t* xs, int 
     return rms_factor_of(acc, ref, p);
 }
 
+// RNE(v / 2^s) for 0 <= s <= 62 and |v| < 2^62, equal to rshift_round64 there:
+// with v = q 2^s + r (0 <= r < 2^s), adding 2^(s-1) - 1 plus q's lowest bit
+// carries into q exactly when r is above one half, or equal to it with q odd.
+// About a quarter of rshift_round64's instructions (no remainder compares,
+// no shift-range selects): the normalisation of a whole activation vector in
+// every block of the decode products runs it per element.
+MYL_FN int64_t rne_shift64_small(int64_t v, uint32_t s) {
+    const int64_t lsb = (v >> s) & 1;
+    const int64_t half = (int64_t)((1ull << s) >> 1);
+    return (v + (s ? half - 1 + lsb : 0)) >> s;
+}
+
 // Per-channel output of rmsnorm.rs:130-159.  |x * lut * gamma| < 2^37, so for
 // 0 <= shift <= 62 and for left shifts up to 25 bits the i64 computation is the
 // i128 one bit for bit; other shifts take the i128 path.
@@ -176,7 +188,8 @@ __device__ inline int16_t rms_out(int16_t x, uint8_t xs, int8_t g, uint8_t gs, c
     const int32_t shift = total - (int32_t)out_frac;
     // |x * g| < 2^22 and the LUT value is an int16: one 32 x 32 -> 64 product
     const int64_t p64 = (int64_t)((int32_t)x * (int32_t)g) * (int64_t)(int32_t)f.lut_val;
-    if (shift >= 0 && shift <= 62) return clamp_i16_i64(clamp_i32_i64(rshift_round64(p64, (uint8_t)shift)));
+    // clamp to i32 then to i16 is the clamp to i16
+    if (shift >= 0 && shift <= 62) return clamp_i16_i64(rne_shift64_small(p64, (uint32_t)shift));
     if (shift < 0 && shift >= -25) return clamp_i16_i64(clamp_i32_i64(p64 << (-shift)));
     const myl_i128 prod = (myl_i128)p64;
     const myl_i128 s = shift >= 0 ? rshift_round128(prod, (uint32_t)shift) : shl128(prod, (uint32_t)(-shift));

@@ -164,3 +164,60 @@ def test_rsqrt_closed_form_equals_the_table(tmp_path):
         want = rsqrt_lut(n - 1, shift, frac).astype(np.int64)
         bad = np.nonzero(got != want)[0]
         assert bad.size == 0, (frac, shift, bad[:10], got[bad[:10]], want[bad[:10]])
+
+
+RNE_SRC = r"""
+#include <hip/hip_runtime.h>
+#include <cstdio>
+#include <cstdint>
+#include "ops.h"
+int main() {
+    long bad = 0, n = 0;
+    auto check = [&](int64_t v, uint32_t s) {
+        ++n;
+        const int64_t a = myl::rne_shift64_small(v, s), b = rshift_round64(v, (uint8_t)s);
+        if (a != b && bad++ < 10) printf("v=%lld s=%u fast=%lld general=%lld\n", (long long)v, s, (long long)a, (long long)b);
+    };
+    const int64_t lim = (1ll << 62) - 1;
+    uint64_t z = 0x9E3779B97F4A7C15ull;
+    auto next = [&]() { z ^= z << 13; z ^= z >> 7; z ^= z << 17; return z; };
+    for (uint32_t s = 0; s <= 62; ++s) {
+        const int64_t half = s ? (1ll << (s - 1)) : 0;
+        for (int64_t v : {(int64_t)0, (int64_t)1, (int64_t)-1, (int64_t)2, (int64_t)-2, (int64_t)3, (int64_t)-3, lim, -lim, lim - 1, -lim + 1}) check(v, s);
+        for (int i = 0; i < 20000; ++i) {
+            // ties and their neighbours: v = q 2^s + 2^(s-1) + d for q of either sign
+            // |q| < 2^(61 - s) keeps |v| below 2^62
+            const uint64_t qmax = s < 61 ? (1ull << (61 - s)) : 1ull;
+            const int64_t q = (int64_t)(next() % qmax) * ((next() & 1) ? 1 : -1);
+            const int64_t base = q * (int64_t)(1ull << s);
+            for (int64_t d = -1; d <= 1; ++d) {
+                const int64_t v = base + half + d;
+                if (v <= lim && v >= -lim) check(v, s);
+            }
+            const int64_t r = (int64_t)(next() >> 2) * ((next() & 1) ? 1 : -1);  // |r| < 2^62
+            check(r, s);
+            check(r >> (next() % 62), s);
+        }
+    }
+    printf("checked %ld, mismatches %ld\n", n, bad);
+    return bad != 0;
+}
+"""
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not Path("/opt/rocm/bin/hipcc").exists(), reason="hipcc absent")
+def test_rne_shift64_small_matches_rshift_round64(tmp_path):
+    """The short round-half-even shift of the norm outputs (rms_out) equals
+    rshift_round64 (fixed_point.rs:140-153) for every shift 0..62 on values
+    below 2^62: ties of both signs and their neighbours, random values of
+    every magnitude, the range ends."""
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    src = tmp_path / "n.hip"
+    src.write_text(RNE_SRC)
+    exe = tmp_path / "n"
+    subprocess.run([hipcc, "-O2", "-std=c++17", "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang",
+                    "-packed-fp32-ops", "-I", str(ROOT / "myelith_amd" / "csrc"), "-I", str(ROOT / "include"),
+                    str(src), "-o", str(exe)], check=True, capture_output=True, timeout=300)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout
+    assert "mismatches 0" in r.stdout
