@@ -436,6 +436,50 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_splitk_kernel(const int8_t
                                            SinkAtomic{acc, N});
 }
 
+// Grouped products (MoE experts): work item t = (expert e, token tile m0,
+// weight tile n0) of the work table; expert e's rows are the byte-plane rows
+// [2 offsets[e], 2 offsets[e+1]) of Ap and its weights W + e * w_stride
+// [N x K].  The epilogue receives (e, n, row, sum) with row the activation
+// row in Ap's token order (SinkGrouped).  K % KS == 0.
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class EpiG>
+__global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_grouped_kernel(const int8_t* __restrict__ Ap,
+                                                                     const int8_t* __restrict__ W, size_t w_stride,
+                                                                     int N, int K, const int* __restrict__ offsets,
+                                                                     const MmWork* __restrict__ work, int nwork,
+                                                                     EpiG epi) {
+    extern __shared__ __align__(16) int8_t lds[];
+    const int t = mm_tile_index(nwork);
+    if (t < 0) return;
+    const MmWork wk = work[t];
+    const int row0 = offsets[wk.e];
+    const int Me = offsets[wk.e + 1] - row0;
+    mm2_tile<MB, NB, WM_, WN_, STAGES, KS>(Ap + (size_t)2 * row0 * K, 2 * Me, W + (size_t)wk.e * w_stride, N, K, 0, K,
+                                           2 * wk.m0, wk.n0, lds, SinkGrouped<EpiG>{epi, wk.e, row0});
+}
+
+// Token rows and weight rows of one grouped work item (for the work table).
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS>
+struct Mm2GroupedShape {
+    using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
+    static constexpr int kTokens = S::BR / 2;
+    static constexpr int kRows = S::BN;
+};
+
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class EpiG>
+hipError_t mm2_grouped_launch(const int8_t* Ap, const int8_t* W, size_t w_stride, int N, int K, const int* offsets,
+                              const MmWork* work, int nwork, const EpiG& epi, hipStream_t st) {
+    using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
+    if (K % KS != 0) return hipErrorInvalidValue;
+    if (nwork <= 0) return hipSuccess;
+    auto kern = mm2_grouped_kernel<MB, NB, WM_, WN_, STAGES, KS, EpiG>;
+    if (S::kLds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
+        if (e != hipSuccess) return e;
+    }
+    kern<<<8 * ((nwork + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, W, w_stride, N, K, offsets, work, nwork, epi);
+    return hipGetLastError();
+}
+
 // K % KS == 0.
 template <int MB, int NB, int WM_, int WN_, int STAGES, int KS = 64, class Epi>
 hipError_t mm2_launch(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi, hipStream_t st,

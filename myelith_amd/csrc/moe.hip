@@ -214,6 +214,42 @@ __global__ __launch_bounds__(256) void moe_gather_kernel(const int16_t* __restri
     for (int i = threadIdx.x; i < H / 8; i += 256) dst[i] = src[i];
 }
 
+// moe_gather_kernel writing byte planes [2R x H] (rows 2p = hi, 2p + 1 = lo')
+// for the grouped byte-plane products.  H % 8 == 0.
+__global__ __launch_bounds__(256) void moe_gather_planes_kernel(const int16_t* __restrict__ x, int H,
+                                                                const int32_t* __restrict__ list_tok,
+                                                                int8_t* __restrict__ Xp) {
+    const int p = blockIdx.x;
+    const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)list_tok[p] * H);
+    int8_t* hi = Xp + (size_t)(2 * p) * H;
+    for (int i = threadIdx.x; i < H / 8; i += 256) {
+        uint2 h, l;
+        split_planes8(src[i], h, l);
+        *reinterpret_cast<uint2*>(hi + i * 8) = h;
+        *reinterpret_cast<uint2*>(hi + H + i * 8) = l;
+    }
+}
+
+__device__ inline int16_t moe_silu_one(uint32_t gu, const int16_t* __restrict__ silu, uint32_t silu_len) {
+    const int16_t g = (int16_t)(gu & 0xFFFFu), u = (int16_t)(gu >> 16);
+    const int32_t g_dom = rescale32((int32_t)g, MYL_MOE_GATE_FRAC, MYL_TV_SILU_IN_FRAC);
+    const int16_t act = lut_lookup_i16((int16_t)g_dom, silu, silu_len, (int16_t)MYL_TV_SILU_LUT_OFFSET);
+    const int64_t prod = (int64_t)act * (int64_t)u;
+    return clamp_i16_i64(rescale64(prod, (uint8_t)(MYL_TV_SILU_OUT_FRAC + MYL_MOE_UP_FRAC), MYL_MOE_DOWN_IN_FRAC));
+}
+
+// moe_silu_kernel writing byte planes [2R x I] of h for the grouped down product.
+__global__ __launch_bounds__(256) void moe_silu_planes_kernel(const int16_t* __restrict__ GU, int I,
+                                                              const int16_t* __restrict__ silu, uint32_t silu_len,
+                                                              int8_t* __restrict__ Hp) {
+    const int r = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= I) return;
+    const int32_t h = moe_silu_one(*reinterpret_cast<const uint32_t*>(GU + (size_t)r * 2 * I + 2 * i), silu, silu_len);
+    Hp[(size_t)(2 * r) * I + i] = (int8_t)(h >> 8);
+    Hp[(size_t)(2 * r + 1) * I + i] = (int8_t)((h & 255) - 128);
+}
+
 // mlp.rs:55-65 per row.
 __global__ __launch_bounds__(256) void moe_silu_kernel(const int16_t* __restrict__ GU, int I,
                                                        const int16_t* __restrict__ silu, uint32_t silu_len,
@@ -221,13 +257,8 @@ __global__ __launch_bounds__(256) void moe_silu_kernel(const int16_t* __restrict
     const int r = blockIdx.y;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= I) return;
-    const uint32_t gu = *reinterpret_cast<const uint32_t*>(GU + (size_t)r * 2 * I + 2 * i);
-    const int16_t g = (int16_t)(gu & 0xFFFFu), u = (int16_t)(gu >> 16);
-    const int32_t g_dom = rescale32((int32_t)g, MYL_MOE_GATE_FRAC, MYL_TV_SILU_IN_FRAC);
-    const int16_t act = lut_lookup_i16((int16_t)g_dom, silu, silu_len, (int16_t)MYL_TV_SILU_LUT_OFFSET);
-    const int64_t prod = (int64_t)act * (int64_t)u;
-    Hh[(size_t)r * I + i] = clamp_i16_i64(rescale64(prod, (uint8_t)(MYL_TV_SILU_OUT_FRAC + MYL_MOE_UP_FRAC),
-                                                    MYL_MOE_DOWN_IN_FRAC));
+    Hh[(size_t)r * I + i] = moe_silu_one(*reinterpret_cast<const uint32_t*>(GU + (size_t)r * 2 * I + 2 * i), silu,
+                                         silu_len);
 }
 
 // out = clamp_i16(RNE(sum_k g_k * y_k + 2^14 * s, 14)).  Grid (ceil(H / 256), T).
@@ -380,6 +411,34 @@ int ensure(myl_moe* m, int T) {
     return MYL_OK;
 }
 
+// Byte-plane tile of the grouped expert products: 0: 128 tokens x 256 weight
+// rows (16 waves, 128-byte stages), 1: 128 x 128 (8 waves, 64-byte stages),
+// 2: 64 x 128 (8 waves).  The whole 4096-token, 60-expert layer on MI355X
+// took 1.42, 1.49 and 1.58 ms with them (1.75 ms with the int16-row tiles of
+// mm_w8_grouped_kernel), so 0 when both K are multiples of 128.
+// MYL_MOE_TILE overrides the choice for sweeps.
+int moe_planes_tile(int H, int I) {
+    const bool k128 = H % 128 == 0 && I % 128 == 0;
+    const int v = mm_env("MYL_MOE_TILE");
+    if (v >= 0 && v <= 2) return (v == 0 && !k128) ? 1 : v;
+    return k128 ? 0 : 1;
+}
+int moe_tile_tokens(int tile) {
+    return tile == 0 ? Mm2GroupedShape<2, 2, 4, 4, 2, 128>::kTokens
+                     : tile == 1 ? Mm2GroupedShape<2, 2, 4, 2, 3, 64>::kTokens : Mm2GroupedShape<2, 1, 2, 4, 4, 64>::kTokens;
+}
+int moe_tile_rows(int tile) {
+    return tile == 0 ? Mm2GroupedShape<2, 2, 4, 4, 2, 128>::kRows
+                     : tile == 1 ? Mm2GroupedShape<2, 2, 4, 2, 3, 64>::kRows : Mm2GroupedShape<2, 1, 2, 4, 4, 64>::kRows;
+}
+template <class EpiG>
+hipError_t moe_grouped(int tile, const int8_t* Ap, const int8_t* W, size_t w_stride, int N, int K, const int* offsets,
+                       const MmWork* work, int nwork, const EpiG& epi, hipStream_t st) {
+    if (tile == 0) return mm2_grouped_launch<2, 2, 4, 4, 2, 128>(Ap, W, w_stride, N, K, offsets, work, nwork, epi, st);
+    if (tile == 1) return mm2_grouped_launch<2, 2, 4, 2, 3, 64>(Ap, W, w_stride, N, K, offsets, work, nwork, epi, st);
+    return mm2_grouped_launch<2, 1, 2, 4, 4, 64>(Ap, W, w_stride, N, K, offsets, work, nwork, epi, st);
+}
+
 // Work table of a grouped product: (expert, m-tile, n-tile), m fastest.
 void work_table(const std::vector<int32_t>& counts, int bm, int bn, int N, std::vector<MmWork>& out) {
     out.clear();
@@ -459,11 +518,16 @@ int myl_moe_forward(myl_moe* m, const int16_t* x_dev, uint32_t n_tokens, int16_t
     if (rc) return rc;
     std::vector<int32_t> offs(E + 1, 0);
     for (int x = 0; x < E; ++x) offs[x + 1] = offs[x] + m->counts_host[x];
-    // grouped work tables: gate/up (N = 2I) and down (N = H), 64 x 128 tiles
+    // grouped work tables: gate/up (N = 2I) and down (N = H).  Both K (H, I)
+    // multiples of 64: byte-plane products (moe_planes_tile), else 64 x 128
+    // tiles of int16 rows
     using GT = MmShape<1, 2, 2, 2>;
+    const bool planes = H % 64 == 0 && I % 64 == 0;
+    const int tile = moe_planes_tile(H, I);
+    const int bm = planes ? moe_tile_tokens(tile) : GT::BM, bn = planes ? moe_tile_rows(tile) : GT::BN;
     std::vector<MmWork> wgu, wdn;
-    work_table(m->counts_host, GT::BM, GT::BN, 2 * I, wgu);
-    work_table(m->counts_host, GT::BM, GT::BN, H, wdn);
+    work_table(m->counts_host, bm, bn, 2 * I, wgu);
+    work_table(m->counts_host, bm, bn, H, wdn);
     const int need = (int)(wgu.size() + wdn.size());
     if (need > m->work_cap) {
         if (m->work) (void)hipFree(m->work);
@@ -480,9 +544,26 @@ int myl_moe_forward(myl_moe* m, const int16_t* x_dev, uint32_t n_tokens, int16_t
     // dispatch (stable), gather, grouped experts
     moe_dispatch_kernel<<<E, 256, 0, st>>>(m->ids, T, K, m->offsets, m->list_tok, m->slotpos);
     const int R = T * K;
-    moe_gather_kernel<<<R, 256, 0, st>>>(x_dev, H, m->list_tok, m->Xg);
-    if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe dispatch");
-    if (!wgu.empty()) {
+    if (planes) {
+        // the planes [2R x H] and [2R x I] take the bytes of Xg and Hh
+        int8_t* Xp = reinterpret_cast<int8_t*>(m->Xg);
+        int8_t* Hp = reinterpret_cast<int8_t*>(m->Hh);
+        moe_gather_planes_kernel<<<R, 256, 0, st>>>(x_dev, H, m->list_tok, Xp);
+        if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe dispatch");
+        EpiExpertGU eg{m->sgu, 2 * I, m->GU};
+        if ((e = moe_grouped(tile, Xp, m->wgu, (size_t)2 * I * H, 2 * I, H, m->offsets, m->work, (int)wgu.size(), eg,
+                             st)) != hipSuccess)
+            return c->hip(e, "moe gate/up");
+        moe_silu_planes_kernel<<<dim3((I + 255) / 256, R), 256, 0, st>>>(m->GU, I, m->silu, (uint32_t)m->silu_len, Hp);
+        EpiExpertDown ed{m->sd, m->out_frac, H, m->Y};
+        if ((e = moe_grouped(tile, Hp, m->wd, (size_t)H * I, H, I, m->offsets, m->work + wgu.size(), (int)wdn.size(),
+                             ed, st)) != hipSuccess)
+            return c->hip(e, "moe down");
+    } else {
+        moe_gather_kernel<<<R, 256, 0, st>>>(x_dev, H, m->list_tok, m->Xg);
+        if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe dispatch");
+    }
+    if (!planes && !wgu.empty()) {
         EpiExpertGU eg{m->sgu, 2 * I, m->GU};
         mm_w8_grouped_kernel<1, 2, 2, 2, EpiExpertGU><<<8 * (((int)wgu.size() + 7) / 8), GT::kThreads, GT::kLds, st>>>(
             m->Xg, H, m->wgu, (size_t)2 * I * H, 2 * I, H, m->offsets, m->work, (int)wgu.size(), eg);
