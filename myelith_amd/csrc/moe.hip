@@ -118,39 +118,43 @@ __global__ void moe_input_kernel(int16_t* __restrict__ x, size_t n, uint64_t tse
 // route: bias, top-k, gates, counts
 // ---------------------------------------------------------------------------
 
-// One thread per token.  E <= 256, K <= 16.
-__global__ __launch_bounds__(256) void moe_topk_kernel(const int32_t* __restrict__ logits, int T, int E, int K,
-                                                       const int32_t* __restrict__ bias,
-                                                       const int16_t* __restrict__ lut, uint32_t lut_len,
-                                                       int32_t* __restrict__ ids, int32_t* __restrict__ gates,
-                                                       int32_t* __restrict__ counts) {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= T) return;
-    const int32_t* z = logits + (size_t)t * E;
-    uint32_t taken[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    int32_t sel[16];
-    int sid[16];
-    for (int k = 0; k < K; ++k) {
-        int best = -1;
-        int32_t bv = INT32_MIN;
-        for (int e = 0; e < E; ++e) {
-            if (taken[e >> 5] & (1u << (e & 31))) continue;
+// The routing of token t by its wave (moe_topk_kernel).
+__device__ inline void moe_topk_token(const int32_t* __restrict__ z, int t, int E, int K,
+                                      const int32_t* __restrict__ bias, const int16_t* __restrict__ lut,
+                                      uint32_t lut_len, int32_t* __restrict__ ids, int32_t* __restrict__ gates,
+                                      int32_t* hist, int lane) {
+    uint64_t key[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        key[j] = 0;  // below every real key (their low words are >= 2^32 - 256)
+        if (e < E) {
             const int32_t v = clamp_i32_i64((int64_t)z[e] + (int64_t)bias[e]);
-            if (best < 0 || v > bv) { best = e; bv = v; }
+            key[j] = ((uint64_t)((uint32_t)v ^ 0x80000000u) << 32) | (0xFFFFFFFFu - (uint32_t)e);
         }
-        taken[best >> 5] |= 1u << (best & 31);
-        sel[k] = bv;
-        sid[k] = best;
     }
-    // softmax.rs:24-64 over the K selected logits (lut_shift 0, frac 14)
+    int32_t sel = 0;
+    int sid = 0;
+    for (int k = 0; k < K; ++k) {
+        const uint64_t b01 = key[0] > key[1] ? key[0] : key[1], b23 = key[2] > key[3] ? key[2] : key[3];
+        const uint64_t w = wave_max_u64(b01 > b23 ? b01 : b23);
+        const int e = (int)(0xFFFFFFFFu - (uint32_t)w);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (lane + 64 * j == e) key[j] = 0;
+        if (lane == k) {
+            sel = (int32_t)((uint32_t)(w >> 32) ^ 0x80000000u);
+            sid = e;
+        }
+    }
+    // softmax.rs:24-64 over the K selected logits (lut_shift 0, frac 14); the
+    // first choice is their maximum
     const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
     const int32_t lut_one = lut_len > 0 ? (int32_t)lut[0] : 1;
-    int32_t mx = sel[0];
-    for (int k = 1; k < K; ++k) mx = max(mx, sel[k]);
-    uint32_t s = 0;
-    for (int k = 0; k < K; ++k) s += (uint32_t)exp_lookup(sat_sub32(mx, sel[k]), lut, lut_len, 0, lut_one);
-    const int32_t S = (int32_t)s;
-    for (int k = 0; k < K; ++k) {
+    const int32_t mx = readlane_i32(sel, 0);
+    const int32_t ev = lane < K ? exp_lookup(sat_sub32(mx, sel), lut, lut_len, 0, lut_one) : 0;
+    const int32_t S = wave_sum_i32(ev);  // wrapping, as the reference's sum
+    if (lane < K) {
         int32_t g;
         if (S == 0) {
             const uint64_t rl = recip32((uint32_t)K);
@@ -158,18 +162,41 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const int32_t* __restrict
             udivmod32((uint32_t)one, (uint32_t)K, rl, &qq, &rr);
             const int32_t base = (int32_t)qq;
             const int32_t rem = wsub32(one, wmul32(base, K));
-            g = base + ((int64_t)k < (int64_t)rem ? 1 : 0);
+            g = base + ((int64_t)lane < (int64_t)rem ? 1 : 0);
         } else {
             const uint64_t rs = recip32(S < 0 ? 0u - (uint32_t)S : (uint32_t)S);
-            const int32_t e = exp_lookup(sat_sub32(mx, sel[k]), lut, lut_len, 0, lut_one);
-            g = softmax_div_round(wmul32(e, one), S, rs);
+            g = softmax_div_round(wmul32(ev, one), S, rs);
         }
-        ids[(size_t)t * K + k] = sid[k];
-        gates[(size_t)t * K + k] = g;
-        atomicAdd(counts + sid[k], 1);
+        ids[(size_t)t * K + lane] = sid;
+        gates[(size_t)t * K + lane] = g;
+        atomicAdd(hist + sid, 1);
     }
 }
 
+// One wave per token (16 per block).  E <= 256, K <= 16.  Lane l holds
+// experts l, l + 64, .. as keys (biased logit ^ 2^31) << 32 | (2^32 - 1 - e):
+// the larger key is the larger biased logit, then the lower expert index
+// (sampling.rs:8-18's first maximum), so each of the K rounds takes the
+// wave's largest key and retires it.  Lane k keeps the k-th choice and
+// computes its gate.  The block's choices are counted in LDS first, so a
+// popular expert's counter takes one global atomic per block, not one per
+// routed token (thousands on one address serialise).
+constexpr int kTopkWaves = 16;
+__global__ __launch_bounds__(kTopkWaves * 64) void moe_topk_kernel(const int32_t* __restrict__ logits, int T, int E, int K,
+                                                       const int32_t* __restrict__ bias,
+                                                       const int16_t* __restrict__ lut, uint32_t lut_len,
+                                                       int32_t* __restrict__ ids, int32_t* __restrict__ gates,
+                                                       int32_t* __restrict__ counts) {
+    __shared__ int32_t hist[256];
+    for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * kTopkWaves + (int)(threadIdx.x >> 6);
+    if (t < T) moe_topk_token(logits + (size_t)t * E, t, E, K, bias, lut, lut_len, ids, gates, hist, lane);
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x)
+        if (hist[e]) atomicAdd(counts + e, hist[e]);
+}
 // Stable dispatch: block e lists the tokens routed to expert e in ascending
 // token order at offsets[e].., and records each (token, slot)'s list position.
 __global__ __launch_bounds__(256) void moe_dispatch_kernel(const int32_t* __restrict__ ids, int T, int K,
@@ -238,43 +265,75 @@ __device__ inline int16_t moe_silu_one(uint32_t gu, const int16_t* __restrict__ 
     return clamp_i16_i64(rescale64(prod, (uint8_t)(MYL_TV_SILU_OUT_FRAC + MYL_MOE_UP_FRAC), MYL_MOE_DOWN_IN_FRAC));
 }
 
-// moe_silu_kernel writing byte planes [2R x I] of h for the grouped down product.
+// moe_silu_kernel writing byte planes [2R x I] of h for the grouped down
+// product: eight outputs per thread (I % 8 == 0), 16-byte loads and 8-byte
+// stores.  Grid (ceil(I / 2048), R).
 __global__ __launch_bounds__(256) void moe_silu_planes_kernel(const int16_t* __restrict__ GU, int I,
                                                               const int16_t* __restrict__ silu, uint32_t silu_len,
                                                               int8_t* __restrict__ Hp) {
     const int r = blockIdx.y;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= I) return;
-    const int32_t h = moe_silu_one(*reinterpret_cast<const uint32_t*>(GU + (size_t)r * 2 * I + 2 * i), silu, silu_len);
-    Hp[(size_t)(2 * r) * I + i] = (int8_t)(h >> 8);
-    Hp[(size_t)(2 * r + 1) * I + i] = (int8_t)((h & 255) - 128);
+    const int i0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (i0 >= I) return;
+    const uint4* src = reinterpret_cast<const uint4*>(GU + (size_t)r * 2 * I + 2 * i0);
+    const uint4 a = src[0], b = src[1];
+    const uint32_t gu[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t hw[2] = {0, 0}, lw[2] = {0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int32_t h = moe_silu_one(gu[j], silu, silu_len);
+        hw[j >> 2] |= ((uint32_t)(h >> 8) & 0xFFu) << (8 * (j & 3));
+        lw[j >> 2] |= ((uint32_t)((h & 255) - 128) & 0xFFu) << (8 * (j & 3));
+    }
+    *reinterpret_cast<uint2*>(Hp + (size_t)(2 * r) * I + i0) = make_uint2(hw[0], hw[1]);
+    *reinterpret_cast<uint2*>(Hp + (size_t)(2 * r + 1) * I + i0) = make_uint2(lw[0], lw[1]);
 }
 
-// mlp.rs:55-65 per row.
+// mlp.rs:55-65 per row, eight outputs per thread (I % 8 == 0).  Grid
+// (ceil(I / 2048), R).
 __global__ __launch_bounds__(256) void moe_silu_kernel(const int16_t* __restrict__ GU, int I,
                                                        const int16_t* __restrict__ silu, uint32_t silu_len,
                                                        int16_t* __restrict__ Hh) {
     const int r = blockIdx.y;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= I) return;
-    Hh[(size_t)r * I + i] = moe_silu_one(*reinterpret_cast<const uint32_t*>(GU + (size_t)r * 2 * I + 2 * i), silu,
-                                         silu_len);
+    const int i0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (i0 >= I) return;
+    const uint4* src = reinterpret_cast<const uint4*>(GU + (size_t)r * 2 * I + 2 * i0);
+    const uint4 a = src[0], b = src[1];
+    const uint32_t gu[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        w[j] = ((uint32_t)(uint16_t)moe_silu_one(gu[2 * j], silu, silu_len)) |
+               ((uint32_t)(uint16_t)moe_silu_one(gu[2 * j + 1], silu, silu_len) << 16);
+    *reinterpret_cast<uint4*>(Hh + (size_t)r * I + i0) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// out = clamp_i16(RNE(sum_k g_k * y_k + 2^14 * s, 14)).  Grid (ceil(H / 256), T).
+// out = clamp_i16(RNE(sum_k g_k * y_k + 2^14 * s, 14)), eight columns per
+// thread (H % 8 == 0, 16-byte rows).  Grid (ceil(H / 2048), T).
 __global__ __launch_bounds__(256) void moe_combine_kernel(const int32_t* __restrict__ gates,
                                                           const int32_t* __restrict__ slotpos, int K,
                                                           const int16_t* __restrict__ Y, const int16_t* __restrict__ Sh,
                                                           int H, int16_t* __restrict__ out) {
     const int t = blockIdx.y;
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= H) return;
-    int64_t acc = (int64_t)Sh[(size_t)t * H + c] * (int64_t)(1 << MYL_TV_PROB_FRAC_BITS);
+    const int c0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (c0 >= H) return;
+    auto unpack = [](uint4 v, int j) { return (int64_t)(int16_t)((j & 1 ? (&v.x)[j >> 1] >> 16 : (&v.x)[j >> 1]) & 0xFFFFu); };
+    const uint4 sv = *reinterpret_cast<const uint4*>(Sh + (size_t)t * H + c0);
+    int64_t acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = unpack(sv, j) * (int64_t)(1 << MYL_TV_PROB_FRAC_BITS);
     for (int k = 0; k < K; ++k) {
         const int p = slotpos[(size_t)t * K + k];
-        acc = wadd64(acc, (int64_t)gates[(size_t)t * K + k] * (int64_t)Y[(size_t)p * H + c]);
+        const int64_t g = gates[(size_t)t * K + k];
+        const uint4 yv = *reinterpret_cast<const uint4*>(Y + (size_t)p * H + c0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = wadd64(acc[j], g * unpack(yv, j));
     }
-    out[(size_t)t * H + c] = clamp_i16_i64(rshift_round64(acc, MYL_TV_PROB_FRAC_BITS));
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        w[j] = (uint32_t)(uint16_t)clamp_i16_i64(rshift_round64(acc[2 * j], MYL_TV_PROB_FRAC_BITS)) |
+               ((uint32_t)(uint16_t)clamp_i16_i64(rshift_round64(acc[2 * j + 1], MYL_TV_PROB_FRAC_BITS)) << 16);
+    *reinterpret_cast<uint4*>(out + (size_t)t * H + c0) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 // ---------------------------------------------------------------------------
@@ -509,7 +568,7 @@ int myl_moe_forward(myl_moe* m, const int16_t* x_dev, uint32_t n_tokens, int16_t
     EpiLogits el{m->r_shift, (uint8_t)MYL_MOE_X_FRAC, (uint8_t)MYL_MOE_ROUTER_FRAC, m->logits, E};
     if ((e = gemv_i8(x_dev, T, H, m->wr, E, H, el, st, mm)) != hipSuccess) return c->hip(e, "moe router");
     if ((e = hipMemsetAsync(m->counts, 0, (size_t)E * 4, st)) != hipSuccess) return c->hip(e, "moe counts");
-    moe_topk_kernel<<<(T + 255) / 256, 256, 0, st>>>(m->logits, T, E, K, m->r_bias, m->exp_lut, (uint32_t)m->exp_len,
+    moe_topk_kernel<<<(T + kTopkWaves - 1) / kTopkWaves, kTopkWaves * 64, 0, st>>>(m->logits, T, E, K, m->r_bias, m->exp_lut, (uint32_t)m->exp_len,
                                                      m->ids, m->gates, m->counts);
     if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe top-k");
     m->counts_host.assign(E, 0);
@@ -554,7 +613,7 @@ int myl_moe_forward(myl_moe* m, const int16_t* x_dev, uint32_t n_tokens, int16_t
         if ((e = moe_grouped(tile, Xp, m->wgu, (size_t)2 * I * H, 2 * I, H, m->offsets, m->work, (int)wgu.size(), eg,
                              st)) != hipSuccess)
             return c->hip(e, "moe gate/up");
-        moe_silu_planes_kernel<<<dim3((I + 255) / 256, R), 256, 0, st>>>(m->GU, I, m->silu, (uint32_t)m->silu_len, Hp);
+        moe_silu_planes_kernel<<<dim3((I / 8 + 255) / 256, R), 256, 0, st>>>(m->GU, I, m->silu, (uint32_t)m->silu_len, Hp);
         EpiExpertDown ed{m->sd, m->out_frac, H, m->Y};
         if ((e = moe_grouped(tile, Hp, m->wd, (size_t)H * I, H, I, m->offsets, m->work + wgu.size(), (int)wdn.size(),
                              ed, st)) != hipSuccess)
@@ -568,7 +627,7 @@ int myl_moe_forward(myl_moe* m, const int16_t* x_dev, uint32_t n_tokens, int16_t
         mm_w8_grouped_kernel<1, 2, 2, 2, EpiExpertGU><<<8 * (((int)wgu.size() + 7) / 8), GT::kThreads, GT::kLds, st>>>(
             m->Xg, H, m->wgu, (size_t)2 * I * H, 2 * I, H, m->offsets, m->work, (int)wgu.size(), eg);
         if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe gate/up");
-        moe_silu_kernel<<<dim3((I + 255) / 256, R), 256, 0, st>>>(m->GU, I, m->silu, (uint32_t)m->silu_len, m->Hh);
+        moe_silu_kernel<<<dim3((I / 8 + 255) / 256, R), 256, 0, st>>>(m->GU, I, m->silu, (uint32_t)m->silu_len, m->Hh);
         EpiExpertDown ed{m->sd, m->out_frac, H, m->Y};
         mm_w8_grouped_kernel<1, 2, 2, 2, EpiExpertDown><<<8 * (((int)wdn.size() + 7) / 8), GT::kThreads, GT::kLds, st>>>(
             m->Hh, I, m->wd, (size_t)H * I, H, I, m->offsets, m->work + wgu.size(), (int)wdn.size(), ed);
@@ -579,10 +638,10 @@ int myl_moe_forward(myl_moe* m, const int16_t* x_dev, uint32_t n_tokens, int16_t
     egs.shifts = m->sgu_s; egs.act_frac = MYL_MOE_X_FRAC; egs.gate_frac = MYL_MOE_GATE_FRAC;
     egs.up_frac = MYL_MOE_UP_FRAC; egs.out = m->GUs; egs.ldo = 2 * S;
     if ((e = gemv_i8(x_dev, T, H, m->wgu_s, 2 * S, H, egs, st, mm)) != hipSuccess) return c->hip(e, "shared gate/up");
-    moe_silu_kernel<<<dim3((S + 255) / 256, T), 256, 0, st>>>(m->GUs, S, m->silu, (uint32_t)m->silu_len, m->Hs);
+    moe_silu_kernel<<<dim3((S / 8 + 255) / 256, T), 256, 0, st>>>(m->GUs, S, m->silu, (uint32_t)m->silu_len, m->Hs);
     EpiShift eds{m->sd_s, m->out_frac, (uint8_t)MYL_MOE_DOWN_IN_FRAC, 0, m->Sh, H};
     if ((e = gemv_i8(m->Hs, T, S, m->wd_s, H, S, eds, st, mm)) != hipSuccess) return c->hip(e, "shared down");
-    moe_combine_kernel<<<dim3((H + 255) / 256, T), 256, 0, st>>>(m->gates, m->slotpos, K, m->Y, m->Sh, H, out_dev);
+    moe_combine_kernel<<<dim3((H / 8 + 255) / 256, T), 256, 0, st>>>(m->gates, m->slotpos, K, m->Y, m->Sh, H, out_dev);
     return c->hip(hipGetLastError(), "moe combine");
 }
 
