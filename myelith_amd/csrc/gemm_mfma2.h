@@ -457,6 +457,79 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_grouped_kernel(const int8_
                                            2 * wk.m0, wk.n0, lds, SinkGrouped<EpiG>{epi, wk.e, row0});
 }
 
+// mm2_grouped_kernel with the staged epilogue of mm2_staged_kernel: every
+// sum is reduced by EpiG::stage(e, n, sum) to an int16 parked in LDS, then
+// EpiG::emit(e, row, i0, v) takes the 16 values of columns 2 i0 .. 2 i0 + 15
+// of activation row `row` (Ap's token order) for 8-column chunks of N / 2
+// (N % 16 == 0).
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class EpiG>
+__global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_grouped_staged_kernel(
+    const int8_t* __restrict__ Ap, const int8_t* __restrict__ W, size_t w_stride, int N, int K,
+    const int* __restrict__ offsets, const MmWork* __restrict__ work, int nwork, EpiG epi) {
+    using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
+    static_assert((size_t)(S::BR / 2) * S::BN * 2 <= S::kLds, "staged tile fits the stage buffers");
+    extern __shared__ __align__(16) int8_t lds[];
+    const int t = mm_tile_index(nwork);
+    if (t < 0) return;
+    const MmWork wk = work[t];
+    const int row0 = offsets[wk.e];
+    const int R2 = 2 * (offsets[wk.e + 1] - row0);
+    const int r0 = 2 * wk.m0, n0 = wk.n0;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave % WM_, wn = wave / WM_;
+    v16i32_t acc[MB][NB];
+    int32_t rs[NB];
+    mm2_main<MB, NB, WM_, WN_, STAGES, KS>(Ap + (size_t)row0 * 2 * K, R2, W + (size_t)wk.e * w_stride, N, K, 0, K, r0,
+                                           n0, lds, acc, rs);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) rs[j] += __shfl_xor(rs[j], 32);
+    __syncthreads();  // every wave is past its last stage read
+    int16_t* tile = reinterpret_cast<int16_t*>(lds);  // [BR / 2][BN]
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int nl = (wn * NB + j) * 32 + (lane & 31);
+            const int n = n0 + nl;
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const int arl = (wm * MB + i) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                int16_t v = 0;
+                if (r0 + arl < R2 && n < N)
+                    v = epi.stage(wk.e, n,
+                                  (int64_t)acc[i][j][r] * 256 + (int64_t)acc[i][j][r + 1] + (int64_t)rs[j] * 128);
+                tile[(arl >> 1) * S::BN + nl] = v;
+            }
+        }
+    __syncthreads();
+    constexpr int kChunks = S::BN / 16;  // 8-column output chunks per tile row
+    const int m0 = r0 >> 1, i00 = n0 >> 1;
+    for (int c = threadIdx.x; c < (S::BR / 2) * kChunks; c += S::kThreads) {
+        const int ml = c / kChunks, ic = c % kChunks;  // powers of two
+        const int m = m0 + ml, i0 = i00 + ic * 8;
+        if (2 * m >= R2 || 2 * i0 >= N) continue;
+        const uint4* src = reinterpret_cast<const uint4*>(tile + ml * S::BN + ic * 16);
+        epi.emit(wk.e, row0 + m, i0, src[0], src[1]);
+    }
+}
+
+template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class EpiG>
+hipError_t mm2_grouped_staged_launch(const int8_t* Ap, const int8_t* W, size_t w_stride, int N, int K,
+                                     const int* offsets, const MmWork* work, int nwork, const EpiG& epi,
+                                     hipStream_t st) {
+    using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
+    if (K % KS != 0 || N % 16 != 0) return hipErrorInvalidValue;
+    if (nwork <= 0) return hipSuccess;
+    auto kern = mm2_grouped_staged_kernel<MB, NB, WM_, WN_, STAGES, KS, EpiG>;
+    if (S::kLds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
+        if (e != hipSuccess) return e;
+    }
+    kern<<<8 * ((nwork + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, W, w_stride, N, K, offsets, work, nwork, epi);
+    return hipGetLastError();
+}
+
 // Token rows and weight rows of one grouped work item (for the work table).
 template <int MB, int NB, int WM_, int WN_, int STAGES, int KS>
 struct Mm2GroupedShape {

@@ -265,29 +265,6 @@ __device__ inline int16_t moe_silu_one(uint32_t gu, const int16_t* __restrict__ 
     return clamp_i16_i64(rescale64(prod, (uint8_t)(MYL_TV_SILU_OUT_FRAC + MYL_MOE_UP_FRAC), MYL_MOE_DOWN_IN_FRAC));
 }
 
-// moe_silu_kernel writing byte planes [2R x I] of h for the grouped down
-// product: eight outputs per thread (I % 8 == 0), 16-byte loads and 8-byte
-// stores.  Grid (ceil(I / 2048), R).
-__global__ __launch_bounds__(256) void moe_silu_planes_kernel(const int16_t* __restrict__ GU, int I,
-                                                              const int16_t* __restrict__ silu, uint32_t silu_len,
-                                                              int8_t* __restrict__ Hp) {
-    const int r = blockIdx.y;
-    const int i0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
-    if (i0 >= I) return;
-    const uint4* src = reinterpret_cast<const uint4*>(GU + (size_t)r * 2 * I + 2 * i0);
-    const uint4 a = src[0], b = src[1];
-    const uint32_t gu[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    uint32_t hw[2] = {0, 0}, lw[2] = {0, 0};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int32_t h = moe_silu_one(gu[j], silu, silu_len);
-        hw[j >> 2] |= ((uint32_t)(h >> 8) & 0xFFu) << (8 * (j & 3));
-        lw[j >> 2] |= ((uint32_t)((h & 255) - 128) & 0xFFu) << (8 * (j & 3));
-    }
-    *reinterpret_cast<uint2*>(Hp + (size_t)(2 * r) * I + i0) = make_uint2(hw[0], hw[1]);
-    *reinterpret_cast<uint2*>(Hp + (size_t)(2 * r + 1) * I + i0) = make_uint2(lw[0], lw[1]);
-}
-
 // mlp.rs:55-65 per row, eight outputs per thread (I % 8 == 0).  Grid
 // (ceil(I / 2048), R).
 __global__ __launch_bounds__(256) void moe_silu_kernel(const int16_t* __restrict__ GU, int I,
@@ -348,6 +325,36 @@ struct EpiExpertGU {
         const uint8_t frac = (n & 1) ? MYL_MOE_UP_FRAC : MYL_MOE_GATE_FRAC;
         out[(size_t)row * n2 + n] =
             clamp_i16_i64(rescale64(acc, (uint8_t)(shifts[(size_t)e * n2 + n] + MYL_MOE_X_FRAC), frac));
+    }
+};
+
+// The grouped gate/up fused with the SiLU gate (mlp.rs:46-65) and the byte-plane
+// split of h (mm2_grouped_staged_kernel): gate row 2i and up row 2i+1 of
+// expert e requantize to their fracs, then h = silu(g) * u leaves as 8-byte
+// pieces of planes rows 2 row (hi) and 2 row + 1 (lo') of the grouped down
+// product's operand [2R x I].
+struct EpiExpertGUSiluPlanes {
+    const uint8_t* shifts;  // [E][2I]
+    int n2;                 // 2I
+    const int16_t* silu;
+    uint32_t silu_len;
+    int8_t* planes;         // [2R x I]
+    __device__ inline int16_t stage(int e, int n, int64_t acc) const {
+        const uint8_t frac = (n & 1) ? MYL_MOE_UP_FRAC : MYL_MOE_GATE_FRAC;
+        return clamp_i16_i64(rescale64(acc, (uint8_t)(shifts[(size_t)e * n2 + n] + MYL_MOE_X_FRAC), frac));
+    }
+    __device__ inline void emit(int, int row, int i0, const uint4& a, const uint4& b) const {
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};  // (g, u) pairs
+        uint32_t hi[2] = {0, 0}, lo[2] = {0, 0};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int32_t h = moe_silu_one(w[k], silu, silu_len);
+            hi[k >> 2] |= ((uint32_t)(h >> 8) & 0xFFu) << (8 * (k & 3));
+            lo[k >> 2] |= ((uint32_t)((h & 255) - 128) & 0xFFu) << (8 * (k & 3));
+        }
+        const int I = n2 >> 1;
+        *reinterpret_cast<uint2*>(planes + (size_t)(2 * row) * I + i0) = make_uint2(hi[0], hi[1]);
+        *reinterpret_cast<uint2*>(planes + (size_t)(2 * row + 1) * I + i0) = make_uint2(lo[0], lo[1]);
     }
 };
 
@@ -498,6 +505,16 @@ hipError_t moe_grouped(int tile, const int8_t* Ap, const int8_t* W, size_t w_str
     return mm2_grouped_launch<2, 1, 2, 4, 4, 64>(Ap, W, w_stride, N, K, offsets, work, nwork, epi, st);
 }
 
+template <class EpiG>
+hipError_t moe_grouped_staged(int tile, const int8_t* Ap, const int8_t* W, size_t w_stride, int N, int K,
+                              const int* offsets, const MmWork* work, int nwork, const EpiG& epi, hipStream_t st) {
+    if (tile == 0)
+        return mm2_grouped_staged_launch<2, 2, 4, 4, 2, 128>(Ap, W, w_stride, N, K, offsets, work, nwork, epi, st);
+    if (tile == 1)
+        return mm2_grouped_staged_launch<2, 2, 4, 2, 3, 64>(Ap, W, w_stride, N, K, offsets, work, nwork, epi, st);
+    return mm2_grouped_staged_launch<2, 1, 2, 4, 4, 64>(Ap, W, w_stride, N, K, offsets, work, nwork, epi, st);
+}
+
 // Work table of a grouped product: (expert, m-tile, n-tile), m fastest.
 void work_table(const std::vector<int32_t>& counts, int bm, int bn, int N, std::vector<MmWork>& out) {
     out.clear();
@@ -609,11 +626,10 @@ int myl_moe_forward(myl_moe* m, const int16_t* x_dev, uint32_t n_tokens, int16_t
         int8_t* Hp = reinterpret_cast<int8_t*>(m->Hh);
         moe_gather_planes_kernel<<<R, 256, 0, st>>>(x_dev, H, m->list_tok, Xp);
         if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe dispatch");
-        EpiExpertGU eg{m->sgu, 2 * I, m->GU};
-        if ((e = moe_grouped(tile, Xp, m->wgu, (size_t)2 * I * H, 2 * I, H, m->offsets, m->work, (int)wgu.size(), eg,
-                             st)) != hipSuccess)
+        EpiExpertGUSiluPlanes eg{m->sgu, 2 * I, m->silu, (uint32_t)m->silu_len, Hp};
+        if ((e = moe_grouped_staged(tile, Xp, m->wgu, (size_t)2 * I * H, 2 * I, H, m->offsets, m->work,
+                                    (int)wgu.size(), eg, st)) != hipSuccess)
             return c->hip(e, "moe gate/up");
-        moe_silu_planes_kernel<<<dim3((I / 8 + 255) / 256, R), 256, 0, st>>>(m->GU, I, m->silu, (uint32_t)m->silu_len, Hp);
         EpiExpertDown ed{m->sd, m->out_frac, H, m->Y};
         if ((e = moe_grouped(tile, Hp, m->wd, (size_t)H * I, H, I, m->offsets, m->work + wgu.size(), (int)wdn.size(),
                              ed, st)) != hipSuccess)
@@ -633,14 +649,26 @@ int myl_moe_forward(myl_moe* m, const int16_t* x_dev, uint32_t n_tokens, int16_t
             m->Hh, I, m->wd, (size_t)H * I, H, I, m->offsets, m->work + wgu.size(), (int)wdn.size(), ed);
         if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe down");
     }
-    // shared expert: dense products over every token
-    EpiGURows egs{};
-    egs.shifts = m->sgu_s; egs.act_frac = MYL_MOE_X_FRAC; egs.gate_frac = MYL_MOE_GATE_FRAC;
-    egs.up_frac = MYL_MOE_UP_FRAC; egs.out = m->GUs; egs.ldo = 2 * S;
-    if ((e = gemv_i8(x_dev, T, H, m->wgu_s, 2 * S, H, egs, st, mm)) != hipSuccess) return c->hip(e, "shared gate/up");
-    moe_silu_kernel<<<dim3((S / 8 + 255) / 256, T), 256, 0, st>>>(m->GUs, S, m->silu, (uint32_t)m->silu_len, m->Hs);
+    // shared expert: dense products over every token.  With byte planes the
+    // gate/up product's staged epilogue applies the SiLU gate and writes the
+    // down product's planes [2T x S] (in the bytes of Hs).
     EpiShift eds{m->sd_s, m->out_frac, (uint8_t)MYL_MOE_DOWN_IN_FRAC, 0, m->Sh, H};
-    if ((e = gemv_i8(m->Hs, T, S, m->wd_s, H, S, eds, st, mm)) != hipSuccess) return c->hip(e, "shared down");
+    if (mm_planes_ok(T, H, mm) && mm_planes_ok(T, S, mm) && T > 64) {
+        int8_t* Sp = reinterpret_cast<int8_t*>(m->Hs);
+        EpiGUSiluPlanes es{m->sgu_s, (uint8_t)MYL_MOE_X_FRAC, (uint8_t)MYL_MOE_GATE_FRAC, (uint8_t)MYL_MOE_UP_FRAC,
+                           (uint8_t)MYL_MOE_DOWN_IN_FRAC, m->silu, (uint32_t)m->silu_len, Sp, S};
+        if ((e = split_planes(x_dev, T, H, H, mm->planes, st)) != hipSuccess) return c->hip(e, "shared planes");
+        if ((e = mm_planes_staged(mm->planes, T, m->wgu_s, 2 * S, H, es, mm, st)) != hipSuccess)
+            return c->hip(e, "shared gate/up");
+        if ((e = mm_planes(Sp, T, m->wd_s, H, S, eds, mm, st)) != hipSuccess) return c->hip(e, "shared down");
+    } else {
+        EpiGURows egs{};
+        egs.shifts = m->sgu_s; egs.act_frac = MYL_MOE_X_FRAC; egs.gate_frac = MYL_MOE_GATE_FRAC;
+        egs.up_frac = MYL_MOE_UP_FRAC; egs.out = m->GUs; egs.ldo = 2 * S;
+        if ((e = gemv_i8(x_dev, T, H, m->wgu_s, 2 * S, H, egs, st, mm)) != hipSuccess) return c->hip(e, "shared gate/up");
+        moe_silu_kernel<<<dim3((S / 8 + 255) / 256, T), 256, 0, st>>>(m->GUs, S, m->silu, (uint32_t)m->silu_len, m->Hs);
+        if ((e = gemv_i8(m->Hs, T, S, m->wd_s, H, S, eds, st, mm)) != hipSuccess) return c->hip(e, "shared down");
+    }
     moe_combine_kernel<<<dim3((H / 8 + 255) / 256, T), 256, 0, st>>>(m->gates, m->slotpos, K, m->Y, m->Sh, H, out_dev);
     return c->hip(hipGetLastError(), "moe combine");
 }
