@@ -17,7 +17,12 @@ Also reported:
                four (N, K) shapes, multiplier requant; M <= 8 streams over
                rotating weight copies (> 512 MB distinct) so the 256 MB
                Infinity Cache cannot serve repeats, M >= 64 runs on the int8
-               matrix cores and reports TOP/s;
+               matrix cores and reports TOP/s; launches replayed from a
+               captured graph;
+  read_ceiling the achievable read rate at the decode kernels' sizes (one
+               pass of plain 16-byte loads over rotating buffers): what a
+               kernel that only streams its bytes reaches, beside the 8 TB/s
+               peak;
   e2e_0.5b     the Qwen2.5-0.5B-shape model end to end at batch 1: 256-token
                prompt, 128 greedy decode tokens;
   teacher_forced_prefill  4 x 1024 Zipf(1.1) token ids through the batched
@@ -112,6 +117,34 @@ def _graph_time(backend, launch, replays):
         return None
     finally:
         del g
+
+
+READ_SIZES = (12_877_312, 16_549_888, 67_895_296, 135_790_592, 544_997_376)
+
+
+def read_ceiling(backend):
+    """The achievable HBM read rate at the sizes the decode kernels stream:
+    one pass of plain 16-byte loads (myl_read_probe) over B bytes, launches
+    rotating over six 545 MB buffers of random bytes so the 256 MB Infinity
+    Cache cannot serve a repeat; 24 launches per size captured as a graph and
+    replayed, events around the replays."""
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(99)
+    bufs = [torch.randint(-128, 128, (READ_SIZES[-1],), dtype=torch.int8, device="cuda", generator=g) for _ in range(6)]
+    out = torch.zeros(4, dtype=torch.int32, device="cuda")
+    rec = {}
+    for B in READ_SIZES:
+        for b in bufs[:3]:
+            backend.read_probe_dev(b[:B], out)
+        ms = _graph_time(backend, lambda: [backend.read_probe_dev(bufs[i % 6][:B], out) for i in range(24)], 4)
+        if ms is None:
+            continue
+        us = ms * 1e3 / 24
+        rec[str(B)] = {"us": round(us, 2), "GBps": round(B / us / 1e3, 1), "frac_of_8TBps": round(B / us / 1e3 / 8000, 3)}
+        log(f"read ceiling {B} B: {us:.2f} us, {B / us / 1e3:.0f} GB/s")
+    del bufs
+    return rec
 
 
 def w8a16_sweep(backend, shapes, ms=(1, 8, 64, 512), target_bytes=6 << 30, target_ops=4e12):
@@ -396,7 +429,7 @@ def main() -> int:
     ap.add_argument("--no-batch", action="store_true",
                     help="skip the batched decode, teacher-forced prefill and MoE sections")
     ap.add_argument("--no-batched-decode", action="store_true", help="skip only the batched decode section")
-    ap.add_argument("--section", choices=("prefill", "batched", "moe", "e2e", "sweep"),
+    ap.add_argument("--section", choices=("prefill", "batched", "moe", "e2e", "sweep", "read"),
                     help="run only this section (for profiling) and print its record as one JSON line")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="also run three 256 MiB device-to-device copies: the known-size kernel that calibrates "
@@ -428,6 +461,8 @@ def main() -> int:
             rec = e2e_05b(backend, args.seed)
         elif args.section == "sweep":
             rec = w8a16_sweep(backend, [(3584, 3584), (18944, 3584), (3584, 18944), (152064, 3584)])
+        elif args.section == "read":
+            rec = read_ceiling(backend)
         else:
             spec = make_spec(QWEN25_7B, seed=args.seed, max_pos=1024 + 8 if args.section == "prefill" else 2048 + 40)
             model = IntegerModel(backend, spec, LutSet.for_head_dim(spec["head_dim"]))
@@ -532,9 +567,10 @@ def main() -> int:
                             "rows) minus plain replays; the second launch follows the first, so it starts warm"}
     log("kernel classes: " + ", ".join(f"{k} {v['avg_us']}us" for k, v in per_class.items()))
 
-    gemv = {}
+    gemv, ceiling = {}, {}
     if not args.no_gemv:
         gemv = w8a16_sweep(backend, [(3584, 3584), (18944, 3584), (3584, 18944), (152064, 3584)])
+        ceiling = read_ceiling(backend)
 
     if args.traffic_probe:
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
@@ -601,6 +637,7 @@ def main() -> int:
                      "in_graph_repeat": repeat},
         "kernel_classes": per_class,
         "w8a16_sweep": gemv,
+        "read_ceiling": ceiling,
         "e2e_0.5b": e2e_small,
         "teacher_forced_prefill": prefill_tf,
         "batched_decode": batch_dec,

@@ -72,6 +72,12 @@ void* myl_stream(myl_ctx* ctx); /* the hipStream_t all *_dev calls use */
 int myl_set_stream(myl_ctx* ctx, void* stream);
 
 /* ---- device memory for callers without their own allocator ------------- */
+/* No counterpart in the reference: a measurement of the achievable read rate
+ * for the roofline figures.  Enqueues one pass of plain 16-byte loads over
+ * `bytes` of device memory at p (16-byte aligned, bytes % 16 == 0), one block
+ * of 512 threads per CU; `out` (one device word) receives at most one
+ * word. */
+int myl_read_probe(myl_ctx* ctx, const void* p, size_t bytes, uint32_t* out);
 int myl_malloc(myl_ctx* ctx, size_t bytes, void** dptr);
 int myl_free(myl_ctx* ctx, void* dptr);
 int myl_memcpy_htod(myl_ctx* ctx, void* dst, const void* src, size_t bytes);

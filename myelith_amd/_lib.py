@@ -63,6 +63,7 @@ SIGNATURES: dict[str, tuple] = {
     "myl_synchronize": (INT, [P]),
     "myl_stream": (P, [P]),
     "myl_set_stream": (INT, [P, P]),
+    "myl_read_probe": (INT, [P, P, sz, P]),
     "myl_malloc": (INT, [P, sz, C.POINTER(P)]),
     "myl_free": (INT, [P, P]),
     "myl_memcpy_htod": (INT, [P, P, P, sz]),

@@ -106,6 +106,12 @@ class RocmBackend:
     def synchronize(self) -> None:
         self.check(lib().myl_synchronize(self._h), "synchronize")
 
+    def read_probe_dev(self, buf, out) -> None:
+        """One pass of plain loads over the device tensor buf (a measurement of
+        the achievable read rate; out: a device int32 word)."""
+        self.check(lib().myl_read_probe(self._h, buf.data_ptr(), buf.numel() * buf.element_size(), out.data_ptr()),
+                   "read_probe")
+
     def use_torch_stream(self) -> None:
         """Launch on torch's current HIP stream (so torch events time our kernels)."""
         import torch

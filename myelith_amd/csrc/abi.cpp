@@ -151,6 +151,14 @@ int myl_set_stream(myl_ctx* ctx, void* stream) {
     return MYL_OK;
 }
 
+int myl_read_probe(myl_ctx* ctx, const void* p, size_t bytes, uint32_t* out) {
+    if (!ctx || !p || !out) return MYL_E_INVALID;
+    if (bytes % 16 || ((uintptr_t)p & 15)) return ctx->fail(MYL_E_INVALID, "read_probe: 16-byte aligned, whole 16-byte words");
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device) != hipSuccess || cus < 1) cus = 256;
+    return ctx->hip(read_probe(p, bytes, out, cus, ctx->stream), "read_probe");
+}
+
 int myl_malloc(myl_ctx* ctx, size_t bytes, void** dptr) {
     if (!ctx || !dptr) return MYL_E_INVALID;
     (void)hipSetDevice(ctx->device);

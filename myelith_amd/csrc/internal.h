@@ -26,6 +26,7 @@ hipError_t linear_w8a16(const int16_t* x, int M, int ldx, const int8_t* W, int N
                         uint8_t act_frac, uint8_t out_frac, const uint8_t* out_frac_pc, int16_t* out, int ldo,
                         hipStream_t st,
                         const MmCtx* mm = nullptr);
+hipError_t read_probe(const void* p, size_t bytes, uint32_t* out, int cus, hipStream_t st);
 hipError_t linear_w8a16_mult(const int16_t* x, int M, int ldx, const int8_t* W, int N, int K, const int32_t* mult,
                              const uint8_t* shift, int16_t* out, int ldo, hipStream_t st,
                         const MmCtx* mm = nullptr);

@@ -528,6 +528,36 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const uint64_t* __rest
     if (threadIdx.x == 0) out[blockIdx.x] = (int64_t)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFu));
 }
 
+// One pass over `bytes` (a multiple of 16) of device memory: nontemporal
+// 16-byte loads, four in flight per thread, grid-stride.  The thread's XOR of
+// its words is stored only when it equals one arbitrary constant, so the
+// loads cannot be dropped and at most a word is written.
+__global__ __launch_bounds__(512) void read_probe_kernel(const uint4* __restrict__ p, size_t n16,
+                                                         uint32_t* __restrict__ out) {
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    const size_t tid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    const size_t nthr = (size_t)gridDim.x * blockDim.x;
+    uint32_t acc = 0;
+    size_t i = tid;
+    for (; i + 3 * nthr < n16; i += 4 * nthr) {
+        v4u v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p + i + u * nthr));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+    }
+    for (; i < n16; i += nthr) {
+        const uint4 v = p[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9E3779B9u) out[0] = acc;
+}
+
+hipError_t read_probe(const void* p, size_t bytes, uint32_t* out, int cus, hipStream_t st) {
+    read_probe_kernel<<<cus, 512, 0, st>>>(reinterpret_cast<const uint4*>(p), bytes / 16, out);
+    return hipGetLastError();
+}
+
 hipError_t argmax_rows(const int32_t* v, int M, int n, int ldv, int64_t* out, uint64_t* part, hipStream_t st) {
     const int nch = (n + kArgChunk - 1) / kArgChunk;
     argmax_part_kernel<<<dim3(nch, M), kBlock, 0, st>>>(v, n, ldv, part, nch);
