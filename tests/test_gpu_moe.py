@@ -26,13 +26,18 @@ def compare_route(g, o):
         assert np.array_equal(g[k], o[k]), k
 
 
-@pytest.mark.parametrize("T", [1, 37, 300])
-def test_small_moe_all_tokens(backend, T):
-    """8 experts, top-2, two of them unreachable (no tokens): every token's output."""
+@pytest.mark.parametrize("T,widths", [(1, (256, 128, 256)), (37, (256, 128, 256)), (300, (256, 128, 256)),
+                                      (300, (240, 144, 272))])
+def test_small_moe_all_tokens(backend, T, widths):
+    """8 experts, top-2, two of them unreachable (no tokens): every token's output.
+    Widths (hidden, inter, shared) that are multiples of 128 take the byte-plane
+    expert products (and, past 64 tokens, the shared expert's fused SiLU);
+    240 / 144 / 272 (not multiples of 64) take the int16-row products."""
     from myelith_amd.moe import moe_spec
-    spec = moe_spec(9, hidden=256, n_experts=8, inter=128, top_k=2, shared_inter=256)
+    H, I, S = widths
+    spec = moe_spec(9, hidden=H, n_experts=8, inter=I, top_k=2, shared_inter=S)
     bias = np.array([0, -100, -200, -10**7, -150, -10**7, -50, -300], np.int32)
-    case(f"small moe T={T}")
+    case(f"small moe T={T} widths={widths}")
     gm, om = build(backend, spec, bias)
     x = gm.synth_input(T)
     xh = x.cpu().numpy()
