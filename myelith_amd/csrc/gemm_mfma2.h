@@ -436,19 +436,32 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_splitk_kernel(const int8_t
                                            SinkAtomic{acc, N});
 }
 
+// Work item of this block when the item count n is in device memory (written
+// by an earlier kernel; grid = 8 ceil(max / 8) for an upper bound max): XCD x
+// takes items [x per, (x + 1) per) with per = ceil(n / 8), as mm_tile_index
+// does for a count known at launch; the other blocks get -1.
+__device__ inline int mm_dyn_tile_index(const int* __restrict__ nwork) {
+    const int n = __builtin_amdgcn_readfirstlane(*nwork);
+    const int b = blockIdx.x, per = (n + 7) >> 3;
+    const int t = (b & 7) * per + (b >> 3);
+    return (b >> 3) < per && t < n ? t : -1;
+}
+
 // Grouped products (MoE experts): work item t = (expert e, token tile m0,
 // weight tile n0) of the work table; expert e's rows are the byte-plane rows
 // [2 offsets[e], 2 offsets[e+1]) of Ap and its weights W + e * w_stride
 // [N x K].  The epilogue receives (e, n, row, sum) with row the activation
-// row in Ap's token order (SinkGrouped).  K % KS == 0.
+// row in Ap's token order (SinkGrouped).  The item count is read from
+// *nwork on the device (the work table is built there); the grid covers
+// maxwork items.  K % KS == 0.
 template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class EpiG>
 __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_grouped_kernel(const int8_t* __restrict__ Ap,
                                                                      const int8_t* __restrict__ W, size_t w_stride,
                                                                      int N, int K, const int* __restrict__ offsets,
-                                                                     const MmWork* __restrict__ work, int nwork,
-                                                                     EpiG epi) {
+                                                                     const MmWork* __restrict__ work,
+                                                                     const int* __restrict__ nwork, EpiG epi) {
     extern __shared__ __align__(16) int8_t lds[];
-    const int t = mm_tile_index(nwork);
+    const int t = mm_dyn_tile_index(nwork);
     if (t < 0) return;
     const MmWork wk = work[t];
     const int row0 = offsets[wk.e];
@@ -465,11 +478,11 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_grouped_kernel(const int8_
 template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class EpiG>
 __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_grouped_staged_kernel(
     const int8_t* __restrict__ Ap, const int8_t* __restrict__ W, size_t w_stride, int N, int K,
-    const int* __restrict__ offsets, const MmWork* __restrict__ work, int nwork, EpiG epi) {
+    const int* __restrict__ offsets, const MmWork* __restrict__ work, const int* __restrict__ nwork, EpiG epi) {
     using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     static_assert((size_t)(S::BR / 2) * S::BN * 2 <= S::kLds, "staged tile fits the stage buffers");
     extern __shared__ __align__(16) int8_t lds[];
-    const int t = mm_tile_index(nwork);
+    const int t = mm_dyn_tile_index(nwork);
     if (t < 0) return;
     const MmWork wk = work[t];
     const int row0 = offsets[wk.e];
@@ -516,17 +529,17 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void mm2_grouped_staged_kernel(
 
 template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class EpiG>
 hipError_t mm2_grouped_staged_launch(const int8_t* Ap, const int8_t* W, size_t w_stride, int N, int K,
-                                     const int* offsets, const MmWork* work, int nwork, const EpiG& epi,
-                                     hipStream_t st) {
+                                     const int* offsets, const MmWork* work, const int* nwork, int maxwork,
+                                     const EpiG& epi, hipStream_t st) {
     using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     if (K % KS != 0 || N % 16 != 0) return hipErrorInvalidValue;
-    if (nwork <= 0) return hipSuccess;
+    if (maxwork <= 0) return hipSuccess;
     auto kern = mm2_grouped_staged_kernel<MB, NB, WM_, WN_, STAGES, KS, EpiG>;
     if (S::kLds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
         if (e != hipSuccess) return e;
     }
-    kern<<<8 * ((nwork + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, W, w_stride, N, K, offsets, work, nwork, epi);
+    kern<<<8 * ((maxwork + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, W, w_stride, N, K, offsets, work, nwork, epi);
     return hipGetLastError();
 }
 
@@ -540,16 +553,16 @@ struct Mm2GroupedShape {
 
 template <int MB, int NB, int WM_, int WN_, int STAGES, int KS, class EpiG>
 hipError_t mm2_grouped_launch(const int8_t* Ap, const int8_t* W, size_t w_stride, int N, int K, const int* offsets,
-                              const MmWork* work, int nwork, const EpiG& epi, hipStream_t st) {
+                              const MmWork* work, const int* nwork, int maxwork, const EpiG& epi, hipStream_t st) {
     using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
     if (K % KS != 0) return hipErrorInvalidValue;
-    if (nwork <= 0) return hipSuccess;
+    if (maxwork <= 0) return hipSuccess;
     auto kern = mm2_grouped_kernel<MB, NB, WM_, WN_, STAGES, KS, EpiG>;
     if (S::kLds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
         if (e != hipSuccess) return e;
     }
-    kern<<<8 * ((nwork + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, W, w_stride, N, K, offsets, work, nwork, epi);
+    kern<<<8 * ((maxwork + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, W, w_stride, N, K, offsets, work, nwork, epi);
     return hipGetLastError();
 }
 

@@ -69,6 +69,7 @@ struct myl_moe {
     int16_t *GUs = nullptr, *Hs = nullptr, *Sh = nullptr;
     MmWork* work = nullptr;
     int work_cap = 0;
+    int32_t* nwork = nullptr;      // [2]: items of the gate/up and down work tables
     std::vector<int32_t> counts_host;
 
     template <class T> T* dalloc(std::vector<void*>& list, size_t count) {
@@ -229,6 +230,40 @@ __global__ __launch_bounds__(256) void moe_dispatch_kernel(const int32_t* __rest
         }
         run += tot;
         __syncthreads();
+    }
+}
+
+// The route's plan on the device (no host round trip): offsets[e] = the
+// exclusive prefix of counts, and the work tables of the two grouped
+// products in work_table's order (expert, weight tile, token tile), the
+// gate/up table at work[0 ..) and the down table at work[max1 ..); their
+// sizes go to nwork[0], nwork[1].  Token tiles of 2^bm_log tokens, weight
+// tiles of bn rows, nt1 / nt2 weight tiles.  One block of 256 threads, E <= 256;
+// thread e writes expert e's items.
+__global__ __launch_bounds__(256) void moe_plan_kernel(const int32_t* __restrict__ counts, int E, int bm_log, int bn,
+                                                       int nt1, int nt2, int max1, int32_t* __restrict__ offsets,
+                                                       MmWork* __restrict__ work, int32_t* __restrict__ nwork) {
+    __shared__ int32_t off[257], w1[257], w2[257];
+    const int e = threadIdx.x;
+    if (e == 0) {
+        off[0] = w1[0] = w2[0] = 0;
+        for (int x = 0; x < E; ++x) {
+            const int c = counts[x], mt = (c + (1 << bm_log) - 1) >> bm_log;
+            off[x + 1] = off[x] + c;
+            w1[x + 1] = w1[x] + mt * nt1;
+            w2[x + 1] = w2[x] + mt * nt2;
+        }
+        nwork[0] = w1[E];
+        nwork[1] = w2[E];
+    }
+    __syncthreads();
+    for (int x = e; x <= E; x += blockDim.x) offsets[x] = off[x];
+    if (e < E) {
+        const int mt = (off[e + 1] - off[e] + (1 << bm_log) - 1) >> bm_log;
+        for (int ni = 0; ni < nt1; ++ni)
+            for (int mi = 0; mi < mt; ++mi) work[w1[e] + ni * mt + mi] = MmWork{e, mi << bm_log, ni * bn, 0};
+        for (int ni = 0; ni < nt2; ++ni)
+            for (int mi = 0; mi < mt; ++mi) work[max1 + w2[e] + ni * mt + mi] = MmWork{e, mi << bm_log, ni * bn, 0};
     }
 }
 
@@ -407,6 +442,7 @@ int build(myl_moe* m, const int32_t* router_bias, const myl_luts* luts) {
     m->exp_lut = m->dalloc<int16_t>(A, luts->exp_len);
     m->counts = m->dalloc<int32_t>(A, E);
     m->offsets = m->dalloc<int32_t>(A, E + 1);
+    m->nwork = m->dalloc<int32_t>(A, 2);
     for (void* p : A)
         if (!p) return c->fail(MYL_E_NOMEM, "moe: weight allocation");
     m->silu_len = (int)luts->silu_len;
@@ -499,21 +535,30 @@ int moe_tile_rows(int tile) {
 }
 template <class EpiG>
 hipError_t moe_grouped(int tile, const int8_t* Ap, const int8_t* W, size_t w_stride, int N, int K, const int* offsets,
-                       const MmWork* work, int nwork, const EpiG& epi, hipStream_t st) {
-    if (tile == 0) return mm2_grouped_launch<2, 2, 4, 4, 2, 128>(Ap, W, w_stride, N, K, offsets, work, nwork, epi, st);
-    if (tile == 1) return mm2_grouped_launch<2, 2, 4, 2, 3, 64>(Ap, W, w_stride, N, K, offsets, work, nwork, epi, st);
-    return mm2_grouped_launch<2, 1, 2, 4, 4, 64>(Ap, W, w_stride, N, K, offsets, work, nwork, epi, st);
+                       const MmWork* work, const int* nwork, int maxwork, const EpiG& epi, hipStream_t st) {
+    if (tile == 0)
+        return mm2_grouped_launch<2, 2, 4, 4, 2, 128>(Ap, W, w_stride, N, K, offsets, work, nwork, maxwork, epi, st);
+    if (tile == 1)
+        return mm2_grouped_launch<2, 2, 4, 2, 3, 64>(Ap, W, w_stride, N, K, offsets, work, nwork, maxwork, epi, st);
+    return mm2_grouped_launch<2, 1, 2, 4, 4, 64>(Ap, W, w_stride, N, K, offsets, work, nwork, maxwork, epi, st);
 }
 
 template <class EpiG>
 hipError_t moe_grouped_staged(int tile, const int8_t* Ap, const int8_t* W, size_t w_stride, int N, int K,
-                              const int* offsets, const MmWork* work, int nwork, const EpiG& epi, hipStream_t st) {
+                              const int* offsets, const MmWork* work, const int* nwork, int maxwork, const EpiG& epi,
+                              hipStream_t st) {
     if (tile == 0)
-        return mm2_grouped_staged_launch<2, 2, 4, 4, 2, 128>(Ap, W, w_stride, N, K, offsets, work, nwork, epi, st);
+        return mm2_grouped_staged_launch<2, 2, 4, 4, 2, 128>(Ap, W, w_stride, N, K, offsets, work, nwork, maxwork, epi,
+                                                             st);
     if (tile == 1)
-        return mm2_grouped_staged_launch<2, 2, 4, 2, 3, 64>(Ap, W, w_stride, N, K, offsets, work, nwork, epi, st);
-    return mm2_grouped_staged_launch<2, 1, 2, 4, 4, 64>(Ap, W, w_stride, N, K, offsets, work, nwork, epi, st);
+        return mm2_grouped_staged_launch<2, 2, 4, 2, 3, 64>(Ap, W, w_stride, N, K, offsets, work, nwork, maxwork, epi,
+                                                            st);
+    return mm2_grouped_staged_launch<2, 1, 2, 4, 4, 64>(Ap, W, w_stride, N, K, offsets, work, nwork, maxwork, epi, st);
 }
+
+// Work items of a grouped product over R routed rows of E experts in token
+// tiles of bm: sum_e ceil(c_e / bm) <= floor(R / bm) + E token tiles.
+int moe_max_items(int R, int E, int bm, int nt) { return (R / bm + E) * nt; }
 
 // Work table of a grouped product: (expert, m-tile, n-tile), m fastest.
 void work_table(const std::vector<int32_t>& counts, int bm, int bn, int N, std::vector<MmWork>& out) {
@@ -588,66 +633,85 @@ int myl_moe_forward(myl_moe* m, const int16_t* x_dev, uint32_t n_tokens, int16_t
     moe_topk_kernel<<<(T + kTopkWaves - 1) / kTopkWaves, kTopkWaves * 64, 0, st>>>(m->logits, T, E, K, m->r_bias, m->exp_lut, (uint32_t)m->exp_len,
                                                      m->ids, m->gates, m->counts);
     if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe top-k");
-    m->counts_host.assign(E, 0);
-    rc = c->hip(hipMemcpyAsync(m->counts_host.data(), m->counts, (size_t)E * 4, hipMemcpyDeviceToHost, st), "counts");
-    if (!rc) rc = c->hip(hipStreamSynchronize(st), "counts");
-    if (rc) return rc;
-    std::vector<int32_t> offs(E + 1, 0);
-    for (int x = 0; x < E; ++x) offs[x + 1] = offs[x] + m->counts_host[x];
-    // grouped work tables: gate/up (N = 2I) and down (N = H).  Both K (H, I)
-    // multiples of 64: byte-plane products (moe_planes_tile), else 64 x 128
-    // tiles of int16 rows
-    using GT = MmShape<1, 2, 2, 2>;
-    const bool planes = H % 64 == 0 && I % 64 == 0;
-    const int tile = moe_planes_tile(H, I);
-    const int bm = planes ? moe_tile_tokens(tile) : GT::BM, bn = planes ? moe_tile_rows(tile) : GT::BN;
-    std::vector<MmWork> wgu, wdn;
-    work_table(m->counts_host, bm, bn, 2 * I, wgu);
-    work_table(m->counts_host, bm, bn, H, wdn);
-    const int need = (int)(wgu.size() + wdn.size());
-    if (need > m->work_cap) {
-        if (m->work) (void)hipFree(m->work);
-        m->work = nullptr;
-        m->work_cap = 0;
-        if (hipMalloc(&m->work, (size_t)need * sizeof(MmWork)) != hipSuccess) return c->fail(MYL_E_NOMEM, "moe work");
-        m->work_cap = need;
-    }
-    std::vector<MmWork> all(wgu);
-    all.insert(all.end(), wdn.begin(), wdn.end());
-    rc = c->hip(hipMemcpyAsync(m->work, all.data(), all.size() * sizeof(MmWork), hipMemcpyHostToDevice, st), "work");
-    if (!rc) rc = c->hip(hipMemcpyAsync(m->offsets, offs.data(), offs.size() * 4, hipMemcpyHostToDevice, st), "offs");
-    if (rc) return rc;
-    // dispatch (stable), gather, grouped experts
-    moe_dispatch_kernel<<<E, 256, 0, st>>>(m->ids, T, K, m->offsets, m->list_tok, m->slotpos);
     const int R = T * K;
+    const bool planes = H % 64 == 0 && I % 64 == 0;
     if (planes) {
-        // the planes [2R x H] and [2R x I] take the bytes of Xg and Hh
+        // byte-plane expert products, planned on the device: offsets and
+        // work tables from the counts without a host round trip; the planes
+        // [2R x H] and [2R x I] take the bytes of Xg and Hh
+        const int tile = moe_planes_tile(H, I);
+        const int bm = moe_tile_tokens(tile), bn = moe_tile_rows(tile);
+        int bm_log = 0;
+        while ((1 << bm_log) < bm) ++bm_log;
+        const int nt1 = (2 * I + bn - 1) / bn, nt2 = (H + bn - 1) / bn;
+        const int max1 = moe_max_items(R, E, bm, nt1), max2 = moe_max_items(R, E, bm, nt2);
+        if (max1 + max2 > m->work_cap) {
+            (void)hipStreamSynchronize(st);
+            if (m->work) (void)hipFree(m->work);
+            m->work = nullptr;
+            m->work_cap = 0;
+            if (hipMalloc(&m->work, (size_t)(max1 + max2) * sizeof(MmWork)) != hipSuccess)
+                return c->fail(MYL_E_NOMEM, "moe work");
+            m->work_cap = max1 + max2;
+        }
+        moe_plan_kernel<<<1, 256, 0, st>>>(m->counts, E, bm_log, bn, nt1, nt2, max1, m->offsets, m->work, m->nwork);
+        moe_dispatch_kernel<<<E, 256, 0, st>>>(m->ids, T, K, m->offsets, m->list_tok, m->slotpos);
         int8_t* Xp = reinterpret_cast<int8_t*>(m->Xg);
         int8_t* Hp = reinterpret_cast<int8_t*>(m->Hh);
         moe_gather_planes_kernel<<<R, 256, 0, st>>>(x_dev, H, m->list_tok, Xp);
         if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe dispatch");
         EpiExpertGUSiluPlanes eg{m->sgu, 2 * I, m->silu, (uint32_t)m->silu_len, Hp};
-        if ((e = moe_grouped_staged(tile, Xp, m->wgu, (size_t)2 * I * H, 2 * I, H, m->offsets, m->work,
-                                    (int)wgu.size(), eg, st)) != hipSuccess)
+        if ((e = moe_grouped_staged(tile, Xp, m->wgu, (size_t)2 * I * H, 2 * I, H, m->offsets, m->work, m->nwork, max1,
+                                    eg, st)) != hipSuccess)
             return c->hip(e, "moe gate/up");
         EpiExpertDown ed{m->sd, m->out_frac, H, m->Y};
-        if ((e = moe_grouped(tile, Hp, m->wd, (size_t)H * I, H, I, m->offsets, m->work + wgu.size(), (int)wdn.size(),
-                             ed, st)) != hipSuccess)
+        if ((e = moe_grouped(tile, Hp, m->wd, (size_t)H * I, H, I, m->offsets, m->work + max1, m->nwork + 1, max2, ed,
+                             st)) != hipSuccess)
             return c->hip(e, "moe down");
     } else {
+        // int16-row expert products (K not a multiple of 64): the work tables
+        // are built on the host from the counts (the one synchronisation)
+        m->counts_host.assign(E, 0);
+        rc = c->hip(hipMemcpyAsync(m->counts_host.data(), m->counts, (size_t)E * 4, hipMemcpyDeviceToHost, st),
+                    "counts");
+        if (!rc) rc = c->hip(hipStreamSynchronize(st), "counts");
+        if (rc) return rc;
+        std::vector<int32_t> offs(E + 1, 0);
+        for (int x = 0; x < E; ++x) offs[x + 1] = offs[x] + m->counts_host[x];
+        using GT = MmShape<1, 2, 2, 2>;
+        std::vector<MmWork> wgu, wdn;
+        work_table(m->counts_host, GT::BM, GT::BN, 2 * I, wgu);
+        work_table(m->counts_host, GT::BM, GT::BN, H, wdn);
+        const int need = (int)(wgu.size() + wdn.size());
+        if (need > m->work_cap) {
+            if (m->work) (void)hipFree(m->work);
+            m->work = nullptr;
+            m->work_cap = 0;
+            if (hipMalloc(&m->work, (size_t)need * sizeof(MmWork)) != hipSuccess) return c->fail(MYL_E_NOMEM, "moe work");
+            m->work_cap = need;
+        }
+        std::vector<MmWork> all(wgu);
+        all.insert(all.end(), wdn.begin(), wdn.end());
+        rc = c->hip(hipMemcpyAsync(m->work, all.data(), all.size() * sizeof(MmWork), hipMemcpyHostToDevice, st), "work");
+        if (!rc) rc = c->hip(hipMemcpyAsync(m->offsets, offs.data(), offs.size() * 4, hipMemcpyHostToDevice, st), "offs");
+        if (rc) return rc;
+        moe_dispatch_kernel<<<E, 256, 0, st>>>(m->ids, T, K, m->offsets, m->list_tok, m->slotpos);
         moe_gather_kernel<<<R, 256, 0, st>>>(x_dev, H, m->list_tok, m->Xg);
         if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe dispatch");
-    }
-    if (!planes && !wgu.empty()) {
-        EpiExpertGU eg{m->sgu, 2 * I, m->GU};
-        mm_w8_grouped_kernel<1, 2, 2, 2, EpiExpertGU><<<8 * (((int)wgu.size() + 7) / 8), GT::kThreads, GT::kLds, st>>>(
-            m->Xg, H, m->wgu, (size_t)2 * I * H, 2 * I, H, m->offsets, m->work, (int)wgu.size(), eg);
-        if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe gate/up");
-        moe_silu_kernel<<<dim3((I / 8 + 255) / 256, R), 256, 0, st>>>(m->GU, I, m->silu, (uint32_t)m->silu_len, m->Hh);
-        EpiExpertDown ed{m->sd, m->out_frac, H, m->Y};
-        mm_w8_grouped_kernel<1, 2, 2, 2, EpiExpertDown><<<8 * (((int)wdn.size() + 7) / 8), GT::kThreads, GT::kLds, st>>>(
-            m->Hh, I, m->wd, (size_t)H * I, H, I, m->offsets, m->work + wgu.size(), (int)wdn.size(), ed);
-        if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe down");
+        if (!wgu.empty()) {
+            EpiExpertGU eg{m->sgu, 2 * I, m->GU};
+            mm_w8_grouped_kernel<1, 2, 2, 2, EpiExpertGU><<<8 * (((int)wgu.size() + 7) / 8), GT::kThreads, GT::kLds,
+                                                             st>>>(m->Xg, H, m->wgu, (size_t)2 * I * H, 2 * I, H,
+                                                                   m->offsets, m->work, (int)wgu.size(), eg);
+            if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe gate/up");
+            moe_silu_kernel<<<dim3((I / 8 + 255) / 256, R), 256, 0, st>>>(m->GU, I, m->silu, (uint32_t)m->silu_len,
+                                                                          m->Hh);
+            EpiExpertDown ed{m->sd, m->out_frac, H, m->Y};
+            mm_w8_grouped_kernel<1, 2, 2, 2, EpiExpertDown><<<8 * (((int)wdn.size() + 7) / 8), GT::kThreads, GT::kLds,
+                                                               st>>>(m->Hh, I, m->wd, (size_t)H * I, H, I, m->offsets,
+                                                                     m->work + wgu.size(), (int)wdn.size(), ed);
+            if ((e = hipGetLastError()) != hipSuccess) return c->hip(e, "moe down");
+        }
     }
     // shared expert: dense products over every token.  With byte planes the
     // gate/up product's staged epilogue applies the SiLU gate and writes the
