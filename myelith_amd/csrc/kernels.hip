@@ -459,22 +459,43 @@ __global__ __launch_bounds__(kBlock) void argmax_kernel(const int32_t* __restric
 //   m = max z;  S = sum_j lut[(m - z_j) << 2] (0 past the table; logits are
 //   Q6 and the exp LUT's input is Q8);  lp = (z_target - m) * 2^10 - ln_q16(S)
 // in Q16.  One block per row; targets < 0 give 0.
+constexpr int kLogsoftmaxLds = 4096;  // exp-table entries a block copies to LDS (8 KB)
 __global__ __launch_bounds__(kBlock) void logsoftmax_kernel(const int32_t* __restrict__ z, int n, int ldz,
                                                            const int16_t* __restrict__ lut, uint32_t lut_len,
                                                            const int64_t* __restrict__ targets,
                                                            int64_t* __restrict__ out) {
     __shared__ int32_t red32[kBlock / 64];
     __shared__ uint64_t red64[kBlock / 64];
+    __shared__ int16_t elut[kLogsoftmaxLds];
     const int32_t* row = z + (size_t)blockIdx.x * ldz;
+    // the table's first entries in LDS (the exp table is zero past a short
+    // prefix, so nearly every lookup is served there); the rest from memory
+    const int nl = (int)min(lut_len, (uint32_t)kLogsoftmaxLds);
+    for (int i = threadIdx.x; i < nl; i += kBlock) elut[i] = lut[i];
+    // 16-byte loads over the aligned part of the row, four in flight per thread
+    const int n4 = ((uintptr_t)row & 15) == 0 ? n >> 2 : 0;
+    const int4* row4 = reinterpret_cast<const int4*>(row);
     int32_t mx = INT32_MIN;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) mx = max(mx, row[i]);
-    const int32_t m = block_max_i32(mx, red32);
-    constexpr uint32_t sh = MYL_TV_EXP_INPUT_FRAC - MYL_TV_LOGIT_FRAC_BITS;
-    int64_t s = 0;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const uint64_t d = (uint64_t)((int64_t)m - (int64_t)row[i]) << sh;
-        s += d < lut_len ? (int64_t)lut[d] : 0;
+#pragma unroll 4
+    for (int i = threadIdx.x; i < n4; i += kBlock) {
+        const int4 v = row4[i];
+        mx = max(mx, max(max(v.x, v.y), max(v.z, v.w)));
     }
+    for (int i = 4 * n4 + threadIdx.x; i < n; i += kBlock) mx = max(mx, row[i]);
+    const int32_t m = block_max_i32(mx, red32);  // its barrier also publishes elut
+    constexpr uint32_t sh = MYL_TV_EXP_INPUT_FRAC - MYL_TV_LOGIT_FRAC_BITS;
+    auto term = [&](int32_t zi) -> int64_t {
+        const uint64_t d = (uint64_t)((int64_t)m - (int64_t)zi) << sh;
+        if (d < (uint64_t)nl) return (int64_t)elut[d];
+        return d < lut_len ? (int64_t)lut[d] : 0;
+    };
+    int64_t s = 0;
+#pragma unroll 4
+    for (int i = threadIdx.x; i < n4; i += kBlock) {
+        const int4 v = row4[i];
+        s += term(v.x) + term(v.y) + term(v.z) + term(v.w);
+    }
+    for (int i = 4 * n4 + threadIdx.x; i < n; i += kBlock) s += term(row[i]);
     s = wave_sum_i64(s);
     if ((threadIdx.x & 63) == 0) red64[threadIdx.x >> 6] = (uint64_t)s;
     __syncthreads();
@@ -507,7 +528,18 @@ __global__ __launch_bounds__(kBlock) void argmax_part_kernel(const int32_t* __re
     const int32_t* row = v + (size_t)blockIdx.y * ldv;
     const int i0 = blockIdx.x * kArgChunk, i1 = min(n, i0 + kArgChunk);
     uint64_t best = 0;
-    for (int i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+    // 16-byte loads when the chunk starts aligned (kArgChunk is a multiple
+    // of 4), the chunk's last partial quad and unaligned rows one by one
+    const int q1 = ((uintptr_t)(row + i0) & 15) == 0 ? i0 + ((i1 - i0) & ~3) : i0;
+#pragma unroll 4
+    for (int i = i0 + 4 * (int)threadIdx.x; i < q1; i += 4 * kBlock) {
+        const int4 q = *reinterpret_cast<const int4*>(row + i);
+        const uint64_t k0 = argmax_key(q.x, (uint32_t)i), k1 = argmax_key(q.y, (uint32_t)i + 1);
+        const uint64_t k2 = argmax_key(q.z, (uint32_t)i + 2), k3 = argmax_key(q.w, (uint32_t)i + 3);
+        const uint64_t a = k0 > k1 ? k0 : k1, b = k2 > k3 ? k2 : k3, c = a > b ? a : b;
+        best = c > best ? c : best;
+    }
+    for (int i = q1 + threadIdx.x; i < i1; i += kBlock) {
         const uint64_t key = argmax_key(row[i], (uint32_t)i);
         best = key > best ? key : best;
     }
