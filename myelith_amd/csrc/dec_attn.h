@@ -1,6 +1,18 @@
 // dec_attn.h -- integer attention of one query row per KV cache
 // (attention.rs:42-90 with softmax.rs:12-64): the decode step's attention.
-// A block covers one query head and kChunk positions.
+//
+// Two kernels per layer:
+//   scores  (query head, kChunk positions): z_j = (i32)RNE(q . k_j * mult, shift)
+//   P.V     (query head, kPvWide positions): the head's max and exp-LUT sum
+//           over all L scores, the chunk's probabilities, and the exact
+//           partial sum_j p_j v_j of the chunk added to the output with one
+//           atomic per dim.
+// The query heads of a KV head (GQA, model.rs:508-511) run back to back on
+// one XCD, so a chunk's K or V rows come from HBM once into that L2.
+// dec_pv_wide accumulates in i32, which is exact when every exp-table entry
+// is non-negative: then 0 <= p_j <= 2^14 and sum_j p_j <= 2^14 + L/2, so
+// |sum_j p_j v_j| < 2^31 for L <= 65536 and wrapping partial sums add up to
+// the exact total.  Other tables take dec_pv (kChunk positions, i64).
 #pragma once
 
 #include "bufload.h"
@@ -272,6 +284,153 @@ __device__ inline void dec_pv(int L, int base, const int32_t* __restrict__ z, in
 #pragma unroll
         for (int k = 0; k < STREAMS; ++k) sum = wadd64(sum, red[k][tid]);
         atomicAdd(acc + tid, (unsigned long long)sum);
+    }
+}
+
+// ---- wide P.V chunks, i32 ----------------------------------------------------
+
+constexpr int kPvWide = 256;  // positions per block of dec_pv_wide
+
+// The exact partial P.V of kPvWide positions for one query head
+// (attention.rs:75-81 with softmax.rs:12-64), for exp tables without a
+// negative entry whose nonzero prefix fits the LDS copy (exp_lds <=
+// kDecExpLds) and L <= 65536.  The block computes the head's max m and
+// wrapping exp-LUT sum S over all L scores (every chunk's block recomputes
+// them: four or so scores per thread), the chunk's probabilities
+// p_j = RNE(e_j 2^14 / S) (the uniform split when S == 0) into LDS, then
+// thread (wave w, lane) holds 8 dims of the V rows rg + NRG i of its row
+// group rg = RS w + lane / (HD / 8) and takes their products with the
+// probabilities on v_dot2_i32_i16, two rows per instruction; the row groups
+// are summed in LDS and one 32-bit atomic per dim adds the chunk to acc[0 ..
+// HD).  Every global load is issued before any is used, through buffer
+// descriptors (past the range a load reads zero).  512 threads.
+template <int HD>
+__device__ inline void dec_pv_wide(int L, int base, const int32_t* __restrict__ z, int zlen,
+                                   const int16_t* __restrict__ vg, const int16_t* __restrict__ lut, uint32_t lut_len,
+                                   uint8_t lut_shift, int exp_lds, int32_t* __restrict__ acc) {
+    constexpr int C = kPvWide;
+    constexpr int OPR = HD / 8;     // lanes per V row, 8 dims each
+    constexpr int RS = 64 / OPR;    // rows per wave load
+    constexpr int NRG = 8 * RS;     // row groups of the block
+    constexpr int PR = C / NRG;     // rows per thread
+    constexpr int ZV = 2;           // 4-score vectors per thread in registers (L <= 4096)
+    static_assert(PR % 2 == 0 && C <= 512, "row pairs; one probability per thread");
+    static_assert(kDecExpLds == 8 * 512, "one 16-byte table piece per thread");
+    __shared__ __align__(16) int16_t elut[kDecExpLds];
+    __shared__ __align__(16) int16_t plt[NRG][PR];
+    __shared__ __align__(16) int32_t red[NRG][HD];
+    __shared__ int32_t redm[8];
+    __shared__ uint32_t reds[8];
+    const int tid = (int)threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // loads: the table's nonzero prefix, the scores (all L, and this
+    // thread's chunk position), then the chunk's V rows
+    const __amdgpu_buffer_rsrc_t rl = weight_rsrc(lut, (uint32_t)((exp_lds + 7) & ~7) * 2u);
+    const uint4 lv = cload16(rl, (uint32_t)tid * 16u);
+    const int32_t lut0 = (int16_t)(cload4(weight_rsrc(lut, ((lut_len + 7u) & ~7u) * 2u), 0) & 0xFFFFu);
+    const __amdgpu_buffer_rsrc_t rz = weight_rsrc(z, (uint32_t)min(zlen, L) * 4u);
+    uint4 zv[ZV];
+#pragma unroll
+    for (int i = 0; i < ZV; ++i) zv[i] = cload16(rz, (uint32_t)(tid + 512 * i) * 16u);
+    const int32_t zown = (int32_t)cload4(rz, (uint32_t)(base + tid) * 4u);  // used for tid < C
+    __builtin_amdgcn_sched_barrier(0);
+    const int oc = lane % OPR, rg = w * RS + lane / OPR;
+    const __amdgpu_buffer_rsrc_t rv = weight_rsrc(vg, (uint32_t)L * HD * 2u);
+    uint4 vv[PR];
+#pragma unroll
+    for (int i = 0; i < PR; ++i) vv[i] = cload16(rv, ((uint32_t)(base + rg + NRG * i) * HD + 8 * oc) * 2u);
+    *reinterpret_cast<uint4*>(elut + tid * 8) = lv;  // read after the max's barrier
+    const int32_t lut_one = lut_len > 0 ? lut0 : 1;
+    const uint32_t sh = lut_shift & 31u;
+    auto zat = [](const uint4& v, int e) { return (int32_t)(e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w); };
+    const bool regs = L <= 2048 * ZV;
+    const int nzv = (L + 2047) >> 11;  // score vectors holding positions below L
+    int32_t mx = INT32_MIN;
+    if (regs) {
+#pragma unroll
+        for (int i = 0; i < ZV; ++i)
+            if (i < nzv) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (4 * (tid + 512 * i) + e < L) mx = max(mx, zat(zv[i], e));
+            }
+    } else {
+        for (int j = tid; j < L; j += 512) mx = max(mx, z[j]);
+    }
+    mx = block_max_i32_dpp(mx, redm);  // also makes the table copy visible
+    // exp_lookup (softmax.rs:12-20) of a score zj <= mx from the LDS copy:
+    // the saturating difference is min(mx - zj, 2^31 - 1) (mx - zj is in
+    // [0, 2^32) as an unsigned word), entries from exp_lds on are zero, and
+    // the read is issued whatever the entry, then selects
+    auto ex = [&](int32_t zj) -> int32_t {
+        const uint32_t x = min((uint32_t)mx - (uint32_t)zj, 0x7FFFFFFFu);
+        const uint32_t idx = x >> sh;
+        const bool in = idx < (uint32_t)exp_lds;
+        const int32_t t = elut[in ? idx : 0u];
+        return x == 0 ? lut_one : (in ? t : 0);
+    };
+    uint32_t s = 0;
+    if (regs) {
+#pragma unroll
+        for (int i = 0; i < ZV; ++i)
+            if (i < nzv) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t v = (uint32_t)ex(zat(zv[i], e));
+                    s += 4 * (tid + 512 * i) + e < L ? v : 0u;
+                }
+            }
+    } else {
+        for (int j = tid; j < L; j += 512) s += (uint32_t)ex(z[j]);
+    }
+    const int32_t eown = ex(zown);  // this thread's numerator (used below L), ahead of the sum's barrier
+    // block-uniform: the reciprocal runs on the scalar unit, ahead of the
+    // per-thread branch.  S > 0 is a sum of non-negative entries below
+    // 2^31; S == 0 takes the uniform split 2^14 = ubase L + urem.
+    const int32_t S = __builtin_amdgcn_readfirstlane((int32_t)block_sum_u32_dpp(s, reds));
+    const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
+    const uint32_t den = S == 0 ? (uint32_t)L : (uint32_t)S;
+    const uint32_t rs = recip32_u32(den);
+    int32_t ubase = 0, urem = 0;
+    if (S == 0) {
+        uint32_t qq, rr;
+        udivmod32((uint32_t)one, (uint32_t)L, recip32((uint32_t)L), &qq, &rr);
+        ubase = (int32_t)qq;
+        urem = wsub32(one, wmul32(ubase, L));
+    }
+    if (tid < C) {
+        const int j = base + tid;
+        int32_t pv = 0;
+        if (j < L)
+            pv = S == 0 ? ubase + (((uint64_t)j < (uint64_t)(int64_t)urem) ? 1 : 0)
+                        : softmax_div_round_pos(eown << MYL_TV_PROB_FRAC_BITS, S, rs);
+        plt[tid % NRG][tid / NRG] = (int16_t)pv;
+    }
+    __syncthreads();
+    typedef short __attribute__((ext_vector_type(2))) s2;
+    auto d2 = [](uint32_t a, uint32_t c, int32_t t) {
+        return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, a), __builtin_bit_cast(s2, c), t, false);
+    };
+    int32_t a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const uint32_t* pw = reinterpret_cast<const uint32_t*>(&plt[rg][0]);
+#pragma unroll
+    for (int k = 0; k < PR / 2; ++k) {
+        const uint32_t pp = pw[k];  // probabilities of rows 2k, 2k + 1
+        const uint32_t ra[4] = {vv[2 * k].x, vv[2 * k].y, vv[2 * k].z, vv[2 * k].w};
+        const uint32_t rb[4] = {vv[2 * k + 1].x, vv[2 * k + 1].y, vv[2 * k + 1].z, vv[2 * k + 1].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            a[2 * t] = d2(pp, (ra[t] & 0xFFFFu) | (rb[t] << 16), a[2 * t]);
+            a[2 * t + 1] = d2(pp, (ra[t] >> 16) | (rb[t] & 0xFFFF0000u), a[2 * t + 1]);
+        }
+    }
+    *reinterpret_cast<int4*>(&red[rg][8 * oc]) = make_int4(a[0], a[1], a[2], a[3]);
+    *reinterpret_cast<int4*>(&red[rg][8 * oc + 4]) = make_int4(a[4], a[5], a[6], a[7]);
+    __syncthreads();
+    if (tid < HD) {
+        uint32_t t = 0;
+#pragma unroll
+        for (int r = 0; r < NRG; ++r) t += (uint32_t)red[r][tid];
+        atomicAdd(acc + tid, (int)t);
     }
 }
 

@@ -84,21 +84,20 @@ __global__ void gen_w16_kernel(int16_t* __restrict__ dst, int row0, int K, uint6
 
 
 
-// Block-level sum of per-thread limbs; thread 0 gets the totals.
+// Block-level sum of per-thread limbs; the first wave (thread 0 among it)
+// gets the totals, reading the per-wave slots in parallel.
 __device__ inline void block_sum_limbs(uint64_t (&l)[3], uint64_t* red /* [16][3] */) {
 #pragma unroll
     for (int j = 0; j < 3; ++j) l[j] = wave_sum_u64(l[j]);
-    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6, lane = threadIdx.x & 63;
     __syncthreads();
-    if ((threadIdx.x & 63) == 0)
+    if (lane == 0)
         for (int j = 0; j < 3; ++j) red[w * 3 + j] = l[j];
     __syncthreads();
-    if (threadIdx.x == 0)
-        for (int j = 0; j < 3; ++j) {
-            uint64_t s = 0;
-            for (int i = 0; i < nw; ++i) s += red[i * 3 + j];
-            l[j] = s;
-        }
+    if (w == 0) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) l[j] = wave_sum_u64(lane < nw ? red[lane * 3 + j] : 0ull);
+    }
 }
 
 // Writes the norm sum of an n-vector computed by one block into slot 0 of acc
@@ -189,9 +188,10 @@ struct SrcNorm {
         uint64_t l[3];
 #pragma unroll
         for (int j = 0; j < 3; ++j) l[j] = wave_sum_u64(q.a[j]);
-        if (threadIdx.x == 0) {
+        if (threadIdx.x < 64) {  // wave 0, every lane: the table entry is a wave-wide search
             const myl_i128 a = (myl_i128)((myl_u128)l[0] + ((myl_u128)l[1] << 42) + ((myl_u128)l[2] << 84));
-            sf = rms_factor_of(a, ref, p);
+            const RmsFactor f = rms_factor_wave(a, ref, p);
+            if (threadIdx.x == 0) sf = f;
         }
         __syncthreads();
         return sf;
@@ -239,31 +239,42 @@ struct SrcNorm {
 };
 
 // Staging source: attention output from the exact P.V accumulator
-// (attention.rs:84-86 then model.rs:563-567).
+// (attention.rs:84-86 then model.rs:563-567): i64 sums (Acc = unsigned long
+// long, the general P.V kernel) or i32 sums (Acc = int32_t, the GQA kernel,
+// exact where it runs).
+template <class Acc>
 struct SrcAttn {
-    const unsigned long long* acc;
+    const Acc* acc;
     uint8_t v_frac, out_frac;
-    // the first chunk of each thread: 8 accumulators as four 16-byte pieces
+    static constexpr int kPieces = (int)sizeof(Acc) / 2;  // 16-byte pieces of 8 accumulators
+    // the first chunk of each thread: 8 accumulators
     struct Pre {
-        uint4 a[4];
+        uint4 a[kPieces];
     };
     __device__ inline Pre pre(int K, int kpad, int nthr) const {
         Pre q;
-        const __amdgpu_buffer_rsrc_t r = weight_rsrc(acc, 8u * (uint32_t)K);
+        const __amdgpu_buffer_rsrc_t r = weight_rsrc(acc, (uint32_t)sizeof(Acc) * (uint32_t)K);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) q.a[t] = cload16(r, threadIdx.x * 64u + 16u * t);
+        for (int t = 0; t < kPieces; ++t) q.a[t] = cload16(r, threadIdx.x * (8u * (uint32_t)sizeof(Acc)) + 16u * t);
         return q;
     }
-    __device__ inline void values8(const uint4 (&a4)[4], int16_t (&v)[8]) const {
-        uint64_t a[8];
+    __device__ inline void values8(const uint4 (&a4)[kPieces], int16_t (&v)[8]) const {
+        int64_t a[8];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            a[2 * t] = ((uint64_t)a4[t].y << 32) | a4[t].x;
-            a[2 * t + 1] = ((uint64_t)a4[t].w << 32) | a4[t].z;
+        for (int t = 0; t < kPieces; ++t) {
+            if (sizeof(Acc) == 8) {
+                a[2 * t] = (int64_t)(((uint64_t)a4[t].y << 32) | a4[t].x);
+                a[2 * t + 1] = (int64_t)(((uint64_t)a4[t].w << 32) | a4[t].z);
+            } else {
+                a[4 * t] = (int32_t)a4[t].x;
+                a[4 * t + 1] = (int32_t)a4[t].y;
+                a[4 * t + 2] = (int32_t)a4[t].z;
+                a[4 * t + 3] = (int32_t)a4[t].w;
+            }
         }
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const int16_t r = clamp_i16_i64(rshift_round64((int64_t)a[t], MYL_TV_PROB_FRAC_BITS));
+            const int16_t r = clamp_i16_i64(rshift_round64(a[t], MYL_TV_PROB_FRAC_BITS));
             v[t] = clamp_i16(rescale32((int32_t)r, v_frac, out_frac));
         }
     }
@@ -281,7 +292,9 @@ struct SrcAttn {
             const int k0 = i * 8;
             if (k0 < K) {
                 const uint4* a4 = reinterpret_cast<const uint4*>(acc + k0);
-                const uint4 w[4] = {a4[0], a4[1], a4[2], a4[3]};
+                uint4 w[kPieces];
+#pragma unroll
+                for (int t = 0; t < kPieces; ++t) w[t] = a4[t];
                 values8(w, v);
             } else {
 #pragma unroll
@@ -297,15 +310,18 @@ struct SrcAttn {
 // ---------------------------------------------------------------------------
 
 // mode 0: token/pos from the arguments; mode 1: greedy continuation (token =
-// argmax of the previous step, pos + 1).  Resets the argmax key for this step
+// argmax of the previous step, pos + 1).  Resets the argmax key for this step,
+// copies the step's RoPE row (cos then sin, half entries each) to rope_cur
 // and seeds the first layer's input-norm accumulator.
 __global__ __launch_bounds__(1024) void embed_kernel(DecodeState* st, int mode, int token_arg, int pos_arg,
                                                      uint32_t rope_rows, int vocab, const int8_t* __restrict__ E,
                                                      const uint8_t* __restrict__ emb_shifts,
                                                      const uint8_t* __restrict__ res_frac0, uint8_t ref0, int H,
                                                      int64_t* __restrict__ tokens_out, int16_t* __restrict__ hidden,
-                                                     NormAcc* norm_acc) {
-    __shared__ int32_t s_tok;
+                                                     NormAcc* norm_acc, const int16_t* __restrict__ cos_lut,
+                                                     const int16_t* __restrict__ sin_lut, int half,
+                                                     int16_t* __restrict__ rope_cur) {
+    __shared__ int32_t s_tok, s_row;
     __shared__ uint64_t red[16 * 3];
     if (threadIdx.x == 0) {
         int32_t tok, pos;
@@ -320,14 +336,20 @@ __global__ __launch_bounds__(1024) void embed_kernel(DecodeState* st, int mode, 
             if (tokens_out) tokens_out[st->step] = tok;
             st->step = st->step + 1;
         }
+        const int32_t row = (int32_t)umod32_slow((uint32_t)pos, rope_rows);
         st->token = tok;
         st->pos = pos;
-        st->rope_row = (int32_t)umod32_slow((uint32_t)pos, rope_rows);
+        st->rope_row = row;
         st->argmax_key = 0;
         s_tok = tok;
+        s_row = row;
     }
     __syncthreads();
     const int tok = s_tok;
+    if ((int)threadIdx.x < 2 * half) {
+        const int i = (int)threadIdx.x % half;
+        rope_cur[threadIdx.x] = ((int)threadIdx.x < half ? cos_lut : sin_lut)[(size_t)s_row * half + i];
+    }
     const int8_t* row = E + (size_t)tok * H;
     const uint8_t sh = emb_shifts[tok];
     uint64_t l[3] = {0, 0, 0};
@@ -348,28 +370,57 @@ __global__ __launch_bounds__(1024) void embed_kernel(DecodeState* st, int mode, 
 // ---------------------------------------------------------------------------
 
 // q/k/v projection rows (pair-ordered) -> bias -> RoPE -> q buffer / KV cache.
+// The step's RoPE row is in rope (cos [hd / 2] then sin [hd / 2], written by
+// the embedding kernel), so every operand of a group is a load that depends
+// on nothing: the lane's first group's operands (shifts, biases, rotation,
+// position) load right after the first weight batch and are in registers
+// when the stream ends.
 struct EpiQKV {
     const uint8_t* shifts;    // per device row
     const int16_t* bias;      // per device row, or null
     const uint8_t* bias_sh;
     uint8_t act_frac, q_frac, k_frac, v_frac;
     int nq, nkv, hd_log, max_pos;
-    const int16_t* cos_lut;
-    const int16_t* sin_lut;
+    const int16_t* rope;
     const DecodeState* st;
     int16_t* q_out;           // [nq]
     int16_t* kc;              // layer base [kv_heads][max_pos][hd]
     int16_t* vc;
-    using State = NoState;
-    __device__ inline void begin(State&) const {}
-    // the per-row operands load in group(): loading them early measured
-    // slower (the RoPE entries depend on the step's row)
-    __device__ inline void prefetch(State&, int, int) const {}
+    struct State {
+        int row0, pos;
+        uint8_t sh[2], bs[2];
+        int16_t b[2], c, s;
+    };
+    __device__ inline void begin(State& s) const { s.row0 = -1; }
+    // through buffer descriptors: no branch (a missing bias is a zero-length
+    // range that reads zero), so the staging's wait for its own earlier
+    // loads stays exact
+    __device__ inline void prefetch(State& s, int row0, int N) const {
+        const int r = min(row0, N - 2);  // N is even (RoPE pairs): r is even
+        const int hd = 1 << hd_log, half = hd >> 1;
+        const int p = ((r - (r < nq ? 0 : (r < nq + nkv ? nq : nq + nkv))) & (hd - 1)) >> 1;
+        const uint32_t sh2 = cload2(weight_rsrc(shifts, (uint32_t)N), (uint32_t)r);
+        const uint32_t b2 = cload4(weight_rsrc(bias, bias ? 2u * (uint32_t)N : 0u), 2u * (uint32_t)r);
+        const uint32_t bs2 = cload2(weight_rsrc(bias_sh, bias ? (uint32_t)N : 0u), (uint32_t)r);
+        const __amdgpu_buffer_rsrc_t rr = weight_rsrc(rope, 4u * (uint32_t)half);
+        const uint32_t c = cload2(rr, 2u * (uint32_t)p), sn = cload2(rr, 2u * (uint32_t)(half + p));
+        s.pos = (int)cload4(weight_rsrc(st, sizeof(DecodeState)), (uint32_t)offsetof(DecodeState, pos));
+        s.sh[0] = (uint8_t)sh2;
+        s.sh[1] = (uint8_t)(sh2 >> 8);
+        s.b[0] = (int16_t)(b2 & 0xFFFFu);
+        s.b[1] = (int16_t)(b2 >> 16);
+        s.bs[0] = (uint8_t)bs2;
+        s.bs[1] = (uint8_t)(bs2 >> 8);
+        s.c = (int16_t)c;
+        s.s = (int16_t)sn;
+        s.row0 = row0;
+    }
     __device__ inline void finish(State&) const {}
     template <int R>
-    __device__ inline void group(State&, int row0, int N, const int64_t (&tot)[R]) const {
+    __device__ inline void group(State& s, int row0, int N, const int64_t (&tot)[R]) const {
         static_assert(R == 2, "the RoPE pair needs two rows per group");
         if (row0 >= N) return;
+        const bool pre = s.row0 == row0;
         const int seg = row0 < nq ? 0 : (row0 < nq + nkv ? 1 : 2);
         const int e = row0 - (seg == 0 ? 0 : (seg == 1 ? nq : nq + nkv));
         const uint8_t frac = seg == 0 ? q_frac : (seg == 1 ? k_frac : v_frac);
@@ -380,17 +431,22 @@ struct EpiQKV {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const int d = row0 + t;
-            int16_t v = clamp_i16_i64(rescale64(tot[t], (uint8_t)(shifts[d] + act_frac), frac));
-            if (bias) v = clamp_i16_i64((int64_t)v + (int64_t)rescale32((int32_t)bias[d], bias_sh[d], frac));
+            const uint8_t sh = pre ? s.sh[t] : shifts[d];
+            int16_t v = clamp_i16_i64(rescale64(tot[t], (uint8_t)(sh + act_frac), frac));
+            if (bias) {
+                const int16_t b = pre ? s.b[t] : bias[d];
+                const uint8_t bs = pre ? s.bs[t] : bias_sh[d];
+                v = clamp_i16_i64((int64_t)v + (int64_t)rescale32((int32_t)b, bs, frac));
+            }
             y[t] = v;
         }
-        const int pos = st->pos;
+        const int pos = pre ? s.pos : st->pos;
         if (seg < 2) {
-            const int32_t c = cos_lut[(size_t)st->rope_row * half + p];
-            const int32_t s = sin_lut[(size_t)st->rope_row * half + p];
+            const int32_t c = pre ? s.c : rope[p];
+            const int32_t sn = pre ? s.s : rope[half + p];
             const int32_t x0 = y[0], x1 = y[1];
-            y[0] = clamp_i16(rshift_round32(wsub32(wmul32(x0, c), wmul32(x1, s)), MYL_TV_ROPE_FRAC_BITS));
-            y[1] = clamp_i16(rshift_round32(wadd32(wmul32(x1, c), wmul32(x0, s)), MYL_TV_ROPE_FRAC_BITS));
+            y[0] = clamp_i16(rshift_round32(wsub32(wmul32(x0, c), wmul32(x1, sn)), MYL_TV_ROPE_FRAC_BITS));
+            y[1] = clamp_i16(rshift_round32(wadd32(wmul32(x1, c), wmul32(x0, sn)), MYL_TV_ROPE_FRAC_BITS));
         }
         int16_t* dst;
         if (seg == 0) dst = q_out + (size_t)head * hd;
@@ -553,7 +609,7 @@ struct EpiHead {
 // decode attention over the KV cache (attention.rs:42-90), GQA (model.rs:508-511)
 // ---------------------------------------------------------------------------
 
-// Launch shape shared by the two attention kernels, 256 threads.  Workgroups
+// Launch shape of the attention kernels, one query head per block.  Workgroups
 // are dispatched to the 8 XCDs round robin in linear-id order, and each XCD
 // has its own L2.  With kv_heads dividing 8 (xs_log = log2(8 / kv_heads)):
 // grid 8 * G * ceil(chunks / 2^xs_log); block x, with k = x >> 3 (the XCD's
@@ -598,6 +654,27 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(const DecodeState* __r
                    scores + (size_t)head * score_ld);
 }
 
+// P.V of one query head over kPvWide positions (dec_pv_wide), i32 partials
+// into acc.  512 threads; AttnBlock over chunks of kPvWide positions.
+template <int HD>
+__global__ __launch_bounds__(512) void attn_pv_wide_kernel(const DecodeState* __restrict__ st,
+                                                          const int32_t* __restrict__ scores,
+                                                          const int16_t* __restrict__ vc, int max_pos, int score_ld,
+                                                          int G, int chunks, const int16_t* __restrict__ lut,
+                                                          uint32_t lut_len, uint8_t lut_shift, int exp_lds,
+                                                          int32_t* __restrict__ acc, int xs_log, uint32_t ginv) {
+    const AttnBlock b(xs_log, G, ginv);
+    if (b.c >= chunks) return;
+    const int L = st->pos + 1;
+    const int base = b.c * kPvWide;
+    if (base >= L) return;
+    const int head = b.g * G + b.h;
+    dec_pv_wide<HD>(L, base, scores + (size_t)head * score_ld, score_ld, vc + (size_t)b.g * max_pos * HD, lut,
+                    lut_len, lut_shift, exp_lds, acc + (size_t)head * HD);
+}
+
+// The general P.V kernel (dec_pv): one query head and kChunk positions, i64
+// partials into acc.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_pv_kernel(const DecodeState* __restrict__ st,
                                                      const int32_t* __restrict__ scores,
@@ -726,6 +803,11 @@ int alloc_impl(myl_model* m, const myl_luts* luts) {
             m->exp_nz = i + 1;
             break;
         }
+    // the wide P.V kernel accumulates in i32: exact for a table without
+    // negative entries (dec_attn.h) whose nonzero prefix fits its LDS copy
+    m->pv32 = m->exp_nz <= kDecExpLds && m->max_pos <= 65536;
+    for (size_t i = 0; i < luts->exp_len && m->pv32; ++i)
+        if (luts->exp[i] < 0) m->pv32 = false;
     // a table equal to its closed form at every entry is computed in the
     // norm setup instead of read: the read is a dependent load that waits
     // behind the weight stream the kernel has already issued
@@ -849,6 +931,8 @@ int alloc_impl(myl_model* m, const myl_luts* luts) {
     m->norm_a = m->dalloc<NormAcc>(1);
     m->norm_b = m->dalloc<NormAcc>(1);
     m->state = m->dalloc<DecodeState>(1);
+    m->rope_cur = m->dalloc<int16_t>(hd);
+    if (!m->rope_cur) return c->fail(MYL_E_NOMEM, "activation allocation");
     if (!m->kcache || !m->vcache || !m->hidden || !m->norm || !m->q || !m->attn || !m->resid || !m->h ||
         !m->logits || !m->scores || !m->attn_acc || !m->state || !m->norm_a || !m->norm_b)
         return c->fail(MYL_E_NOMEM, "activation allocation");
@@ -1020,7 +1104,7 @@ hipError_t layer_step(myl_model* m, int l) {
     {
         const size_t layer_kv = (size_t)l * kvh * m->max_pos * hd;
         EpiQKV q{L.sqkv, L.bqkv, L.bsqkv, f.norm_attn_frac, f.q_frac, f.k_frac, f.v_frac, nq, nkv, m->hd_log,
-                 m->max_pos, m->cos_lut, m->sin_lut, m->state, m->q, m->kcache + layer_kv, m->vcache + layer_kv};
+                 m->max_pos, m->rope_cur, m->state, m->q, m->kcache + layer_kv, m->vcache + layer_kv};
         SrcNorm src{m->hidden, L.res_in, L.in_gamma, L.in_gamma_s, rp, L.ref_in, f.norm_attn_frac, m->norm_a};
         {
             TimedScope t(m, K_QKV);
@@ -1035,43 +1119,68 @@ hipError_t layer_step(myl_model* m, int l) {
         const uint32_t ss = (uint32_t)f.q_frac + f.k_frac + 15u;
         const uint8_t score_shift = (uint8_t)(ss > MYL_TV_SCORE_FRAC_BITS ? ss - MYL_TV_SCORE_FRAC_BITS : 0);
         const uint8_t lut_shift = MYL_TV_SCORE_FRAC_BITS - MYL_TV_EXP_INPUT_FRAC;
-        const int chunks = (m->max_pos + kChunk - 1) / kChunk;
         const int16_t* kc = m->kcache + layer_kv;
         const int16_t* vc = m->vcache + layer_kv;
         int xs_log = -1;  // AttnBlock
         if (kvh <= 8 && 8 % kvh == 0)
             for (xs_log = 0; (kvh << xs_log) < 8;) ++xs_log;
-        if (xs_log >= 0 && (int64_t)G * G * ((chunks + (1 << xs_log) - 1) >> xs_log) >= (1 << 24)) xs_log = -1;
         const uint32_t ginv = ((1u << 24) + (uint32_t)G - 1) / (uint32_t)G;
-        const dim3 agrid = xs_log >= 0 ? dim3(8 * G * ((chunks + (1 << xs_log) - 1) >> xs_log))
-                                       : dim3(8 * G, (chunks + 7) / 8, kvh);
-        const int exp_lds = m->exp_nz <= kDecExpLds ? m->exp_nz : -1;
-        if (hd == 128) {
+        auto attn_grid = [&](int chunks, int& xsl) {
+            xsl = xs_log;
+            if (xsl >= 0 && (int64_t)G * G * ((chunks + (1 << xsl) - 1) >> xsl) >= (1 << 24)) xsl = -1;
+            return xsl >= 0 ? dim3(8 * G * ((chunks + (1 << xsl) - 1) >> xsl)) : dim3(8 * G, (chunks + 7) / 8, kvh);
+        };
+        const int chunks = (m->max_pos + kChunk - 1) / kChunk;
+        int sxs = -1;
+        const dim3 agrid = attn_grid(chunks, sxs);
+        if (hd == 128)
             attn_scores_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, chunks, m->score_mult,
-                                                          score_shift, m->scores, m->score_ld, xs_log, ginv);
-            attn_pv_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G, chunks,
-                                                      m->exp_lut, (uint32_t)m->exp_len, lut_shift, exp_lds, m->attn_acc,
-                                                      xs_log, ginv);
-        } else {
+                                                          score_shift, m->scores, m->score_ld, sxs, ginv);
+        else
             attn_scores_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, chunks, m->score_mult,
-                                                         score_shift, m->scores, m->score_ld, xs_log, ginv);
-            attn_pv_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G, chunks,
-                                                     m->exp_lut, (uint32_t)m->exp_len, lut_shift, exp_lds, m->attn_acc,
-                                                     xs_log, ginv);
+                                                         score_shift, m->scores, m->score_ld, sxs, ginv);
+        if (m->pv32) {
+            const int wchunks = (m->max_pos + kPvWide - 1) / kPvWide;
+            int wxs = -1;
+            const dim3 wgrid = attn_grid(wchunks, wxs);
+            int32_t* acc = reinterpret_cast<int32_t*>(m->attn_acc);
+            if (hd == 128)
+                attn_pv_wide_kernel<128><<<wgrid, 512, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G,
+                                                                wchunks, m->exp_lut, (uint32_t)m->exp_len, lut_shift,
+                                                                m->exp_nz, acc, wxs, ginv);
+            else
+                attn_pv_wide_kernel<64><<<wgrid, 512, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G,
+                                                               wchunks, m->exp_lut, (uint32_t)m->exp_len, lut_shift,
+                                                               m->exp_nz, acc, wxs, ginv);
+        } else {
+            const int exp_lds = m->exp_nz <= kDecExpLds ? m->exp_nz : -1;
+            if (hd == 128)
+                attn_pv_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G, chunks,
+                                                          m->exp_lut, (uint32_t)m->exp_len, lut_shift, exp_lds,
+                                                          m->attn_acc, sxs, ginv);
+            else
+                attn_pv_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G, chunks,
+                                                         m->exp_lut, (uint32_t)m->exp_len, lut_shift, exp_lds,
+                                                         m->attn_acc, sxs, ginv);
         }
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     {
         TimedScope t(m, K_O);
-        SrcAttn src{m->attn_acc, f.v_frac, f.attn_out_frac};
         EpiResid o{L.so, f.attn_out_frac, L.acc_attn, L.res_in, L.res_mid, m->hidden, m->resid, m->norm_b, L.ref_mid,
                    m->norm_a};
         // 8-wave blocks streaming 4 KiB per row per batch, one block per CU:
         // 10.8 -> 9.7 us per launch on MI355X at 7B widths (16-wave blocks,
         // two-step batches, as many blocks as fit: the previous shape)
-        e = nq <= 1024 ? stream_i8<1, 1, 4>(src, L.wo, H, nq, o, st, cus)
-                       : stream_i8<1, 4, 8>(src, L.wo, H, nq, o, st, cus, 1);
+        auto o_proj = [&](const auto& src) {
+            return nq <= 1024 ? stream_i8<1, 1, 4>(src, L.wo, H, nq, o, st, cus)
+                              : stream_i8<1, 4, 8>(src, L.wo, H, nq, o, st, cus, 1);
+        };
+        if (m->pv32)
+            e = o_proj(SrcAttn<int32_t>{reinterpret_cast<const int32_t*>(m->attn_acc), f.v_frac, f.attn_out_frac});
+        else
+            e = o_proj(SrcAttn<unsigned long long>{m->attn_acc, f.v_frac, f.attn_out_frac});
         if (e != hipSuccess) return e;
     }
     {
@@ -1132,8 +1241,19 @@ hipError_t embed_step(myl_model* m, int mode, int token, int pos, int64_t* token
     TimedScope t(m, K_EMBED);
     embed_kernel<<<1, 1024, 0, m->ctx->stream>>>(m->state, mode, token, pos, m->rope_rows, m->V, m->emb, m->emb_shifts,
                                                   m->layers[0].res_in, m->layers[0].ref_in, m->H, tokens_dev, m->hidden,
-                                                  m->norm_a);
+                                                  m->norm_a, m->cos_lut, m->sin_lut, m->hd / 2, m->rope_cur);
     return hipGetLastError();
+}
+
+// The step's RoPE row for layers run from a host-supplied state.
+int set_rope_cur(myl_model* m, int row) {
+    const size_t half = (size_t)m->hd / 2;
+    myl_ctx* c = m->ctx;
+    int rc = c->hip(hipMemcpyAsync(m->rope_cur, m->cos_lut + (size_t)row * half, half * 2, hipMemcpyDeviceToDevice,
+                                   c->stream), "rope row");
+    if (rc) return rc;
+    return c->hip(hipMemcpyAsync(m->rope_cur + half, m->sin_lut + (size_t)row * half, half * 2,
+                                 hipMemcpyDeviceToDevice, c->stream), "rope row");
 }
 
 // The input-norm accumulator for a hidden vector supplied by the host.
@@ -1429,6 +1549,8 @@ int myl_model_run_layers(myl_model* m, int16_t* hidden, uint32_t pos, uint32_t l
     s.pos = (int32_t)pos;
     s.rope_row = (int32_t)(pos % m->rope_rows);
     int rc = c->hip(hipMemcpyAsync(m->state, &s, sizeof(s), hipMemcpyHostToDevice, c->stream), "state");
+    if (rc) return rc;
+    rc = set_rope_cur(m, s.rope_row);
     if (rc) return rc;
     rc = c->hip(hipMemcpyAsync(m->hidden, hidden, (size_t)m->H * 2, hipMemcpyHostToDevice, c->stream), "hidden");
     hipError_t e = hipSuccess;

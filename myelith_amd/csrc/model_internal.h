@@ -103,6 +103,7 @@ struct myl_model {
     int rsqrt_len = 0, silu_len = 0, exp_len = 0;
     uint8_t rsqrt_closed = 0;  // the rsqrt table equals its closed form (RmsParams::closed)
     int exp_nz = 0;  // exp-table entries up to its last nonzero one
+    bool pv32 = false;  // decode P.V by the wide-chunk kernel in i32 (attn_acc holds int32 sums)
     int gu_repeat = 1;  // launches of each layer's gate/up GEMV per step (myl_model_set_kernel_repeat)
     int16_t* h_scratch = nullptr;  // output rows of the repeated launches
     int64_t inv_n_q20 = 0;
@@ -113,12 +114,13 @@ struct myl_model {
     int32_t* logits = nullptr;
     int32_t* scores = nullptr;  // [heads][score_ld] decode attention scores
     int score_ld = 0;           // max_pos rounded up to 4 (16-byte aligned rows)
-    unsigned long long* attn_acc = nullptr;  // [nq] exact P.V sums, cleared after each use
+    unsigned long long* attn_acc = nullptr;  // [nq] exact P.V sums (i64, or i32 when pv32), cleared after each use
     NormAcc* norm_a = nullptr;               // input-norm / final-norm sums of squares
     NormAcc* norm_b = nullptr;               // post-attention-norm sums of squares
     uint8_t ref_final = 0;
     int cus = 0;
     DecodeState* state = nullptr;
+    int16_t* rope_cur = nullptr;  // the step's RoPE row: cos [hd / 2] then sin [hd / 2]
     int64_t* tokens_dev = nullptr;
     uint32_t tokens_cap = 0;
     uint32_t n_cached = 0;

@@ -13,27 +13,31 @@ constexpr int kBlock = 256;
 
 // ---- block reductions -------------------------------------------------------
 
+// The slots are read in parallel (lane l, slot l) and reduced again across
+// the wave, not one LDS read and wait per slot.
 __device__ inline int32_t block_max_i32(int32_t v, int32_t* red) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
-    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6, l = threadIdx.x & 63;
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
+    if (l == 0) red[w] = v;
     __syncthreads();
-    v = red[0];
-    for (int i = 1; i < nw; ++i) v = max(v, red[i]);
+    v = l < nw ? red[l] : INT32_MIN;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
     return v;
 }
 
 __device__ inline uint32_t block_sum_u32(uint32_t v, uint32_t* red) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v += (uint32_t)__shfl_xor((int)v, off, 64);
-    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6, l = threadIdx.x & 63;
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
+    if (l == 0) red[w] = v;
     __syncthreads();
-    v = 0;
-    for (int i = 0; i < nw; ++i) v += red[i];
+    v = l < nw ? red[l] : 0u;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += (uint32_t)__shfl_xor((int)v, off, 64);
     return v;
 }
 
@@ -91,19 +95,24 @@ __device__ inline uint32_t bitlen128(myl_u128 v) {
     return hi ? 128u - (uint32_t)__builtin_clzll(hi) : (lo ? 64u - (uint32_t)__builtin_clzll(lo) : 0u);
 }
 
-// The same factor in 64-bit arithmetic when the sum and m = (sum * inv_n) >> 20
+// Where a row's rsqrt-table entry comes from: the table index of the mean
+// square, and the even scale q that brought it into the table's range
+// (rmsnorm.rs:96-126: mean = acc * inv_n >> 20, scaled down by the smallest
+// even q until it indexes the table).
+struct RmsIdx { bool zero; uint32_t q; int idx; };
+
+// The same index in 64-bit arithmetic when the sum and m = (sum * inv_n) >> 20
 // fit (always, for int16 inputs with fractional-bit spreads below 16): the
 // i128 emulation is the slow part of the serial setup every block runs.
-__device__ inline bool rms_factor_u64(myl_i128 acc, uint8_t ref, const RmsParams& p, RmsFactor& f) {
+__device__ inline bool rms_index_u64(myl_i128 acc, const RmsParams& p, RmsIdx& r) {
     const uint64_t hi = (uint64_t)((myl_u128)acc >> 64), lo = (uint64_t)acc;
     if (hi != 0 || (lo >> 63) != 0) return false;
     const uint64_t ph = __umul64hi(lo, (uint64_t)p.inv_n_q20), pl = lo * (uint64_t)p.inv_n_q20;
     if ((ph >> 20) != 0 || p.inv_n_q20 < 0) return false;
-    f.ref_shift = ref;
-    f.zero = lo == 0;
-    f.lut_val = 0;
-    f.norm_frac = 0;
-    if (!f.zero) {
+    r.zero = lo == 0;
+    r.q = 0;
+    r.idx = 0;
+    if (!r.zero) {
         const uint64_t m = (ph << 44) | (pl >> 20);
         const uint64_t max_idx = (uint64_t)(p.lut_len - 1);
         uint32_t q = 0;
@@ -114,23 +123,19 @@ __device__ inline bool rms_factor_u64(myl_i128 acc, uint8_t ref, const RmsParams
         while ((m >> q) > max_idx) q += 2;
         int64_t idx = rshift_round64((int64_t)m, (uint8_t)q);
         if (idx > (int64_t)max_idx) idx = (int64_t)max_idx;
-        f.lut_val = rms_lut_value(p, (int)idx);
-        f.norm_frac = (uint32_t)p.lut_output_frac + (uint32_t)p.lut_input_shift / 2u + q / 2u;
+        r.q = q;
+        r.idx = (int)idx;
     }
     return true;
 }
 
-// The factor from the aligned sum of squares acc and the largest input
-// shift ref (rmsnorm.rs:96-126): mean = acc * inv_n >> 20, scaled down by
-// an even q until it indexes the rsqrt LUT.
-__device__ inline RmsFactor rms_factor_of(myl_i128 acc, uint8_t ref, const RmsParams& p) {
-    RmsFactor f;
-    if (rms_factor_u64(acc, ref, p, f)) return f;
-    f.ref_shift = ref;
-    f.zero = acc == 0;
-    f.lut_val = 0;
-    f.norm_frac = 0;
-    if (!f.zero) {
+__device__ inline RmsIdx rms_index(myl_i128 acc, const RmsParams& p) {
+    RmsIdx r;
+    if (rms_index_u64(acc, p, r)) return r;
+    r.zero = acc == 0;
+    r.q = 0;
+    r.idx = 0;
+    if (!r.zero) {
         const myl_i128 m = shr128((myl_i128)((myl_u128)acc * (myl_u128)(myl_i128)p.inv_n_q20), 20);
         const myl_i128 max_idx = (myl_i128)(p.lut_len - 1);
         // rmsnorm.rs:121-123 searches the smallest even q with m >> q <= max_idx.
@@ -145,10 +150,61 @@ __device__ inline RmsFactor rms_factor_of(myl_i128 acc, uint8_t ref, const RmsPa
         myl_i128 idx = rshift_round128(m, q);
         if (idx > max_idx) idx = max_idx;
         if (idx < 0) idx = 0;
-        f.lut_val = rms_lut_value(p, (int)idx);
-        f.norm_frac = (uint32_t)p.lut_output_frac + (uint32_t)p.lut_input_shift / 2u + q / 2u;
+        r.q = q;
+        r.idx = (int)idx;
     }
+    return r;
+}
+
+__device__ inline RmsFactor rms_factor_at(const RmsIdx& r, uint8_t ref, const RmsParams& p, int64_t lut_val) {
+    RmsFactor f;
+    f.ref_shift = ref;
+    f.zero = r.zero;
+    f.lut_val = r.zero ? 0 : lut_val;
+    f.norm_frac = r.zero ? 0u : (uint32_t)p.lut_output_frac + (uint32_t)p.lut_input_shift / 2u + r.q / 2u;
     return f;
+}
+
+// The factor from the aligned sum of squares acc and the largest input
+// shift ref (rmsnorm.rs:96-126).
+__device__ inline RmsFactor rms_factor_of(myl_i128 acc, uint8_t ref, const RmsParams& p) {
+    const RmsIdx r = rms_index(acc, p);
+    return rms_factor_at(r, ref, p, r.zero ? 0 : rms_lut_value(p, r.idx));
+}
+
+// rsqrt_closed computed by a whole wave: each round the 64 lanes test 64
+// evenly spaced candidates of the remaining range [lo, hi) (v(lo) holds,
+// v(hi) fails; the test is monotone in v), and the ballot's count moves lo
+// and hi to the last holding and first failing candidate: three rounds for
+// the theta_v table's 4097-wide range instead of twelve bisection steps.
+// x, f, s uniform over the wave; every lane active.
+__device__ inline int32_t rsqrt_closed_wave(uint32_t x, uint32_t f, uint32_t s) {
+    if (x == 0) return (int32_t)(1u << f);
+    const uint32_t e = 2u * f + s + 2u;
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t lo = 0, hi = (1u << (f + (s + 1u) / 2u)) + 1u;
+    while (hi - lo > 1u) {
+        const uint32_t step = (hi - lo + 63u) >> 6;
+        const uint32_t c = lo + step * (lane + 1u);
+        const uint64_t t = 2ull * c - 1ull;
+        const bool ok = c < hi && t * t * (uint64_t)x <= (1ull << e);
+        const uint32_t k = (uint32_t)__popcll(__ballot(ok));
+        const uint32_t nlo = lo + step * k;
+        hi = min(hi, nlo + step);
+        lo = nlo;
+    }
+    return (int32_t)lo;
+}
+
+// rms_factor_of computed by a whole wave (every lane active, acc uniform):
+// the closed-form table entry by rsqrt_closed_wave.  Every lane gets the factor.
+__device__ inline RmsFactor rms_factor_wave(myl_i128 acc, uint8_t ref, const RmsParams& p) {
+    const RmsIdx r = rms_index(acc, p);
+    int64_t v = 0;
+    if (!r.zero)
+        v = p.closed ? (int64_t)rsqrt_closed_wave((uint32_t)r.idx, p.lut_output_frac, p.lut_input_shift)
+                     : (int64_t)p.lut[r.idx];
+    return rms_factor_at(r, ref, p, v);
 }
 
 // Must be called by the whole block.  red128 needs blockDim.x entries.
@@ -181,7 +237,9 @@ MYL_FN int64_t rne_shift64_small(int64_t v, uint32_t s) {
 
 // Per-channel output of rmsnorm.rs:130-159.  |x * lut * gamma| < 2^37, so for
 // 0 <= shift <= 62 and for left shifts up to 25 bits the i64 computation is the
-// i128 one bit for bit; other shifts take the i128 path.
+// i128 one bit for bit; other shifts take the i128 path.  (Branches: a lane
+// computes only the form its shift needs; computing both and selecting
+// measured slower in the decode staging.)
 __device__ inline int16_t rms_out(int16_t x, uint8_t xs, int8_t g, uint8_t gs, const RmsFactor& f, uint8_t out_frac) {
     if (f.zero) return 0;
     const int32_t total = (int32_t)f.norm_frac + (int32_t)gs + ((int32_t)xs - (int32_t)f.ref_shift);

@@ -97,25 +97,23 @@ __device__ inline int32_t wave_max_i32(int32_t v) {
 }
 
 // Block-wide maximum / wrapping sum for blocks of up to 16 waves; red needs
-// one slot per wave.  Every thread gets the result.
+// one slot per wave.  Every thread gets the result: after the barrier each
+// wave reads the slots in parallel (lane l, slot l) and reduces them again
+// with DPP, instead of one LDS read and wait per slot.
 __device__ inline int32_t block_max_i32_dpp(int32_t v, int32_t* red) {
     v = wave_max_i32(v);
-    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
+    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6, l = threadIdx.x & 63;
+    if (l == 0) red[w] = v;
     __syncthreads();
-    v = red[0];
-    for (int i = 1; i < nw; ++i) v = max(v, red[i]);
-    return v;
+    return wave_max_i32(l < nw ? red[l] : INT32_MIN);
 }
 
 __device__ inline uint32_t block_sum_u32_dpp(uint32_t v, uint32_t* red) {
     v = (uint32_t)wave_sum_i32((int32_t)v);
-    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
+    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6, l = threadIdx.x & 63;
+    if (l == 0) red[w] = v;
     __syncthreads();
-    v = 0;
-    for (int i = 0; i < nw; ++i) v += red[i];
-    return v;
+    return (uint32_t)wave_sum_i32(l < nw ? (int32_t)red[l] : 0);
 }
 
 template <int CTRL>

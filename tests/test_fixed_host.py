@@ -221,3 +221,46 @@ def test_rne_shift64_small_matches_rshift_round64(tmp_path):
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout
     assert "mismatches 0" in r.stdout
+
+
+def _rsqrt_wave_search(x: int, f: int, s: int) -> tuple[int, int]:
+    """rsqrt_closed_wave (csrc/ops.h) step by step: 64 lanes test evenly
+    spaced candidates of [lo, hi) per round, the ballot count moves the
+    bounds.  Returns (value, rounds)."""
+    if x == 0:
+        return 1 << f, 0
+    e = 2 * f + s + 2
+    lo, hi = 0, (1 << (f + (s + 1) // 2)) + 1
+    rounds = 0
+    while hi - lo > 1:
+        step = (hi - lo + 63) >> 6
+        k = 0
+        for lane in range(64):
+            c = lo + step * (lane + 1)
+            t = 2 * c - 1
+            if c < hi and t * t * x <= (1 << e):
+                k += 1
+        nlo = lo + step * k
+        hi = min(hi, nlo + step)
+        lo = nlo
+        rounds += 1
+    return lo, rounds
+
+
+def test_rsqrt_wave_search_equals_the_table():
+    """The wave-wide rsqrt search of the decode norm staging (64 candidates per
+    round) against the reference's float64 table generator (luts.py:32-49) at
+    every entry of the contract's table and on the two other parameter sets,
+    and it finishes in at most three rounds for the contract's range (4097
+    candidates); the ballot count is a prefix of holding lanes, so a planted
+    non-monotone test would fail here first."""
+    from myelith_amd.luts import rsqrt_lut
+    for frac, shift, n in ((8, 8, 32768), (6, 4, 4000), (10, 3, 3000)):
+        want = rsqrt_lut(n - 1, shift, frac).astype(np.int64)
+        worst = 0
+        for x in range(n):
+            v, rounds = _rsqrt_wave_search(x, frac, shift)
+            assert v == want[x], (frac, shift, x, v, want[x])
+            worst = max(worst, rounds)
+        if (frac, shift) == (8, 8):
+            assert worst <= 3
