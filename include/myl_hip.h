@@ -73,7 +73,8 @@ int myl_set_stream(myl_ctx* ctx, void* stream);
 
 /* ---- device memory for callers without their own allocator ------------- */
 /* No counterpart in the reference: a measurement of the achievable read rate
- * for the roofline figures.  Enqueues one pass of plain 16-byte loads over
+ * for the roofline figures.  Enqueues one pass of 16-byte nontemporal loads
+ * (the cache policy of the GEMV weight streams) over
  * `bytes` of device memory at p (16-byte aligned, bytes % 16 == 0), one block
  * of 512 threads per CU; `out` (one device word) receives at most one
  * word. */
@@ -232,9 +233,10 @@ int myl_model_set_graphs(myl_model* m, int enable);
 /* No counterpart in the reference: a measurement hook for callers that time a
  * kernel class inside the captured decode step.  Launches the class's kernel
  * `times` (1-4, at most the number of layers) times per layer and step: the
- * first as usual, each repeat over the next layers' weights (never weights the
- * step has already read) into scratch output rows, so every output of the step
- * is unchanged.  Only the gate/up class (kclass 5 of the timing order below)
+ * first as usual, each repeat with the same launch shape over the weights of
+ * layer l + 1, l + 2, ... (wrapping to the first layers: weights the step read
+ * at least a layer's traffic earlier, which no longer sit in the caches) into
+ * scratch output rows, so every output of the step is unchanged.  Only the gate/up class (kclass 5 of the timing order below)
  * is accepted; myl_model_timing does not count the repeats.  The next greedy
  * decode recaptures its step graph. */
 int myl_model_set_kernel_repeat(myl_model* m, int kclass, int times);
@@ -308,8 +310,11 @@ void myl_moe_destroy(myl_moe* m);
 /* The layer's synthetic input for n_tokens tokens (device, [n_tokens x hidden]). */
 int myl_moe_synth_input(myl_moe* m, uint32_t n_tokens, int16_t* x_dev);
 /* out_dev [n_tokens x hidden] = the layer on x_dev [n_tokens x hidden] (device,
- * 16-byte aligned).  Synchronises once with the host (the experts' token
- * counts size the grouped products). */
+ * 16-byte aligned).  When hidden and the intermediate widths are multiples of
+ * 64 the whole layer is planned on the device (expert offsets and the grouped
+ * products' work tables from the token counts) and nothing waits for the
+ * host; other widths synchronise once with the host, whose work tables size
+ * the grouped products. */
 int myl_moe_forward(myl_moe* m, const int16_t* x_dev, uint32_t n_tokens, int16_t* out_dev);
 /* Routing of the last forward (host arrays, any may be NULL): ids and gates
  * [n_tokens x top_k] (descending logit, lowest expert first on ties), counts

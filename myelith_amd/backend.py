@@ -107,8 +107,8 @@ class RocmBackend:
         self.check(lib().myl_synchronize(self._h), "synchronize")
 
     def read_probe_dev(self, buf, out) -> None:
-        """One pass of plain loads over the device tensor buf (a measurement of
-        the achievable read rate; out: a device int32 word)."""
+        """One pass of 16-byte nontemporal loads over the device tensor buf (a
+        measurement of the achievable read rate; out: a device int32 word)."""
         self.check(lib().myl_read_probe(self._h, buf.data_ptr(), buf.numel() * buf.element_size(), out.data_ptr()),
                    "read_probe")
 

@@ -347,8 +347,9 @@ __global__ __launch_bounds__(1024) void embed_kernel(DecodeState* st, int mode, 
     __syncthreads();
     const int tok = s_tok;
     if ((int)threadIdx.x < 2 * half) {
-        const int i = (int)threadIdx.x % half;
-        rope_cur[threadIdx.x] = ((int)threadIdx.x < half ? cos_lut : sin_lut)[(size_t)s_row * half + i];
+        const bool c = (int)threadIdx.x < half;
+        const int i = c ? (int)threadIdx.x : (int)threadIdx.x - half;  // no integer division
+        rope_cur[threadIdx.x] = (c ? cos_lut : sin_lut)[(size_t)s_row * half + i];
     }
     const int8_t* row = E + (size_t)tok * H;
     const uint8_t sh = emb_shifts[tok];
@@ -1198,15 +1199,17 @@ hipError_t layer_step(myl_model* m, int l) {
                           : stream_i8<2, 4, 8>(src, L.wgu, 2 * I, H, s, st, cus);
         }
         // measurement repeats (myl_model_set_kernel_repeat), outside the timed
-        // class: the same launch over the next layers' gate/up weights, which
-        // the step last read one step ago (out of the caches, as this
-        // layer's), into scratch rows
+        // class: the same launch (same shape) over another layer's gate/up
+        // weights, l + rep, wrapping to the first layers (read at least a
+        // layer's traffic ago, so out of the caches as this layer's are),
+        // into scratch rows
         for (int rep = 1; rep < m->gu_repeat && e == hipSuccess; ++rep) {
             const LayerDev& Lr = m->layers[(l + rep) % (int)m->spec.layers];
             EpiSilu sr = s;
             sr.shifts = Lr.sgu;
             sr.h = m->h_scratch;
-            e = stream_i8<2, 4, 8>(src, Lr.wgu, 2 * I, H, sr, st, cus);
+            e = H <= 1024 ? stream_i8<2, 1, 8>(src, Lr.wgu, 2 * I, H, sr, st, cus, 1)
+                          : stream_i8<2, 4, 8>(src, Lr.wgu, 2 * I, H, sr, st, cus);
         }
     }
     if (e != hipSuccess) return e;

@@ -963,6 +963,9 @@ void or_moe_destroy(or_moe* m) {
 or_moe* or_moe_create_synthetic(const myl_moe_spec* spec, const int32_t* router_bias, const myl_luts* luts) {
     const size_t H = spec->hidden, E = spec->n_experts, I = spec->inter, S = spec->shared_inter;
     if (!H || !E || !I || !S || !spec->top_k || spec->top_k > E) return NULL;
+    /* the route's per-token scratch (or_moe_route: z[256], sel[16]) bounds
+       the expert count and top-k, as the device layer's checks do */
+    if (E > 256 || spec->top_k > 16) return NULL;
     or_moe* m = (or_moe*)calloc(1, sizeof(or_moe));
     if (!m) return NULL;
     m->spec = *spec;

@@ -62,3 +62,19 @@ def test_combine_is_one_weighted_sum_and_one_rounding(moe, oracle):
         acc = s * 16384 + sum(int(g) * y for g, y in zip(r["gates"][t], ys))
         exp = np.array([max(-32768, min(32767, oracle.rshift_round_i64(int(a), 14))) for a in acc], np.int16)
         assert np.array_equal(moe.token(x[t], r["ids"][t], r["gates"][t]), exp), t
+
+
+def test_oracle_rejects_routes_beyond_its_scratch():
+    """The oracle's per-token route scratch holds 256 expert logits and 16
+    selections (or_moe_route), the bounds the device layer checks too: a
+    spec past either is refused at creation instead of overrunning it."""
+    from myelith_amd.luts import LutSet
+    from oracle.binding import OracleMoe
+    luts = LutSet.for_head_dim(64)
+    base = dict(seed=3, hidden=64, n_experts=8, inter=64, top_k=2, shared_inter=64)
+    m = OracleMoe(base, np.zeros(8, np.int32), luts)  # within bounds: accepted
+    m.close()
+    for bad in (dict(n_experts=257), dict(n_experts=32, top_k=17)):
+        spec = {**base, **bad}
+        with pytest.raises(ValueError, match="creation failed"):
+            OracleMoe(spec, np.zeros(spec["n_experts"], np.int32), luts)
