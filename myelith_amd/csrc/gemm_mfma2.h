@@ -27,6 +27,7 @@
 
 #include "gemm_mfma.h"
 #include "internal.h"
+#include "mm_plan.h"
 #include "wave.h"
 
 #include <algorithm>
@@ -51,23 +52,9 @@ __global__ __launch_bounds__(256) void split_planes_kernel(const int16_t* __rest
 __device__ inline constexpr int waitcnt_vm(int v) { return (v & 0xF) | (0x7 << 4) | (0xF << 8) | (((v >> 4) & 0x3) << 14); }
 
 template <int MB, int NB, int WM_, int WN_, int STAGES, int KS = 64>
-struct Mm2 {
-    static_assert(KS == 64 || KS == 128, "stage width");
-    static constexpr int kThreads = WM_ * WN_ * 64;
-    static constexpr int BR = 32 * MB * WM_;   // A' rows per block (2 per token)
-    static constexpr int BN = 32 * NB * WN_;   // weight rows per block
-    static constexpr int kCpr = KS / 16;       // 16-byte chunks per stage row
-    static constexpr int kRowsPerLoad = 64 / kCpr;
-    static constexpr int kSwzRows = 256 / KS;  // rows sharing one swizzle slot
-    static constexpr int kStageBytes = (BR + BN) * KS;
-    static constexpr size_t kLds = (size_t)STAGES * kStageBytes;
-    // 1 KiB wave loads per stage, dealt round-robin to the waves: every wave
-    // issues kLoadsMin or kLoadsMax of them
-    static constexpr int kGroups = (BR + BN) / kRowsPerLoad;
-    static constexpr int kLoadsMin = kGroups / (kThreads / 64);
-    static constexpr int kLoadsMax = (kGroups + kThreads / 64 - 1) / (kThreads / 64);
-    static_assert((BR + BN) % kRowsPerLoad == 0, "whole 1 KiB loads");
-    __device__ static int slot(int row, int chunk) { return chunk ^ ((row / kSwzRows) & (kCpr - 1)); }
+struct Mm2 : Mm2Dims<MB, NB, WM_, WN_, STAGES, KS> {
+    using D = Mm2Dims<MB, NB, WM_, WN_, STAGES, KS>;
+    __device__ static int slot(int row, int chunk) { return chunk ^ ((row / D::kSwzRows) & (D::kCpr - 1)); }
 };
 
 // Order of a product's output tiles over the grid.  mm_tile_index gives each
@@ -593,23 +580,16 @@ template <int MB, int NB, int WM_, int WN_, int STAGES, int KS = 64, class Epi, 
 hipError_t mm2_launch_splitk_fin(const int8_t* Ap, int M, const int8_t* W, int N, int K, const Epi& epi,
                                  const MmCtx* mm, int fill, hipStream_t st, const Fin& fin, bool* split) {
     using S = Mm2<MB, NB, WM_, WN_, STAGES, KS>;
-    const int R2 = 2 * M;
-    const int tiles_r = (R2 + S::BR - 1) / S::BR, ntiles = tiles_r * ((N + S::BN - 1) / S::BN);
-    const int nkb = K / KS;
-    int ks = 1;
-    if (ntiles < fill && (size_t)M * N <= mm->acc_elems)
-        ks = std::max(1, std::min((2 * mm->cus + ntiles - 1) / ntiles, nkb / (512 / KS)));
-    *split = ks > 1;
-    if (ks <= 1) return mm2_launch<MB, NB, WM_, WN_, STAGES, KS>(Ap, M, W, N, K, epi, st);
-    const int kslice = ((nkb + ks - 1) / ks) * KS;
-    const int ns = (K + kslice - 1) / kslice, nitems = ntiles * ns;
+    const Mm2SplitPlan p = mm2_split_plan<MB, NB, WM_, WN_, STAGES, KS>(M, N, K, mm->cus, mm->acc_elems, fill);
+    *split = p.split;
+    if (!p.split) return mm2_launch<MB, NB, WM_, WN_, STAGES, KS>(Ap, M, W, N, K, epi, st);
     auto kern = mm2_splitk_kernel<MB, NB, WM_, WN_, STAGES, KS>;
     if (S::kLds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
         if (e != hipSuccess) return e;
     }
-    kern<<<8 * ((nitems + 7) / 8), S::kThreads, S::kLds, st>>>(Ap, R2, W, N, K, Divider::of((uint32_t)tiles_r),
-                                                              Divider::of((uint32_t)ntiles), nitems, kslice, mm->acc);
+    kern<<<p.grid, S::kThreads, S::kLds, st>>>(Ap, 2 * M, W, N, K, Divider::of((uint32_t)p.tiles_r),
+                                               Divider::of((uint32_t)p.ntiles), p.nitems, p.kslice, mm->acc);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return fin(mm->acc, st);
