@@ -106,18 +106,22 @@ __global__ __launch_bounds__(256) void rope_scatter_kernel(const int16_t* __rest
                                                            const int16_t* __restrict__ cos_lut,
                                                            const int16_t* __restrict__ sin_lut, int16_t* __restrict__ Q,
                                                            int16_t* __restrict__ kc, int16_t* __restrict__ vc,
-                                                           size_t seq_stride, int kvh, int max_pos) {
-    const int r = blockIdx.y;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    const int npairs = (nq + 2 * nkv) >> 1;
-    if (i >= npairs) return;
-    const int n0 = 2 * i;
+                                                           size_t seq_stride, int kvh, int max_pos);
+
+// RoPE of a q/k pair (rope.rs:17-31) and its destination: q to Q in
+// head-major order, k (post-RoPE) and v to the sequence's cache at the row's
+// position (model.rs:469-503).  Shared by rope_scatter_kernel and the fused
+// finish of a split q/k/v product.
+__device__ inline void rope_store_pair(int r, int n0, int16_t y0, int16_t y1, const int32_t* __restrict__ rows,
+                                       int rows_cap, int nq, int nkv, int hd_log, const int16_t* __restrict__ cos_lut,
+                                       const int16_t* __restrict__ sin_lut, int16_t* __restrict__ Q,
+                                       int16_t* __restrict__ kc, int16_t* __restrict__ vc, size_t seq_stride,
+                                       int max_pos) {
     const int seg = n0 < nq ? 0 : (n0 < nq + nkv ? 1 : 2);
     const int e = n0 - (seg == 0 ? 0 : (seg == 1 ? nq : nq + nkv));
     const int hd = 1 << hd_log, half = hd >> 1;
     const int head = e >> hd_log;
     const int p = (e & (hd - 1)) >> 1;
-    int16_t y0 = qkv[(size_t)r * ldq + n0], y1 = qkv[(size_t)r * ldq + n0 + 1];
     const int seq = rows[r], pos = rows[rows_cap + r], rope_row = rows[2 * rows_cap + r];
     if (seg < 2) {
         const int32_t c = cos_lut[(size_t)rope_row * half + p];
@@ -131,6 +135,45 @@ __global__ __launch_bounds__(256) void rope_scatter_kernel(const int16_t* __rest
     else dst = (seg == 1 ? kc : vc) + (size_t)seq * seq_stride + ((size_t)head * max_pos + pos) * hd;
     dst[p] = y0;
     dst[p + half] = y1;
+}
+
+__global__ __launch_bounds__(256) void rope_scatter_kernel(const int16_t* __restrict__ qkv, int ldq, const int32_t* __restrict__ rows,
+                                                           int rows_cap, int nq, int nkv, int hd_log,
+                                                           const int16_t* __restrict__ cos_lut,
+                                                           const int16_t* __restrict__ sin_lut, int16_t* __restrict__ Q,
+                                                           int16_t* __restrict__ kc, int16_t* __restrict__ vc,
+                                                           size_t seq_stride, int kvh, int max_pos) {
+    const int r = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int npairs = (nq + 2 * nkv) >> 1;
+    if (i >= npairs) return;
+    const int n0 = 2 * i;
+    rope_store_pair(r, n0, qkv[(size_t)r * ldq + n0], qkv[(size_t)r * ldq + n0 + 1], rows, rows_cap, nq, nkv, hd_log,
+                    cos_lut, sin_lut, Q, kc, vc, seq_stride, max_pos);
+}
+
+// The finish of a split q/k/v product fused with rope_scatter_kernel's work:
+// thread (pair i, row r) takes the pair's two exact sums out of the split-K
+// accumulator (clearing them), requantises them with the bias (EpiQKVRows),
+// rotates q/k pairs and writes q to Q and k, v to the sequence's cache.  The
+// q/k/v rows are pair-ordered, so the pair is outputs 2i, 2i + 1.  Grid
+// (ceil(pairs / 256), R).
+__global__ __launch_bounds__(256) void qkv_finish_rope_kernel(unsigned long long* __restrict__ acc, int N, EpiQKVRows epi,
+                                                              const int32_t* __restrict__ rows, int rows_cap, int nq,
+                                                              int nkv, int hd_log, const int16_t* __restrict__ cos_lut,
+                                                              const int16_t* __restrict__ sin_lut,
+                                                              int16_t* __restrict__ Q, int16_t* __restrict__ kc,
+                                                              int16_t* __restrict__ vc, size_t seq_stride, int max_pos) {
+    const int r = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (N >> 1)) return;
+    const int n0 = 2 * i;
+    unsigned long long* a = acc + (size_t)r * N + n0;
+    const int64_t a0 = (int64_t)a[0], a1 = (int64_t)a[1];
+    const int16_t y0 = epi.value(n0, a0), y1 = epi.value(n0 + 1, a1);
+    a[0] = 0;
+    a[1] = 0;
+    rope_store_pair(r, n0, y0, y1, rows, rows_cap, nq, nkv, hd_log, cos_lut, sin_lut, Q, kc, vc, seq_stride, max_pos);
 }
 
 // softmax.rs:12-64 for one (row, head) over its L scores: m = max, S =
@@ -302,20 +345,37 @@ __global__ __launch_bounds__(kFinNormThreads) void finish_resid_norm_kernel(unsi
     int16_t xv[PER];
     uint8_t sv[PER], gsv[PER];
     int8_t gv[PER];
+    // every load of the thread's elements first, then the arithmetic, then
+    // the stores (the output row and the accumulator's clearing): one memory
+    // latency instead of one per element (6 -> 1.x us on MI355X)
+    int64_t av[PER];
+    EpiResidRows::FinOps op[PER];
+#pragma unroll
+    for (int t = 0; t < PER; ++t) {
+        const int n = min(threadIdx.x + t * kFinNormThreads, N - 1);  // lanes past N load a valid element, unused
+        av[t] = (int64_t)acc[(size_t)m * N + n];
+        op[t] = epi.fin_ops(n, m);
+        sv[t] = xs[n];
+        gv[t] = g[n];
+        gsv[t] = gs[n];
+    }
 #pragma unroll
     for (int t = 0; t < PER; ++t) {
         const int n = threadIdx.x + t * kFinNormThreads;
         xv[t] = 0;
-        sv[t] = gsv[t] = 0;
-        gv[t] = 0;
         if (n < N) {
-            unsigned long long* a = acc + (size_t)m * N + n;
-            const int64_t v = (int64_t)*a;
-            *a = 0;
-            xv[t] = epi.value(n, m, v);
-            sv[t] = xs[n];
-            gv[t] = g[n];
-            gsv[t] = gs[n];
+            xv[t] = epi.value_of(av[t], op[t]);
+        } else {
+            sv[t] = gsv[t] = 0;
+            gv[t] = 0;
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < PER; ++t) {
+        const int n = threadIdx.x + t * kFinNormThreads;
+        if (n < N) {
+            epi.out[(size_t)m * epi.ldo + n] = xv[t];
+            acc[(size_t)m * N + n] = 0;
         }
     }
     const RmsFactor f = rms_factor_limbs<PER>(xv, sv, ref, p, red, &sf);
@@ -504,6 +564,7 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
     for (int l = 0; l < (int)m->spec.layers; ++l) {
         const LayerDev& Ld = m->layers[l];
         const myl_layer_fracs& f = Ld.f;
+        bool qkv_roped = false;  // the q/k/v finish did RoPE and the KV append
         EpiQKVRows eq{};
         eq.shifts = Ld.sqkv; eq.bias = Ld.bqkv; eq.bias_sh = Ld.bsqkv;
         eq.act_frac = f.norm_attn_frac; eq.q_frac = f.q_frac; eq.k_frac = f.k_frac; eq.v_frac = f.v_frac;
@@ -514,7 +575,16 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
                                     MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, f.norm_attn_frac,
                                     mm->planes, st)) != hipSuccess)
                 return e;
-            if ((e = mm_planes(mm->planes, R, Ld.wqkv, nqkv, H, eq, mm, st)) != hipSuccess) return e;
+            // a split product finishes with RoPE and the KV append fused in
+            auto fin = [&](unsigned long long* acc, hipStream_t s) -> hipError_t {
+                qkv_finish_rope_kernel<<<dim3((nqkv / 2 + 255) / 256, R), 256, 0, s>>>(
+                    acc, nqkv, eq, b->rows, b->rows_cap, nq, nkv, m->hd_log, m->cos_lut, m->sin_lut, b->Q,
+                    b->kc + (size_t)l * kvh * m->max_pos * hd, b->vc + (size_t)l * kvh * m->max_pos * hd, sstride,
+                    m->max_pos);
+                return hipGetLastError();
+            };
+            if ((e = mm_planes_fin(mm->planes, R, Ld.wqkv, nqkv, H, eq, mm, st, fin, &qkv_roped)) != hipSuccess)
+                return e;
         } else {
             if ((e = rmsnorm(b->X, R, H, Ld.res_in, Ld.in_gamma, Ld.in_gamma_s, H, m->rsqrt, m->rsqrt_len,
                              MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, f.norm_attn_frac, b->Xn,
@@ -524,10 +594,12 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         }
         int16_t* kc = b->kc + (size_t)l * kvh * m->max_pos * hd;
         int16_t* vc = b->vc + (size_t)l * kvh * m->max_pos * hd;
-        rope_scatter_kernel<<<dim3((nqkv / 2 + 255) / 256, R), 256, 0, st>>>(
-            b->QKV, nqkv, b->rows, b->rows_cap, nq, nkv, m->hd_log, m->cos_lut, m->sin_lut, b->Q, kc, vc, sstride, kvh,
-            m->max_pos);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (!qkv_roped) {
+            rope_scatter_kernel<<<dim3((nqkv / 2 + 255) / 256, R), 256, 0, st>>>(
+                b->QKV, nqkv, b->rows, b->rows_cap, nq, nkv, m->hd_log, m->cos_lut, m->sin_lut, b->Q, kc, vc, sstride,
+                kvh, m->max_pos);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
         const uint32_t ss = (uint32_t)f.q_frac + f.k_frac + 15u;
         const uint8_t score_shift = (uint8_t)(ss > MYL_TV_SCORE_FRAC_BITS ? ss - MYL_TV_SCORE_FRAC_BITS : 0);
         const dim3 ag(b->ntiles, kvh, ranges);

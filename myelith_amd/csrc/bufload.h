@@ -33,8 +33,5 @@ __device__ inline uint2 cload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 __device__ inline uint32_t cload4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, kPreCpol);
 }
-__device__ inline uint32_t cload2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, kPreCpol);
-}
 
 }  // namespace myl

@@ -372,10 +372,9 @@ __global__ __launch_bounds__(1024) void embed_kernel(DecodeState* st, int mode, 
 
 // q/k/v projection rows (pair-ordered) -> bias -> RoPE -> q buffer / KV cache.
 // The step's RoPE row is in rope (cos [hd / 2] then sin [hd / 2], written by
-// the embedding kernel), so every operand of a group is a load that depends
-// on nothing: the lane's first group's operands (shifts, biases, rotation,
-// position) load right after the first weight batch and are in registers
-// when the stream ends.
+// the embedding kernel), so the rotation's operands are loads that depend on
+// nothing.  The per-row operands load in group(): prefetching them after the
+// first weight batch measured 0.46 us slower per launch on MI355X.
 struct EpiQKV {
     const uint8_t* shifts;    // per device row
     const int16_t* bias;      // per device row, or null
@@ -387,41 +386,14 @@ struct EpiQKV {
     int16_t* q_out;           // [nq]
     int16_t* kc;              // layer base [kv_heads][max_pos][hd]
     int16_t* vc;
-    struct State {
-        int row0, pos;
-        uint8_t sh[2], bs[2];
-        int16_t b[2], c, s;
-    };
-    __device__ inline void begin(State& s) const { s.row0 = -1; }
-    // through buffer descriptors: no branch (a missing bias is a zero-length
-    // range that reads zero), so the staging's wait for its own earlier
-    // loads stays exact
-    __device__ inline void prefetch(State& s, int row0, int N) const {
-        const int r = min(row0, N - 2);  // N is even (RoPE pairs): r is even
-        const int hd = 1 << hd_log, half = hd >> 1;
-        const int p = ((r - (r < nq ? 0 : (r < nq + nkv ? nq : nq + nkv))) & (hd - 1)) >> 1;
-        const uint32_t sh2 = cload2(weight_rsrc(shifts, (uint32_t)N), (uint32_t)r);
-        const uint32_t b2 = cload4(weight_rsrc(bias, bias ? 2u * (uint32_t)N : 0u), 2u * (uint32_t)r);
-        const uint32_t bs2 = cload2(weight_rsrc(bias_sh, bias ? (uint32_t)N : 0u), (uint32_t)r);
-        const __amdgpu_buffer_rsrc_t rr = weight_rsrc(rope, 4u * (uint32_t)half);
-        const uint32_t c = cload2(rr, 2u * (uint32_t)p), sn = cload2(rr, 2u * (uint32_t)(half + p));
-        s.pos = (int)cload4(weight_rsrc(st, sizeof(DecodeState)), (uint32_t)offsetof(DecodeState, pos));
-        s.sh[0] = (uint8_t)sh2;
-        s.sh[1] = (uint8_t)(sh2 >> 8);
-        s.b[0] = (int16_t)(b2 & 0xFFFFu);
-        s.b[1] = (int16_t)(b2 >> 16);
-        s.bs[0] = (uint8_t)bs2;
-        s.bs[1] = (uint8_t)(bs2 >> 8);
-        s.c = (int16_t)c;
-        s.s = (int16_t)sn;
-        s.row0 = row0;
-    }
+    using State = NoState;
+    __device__ inline void begin(State&) const {}
+    __device__ inline void prefetch(State&, int, int) const {}
     __device__ inline void finish(State&) const {}
     template <int R>
-    __device__ inline void group(State& s, int row0, int N, const int64_t (&tot)[R]) const {
+    __device__ inline void group(State&, int row0, int N, const int64_t (&tot)[R]) const {
         static_assert(R == 2, "the RoPE pair needs two rows per group");
         if (row0 >= N) return;
-        const bool pre = s.row0 == row0;
         const int seg = row0 < nq ? 0 : (row0 < nq + nkv ? 1 : 2);
         const int e = row0 - (seg == 0 ? 0 : (seg == 1 ? nq : nq + nkv));
         const uint8_t frac = seg == 0 ? q_frac : (seg == 1 ? k_frac : v_frac);
@@ -432,19 +404,14 @@ struct EpiQKV {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const int d = row0 + t;
-            const uint8_t sh = pre ? s.sh[t] : shifts[d];
-            int16_t v = clamp_i16_i64(rescale64(tot[t], (uint8_t)(sh + act_frac), frac));
-            if (bias) {
-                const int16_t b = pre ? s.b[t] : bias[d];
-                const uint8_t bs = pre ? s.bs[t] : bias_sh[d];
-                v = clamp_i16_i64((int64_t)v + (int64_t)rescale32((int32_t)b, bs, frac));
-            }
+            int16_t v = clamp_i16_i64(rescale64(tot[t], (uint8_t)(shifts[d] + act_frac), frac));
+            if (bias) v = clamp_i16_i64((int64_t)v + (int64_t)rescale32((int32_t)bias[d], bias_sh[d], frac));
             y[t] = v;
         }
-        const int pos = pre ? s.pos : st->pos;
+        const int pos = st->pos;
         if (seg < 2) {
-            const int32_t c = pre ? s.c : rope[p];
-            const int32_t sn = pre ? s.s : rope[half + p];
+            const int32_t c = rope[p];
+            const int32_t sn = rope[half + p];
             const int32_t x0 = y[0], x1 = y[1];
             y[0] = clamp_i16(rshift_round32(wsub32(wmul32(x0, c), wmul32(x1, sn)), MYL_TV_ROPE_FRAC_BITS));
             y[1] = clamp_i16(rshift_round32(wadd32(wmul32(x1, c), wmul32(x0, sn)), MYL_TV_ROPE_FRAC_BITS));

@@ -329,10 +329,11 @@ __device__ inline RmsFactor rms_factor_limbs(const int16_t (&x)[PER], const uint
     if ((threadIdx.x & 63) == 0)
         for (int j = 0; j < 3; ++j) red[w][j] = l[j];
     __syncthreads();
-    if (threadIdx.x < 64) {
+    if (threadIdx.x < 64) {  // wave 0, every lane: the table entry is a wave-wide search
 #pragma unroll
         for (int j = 0; j < 3; ++j) l[j] = wave_sum_u64((int)threadIdx.x < nw ? red[threadIdx.x][j] : 0);
-        if (threadIdx.x == 0) *sf = rms_factor_of(limbs_value(l), ref, p);
+        const RmsFactor f = rms_factor_wave(limbs_value(l), ref, p);
+        if (threadIdx.x == 0) *sf = f;
     }
     __syncthreads();
     return *sf;

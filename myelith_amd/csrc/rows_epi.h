@@ -32,12 +32,14 @@ struct EpiQKVRows : EpiApply<EpiQKVRows> {
     int nq, nkv;
     int16_t* out; int ldo;
     EpiQKVRows offset_m(int m0) const { EpiQKVRows e = *this; e.out += (size_t)m0 * ldo; return e; }
-    __device__ inline void one(int n, int m, int64_t acc) const {
+    // the requantised projection (+ bias) of output n, not stored
+    __device__ inline int16_t value(int n, int64_t acc) const {
         const uint8_t frac = n < nq ? q_frac : (n < nq + nkv ? k_frac : v_frac);
         int16_t v = clamp_i16_i64(rescale64(acc, (uint8_t)(shifts[n] + act_frac), frac));
         if (bias) v = clamp_i16_i64((int64_t)v + (int64_t)rescale32((int32_t)bias[n], bias_sh[n], frac));
-        out[(size_t)m * ldo + n] = v;
+        return v;
     }
+    __device__ inline void one(int n, int m, int64_t acc) const { out[(size_t)m * ldo + n] = value(n, acc); }
 };
 
 // o_proj / down_proj with the residual add (model.rs:576-593, 612-671):
@@ -59,12 +61,22 @@ struct EpiResidRows : EpiApply<EpiResidRows> {
     }
     // the output element, also stored
     __device__ inline int16_t value(int n, int m, int64_t acc) const {
-        const uint8_t af = acc_frac[n];
-        const int16_t o = clamp_i16_i64(rescale64(acc, (uint8_t)(shifts[n] + act_frac), af));
-        const int64_t h = rescale64((int64_t)res[(size_t)m * ldr + n], res_frac[n], af);
-        const int16_t y = clamp_i16_i64(rescale64(wadd64(h, (int64_t)o), af, out_frac[n]));
+        const int16_t y = value_of(acc, fin_ops(n, m));
         out[(size_t)m * ldo + n] = y;
         return y;
+    }
+    // The same in two steps, so a caller can issue every operand load of
+    // several elements before any store (a store may alias the operands, so
+    // the compiler would otherwise keep each element's loads behind the
+    // previous element's stores: one memory round trip per element).
+    struct FinOps { uint8_t af, sh, rf, of; int16_t r; };
+    __device__ inline FinOps fin_ops(int n, int m) const {
+        return FinOps{acc_frac[n], shifts[n], res_frac[n], out_frac[n], res[(size_t)m * ldr + n]};
+    }
+    __device__ inline int16_t value_of(int64_t acc, const FinOps& o) const {
+        const int16_t v = clamp_i16_i64(rescale64(acc, (uint8_t)(o.sh + act_frac), o.af));
+        const int64_t h = rescale64((int64_t)o.r, o.rf, o.af);
+        return clamp_i16_i64(rescale64(wadd64(h, (int64_t)v), o.af, o.of));
     }
     __device__ inline void one(int n, int m, int64_t acc) const { (void)value(n, m, acc); }
 };
