@@ -521,3 +521,35 @@ def test_logsoftmax_matches_float_log_softmax(oracle):
     z = np.array([5000, -100000, -200000], np.int32)
     assert oracle.logsoftmax_at(z, lut, 0) == 0
     assert oracle.logsoftmax_at(z, lut, 3) == 0 and oracle.logsoftmax_at(z, lut, -1) == 0
+
+
+def test_probability_sums_bound_the_i32_pv_path(oracle):
+    """The decode P.V kernel for exp tables without negative entries sums
+    p_j v_j in i32 (wrapping partial sums, exact when the total fits).  Its
+    premise, checked on the oracle's softmax_int (softmax.rs:12-64) with the
+    contract's exp table: every p_j lies in [0, 2^14] and sum_j p_j <= 2^14 +
+    L/2 (each p_j is e_j 2^14 / S rounded to nearest), so |sum_j p_j v_j| <=
+    (2^14 + L/2) 2^15 < 2^31 for L <= 65536.  Rows: equal scores (every p_j
+    rounded up the most), two levels, a spike, spreads at the table's edge,
+    and random rows, at lengths up to 4097."""
+    from myelith_amd.luts import LutSet
+    lut = np.asarray(LutSet.for_head_dim(128).exp, np.int16)
+    assert lut.min() >= 0
+    shift = 14 - 8  # score frac 14, exp-table input frac 8
+    r = np.random.default_rng(11)
+    rows = []
+    for L in (1, 2, 3, 7, 100, 257, 1000, 2049, 4097):
+        rows.append(np.zeros(L, np.int32))                                  # all equal
+        rows.append(np.where(np.arange(L) % 2 == 0, 0, -(1 << 12)).astype(np.int32))  # two levels
+        spike = np.full(L, -(1 << 30), np.int32)
+        spike[L // 2] = 5
+        rows.append(spike)
+        edge = len(lut) << shift
+        rows.append((-r.integers(0, edge + 64, L)).astype(np.int32))        # around the table's end
+        rows.append(r.integers(-(1 << 20), 1 << 20, L).astype(np.int32))
+    for z in rows:
+        p = oracle.softmax_int(z, lut, shift, 14).astype(np.int64)
+        L = len(z)
+        assert p.min() >= 0 and p.max() <= 1 << 14, L
+        assert p.sum() <= (1 << 14) + L // 2, (L, int(p.sum()))
+        assert ((1 << 14) + L / 2) * 32768 < 2 ** 31 or L > 65536
