@@ -295,9 +295,9 @@ def batched_decode(model, seed: int, batches=(8, 32), ctx: int = 2048, steps: in
 def e2e_05b(backend, seed: int, prompt_len: int = 256, n_decode: int = 128):
     """The Qwen2.5-0.5B-shape model (24 layers, hidden 896, 14/2 heads,
     head_dim 64, intermediate 4864, vocab 151936, tied int8 LM head) end to
-    end at batch 1: a 256-token seeded prompt through forward_token (the
-    reference's prompt loop, generate.rs:28-32), then 128 greedy decode steps
-    chained on the device.  Bytes per decode token: 357,826,560 of layer
+    end at batch 1: a 256-token seeded prompt (one batch of rows, equal to
+    the reference's forward_token prompt loop, generate.rs:28-32), then 128
+    greedy decode steps chained on the device.  Bytes per decode token: 357,826,560 of layer
     weights + 136,134,656 of LM head + 12,288 per cached position of KV."""
     import numpy as np
     import torch
@@ -307,8 +307,10 @@ def e2e_05b(backend, seed: int, prompt_len: int = 256, n_decode: int = 128):
     model = IntegerModel(backend, spec, LutSet.for_head_dim(spec["head_dim"]))
     rng = np.random.default_rng(seed + 5)
     prompt = rng.integers(0, spec["vocab"], prompt_len).astype(np.uint32)
-    logits = model.prefill(prompt[:8], 0)  # warm-up (also captures the step graph below)
-    model.decode_greedy(int(np.argmax(logits)), 8, 4)
+    # warm-up: a prompt long enough for the row path (16 tokens or more), and
+    # the step graph's capture
+    logits = model.prefill(prompt[:32], 0)
+    model.decode_greedy(int(np.argmax(logits)), 32, 4)
     model.reset()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     torch.cuda.synchronize()

@@ -401,6 +401,93 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i16_stream(Src16 src, const i
     epi.finish(es);
 }
 
+// Short rows (K a multiple of 128, K <= 2048: the 0.5B-shape LM head at K =
+// 896): a wave load of 1 KiB covers eight rows, 128 bytes each, so every lane
+// carries 16 bytes, and the eight rows reduce together with three DPP steps
+// over their 8-lane groups, instead of one whole-wave reduction per row
+// (which dominated at one 1 KiB step per row).  A group is 8 rows (lane l:
+// row 8 g + l / 8, bytes 16 (l % 8) of each 128-byte step), all K / 128 steps
+// of the group in one batch; two batches alternate.  Records hold the rows'
+// exact sums; the epilogue runs on row pairs (Epi::group<2>).
+template <int STEPS, int WAVES, class Src, class Epi>
+__global__ __launch_bounds__(WAVES * 64) void gemv_i8_stream8(Src src, const int8_t* __restrict__ W, int N, int K,
+                                                              int gpw, Epi epi) {
+    extern __shared__ __align__(16) int8_t lds[];
+    constexpr int kRows = 8;  // rows per group
+    const int kpad = ((K + 15) >> 4) << 4;
+    int8_t* hi_plane = lds;
+    int8_t* lo_plane = lds + kpad + kStageSlack;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    int64_t* rec = reinterpret_cast<int64_t*>(lds + 2 * (kpad + kStageSlack)) + (size_t)wave * gpw * kRows;
+    const int nw = gridDim.x * WAVES;
+    const int ngroups = (N + kRows - 1) / kRows;
+    constexpr int kThreads = WAVES * kWave;
+    const typename Src::Pre pre = src.pre(K, kpad, kThreads);
+    typename Epi::State es;
+    epi.begin(es);
+    __builtin_amdgcn_sched_barrier(0);  // staging loads before the first weight batch
+
+    const uint32_t wbytes = (uint32_t)N * (uint32_t)K;  // < 2^32 (checked by the launcher)
+    const __amdgpu_buffer_rsrc_t wr = weight_rsrc(W, wbytes);
+    const int sub = lane & 7, rin = lane >> 3;
+    auto load = [&](uint4 (&buf)[STEPS], int g) {
+        const int row = g * kRows + rin;
+        const uint32_t base = (uint32_t)row * (uint32_t)K + (uint32_t)sub * 16u;
+#pragma unroll
+        for (int u = 0; u < STEPS; ++u) buf[u] = bload16(wr, row < N ? base + (uint32_t)u * 128u : wbytes);
+    };
+    int cnt = 0;
+    auto group = [&](const uint4 (&buf)[STEPS]) {
+        int32_t ahi = 0, alo = 0, aws = 0;
+#pragma unroll
+        for (int u = 0; u < STEPS; ++u) {
+            const int k = u * 128 + sub * 16;
+            const uint4 h = *reinterpret_cast<const uint4*>(hi_plane + k);
+            const uint4 l = *reinterpret_cast<const uint4*>(lo_plane + k);
+            ahi = sdot4(buf[u].x, h.x, ahi);
+            ahi = sdot4(buf[u].y, h.y, ahi);
+            ahi = sdot4(buf[u].z, h.z, ahi);
+            ahi = sdot4(buf[u].w, h.w, ahi);
+            alo = sdot4(buf[u].x, l.x, alo);
+            alo = sdot4(buf[u].y, l.y, alo);
+            alo = sdot4(buf[u].z, l.z, alo);
+            alo = sdot4(buf[u].w, l.w, alo);
+            aws = sdot4(buf[u].x, 0x01010101u, aws);
+            aws = sdot4(buf[u].y, 0x01010101u, aws);
+            aws = sdot4(buf[u].z, 0x01010101u, aws);
+            aws = sdot4(buf[u].w, 0x01010101u, aws);
+        }
+        // each partial is exact in i32 over the row (K <= 2048); the row's 8
+        // lanes reduce together, every lane of the group gets the totals
+        ahi = row_sum8_i32(ahi);
+        alo = row_sum8_i32(alo);
+        aws = row_sum8_i32(aws);
+        if (sub == 0) rec[cnt * kRows + rin] = (int64_t)ahi * 256 + (int64_t)alo + (int64_t)aws * 128;
+        ++cnt;
+    };
+    uint4 A[STEPS], B[STEPS];
+    const int g0 = blockIdx.x * WAVES + wave;
+    load(A, g0);
+    // the lane's first row pair (pairs q = lane: group q / 4, rows 2 (q % 4) ..)
+    epi.prefetch(es, (g0 + (lane >> 2) * nw) * kRows + 2 * (lane & 3), N);
+    src.stage_i8(pre, hi_plane, lo_plane, K, kpad, kThreads);
+    __syncthreads();
+    for (int g = g0; g < ngroups; g += 2 * nw) {
+        load(B, g + nw);  // past the end: zeros
+        group(A);
+        load(A, g + 2 * nw);
+        if (g + nw < ngroups) group(B);
+    }
+    // row pairs: pair q of the wave's records is rows 2 (q % 4), + 1 of group q / 4
+    for (int q = lane; q < cnt * (kRows / 2); q += kWave) {
+        const int j = q >> 2, p = q & 3;
+        const int64_t tot[2] = {rec[j * kRows + 2 * p], rec[j * kRows + 2 * p + 1]};
+        epi.group(es, (g0 + j * nw) * kRows + 2 * p, N, tot);
+    }
+    epi.finish(es);
+}
+
 // ---- launchers ------------------------------------------------------------------
 
 // Blocks of a kernel that fit on one CU at `lds` bytes of dynamic LDS.  The
@@ -456,6 +543,21 @@ hipError_t stream_i8(const Src& src, const int8_t* W, int N, int K, const Epi& e
     const int grid = stream_grid(kern, WAVES, stream_lds_bytes(K, 1, WAVES, kGpwReserve, R), (N + R - 1) / R, cus, &gpw,
                                  occ_cap);
     const size_t lds = stream_lds_bytes(K, 1, WAVES, gpw, R);
+    if (lds > kStreamLdsMax) return hipErrorInvalidValue;
+    kern<<<grid, WAVES * 64, lds, s>>>(src, W, N, K, gpw, e);
+    return hipGetLastError();
+}
+
+// The 8-row short-row stream (gemv_i8_stream8) for K = 128 STEPS.
+template <int STEPS, int WAVES, class Src, class Epi>
+hipError_t stream_i8_rows8(const Src& src, const int8_t* W, int N, int K, const Epi& e, hipStream_t s, int cus,
+                           int occ_cap = 0) {
+    if ((uint64_t)N * (uint64_t)K > 0xFFFFFF00ull || K != 128 * STEPS || N < 1) return hipErrorInvalidValue;
+    auto kern = gemv_i8_stream8<STEPS, WAVES, Src, Epi>;
+    int gpw = 0;
+    const int grid = stream_grid(kern, WAVES, stream_lds_bytes(K, 1, WAVES, kGpwReserve, 8), (N + 7) / 8, cus, &gpw,
+                                 occ_cap);
+    const size_t lds = stream_lds_bytes(K, 1, WAVES, gpw, 8);
     if (lds > kStreamLdsMax) return hipErrorInvalidValue;
     kern<<<grid, WAVES * 64, lds, s>>>(src, W, N, K, gpw, e);
     return hipGetLastError();

@@ -1201,8 +1201,10 @@ hipError_t head_step(myl_model* m) {
         return stream_i16<2, 4, 8>(src, m->lm16, m->V, m->H, hd, st, m->cus);
     }
     EpiHead hd{m->lm8_shifts, m->final_norm_frac, m->logits, m->state};
-    // a small model's row fits one 1 KiB step: one-step batches, one block
-    // per CU (0.5B decode about 1 % faster per token than 4-step batches)
+    // a small model's row is a few 128-byte steps: eight rows per wave load
+    // (K = 896, the 0.5B shape)
+    if (m->H == 896) return stream_i8_rows8<7, 8>(src, m->lm8, m->V, m->H, hd, st, m->cus, 1);
+    // other rows of one 1 KiB step: one-step batches, one block per CU
     if (m->H <= 1024) return stream_i8<2, 1, 8, true>(src, m->lm8, m->V, m->H, hd, st, m->cus, 1);
     return stream_i8<2, 4, 8, true>(src, m->lm8, m->V, m->H, hd, st, m->cus);
 }

@@ -8,7 +8,7 @@ The oracle is the CPU checker (oracle/), run token by token the way the
 reference's generate loop runs (INTEGER_LLM/runtime/src/generate.rs:28-50);
 batches are independent sequences, each on its own cache.  What is written
 is answers, not inputs: hashes of logits and KV caches, greedy tokens,
-log-softmax sums.  About 20 minutes on 8 cores.
+log-softmax sums.  About 25 minutes on 8 cores (the 28-layer prompt included).
 """
 from __future__ import annotations
 
@@ -60,27 +60,35 @@ def decode_b1(om, spec) -> dict:
         lh.append(W.h64(logits))
     dig.step(logits, tok)
     n_pos = cfg["ctx"] + cfg["steps"]
-    return {"tokens": tokens, "logits_h64": lh, "digest": dig.hexdigest(),
-            "kv_sha256": W.kv_hash(om.read_kv, spec["layers"], spec["kv_heads"], n_pos)}
+    kv_greedy = W.kv_hash(om.read_kv, spec["layers"], spec["kv_heads"], n_pos)
+    forced_tokens = W.uniform_tokens(cfg["forced_seed"], cfg["forced"], spec["vocab"])
+    forced_h = []
+    for i, t in enumerate(forced_tokens):
+        forced_h.append(W.h64(om.forward_token(int(t), n_pos + i)))
+    return {"tokens": tokens, "logits_h64": lh, "digest": dig.hexdigest(), "kv_sha256": kv_greedy,
+            "forced_logits_h64": forced_h,
+            "forced_kv_sha256": W.kv_hash(om.read_kv, spec["layers"], spec["kv_heads"], n_pos + cfg["forced"])}
 
 
 def batch_decode(om, spec, cfg) -> dict:
     prompts = W.batch_prompts(cfg, spec["vocab"])
-    first, tokens, last_h, kv = [], [], [], []
+    first, tokens, last_h, step_h, kv = [], [], [], [], []
     for s in range(cfg["B"]):
         logits = run_prompt(om, prompts[s])
         tok = int(np.argmax(logits))
         first.append(tok)
-        seq_toks = []
+        seq_toks, seq_h = [], []
         for i in range(cfg["steps"]):
             logits = om.forward_token(tok, cfg["ctx"][s] + i)
             tok = int(np.argmax(logits))
             seq_toks.append(tok)
+            seq_h.append(W.h64(logits))
         tokens.append(seq_toks)
+        step_h.append(seq_h)
         last_h.append(W.h64(logits))
         kv.append(W.kv_hash(om.read_kv, spec["layers"], spec["kv_heads"], cfg["ctx"][s] + cfg["steps"]))
         log(f"  B={cfg['B']} sequence {s} (context {cfg['ctx'][s]}) done")
-    return {"first": first, "tokens": tokens, "last_logits_h64": last_h, "kv_sha256": kv}
+    return {"first": first, "tokens": tokens, "last_logits_h64": last_h, "step_logits_h64": step_h, "kv_sha256": kv}
 
 
 def teacher_forced(om, spec) -> dict:
@@ -103,16 +111,47 @@ def teacher_forced(om, spec) -> dict:
     return {"row_logits_h64": rows, "argmax": argmax, "logsoftmax_sum_q16": sums, "kv_sha256": kv}
 
 
+def full_depth(threads: int) -> dict:
+    """The 28-layer model: a prompt then greedy steps, token by token on the
+    oracle (its own model object: the other workloads use the two-layer cut)."""
+    cfg, spec = W.FULL_DEPTH, W.spec_full()
+    t0 = time.time()
+    om = OracleModel(spec, LutSet.for_head_dim(spec["head_dim"]), threads=threads)
+    log(f"28-layer oracle model built in {time.time() - t0:.1f} s")
+    prompt = W.uniform_tokens(cfg["prompt_seed"], cfg["ctx"], spec["vocab"])
+    logits = run_prompt(om, prompt)
+    out = {"prompt_logits_h64": W.h64(logits),
+           "prompt_kv_sha256": W.kv_hash(om.read_kv, spec["layers"], spec["kv_heads"], cfg["ctx"])}
+    tok = int(np.argmax(logits))
+    tokens, lh = [tok], []
+    for i in range(cfg["steps"]):
+        logits = om.forward_token(tok, cfg["ctx"] + i)
+        tok = int(np.argmax(logits))
+        tokens.append(tok)
+        lh.append(W.h64(logits))
+    out.update(tokens=tokens, step_logits_h64=lh,
+               kv_sha256=W.kv_hash(om.read_kv, spec["layers"], spec["kv_heads"], cfg["ctx"] + cfg["steps"]))
+    om.close()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--threads", type=int, default=8)
-    ap.add_argument("--only", choices=("decode_b1", "batch_8", "batch_32", "teacher_4x1024"))
+    ap.add_argument("--only", choices=("decode_b1", "batch_8", "batch_32", "teacher_4x1024", "full_depth"))
     args = ap.parse_args()
     spec = W.spec()
     data = json.loads(OUT.read_text()) if OUT.exists() else {}
     data["spec"] = spec
+    data["spec_full"] = W.spec_full()
     data["workloads"] = {"decode_b1": W.DECODE_B1, "batch_8": W.BATCH_8, "batch_32": W.BATCH_32,
-                         "teacher_4x1024": W.TEACHER_4x1024}
+                         "teacher_4x1024": W.TEACHER_4x1024, "full_depth": W.FULL_DEPTH}
+    if args.only == "full_depth":
+        t0 = time.time()
+        data.setdefault("answers", {})["full_depth"] = full_depth(args.threads)
+        log(f"full_depth: {time.time() - t0:.0f} s")
+        OUT.write_text(json.dumps(data, indent=1) + "\n")
+        return 0
     t0 = time.time()
     om = OracleModel(spec, LutSet.for_head_dim(spec["head_dim"]), threads=args.threads)
     log(f"oracle model built in {time.time() - t0:.1f} s")
@@ -128,6 +167,11 @@ def main() -> int:
         log(f"{name}: {time.time() - t0:.0f} s")
         OUT.write_text(json.dumps(data, indent=1) + "\n")
     om.close()
+    if not args.only:
+        t0 = time.time()
+        data.setdefault("answers", {})["full_depth"] = full_depth(args.threads)
+        log(f"full_depth: {time.time() - t0:.0f} s")
+        OUT.write_text(json.dumps(data, indent=1) + "\n")
     return 0
 
 

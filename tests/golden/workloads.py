@@ -10,6 +10,10 @@ layers exercise every kernel of the 28-layer model at its real shape; and
 since every tensor is seeded by (model seed, layer, role), these two layers
 are the first two layers of the 28-layer benchmark model of the same seed.
 
+FULL_DEPTH is the whole 28-layer model of the same seed (the benchmark
+model): a prompt through the row path and greedy steps, so every layer's K/V
+rows are pinned independently of the device's own cache.
+
 Token ids come from the SplitMix64 stream (the reference PRNG,
 INTEGER_LLM/kernels/src/prng.rs:7-14), so the workload does not depend on
 numpy's generators.
@@ -26,11 +30,14 @@ GAMMA = 0x9E3779B97F4A7C15
 ARCH_7B = dict(vocab=152064, hidden=3584, layers=2, heads=28, kv_heads=4, head_dim=128, inter=18944,
                lm_head_int16=1, attention_bias=1)
 SEED = 7
-MAX_POS = 2080
+MAX_POS = 2104
 
 # batch 1: a 2048-token prompt through the prompt row path, then greedy steps
-# at positions 2048-2071 (RoPE LUT rows wrap at 2048).
-DECODE_B1 = dict(prompt_seed=101, ctx=2048, steps=24)
+# at positions 2048-2071 (RoPE LUT rows wrap at 2048), then `forced` steps at
+# positions 2072-2095 whose tokens come from the SplitMix64 stream of
+# forced_seed (a synthetic model's greedy chain tends to settle on one token;
+# drawn tokens make every step read a different embedding row).
+DECODE_B1 = dict(prompt_seed=101, ctx=2048, steps=24, forced=24, forced_seed=102)
 # lock-step greedy decode of B sequences after their contexts were prefilled
 # through the batched forward in chunks of 4096 // B positions per sequence.
 BATCH_8 = dict(B=8, ctx=[2048] * 8, steps=8, prompt_seed=200)
@@ -38,10 +45,21 @@ BATCH_32 = dict(B=32, ctx=[2048 if s % 9 == 0 else 600 + 7 * s for s in range(32
 # teacher-forced rows: 4 sequences x 1024 Zipf(1.1) token ids in one batch.
 TEACHER_4x1024 = dict(B=4, T=1024, zipf_s=1.1, token_seed=400)
 
+# the whole 28-layer benchmark model (same seed): a 1024-token prompt through
+# the prompt row path (every layer's K/V rows written by the row kernels),
+# then greedy steps from the captured step graph.
+FULL_DEPTH = dict(layers=28, max_pos=1040, prompt_seed=500, ctx=1024, steps=8)
+
 
 def spec() -> dict:
     s = dict(ARCH_7B)
     s.update(seed=SEED, max_pos=MAX_POS)
+    return s
+
+
+def spec_full() -> dict:
+    s = dict(ARCH_7B)
+    s.update(seed=SEED, layers=FULL_DEPTH["layers"], max_pos=FULL_DEPTH["max_pos"])
     return s
 
 

@@ -52,8 +52,9 @@ def test_small_moe_all_tokens(backend, T, widths):
 
 def test_qwen15_moe_4096_tokens(backend):
     """The Qwen1.5-MoE-A2.7B-shaped layer on 4096 tokens: the whole route
-    (ids, gates, counts, offsets, dispatch order) and the outputs of 96
-    tokens (first, last and scattered) equal the oracle's."""
+    (ids, gates, counts, offsets, dispatch order) and the output of every
+    one of the 4096 tokens equal the oracle's (about ten seconds of the
+    oracle on the host's cores)."""
     from myelith_amd.moe import moe_spec
     spec = moe_spec(5)
     case("qwen1.5-moe 4096 tokens")
@@ -64,9 +65,8 @@ def test_qwen15_moe_4096_tokens(backend):
     xh = x.cpu().numpy()
     ro = om.route(xh)
     compare_route(gm.route(T), ro)
-    r = np.random.default_rng(3)
-    for t in sorted(set(range(32)) | set(range(T - 32, T)) | set(r.integers(0, T, 32).tolist())):
-        assert np.array_equal(y[t], om.token(xh[t], ro["ids"][t], ro["gates"][t])), t
+    bad = [t for t in range(T) if not np.array_equal(y[t], om.token(xh[t], ro["ids"][t], ro["gates"][t]))]
+    assert not bad, f"{len(bad)} of {T} token outputs differ, first {bad[:8]}"
     # a second call with fewer tokens reuses the buffers
     y2 = gm.forward(x[:100]).cpu().numpy()
     r2 = om.route(xh[:100])

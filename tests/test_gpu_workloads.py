@@ -9,15 +9,23 @@ runs once where the fixtures are made, not on every GPU run.
   - batch 1: a 2048-token prompt through the prompt row path, 24 greedy steps
     from the captured step graph at positions 2048-2071 (RoPE LUT rows wrap at
     2048, GQA group 7): every step's logits, the tokens, the generate.rs
-    digest and the whole KV cache;
+    digest and the whole KV cache; then 24 steps at positions 2072-2095 on
+    SplitMix64-drawn tokens (every step a different embedding row): every
+    step's logits and the KV cache again;
   - lock-step greedy decode of 8 sequences over 2048-token contexts and of 32
     sequences over contexts of 600-2048 positions, contexts prefilled through
     the batched forward in the benchmark's chunks: first tokens, every step's
-    tokens, the last step's logits, every sequence's KV cache;
+    tokens, the last step's logits, every sequence's KV cache; then the same
+    decode again one step per call, every step's logits of every sequence;
   - 4 x 1024 teacher-forced Zipf(1.1) rows in one batch (256 x 256 tiles at
     K = 18944, the byte-plane int16 head at V = 152064, four 256-position
     attention ranges): every row's logits and argmax, the four integer
-    log-softmax sums, the KV caches.
+    log-softmax sums, the KV caches;
+  - the whole 28-layer benchmark model: a 1024-token prompt through the
+    prompt row path (last row's logits, the KV cache of all 28 layers, so
+    every layer's row kernels are pinned by the oracle's own cache), then 8
+    greedy steps from the captured step graph (every step's logits, the
+    tokens, the KV cache).
 """
 from __future__ import annotations
 
@@ -40,6 +48,7 @@ import workloads as W  # noqa: E402
 def answers():
     data = json.loads((GOLDEN / "workloads_7b.json").read_text())
     assert data["spec"] == W.spec(), "workloads_7b.json was written for another model; rerun its generator"
+    assert data["spec_full"] == W.spec_full(), "workloads_7b.json was written for another model; rerun its generator"
     return data["answers"]
 
 
@@ -71,7 +80,15 @@ def test_decode_b1_2048_context(model, answers):
     for lg, t in zip([logits] + list(steps), want["tokens"]):
         dig.step(lg, t)
     assert dig.hexdigest() == want["digest"]
-    assert W.kv_hash(model.read_kv, spec["layers"], spec["kv_heads"], cfg["ctx"] + cfg["steps"]) == want["kv_sha256"]
+    n_pos = cfg["ctx"] + cfg["steps"]
+    assert W.kv_hash(model.read_kv, spec["layers"], spec["kv_heads"], n_pos) == want["kv_sha256"]
+    case(f"7B width decode b1: {cfg['forced']} steps on drawn tokens at positions {n_pos}-")
+    forced = W.uniform_tokens(cfg["forced_seed"], cfg["forced"], spec["vocab"])
+    for i, t in enumerate(forced):
+        lg = model.forward_token(int(t), n_pos + i)
+        assert W.h64(lg) == want["forced_logits_h64"][i], f"logits at position {n_pos + i} (token {int(t)})"
+    assert (W.kv_hash(model.read_kv, spec["layers"], spec["kv_heads"], n_pos + cfg["forced"])
+            == want["forced_kv_sha256"])
 
 
 @pytest.mark.parametrize("name", ["batch_8", "batch_32"])
@@ -101,6 +118,16 @@ def test_batch_decode_long_contexts(model, answers, name):
         got = W.kv_hash(lambda l, h, n: model.batch_read_kv(s, l, h, n), spec["layers"], spec["kv_heads"],
                         ctx[s] + cfg["steps"])
         assert got == want["kv_sha256"][s], f"KV cache of sequence {s}"
+    # every step's logits: the same decode once more, one step per call (the
+    # steps rewrite the same cache rows with the same values)
+    case(f"7B width lock-step decode B={B}: every step's logits")
+    tok = np.array(first)
+    for i in range(cfg["steps"]):
+        step = model.batch_decode_greedy(np.arange(B), np.array(ctx) + i, tok, 1)
+        lg = model.batch_logits_dev(B).cpu().numpy()
+        for s in range(B):
+            assert W.h64(lg[s]) == want["step_logits_h64"][s][i], f"logits of sequence {s} at step {i}"
+        tok = step[0]
 
 
 def test_teacher_forced_4x1024(model, backend, answers):
@@ -129,3 +156,29 @@ def test_teacher_forced_4x1024(model, backend, answers):
     for b in range(B):
         got = W.kv_hash(lambda l, h, n: model.batch_read_kv(b, l, h, n), spec["layers"], spec["kv_heads"], T)
         assert got == want["kv_sha256"][b], f"KV cache of sequence {b}"
+
+
+def test_full_depth_prompt_and_decode(backend, answers):
+    """The 28-layer benchmark model: the prompt's KV cache at every layer and
+    the last row's logits, then graph decode steps, against the oracle's own
+    token-by-token run (no device state handed to the oracle)."""
+    from myelith_amd.luts import LutSet
+    from myelith_amd.model import IntegerModel
+    cfg, want = W.FULL_DEPTH, answers["full_depth"]
+    spec = W.spec_full()
+    case(f"7B 28 layers: prompt {cfg['ctx']} rows, {cfg['steps']} graph steps")
+    m = IntegerModel(backend, spec, LutSet.for_head_dim(spec["head_dim"]))
+    try:
+        prompt = W.uniform_tokens(cfg["prompt_seed"], cfg["ctx"], spec["vocab"])
+        logits = m.prefill(prompt, 0)
+        assert W.h64(logits) == want["prompt_logits_h64"], "last prompt row's logits"
+        assert W.kv_hash(m.read_kv, spec["layers"], spec["kv_heads"], cfg["ctx"]) == want["prompt_kv_sha256"]
+        first = int(np.argmax(logits))
+        toks, steps = m.decode_greedy(first, cfg["ctx"], cfg["steps"], want_logits=True)
+        for i in range(cfg["steps"]):
+            assert W.h64(steps[i]) == want["step_logits_h64"][i], f"logits at position {cfg['ctx'] + i}"
+        assert [first] + [int(t) for t in toks] == want["tokens"]
+        assert (W.kv_hash(m.read_kv, spec["layers"], spec["kv_heads"], cfg["ctx"] + cfg["steps"])
+                == want["kv_sha256"])
+    finally:
+        m.close()
