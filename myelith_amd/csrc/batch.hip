@@ -352,7 +352,7 @@ __global__ __launch_bounds__(kFinNormThreads) void finish_resid_norm_kernel(unsi
     EpiResidRows::FinOps op[PER];
 #pragma unroll
     for (int t = 0; t < PER; ++t) {
-        const int n = min(threadIdx.x + t * kFinNormThreads, N - 1);  // lanes past N load a valid element, unused
+        const int n = min((int)threadIdx.x + t * kFinNormThreads, N - 1);  // lanes past N load a valid element, unused
         av[t] = (int64_t)acc[(size_t)m * N + n];
         op[t] = epi.fin_ops(n, m);
         sv[t] = xs[n];

@@ -434,4 +434,147 @@ __device__ inline void dec_pv_wide(int L, int base, const int32_t* __restrict__ 
     }
 }
 
+// ---- short contexts: one block per query head --------------------------------
+
+// Positions one dec_attn_short block holds: eight 16-byte K and V pieces per
+// thread (512 threads, HD / 8 lanes per row).
+template <int HD>
+constexpr int dec_short_max() { return 8 * 8 * (64 / (HD / 8)); }
+
+// The whole attention of one query head (attention.rs:42-90 with
+// softmax.rs:12-64) for L <= dec_short_max<HD>() positions, in one block:
+// z_j = (i32)RNE(q . k_j * mult, shift) into LDS, the max m and wrapping
+// exp-LUT sum S, p_j = RNE(e_j 2^14 / S) (the uniform split when S == 0),
+// and sum_j p_j v_j per dimension stored to out[0 .. HD).  For the tables
+// dec_pv_wide takes (no negative entry, nonzero prefix exp_lds <=
+// kDecExpLds): the sum is exact in i32.  Thread (wave w, lane) holds the 16
+// bytes at dims 8 (lane % (HD / 8)) of K and V rows RPR i + rr (rr = RS w +
+// lane / (HD / 8)), i < 8; all K, table and V loads are issued first, in
+// that order, through buffer descriptors (rows at L and beyond read zero).
+// 512 threads.
+template <int HD>
+__device__ inline void dec_attn_short(int L, const int16_t* __restrict__ q, const int16_t* __restrict__ kg,
+                                      const int16_t* __restrict__ vg, int64_t score_mult, uint8_t score_shift,
+                                      const int16_t* __restrict__ lut, uint32_t lut_len, uint8_t lut_shift,
+                                      int exp_lds, int32_t* __restrict__ out) {
+    constexpr int OPR = HD / 8;        // lanes per row, 8 dims each
+    constexpr int RS = 64 / OPR;       // rows per wave load
+    constexpr int RPR = 8 * RS;        // rows per block round (also the row groups)
+    constexpr int NR = 8;              // rounds
+    constexpr int LMAX = RPR * NR;
+    static_assert(LMAX == dec_short_max<HD>() && LMAX <= 512, "one score per thread");
+    static_assert(kDecExpLds == 8 * 512, "one 16-byte table piece per thread");
+    __shared__ __align__(16) int16_t elut[kDecExpLds];
+    __shared__ __align__(16) int32_t zs[LMAX];
+    __shared__ __align__(16) int16_t plt[RPR][NR];
+    __shared__ __align__(16) int32_t red[RPR][HD];
+    __shared__ int32_t redm[8];
+    __shared__ uint32_t reds[8];
+    const int tid = (int)threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int oc = lane % OPR, rr = w * RS + lane / OPR;
+    const uint32_t kvbytes = (uint32_t)L * HD * 2u;
+    const __amdgpu_buffer_rsrc_t rk = weight_rsrc(kg, kvbytes);
+    const __amdgpu_buffer_rsrc_t rv = weight_rsrc(vg, kvbytes);
+    const uint4 qv = *reinterpret_cast<const uint4*>(q + 8 * oc);
+    uint4 kv[NR], vv[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) kv[i] = cload16(rk, ((uint32_t)(RPR * i + rr) * HD + 8 * oc) * 2u);
+    const __amdgpu_buffer_rsrc_t rl = weight_rsrc(lut, (uint32_t)((exp_lds + 7) & ~7) * 2u);
+    const uint4 lv = cload16(rl, (uint32_t)tid * 16u);
+    const int32_t lut0 = (int16_t)(cload4(weight_rsrc(lut, ((lut_len + 7u) & ~7u) * 2u), 0) & 0xFFFFu);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NR; ++i) vv[i] = cload16(rv, ((uint32_t)(RPR * i + rr) * HD + 8 * oc) * 2u);
+    __builtin_amdgcn_sched_barrier(0);
+    // scores: q . k = 256 sum(k q_hi) + sum(k q_lo) on v_dot2_i32_i16
+    // (|partials| < 2^31), row sums over the row's OPR lanes by DPP
+    uint4 qh, ql;
+    split_pair(qv.x, qh.x, ql.x);
+    split_pair(qv.y, qh.y, ql.y);
+    split_pair(qv.z, qh.z, ql.z);
+    split_pair(qv.w, qh.w, ql.w);
+    typedef short __attribute__((ext_vector_type(2))) s2;
+    auto d2 = [](uint32_t a, uint32_t c, int32_t t) {
+        return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, a), __builtin_bit_cast(s2, c), t, false);
+    };
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        int32_t ahi = 0, alo = 0;
+        ahi = d2(kv[i].x, qh.x, ahi);
+        ahi = d2(kv[i].y, qh.y, ahi);
+        ahi = d2(kv[i].z, qh.z, ahi);
+        ahi = d2(kv[i].w, qh.w, ahi);
+        alo = d2(kv[i].x, ql.x, alo);
+        alo = d2(kv[i].y, ql.y, alo);
+        alo = d2(kv[i].z, ql.z, alo);
+        alo = d2(kv[i].w, ql.w, alo);
+        if (OPR == 16) {
+            ahi = row_sum16_i32(ahi);
+            alo = row_sum16_i32(alo);
+        } else {
+            ahi = row_sum8_i32(ahi);
+            alo = row_sum8_i32(alo);
+        }
+        if (oc == 0) {
+            const int64_t dot = (int64_t)ahi * 256 + (int64_t)alo;
+            zs[RPR * i + rr] = (int32_t)rshift_round64(wmul64(dot, score_mult), score_shift);
+        }
+    }
+    *reinterpret_cast<uint4*>(elut + tid * 8) = lv;
+    __syncthreads();  // the scores and the table copy
+    const bool live = tid < L;
+    const int32_t zj = live ? zs[tid] : INT32_MIN;
+    const int32_t mx = block_max_i32_dpp(zj, redm);
+    // exp_lookup (softmax.rs:12-20) from the LDS copy, as in dec_pv_wide
+    const uint32_t sh = lut_shift & 31u;
+    const int32_t lut_one = lut_len > 0 ? lut0 : 1;
+    const uint32_t x = min((uint32_t)mx - (uint32_t)zj, 0x7FFFFFFFu);
+    const uint32_t idx = x >> sh;
+    const bool in = idx < (uint32_t)exp_lds;
+    const int32_t t = elut[in ? idx : 0u];
+    const int32_t e = live ? (x == 0 ? lut_one : (in ? t : 0)) : 0;
+    const int32_t S = __builtin_amdgcn_readfirstlane((int32_t)block_sum_u32_dpp((uint32_t)e, reds));
+    const int32_t one = 1 << MYL_TV_PROB_FRAC_BITS;
+    const uint32_t den = S == 0 ? (uint32_t)L : (uint32_t)S;
+    const uint32_t rs = recip32_u32(den);
+    int32_t ubase = 0, urem = 0;
+    if (S == 0) {
+        uint32_t qq, rr2;
+        udivmod32((uint32_t)one, (uint32_t)L, recip32((uint32_t)L), &qq, &rr2);
+        ubase = (int32_t)qq;
+        urem = wsub32(one, wmul32(ubase, L));
+    }
+    if (tid < LMAX) {
+        int32_t pv = 0;
+        if (live)
+            pv = S == 0 ? ubase + (((uint64_t)tid < (uint64_t)(int64_t)urem) ? 1 : 0)
+                        : softmax_div_round_pos(e << MYL_TV_PROB_FRAC_BITS, S, rs);
+        plt[tid % RPR][tid / RPR] = (int16_t)pv;
+    }
+    __syncthreads();
+    // P.V: rows RPR 2k + rr and RPR (2k + 1) + rr per v_dot2
+    int32_t a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const uint32_t* pw = reinterpret_cast<const uint32_t*>(&plt[rr][0]);
+#pragma unroll
+    for (int k = 0; k < NR / 2; ++k) {
+        const uint32_t pp = pw[k];
+        const uint32_t ra[4] = {vv[2 * k].x, vv[2 * k].y, vv[2 * k].z, vv[2 * k].w};
+        const uint32_t rb[4] = {vv[2 * k + 1].x, vv[2 * k + 1].y, vv[2 * k + 1].z, vv[2 * k + 1].w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            a[2 * u] = d2(pp, (ra[u] & 0xFFFFu) | (rb[u] << 16), a[2 * u]);
+            a[2 * u + 1] = d2(pp, (ra[u] >> 16) | (rb[u] & 0xFFFF0000u), a[2 * u + 1]);
+        }
+    }
+    *reinterpret_cast<int4*>(&red[rr][8 * oc]) = make_int4(a[0], a[1], a[2], a[3]);
+    *reinterpret_cast<int4*>(&red[rr][8 * oc + 4]) = make_int4(a[4], a[5], a[6], a[7]);
+    __syncthreads();
+    if (tid < HD) {
+        uint32_t sum = 0;
+#pragma unroll
+        for (int r = 0; r < RPR; ++r) sum += (uint32_t)red[r][tid];
+        out[tid] = (int32_t)sum;
+    }
+}
+
 }  // namespace myl

@@ -527,8 +527,10 @@ struct EpiSilu {
 };
 
 // LM head logits (model.rs:284-308) + first-maximum argmax (sampling.rs:8-18):
-// each lane keeps the best key of its rows; per wave the maximum goes to one
-// atomic, issued only when it beats the current key.
+// each lane keeps the best key of its rows; the block's maximum (waves, then
+// the block through LDS) goes to one atomic, issued only when it beats the
+// current key.  Every atomic of a launch targets one word, so they serialise:
+// one per block rather than one per wave.
 struct EpiHead {
     const uint8_t* shifts;
     uint8_t norm_frac;
@@ -565,10 +567,17 @@ struct EpiHead {
         }
     }
     __device__ inline void finish(State& s) const {
+        __shared__ uint64_t wbest[16];
         const uint64_t best = wave_max_u64(s.best);
-        if ((threadIdx.x & 63) == 0 && best) {
-            const uint64_t cur = __hip_atomic_load(&st->argmax_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (best > cur) atomicMax((unsigned long long*)&st->argmax_key, (unsigned long long)best);
+        const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6, lane = threadIdx.x & 63;
+        if (lane == 0) wbest[w] = best;
+        __syncthreads();
+        if (w == 0) {
+            const uint64_t b = wave_max_u64(lane < nw ? wbest[lane] : 0ull);
+            if (lane == 0 && b) {
+                const uint64_t cur = __hip_atomic_load(&st->argmax_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (b > cur) atomicMax((unsigned long long*)&st->argmax_key, (unsigned long long)b);
+            }
         }
     }
 };
@@ -639,6 +648,25 @@ __global__ __launch_bounds__(512) void attn_pv_wide_kernel(const DecodeState* __
     const int head = b.g * G + b.h;
     dec_pv_wide<HD>(L, base, scores + (size_t)head * score_ld, score_ld, vc + (size_t)b.g * max_pos * HD, lut,
                     lut_len, lut_shift, exp_lds, acc + (size_t)head * HD);
+}
+
+// The whole attention of one query head per block (dec_attn_short) for
+// contexts of at most dec_short_max<HD>() positions: grid (G, kv_heads),
+// block (h, g) works on query head g G + h; the head's i32 output is stored
+// to acc.  512 threads.
+template <int HD>
+__global__ __launch_bounds__(512) void attn_short_kernel(const DecodeState* __restrict__ st,
+                                                        const int16_t* __restrict__ q, const int16_t* __restrict__ kc,
+                                                        const int16_t* __restrict__ vc, int max_pos, int G,
+                                                        int64_t score_mult, uint8_t score_shift,
+                                                        const int16_t* __restrict__ lut, uint32_t lut_len,
+                                                        uint8_t lut_shift, int exp_lds, int32_t* __restrict__ acc) {
+    const int L = st->pos + 1;
+    if (L > dec_short_max<HD>()) return;  // the launcher bounds max_pos
+    const int g = (int)blockIdx.y, head = g * G + (int)blockIdx.x;
+    const size_t kv = (size_t)g * max_pos * HD;
+    dec_attn_short<HD>(L, q + (size_t)head * HD, kc + kv, vc + kv, score_mult, score_shift, lut, lut_len, lut_shift,
+                       exp_lds, acc + (size_t)head * HD);
 }
 
 // The general P.V kernel (dec_pv): one query head and kChunk positions, i64
@@ -1098,38 +1126,52 @@ hipError_t layer_step(myl_model* m, int l) {
             if (xsl >= 0 && (int64_t)G * G * ((chunks + (1 << xsl) - 1) >> xsl) >= (1 << 24)) xsl = -1;
             return xsl >= 0 ? dim3(8 * G * ((chunks + (1 << xsl) - 1) >> xsl)) : dim3(8 * G, (chunks + 7) / 8, kvh);
         };
-        const int chunks = (m->max_pos + kChunk - 1) / kChunk;
-        int sxs = -1;
-        const dim3 agrid = attn_grid(chunks, sxs);
-        if (hd == 128)
-            attn_scores_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, chunks, m->score_mult,
-                                                          score_shift, m->scores, m->score_ld, sxs, ginv);
-        else
-            attn_scores_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, chunks, m->score_mult,
-                                                         score_shift, m->scores, m->score_ld, sxs, ginv);
-        if (m->pv32) {
-            const int wchunks = (m->max_pos + kPvWide - 1) / kPvWide;
-            int wxs = -1;
-            const dim3 wgrid = attn_grid(wchunks, wxs);
+        // a short cache: one kernel, one block per query head
+        if (m->pv32 && m->max_pos <= (hd == 128 ? dec_short_max<128>() : dec_short_max<64>())) {
             int32_t* acc = reinterpret_cast<int32_t*>(m->attn_acc);
             if (hd == 128)
-                attn_pv_wide_kernel<128><<<wgrid, 512, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G,
-                                                                wchunks, m->exp_lut, (uint32_t)m->exp_len, lut_shift,
-                                                                m->exp_nz, acc, wxs, ginv);
+                attn_short_kernel<128><<<dim3(G, kvh), 512, 0, st>>>(m->state, m->q, kc, vc, m->max_pos, G,
+                                                                     m->score_mult, score_shift, m->exp_lut,
+                                                                     (uint32_t)m->exp_len, lut_shift, m->exp_nz, acc);
             else
-                attn_pv_wide_kernel<64><<<wgrid, 512, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G,
-                                                               wchunks, m->exp_lut, (uint32_t)m->exp_len, lut_shift,
-                                                               m->exp_nz, acc, wxs, ginv);
+                attn_short_kernel<64><<<dim3(G, kvh), 512, 0, st>>>(m->state, m->q, kc, vc, m->max_pos, G,
+                                                                    m->score_mult, score_shift, m->exp_lut,
+                                                                    (uint32_t)m->exp_len, lut_shift, m->exp_nz, acc);
         } else {
-            const int exp_lds = m->exp_nz <= kDecExpLds ? m->exp_nz : -1;
+            const int chunks = (m->max_pos + kChunk - 1) / kChunk;
+            int sxs = -1;
+            const dim3 agrid = attn_grid(chunks, sxs);
             if (hd == 128)
-                attn_pv_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G, chunks,
-                                                          m->exp_lut, (uint32_t)m->exp_len, lut_shift, exp_lds,
-                                                          m->attn_acc, sxs, ginv);
+                attn_scores_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, chunks, m->score_mult,
+                                                              score_shift, m->scores, m->score_ld, sxs, ginv);
             else
-                attn_pv_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G, chunks,
-                                                         m->exp_lut, (uint32_t)m->exp_len, lut_shift, exp_lds,
-                                                         m->attn_acc, sxs, ginv);
+                attn_scores_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->q, kc, m->max_pos, G, chunks, m->score_mult,
+                                                             score_shift, m->scores, m->score_ld, sxs, ginv);
+            if (m->pv32) {
+                const int wchunks = (m->max_pos + kPvWide - 1) / kPvWide;
+                int wxs = -1;
+                const dim3 wgrid = attn_grid(wchunks, wxs);
+                int32_t* acc = reinterpret_cast<int32_t*>(m->attn_acc);
+                if (hd == 128)
+                    attn_pv_wide_kernel<128><<<wgrid, 512, 0, st>>>(m->state, m->scores, vc, m->max_pos,
+                                                                    m->score_ld, G, wchunks, m->exp_lut,
+                                                                    (uint32_t)m->exp_len, lut_shift, m->exp_nz, acc,
+                                                                    wxs, ginv);
+                else
+                    attn_pv_wide_kernel<64><<<wgrid, 512, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G,
+                                                                   wchunks, m->exp_lut, (uint32_t)m->exp_len, lut_shift,
+                                                                   m->exp_nz, acc, wxs, ginv);
+            } else {
+                const int exp_lds = m->exp_nz <= kDecExpLds ? m->exp_nz : -1;
+                if (hd == 128)
+                    attn_pv_kernel<128><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G,
+                                                              chunks, m->exp_lut, (uint32_t)m->exp_len, lut_shift,
+                                                              exp_lds, m->attn_acc, sxs, ginv);
+                else
+                    attn_pv_kernel<64><<<agrid, 256, 0, st>>>(m->state, m->scores, vc, m->max_pos, m->score_ld, G,
+                                                             chunks, m->exp_lut, (uint32_t)m->exp_len, lut_shift,
+                                                             exp_lds, m->attn_acc, sxs, ginv);
+            }
         }
         e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -1202,8 +1244,9 @@ hipError_t head_step(myl_model* m) {
     }
     EpiHead hd{m->lm8_shifts, m->final_norm_frac, m->logits, m->state};
     // a small model's row is a few 128-byte steps: eight rows per wave load
-    // (K = 896, the 0.5B shape)
-    if (m->H == 896) return stream_i8_rows8<7, 8>(src, m->lm8, m->V, m->H, hd, st, m->cus, 1);
+    // (K = 896, the 0.5B shape), two blocks per CU (one: 23.2 us, two: 22.2 us
+    // for the 136 MB head on MI355X)
+    if (m->H == 896) return stream_i8_rows8<7, 8>(src, m->lm8, m->V, m->H, hd, st, m->cus, 2);
     // other rows of one 1 KiB step: one-step batches, one block per CU
     if (m->H <= 1024) return stream_i8<2, 1, 8, true>(src, m->lm8, m->V, m->H, hd, st, m->cus, 1);
     return stream_i8<2, 4, 8, true>(src, m->lm8, m->V, m->H, hd, st, m->cus);

@@ -265,6 +265,40 @@ def test_decode_attention_exp_table_variants(backend, hd, variant):
     compare_kv(gm, om, spec, 200)
 
 
+@pytest.mark.parametrize("hd,kvh,variant", [(64, 2, "calibrated"), (128, 1, "calibrated"), (64, 1, "zero"),
+                                             (128, 2, "zero")])
+def test_decode_attention_short_cache(backend, hd, kvh, variant):
+    """A cache of at most 512 (head_dim 64) or 256 (head_dim 128) positions
+    takes the one-kernel attention (a block per query head): every position
+    up to the full cache, through the token loop and the captured step graph,
+    with the calibrated table and an all-zero one (the uniform split); logits
+    and KV cache equal the oracle's."""
+    from myelith_amd.luts import LutSet
+    from myelith_amd.model import IntegerModel
+    from oracle.binding import OracleModel
+    max_pos = 512 if hd == 64 else 256
+    spec = tiny(hd, 0, 1, kvh, max_pos=max_pos)
+    case(f"short cache {variant} {spec}")
+    base = LutSet.for_head_dim(hd)
+    exp = np.asarray(base.exp, dtype=np.int16).copy()
+    if variant == "zero":
+        exp[:] = 0
+    luts = LutSet.from_tables(hd, base.rsqrt, base.silu, exp, base.cos, base.sin)
+    gm, om = IntegerModel(backend, spec, luts), OracleModel(spec, luts, threads=16)
+    r = np.random.default_rng(hd + kvh + len(variant))
+    n_loop = max_pos - 40
+    for pos, t in enumerate(r.integers(0, spec["vocab"], n_loop)):
+        assert np.array_equal(gm.forward_token(int(t), pos), om.forward_token(int(t), pos)), pos
+    t = int(r.integers(0, spec["vocab"]))
+    toks, logits = gm.decode_greedy(t, n_loop, 40, want_logits=True)
+    for i in range(40):
+        ref = om.forward_token(t, n_loop + i)
+        assert np.array_equal(logits[i], ref), n_loop + i
+        t = int(np.argmax(ref))
+        assert int(toks[i]) == t, n_loop + i
+    compare_kv(gm, om, spec, max_pos)
+
+
 def test_decode_rsqrt_table_unlike_its_closed_form(backend):
     """An rsqrt table that differs from round(2^8 / sqrt(x / 2^8)) at every
     odd index: the norm factor must come from the table (the closed form is
