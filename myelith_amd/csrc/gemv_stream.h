@@ -666,11 +666,15 @@ hipError_t stream_rows_i8(int shape, const int16_t* x, const int8_t* W, int N, i
     const typename StreamEpiOf<Epi>::type e{epi};
     // one block per CU for 32-100 MB of weights (measured faster for the
     // 68 MB shapes), as many as fit otherwise (12.8 MB: 5.5 against 6.0 us;
-    // the 545 MB LM-head shape)
+    // the 545 MB LM-head shape).  Many rows at 32-100 MB: one row per wave
+    // group (18944 x 3584 on MI355X: 12.9 us against 14.3-14.7 us with two;
+    // the 545 MB shape is the same either way)
     const uint64_t wb = (uint64_t)N * (uint64_t)K;
     const int occ = wb >= (32ull << 20) && wb <= (100ull << 20) ? 1 : 0;
     switch (shape) {
-        case 1: return stream_i8<2, 4, 8>(src, W, N, K, e, st, cus, occ);
+        case 1:
+            return occ ? stream_i8<1, 4, 8>(src, W, N, K, e, st, cus, occ)
+                       : stream_i8<2, 4, 8>(src, W, N, K, e, st, cus, occ);
         case 2: return stream_i8<1, 4, 8>(src, W, N, K, e, st, cus, occ);
         case 3: return stream_i8<1, 2, 16>(src, W, N, K, e, st, cus, occ);
         default: return hipErrorInvalidValue;
