@@ -24,7 +24,7 @@ Also reported:
                matrix cores and reports TOP/s; launches replayed from a
                captured graph;
   read_ceiling the achievable read rate at the decode kernels' sizes (one
-               pass of plain 16-byte loads over rotating buffers): what a
+               pass of 16-byte nontemporal loads over rotating buffers): what a
                kernel that only streams its bytes reaches, beside the 8 TB/s
                peak;
   e2e_0.5b     the Qwen2.5-0.5B-shape model end to end at batch 1: 256-token

@@ -236,9 +236,10 @@ int myl_model_set_graphs(myl_model* m, int enable);
  * first as usual, each repeat with the same launch shape over the weights of
  * layer l + 1, l + 2, ... (wrapping to the first layers: weights the step read
  * at least a layer's traffic earlier, which no longer sit in the caches) into
- * scratch output rows, so every output of the step is unchanged.  Only the gate/up class (kclass 5 of the timing order below)
- * is accepted; myl_model_timing does not count the repeats.  The next greedy
- * decode recaptures its step graph. */
+ * scratch output rows, so every output of the step is unchanged.  Only the
+ * gate/up class (kclass 5 of the timing order below) is accepted;
+ * myl_model_timing does not count the repeats.  The next greedy decode
+ * recaptures its step graph. */
 int myl_model_set_kernel_repeat(myl_model* m, int kclass, int times);
 /* Per-kernel-class timing with HIP events around each launch (eager launches,
  * no graphs while enabled).  enable = 1 starts; enable = 0 stops and returns

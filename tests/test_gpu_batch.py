@@ -219,6 +219,57 @@ def test_batch_decode_rows_grouped_heads(backend, hd, heads, bias):
         compare_batch_kv(gm, om, spec, s, list(toks[s][:n + 1]) + [first[s]] + exp[:-1])
 
 
+@pytest.mark.parametrize("variant", ["zero", "long_tail"])
+def test_batch_decode_rows_exp_table_variants(backend, variant):
+    """Decode batches with an all-zero exp table (every head sum is 0: the
+    uniform split, softmax.rs:42-48, inside the P.V kernel) and with one whose
+    nonzero entries run past the 4096 the P.V kernel copies into LDS (the
+    probabilities then come from their own kernel): logits and greedy tokens
+    equal each sequence's own forward_token run."""
+    from myelith_amd.luts import LutSet
+    from myelith_amd.model import IntegerModel
+    from oracle.binding import OracleModel
+    spec = dict(seed=6, vocab=1000, hidden=7 * 64, layers=2, heads=7, kv_heads=1, head_dim=64, inter=320,
+                max_pos=640, lm_head_int16=0, attention_bias=1)
+    case(f"batch decode rows, exp table {variant} {spec}")
+    base = LutSet.for_head_dim(64)
+    exp = np.asarray(base.exp, dtype=np.int16).copy()
+    if variant == "zero":
+        exp[:] = 0
+    else:
+        exp[2600:6000] = np.maximum(exp[2600:6000], 1)
+    luts = LutSet.from_tables(64, base.rsqrt, base.silu, exp, base.cos, base.sin)
+    gm, om = IntegerModel(backend, spec, luts), OracleModel(spec, luts, threads=16)
+    r = np.random.default_rng(len(variant))
+    lens = [1, 64, 257, 300]
+    toks = [r.integers(0, spec["vocab"], n + 1) for n in lens]
+    S = len(lens)
+    gm.batch_begin(S)
+    rows = [(s, p) for s, n in enumerate(lens) for p in range(n)]
+    gm.forward_batch([s for s, _ in rows], [p for _, p in rows], [int(toks[s][p]) for s, p in rows],
+                     want_logits=False)
+    logits, am = gm.forward_batch(list(range(S)), lens, [int(toks[s][n]) for s, n in enumerate(lens)])
+    first = []
+    for s, n in enumerate(lens):
+        om.reset()
+        for p in range(n + 1):
+            ref = om.forward_token(int(toks[s][p]), p)
+        assert np.array_equal(logits[s], ref), ("decode row", s, n)
+        first.append(int(np.argmax(ref)))
+    steps = 3
+    out = gm.batch_decode_greedy(range(S), [n + 1 for n in lens], first, steps)
+    for s, n in enumerate(lens):
+        om.reset()
+        for p in range(n + 1):
+            logits_o = om.forward_token(int(toks[s][p]), p)
+        nxt, exp_t = int(np.argmax(logits_o)), []
+        for i in range(steps):
+            logits_o = om.forward_token(nxt, n + 1 + i)
+            nxt = int(np.argmax(logits_o))
+            exp_t.append(nxt)
+        assert [int(t) for t in out[:, s]] == exp_t, s
+
+
 def test_logsoftmax_dev(backend, oracle):
     import torch
     from myelith_amd.luts import exp_lut
