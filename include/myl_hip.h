@@ -133,6 +133,14 @@ int myl_mlp(myl_ctx* ctx, const int16_t* x, const int8_t* W_gate, const int8_t* 
 /* sampling.rs:8-18 (first maximum wins); *out_index receives the token id. */
 int myl_argmax_int(myl_ctx* ctx, const int32_t* values, size_t n, int64_t* out_index);
 
+/* sample_integer_cdf (sampling.rs:27-46, called by IntegerModel::sample_next,
+ * model.rs:785-787): weights z - min z + 1 (i32, wrapping), SplitMix64
+ * (prng.rs:7-14) draw r, threshold r % total, the first token whose running
+ * weight sum exceeds it; total <= 0 (or no logits) gives token 0 and the
+ * state unchanged.  *token and *new_state receive the result. */
+int myl_sample_integer_cdf(myl_ctx* ctx, const int32_t* logits, size_t n, uint64_t state, int64_t* token,
+                           uint64_t* new_state);
+
 /* ======================================================================
  * 2. Device-pointer forms (asynchronous on myl_stream(ctx))
  * ==================================================================== */
@@ -189,6 +197,11 @@ int myl_softmax_dev(myl_ctx* ctx, const int32_t* logits, size_t M, size_t n, siz
 
 /* M rows of argmax_int (sampling.rs:8-18). */
 int myl_argmax_dev(myl_ctx* ctx, const int32_t* values, size_t M, size_t n, size_t ldv, int64_t* out_index);
+
+/* M rows of sample_integer_cdf (sampling.rs:27-46): row m at states[m] gives
+ * tokens[m] and new_states[m] (all device pointers). */
+int myl_sample_dev(myl_ctx* ctx, const int32_t* logits, size_t M, size_t n, size_t ldz, const uint64_t* states,
+                   int64_t* tokens, uint64_t* new_states);
 
 /* Integer log-softmax at a target token per row (no reference counterpart:
  * the reference evaluates perplexity in f64, runtime/src/bin/perplexity_probe.rs:55-67).

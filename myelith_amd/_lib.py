@@ -77,6 +77,7 @@ SIGNATURES: dict[str, tuple] = {
     "myl_rope": (INT, [P, P, P, sz, sz, P, P, sz, P, u8]),
     "myl_mlp": (INT, [P, P, P, P, P, P, sz, sz, P, P, P, P, sz, u8, u8, u8, u8, u8, i16, u8, P]),
     "myl_argmax_int": (INT, [P, P, sz, C.POINTER(i64)]),
+    "myl_sample_integer_cdf": (INT, [P, P, sz, u64, C.POINTER(i64), C.POINTER(u64)]),
     "myl_linear_w8a16_dev": (INT, [P, P, sz, sz, P, sz, sz, P, u8, u8, P, P, sz]),
     "myl_linear_w8a16_dev_noalloc": (INT, [P, P, sz, sz, P, sz, sz, P, u8, u8, P, P, sz]),
     "myl_noalloc_scratch_bytes": (sz, []),
@@ -86,6 +87,7 @@ SIGNATURES: dict[str, tuple] = {
     "myl_rmsnorm_dev": (INT, [P, P, sz, sz, P, P, P, sz, P, sz, u8, u8, i64, u8, P, sz]),
     "myl_softmax_dev": (INT, [P, P, sz, sz, sz, P, sz, u8, u8, P, sz]),
     "myl_argmax_dev": (INT, [P, P, sz, sz, sz, P]),
+    "myl_sample_dev": (INT, [P, P, sz, sz, sz, P, P, P]),
     "myl_logsoftmax_dev": (INT, [P, P, sz, sz, sz, P, sz, P, P]),
     "myl_model_create_synthetic": (INT, [P, C.POINTER(SynthSpec), C.POINTER(Luts), C.POINTER(P)]),
     "myl_model_destroy": (None, [P]),

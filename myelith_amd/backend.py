@@ -212,6 +212,14 @@ class RocmBackend:
         self.check(lib().myl_argmax_int(self._h, _p(v), v.size, C.byref(out)), "argmax_int")
         return out.value
 
+    def sample_integer_cdf(self, logits, state: int):
+        """sampling.rs:27-46 on the GPU: (token, new_state)."""
+        v = _a(logits, np.int32)
+        tok, ns = C.c_int64(), C.c_uint64()
+        self.check(lib().myl_sample_integer_cdf(self._h, _p(v), v.size, int(state) & (2**64 - 1), C.byref(tok),
+                                                C.byref(ns)), "sample_integer_cdf")
+        return int(tok.value), int(ns.value)
+
     # ---- device forms (torch tensors on the GPU) ------------------------------
     def linear_w8a16_dev(self, x, W, w_shifts, act_frac: int, out_frac: int = 0, out_frac_pc=None, out=None):
         import torch
@@ -298,6 +306,19 @@ class RocmBackend:
             out = torch.empty(M, dtype=torch.int64, device=v.device)
         self.check(lib().myl_argmax_dev(self._h, v.data_ptr(), M, n, v.stride(0), out.data_ptr()), "argmax_dev")
         return out
+
+    def sample_dev(self, z, states, tokens=None, new_states=None):
+        """Rows of sample_integer_cdf (sampling.rs:27-46): z int32 [M x n],
+        states uint64 [M] (torch int64 tensors hold the bits)."""
+        import torch
+        M, n = z.shape
+        if tokens is None:
+            tokens = torch.empty(M, dtype=torch.int64, device=z.device)
+        if new_states is None:
+            new_states = torch.empty(M, dtype=torch.int64, device=z.device)
+        self.check(lib().myl_sample_dev(self._h, z.data_ptr(), M, n, z.stride(0), states.data_ptr(), tokens.data_ptr(),
+                                        new_states.data_ptr()), "sample_dev")
+        return tokens, new_states
 
     def logsoftmax_dev(self, z, exp_lut, targets, out=None):
         """Integer log-softmax at targets[m] per row, Q16 int64 (build-defined;

@@ -416,6 +416,25 @@ int myl_argmax_int(myl_ctx* ctx, const int32_t* values, size_t n, int64_t* out_i
     return rc ? rc : s.download();
 }
 
+int myl_sample_integer_cdf(myl_ctx* ctx, const int32_t* logits, size_t n, uint64_t state, int64_t* token,
+                           uint64_t* new_state) {
+    if (!ctx || !token || !new_state) return MYL_E_INVALID;
+    if (n == 0) {  // logits_to_weights of nothing: total 0 (sampling.rs:31-33)
+        *token = 0;
+        *new_state = state;
+        return MYL_OK;
+    }
+    if (!fits_int(n)) return ctx->fail(MYL_E_INVALID, "sample_integer_cdf: too long");
+    Stage s{ctx};
+    size_t ov = s.in(logits, n * 4), os = s.in(&state, 8), ot = s.out(token, 8), on = s.out(new_state, 8);
+    int rc = s.upload();
+    if (rc) return rc;
+    rc = ctx->hip(sample_cdf(s.at<int32_t>(ov), 1, (int)n, (int)n, s.at<uint64_t>(os), s.at<int64_t>(ot),
+                             s.at<uint64_t>(on), ctx->stream),
+                  "sample_integer_cdf");
+    return rc ? rc : s.download();
+}
+
 // ---------------------------------------------------------------------------
 // 2. Device-pointer forms
 // ---------------------------------------------------------------------------
@@ -507,6 +526,15 @@ int myl_argmax_dev(myl_ctx* ctx, const int32_t* values, size_t M, size_t n, size
     if (ldv < n || !fits_int(M) || !fits_int(ldv)) return ctx->fail(MYL_E_INVALID, "argmax_dev: bad shape");
     if (M == 0) return MYL_OK;
     return ctx->hip(argmax(values, (int)M, (int)n, (int)ldv, out_index, ctx->stream), "argmax_dev");
+}
+
+int myl_sample_dev(myl_ctx* ctx, const int32_t* logits, size_t M, size_t n, size_t ldz, const uint64_t* states,
+                   int64_t* tokens, uint64_t* new_states) {
+    if (!ctx) return MYL_E_INVALID;
+    if (n == 0) return ctx->fail(MYL_E_INVALID, "sample_dev: empty rows");
+    if (ldz < n || !fits_int(M) || !fits_int(n) || !fits_int(ldz)) return ctx->fail(MYL_E_INVALID, "sample_dev: bad shape");
+    if (M == 0) return MYL_OK;
+    return ctx->hip(sample_cdf(logits, (int)M, (int)n, (int)ldz, states, tokens, new_states, ctx->stream), "sample_dev");
 }
 
 int myl_logsoftmax_dev(myl_ctx* ctx, const int32_t* logits, size_t M, size_t n, size_t ldz, const int16_t* exp_lut,

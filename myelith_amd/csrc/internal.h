@@ -57,6 +57,8 @@ hipError_t silu_gate(const int16_t* gate, const int16_t* up, int n, const int16_
                      uint8_t gate_frac, uint8_t up_frac, uint8_t down_in_frac, uint8_t silu_in_frac, int16_t silu_off,
                      uint8_t silu_out_frac, int16_t* h, hipStream_t st);
 hipError_t argmax(const int32_t* v, int M, int n, int ldv, int64_t* out, hipStream_t st);
+hipError_t sample_cdf(const int32_t* z, int M, int n, int ldz, const uint64_t* states, int64_t* tokens,
+                      uint64_t* new_states, hipStream_t st);
 // RMSNorm rows written as byte planes [2M x n] (hi row 2m, lo' row 2m + 1) for
 // the int8 products; rows of up to rmsnorm_planes_ok(n) elements.
 bool rmsnorm_planes_ok(int n);

@@ -521,6 +521,134 @@ hipError_t argmax(const int32_t* v, int M, int n, int ldv, int64_t* out, hipStre
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Integer CDF sampling (sampling.rs:20-46): one block per row.
+// ---------------------------------------------------------------------------
+
+// SplitMix64 (prng.rs:7-14): advances the state, returns the output.
+__device__ inline uint64_t splitmix64_next(uint64_t& state) {
+    state += 0x9E3779B97F4A7C15ull;
+    uint64_t z = state;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// n % d by binary long division (no hardware divide); d < 2^63.
+__device__ inline uint64_t umod64(uint64_t n, uint64_t d) {
+    uint64_t r = 0;
+    for (int i = 63; i >= 0; --i) {
+        r = (r << 1) | ((n >> i) & 1u);
+        if (r >= d) r -= d;
+    }
+    return r;
+}
+
+__device__ inline int64_t shfl_up_i64(int64_t v, int d) {
+    const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)v, d, 64);
+    const uint32_t hi = (uint32_t)__shfl_up((int)(uint32_t)((uint64_t)v >> 32), d, 64);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Exclusive prefix sum of one i64 per thread over the block (wrapping),
+// and the block's total.  wt needs one slot per wave.
+__device__ inline int64_t block_scan_i64(int64_t v, int64_t* wt, int64_t& total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    int64_t inc = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int64_t o = shfl_up_i64(inc, d);
+        if (lane >= d) inc = (int64_t)((uint64_t)inc + (uint64_t)o);
+    }
+    if (lane == 63) wt[w] = inc;
+    __syncthreads();
+    int64_t before = 0, all = 0;
+    for (int k = 0; k < nw; ++k) {
+        const int64_t t = wt[k];
+        if (k < w) before = (int64_t)((uint64_t)before + (uint64_t)t);
+        all = (int64_t)((uint64_t)all + (uint64_t)t);
+    }
+    total = all;
+    return (int64_t)((uint64_t)before + (uint64_t)inc - (uint64_t)v);
+}
+
+// sample_integer_cdf (sampling.rs:27-46) of row blockIdx.x at state
+// states[row]: weights w_i = z_i - min z + 1 (logits_to_weights,
+// sampling.rs:20-24; i32 arithmetic, wrapping as the reference's release
+// build does), total = sum w_i as i64; total <= 0 gives token 0 and the state
+// unchanged; otherwise (state', r) = splitmix64(state), threshold = r % total
+// and the token is the first i with threshold < w_0 + ... + w_i (the last
+// index when there is none).  The running sums are scanned over tiles of
+// 4 x kSampleThreads positions in order, so the first such i is exact also
+// when wrapped weights make the sums non-monotone.
+constexpr int kSampleThreads = 1024;
+__global__ __launch_bounds__(kSampleThreads) void sample_cdf_kernel(const int32_t* __restrict__ z, int n, int ldz,
+                                                                   const uint64_t* __restrict__ states,
+                                                                   int64_t* __restrict__ tokens,
+                                                                   uint64_t* __restrict__ new_states) {
+    __shared__ int32_t redm[kSampleThreads / 64];
+    __shared__ int32_t redc[kSampleThreads / 64];
+    __shared__ int64_t wt[kSampleThreads / 64];
+    __shared__ int64_t s_thr;
+    const int32_t* row = z + (size_t)blockIdx.x * ldz;
+    const int tid = threadIdx.x;
+    // the minimum as ~max(~z) (bitwise not reverses the signed order)
+    int32_t nm = INT32_MIN;
+    for (int i = tid; i < n; i += kSampleThreads) nm = max(nm, ~row[i]);
+    const int32_t m = ~block_max_i32_dpp(nm, redm);
+    auto weight = [&](int32_t zi) -> int64_t { return (int64_t)(int32_t)((uint32_t)zi - (uint32_t)m + 1u); };
+    int64_t part = 0;
+    for (int i = tid; i < n; i += kSampleThreads) part += weight(row[i]);
+    int64_t total = 0;
+    (void)block_scan_i64(part, wt, total);
+    uint64_t state = states[blockIdx.x];
+    if (total <= 0) {  // uniform: an empty or non-positive total keeps the state
+        if (tid == 0) {
+            tokens[blockIdx.x] = 0;
+            new_states[blockIdx.x] = state;
+        }
+        return;
+    }
+    if (tid == 0) {
+        const uint64_t r = splitmix64_next(state);
+        s_thr = (int64_t)umod64(r, (uint64_t)total);  // total < 2^62: n < 2^31 weights below 2^31
+        new_states[blockIdx.x] = state;
+    }
+    __syncthreads();
+    const int64_t thr = s_thr;
+    int64_t base = 0;
+    int pick = n - 1;
+    for (int t0 = 0; t0 < n; t0 += 4 * kSampleThreads) {
+        const int i0 = t0 + 4 * tid;
+        int64_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = i0 + e < n ? weight(row[i0 + e]) : 0;
+        const int64_t loc = w[0] + w[1] + w[2] + w[3];
+        int64_t tile = 0;
+        int64_t acc = base + block_scan_i64(loc, wt, tile);
+        int cand = INT32_MAX;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            acc += w[e];
+            if (i0 + e < n && thr < acc && cand == INT32_MAX) cand = i0 + e;
+        }
+        // the first candidate of the tile: a block minimum as ~max(~x)
+        const int first = ~block_max_i32_dpp(~cand, redc);
+        if (first != INT32_MAX) {  // uniform
+            pick = first;
+            break;
+        }
+        base += tile;
+    }
+    if (tid == 0) tokens[blockIdx.x] = pick;
+}
+
+hipError_t sample_cdf(const int32_t* z, int M, int n, int ldz, const uint64_t* states, int64_t* tokens,
+                      uint64_t* new_states, hipStream_t st) {
+    sample_cdf_kernel<<<M, kSampleThreads, 0, st>>>(z, n, ldz, states, tokens, new_states);
+    return hipGetLastError();
+}
+
 // Best key of chunk blockIdx.x of row blockIdx.y.
 __global__ __launch_bounds__(kBlock) void argmax_part_kernel(const int32_t* __restrict__ v, int n, int ldv,
                                                             uint64_t* __restrict__ part, int nch) {

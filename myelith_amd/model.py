@@ -294,6 +294,10 @@ class IntegerModel:
         """argmax_int (sampling.rs:8-18): the first maximum wins."""
         return int(np.argmax(np.asarray(logits)))
 
+    def sample_next(self, logits, state: int):
+        """sample_integer_cdf (sampling.rs:27-46) on the GPU: (token, new_state)."""
+        return self.backend.sample_integer_cdf(logits, state)
+
 
 def _device_view_i32(ptr: int, rows: int, cols: int):
     """A torch int32 tensor over device memory owned by the library."""
@@ -305,11 +309,15 @@ def _device_view_i32(ptr: int, rows: int, cols: int):
     return torch.as_tensor(_Arr(), device="cuda")
 
 
-def dekodieren_mit_digest(model, token_ids, max_new_tokens: int):
-    """generate.rs:98-137 (greedy): prefill the prompt, then for each decode step
-    hash all logits as i32 LE followed by the chosen token as u32 LE.
+def dekodieren_mit_digest(model, token_ids, max_new_tokens: int, seed: int = 0, greedy: bool = True):
+    """generate.rs:98-137: prefill the prompt, then for each decode step hash
+    all logits as i32 LE followed by the chosen token as u32 LE.  The token is
+    the first maximum (greedy_next, model.rs:780-782) or, with greedy False,
+    model.sample_next(logits, state) (model.rs:785-787), the state starting at
+    seed and carried from step to step.
 
-    Works with any object exposing forward_token(token, pos) and reset()."""
+    Works with any object exposing forward_token(token, pos), reset() and,
+    for sampling, sample_next(logits, state)."""
     model.reset()
     pos = 0
     logits = None
@@ -318,9 +326,13 @@ def dekodieren_mit_digest(model, token_ids, max_new_tokens: int):
         pos += 1
     h = hashlib.sha256()
     out = []
+    state = int(seed) & (2**64 - 1)
     for _ in range(max_new_tokens):
         h.update(np.ascontiguousarray(logits, dtype="<i4").tobytes())
-        nxt = int(np.argmax(logits))
+        if greedy:
+            nxt = int(np.argmax(logits))
+        else:
+            nxt, state = model.sample_next(logits, state)
         h.update(np.uint32(nxt).astype("<u4").tobytes())
         out.append(nxt)
         logits = model.forward_token(nxt, pos)

@@ -89,6 +89,7 @@ def _declare(L) -> None:
         "or_mlp_int": (C.c_int, [P, P, P, P, sz, sz, P, P, P, P, sz, u8, u8, u8, u8, u8, i16, u8, P, P]),
         "or_argmax_int": (i64, [P, sz]),
         "or_splitmix64": (None, [u64, C.POINTER(u64), C.POINTER(u64)]),
+        "or_sample_integer_cdf": (None, [P, sz, u64, C.POINTER(i64), C.POINTER(u64)]),
         "or_log2_q16": (None, [u64, C.POINTER(i32), C.POINTER(u32)]),
         "or_ln_q16": (i64, [u64]),
         "or_logsoftmax_at": (i64, [P, sz, P, sz, i64]),
@@ -290,6 +291,14 @@ def argmax_int(v) -> int:
     return lib().or_argmax_int(ptr(a), len(a))
 
 
+def sample_integer_cdf(v, state: int) -> tuple[int, int]:
+    """sampling.rs:27-46: (token, new_state)."""
+    a = _arr(v, np.int32)
+    tok, ns = i64(), u64()
+    lib().or_sample_integer_cdf(ptr(a), len(a), int(state) & (2**64 - 1), C.byref(tok), C.byref(ns))
+    return int(tok.value), int(ns.value)
+
+
 # ---- integer log-softmax (build-defined) ---------------------------------------
 def log2_q16(S: int) -> tuple[int, int]:
     e, f = i32(), u32()
@@ -345,6 +354,11 @@ class OracleModel:
         logits = np.zeros(self.spec["vocab"], np.int32) if want_logits else None
         _check(lib().or_model_forward_token(self._h, token, pos, ptr(logits)), "forward_token")
         return logits
+
+    @staticmethod
+    def sample_next(logits, state: int):
+        """IntegerModel::sample_next (model.rs:785-787)."""
+        return sample_integer_cdf(logits, state)
 
     def embed_token(self, token: int) -> np.ndarray:
         h = np.zeros(self.spec["hidden"], np.int16)

@@ -488,6 +488,38 @@ void or_splitmix64(uint64_t state, uint64_t* new_state, uint64_t* out) {
     *out = myl_mix64(s);
 }
 
+/* sampling.rs:20-46: logits_to_weights (w_i = z_i - min + 1, i32 arithmetic
+ * that wraps as in the reference's release build; no logits: min 0), the
+ * total as i64, (token 0, state) when total <= 0, else one SplitMix64 draw r,
+ * threshold r % total and the first i whose running sum exceeds it (the last
+ * index when none does). */
+void or_sample_integer_cdf(const int32_t* z, size_t n, uint64_t state, int64_t* token, uint64_t* new_state) {
+    int32_t m = 0;
+    if (n > 0) {
+        m = z[0];
+        for (size_t i = 1; i < n; ++i) if (z[i] < m) m = z[i];
+    }
+    int64_t total = 0;
+    for (size_t i = 0; i < n; ++i) total += (int64_t)(int32_t)((uint32_t)z[i] - (uint32_t)m + 1u);
+    if (total <= 0) {
+        *token = 0;
+        *new_state = state;
+        return;
+    }
+    uint64_t r;
+    or_splitmix64(state, new_state, &r);
+    const int64_t threshold = (int64_t)(r % (uint64_t)total);
+    int64_t acc = 0;
+    for (size_t i = 0; i < n; ++i) {
+        acc += (int64_t)(int32_t)((uint32_t)z[i] - (uint32_t)m + 1u);
+        if (threshold < acc) {
+            *token = (int64_t)i;
+            return;
+        }
+    }
+    *token = (int64_t)n - 1;
+}
+
 /* ---- integer log-softmax (build-defined) --------------------------------
  * The binary logarithm by repeated squaring: with x = S / 2^e in [1, 2),
  * log2(x^2) = 2 log2(x), so each squaring shifts the next fraction bit of

@@ -103,6 +103,8 @@ int or_mlp_int(const int16_t* x, const int8_t* W_gate, const int8_t* W_up, const
                const uint8_t* out_frac, int16_t* out);                   /* mlp.rs:28-74 */
 int64_t or_argmax_int(const int32_t* v, size_t n);                       /* sampling.rs:8-18 */
 void or_splitmix64(uint64_t state, uint64_t* new_state, uint64_t* out);  /* prng.rs:7-14 */
+void or_sample_integer_cdf(const int32_t* z, size_t n, uint64_t state, int64_t* token,
+                           uint64_t* new_state);                        /* sampling.rs:20-46 */
 
 /* ---- integer log-softmax (build-defined; no reference counterpart: the
  * reference's perplexity probe works in f64, perplexity_probe.rs:55-67) --- */

@@ -140,6 +140,24 @@ def test_decode_greedy_digest(backend):
         assert np.array_equal(dev_logits[i], om.forward_token(int(t), len(prompt) + i))
 
 
+def test_sampled_digest(backend):
+    """dekodieren_mit_digest with greedy false (generate.rs:98-137): each
+    token drawn by sample_integer_cdf (sampling.rs:27-46) from the step's
+    logits with the SplitMix64 state carried across steps; tokens and digest
+    equal the oracle's for two seeds."""
+    from myelith_amd.model import dekodieren_mit_digest
+    spec = tiny(64, 0, 1, 2)
+    case("sampled decode + digest")
+    gm, om = build(backend, spec)
+    prompt = [5, 77, 901, 3]
+    for seed in (0, 0xDEADBEEF12345678):
+        toks_g, dig_g = dekodieren_mit_digest(gm, prompt, 24, seed=seed, greedy=False)
+        toks_o, dig_o = dekodieren_mit_digest(om, prompt, 24, seed=seed, greedy=False)
+        assert toks_g == toks_o and dig_g == dig_o, seed
+    assert dekodieren_mit_digest(gm, prompt, 24, seed=1, greedy=False)[0] != \
+        dekodieren_mit_digest(gm, prompt, 24, greedy=True)[0]
+
+
 def test_qwen05b_config1_prompt256_decode128(backend):
     """Qwen2.5-0.5B architecture: 256-token seeded prompt + 128 greedy steps:
     identical digest, tokens and KV cache."""

@@ -413,6 +413,47 @@ def test_argmax(backend, oracle):
         backend.argmax_int([])
 
 
+def test_sample_integer_cdf(backend, oracle):
+    """sample_integer_cdf (sampling.rs:27-46) on the GPU against the oracle:
+    ragged lengths around the 4096-position scan tiles, both vocab sizes,
+    logits spanning the i32 range (wrapped weights, non-monotone running sums,
+    totals <= 0), constant rows, the first and last tokens, many states."""
+    case("sample_integer_cdf")
+    r = rng(9)
+    lo, hi = -2**31, 2**31 - 1
+    rows = []
+    for n in (1, 2, 3, 4095, 4096, 4097, 12293, 151936, 152064):
+        rows.append(r.integers(-100000, 100000, n).astype(np.int32))
+    rows.append(np.full(4099, 5, np.int32))
+    rows.append(r.integers(lo, hi, 5000, endpoint=True).astype(np.int32))        # wrapped weights
+    rows.append(np.array([lo, -2, -2, -1, -2], np.int32))                         # non-monotone sums
+    rows.append(np.array([lo, hi - 1], np.int32))                                 # total 0
+    rows.append(np.array([lo, hi], np.int32))                                     # a zero weight
+    z = np.full(9000, -10, np.int32)
+    z[-1] = 2**30                                                                  # nearly all weight last
+    rows.append(z)
+    for v in rows:
+        for state in (0, 1, 42, 2**64 - 1, int(r.integers(0, 2**63)) * 2 + 1):
+            assert backend.sample_integer_cdf(v, state) == oracle.sample_integer_cdf(v, state), (len(v), state)
+    assert backend.sample_integer_cdf(np.zeros(0, np.int32), 3) == (0, 3)
+
+
+def test_sample_dev_rows(backend, oracle):
+    """Rows of the device sampler (myl_sample_dev) with their own states."""
+    import torch
+    case("sample_dev")
+    r = rng(10)
+    M, n = 37, 152064
+    z = r.integers(-300000, 300000, (M, n)).astype(np.int32)
+    states = np.array([int(x) for x in r.integers(0, 2**62, M)], dtype=np.uint64)
+    zt = torch.from_numpy(z).cuda()
+    st = torch.from_numpy(states.view(np.int64)).cuda()
+    tok, ns = backend.sample_dev(zt, st)
+    tok, ns = tok.cpu().numpy(), ns.cpu().numpy().view(np.uint64)
+    for m in range(M):
+        assert (int(tok[m]), int(ns[m])) == oracle.sample_integer_cdf(z[m], int(states[m])), m
+
+
 def test_device_forms_batch_rows(backend, oracle, luts64):
     import torch
     case("rmsnorm/softmax/argmax dev batch")

@@ -404,6 +404,43 @@ def test_splitmix64(oracle):
     assert z == 0xE220A8397B1DCDAF  # first output of SplitMix64 seeded with 0 (published test value)
 
 
+def test_sample_integer_cdf_closed_forms(oracle):
+    """sample_integer_cdf (sampling.rs:27-46) against what its definition
+    fixes, with SplitMix64 pinned above: constant logits (all weights 1: the
+    token is r % n), the reference's own example [10, 20, 30] (weights 1, 11,
+    21), a total of zero from a wrapped weight (token 0, state unchanged),
+    an empty row, and determinism (sampling.rs:58-66)."""
+    for n, state in ((1, 0), (7, 42), (152064, 2**64 - 1), (1000, 123456789)):
+        ns, r = oracle.splitmix64(state)
+        assert oracle.sample_integer_cdf([77] * n, state) == (r % n, ns)
+    ns, r = oracle.splitmix64(42)
+    t = r % 33
+    assert oracle.sample_integer_cdf([10, 20, 30], 42) == (0 if t < 1 else 1 if t < 12 else 2, ns)
+    assert oracle.sample_integer_cdf([10, 20, 30], 42) == oracle.sample_integer_cdf([10, 20, 30], 42)
+    # z - min + 1 = 2^32 - 1 wraps to -1 in i32: total 1 - 1 = 0
+    assert oracle.sample_integer_cdf([-2**31, 2**31 - 2], 99) == (0, 99)
+    # a weight of 2^32 wraps to 0: total 1, threshold 0, token 0, state advanced
+    ns, _ = oracle.splitmix64(5)
+    assert oracle.sample_integer_cdf([-2**31, 2**31 - 1], 5) == (0, ns)
+    assert oracle.sample_integer_cdf([], 7) == (0, 7)
+
+
+def test_sample_integer_cdf_against_a_binary_search(oracle):
+    """For positive weights the token is where the threshold falls in the
+    cumulative weights: numpy's binary search (side right) over cumsum(w),
+    on random logits and states."""
+    rng = np.random.default_rng(8)
+    for trial in range(40):
+        n = int(rng.integers(1, 3000))
+        z = rng.integers(-50000, 50000, n).astype(np.int32)
+        state = int(rng.integers(0, 2**63)) * 2 + int(rng.integers(0, 2))
+        w = z.astype(np.int64) - int(z.min()) + 1
+        ns, r = oracle.splitmix64(state)
+        thr = r % int(w.sum())
+        want = int(np.searchsorted(np.cumsum(w), thr, side="right"))
+        assert oracle.sample_integer_cdf(z, state) == (want, ns), trial
+
+
 # ---- conformance vectors and LUT hashes --------------------------------------------------------
 
 def _hash_tensor(data, dtype):
