@@ -10,8 +10,9 @@ payload, golden_runner.rs:48-87), then the forward op named by the vector runs
 through the Backend-trait entry points of libmyl_hip.so and must reproduce
 the outputs bit for bit.  `model` follows runtime/src/bin/golden_model.rs:
 layer vectors run one layer on a fresh KV cache (:183-215), e2e vectors run
-greedy generation and compare the tokens and the logits digest of
-generate.rs:98-137 (:217-268); --batch walks layer/ then e2e/ in file order
+generation (greedy, or sampled with the vector's seed) and compare the tokens
+and the logits digest of generate.rs:98-137 (:210-268); --batch walks layer/
+then e2e/ in file order
 (:120-160).  `generate` writes layer and e2e vectors of a model the way
 runtime/src/bin/golden_generate.rs does (seeded layer inputs, :40-95), with
 prompt token ids given directly (tokenisation is not part of this backend).
@@ -136,13 +137,14 @@ def validate_layer(model, gv: dict) -> Result:
 
 
 def validate_e2e(model, gv: dict) -> Result:
-    """golden_model.rs:217-268: greedy tokens and the logits digest."""
+    """golden_model.rs:210-268: the generated tokens and the logits digest,
+    greedy or sampled with the vector's seed (defaults true and 42 as there)."""
     from .model import dekodieren_mit_digest
     md = gv["metadata"]
-    if not md.get("greedy", True):
-        return Result(gv["name"], None, "sampled generation is not part of this backend (greedy only)")
+    greedy = bool(md.get("greedy", True))
+    seed = int(md.get("seed", 42))
     prompt = [int(t) for t in gv["inputs"]["prompt_tokens"]["data"]]
-    toks, digest = dekodieren_mit_digest(model, prompt, int(md["max_new_tokens"]))
+    toks, digest = dekodieren_mit_digest(model, prompt, int(md["max_new_tokens"]), seed=seed, greedy=greedy)
     want = [int(t) for t in gv["outputs"]["tokens"]["data"]]
     if toks != want:
         return Result(gv["name"], False, f"token mismatch: generated {toks}, expected {want}")

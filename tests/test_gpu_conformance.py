@@ -43,11 +43,15 @@ def oracle_vectors(om, spec, out: Path, prompts: dict, max_new_tokens=3):
               "outputs": {"hidden_out": tensor_json(y, "int16")}}
         (out / "layer" / f"layer_{l:02d}.golden.json").write_text(json.dumps(gv))
     for name, ids in prompts.items():
-        toks, dig = dekodieren_mit_digest(om, ids, max_new_tokens)
-        gv = {"name": f"e2e_prompt_{name}", "level": "e2e", "theta_v_hash": th,
-              "metadata": {"max_new_tokens": max_new_tokens, "greedy": True, "seed": 42, "logits_sha256": dig},
-              "inputs": {"prompt_tokens": tensor_json(ids, "int32")}, "outputs": {"tokens": tensor_json(toks, "int32")}}
-        (out / "e2e" / f"e2e_{name}.golden.json").write_text(json.dumps(gv))
+        # greedy (as golden_generate.rs:128-150 writes them) and sampled with a seed
+        for suffix, greedy, seed in (("", True, 42), ("_sampled", False, 7)):
+            toks, dig = dekodieren_mit_digest(om, ids, max_new_tokens, seed=seed, greedy=greedy)
+            gv = {"name": f"e2e_prompt_{name}{suffix}", "level": "e2e", "theta_v_hash": th,
+                  "metadata": {"max_new_tokens": max_new_tokens, "greedy": greedy, "seed": seed,
+                               "logits_sha256": dig},
+                  "inputs": {"prompt_tokens": tensor_json(ids, "int32")},
+                  "outputs": {"tokens": tensor_json(toks, "int32")}}
+            (out / "e2e" / f"e2e_{name}{suffix}.golden.json").write_text(json.dumps(gv))
 
 
 def reference_prompts():
@@ -75,7 +79,7 @@ def test_oracle_vectors_replay_on_the_device(backend, tmp_path, shape):
     oracle_vectors(om, spec, tmp_path, prompts)
     gm = IntegerModel(backend, spec, luts)
     res = run_batch(gm, tmp_path)
-    assert len(res) == spec["layers"] + len(prompts)
+    assert len(res) == spec["layers"] + 2 * len(prompts)
     assert all(r.passed for r in res), [(r.name, r.detail) for r in res if not r.passed]
     # a vector whose payload was edited is refused before it is run
     p = tmp_path / "layer" / "layer_00.golden.json"
