@@ -23,6 +23,7 @@
 // then the final norm, the LM head over every row (model.rs:264-308) and a
 // first-maximum argmax per row (sampling.rs:8-18).
 #include "gemm_dispatch.h"
+#include "gemm_frag.h"
 #include "model_internal.h"
 #include "ops.h"
 #include "rows_attn.h"
@@ -31,6 +32,7 @@
 #include "wave.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -136,6 +138,40 @@ __device__ inline void rope_store_pair(int r, int n0, int16_t y0, int16_t y1, co
     dst[p] = y0;
     dst[p + half] = y1;
 }
+
+// The q/k/v product's epilogue on the fragment-major weights (gemm_frag.h):
+// requantise with the bias (EpiQKVRows), rotate q/k pairs and store q and
+// the KV append (rope_store_pair).  Threads take the block's 8 ngb pair
+// columns (FragCols); the pair's operands are fetched before the stream.
+struct FragOutQKV {
+    EpiQKVRows epi;
+    const int32_t* rows;
+    int rows_cap, nq, nkv, hd_log;
+    const int16_t *cos_lut, *sin_lut;
+    int16_t *Q, *kc, *vc;
+    size_t seq_stride;
+    int max_pos;
+    struct Pre { EpiQKVRows::ValOps o0, o1; };
+    __device__ inline Pre pre(int g0, int ngb, int, int N) const {
+        const int c2 = FragCols::of(8 * ngb).col();
+        const int n0 = min(16 * g0 + 2 * c2, N - 2);
+        return Pre{epi.val_ops(n0), epi.val_ops(n0 + 1)};
+    }
+    template <int RT>
+    __device__ inline void run(const Pre& pr, const FragSums<RT>& s, int g0, int ngb, int R, int N, int8_t*) const {
+        const int np = 8 * ngb;
+        const FragCols fc = FragCols::of(np);
+        const int c2 = fc.col(), gg = c2 >> 3, cc = 2 * (c2 & 7);
+        const int n0 = 16 * (g0 + gg) + cc;
+        if (c2 >= np || n0 >= N) return;
+        for (int m = fc.row0(); m < R; m += fc.slices) {
+            const int16_t y0 = epi.value_with(pr.o0, n0, s(gg, m, cc));
+            const int16_t y1 = epi.value_with(pr.o1, n0 + 1, s(gg, m, cc + 1));
+            rope_store_pair(m, n0, y0, y1, rows, rows_cap, nq, nkv, hd_log, cos_lut, sin_lut, Q, kc, vc, seq_stride,
+                            max_pos);
+        }
+    }
+};
 
 __global__ __launch_bounds__(256) void rope_scatter_kernel(const int16_t* __restrict__ qkv, int ldq, const int32_t* __restrict__ rows,
                                                            int rows_cap, int nq, int nkv, int hd_log,
@@ -397,7 +433,8 @@ __global__ __launch_bounds__(kFinNormThreads) void finish_resid_norm_kernel(unsi
 // the norm's input scales xs (rmsnorm.rs:96).
 hipError_t resid_then_norm(const int8_t* Ap, int R, const int8_t* W, int N, int K, const EpiResidRows& epi,
                            const MmCtx* mm, const uint8_t* xs, uint8_t ref, const int8_t* g, const uint8_t* gs,
-                           const myl_model* m, uint8_t out_frac, int8_t* planes, hipStream_t st) {
+                           const myl_model* m, uint8_t out_frac, int8_t* planes, hipStream_t st,
+                           const int8_t* Wf = nullptr) {
     const RmsParams p{m->rsqrt, m->rsqrt_len, MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20,
                       m->rsqrt_closed};
     auto fin = [&](unsigned long long* acc, hipStream_t s) -> hipError_t {
@@ -407,6 +444,11 @@ hipError_t resid_then_norm(const int8_t* Ap, int R, const int8_t* W, int N, int 
             finish_resid_norm_kernel<4><<<R, kFinNormThreads, 0, s>>>(acc, N, epi, xs, ref, g, gs, p, out_frac, planes);
         return hipGetLastError();
     };
+    // fragment-major weights: the K-sliced product into the accumulator, then the same finish
+    if (Wf && N <= 4096 && frag_split_ok(R, K, N, mm->cus, mm->acc_elems)) {
+        hipError_t e = frag_mm_split(Ap, R, K, Wf, N, mm->acc, mm->cus, mm->acc_elems, st);
+        return e != hipSuccess ? e : fin(mm->acc, st);
+    }
     bool split = false;
     hipError_t e = N <= 4096 ? mm_planes_fin(Ap, R, W, N, K, epi, mm, st, fin, &split) : mm_planes(Ap, R, W, N, K, epi, mm, st);
     if (e != hipSuccess || split) return e;
@@ -529,6 +571,44 @@ hipError_t rows_dec_pv(int G, dim3 grid, hipStream_t st, const int32_t* rows, in
 // One batched forward over the rows already uploaded to b->rows; lmax is the
 // largest position + 1 among them.  The final norm and LM head run over rows
 // [h0, R) only, into logits_out [(R - h0) x V] and argmax_out [R - h0].
+// Whether the decode-batch products of R rows take the fragment-major q/k/v,
+// gate/up and down weights (gemm_frag.h): by default for up to 32 rows when the
+// gate/up K (the hidden size) is at least 3 KiB, where they stream the
+// weights faster than the tiled products (B = 8 / 32 at the 7B shape on
+// MI355X: gate/up 30.4 -> 24.1 us and 50.4 -> 32.4 us with its SiLU, down
+// 16.9 -> 14.3 us and 26.3 -> 21.9 us).  MYL_BATCH_FRAG=1 takes them for every
+// shape they support, 0 never.  The copies are built on first use (one
+// relayout per layer on the stream); false when they cannot be (shapes or
+// memory), and the tiled products run.
+bool frag_ready(myl_model* m, int R, const MmCtx* mm, hipStream_t st) {
+    const char* env = std::getenv("MYL_BATCH_FRAG");
+    const int mode = env && *env ? std::atoi(env) : -1;
+    if (mode == 0 || m->frag_state < 0 || !mm || R < 2 || R > kFragMaxRows) return false;
+    const int H = m->H, I = m->I;
+    if (mode < 0 && H < 3072) return false;
+    const int nqkv = m->nq + 2 * m->nkv;
+    if (!frag_full_ok(R, H, 2 * I, mm->cus) || !frag_split_ok(R, I, H, mm->cus, mm->acc_elems) ||
+        !frag_full_ok(R, H, nqkv, mm->cus))
+        return false;
+    if (m->frag_state == 1) return true;
+    for (LayerDev& L : m->layers) {
+        if (!L.wqkv_f) L.wqkv_f = m->dalloc<int8_t>(frag_bytes(nqkv, H));
+        if (!L.wgu_f) L.wgu_f = m->dalloc<int8_t>(frag_bytes(2 * I, H));
+        if (!L.wd_f) L.wd_f = m->dalloc<int8_t>(frag_bytes(H, I));
+        if (!L.wqkv_f || !L.wgu_f || !L.wd_f) {
+            m->frag_state = -1;
+            return false;
+        }
+        if (frag_relayout(L.wqkv, nqkv, H, L.wqkv_f, st) != hipSuccess ||
+            frag_relayout(L.wgu, 2 * I, H, L.wgu_f, st) != hipSuccess || frag_relayout(L.wd, H, I, L.wd_f, st) != hipSuccess) {
+            m->frag_state = -1;
+            return false;
+        }
+    }
+    m->frag_state = 1;
+    return true;
+}
+
 hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, int32_t* logits_out,
                         int64_t* argmax_out) {
     myl_ctx* c = m->ctx;
@@ -549,7 +629,8 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
     // planes itself (staged epilogue) when its tiles need no K split
     // (17-64 rows: the split gate/up product with its own finish and SiLU
     // measured faster on MI355X than the unsplit fused one)
-    const bool fuse_silu = planes && I % 8 == 0 && (R > 64 || (R <= 16 && H % 128 == 0)) &&
+    const bool frag = planes && frag_ready(m, R, mm, st);
+    const bool fuse_silu = planes && I % 8 == 0 && (R > 64 || (R <= 16 && H % 128 == 0) || frag) &&
                            (size_t)2 * R * ((size_t)I + H) <= mm->planes_bytes;
     int8_t* const xin = mm && mm->planes ? mm->planes + (size_t)2 * R * I : nullptr;  // gate/up input planes
     const uint8_t lut_shift = MYL_TV_SCORE_FRAC_BITS - MYL_TV_EXP_INPUT_FRAC;
@@ -575,6 +656,14 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
                                     MYL_TV_RSQRT_INPUT_SHIFT, MYL_TV_RSQRT_OUTPUT_FRAC, m->inv_n_q20, f.norm_attn_frac,
                                     mm->planes, st)) != hipSuccess)
                 return e;
+            if (frag) {
+                // fragment-major weights: RoPE and the KV append in the product's epilogue
+                const FragOutQKV oq{eq, b->rows, b->rows_cap, nq, nkv, m->hd_log, m->cos_lut, m->sin_lut, b->Q,
+                                    b->kc + (size_t)l * kvh * m->max_pos * hd,
+                                    b->vc + (size_t)l * kvh * m->max_pos * hd, sstride, m->max_pos};
+                if ((e = frag_mm_full(mm->planes, R, H, Ld.wqkv_f, nqkv, oq, false, mm->cus, st)) != hipSuccess) return e;
+                qkv_roped = true;
+            }
             // a split product finishes with RoPE and the KV append fused in
             auto fin = [&](unsigned long long* acc, hipStream_t s) -> hipError_t {
                 qkv_finish_rope_kernel<<<dim3((nqkv / 2 + 255) / 256, R), 256, 0, s>>>(
@@ -583,7 +672,7 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
                     m->max_pos);
                 return hipGetLastError();
             };
-            if ((e = mm_planes_fin(mm->planes, R, Ld.wqkv, nqkv, H, eq, mm, st, fin, &qkv_roped)) != hipSuccess)
+            if (!frag && (e = mm_planes_fin(mm->planes, R, Ld.wqkv, nqkv, H, eq, mm, st, fin, &qkv_roped)) != hipSuccess)
                 return e;
         } else {
             if ((e = rmsnorm(b->X, R, H, Ld.res_in, Ld.in_gamma, Ld.in_gamma_s, H, m->rsqrt, m->rsqrt_len,
@@ -694,7 +783,9 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
             // the post-attention norm's planes (xin) come from the o_proj finish
             EpiGUSiluPlanes es{Ld.sgu, f.norm_mlp_frac, f.gate_frac, f.up_frac, f.down_in_frac,
                                m->silu, (uint32_t)m->silu_len, mm->planes, I};
-            if ((e = mm_planes_staged(xin, R, Ld.wgu, 2 * I, H, es, mm, st)) != hipSuccess) return e;
+            if ((e = frag ? frag_mm_staged(xin, R, H, Ld.wgu_f, 2 * I, es, mm->cus, st)
+                          : mm_planes_staged(xin, R, Ld.wgu, 2 * I, H, es, mm, st)) != hipSuccess)
+                return e;
         } else if (planes) {
             // the post-attention norm's planes come from the o_proj finish
             if ((e = mm_planes(mm->planes, R, Ld.wgu, 2 * I, H, eg, mm, st)) != hipSuccess) return e;
@@ -718,7 +809,7 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         if (in_normed) {
             const LayerDev& Ln = m->layers[l + 1];
             e = resid_then_norm(mm->planes, R, Ld.wd, H, I, ed, mm, Ln.res_in, Ln.ref_in, Ln.in_gamma, Ln.in_gamma_s, m,
-                                Ln.f.norm_attn_frac, mm->planes, st);
+                                Ln.f.norm_attn_frac, mm->planes, st, frag ? Ld.wd_f : nullptr);
         } else {
             e = planes ? mm_planes(mm->planes, R, Ld.wd, H, I, ed, mm, st) : gemv_i8(b->Hh, R, I, Ld.wd, H, I, ed, st, mm);
         }

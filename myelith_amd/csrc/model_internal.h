@@ -28,6 +28,9 @@ struct NormAcc { unsigned long long v[kNormSlots][3]; };
 
 struct LayerDev {
     int8_t *wqkv = nullptr, *wo = nullptr, *wgu = nullptr, *wd = nullptr;
+    // fragment-major copies of wqkv, wgu and wd for the decode-batch
+    // products (gemm_frag.h), built on first use
+    int8_t *wqkv_f = nullptr, *wgu_f = nullptr, *wd_f = nullptr;
     uint8_t *sqkv = nullptr, *so = nullptr, *sgu = nullptr, *sd = nullptr;
     int16_t* bqkv = nullptr;
     uint8_t* bsqkv = nullptr;
@@ -79,6 +82,9 @@ struct myl_model {
     int8_t* lm16_planes = nullptr;
     int32_t* lm16_wsum = nullptr;
     bool lm16_planes_ok = false;
+    // the layers' fragment-major q/k/v, gate/up and down copies: 0 not built (or a
+    // weight upload since), 1 current, -1 not available (shapes or memory)
+    int frag_state = 0;
     int8_t* final_gamma = nullptr;
     uint8_t* final_gamma_s = nullptr;
     uint8_t* final_res = nullptr;

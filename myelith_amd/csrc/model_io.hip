@@ -244,6 +244,12 @@ int put_tensor(myl_model* m, Staging& st, const Target& t, Reader& rd, const uin
     }
     m->have[t.slot] = 1;
     if (t.slot == myl::SLOT_LM16) m->lm16_planes_ok = false;
+    if (t.slot >= (size_t)myl::kModelSlots) {
+        const int ls = (int)((t.slot - myl::kModelSlots) % myl::kLayerSlots);
+        const bool frag_src = ls == myl::SLOT_Q || ls == myl::SLOT_K || ls == myl::SLOT_V || ls == myl::SLOT_GATE ||
+                              ls == myl::SLOT_UP || ls == myl::SLOT_DOWN;
+        if (frag_src && m->frag_state > 0) m->frag_state = 0;
+    }
     return MYL_OK;
 }
 

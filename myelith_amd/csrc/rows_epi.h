@@ -33,10 +33,16 @@ struct EpiQKVRows : EpiApply<EpiQKVRows> {
     int16_t* out; int ldo;
     EpiQKVRows offset_m(int m0) const { EpiQKVRows e = *this; e.out += (size_t)m0 * ldo; return e; }
     // the requantised projection (+ bias) of output n, not stored
-    __device__ inline int16_t value(int n, int64_t acc) const {
+    __device__ inline int16_t value(int n, int64_t acc) const { return value_with(val_ops(n), n, acc); }
+    // the same in two steps: the row's operands, fetched ahead of the sum
+    struct ValOps { uint8_t sh, bs; int16_t b; };
+    __device__ inline ValOps val_ops(int n) const {
+        return ValOps{shifts[n], bias ? bias_sh[n] : (uint8_t)0, bias ? bias[n] : (int16_t)0};
+    }
+    __device__ inline int16_t value_with(const ValOps& o, int n, int64_t acc) const {
         const uint8_t frac = n < nq ? q_frac : (n < nq + nkv ? k_frac : v_frac);
-        int16_t v = clamp_i16_i64(rescale64(acc, (uint8_t)(shifts[n] + act_frac), frac));
-        if (bias) v = clamp_i16_i64((int64_t)v + (int64_t)rescale32((int32_t)bias[n], bias_sh[n], frac));
+        int16_t v = clamp_i16_i64(rescale64(acc, (uint8_t)(o.sh + act_frac), frac));
+        if (bias) v = clamp_i16_i64((int64_t)v + (int64_t)rescale32((int32_t)o.b, o.bs, frac));
         return v;
     }
     __device__ inline void one(int n, int m, int64_t acc) const { out[(size_t)m * ldo + n] = value(n, acc); }
@@ -114,8 +120,12 @@ struct EpiGUSiluPlanes {
     uint8_t act_frac, gate_frac, up_frac, down_in_frac;
     const int16_t* silu; uint32_t silu_len;
     int8_t* planes; int I;
-    __device__ inline int16_t stage(int n, int64_t acc) const {
-        return clamp_i16_i64(rescale64(acc, (uint8_t)(shifts[n] + act_frac), (n & 1) ? up_frac : gate_frac));
+    __device__ inline int16_t stage(int n, int64_t acc) const { return stage_with(op(n), n, acc); }
+    // the same in two steps: the row's operand, fetched ahead of the sum
+    using Op = uint8_t;
+    __device__ inline Op op(int n) const { return shifts[n]; }
+    __device__ inline int16_t stage_with(Op sh, int n, int64_t acc) const {
+        return clamp_i16_i64(rescale64(acc, (uint8_t)(sh + act_frac), (n & 1) ? up_frac : gate_frac));
     }
     __device__ inline void emit(int m, int i0, const uint4& a, const uint4& b) const {
         const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};  // (g, u) pairs

@@ -219,6 +219,47 @@ def test_batch_decode_rows_grouped_heads(backend, hd, heads, bias):
         compare_batch_kv(gm, om, spec, s, list(toks[s][:n + 1]) + [first[s]] + exp[:-1])
 
 
+@pytest.mark.parametrize("rows", [5, 16, 32])
+@pytest.mark.parametrize("shape", ["k7", "k64_down2"])
+def test_batch_fragment_products(backend, monkeypatch, shape, rows):
+    """Decode batches through the fragment-major gate/up and down products
+    (MYL_BATCH_FRAG=1 takes them at every size they support): 5, 16 and 32
+    rows (one, two and four 16-row plane tiles); a hidden size of 7 K tiles
+    (one of the eight waves carries K) and one of 64 tiles (eight per wave)
+    whose down product runs in two K slices.  The decode row's logits and
+    argmax and two greedy steps equal the tiled products' (MYL_BATCH_FRAG=0)
+    bit for bit, and the decode row's logits equal the oracle's for the
+    first, a middle and the last sequence."""
+    if shape == "k7":
+        spec = dict(seed=9, vocab=1000, hidden=7 * 64, layers=2, heads=7, kv_heads=1, head_dim=64, inter=320,
+                    max_pos=64, lm_head_int16=0, attention_bias=1)
+    else:
+        spec = dict(seed=10, vocab=1000, hidden=32 * 128, layers=1, heads=32, kv_heads=4, head_dim=128, inter=4160,
+                    max_pos=64, lm_head_int16=1, attention_bias=0)
+    case(f"fragment products, {rows} rows, {spec}")
+    gm, om = build(backend, spec)
+    r = np.random.default_rng(rows * 3 + len(shape))
+    lens = [int(n) for n in r.integers(1, 4, rows)]
+    toks = [r.integers(0, spec["vocab"], n + 1) for n in lens]
+    runs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("MYL_BATCH_FRAG", mode)
+        gm.batch_begin(rows)
+        pre = [(s, p) for s, n in enumerate(lens) for p in range(n)]
+        gm.forward_batch([s for s, _ in pre], [p for _, p in pre], [int(toks[s][p]) for s, p in pre],
+                         want_logits=False)
+        logits, am = gm.forward_batch(list(range(rows)), lens, [int(toks[s][n]) for s, n in enumerate(lens)])
+        out = gm.batch_decode_greedy(range(rows), [n + 1 for n in lens], [int(a) for a in am], 2)
+        runs[mode] = (np.array(logits), np.array(am), np.array(out))
+    for a, b, what in zip(runs["0"], runs["1"], ("logits", "argmax", "greedy tokens")):
+        assert np.array_equal(a, b), what
+    for s in sorted({0, rows // 2, rows - 1}):
+        om.reset()
+        for p in range(lens[s] + 1):
+            ref = om.forward_token(int(toks[s][p]), p)
+        assert np.array_equal(runs["1"][0][s], ref), ("decode row", s)
+
+
 @pytest.mark.parametrize("variant", ["zero", "long_tail"])
 def test_batch_decode_rows_exp_table_variants(backend, variant):
     """Decode batches with an all-zero exp table (every head sum is 0: the
