@@ -12,9 +12,9 @@
 // are stored row group by row group (g, then t), so a wave's 16-byte load
 // of one tile is one contiguous KiB and lands in the B-operand registers.
 //
-// Launch: one block of 8 waves per CU.  Block b takes K slice s = b / P and
-// the row groups of part p = b % P; wave w of the block owns the KPW K tiles
-// [s 8 KPW + w KPW, + KPW) and keeps their A' fragments in registers for the
+// Launch: one block of 8 waves per CU (S P <= CUs blocks).  Block b takes K
+// slice s = b / P and the row groups of part p = b % P; wave w of the block
+// owns the KPW K tiles [s 8 KPW + w KPW, + KPW) and keeps their A' fragments in registers for the
 // whole kernel (RT tiles of 16 plane rows each), then streams the weight
 // tiles (g, its K tiles) of every row group g of the block: the eight waves
 // read each row group's KT KiB side by side, so a block sweeps its weight
@@ -302,29 +302,51 @@ hipError_t frag_mm_staged(const int8_t* Ap, int R, int K, const int8_t* Wf, int 
     return frag_mm_full(Ap, R, K, Wf, N, FragOutStaged<Epi>{epi}, true, cus, st);
 }
 
-// S = ceil(KT / 64) K slices of 64 KiB-tiles (8 per wave), each slice's
-// partial sums added into acc [R x N].
-inline int frag_split_slices(int K) { return (K / 64 + kFragWaves * 8 - 1) / (kFragWaves * 8); }
+// Split-K plan: KPW K tiles per wave (8 or 5), S = ceil(KT / (8 KPW)) K
+// slices of 8 KPW tiles, P = cus / S row parts; the plan whose busiest wave
+// streams the fewest tiles (ceil(NG / P) row groups x KPW).  For the 7B down
+// product (296 K tiles, 224 row groups): 5 x 8 slices, 7 row groups per block
+// (the busiest wave 35 tiles; 8 tiles a wave in 5 slices: 40).
+struct FragSplit {
+    int kpw = 0, S = 0, P = 0, ngb = 0;
+};
+inline FragSplit frag_split_plan(int K, int N, int cus) {
+    FragSplit best;
+    const int KT = K / 64, NG = (N + 15) / 16;
+    for (int kpw : {8, 5}) {
+        const int S = (KT + kFragWaves * kpw - 1) / (kFragWaves * kpw);
+        if (S > cus) continue;
+        const int P = std::max(1, cus / S), ngb = (NG + P - 1) / P;
+        if (best.kpw == 0 || ngb * kpw < best.ngb * best.kpw) best = FragSplit{kpw, S, P, ngb};
+    }
+    return best;
+}
 
 inline bool frag_split_ok(int R, int K, int N, int cus, size_t acc_elems) {
     if (frag_rt(R) == 0 || R < 1 || K <= 0 || K % 64 != 0 || N <= 0 || (size_t)R * (size_t)N > acc_elems) return false;
-    const int S = frag_split_slices(K);
-    if (S > cus) return false;
-    const int P = std::max(1, cus / S), NG = (N + 15) / 16, ngb = (NG + P - 1) / P;
-    return frag_lds(frag_rt(R), ngb, R, false) <= kFragLdsMax;
+    const FragSplit sp = frag_split_plan(K, N, cus);
+    return sp.kpw != 0 && frag_lds(frag_rt(R), sp.ngb, R, false) <= kFragLdsMax;
 }
 
+// The K-sliced product: each slice's partial sums added into acc [R x N].
 inline hipError_t frag_mm_split(const int8_t* Ap, int R, int K, const int8_t* Wf, int N, unsigned long long* acc,
                                 int cus, size_t acc_elems, hipStream_t st) {
     if (!frag_split_ok(R, K, N, cus, acc_elems)) return hipErrorInvalidValue;
-    const int S = frag_split_slices(K), P = std::max(1, cus / S);
-    const int NG = (N + 15) / 16, ngb = (NG + P - 1) / P, rt = frag_rt(R);
-    const size_t lds = frag_lds(rt, ngb, R, false);
+    const FragSplit sp = frag_split_plan(K, N, cus);
+    const int rt = frag_rt(R);
+    const size_t lds = frag_lds(rt, sp.ngb, R, false);
     const FragOutAtomic out{acc};
+    if (sp.kpw == 5) {
+        switch (rt) {
+        case 1: return frag_launch<1, 5>(Ap, R, K, Wf, N, sp.S, sp.P, lds, out, st);
+        case 2: return frag_launch<2, 5>(Ap, R, K, Wf, N, sp.S, sp.P, lds, out, st);
+        default: return frag_launch<4, 5>(Ap, R, K, Wf, N, sp.S, sp.P, lds, out, st);
+        }
+    }
     switch (rt) {
-    case 1: return frag_launch<1, 8>(Ap, R, K, Wf, N, S, P, lds, out, st);
-    case 2: return frag_launch<2, 8>(Ap, R, K, Wf, N, S, P, lds, out, st);
-    default: return frag_launch<4, 8>(Ap, R, K, Wf, N, S, P, lds, out, st);
+    case 1: return frag_launch<1, 8>(Ap, R, K, Wf, N, sp.S, sp.P, lds, out, st);
+    case 2: return frag_launch<2, 8>(Ap, R, K, Wf, N, sp.S, sp.P, lds, out, st);
+    default: return frag_launch<4, 8>(Ap, R, K, Wf, N, sp.S, sp.P, lds, out, st);
     }
 }
 
