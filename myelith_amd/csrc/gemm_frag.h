@@ -14,15 +14,16 @@
 //
 // Launch: one block of 8 waves per CU (S P <= CUs blocks).  Block b takes K
 // slice s = b / P and the row groups of part p = b % P; wave w of the block
-// owns the KPW K tiles [s 8 KPW + w KPW, + KPW) and keeps their A' fragments in registers for the
-// whole kernel (RT tiles of 16 plane rows each), then streams the weight
-// tiles (g, its K tiles) of every row group g of the block: the eight waves
-// read each row group's KT KiB side by side, so a block sweeps its weight
-// range in order.  The batches of KPW tiles of two row groups alternate in
-// two register buffers.  Each wave adds its partial sums of a row group into
-// LDS (exact i32 plane sums); after the stream the block hands every exact
-// sum of its rows to the output policy: the whole product's epilogue when
-// there is one K slice, the split-K accumulator otherwise.
+// owns the KPW K tiles [s 8 KPW + w KPW, + KPW) and keeps their A' fragments
+// in registers for the whole kernel (RT tiles of 16 plane rows each), then
+// streams the weight tiles (g, its K tiles) of every row group g of the
+// block: the eight waves read each row group's KT KiB side by side, so a
+// block sweeps its weight range in order.  The batches of KPW tiles of two
+// row groups alternate in two register buffers.  Each wave adds its partial
+// sums of a row group into LDS (exact i32 plane sums); after the stream the
+// block hands every exact sum of its rows to the output policy: the whole
+// product's epilogue when there is one K slice, the split-K accumulator
+// otherwise.
 //
 // Bounds: |plane sum| <= 128 * 128 * K < 2^31 for K < 2^17.
 #pragma once
