@@ -262,12 +262,10 @@ template <int RT, int KPW, class Out>
 hipError_t frag_launch(const int8_t* Ap, int R, int K, const int8_t* Wf, int N, int S, int P, size_t lds, const Out& out,
                        hipStream_t st) {
     auto kern = frag_mm_kernel<RT, KPW, Out>;
-    static bool attr = false;  // per instantiation
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kFragLdsMax);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    // set on every launch, as the other product launchers do: the attribute
+    // belongs to the current device
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
     kern<<<S * P, kFragWaves * 64, lds, st>>>(Ap, 2 * R, K, Wf, N, (N + 15) / 16, Divider::of((uint32_t)P), out);
     return hipGetLastError();
 }
