@@ -112,22 +112,18 @@ __global__ __launch_bounds__(256) void rope_scatter_kernel(const int16_t* __rest
 
 // RoPE of a q/k pair (rope.rs:17-31) and its destination: q to Q in
 // head-major order, k (post-RoPE) and v to the sequence's cache at the row's
-// position (model.rs:469-503).  Shared by rope_scatter_kernel and the fused
-// finish of a split q/k/v product.
-__device__ inline void rope_store_pair(int r, int n0, int16_t y0, int16_t y1, const int32_t* __restrict__ rows,
-                                       int rows_cap, int nq, int nkv, int hd_log, const int16_t* __restrict__ cos_lut,
-                                       const int16_t* __restrict__ sin_lut, int16_t* __restrict__ Q,
-                                       int16_t* __restrict__ kc, int16_t* __restrict__ vc, size_t seq_stride,
-                                       int max_pos) {
+// position (model.rs:469-503), for row r at sequence seq and position pos
+// with the pair's cos / sin entries c, s (used for q and k).
+__device__ inline void rope_store_pair_at(int r, int n0, int16_t y0, int16_t y1, int seq, int pos, int32_t c,
+                                          int32_t s, int nq, int nkv, int hd_log, int16_t* __restrict__ Q,
+                                          int16_t* __restrict__ kc, int16_t* __restrict__ vc, size_t seq_stride,
+                                          int max_pos) {
     const int seg = n0 < nq ? 0 : (n0 < nq + nkv ? 1 : 2);
     const int e = n0 - (seg == 0 ? 0 : (seg == 1 ? nq : nq + nkv));
     const int hd = 1 << hd_log, half = hd >> 1;
     const int head = e >> hd_log;
     const int p = (e & (hd - 1)) >> 1;
-    const int seq = rows[r], pos = rows[rows_cap + r], rope_row = rows[2 * rows_cap + r];
     if (seg < 2) {
-        const int32_t c = cos_lut[(size_t)rope_row * half + p];
-        const int32_t s = sin_lut[(size_t)rope_row * half + p];
         const int32_t x0 = y0, x1 = y1;
         y0 = clamp_i16(rshift_round32(wsub32(wmul32(x0, c), wmul32(x1, s)), MYL_TV_ROPE_FRAC_BITS));
         y1 = clamp_i16(rshift_round32(wadd32(wmul32(x1, c), wmul32(x0, s)), MYL_TV_ROPE_FRAC_BITS));
@@ -137,6 +133,31 @@ __device__ inline void rope_store_pair(int r, int n0, int16_t y0, int16_t y1, co
     else dst = (seg == 1 ? kc : vc) + (size_t)seq * seq_stride + ((size_t)head * max_pos + pos) * hd;
     dst[p] = y0;
     dst[p + half] = y1;
+}
+
+// The pair's cos / sin entries for RoPE row rope_row (zero for v rows).
+__device__ inline void rope_cs(int n0, int rope_row, int nq, int nkv, int hd_log, const int16_t* __restrict__ cos_lut,
+                               const int16_t* __restrict__ sin_lut, int32_t& c, int32_t& s) {
+    c = s = 0;
+    if (n0 >= nq + nkv) return;
+    const int e = n0 - (n0 < nq ? 0 : nq);
+    const int half = (1 << hd_log) >> 1, p = (e & ((1 << hd_log) - 1)) >> 1;
+    c = cos_lut[(size_t)rope_row * half + p];
+    s = sin_lut[(size_t)rope_row * half + p];
+}
+
+// rope_store_pair_at with the row's sequence, position and RoPE row read
+// from the row table.  Shared by rope_scatter_kernel and the fused finish of
+// a split q/k/v product.
+__device__ inline void rope_store_pair(int r, int n0, int16_t y0, int16_t y1, const int32_t* __restrict__ rows,
+                                       int rows_cap, int nq, int nkv, int hd_log, const int16_t* __restrict__ cos_lut,
+                                       const int16_t* __restrict__ sin_lut, int16_t* __restrict__ Q,
+                                       int16_t* __restrict__ kc, int16_t* __restrict__ vc, size_t seq_stride,
+                                       int max_pos) {
+    const int seq = rows[r], pos = rows[rows_cap + r], rope_row = rows[2 * rows_cap + r];
+    int32_t c, s;
+    rope_cs(n0, rope_row, nq, nkv, hd_log, cos_lut, sin_lut, c, s);
+    rope_store_pair_at(r, n0, y0, y1, seq, pos, c, s, nq, nkv, hd_log, Q, kc, vc, seq_stride, max_pos);
 }
 
 // The q/k/v product's epilogue on the fragment-major weights (gemm_frag.h):
@@ -151,11 +172,20 @@ struct FragOutQKV {
     int16_t *Q, *kc, *vc;
     size_t seq_stride;
     int max_pos;
-    struct Pre { EpiQKVRows::ValOps o0, o1; };
-    __device__ inline Pre pre(int g0, int ngb, int, int N) const {
-        const int c2 = FragCols::of(8 * ngb).col();
-        const int n0 = min(16 * g0 + 2 * c2, N - 2);
-        return Pre{epi.val_ops(n0), epi.val_ops(n0 + 1)};
+    // the pair's operands, and the seq / position / cos / sin of the thread's
+    // first row (the only one while 8 ngb x R <= 512)
+    struct Pre {
+        EpiQKVRows::ValOps o0, o1;
+        int seq, pos;
+        int32_t c, s;
+    };
+    __device__ inline Pre pre(int g0, int ngb, int R, int N) const {
+        const FragCols fc = FragCols::of(8 * ngb);
+        const int n0 = min(16 * g0 + 2 * fc.col(), N - 2);
+        const int m = min(fc.row0(), R - 1);
+        Pre q{epi.val_ops(n0), epi.val_ops(n0 + 1), rows[m], rows[rows_cap + m], 0, 0};
+        rope_cs(n0, rows[2 * rows_cap + m], nq, nkv, hd_log, cos_lut, sin_lut, q.c, q.s);
+        return q;
     }
     template <int RT>
     __device__ inline void run(const Pre& pr, const FragSums<RT>& s, int g0, int ngb, int R, int N, int8_t*) const {
@@ -167,8 +197,12 @@ struct FragOutQKV {
         for (int m = fc.row0(); m < R; m += fc.slices) {
             const int16_t y0 = epi.value_with(pr.o0, n0, s(gg, m, cc));
             const int16_t y1 = epi.value_with(pr.o1, n0 + 1, s(gg, m, cc + 1));
-            rope_store_pair(m, n0, y0, y1, rows, rows_cap, nq, nkv, hd_log, cos_lut, sin_lut, Q, kc, vc, seq_stride,
-                            max_pos);
+            if (m == fc.row0())
+                rope_store_pair_at(m, n0, y0, y1, pr.seq, pr.pos, pr.c, pr.s, nq, nkv, hd_log, Q, kc, vc, seq_stride,
+                                   max_pos);
+            else
+                rope_store_pair(m, n0, y0, y1, rows, rows_cap, nq, nkv, hd_log, cos_lut, sin_lut, Q, kc, vc,
+                                seq_stride, max_pos);
         }
     }
 };
