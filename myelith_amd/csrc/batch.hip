@@ -798,7 +798,8 @@ hipError_t forward_rows(myl_model* m, BatchState* b, int R, int lmax, int h0, in
         if ((e = hipGetLastError()) != hipSuccess) return e;
         if (!loop) {
             rows_attn_out_kernel<<<dim3((nq + 255) / 256, R), 256, 0, st>>>(b->part, pst, b->rows, b->rows_cap, nq,
-                                                                            f.v_frac, f.attn_out_frac, b->A, pplanes);
+                                                                            ranges, f.v_frac, f.attn_out_frac, b->A,
+                                                                            pplanes);
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
         EpiResidRows eo{};

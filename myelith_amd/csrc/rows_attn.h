@@ -448,17 +448,28 @@ __global__ __launch_bounds__(kAttnThreads) void rows_pv_kernel(
 
 // attention.rs:84-86 then model.rs:563-567: the ranges' exact sums, one
 // rounding, the attn_out rescale; into A, or as byte planes when planes is
-// given.  Grid (ceil(nq / 256), R).
+// given.  Grid (ceil(nq / 256), R); nranges is the range count of the P.V
+// launch (every range slot it names lies in part).  The partials of all
+// nranges slots are loaded together, without waiting for the row's length,
+// which then selects the ranges the row's P.V blocks wrote.
 __global__ __launch_bounds__(256) void rows_attn_out_kernel(const int64_t* __restrict__ part, size_t part_stride,
                                                             const int32_t* __restrict__ rows, int rows_cap, int nq,
-                                                            uint8_t v_frac, uint8_t out_frac, int16_t* __restrict__ A,
-                                                            int8_t* __restrict__ planes) {
+                                                            int nranges, uint8_t v_frac, uint8_t out_frac,
+                                                            int16_t* __restrict__ A, int8_t* __restrict__ planes) {
+    constexpr int kBatch = 16;  // range slots loaded before the first add
     const int r = blockIdx.y;
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= nq) return;
     const int nr = rows[rows_cap + r] / kAttnRange + 1;
+    const int64_t* pr = part + (size_t)r * nq + i;
     int64_t s = 0;
-    for (int c = 0; c < nr; ++c) s = wadd64(s, part[(size_t)c * part_stride + (size_t)r * nq + i]);
+    for (int c0 = 0; c0 < nranges; c0 += kBatch) {
+        int64_t v[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) v[k] = c0 + k < nranges ? pr[(size_t)(c0 + k) * part_stride] : 0;
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) s = wadd64(s, c0 + k < nr ? v[k] : 0);
+    }
     const int16_t v = clamp_i16_i64(rshift_round64(s, MYL_TV_PROB_FRAC_BITS));
     const int16_t a = clamp_i16(rescale32((int32_t)v, v_frac, out_frac));
     if (planes) {  // byte planes [2R x nq] for the o_proj product

@@ -30,70 +30,85 @@ __device__ inline const T* uniform_ptr(const T* p) {
 }
 
 // Grid (ceil(lmax / kChunk), KV heads, rows); 256 threads.  Chunks at or
-// past a row's length return at once.  Four lanes hold a K row (a wave 16
-// positions), lane sub of a row the 16-byte pieces 4 p + sub, split once into
-// byte planes k = 256 k_hi + k_lo (k_lo in [0, 255]) for all G heads: q . k =
-// 256 sum(q k_hi) + sum(q k_lo) on v_dot2_i32_i16, exact in i32 (|q k_hi| <
-// 2^22 and 0 <= k_lo < 2^8 over at most 128 dimensions), the four lanes'
-// partials added with two DPP moves.  The G query vectors sit in LDS.
+// past a row's length return at once.  A wave takes 16 positions on
+// v_mfma_i32_16x16x64_i8: lane l holds position (column) l % 16 and query
+// head (row) l % 16, each the 16-dimension block l / 16 of every 64-dimension
+// step, split into byte planes x = 256 hi + lo' + 128 (lo' = lo - 128), so
+//   q . k = 65536 hh + 256 (hl + lh) + ll + 128 sum(q) + 128 sum(k) - 16384 HD
+// with hh = sum(q_hi k_hi) and so on, every plane sum exact in i32 (at most
+// 2^15 HD in magnitude).  Rows G .. 14 of the query tile are padding; row 15
+// holds ones, so the hh and ll products' row 15 are sum(k_hi) and sum(k_lo')
+// of each position, which give sum(k) = 256 sum(k_hi) + sum(k_lo') + 128 HD.
+// Loads past the row's length read zero (the K descriptor ends there).
 template <int HD, int G>
 __global__ __launch_bounds__(256) void rows_dec_qk_kernel(const int32_t* __restrict__ rows, int rows_cap,
                                                           const int16_t* __restrict__ Q, int nq,
                                                           const int16_t* __restrict__ kc, size_t seq_stride,
                                                           int max_pos, int64_t score_mult, uint8_t score_shift,
                                                           int32_t* __restrict__ scores, int heads, int lcap) {
-    constexpr int NP = HD / 32;  // 16-byte pieces per lane
-    constexpr int QP = HD / 8;   // 16-byte pieces per query vector
-    static_assert(G * QP <= 256, "one query piece per thread");
-    __shared__ uint4 qs[G][QP];
+    static_assert(G < 16, "row 15 of the query tile holds the ones of the K sums");
+    static_assert(kChunk == 64, "four waves of 16 positions");
+    constexpr int NS = HD / 64;  // 64-dimension steps
     const int r = blockIdx.z, g = blockIdx.y, base = blockIdx.x * kChunk;
     const int L = __builtin_amdgcn_readfirstlane(rows[rows_cap + r] + 1);
     if (base >= L) return;
     const int seq = __builtin_amdgcn_readfirstlane(rows[r]);
-    const int tid = threadIdx.x, lane = tid & 63, sub = lane & 3;
-    const int j = base + (tid >> 6) * 16 + (lane >> 2);
-    const int16_t* kg = kc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD;
-    uint4 kv[NP];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane & 15, kb = lane >> 4;
+    const int j = base + 16 * wave + c;
+    const __amdgpu_buffer_rsrc_t rk = weight_rsrc(uniform_ptr(kc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD),
+                                                  (uint32_t)L * HD * 2u);
+    // the G query vectors are contiguous in the row's q; rows G and beyond read zero
+    const __amdgpu_buffer_rsrc_t rq = weight_rsrc(uniform_ptr(Q + (size_t)r * nq + (size_t)g * G * HD), G * HD * 2u);
+    uint4 kx[NS][2], qx[NS][2];
 #pragma unroll
-    for (int p = 0; p < NP; ++p)
-        kv[p] = j < L ? *reinterpret_cast<const uint4*>(kg + (size_t)j * HD + 8 * (4 * p + sub)) : make_uint4(0, 0, 0, 0);
-    if (tid < G * QP)  // the G vectors are contiguous in the row's q
-        qs[tid / QP][tid % QP] = *reinterpret_cast<const uint4*>(Q + (size_t)r * nq + (size_t)g * G * HD + tid * 8);
-    uint4 kh[NP], kl[NP];
+    for (int s = 0; s < NS; ++s)
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-        split_pair(kv[p].x, kh[p].x, kl[p].x);
-        split_pair(kv[p].y, kh[p].y, kl[p].y);
-        split_pair(kv[p].z, kh[p].z, kl[p].z);
-        split_pair(kv[p].w, kh[p].w, kl[p].w);
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t d = 64u * s + 16u * kb + 8u * t;
+            kx[s][t] = cload16(rk, ((uint32_t)j * HD + d) * 2u);
+            qx[s][t] = cload16(rq, ((uint32_t)c * HD + d) * 2u);
+        }
+    v4i32_t ah[NS], al[NS], bh[NS], bl[NS];
+    int32_t qsum = 0;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        uint2 h0, l0, h1, l1;
+        split_planes8(kx[s][0], h0, l0);
+        split_planes8(kx[s][1], h1, l1);
+        bh[s] = v4i32_t{(int)h0.x, (int)h0.y, (int)h1.x, (int)h1.y};
+        bl[s] = v4i32_t{(int)l0.x, (int)l0.y, (int)l1.x, (int)l1.y};
+        split_planes8(qx[s][0], h0, l0);
+        split_planes8(qx[s][1], h1, l1);
+        const bool ones = c == 15;
+        const int one4 = 0x01010101;
+        ah[s] = ones ? v4i32_t{one4, one4, one4, one4} : v4i32_t{(int)h0.x, (int)h0.y, (int)h1.x, (int)h1.y};
+        al[s] = ones ? v4i32_t{one4, one4, one4, one4} : v4i32_t{(int)l0.x, (int)l0.y, (int)l1.x, (int)l1.y};
+        qsum += sum8_i16(qx[s][0]) + sum8_i16(qx[s][1]);
     }
-    __syncthreads();
-    typedef short __attribute__((ext_vector_type(2))) s2;
-    auto d2 = [](uint32_t a, uint32_t c, int32_t acc) {
-        return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, a), __builtin_bit_cast(s2, c), acc, false);
-    };
+    v4i32_t hh = {0, 0, 0, 0}, mid = {0, 0, 0, 0}, ll = {0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        hh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[s], bh[s], hh, 0, 0, 0);
+        mid = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[s], bl[s], mid, 0, 0, 0);
+        mid = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[s], bh[s], mid, 0, 0, 0);
+        ll = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[s], bl[s], ll, 0, 0, 0);
+    }
+    // head c's sum over the four dimension blocks, then sum(k) of column c
+    // from row 15 (register 3 of lanes 48-63)
+    qsum += __shfl_xor(qsum, 16, 64);
+    qsum += __shfl_xor(qsum, 32, 64);
+    const int32_t ksum = __shfl(256 * hh[3] + ll[3] + 128 * HD, 48 + c, 64);
+    const int64_t kterm = 128 * (int64_t)ksum - 16384 * (int64_t)HD;
     int32_t* z = scores + ((size_t)r * heads + (size_t)g * G) * lcap;
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-        int32_t ahi = 0, alo = 0;
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            const uint4 qv = qs[h][4 * p + sub];
-            ahi = d2(kh[p].x, qv.x, ahi);
-            ahi = d2(kh[p].y, qv.y, ahi);
-            ahi = d2(kh[p].z, qv.z, ahi);
-            ahi = d2(kh[p].w, qv.w, ahi);
-            alo = d2(kl[p].x, qv.x, alo);
-            alo = d2(kl[p].y, qv.y, alo);
-            alo = d2(kl[p].z, qv.z, alo);
-            alo = d2(kl[p].w, qv.w, alo);
-        }
-        ahi = (int32_t)((uint32_t)ahi + (uint32_t)dpp_mov<dpp::kXor1>(ahi));
-        ahi = (int32_t)((uint32_t)ahi + (uint32_t)dpp_mov<dpp::kXor2>(ahi));
-        alo = (int32_t)((uint32_t)alo + (uint32_t)dpp_mov<dpp::kXor1>(alo));
-        alo = (int32_t)((uint32_t)alo + (uint32_t)dpp_mov<dpp::kXor2>(alo));
-        if (sub == 0 && j < L) {
-            const int64_t dot = (int64_t)ahi * 256 + (int64_t)alo;
+    for (int rr = 0; rr < 4; ++rr) {
+        // lane l holds rows (heads) 4 (l / 16) + rr of column (position) l % 16
+        const int h = 4 * kb + rr;
+        const int32_t qs = __shfl(qsum, h, 64);
+        if (h < G && j < L) {
+            const int64_t dot = 65536 * (int64_t)hh[rr] + 256 * (int64_t)mid[rr] + (int64_t)ll[rr] +
+                                128 * (int64_t)qs + kterm;
             z[(size_t)h * lcap + j] = (int32_t)rshift_round64(wmul64(dot, score_mult), score_shift);
         }
     }
