@@ -219,6 +219,48 @@ def test_batch_decode_rows_grouped_heads(backend, hd, heads, bias):
         compare_batch_kv(gm, om, spec, s, list(toks[s][:n + 1]) + [first[s]] + exp[:-1])
 
 
+def test_batch_decode_rows_past_4096_positions(backend):
+    """Decode rows over contexts past 4096 positions (4100 and 4350, beside a
+    300-position one): the per-row score kernel over 68 position chunks, the
+    P.V kernel over 17 ranges and the output kernel's second batch of range
+    partials.  The contexts go in as batches of 2048 rows; the decode rows'
+    logits, the argmax and three lock-step greedy steps equal each sequence's
+    own forward_token run."""
+    spec = dict(seed=12, vocab=1000, hidden=8 * 64, layers=1, heads=8, kv_heads=2, head_dim=64, inter=320,
+                max_pos=4400, lm_head_int16=0, attention_bias=1)
+    case(f"batch decode rows past 4096 {spec}")
+    gm, om = build(backend, spec)
+    r = np.random.default_rng(4101)
+    lens = [4100, 4350, 300]
+    toks = [r.integers(0, spec["vocab"], n + 1) for n in lens]
+    S = len(lens)
+    gm.batch_begin(S)
+    rows = [(s, p) for s, n in enumerate(lens) for p in range(n)]
+    for i in range(0, len(rows), 2048):
+        chunk = rows[i:i + 2048]
+        gm.forward_batch([s for s, _ in chunk], [p for _, p in chunk], [int(toks[s][p]) for s, p in chunk],
+                         want_logits=False)
+    logits, am = gm.forward_batch(list(range(S)), lens, [int(toks[s][n]) for s, n in enumerate(lens)])
+    steps = 3
+    first, expected = [], []
+    for s, n in enumerate(lens):
+        om.reset()
+        for p in range(n + 1):
+            ref = om.forward_token(int(toks[s][p]), p)
+        assert np.array_equal(logits[s], ref), ("decode row", s, n)
+        nxt = int(np.argmax(ref))
+        first.append(nxt)
+        exp = []
+        for i in range(steps):
+            nxt = int(np.argmax(om.forward_token(nxt, n + 1 + i)))
+            exp.append(nxt)
+        expected.append(exp)
+    assert [int(a) for a in am] == first
+    out = gm.batch_decode_greedy(range(S), [n + 1 for n in lens], first, steps)
+    for s in range(S):
+        assert [int(t) for t in out[:, s]] == expected[s], s
+
+
 @pytest.mark.parametrize("rows", [5, 16, 32])
 @pytest.mark.parametrize("shape", ["k7", "k64_down2"])
 def test_batch_fragment_products(backend, monkeypatch, shape, rows):
