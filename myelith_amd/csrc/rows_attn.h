@@ -30,6 +30,7 @@
 #pragma once
 
 #include "gemm_mfma.h"
+#include "qk_planes.h"
 #include "gemv.h"
 #include "ops.h"
 #include "wave.h"
@@ -62,14 +63,6 @@ constexpr size_t attn_pv_lds() {
     return (size_t)2 * QVM * (kAttnRange + 16) + (size_t)2 * HD * (kAttnRange / attn_pv_passes(QVM) + 16);
 }
 
-// Sum of the eight int16 values of a 16-byte chunk.
-__device__ inline int32_t sum8_i16(const uint4 x) {
-    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
-    int32_t s = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s += (int32_t)(int16_t)(w[i] & 0xFFFFu) + (int32_t)(int16_t)(w[i] >> 16);
-    return s;
-}
 
 // Sum over the CH lanes (CH = 16 or 8, aligned rows of a wave) holding one vector.
 template <int CH>

@@ -16,30 +16,14 @@
 
 #include "bufload.h"
 #include "dec_attn.h"
+#include "qk_planes.h"
 #include "rows_attn.h"
 
 namespace myl {
 
-// A block-uniform pointer kept in scalar registers: a descriptor built from a
-// copy in vector registers makes every buffer load a loop over the lanes.
-template <class T>
-__device__ inline const T* uniform_ptr(const T* p) {
-    const uint64_t v = (uint64_t)(uintptr_t)p;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return reinterpret_cast<const T*>((uintptr_t)(((uint64_t)hi << 32) | lo));
-}
-
-// Grid (ceil(lmax / kChunk), KV heads, rows); 256 threads.  Chunks at or
-// past a row's length return at once.  A wave takes 16 positions on
-// v_mfma_i32_16x16x64_i8: lane l holds position (column) l % 16 and query
-// head (row) l % 16, each the 16-dimension block l / 16 of every 64-dimension
-// step, split into byte planes x = 256 hi + lo' + 128 (lo' = lo - 128), so
-//   q . k = 65536 hh + 256 (hl + lh) + ll + 128 sum(q) + 128 sum(k) - 16384 HD
-// with hh = sum(q_hi k_hi) and so on, every plane sum exact in i32 (at most
-// 2^15 HD in magnitude).  Rows G .. 14 of the query tile are padding; row 15
-// holds ones, so the hh and ll products' row 15 are sum(k_hi) and sum(k_lo')
-// of each position, which give sum(k) = 256 sum(k_hi) + sum(k_lo') + 128 HD.
-// Loads past the row's length read zero (the K descriptor ends there).
+// Grid (ceil(lmax / kChunk), KV heads, rows); 256 threads: wave w takes the
+// 16 positions from base + 16 w of its row's chunk (qk_planes_wave).  Chunks
+// at or past a row's length return at once.
 template <int HD, int G>
 __global__ __launch_bounds__(256) void rows_dec_qk_kernel(const int32_t* __restrict__ rows, int rows_cap,
                                                           const int16_t* __restrict__ Q, int nq,
@@ -48,70 +32,14 @@ __global__ __launch_bounds__(256) void rows_dec_qk_kernel(const int32_t* __restr
                                                           int32_t* __restrict__ scores, int heads, int lcap) {
     static_assert(G < 16, "row 15 of the query tile holds the ones of the K sums");
     static_assert(kChunk == 64, "four waves of 16 positions");
-    constexpr int NS = HD / 64;  // 64-dimension steps
     const int r = blockIdx.z, g = blockIdx.y, base = blockIdx.x * kChunk;
     const int L = __builtin_amdgcn_readfirstlane(rows[rows_cap + r] + 1);
     if (base >= L) return;
     const int seq = __builtin_amdgcn_readfirstlane(rows[r]);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int c = lane & 15, kb = lane >> 4;
-    const int j = base + 16 * wave + c;
-    const __amdgpu_buffer_rsrc_t rk = weight_rsrc(uniform_ptr(kc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD),
-                                                  (uint32_t)L * HD * 2u);
-    // the G query vectors are contiguous in the row's q; rows G and beyond read zero
-    const __amdgpu_buffer_rsrc_t rq = weight_rsrc(uniform_ptr(Q + (size_t)r * nq + (size_t)g * G * HD), G * HD * 2u);
-    uint4 kx[NS][2], qx[NS][2];
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const uint32_t d = 64u * s + 16u * kb + 8u * t;
-            kx[s][t] = cload16(rk, ((uint32_t)j * HD + d) * 2u);
-            qx[s][t] = cload16(rq, ((uint32_t)c * HD + d) * 2u);
-        }
-    v4i32_t ah[NS], al[NS], bh[NS], bl[NS];
-    int32_t qsum = 0;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-        uint2 h0, l0, h1, l1;
-        split_planes8(kx[s][0], h0, l0);
-        split_planes8(kx[s][1], h1, l1);
-        bh[s] = v4i32_t{(int)h0.x, (int)h0.y, (int)h1.x, (int)h1.y};
-        bl[s] = v4i32_t{(int)l0.x, (int)l0.y, (int)l1.x, (int)l1.y};
-        split_planes8(qx[s][0], h0, l0);
-        split_planes8(qx[s][1], h1, l1);
-        const bool ones = c == 15;
-        const int one4 = 0x01010101;
-        ah[s] = ones ? v4i32_t{one4, one4, one4, one4} : v4i32_t{(int)h0.x, (int)h0.y, (int)h1.x, (int)h1.y};
-        al[s] = ones ? v4i32_t{one4, one4, one4, one4} : v4i32_t{(int)l0.x, (int)l0.y, (int)l1.x, (int)l1.y};
-        qsum += sum8_i16(qx[s][0]) + sum8_i16(qx[s][1]);
-    }
-    v4i32_t hh = {0, 0, 0, 0}, mid = {0, 0, 0, 0}, ll = {0, 0, 0, 0};
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-        hh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[s], bh[s], hh, 0, 0, 0);
-        mid = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[s], bl[s], mid, 0, 0, 0);
-        mid = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[s], bh[s], mid, 0, 0, 0);
-        ll = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[s], bl[s], ll, 0, 0, 0);
-    }
-    // head c's sum over the four dimension blocks, then sum(k) of column c
-    // from row 15 (register 3 of lanes 48-63)
-    qsum += __shfl_xor(qsum, 16, 64);
-    qsum += __shfl_xor(qsum, 32, 64);
-    const int32_t ksum = __shfl(256 * hh[3] + ll[3] + 128 * HD, 48 + c, 64);
-    const int64_t kterm = 128 * (int64_t)ksum - 16384 * (int64_t)HD;
-    int32_t* z = scores + ((size_t)r * heads + (size_t)g * G) * lcap;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-        // lane l holds rows (heads) 4 (l / 16) + rr of column (position) l % 16
-        const int h = 4 * kb + rr;
-        const int32_t qs = __shfl(qsum, h, 64);
-        if (h < G && j < L) {
-            const int64_t dot = 65536 * (int64_t)hh[rr] + 256 * (int64_t)mid[rr] + (int64_t)ll[rr] +
-                                128 * (int64_t)qs + kterm;
-            z[(size_t)h * lcap + j] = (int32_t)rshift_round64(wmul64(dot, score_mult), score_shift);
-        }
-    }
+    const int wave = threadIdx.x >> 6;
+    qk_planes_wave<HD>(L, base + 16 * wave, kc + (size_t)seq * seq_stride + (size_t)g * max_pos * HD,
+                       Q + (size_t)r * nq + (size_t)g * G * HD, G, score_mult, score_shift,
+                       scores + ((size_t)r * heads + (size_t)g * G) * lcap, (size_t)lcap);
 }
 
 // Grid (ceil(lmax / kAttnRange), KV heads, rows); 256 threads.  Thread t holds
