@@ -31,14 +31,13 @@
 #include "bufload.h"
 #include "gemm_mfma.h"
 #include "internal.h"
+#include "mm_plan.h"
 #include "wave.h"
 
 #include <algorithm>
 
 namespace myl {
 
-constexpr int kFragWaves = 8;
-constexpr int kFragMaxRows = 32;  // token rows: 64 plane rows, RT = 4
 constexpr int kFragWeightCpol = 2;  // streaming (read once per product)
 
 // Bytes of the fragment copy of an N x K weight matrix (K % 64 == 0).
@@ -63,9 +62,6 @@ inline hipError_t frag_relayout(const int8_t* W, int N, int K, int8_t* Wf, hipSt
     frag_relayout_kernel<<<dim3((K / 64 + 3) / 4, (N + 15) / 16), 256, 0, st>>>(W, N, K, Wf);
     return hipGetLastError();
 }
-
-template <int RT>
-inline size_t frag_red_bytes(int ngb) { return (size_t)ngb * (RT * 256 + 16) * 4; }
 
 // The exact sums of a block's rows, read back from the LDS reduction.
 template <int RT>
@@ -245,19 +241,6 @@ __global__ __launch_bounds__(kFragWaves * 64) void frag_mm_kernel(const int8_t* 
 
 // ---- launches ---------------------------------------------------------------
 
-// Plane-row tiles for R token rows (0: too many rows).
-inline int frag_rt(int R) { return R <= 8 ? 1 : (R <= 16 ? 2 : (R <= kFragMaxRows ? 4 : 0)); }
-
-// The LDS a launch needs: the reduction of ngb row groups and, for the
-// staged epilogue, R x 16 ngb int16.  At least 81 KiB, so that one block
-// runs per CU (the grid has one block per CU).
-inline size_t frag_lds(int rt, int ngb, int R, bool staged) {
-    const size_t red = (size_t)ngb * (rt * 256 + 16) * 4;
-    const size_t stage = staged ? (size_t)R * 16 * ngb * 2 : 0;
-    return std::max<size_t>(red + stage, 81 * 1024);
-}
-constexpr size_t kFragLdsMax = 160 * 1024;
-
 template <int RT, int KPW, class Out>
 hipError_t frag_launch(const int8_t* Ap, int R, int K, const int8_t* Wf, int N, int S, int P, size_t lds, const Out& out,
                        hipStream_t st) {
@@ -268,14 +251,6 @@ hipError_t frag_launch(const int8_t* Ap, int R, int K, const int8_t* Wf, int N, 
     if (e != hipSuccess) return e;
     kern<<<S * P, kFragWaves * 64, lds, st>>>(Ap, 2 * R, K, Wf, N, (N + 15) / 16, Divider::of((uint32_t)P), out);
     return hipGetLastError();
-}
-
-// One K slice, the whole sum to the staged epilogue (gate/up with its SiLU):
-// K <= 8 x 8 KiB (KT <= 64), N % 16 == 0.
-inline bool frag_full_ok(int R, int K, int N, int cus) {
-    if (frag_rt(R) == 0 || R < 1 || K <= 0 || K % 64 != 0 || K / 64 > kFragWaves * 8 || N <= 0 || N % 16 != 0) return false;
-    const int NG = N / 16, ngb = (NG + cus - 1) / cus;
-    return 16 * ngb <= kFragWaves * 64 && frag_lds(frag_rt(R), ngb, R, true) <= kFragLdsMax;
 }
 
 // One K slice: every sum of a block's rows goes to the output policy (the
@@ -299,32 +274,6 @@ template <class Epi>
 hipError_t frag_mm_staged(const int8_t* Ap, int R, int K, const int8_t* Wf, int N, const Epi& epi, int cus,
                           hipStream_t st) {
     return frag_mm_full(Ap, R, K, Wf, N, FragOutStaged<Epi>{epi}, true, cus, st);
-}
-
-// Split-K plan: KPW K tiles per wave (8 or 5), S = ceil(KT / (8 KPW)) K
-// slices of 8 KPW tiles, P = cus / S row parts; the plan whose busiest wave
-// streams the fewest tiles (ceil(NG / P) row groups x KPW).  For the 7B down
-// product (296 K tiles, 224 row groups): 5 x 8 slices, 7 row groups per block
-// (the busiest wave 35 tiles; 8 tiles a wave in 5 slices: 40).
-struct FragSplit {
-    int kpw = 0, S = 0, P = 0, ngb = 0;
-};
-inline FragSplit frag_split_plan(int K, int N, int cus) {
-    FragSplit best;
-    const int KT = K / 64, NG = (N + 15) / 16;
-    for (int kpw : {8, 5}) {
-        const int S = (KT + kFragWaves * kpw - 1) / (kFragWaves * kpw);
-        if (S > cus) continue;
-        const int P = std::max(1, cus / S), ngb = (NG + P - 1) / P;
-        if (best.kpw == 0 || ngb * kpw < best.ngb * best.kpw) best = FragSplit{kpw, S, P, ngb};
-    }
-    return best;
-}
-
-inline bool frag_split_ok(int R, int K, int N, int cus, size_t acc_elems) {
-    if (frag_rt(R) == 0 || R < 1 || K <= 0 || K % 64 != 0 || N <= 0 || (size_t)R * (size_t)N > acc_elems) return false;
-    const FragSplit sp = frag_split_plan(K, N, cus);
-    return sp.kpw != 0 && frag_lds(frag_rt(R), sp.ngb, R, false) <= kFragLdsMax;
 }
 
 // The K-sliced product: each slice's partial sums added into acc [R x N].

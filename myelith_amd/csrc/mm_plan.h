@@ -1,5 +1,6 @@
-// mm_plan.h -- launch planning of the byte-plane products (gemm_mfma2.h):
-// block shapes, tile counts, the K split, grid and LDS sizes.  Plain C++
+// mm_plan.h -- launch planning of the byte-plane products (gemm_mfma2.h) and
+// of the fragment-major products of decode batches (gemm_frag.h): block
+// shapes, tile counts, the K split, grid and LDS sizes.  Plain C++
 // with no HIP dependency: the launchers call these functions, and a host
 // build of them runs under AddressSanitizer and UndefinedBehaviorSanitizer
 // in the CPU tests (tests/test_launch_plan.py).
@@ -65,6 +66,60 @@ inline Mm2SplitPlan mm2_split_plan(int M, int N, int K, int cus, size_t acc_elem
     p.nitems = p.ntiles * p.ns;
     p.grid = mm2_grid_of(p.nitems);
     return p;
+}
+
+// ---- the fragment-major products of decode batches (gemm_frag.h) ----------
+
+constexpr int kFragWaves = 8;
+constexpr int kFragMaxRows = 32;  // token rows: 64 plane rows, RT = 4
+
+// Plane-row tiles for R token rows (0: too many rows).
+inline int frag_rt(int R) { return R <= 8 ? 1 : (R <= 16 ? 2 : (R <= kFragMaxRows ? 4 : 0)); }
+
+// The LDS a launch needs: the reduction of ngb row groups and, for the
+// staged epilogue, R x 16 ngb int16.  At least 81 KiB, so that one block
+// runs per CU (the grid has one block per CU).
+inline size_t frag_lds(int rt, int ngb, int R, bool staged) {
+    const size_t red = (size_t)ngb * (rt * 256 + 16) * 4;
+    const size_t stage = staged ? (size_t)R * 16 * ngb * 2 : 0;
+    return std::max<size_t>(red + stage, 81 * 1024);
+}
+constexpr size_t kFragLdsMax = 160 * 1024;
+
+// One K slice, the whole sum to the staged epilogue (gate/up with its SiLU):
+// K <= 8 x 8 KiB (KT <= 64), N % 16 == 0.
+inline bool frag_full_ok(int R, int K, int N, int cus) {
+    if (frag_rt(R) == 0 || R < 1 || K <= 0 || K % 64 != 0 || K / 64 > kFragWaves * 8 || N <= 0 || N % 16 != 0) return false;
+    const int NG = N / 16, ngb = (NG + cus - 1) / cus;
+    return 16 * ngb <= kFragWaves * 64 && frag_lds(frag_rt(R), ngb, R, true) <= kFragLdsMax;
+}
+
+// Split-K plan: KPW K tiles per wave (8 or 5), S = ceil(KT / (8 KPW)) K
+// slices of 8 KPW tiles, P = cus / S row parts; the plan whose busiest wave
+// streams the fewest tiles (ceil(NG / P) row groups x KPW).  For the 7B down
+// product (296 K tiles, 224 row groups): 5 x 8 slices, 7 row groups per block
+// (the busiest wave 35 tiles; 8 tiles a wave in 5 slices: 40).
+struct FragSplit {
+    int kpw = 0, S = 0, P = 0, ngb = 0;
+};
+inline FragSplit frag_split_plan(int K, int N, int cus) {
+    FragSplit best;
+    const int KT = K / 64, NG = (N + 15) / 16;
+    for (int kpw : {8, 5}) {
+        const int S = (KT + kFragWaves * kpw - 1) / (kFragWaves * kpw);
+        if (S > cus) continue;
+        const int P = std::max(1, cus / S), ngb = (NG + P - 1) / P;
+        if (best.kpw == 0 || ngb * kpw < best.ngb * best.kpw) best = FragSplit{kpw, S, P, ngb};
+    }
+    return best;
+}
+
+// The output policies map the block's 16 ngb columns onto its 512 threads
+// (FragCols), so a plan needs 16 ngb <= 512.
+inline bool frag_split_ok(int R, int K, int N, int cus, size_t acc_elems) {
+    if (frag_rt(R) == 0 || R < 1 || K <= 0 || K % 64 != 0 || N <= 0 || (size_t)R * (size_t)N > acc_elems) return false;
+    const FragSplit sp = frag_split_plan(K, N, cus);
+    return sp.kpw != 0 && 16 * sp.ngb <= kFragWaves * 64 && frag_lds(frag_rt(R), sp.ngb, R, false) <= kFragLdsMax;
 }
 
 }  // namespace myl

@@ -203,3 +203,78 @@ def test_kernel_arguments_match_the_code_object(plan_run, tmp_path):
     # every split-K shape the dispatch launches is in the objects
     assert seen >= len(SPLIT_SHAPES)
     assert any(re.search(r"mm2_splitk_kernelILi2ELi1ELi1ELi4ELi2ELi128E", k["name"]) for k in kernels)
+
+
+FRAG_DRIVER = r"""
+#include "mm_plan.h"
+#include <cstdio>
+using namespace myl;
+static long checked = 0, bad = 0, wide = 0;
+#define CHECK(c, ...) do { ++checked; if (!(c)) { if (bad++ < 20) { std::printf("FAIL " __VA_ARGS__); std::printf("\n"); } } } while (0)
+
+// the row groups block p of P takes in frag_mm_kernel: [p NG / P, (p + 1) NG / P)
+static int block_groups(int p, int P, int NG) { return (int)(((long)(p + 1) * NG) / P - ((long)p * NG) / P); }
+
+int main() {
+    // (N, K) of the decode-batch products: gate/up, down, q/k/v, o_proj of the
+    // 7B and 0.5B shapes and of the test models (hidden 448 / 4096)
+    const int shapes[][2] = {{37888, 3584}, {3584, 18944}, {4608, 3584}, {3584, 3584}, {9728, 896}, {896, 4864},
+                             {1152, 896}, {896, 896}, {640, 448}, {448, 320}, {576, 448}, {8320, 4096},
+                             {4096, 4160}, {5120, 4096}};
+    const int cus_list[] = {1, 2, 3, 4, 7, 8, 16, 32, 38, 64, 80, 128, 160, 256, 304};
+    for (int cus : cus_list)
+        for (auto& nk : shapes) {
+            const int N = nk[0], K = nk[1], KT = K / 64, NG = (N + 15) / 16;
+            for (int R = 1; R <= kFragMaxRows; ++R) {
+                const int rt = frag_rt(R);
+                CHECK(rt == (R <= 8 ? 1 : R <= 16 ? 2 : 4) && 16 * rt >= 2 * R, "rt R=%d", R);
+                if (frag_full_ok(R, K, N, cus)) {
+                    const int ngb = (NG + cus - 1) / cus, kpw = KT <= kFragWaves * 7 ? 7 : 8;
+                    CHECK(kFragWaves * kpw >= KT, "full K=%d cover", K);
+                    CHECK(16 * ngb <= kFragWaves * 64, "full N=%d cus=%d width %d", N, cus, 16 * ngb);
+                    CHECK(frag_lds(rt, ngb, R, true) <= kFragLdsMax, "full lds");
+                    for (int p = 0; p < cus; ++p) CHECK(block_groups(p, cus, NG) <= ngb, "full groups p=%d", p);
+                }
+                const size_t acc = (size_t)R * (size_t)N;
+                const FragSplit sp = frag_split_plan(K, N, cus);
+                if (sp.kpw != 0 && 16 * sp.ngb > kFragWaves * 64 && frag_lds(rt, sp.ngb, R, false) <= kFragLdsMax)
+                    ++wide;  // plans the column guard turns away
+                if (frag_split_ok(R, K, N, cus, acc)) {
+                    CHECK(sp.kpw == 8 || sp.kpw == 5, "split kpw %d", sp.kpw);
+                    const int span = kFragWaves * sp.kpw;
+                    CHECK((long)sp.S * span >= KT && (long)(sp.S - 1) * span < KT, "split K=%d slices %d", K, sp.S);
+                    CHECK(sp.S * sp.P <= cus && sp.P >= 1, "split grid %d x %d on %d CUs", sp.S, sp.P, cus);
+                    CHECK(sp.ngb == (NG + sp.P - 1) / sp.P && 16 * sp.ngb <= kFragWaves * 64,
+                          "split N=%d cus=%d width %d", N, cus, 16 * sp.ngb);
+                    CHECK(frag_lds(rt, sp.ngb, R, false) <= kFragLdsMax, "split lds");
+                    for (int p = 0; p < sp.P; ++p) CHECK(block_groups(p, sp.P, NG) <= sp.ngb, "split groups p=%d", p);
+                    CHECK(!frag_split_ok(R, K, N, cus, acc - 1), "split past the accumulator");
+                }
+            }
+        }
+    std::printf("checked %ld bad %ld wide %ld\n", checked, bad, wide);
+    return bad != 0;
+}
+"""
+
+
+def test_fragment_plans_under_asan_and_ubsan(tmp_path):
+    """The fragment-major products' plans (csrc/mm_plan.h) for 1-32 rows of
+    every decode-batch product shape on 1-304 CUs: the K slices cover K, the
+    grid fits one block per CU, every block's row groups (as the kernel
+    splits them) fit the LDS the plan sized and the 512 output columns the
+    epilogues map onto the block's threads; plans wider than that exist and
+    are turned away."""
+    if not _gxx():
+        pytest.skip("g++ absent")
+    src = tmp_path / "frag.cpp"
+    src.write_text(FRAG_DRIVER)
+    exe = tmp_path / "frag"
+    subprocess.run([_gxx(), "-std=c++17", "-O1", "-g", "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+                    "-fno-omit-frame-pointer", "-I", str(CSRC), str(src), "-o", str(exe)],
+                   check=True, capture_output=True, timeout=300)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, (r.stdout[-3000:], r.stderr[-3000:])
+    assert "runtime error" not in r.stderr
+    m = re.match(r"checked (\d+) bad 0 wide (\d+)", r.stdout.strip().splitlines()[-1])
+    assert m and int(m.group(1)) > 10000 and int(m.group(2)) > 0, r.stdout[-500:]
