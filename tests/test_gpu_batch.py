@@ -261,12 +261,13 @@ def test_batch_decode_rows_past_4096_positions(backend):
         assert [int(t) for t in out[:, s]] == expected[s], s
 
 
-@pytest.mark.parametrize("rows", [5, 16, 32])
+@pytest.mark.parametrize("rows", [2, 5, 9, 16, 17, 32])
 @pytest.mark.parametrize("shape", ["k7", "k64_down2"])
 def test_batch_fragment_products(backend, monkeypatch, shape, rows):
     """Decode batches through the fragment-major gate/up and down products
-    (MYL_BATCH_FRAG=1 takes them at every size they support): 5, 16 and 32
-    rows (one, two and four 16-row plane tiles); a hidden size of 7 K tiles
+    (MYL_BATCH_FRAG=1 takes them at every size they support): 2 and 5 rows
+    (one 16-row plane tile), 9 and 16 (two), 17 and 32 (four), so the least
+    and the most rows of each tile count; a hidden size of 7 K tiles
     (one of the eight waves carries K) and one of 64 tiles (eight per wave)
     whose down product runs in two K slices.  The decode row's logits and
     argmax and two greedy steps equal the tiled products' (MYL_BATCH_FRAG=0)
