@@ -264,3 +264,38 @@ def test_rsqrt_wave_search_equals_the_table():
             worst = max(worst, rounds)
         if (frac, shift) == (8, 8):
             assert worst <= 3
+
+
+def _planes(x):
+    """x = 256 hi + lo' + 128 with hi = x >> 8 (signed) and lo' = (x & 255) - 128,
+    the byte planes of the matrix-core score product (csrc/qk_planes.h)."""
+    x = x.astype(np.int64)
+    return x >> 8, (x & 255) - 128
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_score_byte_plane_identity(hd):
+    """The exact score of the decode-batch kernels' int8 matrix-core form:
+    q . k = 65536 hh + 256 (hl + lh) + ll + 128 sum(q) + 128 sum(k) - 16384 hd,
+    with sum(k) recovered from the products of an all-ones query row as
+    256 sum(k_hi) + sum(k_lo') + 128 hd; every plane sum fits i32.  Random
+    int16 vectors and the extremes (all -32768, all 32767, alternating)."""
+    r = np.random.default_rng(hd)
+    cases = [r.integers(-32768, 32768, (2, hd)) for _ in range(200)]
+    for a in (-32768, 32767):
+        cases.append(np.full((2, hd), a))
+    alt = np.where(np.arange(hd) % 2 == 0, -32768, 32767)
+    cases.append(np.stack([alt, -alt - 1]))
+    for q, k in cases:
+        qh, ql = _planes(q)
+        kh, kl = _planes(k)
+        assert np.array_equal(256 * qh + ql + 128, q) and np.array_equal(256 * kh + kl + 128, k)
+        assert qh.min() >= -128 and qh.max() <= 127 and ql.min() >= -128 and ql.max() <= 127
+        hh, mid, ll = int(qh @ kh), int(qh @ kl + ql @ kh), int(ql @ kl)
+        for v in (hh, mid, ll):
+            assert abs(v) < 2**31
+        ones = np.ones(hd, dtype=np.int64)
+        ksum = 256 * int(ones @ kh) + int(ones @ kl) + 128 * hd
+        assert ksum == int(k.sum())
+        dot = 65536 * hh + 256 * mid + ll + 128 * int(q.sum()) + 128 * ksum - 16384 * hd
+        assert dot == int(q.astype(np.int64) @ k.astype(np.int64))
