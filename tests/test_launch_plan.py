@@ -13,6 +13,10 @@
    object's own metadata (llvm-readelf on the objects this build made), for
    every mm2 kernel instantiation, with the block size and LDS of the launch
    shape.
+3. The plans of the fragment-major products of decode batches (the same
+   header, gemm_frag.h's launchers) for 1-32 rows on 1-304 CUs, under the
+   same sanitizers: K covered, one block per CU, every block's row groups
+   within the LDS and the 512 output columns the epilogues map.
 
 Written to look for a host-side cause of an earlier abort inside the
 launch sequence of mm2_splitk_kernel<2, 1, 1, 4, 2, 128> (B = 32 batched
